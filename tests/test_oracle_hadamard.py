@@ -1,0 +1,94 @@
+"""Pins for oracle.hadamard: Sylvester H, FHT, HadamardLinear forward."""
+import math
+
+import numpy as np
+import scipy.linalg
+
+from oracle import hadamard, ternary
+
+
+def test_sylvester_matches_scipy():
+    for n in (1, 2, 4, 8, 16, 32, 64):
+        assert np.array_equal(hadamard.sylvester(n, normalize=False), scipy.linalg.hadamard(n))
+
+
+def test_sylvester_symmetric_orthonormal():
+    H = hadamard.sylvester(32)
+    assert np.array_equal(H, H.T)
+    assert np.allclose(H @ H, np.eye(32), atol=1e-14)
+
+
+def test_fht_unit_vectors():
+    e0 = np.zeros(32)
+    e0[0] = 1
+    assert np.allclose(hadamard.fht(e0), np.full(32, 1 / math.sqrt(32)))
+    ones = np.ones(32)
+    ref = np.zeros(32)
+    ref[0] = math.sqrt(32)
+    assert np.allclose(hadamard.fht(ones), ref)
+
+
+def test_rust_kat_self_inverse():
+    # inference/src/hadamard.rs:232-247: x[i] = i, fht_32 twice returns x
+    # within 1e-5 (float32 arithmetic).
+    x = np.arange(32, dtype=np.float32)
+    y = hadamard.fht(hadamard.fht(x))
+    assert y.dtype == np.float32
+    assert np.max(np.abs(y - x)) < 1e-5
+
+
+def test_rust_kat_norm_preserving():
+    # inference/src/hadamard.rs:249-265: x[i] = (i+1)/32, ||fht_32(x)|| = ||x||
+    # within 1e-5.
+    x = (np.arange(32, dtype=np.float32) + 1) / 32
+    assert abs(np.linalg.norm(hadamard.fht(x)) - np.linalg.norm(x)) < 1e-5
+
+
+def test_fht_equals_matrix_product():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((5, 32))
+    assert np.allclose(hadamard.fht(x), x @ hadamard.sylvester(32), atol=1e-12)
+
+
+def _layer(in_o, out_o, seed):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(-1, 2, size=(32, out_o, in_o)).astype(np.int8)
+    alpha = rng.uniform(0.5, 1.5, size=(32, in_o))
+    beta = rng.uniform(0.1, 0.4, size=(32, out_o))
+    return codes, alpha, beta
+
+
+def test_layer_matches_dense_matrix():
+    for in_o, out_o in ((1, 1), (16, 16), (16, 43), (43, 16), (3, 5)):
+        codes, alpha, beta = _layer(in_o, out_o, in_o * 100 + out_o)
+        x = np.random.default_rng(1).standard_normal((7, 32 * in_o))
+        A = hadamard.dense_matrix(codes, alpha, beta)
+        assert np.allclose(hadamard.hadamard_linear_f64(x, codes, alpha, beta), x @ A.T, atol=1e-10)
+
+
+def test_layer_scalar_closed_form():
+    # in_o = out_o = 1: the layer is y = beta * H diag(w) H (alpha*x); with
+    # all codes +1 it is the identity up to beta*alpha.
+    codes = np.ones((32, 1, 1), np.int8)
+    x = np.random.default_rng(2).standard_normal((3, 32))
+    y = hadamard.hadamard_linear_f64(x, codes, np.full((32, 1), 2.0), np.full((32, 1), 0.5))
+    assert np.allclose(y, x)
+
+
+def test_torch32_path_close_to_float64():
+    codes, alpha, beta = _layer(16, 16, 3)
+    x = np.random.default_rng(4).standard_normal((64, 512)).astype(np.float32)
+    y32 = hadamard.hadamard_linear_torch32(x, codes, alpha, beta).numpy()
+    y64 = hadamard.hadamard_linear_f64(x, codes, alpha, beta)
+    assert np.linalg.norm(y32 - y64) / np.linalg.norm(y64) < 1e-6
+
+
+def test_init_weight_quantises_to_thirds():
+    import torch
+    g = torch.Generator().manual_seed(0)
+    w = hadamard.init_weight(16, 16, g).numpy()
+    norms = np.linalg.norm(w.reshape(32, -1), axis=1)
+    assert np.allclose(norms, 0.02 * 16, rtol=1e-5)
+    c = ternary.ternary_codes(w, ternary.absmean_gamma(w))
+    frac = np.bincount(c.reshape(-1) + 1, minlength=3) / c.size
+    assert np.all(np.abs(frac - np.array([0.345, 0.31, 0.345])) < 0.04)

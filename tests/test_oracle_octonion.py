@@ -1,0 +1,84 @@
+"""Pins for oracle.octonion: tables re-derived from Cayley-Dickson doubling."""
+import numpy as np
+
+from oracle import octonion
+
+
+def _qmul(a, b):
+    a0, a1, a2, a3 = a
+    b0, b1, b2, b3 = b
+    return np.array([a0 * b0 - a1 * b1 - a2 * b2 - a3 * b3,
+                     a0 * b1 + a1 * b0 + a2 * b3 - a3 * b2,
+                     a0 * b2 - a1 * b3 + a2 * b0 + a3 * b1,
+                     a0 * b3 + a1 * b2 - a2 * b1 + a3 * b0])
+
+
+def _qconj(a):
+    return np.array([a[0], -a[1], -a[2], -a[3]])
+
+
+def _omul(x, w):
+    """Octonion product by Cayley-Dickson doubling of the quaternions:
+    (a, b)(c, d) = (ac - d*b, da + bc*), with x = (a, b), w = (c, d)."""
+    a, b, c, d = x[:4], x[4:], w[:4], w[4:]
+    return np.concatenate([_qmul(a, c) - _qmul(_qconj(d), b),
+                           _qmul(d, a) + _qmul(b, _qconj(c))])
+
+
+def test_quaternion_sanity():
+    i, j, k = np.eye(4)[1], np.eye(4)[2], np.eye(4)[3]
+    assert np.array_equal(_qmul(i, j), k) and np.array_equal(_qmul(j, i), -k)
+    assert np.array_equal(_qmul(i, i), -np.eye(4)[0])
+
+
+def test_tables_are_the_cayley_dickson_product():
+    E = np.eye(8)
+    for j in range(8):
+        for k in range(8):
+            p = _omul(E[j], E[k])
+            m = int(np.flatnonzero(p)[0])
+            assert np.count_nonzero(p) == 1
+            # x = e_j, w = e_k contributes only to y_m with W index k
+            assert m == (j ^ k) and octonion.WEIGHT_IDX[m, j] == k
+            assert p[m] == octonion.SIGN_TABLE[m, j]
+
+
+def test_layer_with_unit_blocks_is_the_octonion_product():
+    rng = np.random.default_rng(0)
+    for _ in range(20):
+        x = rng.standard_normal(8)
+        w = rng.standard_normal(8)
+        y = octonion.octonion_linear_f64(x.reshape(8, 1, 1), w.reshape(8, 1, 1), np.ones(1))
+        assert np.allclose(y.reshape(8), _omul(x, w), atol=1e-12)
+
+
+def test_octonion_norm_multiplicative():
+    # |x w| = |x| |w| holds for octonions; a wrong sign breaks it.
+    rng = np.random.default_rng(1)
+    x, w = rng.standard_normal(8), rng.standard_normal(8)
+    y = octonion.octonion_linear_f64(x.reshape(8, 1, 1), w.reshape(8, 1, 1), np.ones(1)).reshape(8)
+    assert np.isclose(np.linalg.norm(y), np.linalg.norm(x) * np.linalg.norm(w))
+
+
+def test_layer_matches_dense_matrix():
+    rng = np.random.default_rng(2)
+    in_o, out_o, M = 5, 3, 6
+    codes = rng.integers(-1, 2, size=(8, out_o, in_o)).astype(np.int8)
+    beta = rng.uniform(0.1, 1, size=out_o)
+    x = rng.standard_normal((8, M, in_o))
+    y = octonion.octonion_linear_f64(x, codes, beta)                 # [8, M, out_o]
+    A = octonion.dense_matrix(codes, beta)
+    xf = x.transpose(1, 0, 2).reshape(M, 8 * in_o)
+    yf = (xf @ A.T).reshape(M, 8, out_o).transpose(1, 0, 2)
+    assert np.allclose(y, yf, atol=1e-12)
+
+
+def test_bf16_round():
+    v = np.array([1.0, 1.00390625, 1.001953125, 1.0058594, -3.14159, 0.0], np.float32)
+    r = octonion.bf16_round(v)
+    assert r[0] == 1.0
+    assert r[1] == 1.0                        # 1+2^-8 is a tie -> even (1.0)
+    assert r[2] == 1.0                        # below the tie
+    assert r[3] == np.float32(1.0078125)      # above the tie
+    assert abs(r[4] - (-3.140625)) < 1e-7
+    assert r[5] == 0.0
