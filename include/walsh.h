@@ -1,0 +1,112 @@
+/*
+ * walsh.h -- C ABI of libwalsh_hip.so, the MI355X (gfx950) implementation of
+ * Walsh's ternary structured-linear hot path.
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers, int64 sizes/strides in elements, and a HIP
+ *     stream passed as `void *` (a hipStream_t; NULL = the null stream);
+ *   - work is enqueued on that stream; no entry point synchronises the host
+ *     or allocates device memory;
+ *   - return 0 on success, a negative WALSH_E* code for an invalid argument
+ *     or unsupported shape (nothing is launched), or WALSH_EHIP when a HIP
+ *     call fails; walsh_last_error() then returns a message (thread-local);
+ *   - activations use `dtype` WALSH_F32 or WALSH_BF16 (inputs and outputs
+ *     share it); parameters (alpha, beta, gamma, phi ...) are float32;
+ *     arithmetic is float32 with float32 accumulation.
+ *
+ * Each declaration names the reference interface it replaces
+ * (pulseofthemachine/Walsh-Research, file:line).
+ */
+#ifndef WALSH_H
+#define WALSH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WALSH_ABI_VERSION 1
+
+enum walsh_dtype { WALSH_F32 = 0, WALSH_BF16 = 1 };
+
+enum walsh_status {
+    WALSH_OK = 0,
+    WALSH_EINVAL = -1,   /* bad pointer / size / stride */
+    WALSH_ENOTSUP = -2,  /* shape or dtype this build does not handle */
+    WALSH_EHIP = -3      /* a HIP runtime call failed */
+};
+
+/* Library identity and errors. */
+int walsh_abi_version(void);
+const char *walsh_last_error(void);
+/* Binary name of the device code this library carries ("gfx950"). */
+const char *walsh_device_arch(void);
+
+/* ------------------------------------------------------------------ A1 / A11
+ * Absmean ternary quantisation.
+ * Replaces TernaryAbsmeanSTE.forward / quantize_ternary
+ *   (src/model/physics.py:21-51) and the MoE variant
+ *   (src/model/moe.py:276-303).
+ *
+ * walsh_ternary_gamma: gamma = mean(|w|) + 1e-8 (float32) over n weights,
+ *   reduced deterministically in float64 by one workgroup (same result on
+ *   every call and every device).  Writes one float to *gamma.
+ */
+int walsh_ternary_gamma(const float *w, int64_t n, float *gamma, void *stream);
+
+/* walsh_ternary_quantize: codes = clamp(round_half_even(w / *gamma), -1, 1)
+ *   for w viewed as [rows, K] (row-major, contiguous).  Any output may be
+ *   NULL:
+ *     codes  int8  [rows, K]
+ *     packed uint8 [rows, ceil(K/4)] in the 2-bit layout of
+ *            pack_ternary_weights (src/model/fht_cuda.py:65-93):
+ *            byte = v0<<6 | v1<<4 | v2<<2 | v3, v = code + 1; K is padded
+ *            to a multiple of 4 with code 0;
+ *     scaled float [rows, K] = code * gamma (the MoE quantiser's value,
+ *            src/model/moe.py:288).
+ *   `gamma` is a device pointer (usually walsh_ternary_gamma's output).
+ */
+int walsh_ternary_quantize(const float *w, int64_t rows, int64_t K, const float *gamma,
+                           int8_t *codes, uint8_t *packed, float *scaled, void *stream);
+
+/* walsh_ternary_unpack: inverse of the packed layout -> int8 codes [rows, K]
+ *   (unpack_ternary_weights, src/model/fht_cuda.py:96-117). */
+int walsh_ternary_unpack(const uint8_t *packed, int64_t rows, int64_t K, int8_t *codes,
+                         void *stream);
+
+/* ------------------------------------------------------------------ A3-A6
+ * Hadamard-32 ternary linear forward.
+ * Replaces HadamardLinear.forward (src/model/fht_cuda.py:489-519), which is
+ * also what HadamardTernaryLinearTuple (:550-569) and HadamardTernaryLinear
+ * (:392-424) compute:
+ *   x row (32*in_o) viewed [32 g][in_o i];
+ *   y[h, o] = beta[h, o] * sum_g H[g, h] sum_i W[g, o, i] sum_g' H[g', g] alpha[g', i] x[g', i]
+ *   with H the normalised Sylvester matrix (fht_cuda.py:32-56).
+ *
+ * walsh_hadamard_weight_bytes: size of the kernel weight layout for a shape.
+ * walsh_hadamard_prepare: reorders 2-bit packed codes [32, out_o, ceil(in_o/4)]
+ *   (walsh_ternary_quantize's `packed`) into that layout.  Call once per
+ *   weight version; the layout holds the same bytes, permuted.
+ */
+int64_t walsh_hadamard_weight_bytes(int64_t in_o, int64_t out_o);
+int walsh_hadamard_prepare(const uint8_t *packed, int64_t in_o, int64_t out_o,
+                           uint8_t *kweight, void *stream);
+
+/* walsh_hadamard_linear_fwd: y[M, ldy] = layer(x[M, ldx]).
+ *   x row m starts at x + m*ldx (elements); only the first 32*in_o entries
+ *   are read; y row m's first 32*out_o entries are written.
+ *   alpha float [32, in_o]; beta float [32, out_o]; kweight from
+ *   walsh_hadamard_prepare.  dtype: WALSH_F32 (float32 matrix cores) or
+ *   WALSH_BF16 (bf16 matrix cores on bf16-rounded transformed activations,
+ *   float32 accumulation). */
+int walsh_hadamard_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                              const uint8_t *kweight, const float *alpha, const float *beta,
+                              void *y, int64_t ldy, int dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WALSH_H */

@@ -82,3 +82,10 @@ def test_bf16_round():
     assert r[3] == np.float32(1.0078125)      # above the tie
     assert abs(r[4] - (-3.140625)) < 1e-7
     assert r[5] == 0.0
+
+
+def test_bf16_round_matches_torch():
+    import torch
+    v = np.random.default_rng(7).standard_normal(1000).astype(np.float32)
+    t = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(octonion.bf16_round(v), t)

@@ -1,0 +1,370 @@
+// Hadamard-32 ternary linear forward (HadamardLinear.forward,
+// src/model/fht_cuda.py:489-519), one fused kernel:
+//
+//   x row [32 g][in_o i]  --alpha-->  FHT over g  --W_g (ternary, per group)-->
+//   FHT over g  --beta/32-->  y row [32 h][out_o o]
+//
+// Work split.  A wavefront owns a tile of 16 tokens.  Lane l = (t, q) with
+// t = l % 16 the token and q = l / 16 a quad of columns: for a K-chunk c it
+// loads x[t, g*in_o + 16c + 4q .. +3] for all 32 groups g, so both Hadamard
+// transforms run entirely inside the lane's registers (5 butterfly stages on
+// 32 values, no cross-lane traffic).  The per-group contraction
+// y_g[o, t] = sum_i W[g, o, i] xm[t, g, i] is a 16x16 matrix-core product per
+// group with A = W_g (o x i, 2-bit codes expanded through an LDS table) and
+// B = xm^T (i x t, already in the lane layout the instruction wants), so the
+// result lands as 4 consecutive outputs o per lane per group, ready for the
+// output transform and 8/16-byte stores.
+//
+// Both transforms are left unnormalised; the 1/sqrt(32)^2 = 1/32 is folded
+// into beta (exact: a power of two).
+#include "common.h"
+
+namespace walsh {
+
+constexpr int kTile = 16;       // tokens per wavefront tile
+constexpr int kWaves = 4;       // wavefronts per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kKChunk = 16;     // input columns per chunk (4 per lane)
+constexpr int kNTile = 16;      // output columns per matrix-core tile
+
+// ---------------------------------------------------------------- weights
+
+// Kernel weight layout: [Nt][Kc][64 lanes][32 groups] bytes.  Lane l of tile
+// (nt, c) holds, for each group g, the packed byte with codes
+// W[g, 16nt + l%16, 16c + 4(l/16) .. +3]; that is exactly one byte of the
+// reference packing (4 codes per byte along K), so the layout is a byte
+// permutation.  Rows/columns past out_o/in_o hold 0x55 (four zero codes).
+__global__ void hadamard_prepare_kernel(const uint8_t *__restrict__ packed, int in_o, int out_o, int Nt,
+                                        int Kc, uint8_t *__restrict__ kw) {
+    const int64_t total = (int64_t)Nt * Kc * 64 * 32;
+    const int kp4 = (int)ceil_div(in_o, 4);
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int g = (int)(e & 31);
+        const int lane = (int)((e >> 5) & 63);
+        const int64_t tc = e >> 11;
+        const int c = (int)(tc % Kc);
+        const int nt = (int)(tc / Kc);
+        const int o = kNTile * nt + (lane & 15);
+        const int i0 = kKChunk * c + 4 * (lane >> 4);
+        uint8_t b = 0x55;
+        if (o < out_o && i0 < in_o) b = packed[((int64_t)g * out_o + o) * kp4 + i0 / 4];
+        kw[e] = b;
+    }
+}
+
+// ---------------------------------------------------------------- helpers
+
+// Unnormalised 32-point Walsh-Hadamard transform along the group index of
+// 4 independent columns held as v[g][j] (Sylvester ordering, in place).
+__device__ __forceinline__ void fht32x4(f32x4 (&v)[32]) {
+#pragma unroll
+    for (int h = 1; h < 32; h <<= 1) {
+#pragma unroll
+        for (int g = 0; g < 32; ++g) {
+            if (g & h) continue;
+            const f32x4 a = v[g];
+            const f32x4 b = v[g + h];
+            v[g] = a + b;
+            v[g + h] = a - b;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+struct HadArgs {
+    const void *x;      // first row of this launch
+    int64_t ldx;
+    int M;              // rows of this launch (M * ldx * esize < 2^31)
+    int in_o, out_o, Nt, Kc;
+    const uint8_t *kw;
+    const float *alpha;
+    const float *beta;
+    void *y;
+    int64_t ldy;
+};
+
+// Transformed inputs of the lane's 4 columns over the 32 groups.
+template <bool BF16MMA> struct XM;
+template <> struct XM<false> { f32x4 v[32]; };
+template <> struct XM<true> { uint2 b[32]; };
+
+// LDS layout (all 16-byte entries, lane-major so each lane walks its 32
+// groups with immediate offsets):
+//   lut     [256]            code byte -> 4 weights (bf16x4 in 8 B, or f32x4)
+//   alpha_l [Kc][4][32]      alpha[g, 16c+4q .. +3]   (0 past in_o)
+//   beta_l  [Nt][4][32]      beta[h, 16nt+4q .. +3]/32 (0 past out_o)
+template <bool BF16MMA> constexpr int lut_bytes() { return BF16MMA ? 256 * 8 : 256 * 16; }
+
+template <typename T, bool BF16MMA, bool VEC>
+__device__ __forceinline__ void load_transform(const HadArgs &a, __amdgpu_buffer_rsrc_t xr, uint32_t row_off,
+                                               bool row_ok, int c, int q, const f32x4 *__restrict__ alpha_l,
+                                               XM<BF16MMA> &out) {
+    constexpr uint32_t esz = sizeof(T);
+    f32x4 v[32];
+    const int i0 = kKChunk * c + 4 * q;
+    const uint32_t gstride = (uint32_t)a.in_o * esz;
+    if (VEC) {
+        const uint32_t voff = (row_ok && i0 < a.in_o) ? row_off + (uint32_t)i0 * esz : kOOB;
+#pragma unroll
+        for (int g = 0; g < 32; ++g) v[g] = Buf4<T>::load(xr, voff, (uint32_t)g * gstride);
+    } else {
+        uint32_t voff[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) voff[j] = (row_ok && i0 + j < a.in_o) ? row_off + (uint32_t)(i0 + j) * esz : kOOB;
+#pragma unroll
+        for (int g = 0; g < 32; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[g][j] = Buf4<T>::load1(xr, voff[j], (uint32_t)g * gstride);
+    }
+    const f32x4 *al = alpha_l + (c * 4 + q) * 32;
+#pragma unroll
+    for (int g = 0; g < 32; ++g) {
+        v[g] = v[g] * al[g];
+        if ((g & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+    }
+    fht32x4(v);
+    if constexpr (BF16MMA) {
+#pragma unroll
+        for (int g = 0; g < 32; ++g) {
+            out.b[g].x = pack_bf16x2(v[g][0], v[g][1]);
+            out.b[g].y = pack_bf16x2(v[g][2], v[g][3]);
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < 32; ++g) out.v[g] = v[g];
+    }
+}
+
+template <bool BF16MMA>
+__device__ __forceinline__ void contract(const HadArgs &a, int nt, int c, int lane, const XM<BF16MMA> &xm,
+                                         const void *__restrict__ lut, f32x4 (&acc)[32]) {
+    const uint4 *src = (const uint4 *)(a.kw + (((int64_t)nt * a.Kc + c) * 64 + lane) * 32);
+    const uint4 w0 = src[0], w1 = src[1];
+    const uint32_t wb[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int g = 0; g < 32; ++g) {
+        const uint32_t byte = (wb[g >> 2] >> (8 * (g & 3))) & 0xffu;
+        if constexpr (BF16MMA) {
+            const uint2 wa = ((const uint2 *)lut)[byte];
+            acc[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, wa),
+                                                                __builtin_bit_cast(i16x4, xm.b[g]), acc[g], 0, 0, 0);
+        } else {
+            const f32x4 wa = ((const f32x4 *)lut)[byte];
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[s], xm.v[g][s], acc[g], 0, 0, 0);
+        }
+        if ((g & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <typename T, bool VEC>
+__device__ __forceinline__ void transform_store(const HadArgs &a, f32x4 (&acc)[32], __amdgpu_buffer_rsrc_t yr,
+                                                uint32_t row_off, bool row_ok, int nt, int q,
+                                                const f32x4 *__restrict__ beta_l) {
+    constexpr uint32_t esz = sizeof(T);
+    fht32x4(acc);
+    const int o0 = kNTile * nt + 4 * q;
+    const uint32_t hstride = (uint32_t)a.out_o * esz;
+    const f32x4 *bl = beta_l + (nt * 4 + q) * 32;
+    if (VEC) {
+        const uint32_t voff = (row_ok && o0 < a.out_o) ? row_off + (uint32_t)o0 * esz : kOOB;
+#pragma unroll
+        for (int h = 0; h < 32; ++h) {
+            Buf4<T>::store(acc[h] * bl[h], yr, voff, (uint32_t)h * hstride);
+            if ((h & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+        uint32_t voff[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) voff[j] = (row_ok && o0 + j < a.out_o) ? row_off + (uint32_t)(o0 + j) * esz : kOOB;
+#pragma unroll
+        for (int h = 0; h < 32; ++h) {
+            const f32x4 r = acc[h] * bl[h];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Buf4<T>::store1(r[j], yr, voff[j], (uint32_t)h * hstride);
+            if ((h & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// VEC: in_o % 4 == 0 and out_o % 4 == 0 with aligned rows (4-wide loads and
+// stores).  KC1: a single input chunk (in_o <= 16); the transformed inputs
+// are computed once per tile and reused for every output tile.
+template <typename T, bool BF16MMA, bool VEC, bool KC1>
+__global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void hadamard_fwd_kernel(HadArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    void *lut = smem;
+    f32x4 *alpha_l = (f32x4 *)(smem + lut_bytes<BF16MMA>());
+    f32x4 *beta_l = alpha_l + a.Kc * 128;
+
+    const int tid = threadIdx.x;
+    {
+        const uint32_t byte = (uint32_t)tid;  // kThreads == 256 table entries
+        float val[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) val[j] = (float)((int)((byte >> (6 - 2 * j)) & 3u) - 1);
+        if constexpr (BF16MMA) {
+            uint2 e;
+            e.x = pack_bf16x2(val[0], val[1]);
+            e.y = pack_bf16x2(val[2], val[3]);
+            ((uint2 *)lut)[byte] = e;
+        } else {
+            ((f32x4 *)lut)[byte] = f32x4{val[0], val[1], val[2], val[3]};
+        }
+    }
+    for (int e = tid; e < a.Kc * 128; e += kThreads) {  // e = (c*4 + q)*32 + g
+        const int g = e & 31, cq = e >> 5;
+        const int i0 = 4 * cq;  // 16c + 4q
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (i0 + j < a.in_o) ? a.alpha[g * a.in_o + i0 + j] : 0.f;
+        alpha_l[e] = v;
+    }
+    for (int e = tid; e < a.Nt * 128; e += kThreads) {
+        const int h = e & 31, nq = e >> 5;
+        const int o0 = 4 * nq;
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (o0 + j < a.out_o) ? a.beta[h * a.out_o + o0 + j] * 0.03125f : 0.f;
+        beta_l[e] = v;
+    }
+    __syncthreads();
+
+    constexpr uint32_t esz = sizeof(T);
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int t = lane & 15;
+    const int q = lane >> 4;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * esz));
+    const int n_tiles = (int)ceil_div(a.M, kTile);
+    const int stride = gridDim.x * kWaves;
+
+    for (int tile = blockIdx.x * kWaves + wave; tile < n_tiles; tile += stride) {
+        const int row = tile * kTile + t;
+        const bool row_ok = row < a.M;
+        const uint32_t xoff = (uint32_t)((int64_t)row * a.ldx * esz);
+        const uint32_t yoff = (uint32_t)((int64_t)row * a.ldy * esz);
+        if constexpr (KC1) {
+            XM<BF16MMA> xm;
+            load_transform<T, BF16MMA, VEC>(a, xr, xoff, row_ok, 0, q, alpha_l, xm);
+            for (int nt = 0; nt < a.Nt; ++nt) {
+                f32x4 acc[32];
+#pragma unroll
+                for (int g = 0; g < 32; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+                contract<BF16MMA>(a, nt, 0, lane, xm, lut, acc);
+                transform_store<T, VEC>(a, acc, yr, yoff, row_ok, nt, q, beta_l);
+            }
+        } else {
+            for (int nt = 0; nt < a.Nt; ++nt) {
+                f32x4 acc[32];
+#pragma unroll
+                for (int g = 0; g < 32; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int c = 0; c < a.Kc; ++c) {
+                    XM<BF16MMA> xm;
+                    load_transform<T, BF16MMA, VEC>(a, xr, xoff, row_ok, c, q, alpha_l, xm);
+                    contract<BF16MMA>(a, nt, c, lane, xm, lut, acc);
+                }
+                transform_store<T, VEC>(a, acc, yr, yoff, row_ok, nt, q, beta_l);
+            }
+        }
+    }
+}
+
+static size_t hadamard_lds_bytes(bool bf16, int Kc, int Nt) {
+    return (bf16 ? lut_bytes<true>() : lut_bytes<false>()) + (size_t)16 * 128 * (Kc + Nt);
+}
+
+}  // namespace walsh
+
+using namespace walsh;
+
+WALSH_EXPORT int64_t walsh_hadamard_weight_bytes(int64_t in_o, int64_t out_o) {
+    if (in_o <= 0 || out_o <= 0) return 0;
+    return ceil_div(out_o, kNTile) * ceil_div(in_o, kKChunk) * 64 * 32;
+}
+
+WALSH_EXPORT int walsh_hadamard_prepare(const uint8_t *packed, int64_t in_o, int64_t out_o, uint8_t *kweight,
+                                        void *stream) {
+    if (!packed || !kweight) return set_error(WALSH_EINVAL, "walsh_hadamard_prepare: null pointer");
+    if (in_o <= 0 || out_o <= 0 || in_o > (1 << 20) || out_o > (1 << 20))
+        return set_error(WALSH_EINVAL, "walsh_hadamard_prepare: bad shape in_o=%lld out_o=%lld", (long long)in_o,
+                         (long long)out_o);
+    const int Nt = (int)ceil_div(out_o, kNTile), Kc = (int)ceil_div(in_o, kKChunk);
+    const int64_t total = (int64_t)Nt * Kc * 2048;
+    const int block = 256;
+    int grid = (int)ceil_div(total, block);
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(hadamard_prepare_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, packed, (int)in_o,
+                       (int)out_o, Nt, Kc, kweight);
+    return check_hip(hipGetLastError(), "walsh_hadamard_prepare launch");
+}
+
+WALSH_EXPORT int walsh_hadamard_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                                           const uint8_t *kweight, const float *alpha, const float *beta, void *y,
+                                           int64_t ldy, int dtype, void *stream) {
+    if (!x || !y || !kweight || !alpha || !beta)
+        return set_error(WALSH_EINVAL, "walsh_hadamard_linear_fwd: null pointer");
+    if (M < 0 || in_o <= 0 || out_o <= 0 || in_o > 65536 || out_o > 65536)
+        return set_error(WALSH_EINVAL, "walsh_hadamard_linear_fwd: bad shape M=%lld in_o=%lld out_o=%lld",
+                         (long long)M, (long long)in_o, (long long)out_o);
+    if (ldx < 32 * in_o || ldy < 32 * out_o)
+        return set_error(WALSH_EINVAL, "walsh_hadamard_linear_fwd: row stride too small (ldx=%lld ldy=%lld)",
+                         (long long)ldx, (long long)ldy);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16)
+        return set_error(WALSH_ENOTSUP, "walsh_hadamard_linear_fwd: dtype %d not supported", dtype);
+    if (M == 0) return WALSH_OK;
+    const bool bf16 = dtype == WALSH_BF16;
+    const int64_t esz = bf16 ? 2 : 4;
+    const int Nt = (int)ceil_div(out_o, kNTile), Kc = (int)ceil_div(in_o, kKChunk);
+    const size_t lds = hadamard_lds_bytes(bf16, Kc, Nt);
+    if (lds > (size_t)device_info().max_shared_per_block)
+        return set_error(WALSH_ENOTSUP, "walsh_hadamard_linear_fwd: in_o=%lld out_o=%lld need %zu B of LDS",
+                         (long long)in_o, (long long)out_o, lds);
+    const size_t valign = bf16 ? 8 : 16;
+    const bool vec = (in_o % 4 == 0) && (ldx % 4 == 0) && ((uintptr_t)x % valign == 0) && (out_o % 4 == 0) &&
+                     (ldy % 4 == 0) && ((uintptr_t)y % valign == 0);
+    // float32 operands keep 128 registers of transformed input; with several
+    // output tiles they are recomputed per tile instead of kept live.
+    const bool kc1 = Kc == 1 && (bf16 || Nt == 1);
+    // rows per launch so every byte offset fits a 31-bit buffer range
+    const int64_t ld = ldx > ldy ? ldx : ldy;
+    int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz);
+    rows_max = rows_max / kTile * kTile;
+    if (rows_max < kTile) return set_error(WALSH_ENOTSUP, "walsh_hadamard_linear_fwd: row stride too large");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t cap = (int64_t)device_info().cu_count * 2;
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        HadArgs a;
+        a.x = (const char *)x + r0 * ldx * esz;
+        a.ldx = ldx;
+        a.M = (int)rows;
+        a.in_o = (int)in_o;
+        a.out_o = (int)out_o;
+        a.Nt = Nt;
+        a.Kc = Kc;
+        a.kw = kweight;
+        a.alpha = alpha;
+        a.beta = beta;
+        a.y = (char *)y + r0 * ldy * esz;
+        a.ldy = ldy;
+        int64_t grid = ceil_div(ceil_div(rows, kTile), kWaves);
+        if (grid > cap) grid = cap;
+        const dim3 G((unsigned)grid), B(kThreads);
+#define WALSH_HAD_LAUNCH(T, MMA, V, K1) hipLaunchKernelGGL((hadamard_fwd_kernel<T, MMA, V, K1>), G, B, lds, s, a)
+        if (bf16) {
+            if (vec) { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, true, true); else WALSH_HAD_LAUNCH(uint16_t, true, true, false); }
+            else     { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, false, true); else WALSH_HAD_LAUNCH(uint16_t, true, false, false); }
+        } else {
+            if (vec) { if (kc1) WALSH_HAD_LAUNCH(float, false, true, true); else WALSH_HAD_LAUNCH(float, false, true, false); }
+            else     { if (kc1) WALSH_HAD_LAUNCH(float, false, false, true); else WALSH_HAD_LAUNCH(float, false, false, false); }
+        }
+#undef WALSH_HAD_LAUNCH
+        const int rc = check_hip(hipGetLastError(), "walsh_hadamard_linear_fwd launch");
+        if (rc) return rc;
+    }
+    return WALSH_OK;
+}

@@ -1,0 +1,88 @@
+"""ctypes binding of libwalsh_hip.so (the C ABI declared in include/walsh.h).
+
+The library is loaded from ``walsh-research_amd/lib/`` (built in-tree by
+``make -C walsh-research_amd``).  There is no fallback: if the library is
+missing or no GPU is present, every hot-path op raises.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.normpath(os.path.join(_HERE, "..", "..", "lib", "libwalsh_hip.so"))
+
+WALSH_F32 = 0
+WALSH_BF16 = 1
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+
+# name -> (restype, argtypes); mirrors include/walsh.h
+SIGNATURES = {
+    "walsh_abi_version": (_I, []),
+    "walsh_last_error": (ctypes.c_char_p, []),
+    "walsh_device_arch": (ctypes.c_char_p, []),
+    "walsh_ternary_gamma": (_I, [_P, _I64, _P, _P]),
+    "walsh_ternary_quantize": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
+    "walsh_ternary_unpack": (_I, [_P, _I64, _I64, _P, _P]),
+    "walsh_hadamard_weight_bytes": (_I64, [_I64, _I64]),
+    "walsh_hadamard_prepare": (_I, [_P, _I64, _I64, _P, _P]),
+    "walsh_hadamard_linear_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I, _P]),
+}
+
+_lib = None
+
+
+class WalshHipError(RuntimeError):
+    """A walsh_* entry point returned a non-zero status."""
+
+
+def lib():
+    """Load (once) and return the library handle; raise if it is absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"libwalsh_hip.so not found at {LIB_PATH}; build it with "
+                f"`make -C walsh-research_amd` (or __graft_entry__.build())")
+        h = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib
+
+
+def check(rc: int, name: str) -> None:
+    if rc != 0:
+        msg = lib().walsh_last_error().decode(errors="replace")
+        raise WalshHipError(f"{name} failed with status {rc}: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def require_device(t: torch.Tensor, what: str = "tensor") -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{what} must be on a GPU (the Walsh hot path has no CPU implementation); "
+                           f"got device {t.device}")
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return WALSH_F32
+    if dt == torch.bfloat16:
+        return WALSH_BF16
+    raise TypeError(f"activation dtype {dt} is not supported (float32 or bfloat16)")
+
+
+def ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
