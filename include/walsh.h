@@ -105,6 +105,69 @@ int walsh_hadamard_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_
                               const uint8_t *kweight, const float *alpha, const float *beta,
                               void *y, int64_t ldy, int dtype, void *stream);
 
+/* walsh_fht_fwd: fast Walsh-Hadamard transform of `rows` contiguous rows of
+ *   length n (power of two <= 16384), Sylvester order, scaled by 1/sqrt(n)
+ *   when `normalize` (fht_butterfly / fht, src/model/fht_cuda.py:281-337). */
+int walsh_fht_fwd(const void *x, int64_t rows, int64_t n, int normalize, void *y, int dtype, void *stream);
+
+/* ------------------------------------------------------------------ A7-A9
+ * Octonion (Cayley-Dickson) ternary linear forward.
+ * Replaces OctonionTernaryLinearRef.forward (src/model/physics.py:66-82) and
+ * OctonionFusedLinear -> cayley_dickson_fused -> cayley_dickson_fused_kernel
+ * (src/model/cayley_dickson_cuda.py:650-668, :574-619, :313-421):
+ *   y_i = beta * sum_j S[i][j] x_j W[i^j]^T, parts x_j = x[:, j*in_o:(j+1)*in_o]
+ *   and y_i = y[:, i*out_o:(i+1)*out_o], S = SIGN_TABLE (constants.py:13-31).
+ *
+ * walsh_octonion_weight_elems: element count of the expanded block matrix
+ *   B [8*out_o, Kp], Kp = roundup(8*in_o, 32).
+ * walsh_octonion_prepare: B[i*out_o + n][j*in_o + k] = S[i][j] * W[i^j][n][k]
+ *   from packed codes [8, out_o, ceil(in_o/4)]; dtype = element type of B
+ *   (use the activation dtype).  Once per weight version.
+ * walsh_octonion_linear_fwd: y[M, ldy] = (x[M, ldx] B^T) * beta[n % out_o];
+ *   beta float [out_o]; x rows 16-byte aligned.  WALSH_BF16 multiplies bf16
+ *   operands (the reference's kernel casts x to bf16 too, :402) with float32
+ *   accumulation; WALSH_F32 uses float32 matrix cores. */
+int64_t walsh_octonion_weight_elems(int64_t in_o, int64_t out_o);
+int walsh_octonion_prepare(const uint8_t *packed, int64_t in_o, int64_t out_o, void *B, int dtype, void *stream);
+int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o, const void *B,
+                              const float *beta, void *y, int64_t ldy, int dtype, void *stream);
+
+/* ------------------------------------------------------------------ A14-A17
+ * mHC residual streams.  Stream tensors are [M tokens][n streams][C] with row
+ * stride ldx >= n*C (elements); n <= 4 and C % 4 == 0 in this build.
+ *
+ * walsh_sinkhorn_fwd: SinkhornKnopp.forward / sinkhorn_knopp_fused
+ *   (src/model/mhc.py:214-229, :152-195): out = n_iter x {column-normalise,
+ *   row-normalise}(exp(h)) with `eps` added to every sum; h, out float32
+ *   [batch, n, n], n <= 8.
+ */
+int walsh_sinkhorn_fwd(const float *h, int64_t batch, int64_t n, int64_t n_iter, float eps, float *out,
+                       void *stream);
+
+/* walsh_mhc_pre_fwd: the three ResidualStreamMapping.forward calls of one
+ *   mHCResidualStream.forward and its H_pre @ x (src/model/mhc.py:283-318,
+ *   :345-364), fused.  With x_hat = x / sqrt(mean(x^2) + rms_eps) over the
+ *   n*C row and dyn = phi . x_hat:
+ *     h_pre  [M, n]    = sigmoid(coef[0]*dyn[0:n] + bias[0:n])
+ *     h_post [M, n]    = 2*sigmoid(coef[1]*dyn[n:2n] + bias[n:2n])
+ *     h_res  [M, n, n] = Sinkhorn(coef[2]*dyn[2n:2n+n*n] + bias[2n:], n_iter, sk_eps)
+ *     layer_in [M, C]  = sum_s h_pre[:, s] * x[:, s, :]   (row stride ld_in)
+ *   phi: activation dtype, [32, n*C] rows = phi_pre (n), phi_post (n),
+ *   phi_res (n*n), zero rows to 32.  coef = alphas (pre, post, res); bias =
+ *   float32 [2n + n*n].  rms_eps is finfo(activation dtype).eps in the
+ *   reference (F.rms_norm with eps=None, mhc.py:291). */
+int walsh_mhc_pre_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C, const void *phi,
+                      const float *coef, const float *bias, float rms_eps, int64_t n_iter, float sk_eps,
+                      float *h_pre, float *h_post, float *h_res, void *layer_in, int64_t ld_in, int dtype,
+                      void *stream);
+
+/* walsh_mhc_post_fwd: x_new = H_res @ x + H_post^T (x) out
+ *   (src/model/mhc.py:366-381).  out [M, C] row stride ld_out; x_new may not
+ *   alias x. */
+int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out, int64_t ld_out, const float *h_res,
+                       const float *h_post, void *x_new, int64_t ld_new, int64_t M, int64_t n, int64_t C, int dtype,
+                       void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,179 @@
+"""Oracle: functional float32 CPU forward of mHCWalsh from a state dict.
+
+Test infrastructure only (see ``oracle/__init__.py``).  This is the
+reference's CPU path restated with torch-CPU float32 operations in the
+reference's order (generate.py:134 runs the CPU path without autocast):
+
+  mHCWalsh.forward             src/model/mhc.py:617-681
+  mHCLlamaBlock.forward        mhc.py:507-534
+  mHCResidualStream.forward    mhc.py:345-381 (mappings :283-318, Sinkhorn :214-229)
+  CausalSelfAttention.forward  src/model/chassis.py:424-483 (RoPE :332-345)
+  SwiGLUMLP.forward            chassis.py:498-507
+  RMSNorm                      chassis.py:96-106
+  HadamardLinear.forward       src/model/fht_cuda.py:489-519 (quantiser physics.py:13-51)
+  HadamardHeadMixerFused       fht_cuda.py:652-670
+  HadamardMoE.forward          src/model/moe.py:512-542 (router :418-447, experts :337-380)
+
+It also serves as the timed CPU baseline of the full forward.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+def ternary_codes(w: torch.Tensor) -> torch.Tensor:
+    """clamp(round(W / (mean|W| + 1e-8)), -1, 1) in float32 (physics.py:24-29)."""
+    g = w.abs().mean() + 1e-8
+    return torch.clamp(torch.round(w / g), -1, 1)
+
+
+def sylvester(n=32):
+    H = torch.ones(1, 1)
+    while H.shape[0] < n:
+        H = torch.cat([torch.cat([H, H], 1), torch.cat([H, -H], 1)], 0)
+    return H / math.sqrt(n)
+
+
+class Oracle:
+    def __init__(self, sd, n_embd, n_head, n_layer, n_streams=4, head_mixing=True, block_size=256,
+                 use_moe=False, moe_max_experts=4):
+        self.sd = {k: (v.detach().cpu() if v.is_complex() else v.detach().float().cpu()) for k, v in sd.items()}
+        self.C = n_embd
+        self.n_head = n_head
+        self.n_layer = n_layer
+        self.n = n_streams
+        self.head_mixing = head_mixing
+        self.use_moe = use_moe
+        self.moe_k = moe_max_experts
+        self.H = sylvester(32)
+        self._codes = {}
+
+    def codes(self, key):
+        if key not in self._codes:
+            self._codes[key] = ternary_codes(self.sd[key])
+        return self._codes[key]
+
+    # ---------------------------------------------------------------- hot path
+    def hadamard_linear(self, x, p):
+        """fht_cuda.py:497-519 (x.float(), einsum H, einsum W, einsum H, * beta)."""
+        w = self.codes(p + '.weight')
+        G, out_o, in_o = w.shape
+        lead = x.shape[:-1]
+        xs = x.reshape(*lead, G, in_o) * self.sd[p + '.alpha']
+        xm = torch.einsum('...gi,gh->...hi', xs.float(), self.H)
+        yp = torch.einsum('...gi,goi->...go', xm, w)
+        ym = torch.einsum('...go,gh->...ho', yp, self.H)
+        return (ym * self.sd[p + '.beta']).reshape(*lead, G * out_o)
+
+    def mapping(self, x_flat, p, kind):
+        """mhc.py:283-318."""
+        n = self.n
+        xn = F.rms_norm(x_flat, (x_flat.size(-1),))
+        dyn = xn @ self.sd[p + '.phi.weight'].t()
+        a = self.sd[p + '.alpha']
+        b = self.sd[p + '.bias']
+        if kind == 'res':
+            h = a * dyn.view(*dyn.shape[:-1], n, n) + b
+            M = torch.exp(h)
+            for _ in range(20):
+                M = M / (M.sum(dim=-2, keepdim=True) + 1e-8)
+                M = M / (M.sum(dim=-1, keepdim=True) + 1e-8)
+            return M
+        s = torch.sigmoid(a * dyn + b).unsqueeze(-2)
+        return s if kind == 'pre' else 2.0 * s
+
+    def stream(self, x, p, layer_fn):
+        """mhc.py:345-381; x [B, T, n, C]."""
+        B, T, n, C = x.shape
+        xf = x.reshape(B, T, n * C)
+        hp = self.mapping(xf, p + '.H_pre', 'pre')
+        hq = self.mapping(xf, p + '.H_post', 'post')
+        hr = self.mapping(xf, p + '.H_res', 'res')
+        li = torch.matmul(hp, x).squeeze(2)
+        out = layer_fn(li)
+        return torch.matmul(hr, x) + torch.matmul(hq.transpose(-2, -1), out.unsqueeze(2))
+
+    def moe(self, x, p):
+        """moe.py:418-447, 337-380, 512-542 (top-k routing, all-expert einsum)."""
+        B, T, C = x.shape
+        h = F.silu(x @ self.sd[p + '.router.gate.0.weight'].t())
+        logits = h @ self.sd[p + '.router.gate.2.weight'].t()
+        probs = F.softmax(logits, dim=-1)
+        E = probs.shape[-1]
+        k = min(self.moe_k, E)
+        _, idx = probs.topk(k, dim=-1)
+        mask = torch.zeros_like(probs).scatter_(-1, idx, 1.0)
+        mp = probs * mask
+        wts = mp / mp.sum(-1, keepdim=True).clamp(min=1e-8)
+
+        def q(key):
+            w = self.sd[key]
+            g = w.abs().mean() + 1e-8
+            return torch.clamp(torch.round(w / g), -1, 1) * g
+
+        xb = x.view(B, T, E, C // E)
+        g = torch.einsum('bted,ehd->bteh', xb, q(p + '.experts.gate_weights'))
+        u = torch.einsum('bted,ehd->bteh', xb, q(p + '.experts.up_weights'))
+        out = torch.einsum('bteh,edh->bted', F.silu(g) * u, q(p + '.experts.down_weights'))
+        return (out * wts.unsqueeze(-1)).reshape(B, T, C), dict(probs=probs, mask=mask, weights=wts, idx=idx)
+
+    # ---------------------------------------------------------------- harness
+    def rmsnorm(self, x, w, eps=1e-6):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)) * w
+
+    def rope(self, xq, xk, freqs):
+        xq_ = torch.view_as_complex(xq.float().reshape(*xq.shape[:-1], -1, 2))
+        xk_ = torch.view_as_complex(xk.float().reshape(*xk.shape[:-1], -1, 2))
+        f = freqs[:xq.shape[1]].unsqueeze(0).unsqueeze(2)
+        return torch.view_as_real(xq_ * f).flatten(3), torch.view_as_real(xk_ * f).flatten(3)
+
+    def head_mixer(self, y, p):
+        xf = torch.einsum('bhti,hg->bgti', y, self.H)
+        z = torch.einsum('bhti,hio->bhto', xf, self.sd[p + '.W'])
+        zf = torch.einsum('bhti,hg->bgti', z, self.H)
+        return zf * self.sd[p + '.beta']
+
+    def attention(self, x, p, freqs):
+        B, T, C = x.shape
+        hd = C // self.n_head
+        q = self.hadamard_linear(x, p + '.wq.inner').view(B, T, self.n_head, hd)
+        k = self.hadamard_linear(x, p + '.wk.inner').view(B, T, self.n_head, hd)
+        v = self.hadamard_linear(x, p + '.wv.inner').view(B, T, self.n_head, hd)
+        q, k = self.rope(q, k, freqs)
+        y = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True)
+        if self.head_mixing:
+            ng = self.n_head // 32
+            yg = y.view(B, ng, 32, T, hd)
+            y = torch.cat([self.head_mixer(yg[:, g], p + '.head_mixer') for g in range(ng)], dim=1)
+        y = y.transpose(1, 2).contiguous().view(B, T, C)
+        return self.hadamard_linear(y, p + '.wo.inner')
+
+    def swiglu(self, x, p):
+        g = self.hadamard_linear(x, p + '.gate_proj.inner')
+        u = self.hadamard_linear(x, p + '.up_proj.inner')
+        return self.hadamard_linear(F.silu(g) * u, p + '.down_proj.inner')
+
+    def forward(self, idx, return_hidden=False):
+        """Logits of the last position [B, 1, V] (mhc.py:617-681, targets=None)."""
+        sd = self.sd
+        B, T = idx.shape
+        h = F.embedding(idx, sd['tok_embeddings.weight'])
+        h = h @ sd['stream_proj.weight'].t() + sd['stream_proj.bias']
+        h = h.view(B, T, self.n, self.C)
+        freqs = sd['freqs_cis'][:T]
+        for l in range(self.n_layer):
+            p = f'layers.{l}'
+            h = self.stream(h, p + '.attn_stream',
+                            lambda v: self.attention(self.rmsnorm(v, sd[p + '.attention_norm.weight']),
+                                                     p + '.attention', freqs))
+            if self.use_moe:
+                ffn = lambda v: self.moe(self.rmsnorm(v, sd[p + '.ffn_norm.weight']), p + '.feed_forward')[0]  # noqa: E731
+            else:
+                ffn = lambda v: self.swiglu(self.rmsnorm(v, sd[p + '.ffn_norm.weight']), p + '.feed_forward')  # noqa: E731
+            h = self.stream(h, p + '.ffn_stream', ffn)
+        hm = h.reshape(B, T, self.n * self.C) @ sd['stream_merge.weight'].t() + sd['stream_merge.bias']
+        ho = self.rmsnorm(hm, sd['norm.weight'])
+        logits = ho[:, [-1], :] @ sd['output.weight'].t()
+        return (logits, ho) if return_hidden else logits

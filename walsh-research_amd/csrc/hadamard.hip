@@ -273,6 +273,36 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
     }
 }
 
+// ---------------------------------------------------------------- standalone FHT
+// Normalised (or not) fast Walsh-Hadamard transform of rows of length
+// N = 2^logN (fht_cuda.py:281-309): rows staged in LDS, log2(N) butterfly
+// stages (k, k + h) -> (a + b, a - b) separated by barriers.
+template <typename T>
+__global__ __launch_bounds__(256) void fht_kernel(const T *__restrict__ x, int64_t rows, int logN, float scale,
+                                                  T *__restrict__ y) {
+    extern __shared__ float buf[];
+    const int N = 1 << logN;
+    const int rpb = N >= 4096 ? 1 : 4096 / N;
+    const int64_t row0 = (int64_t)blockIdx.x * rpb;
+    const int nr = (int)((rows - row0) < rpb ? (rows - row0) : rpb);
+    const int tot = nr * N;
+    for (int e = threadIdx.x; e < tot; e += blockDim.x) buf[e] = Act<T>::load(x + row0 * N + e);
+    __syncthreads();
+    const int half = N / 2;
+    for (int h = 1; h < N; h <<= 1) {
+        for (int p = threadIdx.x; p < nr * half; p += blockDim.x) {
+            const int r = p / half, j = p - r * half;
+            const int i = (j / h) * 2 * h + (j % h);
+            float *row = buf + r * N;
+            const float a = row[i], b = row[i + h];
+            row[i] = a + b;
+            row[i + h] = a - b;
+        }
+        __syncthreads();
+    }
+    for (int e = threadIdx.x; e < tot; e += blockDim.x) Act<T>::store(y + row0 * N + e, buf[e] * scale);
+}
+
 static size_t hadamard_lds_bytes(bool bf16, int Kc, int Nt) {
     return (bf16 ? lut_bytes<true>() : lut_bytes<false>()) + (size_t)16 * 128 * (Kc + Nt);
 }
@@ -367,4 +397,26 @@ WALSH_EXPORT int walsh_hadamard_linear_fwd(const void *x, int64_t ldx, int64_t M
         if (rc) return rc;
     }
     return WALSH_OK;
+}
+
+WALSH_EXPORT int walsh_fht_fwd(const void *x, int64_t rows, int64_t n, int normalize, void *y, int dtype,
+                               void *stream) {
+    if (!x || !y) return set_error(WALSH_EINVAL, "walsh_fht_fwd: null pointer");
+    if (rows < 0 || n < 1 || (n & (n - 1)) != 0 || n > 16384)
+        return set_error(WALSH_EINVAL, "walsh_fht_fwd: n must be a power of two <= 16384 (got %lld)", (long long)n);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "walsh_fht_fwd: dtype");
+    if (rows == 0) return WALSH_OK;
+    int logN = 0;
+    while ((1LL << logN) < n) ++logN;
+    const int rpb = n >= 4096 ? 1 : (int)(4096 / n);
+    const size_t lds = (size_t)rpb * n * 4;
+    const float scale = normalize ? (float)(1.0 / sqrt((double)n)) : 1.0f;
+    const dim3 G((unsigned)ceil_div(rows, rpb)), B(256);
+    if (dtype == WALSH_BF16)
+        hipLaunchKernelGGL(fht_kernel<uint16_t>, G, B, lds, (hipStream_t)stream, (const uint16_t *)x, rows, logN,
+                           scale, (uint16_t *)y);
+    else
+        hipLaunchKernelGGL(fht_kernel<float>, G, B, lds, (hipStream_t)stream, (const float *)x, rows, logN, scale,
+                           (float *)y);
+    return check_hip(hipGetLastError(), "walsh_fht_fwd launch");
 }

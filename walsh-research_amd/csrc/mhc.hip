@@ -1,0 +1,396 @@
+// mHC (manifold hyper-connection) residual-stream kernels.
+//
+//   walsh_sinkhorn_fwd  SinkhornKnopp.forward (src/model/mhc.py:214-229)
+//   walsh_mhc_pre_fwd   the three ResidualStreamMapping.forward calls of one
+//                       mHCResidualStream.forward plus its H_pre @ x
+//                       (mhc.py:283-318, 345-364), fused: one pass over x
+//   walsh_mhc_post_fwd  x_new = H_res @ x + H_post^T (x) out (mhc.py:366-381)
+//
+// Stream tensors are [M tokens][n streams][C] (row stride ldx >= n*C).
+#include "common.h"
+
+namespace walsh {
+
+constexpr int kMaxStreams = 4;            // n*n + 2n <= 24 outputs -> 2 MMA tiles
+constexpr int kPhiRows = 32;              // projection rows padded to 2 x 16
+constexpr int kPreTok = 32;               // tokens per workgroup (2 x 16)
+constexpr int kPreWaves = 4;              // K split across 4 wavefronts
+constexpr int kPreThreads = 64 * kPreWaves;
+
+// Sinkhorn-Knopp on an n x n matrix in registers: M = exp(H); n_iter x
+// {divide each column by (its sum + eps); divide each row by (its sum + eps)}.
+template <int NMAX>
+__device__ __forceinline__ void sinkhorn_regs(float (&m)[NMAX][NMAX], int n, int n_iter, float eps) {
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i)
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) m[i][j] = (i < n && j < n) ? expf(m[i][j]) : 0.f;
+    for (int it = 0; it < n_iter; ++it) {
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) {
+            if (j >= n) continue;
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) s += (i < n) ? m[i][j] : 0.f;
+            const float d = s + eps;
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) m[i][j] = __fdiv_rn(m[i][j], d);
+        }
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+            if (i >= n) continue;
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) s += (j < n) ? m[i][j] : 0.f;
+            const float d = s + eps;
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) m[i][j] = __fdiv_rn(m[i][j], d);
+        }
+    }
+}
+
+__device__ __forceinline__ float sigmoidf(float v) { return __fdiv_rn(1.0f, 1.0f + expf(-v)); }
+
+// ---------------------------------------------------------------- sinkhorn
+__global__ void sinkhorn_kernel(const float *__restrict__ h, int64_t batch, int n, int n_iter, float eps,
+                                float *__restrict__ out) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < batch; b += (int64_t)gridDim.x * blockDim.x) {
+        float m[8][8];
+        const float *src = h + b * n * n;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) m[i][j] = (i < n && j < n) ? src[i * n + j] : 0.f;
+        sinkhorn_regs<8>(m, n, n_iter, eps);
+        float *dst = out + b * n * n;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (i < n && j < n) dst[i * n + j] = m[i][j];
+    }
+}
+
+// ---------------------------------------------------------------- pre (mapping)
+struct PreArgs {
+    const void *x;
+    int64_t ldx;
+    int M, n, C;
+    const void *phi;        // [32][n*C] activation dtype, rows: pre(n), post(n), res(n*n), zero pad
+    const float *coef;      // alpha_pre, alpha_post, alpha_res
+    const float *bias;      // pre[n], post[n], res[n*n]
+    float rms_eps, sk_eps;
+    int n_iter;
+    float *h_pre, *h_post, *h_res;
+    void *layer_in;
+    int64_t ld_in;
+};
+
+// One workgroup = 32 tokens; wavefront w reduces the K range [w*K/4, (w+1)*K/4)
+// (K = n*C) of the 32 x 32 projection D = x . phi^T on matrix cores, plus the
+// per-token sum of squares.  The epilogue (one thread per token) applies the
+// RMS scale, the sigmoid / 2*sigmoid / Sinkhorn constraints, and finally all
+// threads form layer_in = sum_s H_pre[s] x[s, :] re-reading the (cache-hot) x.
+template <typename T, bool BF16MMA>
+__global__ __launch_bounds__(kPreThreads) void mhc_pre_kernel(PreArgs a) {
+    __shared__ float part[kPreWaves][kPreTok][kPhiRows + 1];
+    __shared__ float ssp[kPreWaves][kPreTok];
+    __shared__ float hpre_s[kPreTok][kMaxStreams];
+
+    constexpr uint32_t esz = sizeof(T);
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int m = lane & 15, kq = lane >> 4;
+    const int n = a.n;
+    const int K = n * a.C;
+    const int tok0 = blockIdx.x * kPreTok;
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.phi, (uint32_t)((int64_t)kPhiRows * K * esz));
+
+    // wave's K slice, a multiple of 16
+    const int kslice = (int)ceil_div(ceil_div(K, kPreWaves), 16) * 16;
+    const int kbeg = wave * kslice;
+    const int kend = min(K, kbeg + kslice);
+
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ss[2] = {0.f, 0.f};
+    uint32_t xrow[2];
+    bool tok_ok[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int tok = tok0 + 16 * mt + m;
+        tok_ok[mt] = tok < a.M;
+        xrow[mt] = (uint32_t)((int64_t)tok * a.ldx * esz);
+    }
+    for (int k0 = kbeg; k0 < kend; k0 += 16) {
+        const int k = k0 + 4 * kq;
+        const bool kok = k < kend;  // K % 4 == 0, so a quad is all-in or all-out
+        f32x4 xa[2], pb[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+            xa[mt] = Buf4<T>::load(xr, (kok && tok_ok[mt]) ? xrow[mt] + (uint32_t)k * esz : kOOB, 0);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+            pb[nt] = Buf4<T>::load(pr, kok ? (uint32_t)(((int64_t)(16 * nt + m) * K + k) * esz) : kOOB, 0);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            ss[mt] += xa[mt].x * xa[mt].x + xa[mt].y * xa[mt].y + xa[mt].z * xa[mt].z + xa[mt].w * xa[mt].w;
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                if constexpr (BF16MMA) {
+                    uint2 av, bv;
+                    av.x = pack_bf16x2(xa[mt].x, xa[mt].y);
+                    av.y = pack_bf16x2(xa[mt].z, xa[mt].w);
+                    bv.x = pack_bf16x2(pb[nt].x, pb[nt].y);
+                    bv.y = pack_bf16x2(pb[nt].z, pb[nt].w);
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                        __builtin_bit_cast(i16x4, av), __builtin_bit_cast(i16x4, bv), acc[mt][nt], 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        acc[mt][nt] =
+                            __builtin_amdgcn_mfma_f32_16x16x4f32(xa[mt][s], pb[nt][s], acc[mt][nt], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // sum of squares: the 4 lanes (kq) of a token hold disjoint k quads
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        ss[mt] += __shfl_xor(ss[mt], 16);
+        ss[mt] += __shfl_xor(ss[mt], 32);
+    }
+    if (kq == 0) {
+        ssp[wave][m] = ss[0];
+        ssp[wave][16 + m] = ss[1];
+    }
+    // D[token 4*kq + j][out m] of each (mt, nt) tile
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) part[wave][16 * mt + 4 * kq + j][16 * nt + m] = acc[mt][nt][j];
+    __syncthreads();
+
+    if (tid < kPreTok) {
+        const int t = tid;
+        const int tok = tok0 + t;
+        float ssum = 0.f;
+#pragma unroll
+        for (int w = 0; w < kPreWaves; ++w) ssum += ssp[w][t];
+        const float r = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(ssum, (float)K) + a.rms_eps));
+        float dyn[kPhiRows];
+#pragma unroll
+        for (int o = 0; o < kPhiRows; ++o) {
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < kPreWaves; ++w) s += part[w][t][o];
+            dyn[o] = s * r;
+        }
+        const float ap = a.coef[0], aq = a.coef[1], ar = a.coef[2];
+        float hm[kMaxStreams][kMaxStreams];
+#pragma unroll
+        for (int s = 0; s < kMaxStreams; ++s) {
+            float pre = 0.f, post = 0.f;
+            if (s < n) {
+                pre = sigmoidf(ap * dyn[s] + a.bias[s]);
+                post = 2.0f * sigmoidf(aq * dyn[n + s] + a.bias[n + s]);
+            }
+            hpre_s[t][s] = pre;
+            if (tok < a.M && s < n) {
+                a.h_pre[(int64_t)tok * n + s] = pre;
+                a.h_post[(int64_t)tok * n + s] = post;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxStreams; ++i)
+#pragma unroll
+            for (int j = 0; j < kMaxStreams; ++j)
+                hm[i][j] = (i < n && j < n) ? ar * dyn[2 * n + i * n + j] + a.bias[2 * n + i * n + j] : 0.f;
+        sinkhorn_regs<kMaxStreams>(hm, n, a.n_iter, a.sk_eps);
+        if (tok < a.M) {
+#pragma unroll
+            for (int i = 0; i < kMaxStreams; ++i)
+#pragma unroll
+                for (int j = 0; j < kMaxStreams; ++j)
+                    if (i < n && j < n) a.h_res[(int64_t)tok * n * n + i * n + j] = hm[i][j];
+        }
+    }
+    __syncthreads();
+
+    // layer_in[t, c] = sum_s H_pre[t, s] x[t, s, c], 4 columns per item
+    const int C = a.C;
+    const int cq = C / 4;
+    const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
+    for (int item = tid; item < kPreTok * cq; item += kPreThreads) {
+        const int t = item / cq;
+        const int c = (item - t * cq) * 4;
+        const int tok = tok0 + t;
+        const bool ok = tok < a.M;
+        const uint32_t xo = ok ? (uint32_t)(((int64_t)tok * a.ldx + c) * esz) : kOOB;
+        f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < n; ++s) sum += hpre_s[t][s] * Buf4<T>::load(xr, xo, (uint32_t)(s * C) * esz);
+        Buf4<T>::store(sum, lr, ok ? (uint32_t)(((int64_t)tok * a.ld_in + c) * esz) : kOOB, 0);
+    }
+}
+
+// ---------------------------------------------------------------- post (apply)
+// x_new[t, r, :] = sum_s H_res[t, r, s] x[t, s, :] + H_post[t, r] out[t, :]
+template <typename T>
+__global__ __launch_bounds__(256) void mhc_post_kernel(const T *__restrict__ x, int64_t ldx, const T *__restrict__ out,
+                                                       int64_t ld_out, const float *__restrict__ h_res,
+                                                       const float *__restrict__ h_post, T *__restrict__ x_new,
+                                                       int64_t ld_new, int M, int n, int C) {
+    constexpr uint32_t esz = sizeof(T);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)((int64_t)M * ldx * esz));
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(out, (uint32_t)((int64_t)M * ld_out * esz));
+    const __amdgpu_buffer_rsrc_t nr = make_rsrc(x_new, (uint32_t)((int64_t)M * ld_new * esz));
+    const int cq = C / 4;
+    const int64_t total = (int64_t)M * cq;
+    for (int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < total;
+         item += (int64_t)gridDim.x * blockDim.x) {
+        const int tok = (int)(item / cq);
+        const int c = (int)(item - (int64_t)tok * cq) * 4;
+        const uint32_t xo = (uint32_t)(((int64_t)tok * ldx + c) * esz);
+        f32x4 xs[kMaxStreams];
+#pragma unroll
+        for (int s = 0; s < kMaxStreams; ++s)
+            xs[s] = Buf4<T>::load(xr, s < n ? xo : kOOB, (uint32_t)(s * C) * esz);
+        const f32x4 o = Buf4<T>::load(orr, (uint32_t)(((int64_t)tok * ld_out + c) * esz), 0);
+        const float *hr = h_res + (int64_t)tok * n * n;
+        const float *hp = h_post + (int64_t)tok * n;
+        const uint32_t no = (uint32_t)(((int64_t)tok * ld_new + c) * esz);
+#pragma unroll
+        for (int r = 0; r < kMaxStreams; ++r) {
+            if (r >= n) continue;
+            f32x4 acc = hp[r] * o;
+#pragma unroll
+            for (int s = 0; s < kMaxStreams; ++s)
+                if (s < n) acc += hr[r * n + s] * xs[s];
+            Buf4<T>::store(acc, nr, no, (uint32_t)(r * C) * esz);
+        }
+    }
+}
+
+}  // namespace walsh
+
+using namespace walsh;
+
+WALSH_EXPORT int walsh_sinkhorn_fwd(const float *h, int64_t batch, int64_t n, int64_t n_iter, float eps, float *out,
+                                    void *stream) {
+    if (!h || !out) return set_error(WALSH_EINVAL, "walsh_sinkhorn_fwd: null pointer");
+    if (batch < 0 || n < 1 || n > 8 || n_iter < 0)
+        return set_error(n > 8 ? WALSH_ENOTSUP : WALSH_EINVAL,
+                         "walsh_sinkhorn_fwd: batch=%lld n=%lld n_iter=%lld (n must be 1..8)", (long long)batch,
+                         (long long)n, (long long)n_iter);
+    if (batch == 0) return WALSH_OK;
+    const int block = 128;
+    int64_t grid = ceil_div(batch, block);
+    if (grid > (int64_t)device_info().cu_count * 8) grid = (int64_t)device_info().cu_count * 8;
+    hipLaunchKernelGGL(sinkhorn_kernel, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream, h, batch, (int)n,
+                       (int)n_iter, eps, out);
+    return check_hip(hipGetLastError(), "walsh_sinkhorn_fwd launch");
+}
+
+WALSH_EXPORT int walsh_mhc_pre_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C, const void *phi,
+                                   const float *coef, const float *bias, float rms_eps, int64_t n_iter, float sk_eps,
+                                   float *h_pre, float *h_post, float *h_res, void *layer_in, int64_t ld_in,
+                                   int dtype, void *stream) {
+    if (!x || !phi || !coef || !bias || !h_pre || !h_post || !h_res || !layer_in)
+        return set_error(WALSH_EINVAL, "walsh_mhc_pre_fwd: null pointer");
+    if (M < 0 || n < 1 || C < 4 || ldx < n * C || ld_in < C || n_iter < 0)
+        return set_error(WALSH_EINVAL, "walsh_mhc_pre_fwd: bad shape M=%lld n=%lld C=%lld", (long long)M,
+                         (long long)n, (long long)C);
+    if (n > kMaxStreams || C % 4 != 0 || ldx % 4 != 0 || ld_in % 4 != 0)
+        return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_fwd: needs n <= %d and C, row strides multiples of 4",
+                         kMaxStreams);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16)
+        return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_fwd: dtype %d", dtype);
+    if (M == 0) return WALSH_OK;
+    const int64_t esz = dtype == WALSH_BF16 ? 2 : 4;
+    const size_t valign = dtype == WALSH_BF16 ? 8 : 16;
+    if ((uintptr_t)x % valign || (uintptr_t)layer_in % valign || (uintptr_t)phi % valign)
+        return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_fwd: x, phi and layer_in must be %zu-byte aligned", valign);
+    if ((int64_t)kPhiRows * n * C * esz > (int64_t)kMaxBufferBytes)
+        return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_fwd: projection too large");
+    const int64_t ld = ldx > ld_in ? ldx : ld_in;
+    int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / kPreTok * kPreTok;
+    if (rows_max < kPreTok) return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_fwd: row stride too large");
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        PreArgs a;
+        a.x = (const char *)x + r0 * ldx * esz;
+        a.ldx = ldx;
+        a.M = (int)rows;
+        a.n = (int)n;
+        a.C = (int)C;
+        a.phi = phi;
+        a.coef = coef;
+        a.bias = bias;
+        a.rms_eps = rms_eps;
+        a.sk_eps = sk_eps;
+        a.n_iter = (int)n_iter;
+        a.h_pre = h_pre + r0 * n;
+        a.h_post = h_post + r0 * n;
+        a.h_res = h_res + r0 * n * n;
+        a.layer_in = (char *)layer_in + r0 * ld_in * esz;
+        a.ld_in = ld_in;
+        const dim3 G((unsigned)ceil_div(rows, kPreTok)), B(kPreThreads);
+        if (dtype == WALSH_BF16)
+            hipLaunchKernelGGL((mhc_pre_kernel<uint16_t, true>), G, B, 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL((mhc_pre_kernel<float, false>), G, B, 0, (hipStream_t)stream, a);
+        const int rc = check_hip(hipGetLastError(), "walsh_mhc_pre_fwd launch");
+        if (rc) return rc;
+    }
+    return WALSH_OK;
+}
+
+WALSH_EXPORT int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out, int64_t ld_out, const float *h_res,
+                                    const float *h_post, void *x_new, int64_t ld_new, int64_t M, int64_t n, int64_t C,
+                                    int dtype, void *stream) {
+    if (!x || !out || !h_res || !h_post || !x_new) return set_error(WALSH_EINVAL, "walsh_mhc_post_fwd: null pointer");
+    if (M < 0 || n < 1 || C < 4 || ldx < n * C || ld_new < n * C || ld_out < C)
+        return set_error(WALSH_EINVAL, "walsh_mhc_post_fwd: bad shape M=%lld n=%lld C=%lld", (long long)M,
+                         (long long)n, (long long)C);
+    if (n > kMaxStreams || C % 4 || ldx % 4 || ld_out % 4 || ld_new % 4)
+        return set_error(WALSH_ENOTSUP, "walsh_mhc_post_fwd: needs n <= %d and C, row strides multiples of 4",
+                         kMaxStreams);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "walsh_mhc_post_fwd: dtype");
+    if (M == 0) return WALSH_OK;
+    const int64_t esz = dtype == WALSH_BF16 ? 2 : 4;
+    const size_t valign = dtype == WALSH_BF16 ? 8 : 16;
+    if ((uintptr_t)x % valign || (uintptr_t)out % valign || (uintptr_t)x_new % valign)
+        return set_error(WALSH_ENOTSUP, "walsh_mhc_post_fwd: tensors must be %zu-byte aligned", valign);
+    int64_t ld = ldx > ld_new ? ldx : ld_new;
+    if (ld_out > ld) ld = ld_out;
+    const int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz);
+    if (rows_max < 1) return set_error(WALSH_ENOTSUP, "walsh_mhc_post_fwd: row stride too large");
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        const int block = 256;
+        int64_t grid = ceil_div(rows * (C / 4), block);
+        const int64_t cap = (int64_t)device_info().cu_count * 8;
+        if (grid > cap) grid = cap;
+        hipStream_t s = (hipStream_t)stream;
+        if (dtype == WALSH_BF16)
+            hipLaunchKernelGGL(mhc_post_kernel<uint16_t>, dim3((unsigned)grid), dim3(block), 0, s,
+                               (const uint16_t *)x + r0 * ldx, ldx, (const uint16_t *)out + r0 * ld_out, ld_out,
+                               h_res + r0 * n * n, h_post + r0 * n, (uint16_t *)x_new + r0 * ld_new, ld_new, (int)rows,
+                               (int)n, (int)C);
+        else
+            hipLaunchKernelGGL(mhc_post_kernel<float>, dim3((unsigned)grid), dim3(block), 0, s,
+                               (const float *)x + r0 * ldx, ldx, (const float *)out + r0 * ld_out, ld_out,
+                               h_res + r0 * n * n, h_post + r0 * n, (float *)x_new + r0 * ld_new, ld_new, (int)rows,
+                               (int)n, (int)C);
+        const int rc = check_hip(hipGetLastError(), "walsh_mhc_post_fwd launch");
+        if (rc) return rc;
+    }
+    return WALSH_OK;
+}

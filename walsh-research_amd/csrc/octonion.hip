@@ -1,0 +1,241 @@
+// Octonion (Cayley-Dickson) ternary linear forward.
+//
+// Reference: OctonionTernaryLinearRef.forward (src/model/physics.py:66-82) and
+// the fused GPU path cayley_dickson_fused_kernel
+// (src/model/cayley_dickson_cuda.py:313-421):
+//     y_i = beta * sum_j S[i][j] x_j @ W[i ^ j]^T      (i, j = 0..7)
+// with the sign table S of src/model/constants.py:13-31.
+//
+// MI355X design.  The 8x8 block structure is a signed permutation of only 8
+// distinct ternary blocks, so at weight-preparation time it is expanded once
+// into the dense block matrix B[i*out_o + n][j*in_o + k] = S[i][j] W[i^j][n][k]
+// (still exactly {-1, 0, 1}, stored bf16 or f32, K-contiguous).  The forward
+// is then one matrix-core GEMM  y = (x B^T) * beta  with 128x128 output tiles,
+// four wavefronts each owning 64x64 (4x4 tiles of 16x16), K staged through
+// double-buffered LDS, and beta fused into the epilogue.
+#include "common.h"
+
+namespace walsh {
+
+__constant__ int8_t kOctSign[8][8] = {
+    {+1, -1, -1, -1, -1, -1, -1, -1}, {+1, +1, +1, -1, +1, -1, -1, +1}, {+1, -1, +1, +1, +1, +1, -1, -1},
+    {+1, +1, -1, +1, +1, -1, +1, -1}, {+1, -1, -1, -1, +1, +1, +1, +1}, {+1, +1, -1, +1, -1, +1, -1, +1},
+    {+1, +1, +1, -1, -1, +1, +1, -1}, {+1, -1, +1, +1, -1, -1, +1, +1}};
+
+constexpr int kBM = 128, kBN = 128;
+constexpr int kGemmThreads = 256;
+
+// B[i*out_o + n][j*in_o + k] = S[i][j] * code(W[i^j][n][k]), from packed
+// codes [8, out_o, ceil(in_o/4)]; row length Kp (>= 8*in_o, zero padded).
+template <typename T>
+__global__ void octonion_expand_kernel(const uint8_t *__restrict__ packed, int in_o, int out_o, int Kp,
+                                       T *__restrict__ B) {
+    const int64_t N = 8LL * out_o;
+    const int64_t total = N * Kp;
+    const int kp4 = (int)ceil_div(in_o, 4);
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = e / Kp;
+        const int col = (int)(e - row * Kp);
+        float v = 0.f;
+        if (col < 8 * in_o) {
+            const int i = (int)(row / out_o), n = (int)(row - (int64_t)i * out_o);
+            const int j = col / in_o, k = col - j * in_o;
+            const int w = i ^ j;
+            const uint32_t byte = packed[((int64_t)w * out_o + n) * kp4 + k / 4];
+            const int code = (int)((byte >> (6 - 2 * (k & 3))) & 3u) - 1;
+            v = (float)(kOctSign[i][j] * code);
+        }
+        Act<T>::store(B + e, v);
+    }
+}
+
+// -------------------------------------------------------------------- GEMM
+// y[m, n] = beta[n % out_o] * sum_k x[m, k] B[n, k]
+// T = uint16_t (bf16 operands, 16x16x32 bf16 MFMA) or float (16x16x4 f32 MFMA).
+template <typename T> struct GemmCfg;
+template <> struct GemmCfg<uint16_t> { static constexpr int BK = 32; };  // 64 B per row
+template <> struct GemmCfg<float> { static constexpr int BK = 16; };     // 64 B per row
+constexpr int kLdsStride = 80;  // 64 B + 16 B pad: 8 consecutive rows cover all banks once
+
+struct OctArgs {
+    const void *x;
+    int64_t ldx;
+    int M, N, K, Kp;     // K = 8*in_o (multiple of 8), Kp = B row length
+    const void *B;
+    const float *beta;
+    int out_o;
+    void *y;
+    int64_t ldy;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs a) {
+    constexpr int BK = GemmCfg<T>::BK;
+    constexpr uint32_t esz = sizeof(T);
+    __shared__ __align__(16) unsigned char lds[2][2][kBM * kLdsStride];  // [buf][A/B]
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.B, (uint32_t)((int64_t)a.N * a.Kp * esz));
+
+    // global -> register staging: a 128-row x 64-byte tile is 512 chunks of
+    // 16 B; thread t moves chunks t and t + 256 of A and of B per K step
+    const int ch0 = tid, ch1 = tid + kGemmThreads;  // chunk id = row*4 + part
+    const int ra0 = ch0 >> 2, pa0 = ch0 & 3, ra1 = ch1 >> 2, pa1 = ch1 & 3;
+    constexpr int kElemsPerChunk = 16 / esz;
+
+    auto load_tile = [&](int k0, u32x4 (&ra)[2], u32x4 (&rb)[2]) {
+        const int ka0 = k0 + pa0 * kElemsPerChunk, ka1 = k0 + pa1 * kElemsPerChunk;
+        const int am0 = m0 + ra0, am1 = m0 + ra1;
+        ra[0] = __builtin_amdgcn_raw_buffer_load_b128(
+            xr, (am0 < a.M && ka0 < a.K) ? (uint32_t)(((int64_t)am0 * a.ldx + ka0) * esz) : kOOB, 0, 0);
+        ra[1] = __builtin_amdgcn_raw_buffer_load_b128(
+            xr, (am1 < a.M && ka1 < a.K) ? (uint32_t)(((int64_t)am1 * a.ldx + ka1) * esz) : kOOB, 0, 0);
+        const int bn0 = n0 + ra0, bn1 = n0 + ra1;
+        rb[0] = __builtin_amdgcn_raw_buffer_load_b128(
+            br, (bn0 < a.N && ka0 < a.Kp) ? (uint32_t)(((int64_t)bn0 * a.Kp + ka0) * esz) : kOOB, 0, 0);
+        rb[1] = __builtin_amdgcn_raw_buffer_load_b128(
+            br, (bn1 < a.N && ka1 < a.Kp) ? (uint32_t)(((int64_t)bn1 * a.Kp + ka1) * esz) : kOOB, 0, 0);
+    };
+    auto store_tile = [&](int buf, const u32x4 (&ra)[2], const u32x4 (&rb)[2]) {
+        *(u32x4 *)(&lds[buf][0][ra0 * kLdsStride + pa0 * 16]) = ra[0];
+        *(u32x4 *)(&lds[buf][0][ra1 * kLdsStride + pa1 * 16]) = ra[1];
+        *(u32x4 *)(&lds[buf][1][ra0 * kLdsStride + pa0 * 16]) = rb[0];
+        *(u32x4 *)(&lds[buf][1][ra1 * kLdsStride + pa1 * 16]) = rb[1];
+    };
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int nk = (int)ceil_div(a.K, BK);
+    u32x4 ra[2], rb[2];
+    load_tile(0, ra, rb);
+    store_tile(0, ra, rb);
+    __syncthreads();
+
+    const int fr = lane & 15, fq = lane >> 4;  // fragment row, 16-byte chunk
+    for (int kk = 0; kk < nk; ++kk) {
+        const int cur = kk & 1;
+        if (kk + 1 < nk) load_tile((kk + 1) * BK, ra, rb);
+        u32x4 af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            af[i] = *(const u32x4 *)(&lds[cur][0][(wm * 64 + i * 16 + fr) * kLdsStride + fq * 16]);
+            bf[i] = *(const u32x4 *)(&lds[cur][1][(wn * 64 + i * 16 + fr) * kLdsStride + fq * 16]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (sizeof(T) == 2) {
+                    // A rows = tokens (i), B rows = outputs (j): D[token][out]
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
+                                                                        __builtin_bit_cast(bf16x8, bf[j]), acc[i][j],
+                                                                        0, 0, 0);
+                } else {
+                    const f32x4 av = __builtin_bit_cast(f32x4, af[i]);
+                    const f32x4 bv = __builtin_bit_cast(f32x4, bf[j]);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc[i][j], 0, 0, 0);
+                }
+            }
+        if (kk + 1 < nk) store_tile(cur ^ 1, ra, rb);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds D[m = 4*fq + r][n = fr] of each 16x16 tile
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * esz));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 64 + j * 16 + fr;
+        const float b = n < a.N ? a.beta[n % a.out_o] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm * 64 + i * 16 + 4 * fq + r;
+                const uint32_t off = (m < a.M && n < a.N) ? (uint32_t)(((int64_t)m * a.ldy + n) * esz) : kOOB;
+                Buf4<T>::store1(acc[i][j][r] * b, yr, off, 0);
+            }
+    }
+}
+
+}  // namespace walsh
+
+using namespace walsh;
+
+WALSH_EXPORT int64_t walsh_octonion_weight_elems(int64_t in_o, int64_t out_o) {
+    if (in_o <= 0 || out_o <= 0) return 0;
+    return 8 * out_o * ceil_div(8 * in_o, 32) * 32;
+}
+
+WALSH_EXPORT int walsh_octonion_prepare(const uint8_t *packed, int64_t in_o, int64_t out_o, void *B, int dtype,
+                                        void *stream) {
+    if (!packed || !B) return set_error(WALSH_EINVAL, "walsh_octonion_prepare: null pointer");
+    if (in_o <= 0 || out_o <= 0 || in_o > 65536 || out_o > 65536)
+        return set_error(WALSH_EINVAL, "walsh_octonion_prepare: bad shape");
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "walsh_octonion_prepare: dtype");
+    const int Kp = (int)(ceil_div(8 * in_o, 32) * 32);
+    const int64_t total = 8 * out_o * (int64_t)Kp;
+    const int block = 256;
+    int64_t grid = ceil_div(total, block);
+    if (grid > 8192) grid = 8192;
+    if (dtype == WALSH_BF16)
+        hipLaunchKernelGGL(octonion_expand_kernel<uint16_t>, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream,
+                           packed, (int)in_o, (int)out_o, Kp, (uint16_t *)B);
+    else
+        hipLaunchKernelGGL(octonion_expand_kernel<float>, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream,
+                           packed, (int)in_o, (int)out_o, Kp, (float *)B);
+    return check_hip(hipGetLastError(), "walsh_octonion_prepare launch");
+}
+
+WALSH_EXPORT int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                                           const void *B, const float *beta, void *y, int64_t ldy, int dtype,
+                                           void *stream) {
+    if (!x || !B || !beta || !y) return set_error(WALSH_EINVAL, "walsh_octonion_linear_fwd: null pointer");
+    if (M < 0 || in_o <= 0 || out_o <= 0 || ldx < 8 * in_o || ldy < 8 * out_o)
+        return set_error(WALSH_EINVAL, "walsh_octonion_linear_fwd: bad shape M=%lld in_o=%lld out_o=%lld",
+                         (long long)M, (long long)in_o, (long long)out_o);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "walsh_octonion_linear_fwd: dtype");
+    if (M == 0) return WALSH_OK;
+    const int64_t esz = dtype == WALSH_BF16 ? 2 : 4;
+    const int64_t vec = 16 / esz;
+    if (ldx % vec || (uintptr_t)x % 16 || (uintptr_t)B % 16 || (8 * in_o) % vec)
+        return set_error(WALSH_ENOTSUP, "walsh_octonion_linear_fwd: x/B must be 16-byte aligned rows");
+    const int64_t N = 8 * out_o, K = 8 * in_o, Kp = ceil_div(K, 32) * 32;
+    if (N * Kp * esz > (int64_t)kMaxBufferBytes) return set_error(WALSH_ENOTSUP, "walsh_octonion_linear_fwd: too large");
+    const int64_t ld = ldx > ldy ? ldx : ldy;
+    int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / kBM * kBM;
+    if (rows_max < kBM) return set_error(WALSH_ENOTSUP, "walsh_octonion_linear_fwd: row stride too large");
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        OctArgs a;
+        a.x = (const char *)x + r0 * ldx * esz;
+        a.ldx = ldx;
+        a.M = (int)rows;
+        a.N = (int)N;
+        a.K = (int)K;
+        a.Kp = (int)Kp;
+        a.B = B;
+        a.beta = beta;
+        a.out_o = (int)out_o;
+        a.y = (char *)y + r0 * ldy * esz;
+        a.ldy = ldy;
+        const dim3 G((unsigned)ceil_div(rows, kBM), (unsigned)ceil_div(N, kBN)), Bk(kGemmThreads);
+        if (dtype == WALSH_BF16)
+            hipLaunchKernelGGL(octonion_gemm_kernel<uint16_t>, G, Bk, 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL(octonion_gemm_kernel<float>, G, Bk, 0, (hipStream_t)stream, a);
+        const int rc = check_hip(hipGetLastError(), "walsh_octonion_linear_fwd launch");
+        if (rc) return rc;
+    }
+    return WALSH_OK;
+}

@@ -1,0 +1,69 @@
+"""Shared host-side helpers for the nn.Module layer."""
+import torch
+
+
+def act_dtype(x: torch.Tensor) -> torch.dtype:
+    """Activation dtype the hot-path kernels compute in for input ``x``.
+
+    Under ``torch.autocast('cuda', dtype=bf16)`` -- how the reference runs bf16
+    (train.py:107, generate.py:134) -- it is the autocast dtype; otherwise the
+    input's own dtype (float32 or bfloat16)."""
+    if x.is_cuda and torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return x.dtype
+
+
+class WeightCache:
+    """Caches a device-side derivative of a parameter (its ternary codes,
+    packed layouts, concatenations ...) until the parameter changes.
+
+    The key is (data_ptr, _version, device, shape): an optimizer step bumps
+    ``_version`` and a ``.to()`` moves ``data_ptr``, so either rebuilds."""
+
+    def __init__(self):
+        self._key = None
+        self._val = None
+
+    def get(self, tensors, build, extra=()):
+        key = tuple((t.data_ptr(), t._version, t.device, tuple(t.shape), t.dtype) for t in tensors) + tuple(extra)
+        if key != self._key:
+            self._val = build()
+            self._key = key
+        return self._val
+
+    def clear(self):
+        self._key = None
+        self._val = None
+
+
+def adjacent_parts_view(parts, width: int):
+    """If ``parts`` are equal-shape slices laid side by side along the last
+    dim of one tensor (what ``x.split(width, -1)`` returns), return the
+    covering view without copying; otherwise None."""
+    p0 = parts[0]
+    if p0.shape[-1] != width or p0.stride(-1) != 1:
+        return None
+    esz = p0.element_size()
+    base = p0.data_ptr()
+    for i, p in enumerate(parts):
+        if p.shape != p0.shape or p.stride() != p0.stride() or p.dtype != p0.dtype:
+            return None
+        if p.data_ptr() != base + i * width * esz:
+            return None
+    full = width * len(parts)
+    if p0.dim() >= 2 and p0.stride(-2) < full:
+        return None
+    return torch.as_strided(p0, p0.shape[:-1] + (full,), p0.stride(), p0.storage_offset())
+
+
+class NoBackward(torch.autograd.Function):
+    """Marks outputs of forward-only HIP ops: calling backward raises."""
+
+    @staticmethod
+    def forward(ctx, name, *tensors):
+        ctx.name = name
+        return tensors[0] if len(tensors) == 1 else tensors
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(f"{ctx.name}: this build implements the forward pass only")

@@ -1,0 +1,274 @@
+"""Walsh configuration, layer factories and the transformer harness around
+the hot path (module surface of src/model/chassis.py).
+
+The hot-path layers (Hadamard / octonion ternary linears, Hadamard MoE) run
+on HIP kernels; attention (SDPA), RoPE, RMSNorm, embeddings and the head
+mixers stay PyTorch operations on the GPU.  Class names, constructor
+signatures, parameter names, shapes and the order in which parameters are
+created (hence the RNG stream consumed by seeded initialisation) follow the
+reference.
+"""
+import math
+from dataclasses import dataclass
+from typing import List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+from torch.nn import functional as F
+
+from .hadamard import HadamardLinear, HadamardTernaryLinear, HadamardTernaryLinearTuple  # noqa: F401
+from .hadamard import HadamardHeadMixer, HadamardHeadMixerFused
+from .octonion import OctonionHeadMixerFused, OctonionTernaryLinear
+from ._common import act_dtype
+
+_HADAMARD_AVAILABLE = True
+_HADAMARD_HEAD_MIXER_AVAILABLE = True
+
+
+@dataclass
+class WalshConfig:
+    """chassis.py:33-51 (fields and defaults unchanged)."""
+    block_size: int = 256
+    vocab_size: int = 65
+    n_layer: int = 6
+    n_head: int = 6
+    n_embd: int = 768
+    dropout: float = 0.0
+    bias: bool = False
+    head_mixing: bool = False
+    algebra: str = "octonion"
+    hash_embeddings: bool = False
+    use_moe: bool = False
+    moe_threshold: float = 0.1
+    moe_min_experts: int = 1
+    moe_max_experts: int = 4
+    use_channel_mod: bool = False
+
+
+def get_linear_layer(config: WalshConfig):
+    """(LayerClass, algebra_dim) for the configured algebra (chassis.py:54-65)."""
+    if config.algebra == "hadamard":
+        return HadamardTernaryLinearTuple, 32
+    return OctonionTernaryLinear, 8
+
+
+def get_head_mixer(config: WalshConfig, head_dim: int):
+    """Head mixer for the configured algebra, or None (chassis.py:68-94)."""
+    if not config.head_mixing:
+        return None
+    if config.algebra == "hadamard":
+        if config.n_head % 32 != 0:
+            raise ValueError(f"Hadamard head_mixing requires n_head % 32 == 0, got {config.n_head}")
+        return HadamardHeadMixerFused(head_dim)
+    if config.n_head % 8 != 0:
+        raise ValueError(f"Octonion head_mixing requires n_head % 8 == 0, got {config.n_head}")
+    return OctonionHeadMixerFused(head_dim)
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2) + eps) * weight, computed in float32 (chassis.py:96-106)."""
+
+    def __init__(self, dim, eps=1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def _norm(self, x):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
+
+    def forward(self, x):
+        return self._norm(x.float()).type_as(x) * self.weight
+
+
+class KVCache:
+    """Per-layer K/V cache (chassis.py:262-330), extended to a batch
+    dimension: tensors [batch, max_seq_len, n_head, head_dim] (batch=1 is the
+    reference's layout with the batch axis kept)."""
+
+    def __init__(self, n_layers: int, max_seq_len: int, n_head: int, head_dim: int,
+                 device: torch.device, dtype: torch.dtype = torch.bfloat16, batch: int = 1):
+        self.n_layers = n_layers
+        self.max_seq_len = max_seq_len
+        self.n_head = n_head
+        self.head_dim = head_dim
+        self.batch = batch
+        self.k_cache: List[torch.Tensor] = [
+            torch.zeros(batch, max_seq_len, n_head, head_dim, device=device, dtype=dtype) for _ in range(n_layers)]
+        self.v_cache: List[torch.Tensor] = [
+            torch.zeros(batch, max_seq_len, n_head, head_dim, device=device, dtype=dtype) for _ in range(n_layers)]
+        self.cached_len = 0
+
+    def update(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        b, new_len = k.shape[0], k.shape[1]
+        assert b <= self.batch, f"batch {b} exceeds cache batch {self.batch}"
+        s, e = self.cached_len, self.cached_len + new_len
+        assert e <= self.max_seq_len, "KV cache overflow"
+        self.k_cache[layer_idx][:b, s:e] = k.to(self.k_cache[layer_idx].dtype)
+        self.v_cache[layer_idx][:b, s:e] = v.to(self.v_cache[layer_idx].dtype)
+        return self.k_cache[layer_idx][:b, :e], self.v_cache[layer_idx][:b, :e]
+
+    def increment(self, n: int = 1):
+        self.cached_len += n
+
+    def reset(self):
+        self.cached_len = 0
+
+
+def precompute_freqs_cis(dim: int, end: int, theta: float = 10000.0):
+    """RoPE table (chassis.py:332-337)."""
+    freqs = 1.0 / (theta ** (torch.arange(0, dim, 2)[: (dim // 2)].float() / dim))
+    t = torch.arange(end, device=freqs.device)
+    freqs = torch.outer(t, freqs).float()
+    return torch.polar(torch.ones_like(freqs), freqs)
+
+
+def apply_rotary_emb(xq, xk, freqs_cis):
+    """Complex rotation of (q, k) pairs (chassis.py:339-345)."""
+    xq_ = torch.view_as_complex(xq.float().reshape(*xq.shape[:-1], -1, 2))
+    xk_ = torch.view_as_complex(xk.float().reshape(*xk.shape[:-1], -1, 2))
+    freqs_cis = freqs_cis[:xq.shape[1]].unsqueeze(0).unsqueeze(2)
+    xq_out = torch.view_as_real(xq_ * freqs_cis).flatten(3)
+    xk_out = torch.view_as_real(xk_ * freqs_cis).flatten(3)
+    return xq_out.type_as(xq), xk_out.type_as(xk)
+
+
+class OctonionHeadMixer(OctonionHeadMixerFused):
+    """chassis.py:347-399: same parameters and result as the fused mixer."""
+
+
+def _full(layer, x):
+    """Apply a tuple-interface ternary linear to a full [.., C] tensor."""
+    return layer.forward_full(x)
+
+
+class CausalSelfAttention(nn.Module):
+    """chassis.py:401-483.  q/k/v/o are the algebra's ternary linears applied
+    to whole rows (identical to split -> layer -> cat)."""
+
+    def __init__(self, config):
+        super().__init__()
+        self.n_head = config.n_head
+        self.n_embd = config.n_embd
+        self.head_dim = config.n_embd // config.n_head
+        self.head_mixing = config.head_mixing
+        LinearLayer, self.algebra_dim = get_linear_layer(config)
+        self.mixer_dim = 32 if config.algebra == "hadamard" else 8
+        self.wq = LinearLayer(config.n_embd, config.n_embd)
+        self.wk = LinearLayer(config.n_embd, config.n_embd)
+        self.wv = LinearLayer(config.n_embd, config.n_embd)
+        self.wo = LinearLayer(config.n_embd, config.n_embd)
+        self.dropout = config.dropout
+        self.head_mixer = get_head_mixer(config, self.head_dim)
+
+    def forward(self, x, freqs_cis, kv_cache: Optional[KVCache] = None, layer_idx: int = 0):
+        B, T, C = x.size()
+        dt = act_dtype(x)
+        x = x.to(dt)
+        q = _full(self.wq, x).view(B, T, self.n_head, self.head_dim)
+        k = _full(self.wk, x).view(B, T, self.n_head, self.head_dim)
+        v = _full(self.wv, x).view(B, T, self.n_head, self.head_dim)
+        q, k = apply_rotary_emb(q, k, freqs_cis)
+        if kv_cache is not None:
+            k, v = kv_cache.update(layer_idx, k, v)
+        q = q.transpose(1, 2)
+        k = k.transpose(1, 2).to(q.dtype)
+        v = v.transpose(1, 2).to(q.dtype)
+        drop = self.dropout if self.training else 0
+        if kv_cache is not None and kv_cache.cached_len > 0:
+            total = k.size(2)
+            mask = torch.ones(T, total, dtype=torch.bool, device=q.device).tril(diagonal=total - T)
+            y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=drop)
+        else:
+            y = F.scaled_dot_product_attention(q, k, v, is_causal=True, dropout_p=drop)
+        if self.head_mixer is not None:
+            n_groups = self.n_head // self.mixer_dim
+            yg = y.view(B, n_groups, self.mixer_dim, T, self.head_dim)
+            y = torch.cat([self.head_mixer(yg[:, g]) for g in range(n_groups)], dim=1)
+        y = y.transpose(1, 2).contiguous().view(B, T, C).to(dt)
+        return _full(self.wo, y)
+
+
+class SwiGLUMLP(nn.Module):
+    """down(silu(gate(x)) * up(x)) with ternary algebra linears (chassis.py:485-507)."""
+
+    def __init__(self, config):
+        super().__init__()
+        LinearLayer, self.algebra_dim = get_linear_layer(config)
+        hidden_dim = 4 * config.n_embd
+        hidden_dim = int(2 * hidden_dim / 3)
+        hidden_dim = math.ceil(hidden_dim / self.algebra_dim) * self.algebra_dim
+        self.gate_proj = LinearLayer(config.n_embd, hidden_dim)
+        self.up_proj = LinearLayer(config.n_embd, hidden_dim)
+        self.down_proj = LinearLayer(hidden_dim, config.n_embd)
+
+    def forward(self, x):
+        x = x.to(act_dtype(x))
+        h = F.silu(_full(self.gate_proj, x)) * _full(self.up_proj, x)
+        return _full(self.down_proj, h)
+
+
+class LlamaBlock(nn.Module):
+    """Pre-norm residual block (chassis.py:509-531)."""
+
+    def __init__(self, config):
+        super().__init__()
+        self.attention_norm = RMSNorm(config.n_embd)
+        self.attention = CausalSelfAttention(config)
+        self.ffn_norm = RMSNorm(config.n_embd)
+        if getattr(config, 'use_moe', False):
+            from .moe import HadamardMoE
+            self.feed_forward = HadamardMoE(
+                config,
+                threshold=getattr(config, 'moe_threshold', 0.1),
+                min_experts=getattr(config, 'moe_min_experts', 1),
+                max_experts=getattr(config, 'moe_max_experts', 4),
+            )
+        else:
+            self.feed_forward = SwiGLUMLP(config)
+
+    def forward(self, x, freqs_cis, kv_cache: Optional[KVCache] = None, layer_idx: int = 0):
+        dt = act_dtype(x)
+        h = x + self.attention(self.attention_norm(x).to(dt), freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
+        return h + self.feed_forward(self.ffn_norm(h).to(dt))
+
+
+class Walsh(nn.Module):
+    """Single-stream Walsh model (chassis.py:533-668)."""
+
+    def __init__(self, config):
+        super().__init__()
+        if config.hash_embeddings:
+            raise NotImplementedError("hash embeddings are outside this build's scope")
+        self.config = config
+        self.tok_embeddings = nn.Embedding(config.vocab_size, config.n_embd)
+        self.output = nn.Linear(config.n_embd, config.vocab_size, bias=False)
+        self.tok_embeddings.weight = self.output.weight
+        self.layers = nn.ModuleList([LlamaBlock(config) for _ in range(config.n_layer)])
+        self.norm = RMSNorm(config.n_embd)
+        self.register_buffer("freqs_cis", precompute_freqs_cis(config.n_embd // config.n_head, config.block_size * 2))
+        self.apply(self._init_weights)
+        for pn, p in self.named_parameters():
+            if pn.endswith('.beta'):
+                torch.nn.init.constant_(p, 0.1)
+
+    def _init_weights(self, module):
+        if isinstance(module, (nn.Linear, nn.Embedding)):
+            torch.nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+    def forward(self, idx, targets=None, kv_cache: Optional[KVCache] = None, start_pos: int = 0,
+                return_hidden: bool = False):
+        B, T = idx.shape
+        h = self.tok_embeddings(idx)
+        freqs_cis = self.freqs_cis[start_pos:start_pos + T]
+        for layer_idx, layer in enumerate(self.layers):
+            h = layer(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
+        h = self.norm(h)
+        if targets is not None:
+            logits = self.output(h)
+            loss = F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1))
+        else:
+            logits = self.output(h[:, [-1], :])
+            loss = None
+        if return_hidden:
+            return logits, loss, h
+        return logits, loss

@@ -1,0 +1,190 @@
+"""Hadamard-32 ternary linear layers on the fused HIP kernel.
+
+Module surface of src/model/fht_cuda.py (hadamard_matrix :32-56, packing
+:65-117, fht :281-337, HadamardTernaryLinear :344-427, HadamardLinear
+:436-519, HadamardTernaryLinearTuple :526-569, head mixers :576-670):
+same class names, constructor signatures, parameter/buffer names, shapes
+and initialisation; forward runs walsh_hadamard_linear_fwd.
+"""
+import math
+
+import torch
+import torch.nn as nn
+
+from . import kernels
+from ._common import WeightCache, act_dtype, adjacent_parts_view
+
+ALGEBRA_DIM = 32
+
+
+def hadamard_matrix(n: int, normalize: bool = True) -> torch.Tensor:
+    """Sylvester Hadamard matrix H_n (fht_cuda.py:32-56), float32."""
+    assert n > 0 and (n & (n - 1)) == 0, f"n must be power of 2, got {n}"
+    idx = torch.arange(n)
+    bits = (idx[:, None] & idx[None, :])
+    parity = torch.zeros_like(bits)
+    while bool(bits.any()):
+        parity ^= bits & 1
+        bits = bits >> 1
+    H = (1 - 2 * parity).to(torch.float32)
+    if normalize:
+        H = H / math.sqrt(n)
+    return H
+
+
+def pack_ternary_weights(w: torch.Tensor) -> torch.Tensor:
+    """Pack ternary values {-1,0,1} [.., K] -> uint8 [.., K/4] on the GPU
+    (fht_cuda.py:65-93): byte = v0<<6 | v1<<4 | v2<<2 | v3, v = w + 1."""
+    assert w.shape[-1] % 4 == 0, f"K dimension must be divisible by 4, got {w.shape[-1]}"
+    # values are already ternary: gamma = 1 leaves them unchanged
+    one = torch.ones(1, device=w.device, dtype=torch.float32)
+    return kernels.ternary_quantize(w.float(), gamma=one, packed=True)["packed"]
+
+
+def unpack_ternary_weights(packed: torch.Tensor, original_k: int) -> torch.Tensor:
+    """Inverse of pack_ternary_weights, float32 (fht_cuda.py:96-117)."""
+    return kernels.ternary_unpack(packed, original_k).float()
+
+
+def _init_latent(out_o: int, in_o: int) -> torch.Tensor:
+    # fht_cuda.py:459-466: N(0, 0.02), every group rescaled to Frobenius
+    # norm 0.02*sqrt(out_o*in_o)
+    w = torch.randn(ALGEBRA_DIM, out_o, in_o) * 0.02
+    norms = w.view(ALGEBRA_DIM, -1).norm(dim=1, keepdim=True).unsqueeze(-1)
+    return w / (norms + 1e-8) * 0.02 * math.sqrt(out_o * in_o)
+
+
+class _HadamardBase(nn.Module):
+    """Parameters and the HIP forward shared by the Hadamard linear classes."""
+
+    ALGEBRA_DIM = ALGEBRA_DIM
+
+    def _init_params(self, in_features: int, out_features: int):
+        assert in_features % ALGEBRA_DIM == 0, f"in_features must be divisible by {ALGEBRA_DIM}"
+        assert out_features % ALGEBRA_DIM == 0, f"out_features must be divisible by {ALGEBRA_DIM}"
+        self.in_o = in_features // ALGEBRA_DIM
+        self.out_o = out_features // ALGEBRA_DIM
+        self.weight = nn.Parameter(_init_latent(self.out_o, self.in_o))
+        self.alpha = nn.Parameter(torch.ones(ALGEBRA_DIM, self.in_o))
+        self.beta = nn.Parameter(torch.ones(ALGEBRA_DIM, self.out_o) * math.sqrt(3.0 / (2.0 * self.in_o)))
+        self._wcache = WeightCache()
+
+    def ternary_state(self):
+        """(gamma, packed codes, kernel layout) of the current weight, cached."""
+        w = self.weight
+
+        def build():
+            q = kernels.ternary_quantize(w, packed=True)
+            return q["gamma"], q["packed"], kernels.hadamard_prepare(q["packed"], self.in_o, self.out_o)
+
+        return self._wcache.get([w], build)
+
+    def _apply_2d(self, x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        _, _, kw = self.ternary_state()
+        return kernels.hadamard_linear(x if x.dtype == dtype else x.to(dtype), self.in_o, self.out_o, kw,
+                                       self.alpha, self.beta)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        assert x.shape[-1] == self.in_o * ALGEBRA_DIM, f"expected last dim {self.in_o * ALGEBRA_DIM}, got {x.shape[-1]}"
+        y = self._apply_2d(x, act_dtype(x))
+        return y.to(x.dtype)
+
+
+class HadamardTernaryLinear(_HadamardBase):
+    """y = beta * FHT(W_ternary * FHT(alpha * x)) (fht_cuda.py:344-427)."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False):
+        super().__init__()
+        self._init_params(in_features, out_features)
+
+    def extra_repr(self) -> str:
+        return f"in={self.in_o * ALGEBRA_DIM}, out={self.out_o * ALGEBRA_DIM}, algebra=hadamard32"
+
+
+class HadamardLinear(_HadamardBase):
+    """y = beta * H W_ternary H (alpha * x) (fht_cuda.py:436-519)."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False):
+        super().__init__()
+        self._init_params(in_features, out_features)
+        self.in_features = in_features
+        self.out_features = out_features
+        self.register_buffer('H', hadamard_matrix(ALGEBRA_DIM, normalize=True))
+
+
+class HadamardTernaryLinearTuple(nn.Module):
+    """Tuple interface over HadamardLinear (fht_cuda.py:526-569): 32 parts
+    [..., in_o] in, 32 views [..., out_o] out.  Parts that are adjacent
+    slices of one tensor (``x.split``) are read in place, without the cat."""
+
+    ALGEBRA_DIM = ALGEBRA_DIM
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False):
+        super().__init__()
+        self.inner = HadamardLinear(in_features, out_features, bias)
+        self.in_o = self.inner.in_o
+        self.out_o = self.inner.out_o
+
+    @property
+    def weight(self):
+        return self.inner.weight
+
+    @property
+    def beta(self):
+        return self.inner.beta
+
+    def forward_full(self, x: torch.Tensor) -> torch.Tensor:
+        """Whole rows [..., 32*in_o] -> [..., 32*out_o] in the activation dtype
+        (the same result as split -> forward -> cat, without the copies)."""
+        return self.inner._apply_2d(x, act_dtype(x))
+
+    def forward(self, x_parts: tuple) -> tuple:
+        assert len(x_parts) == ALGEBRA_DIM, f"Expected {ALGEBRA_DIM} parts, got {len(x_parts)}"
+        x = adjacent_parts_view(x_parts, self.in_o)
+        if x is None:
+            x = torch.cat(x_parts, dim=-1)
+        y = self.inner(x)
+        return tuple(y.split(self.out_o, dim=-1))
+
+
+def fht_butterfly(x: torch.Tensor) -> torch.Tensor:
+    """Normalised fast Hadamard transform along the last dim (any power of
+    two N <= 16384), fht_cuda.py:281-309, on the GPU."""
+    return kernels.fht(x, normalize=True)
+
+
+def fht(x: torch.Tensor) -> torch.Tensor:
+    """fht (fht_cuda.py:316-337): forward-only here."""
+    return kernels.fht(x, normalize=True)
+
+
+def fht_reference(x: torch.Tensor) -> torch.Tensor:
+    """fht_reference (fht_cuda.py:266-278) computes the same transform."""
+    return kernels.fht(x, normalize=True)
+
+
+class HadamardHeadMixerFused(nn.Module):
+    """Hadamard head mixer (fht_cuda.py:627-670), same parameters; runs as
+    torch einsums on the GPU (outside the hot path of this build)."""
+
+    ALGEBRA_DIM = ALGEBRA_DIM
+
+    def __init__(self, head_dim: int):
+        super().__init__()
+        self.head_dim = head_dim
+        self.W = nn.Parameter(torch.randn(ALGEBRA_DIM, head_dim, head_dim) * 0.02)
+        self.beta = nn.Parameter(torch.ones(head_dim) * math.sqrt(3.0 / (2.0 * head_dim)))
+        self.register_buffer('H', hadamard_matrix(ALGEBRA_DIM, normalize=True))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        B, Hh, T, D = x.shape
+        assert Hh == ALGEBRA_DIM
+        dt = x.dtype
+        H = self.H.to(dt).contiguous()          # symmetric: H^T x == H x
+        xf = torch.matmul(H, x.reshape(B, Hh, T * D).contiguous()).view(B, Hh, T, D)
+        y = torch.matmul(xf, self.W.to(dt).contiguous())
+        yf = torch.matmul(H, y.reshape(B, Hh, T * D).contiguous()).view(B, Hh, T, D)
+        return yf * self.beta.to(dt)
+
+
+HadamardHeadMixer = HadamardHeadMixerFused

@@ -127,3 +127,111 @@ def hadamard_linear(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tenso
     _hip.call("walsh_hadamard_linear_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, kweight.data_ptr(),
               alpha.data_ptr(), beta.data_ptr(), y.data_ptr(), 32 * out_o, code, _hip.stream(x.device))
     return y
+
+
+def fht(x: torch.Tensor, normalize: bool = True) -> torch.Tensor:
+    """Fast Walsh-Hadamard transform along the last dim (fht_cuda.py:281-309)."""
+    _hip.require_device(x, "input")
+    N = x.shape[-1]
+    dt = x.dtype if x.dtype in (torch.float32, torch.bfloat16) else torch.float32
+    xc = x.to(dt).contiguous()
+    y = torch.empty_like(xc)
+    rows = xc.numel() // N if N else 0
+    _hip.call("walsh_fht_fwd", xc.data_ptr(), rows, N, int(bool(normalize)), y.data_ptr(), _hip.dtype_code(dt),
+              _hip.stream(x.device))
+    return y
+
+
+# ------------------------------------------------------------------ octonion
+
+def octonion_prepare(packed: torch.Tensor, in_o: int, out_o: int, dtype: torch.dtype) -> torch.Tensor:
+    """Dense signed-permutation block matrix [8*out_o, Kp] (elements of dtype)
+    from packed codes [8, out_o, ceil(in_o/4)]."""
+    _hip.require_device(packed, "packed weight")
+    assert tuple(packed.shape) == (8, out_o, (in_o + 3) // 4), f"packed shape {tuple(packed.shape)}"
+    n = _hip.lib().walsh_octonion_weight_elems(in_o, out_o)
+    B = torch.empty(n, device=packed.device, dtype=dtype)
+    _hip.call("walsh_octonion_prepare", packed.contiguous().data_ptr(), in_o, out_o, B.data_ptr(),
+              _hip.dtype_code(dtype), _hip.stream(packed.device))
+    return B
+
+
+def octonion_linear(x: torch.Tensor, in_o: int, out_o: int, B: torch.Tensor, beta: torch.Tensor) -> torch.Tensor:
+    """Cayley-Dickson ternary linear on full rows x [..., 8*in_o] -> [..., 8*out_o]
+    (physics.py:66-82); B from octonion_prepare in x.dtype."""
+    _hip.require_device(x, "input")
+    assert B.dtype == x.dtype, "prepared weight dtype must match the activation dtype"
+    K = 8 * in_o
+    lead = x.shape[:-1]
+    xv, rows, ldx = _rows_view(x, K)
+    y = torch.empty(lead + (8 * out_o,), device=x.device, dtype=x.dtype)
+    if rows == 0:
+        return y
+    vec = 16 // x.element_size()
+    if ldx % vec or xv.data_ptr() % 16:
+        xv = xv.reshape(rows, -1)[:, :K].contiguous()
+        ldx = K
+    beta = beta.detach().float().contiguous()
+    _hip.call("walsh_octonion_linear_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, B.data_ptr(), beta.data_ptr(),
+              y.data_ptr(), 8 * out_o, _hip.dtype_code(x.dtype), _hip.stream(x.device))
+    return y
+
+
+# ------------------------------------------------------------------ mHC
+
+def sinkhorn(h: torch.Tensor, n_iter: int = 20, eps: float = 1e-8) -> torch.Tensor:
+    """SinkhornKnopp.forward (mhc.py:214-229) on [..., n, n] (computed in float32)."""
+    _hip.require_device(h, "H")
+    n = h.shape[-1]
+    assert h.shape[-2] == n, "Sinkhorn needs square matrices"
+    hf = h.detach().float().contiguous()
+    out = torch.empty_like(hf)
+    batch = hf.numel() // (n * n)
+    _hip.call("walsh_sinkhorn_fwd", hf.data_ptr(), batch, n, int(n_iter), float(eps), out.data_ptr(),
+              _hip.stream(h.device))
+    return out
+
+
+def mhc_pre(x: torch.Tensor, phi_cat: torch.Tensor, coef: torch.Tensor, bias_cat: torch.Tensor, rms_eps: float,
+            n_iter: int = 20, sk_eps: float = 1e-8):
+    """Fused mappings + H_pre @ x for x [..., n, C] (mhc.py:283-318, 345-364).
+
+    phi_cat [32, n*C] in x.dtype (rows pre|post|res|0), coef float32 [3],
+    bias_cat float32 [2n + n*n].  Returns (layer_in [..., C], H_pre [..., n],
+    H_post [..., n], H_res [..., n, n]) with the H's in float32."""
+    _hip.require_device(x, "stream input")
+    n, C = x.shape[-2], x.shape[-1]
+    lead = x.shape[:-2]
+    xv = x if x.is_contiguous() else x.contiguous()
+    M = xv.numel() // (n * C)
+    dev = x.device
+    layer_in = torch.empty(lead + (C,), device=dev, dtype=x.dtype)
+    h_pre = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_post = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_res = torch.empty(lead + (n, n), device=dev, dtype=torch.float32)
+    if M == 0:
+        return layer_in, h_pre, h_post, h_res
+    assert phi_cat.dtype == x.dtype and tuple(phi_cat.shape) == (32, n * C), "phi_cat layout"
+    _hip.call("walsh_mhc_pre_fwd", xv.data_ptr(), n * C, M, n, C, phi_cat.data_ptr(), coef.data_ptr(),
+              bias_cat.data_ptr(), float(rms_eps), int(n_iter), float(sk_eps), h_pre.data_ptr(), h_post.data_ptr(),
+              h_res.data_ptr(), layer_in.data_ptr(), C, _hip.dtype_code(x.dtype), _hip.stream(dev))
+    return layer_in, h_pre, h_post, h_res
+
+
+def mhc_post(x: torch.Tensor, out: torch.Tensor, h_res: torch.Tensor, h_post: torch.Tensor) -> torch.Tensor:
+    """x_new = H_res @ x + H_post^T (x) out (mhc.py:366-381); x [..., n, C], out [..., C]."""
+    _hip.require_device(x, "stream input")
+    n, C = x.shape[-2], x.shape[-1]
+    xv = x if x.is_contiguous() else x.contiguous()
+    M = xv.numel() // (n * C)
+    o = out.to(x.dtype)
+    o = o if o.is_contiguous() else o.contiguous()
+    assert o.numel() == M * C, "layer output shape"
+    x_new = torch.empty_like(xv)
+    if M == 0:
+        return x_new
+    hr = h_res.detach().float().contiguous()
+    hp = h_post.detach().float().contiguous()
+    _hip.call("walsh_mhc_post_fwd", xv.data_ptr(), n * C, o.data_ptr(), C, hr.data_ptr(), hp.data_ptr(),
+              x_new.data_ptr(), n * C, M, n, C, _hip.dtype_code(x.dtype), _hip.stream(x.device))
+    return x_new

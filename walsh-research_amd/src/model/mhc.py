@@ -1,0 +1,312 @@
+"""Manifold-constrained hyper-connections (module surface of src/model/mhc.py).
+
+SinkhornKnopp / sinkhorn_knopp_fused -> walsh_sinkhorn_fwd;
+mHCResidualStream.forward -> walsh_mhc_pre_fwd (RMS scale, the three phi
+projections, sigmoid / 2*sigmoid / Sinkhorn and H_pre @ x in one pass), the
+layer function, then walsh_mhc_post_fwd (H_res @ x + H_post^T (x) out).
+"""
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import kernels
+from ._common import WeightCache, act_dtype
+
+_MAX_STREAMS = 4
+
+
+def sinkhorn_knopp_fused(H_tilde, n_iter=20):
+    """Doubly-stochastic projection of [..., n, n] (mhc.py:152-195), float32."""
+    return kernels.sinkhorn(H_tilde, n_iter=n_iter, eps=1e-8)
+
+
+class SinkhornKnopp(nn.Module):
+    """M = exp(H); n_iter x {column-normalise, row-normalise} (mhc.py:198-229)."""
+
+    def __init__(self, n_iter=20, eps=1e-8):
+        super().__init__()
+        self.n_iter = n_iter
+        self.eps = eps
+
+    def forward(self, H):
+        return kernels.sinkhorn(H, n_iter=self.n_iter, eps=self.eps)
+
+
+def _rms_eps(dtype: torch.dtype) -> float:
+    # F.rms_norm(x, ...) with eps=None uses finfo(x.dtype).eps (mhc.py:291);
+    # rms_norm has no autocast rule, so x keeps the activation dtype
+    return float(torch.finfo(dtype).eps)
+
+
+def _phi_block(n: int, C: int, parts, dtype, device):
+    """[32, n*C] projection in the activation dtype: rows pre|post|res, zero padded."""
+    out = torch.zeros(32, n * C, device=device, dtype=dtype)
+    r = 0
+    for w, rows in parts:
+        if w is not None:
+            out[r:r + rows] = w.detach().to(dtype)
+        r += rows
+    return out
+
+
+class ResidualStreamMapping(nn.Module):
+    """H = P(alpha * phi(rms_norm(x)) + bias) with P = sigmoid ('pre'),
+    2*sigmoid ('post') or Sinkhorn ('res') (mhc.py:232-318)."""
+
+    def __init__(self, n_embd, n_streams, mapping_type='res'):
+        super().__init__()
+        self.n_embd = n_embd
+        self.n_streams = n_streams
+        self.mapping_type = mapping_type
+        self.alpha = nn.Parameter(torch.tensor(0.01))
+        if mapping_type == 'res':
+            self.phi = nn.Linear(n_streams * n_embd, n_streams * n_streams, bias=False)
+            self.bias = nn.Parameter(torch.zeros(n_streams, n_streams))
+            self.sinkhorn = SinkhornKnopp(n_iter=20)
+            with torch.no_grad():
+                self.bias.copy_(torch.eye(n_streams) * 2.0)
+        elif mapping_type == 'pre':
+            self.phi = nn.Linear(n_streams * n_embd, n_streams, bias=False)
+            self.bias = nn.Parameter(torch.zeros(1, n_streams))
+        elif mapping_type == 'post':
+            self.phi = nn.Linear(n_streams * n_embd, n_streams, bias=False)
+            self.bias = nn.Parameter(torch.zeros(1, n_streams))
+        nn.init.normal_(self.phi.weight, std=0.01)
+        self._cache = WeightCache()
+
+    def forward(self, x):
+        """x [B, T, n*C] -> [B, T, n, n] ('res') or [B, T, 1, n]."""
+        n, C = self.n_streams, self.n_embd
+        if n > _MAX_STREAMS:
+            raise NotImplementedError(f"n_streams={n} > {_MAX_STREAMS} is not supported by this build")
+        B, T, _ = x.shape
+        dt = act_dtype(x)
+        slot = {'pre': 0, 'post': 1, 'res': 2}[self.mapping_type]
+
+        def build():
+            ws = [None, None, None]
+            ws[slot] = self.phi.weight
+            phi = _phi_block(n, C, [(ws[0], n), (ws[1], n), (ws[2], n * n)], dt, x.device)
+            coef = torch.zeros(3, device=x.device)
+            coef[slot] = self.alpha.detach().float()
+            bias = torch.zeros(2 * n + n * n, device=x.device)
+            off = [0, n, 2 * n][slot]
+            bias[off:off + self.bias.numel()] = self.bias.detach().float().reshape(-1)
+            return phi, coef, bias
+
+        phi, coef, bias = self._cache.get([self.phi.weight, self.alpha, self.bias], build, extra=(dt, x.device))
+        xs = x.to(dt).reshape(B, T, n, C)
+        _, hp, hq, hr = kernels.mhc_pre(xs, phi, coef, bias, _rms_eps(dt))
+        if self.mapping_type == 'res':
+            return hr
+        return (hp if self.mapping_type == 'pre' else hq).unsqueeze(2)
+
+
+class mHCResidualStream(nn.Module):
+    """x_{l+1} = H_res @ x_l + H_post^T F(H_pre @ x_l) (mhc.py:321-381)."""
+
+    def __init__(self, n_embd, n_streams=4):
+        super().__init__()
+        self.n_embd = n_embd
+        self.n_streams = n_streams
+        self.H_pre = ResidualStreamMapping(n_embd, n_streams, 'pre')
+        self.H_post = ResidualStreamMapping(n_embd, n_streams, 'post')
+        self.H_res = ResidualStreamMapping(n_embd, n_streams, 'res')
+        self._cache = WeightCache()
+
+    def fused_params(self, dtype, device):
+        """(phi [32, n*C], coef [3], bias [2n + n*n]) for the fused kernel."""
+        n, C = self.n_streams, self.n_embd
+        maps = (self.H_pre, self.H_post, self.H_res)
+
+        def build():
+            phi = _phi_block(n, C, [(self.H_pre.phi.weight, n), (self.H_post.phi.weight, n),
+                                    (self.H_res.phi.weight, n * n)], dtype, device)
+            coef = torch.stack([m.alpha.detach().float() for m in maps]).to(device)
+            bias = torch.cat([m.bias.detach().float().reshape(-1) for m in maps]).to(device)
+            return phi, coef, bias
+
+        tensors = [t for m in maps for t in (m.phi.weight, m.alpha, m.bias)]
+        return self._cache.get(tensors, build, extra=(dtype, device))
+
+    def forward(self, x, layer_fn):
+        """x [B, T, n, C]; layer_fn maps [B, T, C] -> [B, T, C]."""
+        n = self.n_streams
+        if n > _MAX_STREAMS:
+            raise NotImplementedError(f"n_streams={n} > {_MAX_STREAMS} is not supported by this build")
+        dt = act_dtype(x)
+        x = x.to(dt)
+        phi, coef, bias = self.fused_params(dt, x.device)
+        layer_in, _, h_post, h_res = kernels.mhc_pre(x, phi, coef, bias, _rms_eps(dt))
+        out = layer_fn(layer_in)
+        return kernels.mhc_post(x, out, h_res, h_post)
+
+
+class mHCBlock(nn.Module):
+    """Attention and FFN each wrapped in an mHC stream (mhc.py:384-423)."""
+
+    def __init__(self, attention_module, ffn_module, n_embd, n_streams=4):
+        super().__init__()
+        self.n_streams = n_streams
+        self.attention = attention_module
+        self.ffn = ffn_module
+        self.attn_stream = mHCResidualStream(n_embd, n_streams)
+        self.ffn_stream = mHCResidualStream(n_embd, n_streams)
+
+    def forward(self, x, freqs_cis, kv_cache=None, layer_idx=0):
+        x = self.attn_stream(x, lambda v: self.attention(v, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx))
+        return self.ffn_stream(x, lambda v: self.ffn(v))
+
+
+def wrap_with_mhc(model_class, n_streams=4):
+    """As in the reference (mhc.py:426-445): use mHCBlock directly."""
+    raise NotImplementedError("Use mHCBlock directly in your model architecture. See mHCWalsh for an example.")
+
+
+class mHCLlamaBlock(nn.Module):
+    """Llama block with mHC streams around attention and FFN (mhc.py:451-534)."""
+
+    def __init__(self, config, n_streams=4):
+        super().__init__()
+        self.n_streams = n_streams
+        self.n_embd = config.n_embd
+        from .chassis import CausalSelfAttention, RMSNorm, SwiGLUMLP
+        self.attention_norm = RMSNorm(config.n_embd)
+        self.ffn_norm = RMSNorm(config.n_embd)
+        self.attention = CausalSelfAttention(config)
+        if getattr(config, 'use_moe', False):
+            from .moe import HadamardMoE
+            self.feed_forward = HadamardMoE(
+                config,
+                threshold=getattr(config, 'moe_threshold', 0.1),
+                min_experts=getattr(config, 'moe_min_experts', 1),
+                max_experts=getattr(config, 'moe_max_experts', 4),
+            )
+        else:
+            self.feed_forward = SwiGLUMLP(config)
+        self.use_channel_mod = getattr(config, 'use_channel_mod', False)
+        if self.use_channel_mod:
+            raise NotImplementedError("channel modulation (use_channel_mod) is outside this build's scope")
+        self.attn_stream = mHCResidualStream(config.n_embd, n_streams)
+        self.ffn_stream = mHCResidualStream(config.n_embd, n_streams)
+
+    def forward(self, x, freqs_cis, kv_cache=None, layer_idx=0):
+        dt = act_dtype(x)
+
+        def attn_fn(x_in):
+            return self.attention(self.attention_norm(x_in).to(dt), freqs_cis, kv_cache=kv_cache,
+                                  layer_idx=layer_idx)
+
+        def ffn_fn(x_in):
+            return self.feed_forward(self.ffn_norm(x_in).to(dt))
+
+        x = self.attn_stream(x, attn_fn)
+        return self.ffn_stream(x, ffn_fn)
+
+
+class mHCWalsh(nn.Module):
+    """Walsh model with n parallel residual streams (mhc.py:537-789)."""
+
+    def __init__(self, config, n_streams=4, gradient_checkpointing=False):
+        super().__init__()
+        self.config = config
+        self.n_streams = n_streams
+        self.gradient_checkpointing = gradient_checkpointing
+        from .chassis import RMSNorm, precompute_freqs_cis
+        if getattr(config, 'hash_embeddings', False):
+            raise NotImplementedError("hash embeddings are outside this build's scope")
+        self.tok_embeddings = nn.Embedding(config.vocab_size, config.n_embd)
+        self.output = nn.Linear(config.n_embd, config.vocab_size, bias=False)
+        self.tok_embeddings.weight = self.output.weight
+        self.stream_proj = nn.Linear(config.n_embd, n_streams * config.n_embd)
+        self.layers = nn.ModuleList([mHCLlamaBlock(config, n_streams) for _ in range(config.n_layer)])
+        self.stream_merge = nn.Linear(n_streams * config.n_embd, config.n_embd)
+        self.norm = RMSNorm(config.n_embd)
+        self.register_buffer("freqs_cis", precompute_freqs_cis(config.n_embd // config.n_head,
+                                                               config.block_size * 2))
+        self.apply(self._init_weights)
+        with torch.no_grad():
+            eye = torch.eye(config.n_embd).repeat(n_streams, 1) / math.sqrt(n_streams)
+            self.stream_proj.weight.copy_(eye)
+            if self.stream_proj.bias is not None:
+                self.stream_proj.bias.zero_()
+            avg = torch.eye(config.n_embd).repeat(1, n_streams) / n_streams
+            self.stream_merge.weight.copy_(avg)
+            if self.stream_merge.bias is not None:
+                self.stream_merge.bias.zero_()
+
+    def _init_weights(self, module):
+        if isinstance(module, nn.Linear):
+            torch.nn.init.normal_(module.weight, mean=0.0, std=0.02)
+            if module.bias is not None:
+                torch.nn.init.zeros_(module.bias)
+        elif isinstance(module, nn.Embedding):
+            torch.nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+    def forward(self, idx, targets=None, kv_cache=None, start_pos=0, return_hidden=False):
+        B, T = idx.shape
+        h = self.tok_embeddings(idx)
+        h = self.stream_proj(h)
+        dt = act_dtype(h)
+        h = h.to(dt).view(B, T, self.n_streams, self.config.n_embd)
+        freqs_cis = self.freqs_cis[start_pos:start_pos + T]
+        for layer_idx, layer in enumerate(self.layers):
+            h = layer(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
+        h_flat = h.reshape(B, T, self.n_streams * self.config.n_embd)
+        h_out = self.norm(self.stream_merge(h_flat))
+        if targets is not None:
+            logits = self.output(h_out)
+            loss = F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1), ignore_index=-1)
+        else:
+            logits = self.output(h_out[:, [-1], :])
+            loss = None
+        if return_hidden:
+            return logits, loss, h_out
+        return logits, loss
+
+    @property
+    def num_parameters(self):
+        total = sum(p.numel() for p in self.parameters())
+        trainable = sum(p.numel() for p in self.parameters() if p.requires_grad)
+        return total, trainable
+
+    def get_aux_loss(self):
+        aux = 0.0
+        for layer in self.layers:
+            if hasattr(layer.feed_forward, 'get_aux_loss'):
+                aux = aux + layer.feed_forward.get_aux_loss()
+        return aux
+
+    def get_moe_stats(self) -> dict:
+        stats = [l.feed_forward.get_expert_stats() for l in self.layers if hasattr(l.feed_forward, 'get_expert_stats')]
+        if not stats:
+            return {}
+        E = len(stats[0]['expert_load'])
+        load = [sum(s['expert_load'][i] for s in stats) / len(stats) for i in range(E)]
+        return {'expert_load': load,
+                'avg_experts': sum(s['avg_experts'] for s in stats) / len(stats),
+                'load_balance': sum(s['load_balance'] for s in stats) / len(stats)}
+
+    def reset_moe_stats(self):
+        for layer in self.layers:
+            if hasattr(layer.feed_forward, 'reset_stats'):
+                layer.feed_forward.reset_stats()
+
+    def get_channel_mod_stats(self) -> dict:
+        return {}
+
+    @torch.no_grad()
+    def generate(self, idx, max_new_tokens, temperature=1.0, top_k=None):
+        """Sampling loop without a cache, as in the reference (mhc.py:754-772)."""
+        for _ in range(max_new_tokens):
+            idx_cond = idx if idx.size(1) <= self.config.block_size else idx[:, -self.config.block_size:]
+            logits, _ = self(idx_cond)
+            logits = logits[:, -1, :].float() / temperature
+            if top_k is not None and top_k > 0:
+                v, _ = torch.topk(logits, min(top_k, logits.size(-1)))
+                logits[logits < v[:, [-1]]] = -float('Inf')
+            probs = F.softmax(logits, dim=-1)
+            idx = torch.cat((idx, torch.multinomial(probs, num_samples=1)), dim=1)
+        return idx
