@@ -70,8 +70,51 @@ def check(rc: int, name: str) -> None:
         raise WalshHipError(f"{name} failed with status {rc}: {msg}")
 
 
-def call(name: str, *args) -> None:
-    check(getattr(lib(), name)(*args), name)
+_timer = None
+
+
+class LaunchTimer:
+    """Context manager that brackets every hot-path launch with HIP events on
+    the launching (current torch) stream and records (kernel, bytes, flops,
+    start, end).  Used by bench.py to time the dominant kernel."""
+
+    def __init__(self):
+        self.records = []
+
+    def __enter__(self):
+        global _timer
+        _timer = self
+        return self
+
+    def __exit__(self, *exc):
+        global _timer
+        _timer = None
+
+    def summary(self):
+        """{kernel: dict(launches, ms, bytes, flops)} (synchronises first)."""
+        torch.cuda.synchronize()
+        out = {}
+        for kname, nbytes, flops, s, e in self.records:
+            d = out.setdefault(kname, dict(launches=0, ms=0.0, bytes=0, flops=0))
+            d["launches"] += 1
+            d["ms"] += s.elapsed_time(e)
+            d["bytes"] += nbytes
+            d["flops"] += flops
+        return out
+
+
+def call(name: str, *args, kernel: str = None, nbytes: int = 0, flops: int = 0) -> None:
+    t = _timer
+    if t is None or kernel is None:
+        check(getattr(lib(), name)(*args), name)
+        return
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    rc = getattr(lib(), name)(*args)
+    e.record()
+    check(rc, name)
+    t.records.append((kernel, int(nbytes), int(flops), s, e))
 
 
 def require_device(t: torch.Tensor, what: str = "tensor") -> None:

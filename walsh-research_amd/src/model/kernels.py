@@ -124,8 +124,16 @@ def hadamard_linear(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tenso
     alpha = alpha.detach().float().contiguous()
     beta = beta.detach().float().contiguous()
     assert alpha.numel() == C_in and beta.numel() == 32 * out_o, "alpha/beta shapes"
+    esz = x.element_size()
+    vec = in_o % 4 == 0 and out_o % 4 == 0 and ldx % 4 == 0 and xv.data_ptr() % (4 * esz) == 0
+    kc1 = in_o <= 16 and (dt == torch.bfloat16 or out_o <= 16)
+    kname = "hadamard_fwd_kernel<%s,%s,%s>" % ("bf16" if dt == torch.bfloat16 else "f32",
+                                                "vec" if vec else "scalar", "kc1" if kc1 else "kloop")
+    nbytes = rows * 32 * (in_o + out_o) * esz + 32 * out_o * ((in_o + 3) // 4) + 4 * 32 * (in_o + out_o)
+    flops = rows * (2 * 32 * in_o * out_o + 5 * 32 * (in_o + out_o) * 2 + 32 * (in_o + out_o))
     _hip.call("walsh_hadamard_linear_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, kweight.data_ptr(),
-              alpha.data_ptr(), beta.data_ptr(), y.data_ptr(), 32 * out_o, code, _hip.stream(x.device))
+              alpha.data_ptr(), beta.data_ptr(), y.data_ptr(), 32 * out_o, code, _hip.stream(x.device),
+              kernel=kname, nbytes=nbytes, flops=flops)
     return y
 
 
@@ -172,8 +180,13 @@ def octonion_linear(x: torch.Tensor, in_o: int, out_o: int, B: torch.Tensor, bet
         xv = xv.reshape(rows, -1)[:, :K].contiguous()
         ldx = K
     beta = beta.detach().float().contiguous()
+    esz = x.element_size()
+    nbytes = rows * 8 * (in_o + out_o) * esz + 8 * out_o * ((in_o + 3) // 4) + 4 * out_o
+    flops = 2 * rows * (8 * in_o) * (8 * out_o)
     _hip.call("walsh_octonion_linear_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, B.data_ptr(), beta.data_ptr(),
-              y.data_ptr(), 8 * out_o, _hip.dtype_code(x.dtype), _hip.stream(x.device))
+              y.data_ptr(), 8 * out_o, _hip.dtype_code(x.dtype), _hip.stream(x.device),
+              kernel="octonion_gemm_kernel<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"),
+              nbytes=nbytes, flops=flops)
     return y
 
 
@@ -212,9 +225,14 @@ def mhc_pre(x: torch.Tensor, phi_cat: torch.Tensor, coef: torch.Tensor, bias_cat
     if M == 0:
         return layer_in, h_pre, h_post, h_res
     assert phi_cat.dtype == x.dtype and tuple(phi_cat.shape) == (32, n * C), "phi_cat layout"
+    esz = x.element_size()
+    nbytes = M * (n * C + C) * esz + M * (2 * n + n * n) * 4 + (2 * n + n * n) * n * C * esz
+    flops = M * (2 * n * C * (2 * n + n * n) + 2 * n * C + 2 * n * C)
     _hip.call("walsh_mhc_pre_fwd", xv.data_ptr(), n * C, M, n, C, phi_cat.data_ptr(), coef.data_ptr(),
               bias_cat.data_ptr(), float(rms_eps), int(n_iter), float(sk_eps), h_pre.data_ptr(), h_post.data_ptr(),
-              h_res.data_ptr(), layer_in.data_ptr(), C, _hip.dtype_code(x.dtype), _hip.stream(dev))
+              h_res.data_ptr(), layer_in.data_ptr(), C, _hip.dtype_code(x.dtype), _hip.stream(dev),
+              kernel="mhc_pre_kernel<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"), nbytes=nbytes,
+              flops=flops)
     return layer_in, h_pre, h_post, h_res
 
 
@@ -232,6 +250,11 @@ def mhc_post(x: torch.Tensor, out: torch.Tensor, h_res: torch.Tensor, h_post: to
         return x_new
     hr = h_res.detach().float().contiguous()
     hp = h_post.detach().float().contiguous()
+    esz = x.element_size()
+    nbytes = M * (2 * n * C + C) * esz + M * (n * n + n) * 4
+    flops = M * n * C * (2 * n + 2)
     _hip.call("walsh_mhc_post_fwd", xv.data_ptr(), n * C, o.data_ptr(), C, hr.data_ptr(), hp.data_ptr(),
-              x_new.data_ptr(), n * C, M, n, C, _hip.dtype_code(x.dtype), _hip.stream(x.device))
+              x_new.data_ptr(), n * C, M, n, C, _hip.dtype_code(x.dtype), _hip.stream(x.device),
+              kernel="mhc_post_kernel<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"), nbytes=nbytes,
+              flops=flops)
     return x_new
