@@ -105,6 +105,27 @@ int walsh_hadamard_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_
                               const uint8_t *kweight, const float *alpha, const float *beta,
                               void *y, int64_t ldy, int dtype, void *stream);
 
+/* walsh_hadamard_linear_ex_fwd: walsh_hadamard_linear_fwd with explicit group
+ *   strides: x row element (g, i) at g*gsx + i (gsx >= in_o), y row element
+ *   (h, o) at h*gsy + o (gsy >= out_o).  With gsy > out_o the slots o in
+ *   [out_o, roundup(out_o, 4)) are written as exact zeros; slots i in
+ *   [in_o, gsx) of x must hold finite values (they meet zero weights).  Used
+ *   for the group-padded SwiGLU hidden layout (see walsh_hadamard_swiglu_fwd). */
+int walsh_hadamard_linear_ex_fwd(const void *x, int64_t ldx, int64_t gsx, int64_t M, int64_t in_o, int64_t out_o,
+                                 const uint8_t *kweight, const float *alpha, const float *beta, void *y, int64_t ldy,
+                                 int64_t gsy, int dtype, void *stream);
+
+/* walsh_hadamard_swiglu_fwd: h = silu(gate(x)) * up(x) for two Hadamard
+ *   linears of the same shape (in_o -> hid_o) on the same input, fused
+ *   (SwiGLUMLP.forward, src/model/chassis.py:498-504, gate_proj/up_proj).
+ *   h is written with group stride gsh (>= hid_o; pad slots up to
+ *   roundup(hid_o, 4) get zeros), ready for down_proj through
+ *   walsh_hadamard_linear_ex_fwd with gsx = gsh. */
+int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t gsx, int64_t M, int64_t in_o, int64_t hid_o,
+                              const uint8_t *kw_gate, const float *alpha_gate, const float *beta_gate,
+                              const uint8_t *kw_up, const float *alpha_up, const float *beta_up, void *h,
+                              int64_t ldh, int64_t gsh, int dtype, void *stream);
+
 /* walsh_fht_fwd: fast Walsh-Hadamard transform of `rows` contiguous rows of
  *   length n (power of two <= 16384), Sylvester order, scaled by 1/sqrt(n)
  *   when `normalize` (fht_butterfly / fht, src/model/fht_cuda.py:281-337). */
@@ -160,6 +181,19 @@ int walsh_mhc_pre_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t 
                       const float *coef, const float *bias, float rms_eps, int64_t n_iter, float sk_eps,
                       float *h_pre, float *h_post, float *h_res, void *layer_in, int64_t ld_in, int dtype,
                       void *stream);
+
+/* walsh_mhc_pre_norm_fwd: walsh_mhc_pre_fwd for rows of up to 8 KB (n*C*esize
+ *   <= 8192, C <= 1024, n*C % 16 == 0), each workgroup keeping its token tile
+ *   in LDS so x is read once; phi_frag is phi in matrix-core fragment order
+ *   [n*C/16][2][64][4] (element (ks, nt, lane = 16*kq + r, j) =
+ *   phi[16*nt + r][16*ks + 4*kq + j]).  If norm_w is non-NULL, layer_in is
+ *   also RMS-normalised over its C values and scaled by norm_w (float32 [C]):
+ *   layer_in * rsqrt(mean(layer_in^2) + norm_eps) * norm_w, the block's
+ *   attention_norm / ffn_norm (src/model/chassis.py:96-106) fused in. */
+int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C, const void *phi_frag,
+                           const float *coef, const float *bias, float rms_eps, int64_t n_iter, float sk_eps,
+                           float *h_pre, float *h_post, float *h_res, void *layer_in, int64_t ld_in,
+                           const float *norm_w, float norm_eps, int dtype, void *stream);
 
 /* walsh_mhc_post_fwd: x_new = H_res @ x + H_post^T (x) out
  *   (src/model/mhc.py:366-381).  out [M, C] row stride ld_out; x_new may not

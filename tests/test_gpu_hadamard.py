@@ -172,3 +172,35 @@ def test_hadamard_linear_closed_form_identity(K):
     x = np.random.default_rng(6).standard_normal((33, 32)).astype(np.float32)
     y, _ = _run(K, x, codes, np.full((32, 1), 2.0, np.float32), np.full((32, 1), 0.5, np.float32), torch.float32)
     assert np.max(np.abs(y - x)) < 1e-6
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("in_o,hid_o", [(16, 43), (16, 16), (8, 21), (4, 12)])
+def test_hadamard_swiglu_and_padded_down(K, dtype, in_o, hid_o):
+    """silu(gate(x)) * up(x) into the group-padded layout, then down_proj
+    reading it in place, against the oracle's three separate layers."""
+    rng = np.random.default_rng(in_o * 100 + hid_o)
+    M = 70
+    cg = rng.integers(-1, 2, size=(32, hid_o, in_o)).astype(np.int8)
+    cu = rng.integers(-1, 2, size=(32, hid_o, in_o)).astype(np.int8)
+    cd = rng.integers(-1, 2, size=(32, in_o, hid_o)).astype(np.int8)
+    ag, au = (rng.uniform(0.5, 1.5, (32, in_o)).astype(np.float32) for _ in range(2))
+    bg, bu = (rng.uniform(0.1, 0.4, (32, hid_o)).astype(np.float32) for _ in range(2))
+    ad = rng.uniform(0.5, 1.5, (32, hid_o)).astype(np.float32)
+    bd = rng.uniform(0.1, 0.4, (32, in_o)).astype(np.float32)
+    x = rng.standard_normal((M, 32 * in_o)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).cuda()  # noqa: E731
+    xt = t(x).to(dtype)
+    h = K.hadamard_swiglu(xt, in_o, hid_o, (_prepare(K, cg), t(ag), t(bg)), (_prepare(K, cu), t(au), t(bu)))
+    gsh = ((hid_o + 3) // 4) * 4
+    assert h.shape == (M, 32 * gsh)
+    hv = h.float().cpu().numpy().reshape(M, 32, gsh)
+    assert np.all(hv[:, :, hid_o:] == 0)                     # pad slots are exact zeros
+    xq = xt.float().cpu().numpy().astype(np.float64)
+    g = ohad.hadamard_linear_f64(xq, cg, ag, bg)
+    u = ohad.hadamard_linear_f64(xq, cu, au, bu)
+    h_ref = g / (1 + np.exp(-g)) * u
+    assert_close(hv[:, :, :hid_o].reshape(M, -1), h_ref, dtype, f"swiglu h {dtype} {in_o}->{hid_o}")
+    y = K.hadamard_linear(h, hid_o, in_o, _prepare(K, cd), t(ad), t(bd), gsx=gsh)
+    hq = hv[:, :, :hid_o].reshape(M, -1).astype(np.float64)
+    assert_close(y.float().cpu().numpy(), ohad.hadamard_linear_f64(hq, cd, ad, bd), dtype, f"down {dtype}")

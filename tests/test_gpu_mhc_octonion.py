@@ -178,3 +178,35 @@ def test_octonion_module_tuple_interface():
     wq = torch.from_numpy(codes.astype(np.float32)).cuda()
     yf = cayley_dickson_fused(parts, wq)
     assert yf[0].dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,n,C", [(100, 4, 512), (33, 4, 64), (7, 2, 32), (64, 1, 16), (50, 4, 1024), (40, 3, 48)])
+@pytest.mark.parametrize("with_norm", [False, True])
+def test_mhc_pre_norm_matches_oracle(K, dtype, M, n, C, with_norm):
+    if not K.mhc_pre_supported(n, C, dtype):
+        pytest.skip("shape served by walsh_mhc_pre_fwd (row too large for the LDS tile)")
+    rng = np.random.default_rng(M * 7 + n + C)
+    x = rng.normal(0, 1, (M, n, C)).astype(np.float32)
+    maps = _maps(rng, n, C)
+    xt = torch.from_numpy(x).cuda().to(dtype)
+    xq = xt.float().cpu().numpy().astype(np.float64)
+    eps = float(torch.finfo(dtype).eps)
+    phi, coef, bias = _fused_params(maps, n, C, dtype)
+    w = rng.uniform(0.5, 1.5, C).astype(np.float32)
+    li, hp, hq, hr = K.mhc_pre_norm(xt, K.phi_fragments(phi), coef, bias, eps,
+                                    norm_w=torch.from_numpy(w).cuda() if with_norm else None, norm_eps=1e-6)
+    phiq = phi.float().cpu().numpy().astype(np.float64)
+    m2 = dict(pre=(phiq[:n], *maps['pre'][1:]), post=(phiq[n:2 * n], *maps['post'][1:]),
+              res=(phiq[2 * n:2 * n + n * n], *maps['res'][1:]))
+    _, hp_ref, hq_ref, hr_ref, li_ref = omhc.stream_forward(xq, m2, lambda v: v, eps)
+    if with_norm:
+        li_ref = li_ref / np.sqrt((li_ref ** 2).mean(-1, keepdims=True) + 1e-6) * w
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert np.max(np.abs(hp.cpu().numpy() - hp_ref[:, 0])) < tol
+    assert np.max(np.abs(hq.cpu().numpy() - hq_ref[:, 0])) < 2 * tol
+    assert np.max(np.abs(hr.cpu().numpy() - hr_ref)) < tol
+    assert_close(li.float().cpu().numpy(), li_ref, dtype, f"pre_norm {dtype} M={M} n={n} C={C} norm={with_norm}")
+    # identical H to the one-pass-per-K-slice kernel
+    _, hp1, hq1, hr1 = K.mhc_pre(xt, phi, coef, bias, eps)
+    assert torch.allclose(hr, hr1, atol=1e-6) and torch.allclose(hp, hp1, atol=1e-6)

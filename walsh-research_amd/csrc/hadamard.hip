@@ -77,6 +77,7 @@ struct HadArgs {
     int64_t ldx;
     int M;              // rows of this launch (M * ldx * esize < 2^31)
     int in_o, out_o, Nt, Kc;
+    int gsx, gsy;       // group strides of x / y rows (>= in_o / out_o)
     const uint8_t *kw;
     const float *alpha;
     const float *beta;
@@ -103,7 +104,7 @@ __device__ __forceinline__ void load_transform(const HadArgs &a, __amdgpu_buffer
     constexpr uint32_t esz = sizeof(T);
     f32x4 v[32];
     const int i0 = kKChunk * c + 4 * q;
-    const uint32_t gstride = (uint32_t)a.in_o * esz;
+    const uint32_t gstride = (uint32_t)a.gsx * esz;
     if (VEC) {
         const uint32_t voff = (row_ok && i0 < a.in_o) ? row_off + (uint32_t)i0 * esz : kOOB;
 #pragma unroll
@@ -166,7 +167,7 @@ __device__ __forceinline__ void transform_store(const HadArgs &a, f32x4 (&acc)[3
     constexpr uint32_t esz = sizeof(T);
     fht32x4(acc);
     const int o0 = kNTile * nt + 4 * q;
-    const uint32_t hstride = (uint32_t)a.out_o * esz;
+    const uint32_t hstride = (uint32_t)a.gsy * esz;
     const f32x4 *bl = beta_l + (nt * 4 + q) * 32;
     if (VEC) {
         const uint32_t voff = (row_ok && o0 < a.out_o) ? row_off + (uint32_t)o0 * esz : kOOB;
@@ -273,6 +274,176 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
     }
 }
 
+// ---------------------------------------------------------------- fused SwiGLU
+// h = silu(gate(x)) * up(x) for two Hadamard linears sharing the input x
+// (SwiGLUMLP.forward, src/model/chassis.py:498-504, whose gate_proj/up_proj
+// are HadamardTernaryLinearTuple layers).  A work item is one 16-token tile
+// and one 16-wide output tile: the gate result (after its output transform
+// and beta) waits in an LDS stash while the up projection runs, then
+// silu(g)*u is written once.  `g` and `u` carry the per-projection weights,
+// alpha and beta; x/y geometry is read from `g`.
+template <bool BF16MMA> struct Stash;
+template <> struct Stash<true> { typedef uint2 type; };   // 4 x bf16
+template <> struct Stash<false> { typedef f32x4 type; };  // 4 x f32
+
+__device__ __forceinline__ float silu_fast(float v) {
+    return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+}
+
+template <typename T, bool BF16MMA, bool VEC, bool KC1>
+__global__ __launch_bounds__(kThreads, (BF16MMA && KC1) ? 2 : 1) void hadamard_swiglu_kernel(HadArgs g, HadArgs u) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    typedef typename Stash<BF16MMA>::type SType;
+    void *lut = smem;
+    f32x4 *ag_l = (f32x4 *)(smem + lut_bytes<BF16MMA>());
+    f32x4 *au_l = ag_l + g.Kc * 128;
+    f32x4 *bg_l = au_l + g.Kc * 128;
+    f32x4 *bu_l = bg_l + g.Nt * 128;
+    SType *stash = (SType *)(bu_l + g.Nt * 128);     // [kWaves][32][64]
+
+    const int tid = threadIdx.x;
+    {
+        const uint32_t byte = (uint32_t)tid;
+        float val[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) val[j] = (float)((int)((byte >> (6 - 2 * j)) & 3u) - 1);
+        if constexpr (BF16MMA) {
+            uint2 e;
+            e.x = pack_bf16x2(val[0], val[1]);
+            e.y = pack_bf16x2(val[2], val[3]);
+            ((uint2 *)lut)[byte] = e;
+        } else {
+            ((f32x4 *)lut)[byte] = f32x4{val[0], val[1], val[2], val[3]};
+        }
+    }
+    for (int e = tid; e < g.Kc * 128; e += kThreads) {
+        const int gg = e & 31, i0 = 4 * (e >> 5);
+        f32x4 va, vb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = i0 + j < g.in_o;
+            va[j] = ok ? g.alpha[gg * g.in_o + i0 + j] : 0.f;
+            vb[j] = ok ? u.alpha[gg * g.in_o + i0 + j] : 0.f;
+        }
+        ag_l[e] = va;
+        au_l[e] = vb;
+    }
+    for (int e = tid; e < g.Nt * 128; e += kThreads) {
+        const int h = e & 31, o0 = 4 * (e >> 5);
+        f32x4 va, vb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = o0 + j < g.out_o;
+            va[j] = ok ? g.beta[h * g.out_o + o0 + j] * 0.03125f : 0.f;
+            vb[j] = ok ? u.beta[h * g.out_o + o0 + j] * 0.03125f : 0.f;
+        }
+        bg_l[e] = va;
+        bu_l[e] = vb;
+    }
+    __syncthreads();
+
+    constexpr uint32_t esz = sizeof(T);
+    const int wave = tid >> 6, lane = tid & 63;
+    const int t = lane & 15, q = lane >> 4;
+    SType *st = stash + wave * 32 * 64;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)g.M * g.ldx * esz));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(g.y, (uint32_t)((int64_t)g.M * g.ldy * esz));
+    const int n_items = (int)ceil_div(g.M, kTile) * g.Nt;
+    const int stride = gridDim.x * kWaves;
+
+    for (int item = blockIdx.x * kWaves + wave; item < n_items; item += stride) {
+        const int tile = item / g.Nt, nt = item - tile * g.Nt;
+        const int row = tile * kTile + t;
+        const bool row_ok = row < g.M;
+        const uint32_t xoff = (uint32_t)((int64_t)row * g.ldx * esz);
+        const uint32_t yoff = (uint32_t)((int64_t)row * g.ldy * esz);
+        f32x4 acc[32];
+        // gate (single input chunk: transform before the accumulators are live)
+        if constexpr (KC1) {
+            XM<BF16MMA> xm;
+            load_transform<T, BF16MMA, VEC>(g, xr, xoff, row_ok, 0, q, ag_l, xm);
+#pragma unroll
+            for (int k = 0; k < 32; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+            contract<BF16MMA>(g, nt, 0, lane, xm, lut, acc);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 32; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int c = 0; c < g.Kc; ++c) {
+                XM<BF16MMA> xm;
+                load_transform<T, BF16MMA, VEC>(g, xr, xoff, row_ok, c, q, ag_l, xm);
+                contract<BF16MMA>(g, nt, c, lane, xm, lut, acc);
+            }
+        }
+        fht32x4(acc);
+        {
+            const f32x4 *bl = bg_l + (nt * 4 + q) * 32;
+#pragma unroll
+            for (int h = 0; h < 32; ++h) {
+                const f32x4 v = acc[h] * bl[h];
+                if constexpr (BF16MMA) {
+                    uint2 e;
+                    e.x = pack_bf16x2(v.x, v.y);
+                    e.y = pack_bf16x2(v.z, v.w);
+                    st[h * 64 + lane] = e;
+                } else {
+                    st[h * 64 + lane] = v;
+                }
+            }
+        }
+        // up
+        if constexpr (KC1) {
+            XM<BF16MMA> xm;
+            load_transform<T, BF16MMA, VEC>(g, xr, xoff, row_ok, 0, q, au_l, xm);
+#pragma unroll
+            for (int k = 0; k < 32; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+            contract<BF16MMA>(u, nt, 0, lane, xm, lut, acc);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 32; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int c = 0; c < g.Kc; ++c) {
+                XM<BF16MMA> xm;
+                load_transform<T, BF16MMA, VEC>(g, xr, xoff, row_ok, c, q, au_l, xm);
+                contract<BF16MMA>(u, nt, c, lane, xm, lut, acc);
+            }
+        }
+        fht32x4(acc);
+        const int o0 = kNTile * nt + 4 * q;
+        const uint32_t hstride = (uint32_t)g.gsy * esz;
+        const f32x4 *bl = bu_l + (nt * 4 + q) * 32;
+        uint32_t voff[4];
+        if (VEC) {
+            voff[0] = (row_ok && o0 < g.out_o) ? yoff + (uint32_t)o0 * esz : kOOB;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) voff[j] = (row_ok && o0 + j < g.out_o) ? yoff + (uint32_t)(o0 + j) * esz : kOOB;
+        }
+#pragma unroll
+        for (int h = 0; h < 32; ++h) {
+            const f32x4 uv = acc[h] * bl[h];
+            f32x4 gv;
+            if constexpr (BF16MMA) {
+                const uint2 e = st[h * 64 + lane];
+                gv.x = __uint_as_float(e.x << 16);
+                gv.y = __uint_as_float(e.x & 0xffff0000u);
+                gv.z = __uint_as_float(e.y << 16);
+                gv.w = __uint_as_float(e.y & 0xffff0000u);
+            } else {
+                gv = st[h * 64 + lane];
+            }
+            f32x4 hv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) hv[j] = silu_fast(gv[j]) * uv[j];
+            if (VEC) {
+                Buf4<T>::store(hv, yr, voff[0], (uint32_t)h * hstride);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) Buf4<T>::store1(hv[j], yr, voff[j], (uint32_t)h * hstride);
+            }
+            if ((h & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- standalone FHT
 // Normalised (or not) fast Walsh-Hadamard transform of rows of length
 // N = 2^logN (fht_cuda.py:281-309): rows staged in LDS, log2(N) butterfly
@@ -332,71 +503,136 @@ WALSH_EXPORT int walsh_hadamard_prepare(const uint8_t *packed, int64_t in_o, int
     return check_hip(hipGetLastError(), "walsh_hadamard_prepare launch");
 }
 
-WALSH_EXPORT int walsh_hadamard_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
-                                           const uint8_t *kweight, const float *alpha, const float *beta, void *y,
-                                           int64_t ldy, int dtype, void *stream) {
-    if (!x || !y || !kweight || !alpha || !beta)
-        return set_error(WALSH_EINVAL, "walsh_hadamard_linear_fwd: null pointer");
+static int hadamard_check(const char *fn, const void *x, int64_t ldx, int64_t gsx, int64_t M, int64_t in_o,
+                          int64_t out_o, const void *y, int64_t ldy, int64_t gsy, int dtype) {
+    if (!x || !y) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
     if (M < 0 || in_o <= 0 || out_o <= 0 || in_o > 65536 || out_o > 65536)
-        return set_error(WALSH_EINVAL, "walsh_hadamard_linear_fwd: bad shape M=%lld in_o=%lld out_o=%lld",
-                         (long long)M, (long long)in_o, (long long)out_o);
-    if (ldx < 32 * in_o || ldy < 32 * out_o)
-        return set_error(WALSH_EINVAL, "walsh_hadamard_linear_fwd: row stride too small (ldx=%lld ldy=%lld)",
-                         (long long)ldx, (long long)ldy);
-    if (dtype != WALSH_F32 && dtype != WALSH_BF16)
-        return set_error(WALSH_ENOTSUP, "walsh_hadamard_linear_fwd: dtype %d not supported", dtype);
-    if (M == 0) return WALSH_OK;
-    const bool bf16 = dtype == WALSH_BF16;
+        return set_error(WALSH_EINVAL, "%s: bad shape M=%lld in_o=%lld out_o=%lld", fn, (long long)M, (long long)in_o,
+                         (long long)out_o);
+    if (gsx < in_o || gsy < out_o || ldx < 32 * gsx || ldy < 32 * gsy)
+        return set_error(WALSH_EINVAL, "%s: strides too small (ldx=%lld gsx=%lld ldy=%lld gsy=%lld)", fn,
+                         (long long)ldx, (long long)gsx, (long long)ldy, (long long)gsy);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype %d not supported", fn, dtype);
+    return WALSH_OK;
+}
+
+// Launch one Hadamard-linear (two for the fused SwiGLU: u != NULL) over M
+// rows in chunks whose byte offsets fit a 31-bit buffer range.
+static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, int64_t M, bool bf16, hipStream_t s) {
     const int64_t esz = bf16 ? 2 : 4;
-    const int Nt = (int)ceil_div(out_o, kNTile), Kc = (int)ceil_div(in_o, kKChunk);
-    const size_t lds = hadamard_lds_bytes(bf16, Kc, Nt);
+    const int Nt = base.Nt, Kc = base.Kc;
+    const bool swiglu = ubase != nullptr;
+    size_t lds = hadamard_lds_bytes(bf16, Kc, Nt);
+    if (swiglu) lds += (size_t)16 * 128 * (Kc + Nt) + (size_t)kWaves * 32 * 64 * (bf16 ? 8 : 16);
     if (lds > (size_t)device_info().max_shared_per_block)
-        return set_error(WALSH_ENOTSUP, "walsh_hadamard_linear_fwd: in_o=%lld out_o=%lld need %zu B of LDS",
-                         (long long)in_o, (long long)out_o, lds);
+        return set_error(WALSH_ENOTSUP, "%s: in_o=%d out_o=%d need %zu B of LDS", fn, base.in_o, base.out_o, lds);
     const size_t valign = bf16 ? 8 : 16;
-    const bool vec = (in_o % 4 == 0) && (ldx % 4 == 0) && ((uintptr_t)x % valign == 0) && (out_o % 4 == 0) &&
-                     (ldy % 4 == 0) && ((uintptr_t)y % valign == 0);
+    const bool vec = (base.gsx % 4 == 0) && (base.ldx % 4 == 0) && ((uintptr_t)base.x % valign == 0) &&
+                     (base.gsy % 4 == 0) && (base.ldy % 4 == 0) && ((uintptr_t)base.y % valign == 0);
     // float32 operands keep 128 registers of transformed input; with several
     // output tiles they are recomputed per tile instead of kept live.
     const bool kc1 = Kc == 1 && (bf16 || Nt == 1);
-    // rows per launch so every byte offset fits a 31-bit buffer range
-    const int64_t ld = ldx > ldy ? ldx : ldy;
+    const int64_t ld = base.ldx > base.ldy ? base.ldx : base.ldy;
     int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz);
     rows_max = rows_max / kTile * kTile;
-    if (rows_max < kTile) return set_error(WALSH_ENOTSUP, "walsh_hadamard_linear_fwd: row stride too large");
-    hipStream_t s = (hipStream_t)stream;
-    const int64_t cap = (int64_t)device_info().cu_count * 2;
+    if (rows_max < kTile) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
+    const int64_t cap = (int64_t)device_info().cu_count * (swiglu ? 8 : 2);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
-        HadArgs a;
-        a.x = (const char *)x + r0 * ldx * esz;
-        a.ldx = ldx;
+        HadArgs a = base;
+        a.x = (const char *)base.x + r0 * base.ldx * esz;
+        a.y = (char *)base.y + r0 * base.ldy * esz;
         a.M = (int)rows;
-        a.in_o = (int)in_o;
-        a.out_o = (int)out_o;
-        a.Nt = Nt;
-        a.Kc = Kc;
-        a.kw = kweight;
-        a.alpha = alpha;
-        a.beta = beta;
-        a.y = (char *)y + r0 * ldy * esz;
-        a.ldy = ldy;
-        int64_t grid = ceil_div(ceil_div(rows, kTile), kWaves);
+        int64_t work = ceil_div(rows, kTile) * (swiglu ? Nt : 1);
+        int64_t grid = ceil_div(work, kWaves);
         if (grid > cap) grid = cap;
         const dim3 G((unsigned)grid), B(kThreads);
-#define WALSH_HAD_LAUNCH(T, MMA, V, K1) hipLaunchKernelGGL((hadamard_fwd_kernel<T, MMA, V, K1>), G, B, lds, s, a)
-        if (bf16) {
-            if (vec) { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, true, true); else WALSH_HAD_LAUNCH(uint16_t, true, true, false); }
-            else     { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, false, true); else WALSH_HAD_LAUNCH(uint16_t, true, false, false); }
+        if (swiglu) {
+            HadArgs ua = *ubase;
+            ua.x = a.x;
+            ua.y = a.y;
+            ua.M = a.M;
+#define WALSH_SW_LAUNCH(T, MMA, V, K1) hipLaunchKernelGGL((hadamard_swiglu_kernel<T, MMA, V, K1>), G, B, lds, s, a, ua)
+            const bool one = Kc == 1;
+            if (bf16) {
+                if (vec) { if (one) WALSH_SW_LAUNCH(uint16_t, true, true, true); else WALSH_SW_LAUNCH(uint16_t, true, true, false); }
+                else     { if (one) WALSH_SW_LAUNCH(uint16_t, true, false, true); else WALSH_SW_LAUNCH(uint16_t, true, false, false); }
+            } else {
+                if (vec) { if (one) WALSH_SW_LAUNCH(float, false, true, true); else WALSH_SW_LAUNCH(float, false, true, false); }
+                else     { if (one) WALSH_SW_LAUNCH(float, false, false, true); else WALSH_SW_LAUNCH(float, false, false, false); }
+            }
+#undef WALSH_SW_LAUNCH
         } else {
-            if (vec) { if (kc1) WALSH_HAD_LAUNCH(float, false, true, true); else WALSH_HAD_LAUNCH(float, false, true, false); }
-            else     { if (kc1) WALSH_HAD_LAUNCH(float, false, false, true); else WALSH_HAD_LAUNCH(float, false, false, false); }
-        }
+#define WALSH_HAD_LAUNCH(T, MMA, V, K1) hipLaunchKernelGGL((hadamard_fwd_kernel<T, MMA, V, K1>), G, B, lds, s, a)
+            if (bf16) {
+                if (vec) { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, true, true); else WALSH_HAD_LAUNCH(uint16_t, true, true, false); }
+                else     { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, false, true); else WALSH_HAD_LAUNCH(uint16_t, true, false, false); }
+            } else {
+                if (vec) { if (kc1) WALSH_HAD_LAUNCH(float, false, true, true); else WALSH_HAD_LAUNCH(float, false, true, false); }
+                else     { if (kc1) WALSH_HAD_LAUNCH(float, false, false, true); else WALSH_HAD_LAUNCH(float, false, false, false); }
+            }
 #undef WALSH_HAD_LAUNCH
-        const int rc = check_hip(hipGetLastError(), "walsh_hadamard_linear_fwd launch");
+        }
+        const int rc = check_hip(hipGetLastError(), fn);
         if (rc) return rc;
     }
     return WALSH_OK;
+}
+
+static HadArgs had_args(const void *x, int64_t ldx, int64_t gsx, int64_t in_o, int64_t out_o, const uint8_t *kw,
+                        const float *alpha, const float *beta, void *y, int64_t ldy, int64_t gsy) {
+    HadArgs a;
+    a.x = x;
+    a.ldx = ldx;
+    a.M = 0;
+    a.in_o = (int)in_o;
+    a.out_o = (int)out_o;
+    a.Nt = (int)ceil_div(out_o, kNTile);
+    a.Kc = (int)ceil_div(in_o, kKChunk);
+    a.gsx = (int)gsx;
+    a.gsy = (int)gsy;
+    a.kw = kw;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.y = y;
+    a.ldy = ldy;
+    return a;
+}
+
+WALSH_EXPORT int walsh_hadamard_linear_ex_fwd(const void *x, int64_t ldx, int64_t gsx, int64_t M, int64_t in_o,
+                                              int64_t out_o, const uint8_t *kweight, const float *alpha,
+                                              const float *beta, void *y, int64_t ldy, int64_t gsy, int dtype,
+                                              void *stream) {
+    const char *fn = "walsh_hadamard_linear_ex_fwd";
+    int rc = hadamard_check(fn, x, ldx, gsx, M, in_o, out_o, y, ldy, gsy, dtype);
+    if (rc) return rc;
+    if (!kweight || !alpha || !beta) return set_error(WALSH_EINVAL, "%s: null weight pointer", fn);
+    if (M == 0) return WALSH_OK;
+    return hadamard_launch(fn, had_args(x, ldx, gsx, in_o, out_o, kweight, alpha, beta, y, ldy, gsy), nullptr, M,
+                           dtype == WALSH_BF16, (hipStream_t)stream);
+}
+
+WALSH_EXPORT int walsh_hadamard_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                                           const uint8_t *kweight, const float *alpha, const float *beta, void *y,
+                                           int64_t ldy, int dtype, void *stream) {
+    return walsh_hadamard_linear_ex_fwd(x, ldx, in_o, M, in_o, out_o, kweight, alpha, beta, y, ldy, out_o, dtype,
+                                        stream);
+}
+
+WALSH_EXPORT int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t gsx, int64_t M, int64_t in_o,
+                                           int64_t hid_o, const uint8_t *kw_gate, const float *alpha_gate,
+                                           const float *beta_gate, const uint8_t *kw_up, const float *alpha_up,
+                                           const float *beta_up, void *h, int64_t ldh, int64_t gsh, int dtype,
+                                           void *stream) {
+    const char *fn = "walsh_hadamard_swiglu_fwd";
+    int rc = hadamard_check(fn, x, ldx, gsx, M, in_o, hid_o, h, ldh, gsh, dtype);
+    if (rc) return rc;
+    if (!kw_gate || !alpha_gate || !beta_gate || !kw_up || !alpha_up || !beta_up)
+        return set_error(WALSH_EINVAL, "%s: null weight pointer", fn);
+    if (M == 0) return WALSH_OK;
+    const HadArgs ga = had_args(x, ldx, gsx, in_o, hid_o, kw_gate, alpha_gate, beta_gate, h, ldh, gsh);
+    const HadArgs ua = had_args(x, ldx, gsx, in_o, hid_o, kw_up, alpha_up, beta_up, h, ldh, gsh);
+    return hadamard_launch(fn, ga, &ua, M, dtype == WALSH_BF16, (hipStream_t)stream);
 }
 
 WALSH_EXPORT int walsh_fht_fwd(const void *x, int64_t rows, int64_t n, int normalize, void *y, int dtype,

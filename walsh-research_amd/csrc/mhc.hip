@@ -51,6 +51,57 @@ __device__ __forceinline__ void sinkhorn_regs(float (&m)[NMAX][NMAX], int n, int
 
 __device__ __forceinline__ float sigmoidf(float v) { return __fdiv_rn(1.0f, 1.0f + expf(-v)); }
 
+// Sum over the 4 lanes of a quad with DPP quad_perm moves (no LDS round trip).
+__device__ __forceinline__ float quad_sum(float v) {
+    const int x1 = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true);    // lanes ^1
+    const float s = v + __int_as_float(x1);
+    const int x2 = __builtin_amdgcn_mov_dpp(__float_as_int(s), 0x4E, 0xF, 0xF, true);    // lanes ^2
+    return s + __int_as_float(x2);
+}
+
+// Per-token constraints with 4 lanes per token (lane r = row r of the n x n
+// residual matrix; r < n active).  dynf(o) returns the RMS-scaled projection
+// output o of this token.  Column sums of the Sinkhorn iteration are quad
+// shuffles; each lane divides its own row, so a whole wavefront projects 16
+// tokens at once.  Results go to hpre_lds[t*4 + r] and (if tok valid) global.
+template <typename DynF>
+__device__ __forceinline__ void token_constraints_quad(int t, int r, int tok, int M, int n, const float *coef,
+                                                       const float *bias, int n_iter, float sk_eps, DynF dynf,
+                                                       float *hpre_lds, float *h_pre, float *h_post, float *h_res) {
+    const bool act = r < n;
+    float pre = 0.f, post = 0.f;
+    if (act) {
+        pre = __builtin_amdgcn_rcpf(1.0f + __expf(-(coef[0] * dynf(r) + bias[r])));
+        post = 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(-(coef[1] * dynf(n + r) + bias[n + r])));
+    }
+    float m[kMaxStreams];
+#pragma unroll
+    for (int j = 0; j < kMaxStreams; ++j)
+        m[j] = (act && j < n) ? __expf(coef[2] * dynf(2 * n + r * n + j) + bias[2 * n + r * n + j]) : 0.f;
+    for (int it = 0; it < n_iter; ++it) {
+#pragma unroll
+        for (int j = 0; j < kMaxStreams; ++j) {
+            const float cs = quad_sum(m[j]);
+            if (j < n) m[j] *= __builtin_amdgcn_rcpf(cs + sk_eps);
+        }
+        float rs = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxStreams; ++j) rs += (j < n) ? m[j] : 0.f;
+        const float rd = __builtin_amdgcn_rcpf(rs + sk_eps);
+#pragma unroll
+        for (int j = 0; j < kMaxStreams; ++j)
+            if (j < n) m[j] *= rd;
+    }
+    hpre_lds[t * 4 + r] = pre;
+    if (act && tok < M) {
+        h_pre[(int64_t)tok * n + r] = pre;
+        h_post[(int64_t)tok * n + r] = post;
+#pragma unroll
+        for (int j = 0; j < kMaxStreams; ++j)
+            if (j < n) h_res[((int64_t)tok * n + r) * n + j] = m[j];
+    }
+}
+
 // ---------------------------------------------------------------- sinkhorn
 __global__ void sinkhorn_kernel(const float *__restrict__ h, int64_t batch, int n, int n_iter, float eps,
                                 float *__restrict__ out) {
@@ -178,49 +229,20 @@ __global__ __launch_bounds__(kPreThreads) void mhc_pre_kernel(PreArgs a) {
             for (int j = 0; j < 4; ++j) part[wave][16 * mt + 4 * kq + j][16 * nt + m] = acc[mt][nt][j];
     __syncthreads();
 
-    if (tid < kPreTok) {
-        const int t = tid;
-        const int tok = tok0 + t;
+    if (tid < 4 * kPreTok) {
+        const int t = tid >> 2, r = tid & 3;
         float ssum = 0.f;
 #pragma unroll
         for (int w = 0; w < kPreWaves; ++w) ssum += ssp[w][t];
-        const float r = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(ssum, (float)K) + a.rms_eps));
-        float dyn[kPhiRows];
-#pragma unroll
-        for (int o = 0; o < kPhiRows; ++o) {
+        const float rs = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(ssum, (float)K) + a.rms_eps));
+        auto dynf = [&](int o) {
             float s = 0.f;
 #pragma unroll
             for (int w = 0; w < kPreWaves; ++w) s += part[w][t][o];
-            dyn[o] = s * r;
-        }
-        const float ap = a.coef[0], aq = a.coef[1], ar = a.coef[2];
-        float hm[kMaxStreams][kMaxStreams];
-#pragma unroll
-        for (int s = 0; s < kMaxStreams; ++s) {
-            float pre = 0.f, post = 0.f;
-            if (s < n) {
-                pre = sigmoidf(ap * dyn[s] + a.bias[s]);
-                post = 2.0f * sigmoidf(aq * dyn[n + s] + a.bias[n + s]);
-            }
-            hpre_s[t][s] = pre;
-            if (tok < a.M && s < n) {
-                a.h_pre[(int64_t)tok * n + s] = pre;
-                a.h_post[(int64_t)tok * n + s] = post;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kMaxStreams; ++i)
-#pragma unroll
-            for (int j = 0; j < kMaxStreams; ++j)
-                hm[i][j] = (i < n && j < n) ? ar * dyn[2 * n + i * n + j] + a.bias[2 * n + i * n + j] : 0.f;
-        sinkhorn_regs<kMaxStreams>(hm, n, a.n_iter, a.sk_eps);
-        if (tok < a.M) {
-#pragma unroll
-            for (int i = 0; i < kMaxStreams; ++i)
-#pragma unroll
-                for (int j = 0; j < kMaxStreams; ++j)
-                    if (i < n && j < n) a.h_res[(int64_t)tok * n * n + i * n + j] = hm[i][j];
-        }
+            return s * rs;
+        };
+        token_constraints_quad(t, r, tok0 + t, a.M, n, a.coef, a.bias, a.n_iter, a.sk_eps, dynf, &hpre_s[0][0],
+                               a.h_pre, a.h_post, a.h_res);
     }
     __syncthreads();
 
@@ -237,6 +259,250 @@ __global__ __launch_bounds__(kPreThreads) void mhc_pre_kernel(PreArgs a) {
         f32x4 sum = {0.f, 0.f, 0.f, 0.f};
         for (int s = 0; s < n; ++s) sum += hpre_s[t][s] * Buf4<T>::load(xr, xo, (uint32_t)(s * C) * esz);
         Buf4<T>::store(sum, lr, ok ? (uint32_t)(((int64_t)tok * a.ld_in + c) * esz) : kOOB, 0);
+    }
+}
+
+// ---------------------------------------------------------------- pre, LDS-resident tile
+// Same results as mhc_pre_kernel, for rows up to 8 KB: a workgroup keeps its
+// whole tile of TT = 16*MT tokens (n*C values each) in LDS, so x is read
+// from HBM once.  phi arrives in matrix-core fragment order
+// ([K/16][2][64 lanes][4]: one coalesced 512-byte read per K step), the four
+// wavefronts split K, partial projections meet in LDS, one thread per token
+// runs the constraints, and layer_in (optionally RMS-normalised with a
+// weight, the block's attention_norm / ffn_norm) is formed from LDS.
+struct Pre2Args {
+    const void *x;
+    int64_t ldx;
+    int M, n, C;
+    const void *phi_frag;   // [K/16][2][64][4] activation dtype
+    const float *coef, *bias;
+    float rms_eps, sk_eps;
+    int n_iter;
+    float *h_pre, *h_post, *h_res;
+    void *layer_in;
+    int64_t ld_in;
+    const float *norm_w;    // nullable: layer_in = rmsnorm(layer_in) * norm_w
+    float norm_eps;
+};
+
+constexpr int kTileBytes = 128 * 1024;
+
+template <typename T, bool BF16MMA, int MT>
+__global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
+    constexpr int TT = 16 * MT;
+    constexpr uint32_t esz = sizeof(T);
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int n = a.n, C = a.C, K = n * C;
+    const int rowb = K * (int)esz;
+    const int stride = rowb + 8;              // 8-byte pad: 16 rows of a fragment read hit distinct banks
+    unsigned char *xs = smem;                 // [TT][stride]
+    float *part = (float *)(smem + TT * stride);              // [4][TT][33]
+    float *ssp = part + kPreWaves * TT * (kPhiRows + 1);     // [4][TT]
+    float *hpre = ssp + kPreWaves * TT;                      // [TT][4]
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tok0 = blockIdx.x * TT;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+
+    // phase 1 set-up (its first phi batch is requested before the tile lands)
+    const int m = lane & 15, kq = lane >> 4;
+    const int nks = K / 16;
+    const int ks_per = (nks + kPreWaves - 1) / kPreWaves;
+    const int ks0 = wave * ks_per, ks1 = min(nks, ks0 + ks_per);
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.phi_frag, (uint32_t)((int64_t)nks * 2 * 64 * 4 * esz));
+    constexpr int kPf = 8;                    // K steps of phi per batch
+    f32x4 pa[kPf][2], pbb[kPf][2];            // ping-pong buffers (static indexing keeps them in VGPRs)
+    auto load_phi = [&](int kb, f32x4 (&dst)[kPf][2]) {
+#pragma unroll
+        for (int u = 0; u < kPf; ++u)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int ks = kb + u;
+                dst[u][nt] = Buf4<T>::load(
+                    pr, ks < ks1 ? (uint32_t)((((int64_t)ks * 2 + nt) * 64 + lane) * 4 * esz) : kOOB, 0);
+            }
+    };
+
+    // phase 0: tile -> LDS, all 16-byte loads in flight together
+    {
+        const int cpr = rowb / 16;            // chunks per row
+        const int nch = TT * cpr;
+        const bool pow2 = (cpr & (cpr - 1)) == 0;
+        const int lg = 31 - __builtin_clz(cpr);
+        constexpr int kMaxPer = kTileBytes / 16 / kPreThreads;   // 32
+        u32x4 st[kMaxPer];
+#pragma unroll
+        for (int j = 0; j < kMaxPer; ++j) {
+            const int ch = tid + j * kPreThreads;
+            const int r = pow2 ? (ch >> lg) : ch / cpr, cc = ch - r * cpr;
+            const bool ok = ch < nch && tok0 + r < a.M;
+            st[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                xr, ok ? (uint32_t)(((int64_t)(tok0 + r) * a.ldx) * esz + cc * 16) : kOOB, 0, 0);
+        }
+        load_phi(ks0, pa);
+#pragma unroll
+        for (int j = 0; j < kMaxPer; ++j) {
+            const int ch = tid + j * kPreThreads;
+            if (ch < nch) {
+                const int r = pow2 ? (ch >> lg) : ch / cpr, cc = ch - r * cpr;
+                u32x2 *d = (u32x2 *)(xs + r * stride + cc * 16);
+                d[0] = u32x2{st[j].x, st[j].y};
+                d[1] = u32x2{st[j].z, st[j].w};
+            }
+        }
+    }
+    __syncthreads();
+
+    // phase 1: projection on matrix cores, K split over the 4 wavefronts
+    f32x4 acc[MT][2];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ss[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) ss[i] = 0.f;
+    auto compute = [&](int kb, const f32x4 (&p)[kPf][2]) {
+#pragma unroll
+        for (int u = 0; u < kPf; ++u) {
+            const int ks = kb + u;
+            if (ks >= ks1) break;
+            const int k = ks * 16 + 4 * kq;
+            uint2 bv[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                bv[nt].x = pack_bf16x2(p[u][nt].x, p[u][nt].y);
+                bv[nt].y = pack_bf16x2(p[u][nt].z, p[u][nt].w);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const unsigned char *src = xs + (16 * mt + m) * stride + k * esz;
+                f32x4 xa;
+                if constexpr (sizeof(T) == 2) {
+                    const u32x2 u2 = *(const u32x2 *)src;
+                    xa.x = __uint_as_float(u2.x << 16);
+                    xa.y = __uint_as_float(u2.x & 0xffff0000u);
+                    xa.z = __uint_as_float(u2.y << 16);
+                    xa.w = __uint_as_float(u2.y & 0xffff0000u);
+                } else {
+                    const u32x2 lo = *(const u32x2 *)src, hi = *(const u32x2 *)(src + 8);
+                    xa = __builtin_bit_cast(f32x4, u32x4{lo.x, lo.y, hi.x, hi.y});
+                }
+                ss[mt] += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w;
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    if constexpr (BF16MMA) {
+                        uint2 av;
+                        av.x = pack_bf16x2(xa.x, xa.y);
+                        av.y = pack_bf16x2(xa.z, xa.w);
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                            __builtin_bit_cast(i16x4, av), __builtin_bit_cast(i16x4, bv[nt]), acc[mt][nt], 0, 0, 0);
+                    } else {
+#pragma unroll
+                        for (int s2 = 0; s2 < 4; ++s2)
+                            acc[mt][nt] =
+                                __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s2], p[u][nt][s2], acc[mt][nt], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    };
+    for (int kb = ks0; kb < ks1; kb += 2 * kPf) {
+        if (kb + kPf < ks1) load_phi(kb + kPf, pbb);
+        compute(kb, pa);
+        if (kb + kPf < ks1) {
+            if (kb + 2 * kPf < ks1) load_phi(kb + 2 * kPf, pa);
+            compute(kb + kPf, pbb);
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        ss[mt] += __shfl_xor(ss[mt], 16);
+        ss[mt] += __shfl_xor(ss[mt], 32);
+        if (kq == 0) ssp[wave * TT + 16 * mt + m] = ss[mt];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                part[(wave * TT + 16 * mt + 4 * kq + j) * (kPhiRows + 1) + 16 * nt + m] = acc[mt][nt][j];
+    }
+    __syncthreads();
+
+    // phase 2: per-token constraints, 4 lanes per token
+    if (tid < 4 * TT) {
+        const int t = tid >> 2, r = tid & 3;
+        float ssum = 0.f;
+#pragma unroll
+        for (int w = 0; w < kPreWaves; ++w) ssum += ssp[w * TT + t];
+        const float rs = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(ssum, (float)K) + a.rms_eps));
+        auto dynf = [&](int o) {
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < kPreWaves; ++w) s += part[(w * TT + t) * (kPhiRows + 1) + o];
+            return s * rs;
+        };
+        token_constraints_quad(t, r, tok0 + t, a.M, n, a.coef, a.bias, a.n_iter, a.sk_eps, dynf, hpre, a.h_pre,
+                               a.h_post, a.h_res);
+    }
+    __syncthreads();
+
+    // phase 3: layer_in = sum_s H_pre[s] x[s, :] (8 threads per token, 4 values per
+    // item), optional RMS normalisation over the row with weight norm_w
+    {
+        const int t = tid >> 3, sub = tid & 7;
+        const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
+        constexpr int kMaxQ = 1024 / 4 / 8;   // C <= 1024: at most 32 quads per thread
+        for (int tb = 0; tb < TT; tb += kPreThreads / 8) {
+            const int tt = tb + t;
+            if (tt >= TT) continue;           // whole 8-lane groups skip together
+            const int tok = tok0 + tt;
+            const int nq = C / 4;
+            f32x4 v[kMaxQ];
+            float sq = 0.f;
+            float hp[kMaxStreams];
+#pragma unroll
+            for (int s = 0; s < kMaxStreams; ++s) hp[s] = hpre[tt * 4 + s];
+#pragma unroll
+            for (int j = 0; j < kMaxQ; ++j) {
+                const int q = sub + 8 * j;
+                f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
+                if (q < nq) {
+#pragma unroll
+                    for (int s = 0; s < kMaxStreams; ++s) {
+                        if (s >= n) continue;
+                        const unsigned char *src = xs + tt * stride + (s * C + 4 * q) * esz;
+                        f32x4 xv;
+                        if constexpr (sizeof(T) == 2) {
+                            const u32x2 u2 = *(const u32x2 *)src;
+                            xv.x = __uint_as_float(u2.x << 16);
+                            xv.y = __uint_as_float(u2.x & 0xffff0000u);
+                            xv.z = __uint_as_float(u2.y << 16);
+                            xv.w = __uint_as_float(u2.y & 0xffff0000u);
+                        } else {
+                            const u32x2 lo = *(const u32x2 *)src, hi = *(const u32x2 *)(src + 8);
+                            xv = __builtin_bit_cast(f32x4, u32x4{lo.x, lo.y, hi.x, hi.y});
+                        }
+                        acc4 += hp[s] * xv;
+                    }
+                }
+                v[j] = acc4;
+                sq += acc4.x * acc4.x + acc4.y * acc4.y + acc4.z * acc4.z + acc4.w * acc4.w;
+            }
+            float scale = 1.f;
+            if (a.norm_w) {
+                sq += __shfl_xor(sq, 1);
+                sq += __shfl_xor(sq, 2);
+                sq += __shfl_xor(sq, 4);
+                scale = 1.0f / sqrtf(__fdiv_rn(sq, (float)C) + a.norm_eps);
+            }
+            const bool ok = tok < a.M;
+#pragma unroll
+            for (int j = 0; j < kMaxQ; ++j) {
+                const int q = sub + 8 * j;
+                if (q >= nq) continue;
+                f32x4 o = v[j] * scale;
+                if (a.norm_w) o *= *(const f32x4 *)(a.norm_w + 4 * q);
+                Buf4<T>::store(o, lr, ok ? (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz) : kOOB, 0);
+            }
+        }
     }
 }
 
@@ -390,6 +656,74 @@ WALSH_EXPORT int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out,
                                h_res + r0 * n * n, h_post + r0 * n, (float *)x_new + r0 * ld_new, ld_new, (int)rows,
                                (int)n, (int)C);
         const int rc = check_hip(hipGetLastError(), "walsh_mhc_post_fwd launch");
+        if (rc) return rc;
+    }
+    return WALSH_OK;
+}
+
+WALSH_EXPORT int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C,
+                                        const void *phi_frag, const float *coef, const float *bias, float rms_eps,
+                                        int64_t n_iter, float sk_eps, float *h_pre, float *h_post, float *h_res,
+                                        void *layer_in, int64_t ld_in, const float *norm_w, float norm_eps,
+                                        int dtype, void *stream) {
+    if (!x || !phi_frag || !coef || !bias || !h_pre || !h_post || !h_res || !layer_in)
+        return set_error(WALSH_EINVAL, "walsh_mhc_pre_norm_fwd: null pointer");
+    if (M < 0 || n < 1 || C < 4 || ldx < n * C || ld_in < C || n_iter < 0)
+        return set_error(WALSH_EINVAL, "walsh_mhc_pre_norm_fwd: bad shape M=%lld n=%lld C=%lld", (long long)M,
+                         (long long)n, (long long)C);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: dtype");
+    const int64_t esz = dtype == WALSH_BF16 ? 2 : 4;
+    const int64_t rowb = n * C * esz;
+    if (n > kMaxStreams || (n * C) % 16 || C % 4 || C > 1024 || rowb % 16 || ldx % (16 / esz) || ld_in % 4 ||
+        rowb * 16 > kTileBytes)
+        return set_error(WALSH_ENOTSUP,
+                         "walsh_mhc_pre_norm_fwd: needs n <= %d, n*C %% 16 == 0, C <= 1024, 16 rows in 128 KB",
+                         kMaxStreams);
+    if ((uintptr_t)x % 16 || (uintptr_t)layer_in % 16 || (uintptr_t)phi_frag % 16 || (norm_w && (uintptr_t)norm_w % 16))
+        return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: pointers must be 16-byte aligned");
+    if (M == 0) return WALSH_OK;
+    // 16-token tiles: ~74 KB of LDS at 4 KB rows, so two workgroups share a
+    // CU and overlap their load / projection / write phases
+    const int MT = 1;
+    const int TT = 16 * MT;
+    const size_t lds = (size_t)TT * (rowb + 8) + (size_t)kPreWaves * TT * (kPhiRows + 1) * 4 + kPreWaves * TT * 4 +
+                       TT * 16;
+    if (lds > (size_t)device_info().max_shared_per_block)
+        return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: needs %zu B of LDS", lds);
+    const int64_t ld = ldx > ld_in ? ldx : ld_in;
+    int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / TT * TT;
+    if (rows_max < TT) return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: row stride too large");
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        Pre2Args a;
+        a.x = (const char *)x + r0 * ldx * esz;
+        a.ldx = ldx;
+        a.M = (int)rows;
+        a.n = (int)n;
+        a.C = (int)C;
+        a.phi_frag = phi_frag;
+        a.coef = coef;
+        a.bias = bias;
+        a.rms_eps = rms_eps;
+        a.sk_eps = sk_eps;
+        a.n_iter = (int)n_iter;
+        a.h_pre = h_pre + r0 * n;
+        a.h_post = h_post + r0 * n;
+        a.h_res = h_res + r0 * n * n;
+        a.layer_in = (char *)layer_in + r0 * ld_in * esz;
+        a.ld_in = ld_in;
+        a.norm_w = norm_w;
+        a.norm_eps = norm_eps;
+        const dim3 G((unsigned)ceil_div(rows, TT)), B(kPreThreads);
+        hipStream_t s = (hipStream_t)stream;
+        if (dtype == WALSH_BF16) {
+            if (MT == 2) hipLaunchKernelGGL((mhc_pre2_kernel<uint16_t, true, 2>), G, B, lds, s, a);
+            else hipLaunchKernelGGL((mhc_pre2_kernel<uint16_t, true, 1>), G, B, lds, s, a);
+        } else {
+            if (MT == 2) hipLaunchKernelGGL((mhc_pre2_kernel<float, false, 2>), G, B, lds, s, a);
+            else hipLaunchKernelGGL((mhc_pre2_kernel<float, false, 1>), G, B, lds, s, a);
+        }
+        const int rc = check_hip(hipGetLastError(), "walsh_mhc_pre_norm_fwd launch");
         if (rc) return rc;
     }
     return WALSH_OK;

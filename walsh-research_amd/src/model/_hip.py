@@ -30,6 +30,9 @@ SIGNATURES = {
     "walsh_hadamard_weight_bytes": (_I64, [_I64, _I64]),
     "walsh_hadamard_prepare": (_I, [_P, _I64, _I64, _P, _P]),
     "walsh_hadamard_linear_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I, _P]),
+    "walsh_hadamard_linear_ex_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _I, _P]),
+    "walsh_hadamard_swiglu_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                       _I, _P]),
     "walsh_fht_fwd": (_I, [_P, _I64, _I64, _I, _P, _I, _P]),
     "walsh_octonion_weight_elems": (_I64, [_I64, _I64]),
     "walsh_octonion_prepare": (_I, [_P, _I64, _I64, _P, _I, _P]),
@@ -37,6 +40,8 @@ SIGNATURES = {
     "walsh_sinkhorn_fwd": (_I, [_P, _I64, _I64, _I64, ctypes.c_float, _P, _P]),
     "walsh_mhc_pre_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float, _I64, ctypes.c_float,
                                _P, _P, _P, _P, _I64, _I, _P]),
+    "walsh_mhc_pre_norm_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float, _I64, ctypes.c_float,
+                                    _P, _P, _P, _P, _I64, _P, ctypes.c_float, _I, _P]),
     "walsh_mhc_post_fwd": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P]),
 }
 

@@ -19,6 +19,7 @@ from torch.nn import functional as F
 from .hadamard import HadamardLinear, HadamardTernaryLinear, HadamardTernaryLinearTuple  # noqa: F401
 from .hadamard import HadamardHeadMixer, HadamardHeadMixerFused
 from .octonion import OctonionHeadMixerFused, OctonionTernaryLinear
+from . import kernels
 from ._common import act_dtype
 
 _HADAMARD_AVAILABLE = True
@@ -203,6 +204,15 @@ class SwiGLUMLP(nn.Module):
 
     def forward(self, x):
         x = x.to(act_dtype(x))
+        if isinstance(self.gate_proj, HadamardTernaryLinearTuple):
+            # fused gate/up/silu*mul; the hidden activation stays in a
+            # group-padded layout (stride roundup(hid_o, 4)) read in place by down_proj
+            g, u, d = self.gate_proj.inner, self.up_proj.inner, self.down_proj.inner
+            hid_o = g.out_o
+            h = kernels.hadamard_swiglu(x, g.in_o, hid_o, (g.ternary_state()[2], g.alpha, g.beta),
+                                        (u.ternary_state()[2], u.alpha, u.beta))
+            return kernels.hadamard_linear(h, d.in_o, d.out_o, d.ternary_state()[2], d.alpha, d.beta,
+                                           gsx=h.shape[-1] // 32)
         h = F.silu(_full(self.gate_proj, x)) * _full(self.up_proj, x)
         return _full(self.down_proj, h)
 

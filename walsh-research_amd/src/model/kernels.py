@@ -103,38 +103,77 @@ def hadamard_prepare(packed: torch.Tensor, in_o: int, out_o: int) -> torch.Tenso
     return kw
 
 
+def _had_meta(rows, in_o, out_o, dt, vec, kc1, swiglu=False):
+    esz = 2 if dt == torch.bfloat16 else 4
+    tag = "bf16" if dt == torch.bfloat16 else "f32"
+    if swiglu:
+        kname = "hadamard_swiglu_kernel<%s,%s>" % (tag, "vec" if vec else "scalar")
+        nbytes = rows * 32 * (in_o + out_o) * esz + 2 * 32 * out_o * ((in_o + 3) // 4) + 8 * 32 * (in_o + out_o)
+        flops = rows * 2 * (2 * 32 * in_o * out_o + 10 * 32 * (in_o + out_o)) + rows * 32 * out_o * 4
+    else:
+        kname = "hadamard_fwd_kernel<%s,%s,%s>" % (tag, "vec" if vec else "scalar", "kc1" if kc1 else "kloop")
+        nbytes = rows * 32 * (in_o + out_o) * esz + 32 * out_o * ((in_o + 3) // 4) + 4 * 32 * (in_o + out_o)
+        flops = rows * (2 * 32 * in_o * out_o + 10 * 32 * (in_o + out_o) + 32 * (in_o + out_o))
+    return kname, nbytes, flops
+
+
 def hadamard_linear(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tensor, alpha: torch.Tensor,
-                    beta: torch.Tensor, out_dtype: torch.dtype = None) -> torch.Tensor:
-    """HadamardLinear forward (fht_cuda.py:489-519) on x [..., >=32*in_o].
+                    beta: torch.Tensor, out_dtype: torch.dtype = None, gsx: int = None,
+                    gsy: int = None) -> torch.Tensor:
+    """HadamardLinear forward (fht_cuda.py:489-519) on x [..., >=32*gsx].
 
     Computes in float32 matrix cores for float32 activations and bf16 matrix
-    cores (float32 accumulate) for bfloat16 activations.  Returns
-    [..., 32*out_o] in ``out_dtype`` (default x.dtype; must equal it)."""
+    cores (float32 accumulate) for bfloat16 activations.  gsx / gsy are the
+    group strides of the input and output rows (default in_o / out_o); the
+    result is [..., 32*gsy] in ``out_dtype`` (default x.dtype; must equal it)."""
     _hip.require_device(x, "input")
     dt = x.dtype if out_dtype is None else out_dtype
     if dt != x.dtype:
         x = x.to(dt)
     code = _hip.dtype_code(dt)
-    C_in = 32 * in_o
+    gsx = in_o if gsx is None else gsx
+    gsy = out_o if gsy is None else gsy
     lead = x.shape[:-1]
-    xv, rows, ldx = _rows_view(x, C_in)
-    y = torch.empty(lead + (32 * out_o,), device=x.device, dtype=dt)
+    xv, rows, ldx = _rows_view(x, 32 * gsx)
+    y = torch.empty(lead + (32 * gsy,), device=x.device, dtype=dt)
     if rows == 0:
         return y
     alpha = alpha.detach().float().contiguous()
     beta = beta.detach().float().contiguous()
-    assert alpha.numel() == C_in and beta.numel() == 32 * out_o, "alpha/beta shapes"
+    assert alpha.numel() == 32 * in_o and beta.numel() == 32 * out_o, "alpha/beta shapes"
     esz = x.element_size()
-    vec = in_o % 4 == 0 and out_o % 4 == 0 and ldx % 4 == 0 and xv.data_ptr() % (4 * esz) == 0
+    vec = gsx % 4 == 0 and gsy % 4 == 0 and ldx % 4 == 0 and xv.data_ptr() % (4 * esz) == 0
     kc1 = in_o <= 16 and (dt == torch.bfloat16 or out_o <= 16)
-    kname = "hadamard_fwd_kernel<%s,%s,%s>" % ("bf16" if dt == torch.bfloat16 else "f32",
-                                                "vec" if vec else "scalar", "kc1" if kc1 else "kloop")
-    nbytes = rows * 32 * (in_o + out_o) * esz + 32 * out_o * ((in_o + 3) // 4) + 4 * 32 * (in_o + out_o)
-    flops = rows * (2 * 32 * in_o * out_o + 5 * 32 * (in_o + out_o) * 2 + 32 * (in_o + out_o))
-    _hip.call("walsh_hadamard_linear_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, kweight.data_ptr(),
-              alpha.data_ptr(), beta.data_ptr(), y.data_ptr(), 32 * out_o, code, _hip.stream(x.device),
+    kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, vec, kc1)
+    _hip.call("walsh_hadamard_linear_ex_fwd", xv.data_ptr(), ldx, gsx, rows, in_o, out_o, kweight.data_ptr(),
+              alpha.data_ptr(), beta.data_ptr(), y.data_ptr(), 32 * gsy, gsy, code, _hip.stream(x.device),
               kernel=kname, nbytes=nbytes, flops=flops)
     return y
+
+
+def hadamard_swiglu(x: torch.Tensor, in_o: int, hid_o: int, gate, up, gsh: int = None) -> torch.Tensor:
+    """silu(gate(x)) * up(x) for two Hadamard linears (chassis.py:498-504);
+    gate/up = (kweight, alpha, beta).  Returns [..., 32*gsh] with group stride
+    gsh (default roundup(hid_o, 4); pad slots are zeros)."""
+    _hip.require_device(x, "input")
+    dt = x.dtype
+    code = _hip.dtype_code(dt)
+    gsh = ((hid_o + 3) // 4) * 4 if gsh is None else gsh
+    lead = x.shape[:-1]
+    xv, rows, ldx = _rows_view(x, 32 * in_o)
+    h = torch.empty(lead + (32 * gsh,), device=x.device, dtype=dt)
+    if rows == 0:
+        return h
+    kg, ag, bg = gate
+    ku, au, bu = up
+    ag, bg, au, bu = (t.detach().float().contiguous() for t in (ag, bg, au, bu))
+    esz = x.element_size()
+    vec = in_o % 4 == 0 and gsh % 4 == 0 and ldx % 4 == 0 and xv.data_ptr() % (4 * esz) == 0
+    kname, nbytes, flops = _had_meta(rows, in_o, hid_o, dt, vec, True, swiglu=True)
+    _hip.call("walsh_hadamard_swiglu_fwd", xv.data_ptr(), ldx, in_o, rows, in_o, hid_o, kg.data_ptr(), ag.data_ptr(),
+              bg.data_ptr(), ku.data_ptr(), au.data_ptr(), bu.data_ptr(), h.data_ptr(), 32 * gsh, gsh, code,
+              _hip.stream(x.device), kernel=kname, nbytes=nbytes, flops=flops)
+    return h
 
 
 def fht(x: torch.Tensor, normalize: bool = True) -> torch.Tensor:
@@ -233,6 +272,51 @@ def mhc_pre(x: torch.Tensor, phi_cat: torch.Tensor, coef: torch.Tensor, bias_cat
               h_res.data_ptr(), layer_in.data_ptr(), C, _hip.dtype_code(x.dtype), _hip.stream(dev),
               kernel="mhc_pre_kernel<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"), nbytes=nbytes,
               flops=flops)
+    return layer_in, h_pre, h_post, h_res
+
+
+def phi_fragments(phi_cat: torch.Tensor) -> torch.Tensor:
+    """phi_cat [32, K] -> matrix-core fragment order [K/16][2][64][4] (K % 16 == 0)."""
+    K = phi_cat.shape[1]
+    return phi_cat.view(2, 16, K // 16, 4, 4).permute(2, 0, 3, 1, 4).contiguous()
+
+
+def mhc_pre_supported(n: int, C: int, dtype: torch.dtype) -> bool:
+    """Whether walsh_mhc_pre_norm_fwd handles this shape (16 rows fit in LDS)."""
+    esz = 2 if dtype == torch.bfloat16 else 4
+    return n <= 4 and (n * C) % 16 == 0 and C % 4 == 0 and C <= 1024 and n * C * esz * 16 <= 128 * 1024
+
+
+def mhc_pre_norm(x: torch.Tensor, phi_frag: torch.Tensor, coef: torch.Tensor, bias_cat: torch.Tensor,
+                 rms_eps: float, norm_w: torch.Tensor = None, norm_eps: float = 1e-6, n_iter: int = 20,
+                 sk_eps: float = 1e-8):
+    """mhc_pre with the token tile held in LDS (one HBM pass over x) and the
+    optional RMSNorm of layer_in fused (chassis.py:96-106)."""
+    _hip.require_device(x, "stream input")
+    n, C = x.shape[-2], x.shape[-1]
+    lead = x.shape[:-2]
+    xv = x if x.is_contiguous() else x.contiguous()
+    M = xv.numel() // (n * C)
+    dev = x.device
+    layer_in = torch.empty(lead + (C,), device=dev, dtype=x.dtype)
+    h_pre = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_post = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_res = torch.empty(lead + (n, n), device=dev, dtype=torch.float32)
+    if M == 0:
+        return layer_in, h_pre, h_post, h_res
+    assert phi_frag.dtype == x.dtype and phi_frag.numel() == 32 * n * C, "phi_frag layout"
+    nw = None
+    if norm_w is not None:
+        nw = norm_w.detach().float().contiguous()
+        assert nw.numel() == C
+    esz = x.element_size()
+    nbytes = M * (n * C + C) * esz + M * (2 * n + n * n) * 4 + 32 * n * C * esz
+    flops = M * (2 * n * C * 32 + 2 * n * C + 2 * n * C)
+    _hip.call("walsh_mhc_pre_norm_fwd", xv.data_ptr(), n * C, M, n, C, phi_frag.data_ptr(), coef.data_ptr(),
+              bias_cat.data_ptr(), float(rms_eps), int(n_iter), float(sk_eps), h_pre.data_ptr(), h_post.data_ptr(),
+              h_res.data_ptr(), layer_in.data_ptr(), C, _hip.ptr(nw), float(norm_eps), _hip.dtype_code(x.dtype),
+              _hip.stream(dev), kernel="mhc_pre2_kernel<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"),
+              nbytes=nbytes, flops=flops)
     return layer_in, h_pre, h_post, h_res
 
 

@@ -126,20 +126,40 @@ class mHCResidualStream(nn.Module):
                                     (self.H_res.phi.weight, n * n)], dtype, device)
             coef = torch.stack([m.alpha.detach().float() for m in maps]).to(device)
             bias = torch.cat([m.bias.detach().float().reshape(-1) for m in maps]).to(device)
-            return phi, coef, bias
+            frag = kernels.phi_fragments(phi) if (n * C) % 16 == 0 else None
+            return phi, coef, bias, frag
 
         tensors = [t for m in maps for t in (m.phi.weight, m.alpha, m.bias)]
         return self._cache.get(tensors, build, extra=(dtype, device))
 
-    def forward(self, x, layer_fn):
-        """x [B, T, n, C]; layer_fn maps [B, T, C] -> [B, T, C]."""
-        n = self.n_streams
+    def _pre(self, x, dt, norm=None):
+        n, C = self.n_streams, self.n_embd
         if n > _MAX_STREAMS:
             raise NotImplementedError(f"n_streams={n} > {_MAX_STREAMS} is not supported by this build")
+        phi, coef, bias, frag = self.fused_params(dt, x.device)
+        if frag is not None and kernels.mhc_pre_supported(n, C, dt):
+            return kernels.mhc_pre_norm(x, frag, coef, bias, _rms_eps(dt),
+                                        norm_w=None if norm is None else norm.weight,
+                                        norm_eps=1e-6 if norm is None else norm.eps)
+        li, hp, hq, hr = kernels.mhc_pre(x, phi, coef, bias, _rms_eps(dt))
+        if norm is not None:
+            li = norm(li).to(dt)
+        return li, hp, hq, hr
+
+    def forward(self, x, layer_fn):
+        """x [B, T, n, C]; layer_fn maps [B, T, C] -> [B, T, C]."""
         dt = act_dtype(x)
         x = x.to(dt)
-        phi, coef, bias = self.fused_params(dt, x.device)
-        layer_in, _, h_post, h_res = kernels.mhc_pre(x, phi, coef, bias, _rms_eps(dt))
+        layer_in, _, h_post, h_res = self._pre(x, dt)
+        out = layer_fn(layer_in)
+        return kernels.mhc_post(x, out, h_res, h_post)
+
+    def forward_normed(self, x, norm, layer_fn):
+        """forward(x, lambda v: layer_fn(norm(v))) with the RMSNorm ``norm``
+        (chassis.RMSNorm) fused into the mapping kernel."""
+        dt = act_dtype(x)
+        x = x.to(dt)
+        layer_in, _, h_post, h_res = self._pre(x, dt, norm=norm)
         out = layer_fn(layer_in)
         return kernels.mhc_post(x, out, h_res, h_post)
 
@@ -193,17 +213,13 @@ class mHCLlamaBlock(nn.Module):
         self.ffn_stream = mHCResidualStream(config.n_embd, n_streams)
 
     def forward(self, x, freqs_cis, kv_cache=None, layer_idx=0):
-        dt = act_dtype(x)
-
-        def attn_fn(x_in):
-            return self.attention(self.attention_norm(x_in).to(dt), freqs_cis, kv_cache=kv_cache,
-                                  layer_idx=layer_idx)
-
-        def ffn_fn(x_in):
-            return self.feed_forward(self.ffn_norm(x_in).to(dt))
-
-        x = self.attn_stream(x, attn_fn)
-        return self.ffn_stream(x, ffn_fn)
+        # attn_stream(x, attention(attention_norm(.))) then
+        # ffn_stream(x, feed_forward(ffn_norm(.))) (mhc.py:507-534), with each
+        # RMSNorm fused into its stream's mapping kernel
+        x = self.attn_stream.forward_normed(
+            x, self.attention_norm,
+            lambda v: self.attention(v, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx))
+        return self.ffn_stream.forward_normed(x, self.ffn_norm, lambda v: self.feed_forward(v))
 
 
 class mHCWalsh(nn.Module):
