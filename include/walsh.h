@@ -202,6 +202,71 @@ int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out, int64_t ld_o
                        const float *h_post, void *x_new, int64_t ld_new, int64_t M, int64_t n, int64_t C, int dtype,
                        void *stream);
 
+/* ------------------------------------------------------------------ A10-A13
+ * Hadamard mixture-of-experts FFN (src/model/moe.py:306-560).  Expert e owns
+ * the 32-wide feature block x[:, 32e:32e+32]; E <= 128 experts; each token
+ * is routed to k = min(max_experts, E) <= 8 experts.
+ *
+ * Routing outputs (shared by walsh_moe_route_fwd and walsh_moe_topk_fwd):
+ *   topk_idx [M, k] int32, experts by decreasing probability (equal
+ *     probabilities: lower expert index first);
+ *   topk_w [M, k] float32, probs / max(sum of the selected probs, 1e-8);
+ *   count [E] int32 = tokens routed to each expert; probsum [E] float32 =
+ *     sum over tokens of the softmax probability (for the balance loss);
+ *     both are cleared by the call itself;
+ *   cursor [E] int32 scratch for walsh_moe_scatter (cleared by the call);
+ *   probs / mask / weights_dense [M, E] float32 are optional (NULL skips):
+ *     the three outputs of HadamardRouter.forward.
+ *
+ * walsh_moe_route_fwd: HadamardRouter.forward (src/model/moe.py:418-447),
+ *   logits = W2 silu(W1 x) (no biases), softmax (float32), top-k,
+ *   renormalised weights.  x [M, C] (row stride ldx, dtype), W1 [H1, C] and
+ *   W2 [E, H1] given in matrix-core fragment order (dtype elements):
+ *   w1_frag[H1/16][C/16][64][4] holds W1[16a + l%16][16b + 4(l/16) + j] and
+ *   w2_frag[ceil(E/16)][H1/16][64][4] holds W2[16a + l%16][16b + 4(l/16) + j]
+ *   (rows >= E zero).  With dtype WALSH_BF16 the hidden activations and the
+ *   logits are rounded to bfloat16 where torch.autocast rounds them.  If y
+ *   is not NULL, the output blocks y[t, 32e:32e+32] (ydtype, row stride ldy)
+ *   of every unselected expert are set to zero.  Needs C % 16 == 0,
+ *   H1 % 16 == 0, E <= 64.
+ */
+int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_t H1, const void *w1_frag,
+                        const void *w2_frag, int64_t E, int64_t k, float *probs, float *mask, float *weights_dense,
+                        int *topk_idx, float *topk_w, int *count, float *probsum, int *cursor, void *y,
+                        int64_t ldy, int dtype, int ydtype, void *stream);
+
+/* walsh_moe_topk_fwd: the softmax / top-k / renormalisation part of
+ *   HadamardRouter.forward (src/model/moe.py:432-445) from given float32
+ *   logits [M, E] (contiguous). */
+int walsh_moe_topk_fwd(const float *logits, int64_t M, int64_t E, int64_t k, float *probs, float *mask,
+                       float *weights_dense, int *topk_idx, float *topk_w, int *count, float *probsum, int *cursor,
+                       void *stream);
+
+/* walsh_moe_scatter: per-expert lists of the M*k (token, slot) pairs, the
+ *   grouping that replaces the dense all-expert einsum of
+ *   FastMoEExperts.forward (src/model/moe.py:363-374).  list [M*k] holds
+ *   pair ids t*k + j grouped by expert (order inside a group unspecified);
+ *   offset [E+1] = exclusive scan of count; tile_off [E+1] = exclusive scan
+ *   of ceil(count/16).  Reads the count and cursor a routing call wrote. */
+int walsh_moe_scatter(const int *topk_idx, int64_t M, int64_t E, int64_t k, const int *count, int *cursor,
+                      int *list, int *offset, int *tile_off, void *stream);
+
+/* walsh_moe_experts_fwd: FastMoEExperts.forward (src/model/moe.py:337-380)
+ *   on the routed pairs only: y[t, 32e:32e+32] = w * down_e(silu(gate_e x_e)
+ *   * up_e x_e) for x_e = x[t, 32e:32e+32], with ternary weights
+ *   code * gamma (moe.py:268-303).  Expert hidden size H in {64, 128, 256}.
+ *   Packed codes (2-bit, pack_ternary_weights byte order) in fragment order:
+ *   gate_frag/up_frag [E][H/16][2][64]: byte of row 16a + l%16, K bytes
+ *   4c + l/16 (c = second index); down_frag [E][2][H/16][64]: byte of row
+ *   16m + l%16, K byte 4b + l/16.  gammas [3] float32 (gate, up, down).
+ *   Writes only the selected blocks of y (the router zero-fills the rest).
+ *   (dtype, ydtype) is (f32, f32), (bf16, bf16) or (bf16, f32); bf16
+ *   rounds where torch.autocast rounds. */
+int walsh_moe_experts_fwd(const void *x, int64_t ldx, void *y, int64_t ldy, int64_t M, int64_t E, int64_t k,
+                          int64_t H, const uint8_t *gate_frag, const uint8_t *up_frag, const uint8_t *down_frag,
+                          const float *gammas, const int *list, const int *offset, const int *tile_off,
+                          const int *count, const float *topk_w, int dtype, int ydtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

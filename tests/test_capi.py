@@ -43,3 +43,20 @@ def test_identity_calls_need_no_gpu():
     L = _hip.lib()
     assert L.walsh_abi_version() == 1
     assert L.walsh_device_arch() == b"gfx950"
+
+
+def declared_arities():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(walsh_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_ctypes_arity_matches_header():
+    from src.model import _hip
+    ar = declared_arities()
+    bad = {n: (ar[n], len(a)) for n, (_, a) in _hip.SIGNATURES.items() if ar.get(n) != len(a)}
+    assert not bad, bad

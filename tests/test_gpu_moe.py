@@ -1,0 +1,286 @@
+"""GPU parity of the Hadamard MoE FFN (router, top-k routing, scatter,
+routed experts, HadamardMoE module) against oracle/moe.py.
+
+Bars:
+  * routing from given logits (walsh_moe_topk_fwd): expert indices, mask and
+    counts bit-exact; probabilities / weights within 1e-6 relative;
+  * end to end in float32: assignments equal the oracle's for every token
+    whose k-th and (k+1)-th probabilities are not a near tie (gap below
+    1e-6 * p; near ties are counted and reported), outputs within 1e-5
+    relative on the tokens routed identically;
+  * bfloat16 (autocast): outputs within 1e-2 relative of the oracle run on
+    the same routing; assignments differ from the float64 oracle only where
+    the bf16-rounded logits make the k-th choice a near tie.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as omoe
+from oracle import ternary as otern
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2}
+
+
+def rel(y, ref):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    d = y - ref
+    n = np.linalg.norm(ref)
+    m = np.abs(ref).max()
+    return (np.linalg.norm(d) / n if n > 0 else np.linalg.norm(d),
+            np.abs(d).max() / m if m > 0 else np.abs(d).max())
+
+
+def check(y, ref, tol, what):
+    a, b = rel(y, ref)
+    print(f"{what}: rel_norm={a:.3e} rel_max={b:.3e} tol={tol}", flush=True)
+    assert a <= tol and b <= tol, (what, a, b)
+
+
+@pytest.fixture(scope="module")
+def K():
+    from src.model import kernels
+    return kernels
+
+
+class Cfg:
+    def __init__(self, n_embd):
+        self.n_embd = n_embd
+
+
+def make_moe(C, max_experts=6, expansion=4, seed=0, router_std=0.02):
+    from src.model.moe import HadamardMoE
+    torch.manual_seed(seed)
+    m = HadamardMoE(Cfg(C), max_experts=max_experts, expansion=expansion)
+    with torch.no_grad():
+        for lin in (m.router.gate[0], m.router.gate[2]):
+            lin.weight.normal_(0.0, router_std)
+    return m.cuda()
+
+
+def sd_np(m):
+    return {k: v.detach().cpu().numpy() for k, v in m.state_dict().items()}
+
+
+def near_ties(probs, k, rel_gap=1e-6):
+    s = -np.sort(-np.asarray(probs, np.float64), axis=-1)
+    if k >= s.shape[-1]:
+        return np.zeros(s.shape[0], bool)
+    return (s[:, k - 1] - s[:, k]) < rel_gap * s[:, k - 1]
+
+
+# ------------------------------------------------------------ routing from logits
+
+@pytest.mark.parametrize("M,E,k", [(1000, 16, 6), (77, 16, 4), (513, 128, 6), (64, 128, 8), (50, 20, 3),
+                                   (33, 48, 6), (16, 1, 1), (40, 8, 8), (0, 16, 6)])
+def test_topk_routing_bit_exact(K, M, E, k):
+    rng = np.random.default_rng(M * 131 + E * 7 + k)
+    # distinct logits on a 1/64 grid: no two probabilities of a token coincide
+    lg = np.stack([rng.permutation(E) for _ in range(M)]).astype(np.float32) / 64.0 if M else \
+        np.zeros((0, E), np.float32)
+    lg += (rng.standard_normal((M, 1)) * 3).astype(np.float32)
+    r = K.moe_topk(torch.from_numpy(lg).cuda(), k, dense=True)
+    torch.cuda.synchronize()
+    probs = omoe.softmax(lg.astype(np.float64))
+    w_ref, mask_ref, idx_ref = omoe.route_from_probs(probs, k)
+    assert np.array_equal(r.topk_idx.cpu().numpy(), idx_ref.astype(np.int32))
+    assert np.array_equal(r.mask.cpu().numpy(), mask_ref.astype(np.float32))
+    assert np.array_equal(r.count.cpu().numpy(), mask_ref.sum(0).astype(np.int32))
+    if M:
+        check(r.probs.cpu().numpy(), probs, 1e-6, "probs")
+        check(r.weights.cpu().numpy(), w_ref, 1e-6, "weights_dense")
+        check(r.topk_w.cpu().numpy(), np.take_along_axis(w_ref, idx_ref, -1), 1e-6, "topk_w")
+        check(r.probsum.cpu().numpy(), probs.sum(0), 1e-5, "probsum")
+
+
+def test_topk_equal_probabilities_pick_lower_index(K):
+    # every logit equal: the k lowest expert indices, in order, weights 1/k
+    M, E, k = 48, 16, 6
+    r = K.moe_topk(torch.zeros(M, E, device="cuda"), k, dense=True)
+    idx = r.topk_idx.cpu().numpy()
+    assert np.array_equal(idx, np.tile(np.arange(k, dtype=np.int32), (M, 1)))
+    assert np.allclose(r.topk_w.cpu().numpy(), 1.0 / k, rtol=1e-6)
+    # pairs of equal logits: lower index first (oracle tie rule)
+    lg = np.tile(np.array([0, 1, 1, 0, 2, 2, 0, 0, 3, 3, 0, 0, 0, 0, 0, 0], np.float32), (M, 1))
+    r = K.moe_topk(torch.from_numpy(lg).cuda(), 5)
+    assert np.array_equal(r.topk_idx.cpu().numpy(), np.tile(omoe.topk_indices(lg[:1], 5)[0].astype(np.int32), (M, 1)))
+    assert np.array_equal(r.topk_idx.cpu().numpy()[0], np.array([8, 9, 4, 5, 1], np.int32))
+
+
+def test_topk_rejects_bad_k(K):
+    from src.model import _hip
+    with pytest.raises(_hip.WalshHipError):
+        K.moe_topk(torch.zeros(4, 16, device="cuda"), 9)
+    with pytest.raises(_hip.WalshHipError):
+        K.moe_topk(torch.zeros(4, 4, device="cuda"), 5)
+
+
+# ------------------------------------------------------------ scatter
+
+def test_scatter_groups_pairs_by_expert(K):
+    rng = np.random.default_rng(5)
+    M, E, k = 1000, 16, 6
+    lg = rng.standard_normal((M, E)).astype(np.float32)
+    r = K.moe_topk(torch.from_numpy(lg).cuda(), k)
+    lst, off, toff = K.moe_scatter(r)
+    idx = r.topk_idx.cpu().numpy().reshape(-1)
+    lst, off, toff = lst.cpu().numpy(), off.cpu().numpy(), toff.cpu().numpy()
+    cnt = np.bincount(idx, minlength=E)
+    assert np.array_equal(off, np.concatenate([[0], np.cumsum(cnt)]))
+    assert np.array_equal(toff, np.concatenate([[0], np.cumsum((cnt + 15) // 16)]))
+    assert np.array_equal(np.sort(lst), np.arange(M * k))
+    for e in range(E):
+        assert np.all(idx[lst[off[e]:off[e + 1]]] == e)
+
+
+# ------------------------------------------------------------ router + module, float32
+
+@pytest.mark.parametrize("B,T,C,kmax", [(2, 256, 512, 6), (1, 77, 512, 4), (3, 40, 256, 8), (1, 64, 2048, 6)])
+def test_moe_module_fp32_vs_oracle(B, T, C, kmax):
+    m = make_moe(C, max_experts=kmax, seed=C + T)
+    rng = np.random.default_rng(T)
+    x = rng.standard_normal((B, T, C)).astype(np.float32)
+    with torch.no_grad():
+        y = m(torch.from_numpy(x).cuda())
+    assert y.dtype == torch.float32
+    sd = sd_np(m)
+    ref = omoe.moe_forward(x.reshape(-1, C), sd["router.gate.0.weight"], sd["router.gate.2.weight"],
+                           sd["experts.gate_weights"], sd["experts.up_weights"], sd["experts.down_weights"], kmax)
+    E = C // 32
+    k = min(kmax, E)
+    idx = m._route.topk_idx.cpu().numpy()
+    ties = near_ties(ref["probs"], k)
+    same = np.all(np.sort(idx, -1) == np.sort(ref["idx"], -1), axis=-1)
+    print(f"C={C} tokens={B * T} near_ties={int(ties.sum())} routed_differently={int((~same).sum())}")
+    assert np.all(same | ties)
+    assert np.array_equal(idx[same & ~ties], ref["idx"][same & ~ties].astype(np.int32))
+    yv = y.cpu().numpy().reshape(-1, C)
+    check(yv[same], ref["out"][same], TOL[torch.float32], f"MoE out C={C}")
+    # unselected blocks are exactly zero
+    mask = m._last_expert_mask.cpu().numpy().reshape(-1, E)
+    assert np.all(yv.reshape(-1, E, 32)[mask == 0] == 0)
+    assert np.array_equal(mask[same], ref["mask"][same])
+    assert abs(float(m.get_aux_loss()) - ref["aux"]) <= 1e-5 * abs(ref["aux"]) + 1e-7
+
+
+def test_router_forward_dense_outputs():
+    from src.model.moe import HadamardRouter
+    torch.manual_seed(3)
+    r = HadamardRouter(512, n_experts=16, max_experts=6).cuda()
+    x = torch.randn(2, 100, 512)
+    with torch.no_grad():
+        w, mask, probs = r(x.cuda())
+    w1, w2 = r.gate[0].weight.detach().cpu().numpy(), r.gate[2].weight.detach().cpu().numpy()
+    p_ref = omoe.softmax(omoe.router_logits(x.numpy().reshape(-1, 512), w1, w2))
+    w_ref, m_ref, _ = omoe.route_from_probs(p_ref, 6)
+    assert not near_ties(p_ref, 6).any()
+    check(probs.cpu().numpy().reshape(-1, 16), p_ref, 1e-5, "router probs")
+    assert np.array_equal(mask.cpu().numpy().reshape(-1, 16), m_ref)
+    check(w.cpu().numpy().reshape(-1, 16), w_ref, 1e-5, "router weights")
+
+
+@pytest.mark.parametrize("expansion", [2, 4, 8])
+def test_fast_experts_dense_weights(expansion):
+    from src.model.moe import FastMoEExperts
+    torch.manual_seed(expansion)
+    ex = FastMoEExperts(n_experts=16, dim=32, expansion=expansion).cuda()
+    rng = np.random.default_rng(expansion)
+    x = rng.standard_normal((2, 50, 16, 32)).astype(np.float32)
+    w = rng.random((2, 50, 16)).astype(np.float32)
+    w[w < 0.5] = 0.0
+    with torch.no_grad():
+        y = ex(torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda())
+    q = [otern.moe_quantized(p.detach().cpu().numpy()) for p in (ex.gate_weights, ex.up_weights, ex.down_weights)]
+    ref = omoe.experts_forward(x.reshape(-1, 16, 32), q[0][0], q[1][0], q[2][0], q[0][1], q[1][1], q[2][1],
+                               w.reshape(-1, 16))
+    check(y.cpu().numpy().reshape(-1, 16, 32), ref, TOL[torch.float32], f"FastMoEExperts x{expansion}")
+
+
+def test_moe_empty_and_stats():
+    m = make_moe(512, max_experts=6, seed=11)
+    with torch.no_grad():
+        y = m(torch.zeros(1, 0, 512, device="cuda"))
+    assert tuple(y.shape) == (1, 0, 512)
+    m.train()
+    x = torch.randn(2, 64, 512, device="cuda")
+    with torch.no_grad():
+        m(x)
+        m(x)
+    st = m.get_expert_stats()
+    assert abs(st["avg_experts"] - 6.0) < 1e-6
+    assert abs(sum(st["expert_load"]) - 6.0) < 1e-6
+    assert 0.0 <= st["load_balance"] <= 1.0
+    assert m.get_expert_usage() == st
+    m.reset_stats()
+    assert m.get_expert_stats()["avg_experts"] == 0.0
+
+
+# ------------------------------------------------------------ bfloat16 (autocast)
+
+def _bf16(a):
+    return torch.from_numpy(np.asarray(a, np.float32)).bfloat16().float().numpy()
+
+
+@pytest.mark.parametrize("B,T,C", [(2, 512, 512), (1, 100, 256)])
+def test_moe_module_bf16_autocast(B, T, C):
+    m = make_moe(C, max_experts=6, seed=7 + C)
+    rng = np.random.default_rng(C + 1)
+    x = rng.standard_normal((B, T, C)).astype(np.float32)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        y = m(torch.from_numpy(x).cuda())
+    assert y.dtype == torch.float32          # routing weights are float32 under autocast
+    sd = sd_np(m)
+    E = C // 32
+    k = min(6, E)
+    idx = m._route.topk_idx.cpu().numpy()
+    tw = m._route.topk_w.cpu().numpy()
+    # experts on the GPU's own routing, bf16-rounded input, float64 oracle
+    wdense = np.zeros((B * T, E))
+    np.put_along_axis(wdense, idx.astype(np.int64), tw, -1)
+    q = [otern.moe_quantized(sd[f"experts.{n}_weights"]) for n in ("gate", "up", "down")]
+    ref = omoe.experts_forward(_bf16(x).reshape(-1, E, 32), q[0][0], q[1][0], q[2][0], q[0][1], q[1][1],
+                               q[2][1], wdense)
+    check(y.cpu().numpy().reshape(-1, E, 32), ref, TOL[torch.bfloat16], f"MoE bf16 out C={C}")
+    # routing: compare with the float64 oracle; differences only at bf16-level near ties
+    p64 = omoe.softmax(omoe.router_logits(x.reshape(-1, C), sd["router.gate.0.weight"], sd["router.gate.2.weight"]))
+    _, _, idx64 = omoe.route_from_probs(p64, k)
+    same = np.all(np.sort(idx, -1) == np.sort(idx64, -1), axis=-1)
+    ties = near_ties(p64, k, rel_gap=2 ** -6)
+    print(f"bf16 routing: tokens={B * T} differ_from_f64={int((~same).sum())} bf16_near_ties={int(ties.sum())}")
+    assert np.all(same | ties)
+    # the router's probabilities (float32 softmax of bf16 logits) against float64
+    r = m.router.route(torch.from_numpy(x).cuda().bfloat16().reshape(-1, C), dense=True)
+    out_p = r.probs.cpu().numpy()
+    check(out_p, p64, TOL[torch.bfloat16], "bf16 router probs")
+    # mHC callers may ask for the stream dtype directly
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        yb = m(torch.from_numpy(x).cuda(), out_dtype=torch.bfloat16)
+    assert yb.dtype == torch.bfloat16
+    same_route = np.array_equal(m._route.topk_idx.cpu().numpy(), idx)
+    assert same_route
+    check(yb.float().cpu().numpy(), y.cpu().numpy(), 2 ** -7, "bf16 output vs float32 output")
+
+
+# ------------------------------------------------------------ model with MoE on
+
+def test_mhcwalsh_moe_fp32_vs_oracle():
+    from oracle.model import Oracle
+    from src.model import WalshConfig, mHCWalsh
+    torch.manual_seed(0)
+    cfg = WalshConfig(block_size=256, vocab_size=1000, n_layer=2, n_head=32, n_embd=512, algebra="hadamard",
+                      head_mixing=True, use_moe=True, moe_max_experts=4, use_channel_mod=False)
+    model = mHCWalsh(cfg, n_streams=4).cuda().eval()
+    idx = torch.randint(0, 1000, (2, 64))
+    with torch.no_grad():
+        logits, _, h = model(idx.cuda(), return_hidden=True)
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    orc = Oracle(sd, 512, 32, 2, n_streams=4, use_moe=True, moe_max_experts=4)
+    with torch.no_grad():
+        ref_logits, ref_h = orc.forward(idx, return_hidden=True)
+    check(h.cpu().numpy(), ref_h.numpy(), TOL[torch.float32], "mHCWalsh+MoE hidden")
+    check(logits.cpu().numpy(), ref_logits.numpy(), TOL[torch.float32], "mHCWalsh+MoE logits")
+    aux = float(model.get_aux_loss())
+    assert np.isfinite(aux) and aux > 0

@@ -43,6 +43,12 @@ SIGNATURES = {
     "walsh_mhc_pre_norm_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float, _I64, ctypes.c_float,
                                     _P, _P, _P, _P, _I64, _P, ctypes.c_float, _I, _P]),
     "walsh_mhc_post_fwd": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P]),
+    "walsh_moe_route_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
+                                 _P, _I64, _I, _I, _P]),
+    "walsh_moe_topk_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "walsh_moe_scatter": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
+    "walsh_moe_experts_fwd": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                   _I, _I, _P]),
 }
 
 _lib = None

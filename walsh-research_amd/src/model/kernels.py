@@ -342,3 +342,131 @@ def mhc_post(x: torch.Tensor, out: torch.Tensor, h_res: torch.Tensor, h_post: to
               kernel="mhc_post_kernel<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"), nbytes=nbytes,
               flops=flops)
     return x_new
+
+
+# ------------------------------------------------------------------ MoE
+
+def moe_router_fragments(w1: torch.Tensor, w2: torch.Tensor, dtype: torch.dtype):
+    """Router weights W1 [H1, C], W2 [E, H1] in the fragment order of
+    walsh_moe_route_fwd, as ``dtype`` elements: W1 -> [H1/16][C/16][64][4],
+    W2 -> [ceil(E/16)][H1/16][64][4] with rows >= E zero (lane = 16*kq + m)."""
+    H1, C = w1.shape
+    E = w2.shape[0]
+    assert C % 16 == 0 and H1 % 16 == 0, "router needs n_embd % 64 == 0"
+    assert w2.shape[1] == H1, "router W2 shape"
+    f1 = w1.detach().to(dtype).reshape(H1 // 16, 16, C // 16, 4, 4).permute(0, 2, 3, 1, 4).contiguous()
+    ET = (E + 15) // 16
+    w2p = torch.zeros(ET * 16, H1, device=w2.device, dtype=dtype)
+    w2p[:E] = w2.detach().to(dtype)
+    f2 = w2p.reshape(ET, 16, H1 // 16, 4, 4).permute(0, 2, 3, 1, 4).contiguous()
+    return f1, f2
+
+
+def moe_expert_fragments(gate_packed: torch.Tensor, up_packed: torch.Tensor, down_packed: torch.Tensor):
+    """Packed expert codes (pack_ternary_weights layout: gate/up [E, H, 8],
+    down [E, 32, H/4]) -> fragment order of walsh_moe_experts_fwd."""
+    E, H, kb = gate_packed.shape
+    assert kb == 8 and tuple(up_packed.shape) == (E, H, 8), "gate/up packed shape"
+    assert tuple(down_packed.shape) == (E, 32, H // 4) and H % 16 == 0, "down packed shape"
+
+    def gu(p):  # [e][nt][m][c][kq] -> [e][nt][c][kq][m]
+        return p.reshape(E, H // 16, 16, 2, 4).permute(0, 1, 3, 4, 2).contiguous()
+
+    down = down_packed.reshape(E, 2, 16, H // 16, 4).permute(0, 1, 3, 4, 2).contiguous()  # [e][mt][ks][kq][m]
+    return gu(gate_packed), gu(up_packed), down
+
+
+class MoERoute:
+    """Device-side routing of one MoE call: topk_idx [M, k] int32, topk_w
+    [M, k] float32, count / probsum [E], optional dense [M, E] outputs."""
+
+    __slots__ = ("M", "E", "k", "topk_idx", "topk_w", "count", "probsum", "cursor", "probs", "mask", "weights")
+
+    def __init__(self, M, E, k, dev, dense):
+        self.M, self.E, self.k = M, E, k
+        self.topk_idx = torch.empty(M, k, device=dev, dtype=torch.int32)
+        self.topk_w = torch.empty(M, k, device=dev, dtype=torch.float32)
+        ints = torch.empty(2 * E, device=dev, dtype=torch.int32)
+        self.count, self.cursor = ints[:E], ints[E:]
+        self.probsum = torch.empty(E, device=dev, dtype=torch.float32)
+        if dense:
+            d = torch.empty(3, M, E, device=dev, dtype=torch.float32)
+            self.probs, self.mask, self.weights = d[0], d[1], d[2]
+        else:
+            self.probs = self.mask = self.weights = None
+
+
+def moe_route(x: torch.Tensor, w1f: torch.Tensor, w2f: torch.Tensor, H1: int, E: int, k: int, dense: bool = False,
+              y: torch.Tensor = None) -> MoERoute:
+    """Fused router (moe.py:418-447) on x [M, C] (unit inner stride): logits,
+    softmax, top-k, renormalised weights, per-expert counts and probability
+    sums.  If y [M, 32E] is given, the blocks of unselected experts are zeroed."""
+    _hip.require_device(x, "input")
+    dt = x.dtype
+    assert w1f.dtype == dt and w2f.dtype == dt, "router fragments must be in the activation dtype"
+    xv, M, ldx = _rows_view(x, x.shape[-1])
+    C = x.shape[-1]
+    r = MoERoute(M, E, k, x.device, dense)
+    ldy, ydt = 0, dt
+    if y is not None:
+        assert y.shape[-1] == 32 * E and y.stride(-1) == 1, "output layout"
+        ldy, ydt = (y.stride(0) if y.dim() == 2 else 32 * E), y.dtype
+    esz = x.element_size()
+    nbytes = M * C * esz + (H1 * C + E * H1) * esz + M * k * 8
+    if y is not None:
+        nbytes += M * (E - k) * 32 * y.element_size()
+    _hip.call("walsh_moe_route_fwd", xv.data_ptr(), ldx, M, C, H1, w1f.data_ptr(), w2f.data_ptr(), E, k,
+              _hip.ptr(r.probs), _hip.ptr(r.mask), _hip.ptr(r.weights), r.topk_idx.data_ptr(), r.topk_w.data_ptr(),
+              r.count.data_ptr(), r.probsum.data_ptr(), r.cursor.data_ptr(), _hip.ptr(y), ldy, _hip.dtype_code(dt),
+              _hip.dtype_code(ydt), _hip.stream(x.device),
+              kernel="moe_route_kernel<%s>" % ("bf16" if dt == torch.bfloat16 else "f32"), nbytes=nbytes,
+              flops=2 * M * (C * H1 + H1 * E))
+    return r
+
+
+def moe_topk(logits: torch.Tensor, k: int, dense: bool = False) -> MoERoute:
+    """Softmax / top-k / renormalisation (moe.py:432-445) on float32 logits [M, E]."""
+    _hip.require_device(logits, "logits")
+    lg = logits.detach().float().contiguous()
+    M, E = lg.shape
+    r = MoERoute(M, E, k, lg.device, dense)
+    _hip.call("walsh_moe_topk_fwd", lg.data_ptr(), M, E, k, _hip.ptr(r.probs), _hip.ptr(r.mask),
+              _hip.ptr(r.weights), r.topk_idx.data_ptr(), r.topk_w.data_ptr(), r.count.data_ptr(),
+              r.probsum.data_ptr(), r.cursor.data_ptr(), _hip.stream(lg.device), kernel="moe_topk_kernel",
+              nbytes=M * E * 4 + M * k * 8)
+    return r
+
+
+def moe_scatter(r: MoERoute):
+    """Per-expert pair lists: (list [M*k], offset [E+1], tile_off [E+1]) int32."""
+    dev = r.topk_idx.device
+    lst = torch.empty(max(r.M * r.k, 1), device=dev, dtype=torch.int32)
+    offs = torch.empty(2 * (r.E + 1), device=dev, dtype=torch.int32)
+    offset, tile_off = offs[:r.E + 1], offs[r.E + 1:]
+    _hip.call("walsh_moe_scatter", r.topk_idx.data_ptr(), r.M, r.E, r.k, r.count.data_ptr(), r.cursor.data_ptr(),
+              lst.data_ptr(), offset.data_ptr(), tile_off.data_ptr(), _hip.stream(dev), kernel="moe_scatter_kernel",
+              nbytes=r.M * r.k * 8)
+    return lst, offset, tile_off
+
+
+def moe_experts(x: torch.Tensor, y: torch.Tensor, r: MoERoute, lists, frags, gammas: torch.Tensor, H: int):
+    """Routed ternary SwiGLU experts (moe.py:337-380) for the pairs of ``r``:
+    writes y[t, 32e:32e+32] for every selected (t, e).  x [M, 32E] and y
+    [M, 32E] with unit inner stride; frags from moe_expert_fragments."""
+    _hip.require_device(x, "input")
+    E = r.E
+    xv, M, ldx = _rows_view(x, 32 * E)
+    assert M == r.M and y.shape[-1] == 32 * E and y.stride(-1) == 1, "expert input/output layout"
+    ldy = y.stride(0) if y.dim() == 2 else 32 * E
+    lst, offset, tile_off = lists
+    gf, uf, df = frags
+    g = gammas.detach().float().contiguous()
+    esz, ysz = x.element_size(), y.element_size()
+    pairs = M * r.k
+    nbytes = pairs * 32 * (esz + ysz) + pairs * 8 + 3 * E * H * 8
+    tag = "bf16" if x.dtype == torch.bfloat16 else "f32"
+    _hip.call("walsh_moe_experts_fwd", xv.data_ptr(), ldx, y.data_ptr(), ldy, M, E, r.k, H, gf.data_ptr(),
+              uf.data_ptr(), df.data_ptr(), g.data_ptr(), lst.data_ptr(), offset.data_ptr(), tile_off.data_ptr(),
+              r.count.data_ptr(), r.topk_w.data_ptr(), _hip.dtype_code(x.dtype), _hip.dtype_code(y.dtype),
+              _hip.stream(x.device), kernel="moe_experts_kernel<%s>" % tag, nbytes=nbytes,
+              flops=2 * pairs * 3 * 32 * H)

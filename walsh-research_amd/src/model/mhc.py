@@ -206,6 +206,7 @@ class mHCLlamaBlock(nn.Module):
             )
         else:
             self.feed_forward = SwiGLUMLP(config)
+        self._moe = getattr(config, 'use_moe', False)
         self.use_channel_mod = getattr(config, 'use_channel_mod', False)
         if self.use_channel_mod:
             raise NotImplementedError("channel modulation (use_channel_mod) is outside this build's scope")
@@ -219,7 +220,12 @@ class mHCLlamaBlock(nn.Module):
         x = self.attn_stream.forward_normed(
             x, self.attention_norm,
             lambda v: self.attention(v, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx))
-        return self.ffn_stream.forward_normed(x, self.ffn_norm, lambda v: self.feed_forward(v))
+        ff = self.feed_forward
+        if self._moe:
+            # the stream update rounds the FFN output to the stream dtype
+            # (autocast matmul, mhc.py:374-377), so produce it in that dtype
+            return self.ffn_stream.forward_normed(x, self.ffn_norm, lambda v: ff(v, out_dtype=v.dtype))
+        return self.ffn_stream.forward_normed(x, self.ffn_norm, ff)
 
 
 class mHCWalsh(nn.Module):

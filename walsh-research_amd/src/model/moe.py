@@ -1,0 +1,318 @@
+"""Hadamard mixture-of-experts FFN (module surface of src/model/moe.py).
+
+``HadamardMoE`` keeps the reference's constructor, submodules and parameter
+names (``router.gate.{0,2}.weight``, ``experts.{gate,up,down}_weights``) and
+its side state (``_aux_loss``, ``_last_expert_mask``, ``_expert_counts``,
+``_total_tokens``), but runs on four HIP launches instead of a dense einsum
+over all experts (moe.py:363-374):
+
+  1. walsh_moe_route_fwd   router MLP + softmax + top-k + weights + per-expert
+                           counts, zero-filling the blocks of unselected
+                           experts (or, for a large router, torch GEMMs for
+                           the two Linears and walsh_moe_topk_fwd);
+  2. walsh_moe_scatter     per-expert pair lists;
+  3. walsh_moe_experts_fwd ternary SwiGLU on the selected (token, expert)
+                           pairs only, weighted by the routing weight.
+
+Routing semantics are the reference's: top-k with k = min(max_experts, E)
+for every token (moe.py:434-436); ``threshold`` and ``min_experts`` are
+stored and unused, as there.  Equal probabilities select the lower expert
+index first.
+"""
+from typing import Optional, Tuple
+
+import numpy as np
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import kernels
+from ._common import WeightCache, act_dtype
+
+# A fused router keeps W1 in each wavefront's working set; beyond this width
+# the two Linears run as library GEMMs (plain dense products) instead.
+_FUSED_ROUTER_MAX_C = 1024
+_FUSED_ROUTER_MAX_E = 64
+
+
+class TernaryAbsmeanSTE(torch.autograd.Function):
+    """Absmean ternary quantiser of the MoE experts (moe.py:268-294): returns
+    clamp(round(W / gamma), -1, 1) * gamma, gamma = mean(|W|) + 1e-8 over the
+    whole tensor; backward passes the gradient clipped to [-2, 2]."""
+
+    @staticmethod
+    def forward(ctx, w_latent):
+        q = kernels.ternary_quantize(w_latent, packed=False, scaled=True)
+        return q["scaled"].to(w_latent.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        return torch.clamp(grad_output, -2.0, 2.0)
+
+
+def quantize_ternary(w: torch.Tensor) -> torch.Tensor:
+    """W_ternary = clip(round(W / gamma), -1, 1) * gamma (moe.py:297-303)."""
+    return TernaryAbsmeanSTE.apply(w)
+
+
+def _output_dtype(x: torch.Tensor, weights_dtype: torch.dtype = torch.float32) -> torch.dtype:
+    """dtype of ``expert_out * routing_weight`` in the reference: the routing
+    weights come out of a float32 softmax under autocast, so the product is
+    float32 there; without autocast it is the promotion of the two dtypes."""
+    return torch.promote_types(act_dtype(x), weights_dtype)
+
+
+class FastMoEExperts(nn.Module):
+    """Ternary SwiGLU experts on 32-wide blocks (moe.py:306-380).
+
+    gate_weights / up_weights [E, H, dim] and down_weights [E, dim, H]
+    (H = dim * expansion) are float32 latents initialised U(-1, 1) in that
+    order; the forward uses their gamma-scaled ternary codes."""
+
+    def __init__(self, n_experts: int = 8, dim: int = 32, expansion: int = 4, use_ternary: bool = True):
+        super().__init__()
+        self.n_experts = n_experts
+        self.dim = dim
+        self.hidden = dim * expansion
+        self.use_ternary = use_ternary
+        self.gate_weights = nn.Parameter(torch.empty(n_experts, self.hidden, dim))
+        self.up_weights = nn.Parameter(torch.empty(n_experts, self.hidden, dim))
+        self.down_weights = nn.Parameter(torch.empty(n_experts, dim, self.hidden))
+        nn.init.uniform_(self.gate_weights, -1, 1)
+        nn.init.uniform_(self.up_weights, -1, 1)
+        nn.init.uniform_(self.down_weights, -1, 1)
+        self._prep = WeightCache()
+
+    def _check(self):
+        if not self.use_ternary:
+            raise NotImplementedError("FastMoEExperts(use_ternary=False) is outside this build's scope")
+        if self.dim != 32 or self.hidden not in (64, 128, 256):
+            raise NotImplementedError(f"experts need dim 32 and expansion 2, 4 or 8 (dim={self.dim}, "
+                                      f"hidden={self.hidden})")
+
+    def ternary_state(self, dtype: torch.dtype):
+        """(gammas float32 [3], fragments) of the three weight tensors; under
+        bf16 the gammas are rounded to bf16 as autocast rounds code * gamma."""
+        self._check()
+        ws = (self.gate_weights, self.up_weights, self.down_weights)
+
+        def build():
+            qs = [kernels.ternary_quantize(w, packed=True) for w in ws]
+            g = torch.cat([q["gamma"] for q in qs])
+            if dtype == torch.bfloat16:
+                g = g.to(torch.bfloat16).float()
+            return g, kernels.moe_expert_fragments(*(q["packed"] for q in qs))
+
+        return self._prep.get(ws, build, extra=(dtype,))
+
+    def routed(self, x2d: torch.Tensor, route: "kernels.MoERoute", y2d: torch.Tensor) -> None:
+        """Write w * expert_e(x_e) into y2d for every routed (token, e)."""
+        gammas, frags = self.ternary_state(x2d.dtype)
+        lists = kernels.moe_scatter(route)
+        kernels.moe_experts(x2d, y2d, route, lists, frags, gammas, self.hidden)
+
+    def forward(self, x: torch.Tensor, expert_weights: torch.Tensor) -> torch.Tensor:
+        """x [B, T, E, dim], expert_weights [B, T, E] -> [B, T, E, dim]: every
+        expert on its block, times its weight (moe.py:337-380)."""
+        B, T, E, D = x.shape
+        assert E == self.n_experts and D == self.dim, f"expert input shape {tuple(x.shape)}"
+        assert tuple(expert_weights.shape) == (B, T, E), "expert_weights shape"
+        dt = act_dtype(x)
+        M = B * T
+        x2d = x.to(dt).reshape(M, E * D)
+        y = torch.empty(M, E * D, device=x.device, dtype=_output_dtype(x, expert_weights.dtype))
+        if M:
+            # every (token, expert) pair, weighted by the given weights
+            r = kernels.MoERoute(M, E, E, x.device, dense=False)
+            r.topk_idx.copy_(torch.arange(E, device=x.device, dtype=torch.int32).expand(M, E))
+            r.topk_w.copy_(expert_weights.reshape(M, E))
+            r.count.fill_(M)
+            r.cursor.zero_()
+            self.routed(x2d, r, y)
+        return y.view(B, T, E, D)
+
+
+class HadamardRouter(nn.Module):
+    """Router MLP Linear(C, C/4) -> SiLU -> Linear(C/4, E), no biases,
+    weights N(0, 0.01) (moe.py:383-416); forward is moe.py:418-447."""
+
+    def __init__(self, n_embd: int, n_experts: int = 8, threshold: float = 0.1, min_experts: int = 1,
+                 max_experts: int = 4):
+        super().__init__()
+        self.n_experts = n_experts
+        self.threshold = threshold
+        self.min_experts = min_experts
+        self.max_experts = max_experts
+        hidden = n_embd // 4
+        self.gate = nn.Sequential(
+            nn.Linear(n_embd, hidden, bias=False),
+            nn.SiLU(),
+            nn.Linear(hidden, n_experts, bias=False),
+        )
+        for m in self.gate:
+            if isinstance(m, nn.Linear):
+                nn.init.normal_(m.weight, std=0.01)
+        self._frag = WeightCache()
+
+    @property
+    def top_k(self) -> int:
+        return min(self.max_experts, self.n_experts)
+
+    def _fused(self, C: int) -> bool:
+        return C <= _FUSED_ROUTER_MAX_C and self.n_experts <= _FUSED_ROUTER_MAX_E and C % 64 == 0
+
+    def route(self, x2d: torch.Tensor, dense: bool = False, y2d: torch.Tensor = None) -> "kernels.MoERoute":
+        """Routing of x2d [M, C] (activation dtype); see kernels.moe_route."""
+        w1, w2 = self.gate[0].weight, self.gate[2].weight
+        C = x2d.shape[-1]
+        if self._fused(C):
+            f1, f2 = self._frag.get((w1, w2), lambda: kernels.moe_router_fragments(w1, w2, x2d.dtype),
+                                    extra=(x2d.dtype,))
+            return kernels.moe_route(x2d, f1, f2, w1.shape[0], self.n_experts, self.top_k, dense=dense, y=y2d)
+        # wide router: the two Linears are plain GEMMs; routing on the logits
+        w1c, w2c = w1.to(x2d.dtype), w2.to(x2d.dtype)
+        logits = F.linear(F.silu(F.linear(x2d, w1c)), w2c)
+        r = kernels.moe_topk(logits, self.top_k, dense=dense)
+        if y2d is not None:
+            _zero_unselected(y2d, r)
+        return r
+
+    def forward(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """x [B, T, C] -> (expert_weights, expert_mask, router_probs), each
+        [B, T, E] float32."""
+        B, T, C = x.shape
+        dt = act_dtype(x)
+        r = self.route(x.to(dt).reshape(B * T, C), dense=True)
+        E = self.n_experts
+        return r.weights.view(B, T, E), r.mask.view(B, T, E), r.probs.view(B, T, E)
+
+
+def _zero_unselected(y2d: torch.Tensor, r: "kernels.MoERoute") -> None:
+    """Zero the output blocks of unselected experts when the router ran as
+    GEMMs + walsh_moe_topk_fwd (the fused router does this itself)."""
+    keep = torch.zeros(r.M, r.E, device=y2d.device, dtype=torch.bool)
+    keep.scatter_(1, r.topk_idx.long(), True)
+    y2d.view(r.M, r.E, 32).masked_fill_(~keep.unsqueeze(-1), 0)
+
+
+class HadamardMoE(nn.Module):
+    """Sparse FFN over the 32-wide Hadamard blocks (moe.py:450-598)."""
+    BLOCK_DIM = 32
+
+    def __init__(self, config, n_experts: int = None, expansion: int = 4, threshold: float = 0.1,
+                 min_experts: int = 1, max_experts: int = 4, aux_loss_weight: float = 0.01):
+        super().__init__()
+        self.n_embd = config.n_embd
+        if n_experts is None:
+            n_experts = config.n_embd // self.BLOCK_DIM
+        self.n_experts = n_experts
+        self.block_dim = config.n_embd // n_experts
+        self.aux_loss_weight = aux_loss_weight
+        assert config.n_embd % n_experts == 0, \
+            f"n_embd ({config.n_embd}) must be divisible by n_experts ({n_experts})"
+        assert self.block_dim == self.BLOCK_DIM, \
+            f"block_dim ({self.block_dim}) should be {self.BLOCK_DIM} for Hadamard structure"
+        self.router = HadamardRouter(n_embd=config.n_embd, n_experts=n_experts, threshold=threshold,
+                                     min_experts=min_experts, max_experts=max_experts)
+        self.experts = FastMoEExperts(n_experts=n_experts, dim=self.block_dim, expansion=expansion)
+        self.register_buffer('_expert_counts', torch.zeros(n_experts), persistent=False)
+        self.register_buffer('_total_tokens', torch.zeros(1), persistent=False)
+        self._route = None          # routing of the last forward (device tensors)
+        self._route_shape = None
+        self._aux_value = None
+        self._mask_value = None
+
+    # Side state of the last forward, materialised on first access: the
+    # balance loss E * sum_e mean(mask_e) * mean(p_e) (moe.py:544-560) from
+    # the per-expert counts and probability sums, and the dense selection mask.
+    @property
+    def _aux_loss(self):
+        if self._aux_value is None and self._route is not None:
+            r = self._route
+            self._aux_value = (r.count.float() / r.M * (r.probsum / r.M)).sum() * self.n_experts
+        return self._aux_value
+
+    @_aux_loss.setter
+    def _aux_loss(self, v):
+        self._aux_value = v
+
+    @property
+    def _last_expert_mask(self):
+        if self._mask_value is None and self._route is not None:
+            r = self._route
+            m = torch.zeros(r.M, r.E, device=r.topk_idx.device, dtype=torch.float32)
+            m.scatter_(1, r.topk_idx.long(), 1.0)
+            self._mask_value = m.view(*self._route_shape, r.E)
+        return self._mask_value
+
+    @_last_expert_mask.setter
+    def _last_expert_mask(self, v):
+        self._mask_value = v
+
+    def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """x [B, T, C] -> [B, T, C].  The result dtype is the reference's
+        (float32 under autocast, where the routing weights are float32);
+        ``out_dtype`` overrides it for callers that round the result anyway."""
+        B, T, C = x.shape
+        assert C == self.n_embd, f"expected n_embd {self.n_embd}, got {C}"
+        dt = act_dtype(x)
+        M = B * T
+        x2d = x.to(dt).reshape(M, C)
+        ydt = _output_dtype(x) if out_dtype is None else out_dtype
+        if dt == torch.float32:
+            ydt = torch.float32
+        y = torch.empty(M, C, device=x.device, dtype=ydt)
+        r = self.router.route(x2d, y2d=y)
+        self._route, self._route_shape = r, (B, T)
+        self._aux_value = self._mask_value = None
+        if self.training:
+            with torch.no_grad():
+                self._expert_counts += r.count.float()
+                self._total_tokens += M
+        if M:
+            self.experts.routed(x2d, r, y)
+        return y.view(B, T, C)
+
+    def get_aux_loss(self) -> Optional[torch.Tensor]:
+        a = self._aux_loss
+        return a if a is not None else torch.tensor(0.0)
+
+    def get_expert_stats(self) -> dict:
+        """Expert load, mean experts per token and 1 - |Gini| of the load
+        (moe.py:566-589)."""
+        total = self._total_tokens.item()
+        if total == 0:
+            return {'expert_load': [0.0] * self.n_experts, 'avg_experts': 0.0, 'load_balance': 0.0}
+        load = self._expert_counts.cpu().numpy() / total
+        s = np.sort(load)
+        n = len(s)
+        csum = np.cumsum(s)
+        gini = (2 * np.sum(np.arange(1, n + 1) * s) - (n + 1) * csum[-1]) / (n * csum[-1] + 1e-8)
+        return {'expert_load': load.tolist(), 'avg_experts': float(load.sum()),
+                'load_balance': float(1 - abs(gini))}
+
+    def reset_stats(self):
+        self._expert_counts.zero_()
+        self._total_tokens.zero_()
+
+    def get_expert_usage(self) -> dict:
+        return self.get_expert_stats()
+
+
+def should_use_moe(config) -> bool:
+    return getattr(config, 'use_moe', False)
+
+
+def should_use_channel_mod(config) -> bool:
+    return getattr(config, 'use_channel_mod', False)
+
+
+class HadamardChannelModulation(nn.Module):
+    """Channel modulation (moe.py:610-771) is outside this build's scope."""
+
+    def __init__(self, *args, **kwargs):
+        raise NotImplementedError("channel modulation (HadamardChannelModulation) is outside this build's scope")
+
+
+class HadamardChannelModulationBlock(HadamardChannelModulation):
+    pass
