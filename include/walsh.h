@@ -211,10 +211,12 @@ int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out, int64_t ld_o
  *   topk_idx [M, k] int32, experts by decreasing probability (equal
  *     probabilities: lower expert index first);
  *   topk_w [M, k] float32, probs / max(sum of the selected probs, 1e-8);
- *   count [E] int32 = tokens routed to each expert; probsum [E] float32 =
- *     sum over tokens of the softmax probability (for the balance loss);
- *     both are cleared by the call itself;
- *   cursor [E] int32 scratch for walsh_moe_scatter (cleared by the call);
+ *   count [n_part][E] int32 and probsum [n_part][E] float32: per-workgroup
+ *     partial sums of the tokens routed to each expert and of the softmax
+ *     probabilities (for the balance loss); the totals are the sums over
+ *     the first index (walsh_moe_scatter forms them).  Rows a call does not
+ *     use are zeroed; 1 <= n_part <= 65536.  Partial sums replace
+ *     same-address global atomics, which serialise across the chip;
  *   probs / mask / weights_dense [M, E] float32 are optional (NULL skips):
  *     the three outputs of HadamardRouter.forward.
  *
@@ -232,24 +234,27 @@ int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out, int64_t ld_o
  */
 int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_t H1, const void *w1_frag,
                         const void *w2_frag, int64_t E, int64_t k, float *probs, float *mask, float *weights_dense,
-                        int *topk_idx, float *topk_w, int *count, float *probsum, int *cursor, void *y,
+                        int *topk_idx, float *topk_w, int *count, float *probsum, int64_t n_part, void *y,
                         int64_t ldy, int dtype, int ydtype, void *stream);
 
 /* walsh_moe_topk_fwd: the softmax / top-k / renormalisation part of
  *   HadamardRouter.forward (src/model/moe.py:432-445) from given float32
  *   logits [M, E] (contiguous). */
 int walsh_moe_topk_fwd(const float *logits, int64_t M, int64_t E, int64_t k, float *probs, float *mask,
-                       float *weights_dense, int *topk_idx, float *topk_w, int *count, float *probsum, int *cursor,
-                       void *stream);
+                       float *weights_dense, int *topk_idx, float *topk_w, int *count, float *probsum,
+                       int64_t n_part, void *stream);
 
 /* walsh_moe_scatter: per-expert lists of the M*k (token, slot) pairs, the
  *   grouping that replaces the dense all-expert einsum of
- *   FastMoEExperts.forward (src/model/moe.py:363-374).  list [M*k] holds
- *   pair ids t*k + j grouped by expert (order inside a group unspecified);
- *   offset [E+1] = exclusive scan of count; tile_off [E+1] = exclusive scan
- *   of ceil(count/16).  Reads the count and cursor a routing call wrote. */
-int walsh_moe_scatter(const int *topk_idx, int64_t M, int64_t E, int64_t k, const int *count, int *cursor,
-                      int *list, int *offset, int *tile_off, void *stream);
+ *   FastMoEExperts.forward (src/model/moe.py:363-374).  From the partial
+ *   sums of a routing call it forms count [E] and probsum [E] (totals),
+ *   offset [E+1] = exclusive scan of count and tile_off [E+1] = exclusive
+ *   scan of ceil(count/16); list [M*k] then holds the pair ids t*k + j
+ *   grouped by expert (order inside a group unspecified).  cursor [E] is
+ *   scratch. */
+int walsh_moe_scatter(const int *topk_idx, int64_t M, int64_t E, int64_t k, const int *count_part,
+                      const float *probsum_part, int64_t n_part, int *count, float *probsum, int *cursor, int *list,
+                      int *offset, int *tile_off, void *stream);
 
 /* walsh_moe_experts_fwd: FastMoEExperts.forward (src/model/moe.py:337-380)
  *   on the routed pairs only: y[t, 32e:32e+32] = w * down_e(silu(gate_e x_e)
@@ -266,6 +271,25 @@ int walsh_moe_experts_fwd(const void *x, int64_t ldx, void *y, int64_t ldy, int6
                           int64_t H, const uint8_t *gate_frag, const uint8_t *up_frag, const uint8_t *down_frag,
                           const float *gammas, const int *list, const int *offset, const int *tile_off,
                           const int *count, const float *topk_w, int dtype, int ydtype, void *stream);
+
+/* walsh_moe_ffn_fwd: the whole HadamardMoE.forward (src/model/moe.py:512-542)
+ *   in one launch for n_embd 512 (E = 16 experts, router 512 -> 128 -> 16),
+ *   bf16 input: router, routing (outputs as walsh_moe_route_fwd, zeroed
+ *   blocks of unselected experts included) and the routed experts.
+ *   Fragment orders (bf16 elements for the router, 16-bit code pairs for the
+ *   experts; l = lane 0..63, s = slot):
+ *     w1_frag [8][16][64][8]: W1[16a + l%16][32b + 8(l/16) + s];
+ *     w2_frag [8][64][4]: W2[l%16][16c + 4(l/16) + s] (rows >= E zero);
+ *     gate_frag / up_frag [16][64][H/16]: packed bytes 2(l/16) (low) and
+ *       2(l/16) + 1 (high) of row 16a + l%16 (rows of 8 bytes);
+ *     down_frag [16][64][2][H/32]: packed bytes 8c + l/16 (low) and
+ *       8c + 4 + l/16 (high) of row 16m + l%16 (rows of H/4 bytes).
+ *   count [n_part][E] and probsum [n_part][E]: partial sums as above.
+ *   H in {64, 128}, k <= 8, ydtype WALSH_F32 or WALSH_BF16. */
+int walsh_moe_ffn_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, const void *w1_frag, const void *w2_frag,
+                      int64_t E, int64_t k, int64_t H, const uint16_t *gate_frag, const uint16_t *up_frag,
+                      const uint16_t *down_frag, const float *gammas, int *topk_idx, float *topk_w, int *count,
+                      float *probsum, int64_t n_part, void *y, int64_t ldy, int dtype, int ydtype, void *stream);
 
 #ifdef __cplusplus
 }

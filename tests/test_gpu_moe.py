@@ -284,3 +284,44 @@ def test_mhcwalsh_moe_fp32_vs_oracle():
     check(logits.cpu().numpy(), ref_logits.numpy(), TOL[torch.float32], "mHCWalsh+MoE logits")
     aux = float(model.get_aux_loss())
     assert np.isfinite(aux) and aux > 0
+
+
+# ------------------------------------------------------------ single-launch MoE (bf16, n_embd 512)
+
+@pytest.mark.parametrize("M,kmax,expansion,ydt", [(1024, 6, 4, torch.float32), (1000, 6, 4, torch.bfloat16),
+                                                  (77, 1, 4, torch.float32), (300, 8, 2, torch.float32),
+                                                  (129, 4, 2, torch.bfloat16)])
+def test_moe_ffn_single_launch(M, kmax, expansion, ydt):
+    from src.model import kernels
+    m = make_moe(512, max_experts=kmax, expansion=expansion, seed=M + kmax)
+    rng = np.random.default_rng(M)
+    x = rng.standard_normal((1, M, 512)).astype(np.float32)
+    xb = torch.from_numpy(x).cuda().bfloat16()
+    assert kernels.moe_ffn_supported(xb[0], 16, m.experts.hidden, min(kmax, 16))
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        y = m(xb, out_dtype=ydt)
+        r = m._route
+        m.use_fused = False
+        y2 = m(xb, out_dtype=ydt)
+        r2 = m._route
+        m.use_fused = True
+    k = min(kmax, 16)
+    idx, idx2 = r.topk_idx.cpu().numpy(), r2.topk_idx.cpu().numpy()
+    same = np.all(idx == idx2, axis=-1)
+    print(f"single-launch vs three-launch routing: {int((~same).sum())} of {M} tokens differ")
+    assert same.mean() >= 0.98
+    assert np.array_equal(r.count.cpu().numpy(), np.bincount(idx.reshape(-1), minlength=16))
+    sd = sd_np(m)
+    wdense = np.zeros((M, 16))
+    np.put_along_axis(wdense, idx.astype(np.int64), r.topk_w.cpu().numpy(), -1)
+    q = [otern.moe_quantized(sd[f"experts.{n}_weights"]) for n in ("gate", "up", "down")]
+    ref = omoe.experts_forward(_bf16(x[0]).reshape(-1, 16, 32), q[0][0], q[1][0], q[2][0], q[0][1], q[1][1],
+                               q[2][1], wdense)
+    yv = y.float().cpu().numpy().reshape(M, 16, 32)
+    check(yv, ref, TOL[torch.bfloat16], "single-launch MoE vs oracle")
+    check(yv[same], y2.float().cpu().numpy().reshape(M, 16, 32)[same], 2 ** -7, "single vs three launches")
+    # probability sums vs the three-launch router (same bf16 logits up to accumulation order)
+    check(r.probsum.cpu().numpy(), r2.probsum.cpu().numpy(), 1e-3, "probsum")
+    sel = np.zeros((M, 16), bool)
+    np.put_along_axis(sel, idx.astype(np.int64), True, -1)
+    assert np.all(yv[~sel] == 0)

@@ -30,6 +30,7 @@ namespace walsh {
 constexpr int kMoeWaves = 4;
 constexpr int kMoeThreads = 64 * kMoeWaves;
 constexpr int kMaxETiles = 8;      // E <= 128
+constexpr int kMaxE = 16 * kMaxETiles;
 constexpr int kMaxK = 8;           // experts per token
 constexpr int kHChunk = 8;         // router hidden tiles per pass (128 units)
 
@@ -67,19 +68,34 @@ struct RouteOut {
     float *wdense;    // [M, E] or null
     int *topk_idx;    // [M, k]
     float *topk_w;    // [M, k]
-    int *count;       // [E]  (accumulated)
-    float *probsum;   // [E]  (accumulated)
+    int *count;       // [n_part][E] per-workgroup partial sums
+    float *probsum;   // [n_part][E]
+    int n_part;
     void *y;          // [M, ldy] or null: zero the blocks of unselected experts
     int64_t ldy;
     int y_bf16;
 };
 
-// Lane (t, q) of a 16-token tile holds lg[et][j] = logit of expert
-// 16*et + 4q + j of token `tok`.  Softmax, top-k and outputs.
+// Softmax and top-k of one 16-token tile.  Lane (t, q) holds lg[et][j] =
+// logit of expert 16*et + 4q + j of its token; the token's 4 lanes (q = 0..3)
+// cooperate through cross-lane exchanges.  Results: p = probabilities,
+// rank = position of each of the lane's experts in the token's order
+// (largest probability first, lower expert index on ties; >= k when not
+// selected), sel = bit j of sel[et] set when rank[et][j] < k, and den =
+// max(sum of the selected probabilities, 1e-8).
+template <int NET> struct TopK {
+    float p[NET][4];
+    int rank[NET][4];
+    unsigned sel[NET];
+    float den;
+};
+
+// x > y in the routing order (ties: the lower expert index wins; lower_x
+// says whether x's expert index is the lower one).
+__device__ __forceinline__ int beats(float x, float y, bool lower_x) { return (x > y) || (x == y && lower_x); }
+
 template <int NET>
-__device__ __forceinline__ void route_tile(float (&lg)[NET][4], int net, int tok, bool tok_ok, int q,
-                                           const RouteOut &o) {
-    const int E = o.E;
+__device__ __forceinline__ void topk_core(float (&lg)[NET][4], int net, int E, int k, int q, TopK<NET> &r) {
     // softmax (fp32): max, exp, sum over the token's 4 lanes
     float mx = -INFINITY;
 #pragma unroll
@@ -92,71 +108,136 @@ __device__ __forceinline__ void route_tile(float (&lg)[NET][4], int net, int tok
         }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    float p[NET][4];
     float sum = 0.f;
 #pragma unroll
     for (int et = 0; et < NET; ++et)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            p[et][j] = (lg[et][j] == -INFINITY) ? 0.f : expf(lg[et][j] - mx);
-            sum += p[et][j];
+            r.p[et][j] = (lg[et][j] == -INFINITY) ? 0.f : expf(lg[et][j] - mx);
+            sum += r.p[et][j];
         }
     sum += __shfl_xor(sum, 16);
     sum += __shfl_xor(sum, 32);
 #pragma unroll
     for (int et = 0; et < NET; ++et)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[et][j] = __fdiv_rn(p[et][j], sum);
+        for (int j = 0; j < 4; ++j) r.p[et][j] = __fdiv_rn(r.p[et][j], sum);
 
-    // top-k: k rounds of (largest probability, lowest expert index on ties)
-    unsigned sel[NET];  // bit j of sel[et]
+    if constexpr (NET == 1) {
+        // E <= 16: every lane of the token gathers all 16 probabilities and
+        // ranks its own 4 by counting the entries that beat them.
+        float o[4], a1[4], a2[4], a3[4];  // experts 4q+j, 4(q^1)+j, 4(q^2)+j, 4(q^3)+j
 #pragma unroll
-    for (int et = 0; et < NET; ++et) sel[et] = 0;
-    int idx_k[kMaxK];
-    float p_k[kMaxK];
-    float wsum = 0.f;
+        for (int j = 0; j < 4; ++j) o[j] = (4 * q + j < E) ? r.p[0][j] : -1.f;
 #pragma unroll
-    for (int r = 0; r < kMaxK; ++r) {
-        if (r >= o.k) break;
-        float bv = -1.f;
-        int be = 0x7fffffff;
+        for (int j = 0; j < 4; ++j) {
+            a1[j] = __shfl_xor(o[j], 16);
+            a2[j] = __shfl_xor(o[j], 32);
+        }
 #pragma unroll
-        for (int et = 0; et < NET; ++et)
+        for (int j = 0; j < 4; ++j) a3[j] = __shfl_xor(a1[j], 32);
+        const bool l1 = (q ^ 1) < q, l2 = (q ^ 2) < q, l3 = (q ^ 3) < q;
+        float ssum = 0.f;
+        r.sel[0] = 0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int e = 16 * et + 4 * q + j;
-                if (e < E && !((sel[et] >> j) & 1u) && (p[et][j] > bv || (p[et][j] == bv && e < be))) {
-                    bv = p[et][j];
-                    be = e;
+        for (int j = 0; j < 4; ++j) {
+            int rk = 0;
+#pragma unroll
+            for (int j2 = 0; j2 < 4; ++j2) {
+                if (j2 != j) rk += beats(o[j2], o[j], j2 < j);
+                rk += beats(a1[j2], o[j], l1);
+                rk += beats(a2[j2], o[j], l2);
+                rk += beats(a3[j2], o[j], l3);
+            }
+            const bool s = rk < k && 4 * q + j < E;
+            r.rank[0][j] = s ? rk : kMaxE;
+            r.sel[0] |= s ? 1u << j : 0u;
+            ssum += s ? r.p[0][j] : 0.f;
+        }
+        ssum += __shfl_xor(ssum, 16);
+        ssum += __shfl_xor(ssum, 32);
+        r.den = fmaxf(ssum, 1e-8f);
+    } else {
+        // k rounds of (largest probability, lowest expert index on ties)
+#pragma unroll
+        for (int et = 0; et < NET; ++et) {
+            r.sel[et] = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r.rank[et][j] = kMaxE;
+        }
+        float wsum = 0.f;
+#pragma unroll
+        for (int i = 0; i < kMaxK; ++i) {
+            if (i >= k) break;
+            float bv = -1.f;
+            int be = 0x7fffffff;
+#pragma unroll
+            for (int et = 0; et < NET; ++et)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 16 * et + 4 * q + j;
+                    const bool better = e < E && !((r.sel[et] >> j) & 1u) && beats(r.p[et][j], bv, e < be);
+                    bv = better ? r.p[et][j] : bv;
+                    be = better ? e : be;
                 }
+#pragma unroll
+            for (int sh = 16; sh <= 32; sh <<= 1) {
+                const float ov = __shfl_xor(bv, sh);
+                const int oe = __shfl_xor(be, sh);
+                const bool better = beats(ov, bv, oe < be);
+                bv = better ? ov : bv;
+                be = better ? oe : be;
             }
+            // the owner lane marks it
+            const int wet = be >> 4, wq = (be >> 2) & 3, wj = be & 3;
 #pragma unroll
-        for (int sh = 16; sh <= 32; sh <<= 1) {
-            const float ov = __shfl_xor(bv, sh);
-            const int oe = __shfl_xor(be, sh);
-            if (ov > bv || (ov == bv && oe < be)) {
-                bv = ov;
-                be = oe;
+            for (int et = 0; et < NET; ++et)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (et == wet && wq == q && j == wj) {
+                        r.sel[et] |= 1u << j;
+                        r.rank[et][j] = i;
+                    }
+            wsum += bv;
+        }
+        r.den = fmaxf(wsum, 1e-8f);
+    }
+}
+
+// Zero the 32-element output block starting at element `at` of y.
+__device__ __forceinline__ void zero_block(void *y, int bf16, int64_t at) {
+    if (bf16) {
+        uint4 *d = (uint4 *)((uint16_t *)y + at);
+#pragma unroll
+        for (int z = 0; z < 4; ++z) d[z] = uint4{0, 0, 0, 0};
+    } else {
+        uint4 *d = (uint4 *)((float *)y + at);
+#pragma unroll
+        for (int z = 0; z < 8; ++z) d[z] = uint4{0, 0, 0, 0};
+    }
+}
+
+// Outputs of a routed tile (see RouteOut); counts and probability sums go
+// to the workgroup's LDS accumulators cnt_l / ps_l.
+template <int NET>
+__device__ __forceinline__ void route_tile(float (&lg)[NET][4], int net, int tok, bool tok_ok, int q,
+                                           const RouteOut &o, int *cnt_l, float *ps_l) {
+    const int E = o.E;
+    TopK<NET> r;
+    topk_core<NET>(lg, net, E, o.k, q, r);
+    const float den = r.den;
+    float (&p)[NET][4] = r.p;
+    unsigned (&sel)[NET] = r.sel;
+    // each lane writes the top-k entries of its own selected experts
+#pragma unroll
+    for (int et = 0; et < NET; ++et)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (tok_ok && ((sel[et] >> j) & 1u)) {
+                const int64_t at = (int64_t)tok * o.k + r.rank[et][j];
+                o.topk_idx[at] = 16 * et + 4 * q + j;
+                o.topk_w[at] = __fdiv_rn(p[et][j], den);
             }
-        }
-        // the owner lane marks it
-        const int wet = be >> 4, wq = (be >> 2) & 3, wj = be & 3;
-#pragma unroll
-        for (int et = 0; et < NET; ++et)
-            if (et == wet && wq == q) sel[et] |= 1u << wj;
-        idx_k[r] = be;
-        p_k[r] = bv;
-        wsum += bv;
-    }
-    const float den = fmaxf(wsum, 1e-8f);
-    if (tok_ok && q == 0) {
-#pragma unroll
-        for (int r = 0; r < kMaxK; ++r) {
-            if (r >= o.k) break;
-            o.topk_idx[(int64_t)tok * o.k + r] = idx_k[r];
-            o.topk_w[(int64_t)tok * o.k + r] = __fdiv_rn(p_k[r], den);
-        }
-    }
     // dense outputs and zero blocks for the unselected experts of this lane
 #pragma unroll
     for (int et = 0; et < NET; ++et) {
@@ -170,17 +251,7 @@ __device__ __forceinline__ void route_tile(float (&lg)[NET][4], int net, int tok
             if (o.probs) o.probs[pe] = p[et][j];
             if (o.mask) o.mask[pe] = s ? 1.f : 0.f;
             if (o.wdense) o.wdense[pe] = s ? __fdiv_rn(p[et][j], den) : 0.f;
-            if (o.y && !s) {
-                if (o.y_bf16) {
-                    uint4 *d = (uint4 *)((uint16_t *)o.y + tok * o.ldy + 32 * e);
-#pragma unroll
-                    for (int z = 0; z < 4; ++z) d[z] = uint4{0, 0, 0, 0};
-                } else {
-                    uint4 *d = (uint4 *)((float *)o.y + tok * o.ldy + 32 * e);
-#pragma unroll
-                    for (int z = 0; z < 8; ++z) d[z] = uint4{0, 0, 0, 0};
-                }
-            }
+            if (o.y && !s) zero_block(o.y, o.y_bf16, tok * o.ldy + 32 * e);
         }
     }
     // per-expert count and probability sum over the tile's 16 tokens
@@ -198,9 +269,32 @@ __device__ __forceinline__ void route_tile(float (&lg)[NET][4], int net, int tok
             }
             const int e = 16 * et + 4 * q + j;
             if ((threadIdx.x & 15) == 0 && e < E) {
-                if (c > 0.f) atomicAdd(o.count + e, (int)c);
-                atomicAdd(o.probsum + e, ps);
+                if (c > 0.f) atomicAdd(cnt_l + e, (int)c);
+                atomicAdd(ps_l + e, ps);
             }
+        }
+    }
+}
+
+__device__ __forceinline__ void part_init(int *cnt_l, float *ps_l) {
+    for (int e = threadIdx.x; e < kMaxE; e += blockDim.x) {
+        cnt_l[e] = 0;
+        ps_l[e] = 0.f;
+    }
+}
+
+// Store this workgroup's partial sums in row blockIdx.x (and zero the rows
+// no workgroup of this launch owns).  Same-address global atomics from
+// every workgroup would serialise across the chip.
+__device__ __forceinline__ void part_store(const int *cnt_l, const float *ps_l, int *count, float *probsum, int E,
+                                           int n_part) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        count[(int64_t)blockIdx.x * E + e] = cnt_l[e];
+        probsum[(int64_t)blockIdx.x * E + e] = ps_l[e];
+        for (int r = blockIdx.x + gridDim.x; r < n_part; r += gridDim.x) {
+            count[(int64_t)r * E + e] = 0;
+            probsum[(int64_t)r * E + e] = 0.f;
         }
     }
 }
@@ -217,6 +311,10 @@ struct RouterArgs {
 
 template <typename T, bool BF16MMA, int NET>
 __global__ __launch_bounds__(kMoeThreads, 2) void moe_route_kernel(RouterArgs a) {
+    __shared__ int cnt_l[kMaxE];
+    __shared__ float ps_l[kMaxE];
+    part_init(cnt_l, ps_l);
+    __syncthreads();
     constexpr uint32_t esz = sizeof(T);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = lane & 15, q = lane >> 4;
@@ -268,13 +366,18 @@ __global__ __launch_bounds__(kMoeThreads, 2) void moe_route_kernel(RouterArgs a)
         for (int et = 0; et < NET; ++et)
 #pragma unroll
             for (int j = 0; j < 4; ++j) l2[et][j] = BF16MMA ? bf16r(lg[et][j]) : lg[et][j];
-        route_tile(l2, a.net, tok, tok_ok, q, a.o);
+        route_tile(l2, a.net, tok, tok_ok, q, a.o, cnt_l, ps_l);
     }
+    part_store(cnt_l, ps_l, a.o.count, a.o.probsum, a.o.E, a.o.n_part);
 }
 
 template <int NET>
 __global__ __launch_bounds__(kMoeThreads) void moe_topk_kernel(const float *__restrict__ logits, int net,
                                                                RouteOut o) {
+    __shared__ int cnt_l[kMaxE];
+    __shared__ float ps_l[kMaxE];
+    part_init(cnt_l, ps_l);
+    __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = lane & 15, q = lane >> 4;
     const int n_tiles = (int)ceil_div(o.M, 16);
@@ -289,50 +392,81 @@ __global__ __launch_bounds__(kMoeThreads) void moe_topk_kernel(const float *__re
                 const int e = 16 * et + 4 * q + j;
                 lg[et][j] = (tok_ok && et < net && e < o.E) ? logits[(int64_t)tok * o.E + e] : -INFINITY;
             }
-        route_tile(lg, net, tok, tok_ok, q, o);
+        route_tile(lg, net, tok, tok_ok, q, o, cnt_l, ps_l);
     }
+    part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
 }
 
-__global__ void moe_zero_kernel(int *count, float *probsum, int *cursor, int E) {
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+__global__ void moe_zero_kernel(int *count, float *probsum, int n) {
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
         count[e] = 0;
         probsum[e] = 0.f;
-        cursor[e] = 0;
     }
 }
 
 // ------------------------------------------------------------------ scatter
-// Every block scans the E counts itself (E <= 128), then places its pairs:
-// list[offset[e] + atomic cursor[e]] = pair id (t*k + j).  Block 0 also
-// publishes offset[E+1] and tile_off[E+1] (16-pair tiles per expert).
-__global__ __launch_bounds__(256) void moe_scatter_kernel(const int *__restrict__ topk_idx, int64_t n_pairs, int E,
-                                                          const int *__restrict__ count, int *__restrict__ cursor,
-                                                          int *__restrict__ list, int *__restrict__ offset,
-                                                          int *__restrict__ tile_off) {
-    __shared__ int off_s[129];
-    if (threadIdx.x == 0) {
-        int acc = 0, tacc = 0;
-        for (int e = 0; e < E; ++e) {
-            off_s[e] = acc;
-            if (blockIdx.x == 0) {
-                offset[e] = acc;
-                tile_off[e] = tacc;
-            }
-            acc += count[e];
-            tacc += (count[e] + 15) / 16;
+// moe_finalize_kernel (one workgroup): totals of the per-workgroup partial
+// sums, offset = exclusive scan of the counts, tile_off = exclusive scan of
+// ceil(count / 16), cursor cleared.
+__global__ __launch_bounds__(kMaxE) void moe_finalize_kernel(const int *__restrict__ count_part,
+                                                             const float *__restrict__ probsum_part, int n_part, int E,
+                                                             int *__restrict__ count, float *__restrict__ probsum,
+                                                             int *__restrict__ cursor, int *__restrict__ offset,
+                                                             int *__restrict__ tile_off) {
+    __shared__ int c_s[kMaxE];
+    const int e = threadIdx.x;
+    int c = 0;
+    float ps = 0.f;
+    if (e < E) {
+        for (int r = 0; r < n_part; ++r) {
+            c += count_part[(int64_t)r * E + e];
+            ps += probsum_part[(int64_t)r * E + e];
         }
-        off_s[E] = acc;
-        if (blockIdx.x == 0) {
-            offset[E] = acc;
-            tile_off[E] = tacc;
-        }
+        count[e] = c;
+        probsum[e] = ps;
+        cursor[e] = 0;
     }
+    c_s[e] = c;
     __syncthreads();
-    for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < n_pairs; p += (int64_t)gridDim.x * blockDim.x) {
-        const int e = topk_idx[p];
-        const int pos = off_s[e] + atomicAdd(cursor + e, 1);
-        list[pos] = (int)p;
+    if (e == 0) {
+        int acc = 0, tacc = 0;
+        for (int i = 0; i < E; ++i) {
+            offset[i] = acc;
+            tile_off[i] = tacc;
+            acc += c_s[i];
+            tacc += (c_s[i] + 15) / 16;
+        }
+        offset[E] = acc;
+        tile_off[E] = tacc;
     }
+}
+
+// Each workgroup places a contiguous chunk of kScatterPerThread * 256 pairs:
+// ranks inside the chunk come from LDS atomics, and one global atomic per
+// (workgroup, expert) reserves the chunk's range of the expert's list.
+constexpr int kScatterPerThread = 32;
+__global__ __launch_bounds__(256) void moe_scatter_kernel(const int *__restrict__ topk_idx, int64_t n_pairs, int E,
+                                                          const int *__restrict__ offset, int *__restrict__ cursor,
+                                                          int *__restrict__ list) {
+    __shared__ int hist[kMaxE], base[kMaxE];
+    for (int e = threadIdx.x; e < kMaxE; e += 256) hist[e] = 0;
+    __syncthreads();
+    const int64_t p0 = (int64_t)blockIdx.x * 256 * kScatterPerThread;
+    int ex[kScatterPerThread], rk[kScatterPerThread];
+#pragma unroll
+    for (int i = 0; i < kScatterPerThread; ++i) {
+        const int64_t p = p0 + (int64_t)i * 256 + threadIdx.x;
+        const int e = p < n_pairs ? topk_idx[p] : -1;
+        ex[i] = (unsigned)e < (unsigned)E ? e : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kScatterPerThread; ++i) rk[i] = ex[i] >= 0 ? atomicAdd(&hist[ex[i]], 1) : 0;
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += 256) base[e] = hist[e] ? offset[e] + atomicAdd(cursor + e, hist[e]) : 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kScatterPerThread; ++i)
+        if (ex[i] >= 0) list[base[ex[i]] + rk[i]] = (int)(p0 + (int64_t)i * 256 + threadIdx.x);
 }
 
 // ------------------------------------------------------------------ experts
@@ -429,21 +563,305 @@ __global__ __launch_bounds__(kMoeThreads, 2) void moe_experts_kernel(ExpArgs a) 
     }
 }
 
+// ------------------------------------------------------------------ fused FFN
+// The whole HadamardMoE.forward (moe.py:512-542) for n_embd 512 (16 experts,
+// router 512 -> 128 -> 16) in one persistent kernel, bf16 operands on the
+// matrix cores.  A workgroup (8 waves, two per SIMD so that one wave's
+// matrix-core and memory waits overlap the other's VALU work) takes 64
+// tokens at a time:
+//   0. the 64 x 512 input tile is copied to LDS (the only HBM read of x);
+//   1. wave w computes router hidden units 16w..16w+15 for all 64 tokens
+//      (its W1 rows come from L2 in the same batch of loads as the tile),
+//      applies silu and forms its partial logits over those 16 units;
+//   2. waves 0-3 each sum the 8 partial logits of 16 tokens (fixed order)
+//      and route them (softmax, top-k, weights): routing outputs, and a
+//      per-token selection mask and weights in LDS;
+//   3. wave w runs experts w and w+8: it zeroes the expert's output blocks
+//      of the tokens that did not choose it, then a ballot over the 64
+//      tokens' masks and a prefix count compact the tokens that did, which
+//      are processed 16 at a time (gate/up, silu, down) with x read back
+//      from LDS; outputs go straight to y (blocks are disjoint).
+// Per-expert counts and probability sums accumulate in LDS; each workgroup
+// stores its partial sums in its own row (same-address global atomics from
+// every workgroup would serialise across the chip).
+constexpr int kFfnC = 512, kFfnE = 16, kFfnTok = 64, kFfnWaves = 8, kFfnThreads = 64 * kFfnWaves;
+constexpr int kXsStride = kFfnC * 2 + 16;  // bytes per token row of the LDS tile (padded)
+
+// Workgroup barrier ordering LDS only: global stores issued before it (the
+// zeroed output blocks, routing outputs) stay in flight instead of being
+// drained at every phase boundary.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ f32x4 mma32(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mma16bf(uint2 a, uint2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c,
+                                                     0, 0, 0);
+}
+
+// 8 ternary codes (two packed bytes, low byte first) -> 8 bf16.
+__device__ __forceinline__ uint4 decode8(const uint2 *lut, uint32_t u16) {
+    const uint2 lo = lut[u16 & 0xffu], hi = lut[(u16 >> 8) & 0xffu];
+    return uint4{lo.x, lo.y, hi.x, hi.y};
+}
+
+// NH (multiple of 4) consecutive 16-bit code pairs as NH/2 words, 8 bytes
+// per load; code pair i is (w[i / 2] >> (16 * (i % 2))) (decode8 masks).
+template <int NH>
+__device__ __forceinline__ void load_codes(const uint16_t *p, uint32_t (&w)[NH / 2]) {
+#pragma unroll
+    for (int i = 0; i < NH / 4; ++i) {
+        const uint2 v = *(const uint2 *)(p + 4 * i);
+        w[2 * i] = v.x;
+        w[2 * i + 1] = v.y;
+    }
+}
+
+template <int NH>
+__device__ __forceinline__ uint32_t code_pair(const uint32_t (&w)[NH / 2], int i) {
+    return w[i >> 1] >> (16 * (i & 1));
+}
+
+struct FfnArgs {
+    const uint16_t *x;
+    int64_t ldx;
+    int M, k;
+    const uint4 *w1f;         // [8 nt][16 ks][64]: W1[16nt + l%16][32ks + 8(l/16) + s], s < 8
+    const uint2 *w2f;         // [8 c][64]: W2[l%16][16c + 4(l/16) + s], s < 4 (rows >= E zero)
+    const uint16_t *gate_f;   // [16][64][NH]: packed bytes 2(l/16), 2(l/16)+1 of row 16nt + l%16
+    const uint16_t *up_f;     // [16][64][NH]
+    const uint16_t *down_f;   // [16][64][2][NH/2]: bytes 8c + l/16, 8c + 4 + l/16 of row 16mt + l%16
+    const float *gammas;
+    int *topk_idx;
+    float *topk_w;
+    int *count;       // [n_part][16] per-workgroup partial counts
+    float *probsum;   // [n_part][16]
+    int n_part;
+    void *y;
+    int64_t ldy;
+};
+
+template <typename TY, int NH>
+__global__ __launch_bounds__(kFfnThreads, 1) void moe_ffn_kernel(FfnArgs a) {
+    __shared__ __align__(16) uint8_t xs[kFfnTok * kXsStride];
+    __shared__ __align__(16) f32x4 lp[kFfnWaves][kFfnTok][4];  // partial logits [wave][token][q]
+    __shared__ __align__(16) float ws[kFfnTok][kFfnE];         // routing weights (0 = unselected)
+    __shared__ uint32_t sel_s[kFfnTok];                        // bit e: token chose expert e
+    __shared__ int list_s[kFfnWaves][kFfnTok];
+    __shared__ uint2 lut[256];
+    __shared__ int cnt_s[kFfnE];
+    __shared__ float ps_s[kFfnE];
+    static_assert(NH <= 8, "hidden <= 128");
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int t = lane & 15, q = lane >> 4;
+    if (tid < 256) {
+        uint32_t w[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int v0 = (int)((tid >> (6 - 4 * h)) & 3u) - 1, v1 = (int)((tid >> (4 - 4 * h)) & 3u) - 1;
+            const uint32_t b0 = v0 == 0 ? 0u : (v0 > 0 ? 0x3f80u : 0xbf80u);
+            const uint32_t b1 = v1 == 0 ? 0u : (v1 > 0 ? 0x3f80u : 0xbf80u);
+            w[h] = b0 | (b1 << 16);
+        }
+        lut[tid] = uint2{w[0], w[1]};
+    }
+    if (tid < kFfnE) {
+        cnt_s[tid] = 0;
+        ps_s[tid] = 0.f;
+    }
+    const int M = a.M;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)M * a.ldx * 2));
+    // silu(gg g) * (gu u) = gg gu * [g / (1 + exp(-gg g))] * u: the exp
+    // argument carries gg (with log2 e), the down scale carries gg gu gd
+    const float gg = a.gammas[0], gu = a.gammas[1], gd = a.gammas[2];
+    const float kexp = -gg * 1.4426950408889634f, gdown = gd * gg * gu;
+    const int ybf = sizeof(TY) == 2;
+
+    for (int base = blockIdx.x * kFfnTok; base < M; base += gridDim.x * kFfnTok) {
+        lds_barrier();  // the previous tile is no longer read
+        // 0. input tile -> LDS (rows past M read as zeros), with this wave's
+        //    router rows requested in the same batch of loads
+        uint4 w1r[kFfnC / 32];
+        uint2 w2;
+        // this wave's experts (w, w + 8): packed codes, decoded in phase 3
+        uint32_t cg[2][NH / 2], cu[2][NH / 2], cd[2][NH / 2];
+#pragma unroll
+        for (int x2 = 0; x2 < 2; ++x2) {
+            const int64_t off = ((int64_t)(wave + kFfnWaves * x2) * 64 + lane) * NH;
+            load_codes<NH>(a.gate_f + off, cg[x2]);
+            load_codes<NH>(a.up_f + off, cu[x2]);
+            load_codes<NH>(a.down_f + off, cd[x2]);
+        }
+        {
+            uint4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int r = 8 * i + wave, c = lane;
+                const uint32_t off = base + r < M ? (uint32_t)(((int64_t)(base + r) * a.ldx + 8 * c) * 2) : kOOB;
+                v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            }
+#pragma unroll
+            for (int ks = 0; ks < kFfnC / 32; ++ks) w1r[ks] = a.w1f[(wave * 16 + ks) * 64 + lane];
+            w2 = a.w2f[wave * 64 + lane];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) *(uint4 *)(xs + (8 * i + wave) * kXsStride + 16 * lane) = v[i];
+        }
+        lds_barrier();
+        // 1. router hidden units 16w..16w+15 for the 64 tokens, then partial logits
+        {
+            f32x4 acc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < kFfnC / 32; ++ks) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint4 b = *(const uint4 *)(xs + (16 * i + t) * kXsStride + (32 * ks + 8 * q) * 2);
+                    acc[i] = mma32(w1r[ks], b, acc[i]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float h[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) h[j] = silu_f(bf16r(acc[i][j]));
+                const uint2 hb{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+                lp[wave][16 * i + t][q] = mma16bf(w2, hb, f32x4{0.f, 0.f, 0.f, 0.f});
+            }
+        }
+        lds_barrier();
+        // 2. routing of tokens 16w..16w+15 (waves 0-3)
+        if (wave < 4) {
+            const int tl = 16 * wave + t, tok = base + tl;
+            const bool tok_ok = tok < M;
+            f32x4 sl = lp[0][tl][q];
+#pragma unroll
+            for (int w = 1; w < kFfnWaves; ++w) sl += lp[w][tl][q];
+            float lg[1][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) lg[0][j] = bf16r(sl[j]);
+            TopK<1> r;
+            topk_core<1>(lg, 1, kFfnE, a.k, q, r);
+            f32x4 wv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool sj = tok_ok && ((r.sel[0] >> j) & 1u);
+                wv[j] = sj ? __fdiv_rn(r.p[0][j], r.den) : 0.f;
+                if (sj) {
+                    const int64_t at = (int64_t)tok * a.k + r.rank[0][j];
+                    a.topk_idx[at] = 4 * q + j;
+                    a.topk_w[at] = wv[j];
+                }
+                if (sj) atomicAdd(&cnt_s[4 * q + j], 1);
+                if (tok_ok) atomicAdd(&ps_s[4 * q + j], r.p[0][j]);
+            }
+            *(f32x4 *)&ws[tl][4 * q] = wv;
+            uint32_t m = tok_ok ? (r.sel[0] & 15u) << (4 * q) : 0u;
+            m |= __shfl_xor(m, 16);
+            m |= __shfl_xor(m, 32);
+            if (q == 0) sel_s[tl] = m;
+        }
+        lds_barrier();
+        // 3. experts w and w + 8 on the tokens that chose them
+#pragma unroll
+        for (int x2 = 0; x2 < 2; ++x2) {
+            const int e = wave + kFfnWaves * x2;
+            const uint32_t tsel = sel_s[lane];
+            const bool mine = (tsel >> e) & 1u;
+            // zero blocks of the tile's tokens that did not choose e (their
+            // stores overlap this wave's expert arithmetic)
+            if (!mine && base + lane < M) zero_block(a.y, ybf, (int64_t)(base + lane) * a.ldy + 32 * e);
+            const uint64_t bal = __ballot(mine);
+            const int n = __popcll(bal);
+            if (mine) {
+                const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                list_s[wave][rank] = lane;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (n == 0) continue;
+            // the expert's weights as bf16 operands, decoded once for all its groups
+            uint4 ag[NH], au[NH], ad[NH];
+#pragma unroll
+            for (int i = 0; i < NH; ++i) {
+                ag[i] = decode8(lut, code_pair<NH>(cg[x2], i));
+                au[i] = decode8(lut, code_pair<NH>(cu[x2], i));
+                ad[i] = decode8(lut, code_pair<NH>(cd[x2], i));
+            }
+            for (int g = 0; g < n; g += 16) {
+                const bool ok = g + t < n;
+                const int tl = ok ? list_s[wave][g + t] : 0;
+                const uint4 xb = ok ? *(const uint4 *)(xs + tl * kXsStride + (32 * e + 8 * q) * 2) : uint4{0, 0, 0, 0};
+                const float wr = ok ? ws[tl][e] : 0.f;
+                uint4 hb[NH / 2];
+#pragma unroll
+                for (int c = 0; c < NH / 2; ++c) {
+                    float hv[2][4];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const f32x4 z{0.f, 0.f, 0.f, 0.f};
+                        const f32x4 gv = mma32(ag[2 * c + h], xb, z);
+                        const f32x4 uv = mma32(au[2 * c + h], xb, z);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            hv[h][j] = gv[j] * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(kexp * gv[j])) * uv[j];
+                    }
+                    hb[c] = uint4{pack_bf16x2(hv[0][0], hv[0][1]), pack_bf16x2(hv[0][2], hv[0][3]),
+                                  pack_bf16x2(hv[1][0], hv[1][1]), pack_bf16x2(hv[1][2], hv[1][3])};
+                }
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    f32x4 d{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int c = 0; c < NH / 2; ++c) d = mma32(ad[mt * (NH / 2) + c], hb[c], d);
+                    if (ok) {
+                        f32x4 o;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) o[j] = bf16r(gdown * d[j]) * wr;
+                        const int64_t at = (int64_t)(base + tl) * a.ldy + 32 * e + 16 * mt + 4 * q;
+                        store4((TY *)a.y + at, o);
+                    }
+                }
+            }
+        }
+    }
+    lds_barrier();
+    if (tid < kFfnE) {
+        a.count[blockIdx.x * kFfnE + tid] = cnt_s[tid];
+        a.probsum[blockIdx.x * kFfnE + tid] = ps_s[tid];
+        for (int r = blockIdx.x + gridDim.x; r < a.n_part; r += gridDim.x) {
+            a.count[r * kFfnE + tid] = 0;
+            a.probsum[r * kFfnE + tid] = 0.f;
+        }
+    }
+}
+
 }  // namespace walsh
 
 using namespace walsh;
 
-static int grid_cap(int64_t waves_needed) {
+static int grid_cap(int64_t waves_needed, int64_t limit = 0) {
     int64_t g = ceil_div(waves_needed, kMoeWaves);
     const int64_t cap = (int64_t)device_info().cu_count * 4;
     if (g > cap) g = cap;
+    if (limit > 0 && g > limit) g = limit;
     return (int)(g < 1 ? 1 : g);
 }
 
 static int route_out_check(const char *fn, int64_t M, int64_t E, int64_t k, const int *topk_idx, const float *topk_w,
-                           const int *count, const float *probsum) {
+                           const int *count, const float *probsum, int64_t n_part) {
     if (!count || !probsum || (M > 0 && (!topk_idx || !topk_w)))
         return set_error(WALSH_EINVAL, "%s: null output pointer", fn);
+    if (n_part < 1 || n_part > 65536) return set_error(WALSH_EINVAL, "%s: n_part must be in [1, 65536]", fn);
     if (M < 0 || E < 1 || E > 16 * kMaxETiles || k < 1 || k > kMaxK || k > E)
         return set_error(WALSH_ENOTSUP, "%s: needs 1 <= k <= min(E, %d) and E <= %d (M=%lld E=%lld k=%lld)", fn, kMaxK,
                          16 * kMaxETiles, (long long)M, (long long)E, (long long)k);
@@ -453,11 +871,11 @@ static int route_out_check(const char *fn, int64_t M, int64_t E, int64_t k, cons
 WALSH_EXPORT int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_t H1, const void *w1_frag,
                                      const void *w2_frag, int64_t E, int64_t k, float *probs, float *mask,
                                      float *weights_dense, int *topk_idx, float *topk_w, int *count, float *probsum,
-                                     int *cursor, void *y, int64_t ldy, int dtype, int ydtype, void *stream) {
+                                     int64_t n_part, void *y, int64_t ldy, int dtype, int ydtype, void *stream) {
     const char *fn = "walsh_moe_route_fwd";
-    int rc = route_out_check(fn, M, E, k, topk_idx, topk_w, count, probsum);
+    int rc = route_out_check(fn, M, E, k, topk_idx, topk_w, count, probsum, n_part);
     if (rc) return rc;
-    if ((M > 0 && !x) || !w1_frag || !w2_frag || !cursor) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if ((M > 0 && !x) || !w1_frag || !w2_frag) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
     if (C % 16 || H1 % 16 || C < 16 || H1 < 16 || ldx < C || (y && ldy < 32 * E))
         return set_error(WALSH_ENOTSUP, "%s: needs C %% 16 == 0 and H1 %% 16 == 0 (C=%lld H1=%lld)", fn, (long long)C,
                          (long long)H1);
@@ -469,8 +887,10 @@ WALSH_EXPORT int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int6
         return set_error(WALSH_ENOTSUP, "%s: x and y rows must be 16-byte aligned", fn);
     if (M * ldx * esz > (int64_t)kMaxBufferBytes) return set_error(WALSH_ENOTSUP, "%s: input too large", fn);
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(moe_zero_kernel, dim3(1), dim3(128), 0, s, count, probsum, cursor, (int)E);
-    if (M == 0) return check_hip(hipGetLastError(), fn);
+    if (M == 0) {
+        hipLaunchKernelGGL(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
+        return check_hip(hipGetLastError(), fn);
+    }
     RouterArgs a;
     a.x = x;
     a.ldx = ldx;
@@ -479,9 +899,9 @@ WALSH_EXPORT int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int6
     a.w1f = w1_frag;
     a.w2f = w2_frag;
     a.net = (int)ceil_div(E, 16);
-    a.o = RouteOut{(int)M, (int)E, (int)k, probs, mask, weights_dense, topk_idx, topk_w, count, probsum, y, ldy,
-                   ydtype == WALSH_BF16};
-    const dim3 G(grid_cap(ceil_div(M, 16))), B(kMoeThreads);
+    a.o = RouteOut{(int)M,   (int)E,  (int)k,   probs, mask, weights_dense,        topk_idx,
+                   topk_w,   count,   probsum,  (int)n_part, y, ldy, ydtype == WALSH_BF16};
+    const dim3 G(grid_cap(ceil_div(M, 16), n_part)), B(kMoeThreads);
 #define WALSH_ROUTE(NE)                                                                               \
     if (dtype == WALSH_BF16) hipLaunchKernelGGL((moe_route_kernel<uint16_t, true, NE>), G, B, 0, s, a); \
     else hipLaunchKernelGGL((moe_route_kernel<float, false, NE>), G, B, 0, s, a);
@@ -492,17 +912,20 @@ WALSH_EXPORT int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int6
 
 WALSH_EXPORT int walsh_moe_topk_fwd(const float *logits, int64_t M, int64_t E, int64_t k, float *probs, float *mask,
                                     float *weights_dense, int *topk_idx, float *topk_w, int *count, float *probsum,
-                                    int *cursor, void *stream) {
+                                    int64_t n_part, void *stream) {
     const char *fn = "walsh_moe_topk_fwd";
-    int rc = route_out_check(fn, M, E, k, topk_idx, topk_w, count, probsum);
+    int rc = route_out_check(fn, M, E, k, topk_idx, topk_w, count, probsum, n_part);
     if (rc) return rc;
-    if ((M > 0 && !logits) || !cursor) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (M > 0 && !logits) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(moe_zero_kernel, dim3(1), dim3(128), 0, s, count, probsum, cursor, (int)E);
-    if (M == 0) return check_hip(hipGetLastError(), fn);
-    RouteOut o{(int)M, (int)E, (int)k, probs, mask, weights_dense, topk_idx, topk_w, count, probsum, nullptr, 0, 0};
+    if (M == 0) {
+        hipLaunchKernelGGL(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
+        return check_hip(hipGetLastError(), fn);
+    }
+    RouteOut o{(int)M, (int)E, (int)k, probs, mask, weights_dense, topk_idx, topk_w, count, probsum, (int)n_part,
+               nullptr, 0, 0};
     const int net = (int)ceil_div(E, 16);
-    const dim3 G(grid_cap(ceil_div(M, 16))), B(kMoeThreads);
+    const dim3 G(grid_cap(ceil_div(M, 16), n_part)), B(kMoeThreads);
     if (net <= 1) hipLaunchKernelGGL(moe_topk_kernel<1>, G, B, 0, s, logits, net, o);
     else if (net <= 2) hipLaunchKernelGGL(moe_topk_kernel<2>, G, B, 0, s, logits, net, o);
     else if (net <= 4) hipLaunchKernelGGL(moe_topk_kernel<4>, G, B, 0, s, logits, net, o);
@@ -510,18 +933,26 @@ WALSH_EXPORT int walsh_moe_topk_fwd(const float *logits, int64_t M, int64_t E, i
     return check_hip(hipGetLastError(), fn);
 }
 
-WALSH_EXPORT int walsh_moe_scatter(const int *topk_idx, int64_t M, int64_t E, int64_t k, const int *count, int *cursor,
+WALSH_EXPORT int walsh_moe_scatter(const int *topk_idx, int64_t M, int64_t E, int64_t k, const int *count_part,
+                                   const float *probsum_part, int64_t n_part, int *count, float *probsum, int *cursor,
                                    int *list, int *offset, int *tile_off, void *stream) {
-    if ((M > 0 && (!topk_idx || !list)) || !count || !cursor || !offset || !tile_off)
-        return set_error(WALSH_EINVAL, "walsh_moe_scatter: null pointer");
-    if (M < 0 || E < 1 || E > 128 || k < 1) return set_error(WALSH_EINVAL, "walsh_moe_scatter: bad shape");
+    const char *fn = "walsh_moe_scatter";
+    if ((M > 0 && (!topk_idx || !list)) || !count_part || !probsum_part || !count || !probsum || !cursor ||
+        !offset || !tile_off)
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (M < 0 || E < 1 || E > kMaxE || k < 1 || n_part < 1 || n_part > 65536)
+        return set_error(WALSH_EINVAL, "%s: bad shape (M=%lld E=%lld k=%lld n_part=%lld)", fn, (long long)M,
+                         (long long)E, (long long)k, (long long)n_part);
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(moe_finalize_kernel, dim3(1), dim3(kMaxE), 0, s, count_part, probsum_part, (int)n_part,
+                       (int)E, count, probsum, cursor, offset, tile_off);
     const int64_t n_pairs = M * k;
-    int64_t grid = ceil_div(n_pairs, 256);
-    if (grid > (int64_t)device_info().cu_count * 4) grid = (int64_t)device_info().cu_count * 4;
-    if (grid < 1) grid = 1;
-    hipLaunchKernelGGL(moe_scatter_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, topk_idx, n_pairs,
-                       (int)E, count, cursor, list, offset, tile_off);
-    return check_hip(hipGetLastError(), "walsh_moe_scatter launch");
+    if (n_pairs > 0) {
+        const int64_t grid = ceil_div(n_pairs, 256 * kScatterPerThread);
+        hipLaunchKernelGGL(moe_scatter_kernel, dim3((unsigned)grid), dim3(256), 0, s, topk_idx, n_pairs, (int)E,
+                           offset, cursor, list);
+    }
+    return check_hip(hipGetLastError(), fn);
 }
 
 WALSH_EXPORT int walsh_moe_experts_fwd(const void *x, int64_t ldx, void *y, int64_t ldy, int64_t M, int64_t E,
@@ -572,5 +1003,58 @@ WALSH_EXPORT int walsh_moe_experts_fwd(const void *x, int64_t ldx, void *y, int6
     else hipLaunchKernelGGL((moe_experts_kernel<uint16_t, float, true, NH>), G, B, 0, s, a);
     if (H == 64) { WALSH_EXP_LAUNCH(4) } else if (H == 128) { WALSH_EXP_LAUNCH(8) } else { WALSH_EXP_LAUNCH(16) }
 #undef WALSH_EXP_LAUNCH
+    return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int walsh_moe_ffn_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, const void *w1_frag,
+                                   const void *w2_frag, int64_t E, int64_t k, int64_t H, const uint16_t *gate_frag,
+                                   const uint16_t *up_frag, const uint16_t *down_frag, const float *gammas,
+                                   int *topk_idx, float *topk_w, int *count, float *probsum, int64_t n_part,
+                                   void *y, int64_t ldy, int dtype, int ydtype, void *stream) {
+    const char *fn = "walsh_moe_ffn_fwd";
+    if (!w1_frag || !w2_frag || !gate_frag || !up_frag || !down_frag || !gammas || !count || !probsum ||
+        (M > 0 && (!x || !y || !topk_idx || !topk_w)))
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (C != kFfnC || E != kFfnE || dtype != WALSH_BF16 || (H != 64 && H != 128) || k < 1 || k > kMaxK || M < 0 ||
+        (ydtype != WALSH_F32 && ydtype != WALSH_BF16))
+        return set_error(WALSH_ENOTSUP, "%s: needs bf16 input, n_embd 512 (16 experts), hidden 64/128, k <= 8", fn);
+    const int64_t ysz = ydtype == WALSH_BF16 ? 2 : 4;
+    if (ldx < C || ldy < C || ldx % 8 || ldy % (16 / ysz) || (uintptr_t)x % 16 || (uintptr_t)y % 16)
+        return set_error(WALSH_ENOTSUP, "%s: x and y rows must be 16-byte aligned", fn);
+    if (M * ldx * 2 > (int64_t)kMaxBufferBytes) return set_error(WALSH_ENOTSUP, "%s: input too large", fn);
+    if (n_part < 1 || n_part > 65536) return set_error(WALSH_EINVAL, "%s: n_part must be in [1, 65536]", fn);
+    hipStream_t s = (hipStream_t)stream;
+    if (M == 0) {
+        hipLaunchKernelGGL(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
+        return check_hip(hipGetLastError(), fn);
+    }
+    FfnArgs a;
+    a.x = (const uint16_t *)x;
+    a.ldx = ldx;
+    a.M = (int)M;
+    a.k = (int)k;
+    a.w1f = (const uint4 *)w1_frag;
+    a.w2f = (const uint2 *)w2_frag;
+    a.gate_f = gate_frag;
+    a.up_f = up_frag;
+    a.down_f = down_frag;
+    a.gammas = gammas;
+    a.topk_idx = topk_idx;
+    a.topk_w = topk_w;
+    a.count = count;
+    a.probsum = probsum;
+    a.n_part = (int)n_part;
+    a.y = y;
+    a.ldy = ldy;
+    int64_t g = ceil_div(M, kFfnTok);
+    const int64_t cap = device_info().cu_count;
+    if (g > cap) g = cap;
+    if (g > n_part) g = n_part;
+    const dim3 G((unsigned)g), B(kFfnThreads);
+#define WALSH_FFN(NHV)                                                                 \
+    if (ydtype == WALSH_F32) hipLaunchKernelGGL((moe_ffn_kernel<float, NHV>), G, B, 0, s, a); \
+    else hipLaunchKernelGGL((moe_ffn_kernel<uint16_t, NHV>), G, B, 0, s, a);
+    if (H == 64) { WALSH_FFN(4) } else { WALSH_FFN(8) }
+#undef WALSH_FFN
     return check_hip(hipGetLastError(), fn);
 }

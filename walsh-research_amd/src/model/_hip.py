@@ -43,12 +43,14 @@ SIGNATURES = {
     "walsh_mhc_pre_norm_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float, _I64, ctypes.c_float,
                                     _P, _P, _P, _P, _I64, _P, ctypes.c_float, _I, _P]),
     "walsh_mhc_post_fwd": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P]),
-    "walsh_moe_route_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
+    "walsh_moe_route_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64,
                                  _P, _I64, _I, _I, _P]),
-    "walsh_moe_topk_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
-    "walsh_moe_scatter": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
+    "walsh_moe_topk_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),
+    "walsh_moe_scatter": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P]),
     "walsh_moe_experts_fwd": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _I, _I, _P]),
+    "walsh_moe_ffn_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                               _P, _I64, _I, _I, _P]),
 }
 
 _lib = None
@@ -144,6 +146,17 @@ def dtype_code(dt: torch.dtype) -> int:
     if dt == torch.bfloat16:
         return WALSH_BF16
     raise TypeError(f"activation dtype {dt} is not supported (float32 or bfloat16)")
+
+
+_cu = {}
+
+
+def cu_count(device) -> int:
+    """Compute units of ``device`` (cached)."""
+    i = torch.device(device).index or 0
+    if i not in _cu:
+        _cu[i] = torch.cuda.get_device_properties(i).multi_processor_count
+    return _cu[i]
 
 
 def ptr(t) -> int:

@@ -378,22 +378,47 @@ def moe_expert_fragments(gate_packed: torch.Tensor, up_packed: torch.Tensor, dow
 
 class MoERoute:
     """Device-side routing of one MoE call: topk_idx [M, k] int32, topk_w
-    [M, k] float32, count / probsum [E], optional dense [M, E] outputs."""
+    [M, k] float32, optional dense [M, E] outputs, and the per-expert token
+    counts / probability sums, written by the kernels as [parts, E]
+    per-workgroup partial sums.  ``count`` / ``probsum`` are the totals:
+    set by moe_scatter, or summed from the partials on first access."""
 
-    __slots__ = ("M", "E", "k", "topk_idx", "topk_w", "count", "probsum", "cursor", "probs", "mask", "weights")
+    __slots__ = ("M", "E", "k", "topk_idx", "topk_w", "count_part", "probsum_part", "_count", "_probsum", "probs",
+                 "mask", "weights")
 
-    def __init__(self, M, E, k, dev, dense):
+    def __init__(self, M, E, k, dev, dense, parts):
         self.M, self.E, self.k = M, E, k
         self.topk_idx = torch.empty(M, k, device=dev, dtype=torch.int32)
         self.topk_w = torch.empty(M, k, device=dev, dtype=torch.float32)
-        ints = torch.empty(2 * E, device=dev, dtype=torch.int32)
-        self.count, self.cursor = ints[:E], ints[E:]
-        self.probsum = torch.empty(E, device=dev, dtype=torch.float32)
+        self.count_part = torch.empty(parts, E, device=dev, dtype=torch.int32)
+        self.probsum_part = torch.empty(parts, E, device=dev, dtype=torch.float32)
+        self._count = self._probsum = None
         if dense:
             d = torch.empty(3, M, E, device=dev, dtype=torch.float32)
             self.probs, self.mask, self.weights = d[0], d[1], d[2]
         else:
             self.probs = self.mask = self.weights = None
+
+    @property
+    def parts(self) -> int:
+        return self.count_part.shape[0]
+
+    @property
+    def count(self):
+        if self._count is None:
+            self._count = self.count_part.sum(0, dtype=torch.int32)
+        return self._count
+
+    @property
+    def probsum(self):
+        if self._probsum is None:
+            self._probsum = self.probsum_part.sum(0)
+        return self._probsum
+
+
+def _parts(M: int, per: int, dev) -> int:
+    """Partial-sum rows of a routing launch: one per workgroup."""
+    return max(1, min((M + per - 1) // per, 4 * _hip.cu_count(dev)))
 
 
 def moe_route(x: torch.Tensor, w1f: torch.Tensor, w2f: torch.Tensor, H1: int, E: int, k: int, dense: bool = False,
@@ -406,7 +431,7 @@ def moe_route(x: torch.Tensor, w1f: torch.Tensor, w2f: torch.Tensor, H1: int, E:
     assert w1f.dtype == dt and w2f.dtype == dt, "router fragments must be in the activation dtype"
     xv, M, ldx = _rows_view(x, x.shape[-1])
     C = x.shape[-1]
-    r = MoERoute(M, E, k, x.device, dense)
+    r = MoERoute(M, E, k, x.device, dense, _parts(M, 64, x.device))
     ldy, ydt = 0, dt
     if y is not None:
         assert y.shape[-1] == 32 * E and y.stride(-1) == 1, "output layout"
@@ -417,7 +442,7 @@ def moe_route(x: torch.Tensor, w1f: torch.Tensor, w2f: torch.Tensor, H1: int, E:
         nbytes += M * (E - k) * 32 * y.element_size()
     _hip.call("walsh_moe_route_fwd", xv.data_ptr(), ldx, M, C, H1, w1f.data_ptr(), w2f.data_ptr(), E, k,
               _hip.ptr(r.probs), _hip.ptr(r.mask), _hip.ptr(r.weights), r.topk_idx.data_ptr(), r.topk_w.data_ptr(),
-              r.count.data_ptr(), r.probsum.data_ptr(), r.cursor.data_ptr(), _hip.ptr(y), ldy, _hip.dtype_code(dt),
+              r.count_part.data_ptr(), r.probsum_part.data_ptr(), r.parts, _hip.ptr(y), ldy, _hip.dtype_code(dt),
               _hip.dtype_code(ydt), _hip.stream(x.device),
               kernel="moe_route_kernel<%s>" % ("bf16" if dt == torch.bfloat16 else "f32"), nbytes=nbytes,
               flops=2 * M * (C * H1 + H1 * E))
@@ -429,23 +454,28 @@ def moe_topk(logits: torch.Tensor, k: int, dense: bool = False) -> MoERoute:
     _hip.require_device(logits, "logits")
     lg = logits.detach().float().contiguous()
     M, E = lg.shape
-    r = MoERoute(M, E, k, lg.device, dense)
+    r = MoERoute(M, E, k, lg.device, dense, _parts(M, 64, lg.device))
     _hip.call("walsh_moe_topk_fwd", lg.data_ptr(), M, E, k, _hip.ptr(r.probs), _hip.ptr(r.mask),
-              _hip.ptr(r.weights), r.topk_idx.data_ptr(), r.topk_w.data_ptr(), r.count.data_ptr(),
-              r.probsum.data_ptr(), r.cursor.data_ptr(), _hip.stream(lg.device), kernel="moe_topk_kernel",
+              _hip.ptr(r.weights), r.topk_idx.data_ptr(), r.topk_w.data_ptr(), r.count_part.data_ptr(),
+              r.probsum_part.data_ptr(), r.parts, _hip.stream(lg.device), kernel="moe_topk_kernel",
               nbytes=M * E * 4 + M * k * 8)
     return r
 
 
 def moe_scatter(r: MoERoute):
-    """Per-expert pair lists: (list [M*k], offset [E+1], tile_off [E+1]) int32."""
+    """Per-expert pair lists: (list [M*k], offset [E+1], tile_off [E+1]) int32;
+    also sets the totals r.count / r.probsum."""
     dev = r.topk_idx.device
+    E = r.E
     lst = torch.empty(max(r.M * r.k, 1), device=dev, dtype=torch.int32)
-    offs = torch.empty(2 * (r.E + 1), device=dev, dtype=torch.int32)
-    offset, tile_off = offs[:r.E + 1], offs[r.E + 1:]
-    _hip.call("walsh_moe_scatter", r.topk_idx.data_ptr(), r.M, r.E, r.k, r.count.data_ptr(), r.cursor.data_ptr(),
+    ints = torch.empty(4 * E + 2, device=dev, dtype=torch.int32)
+    count, cursor, offset, tile_off = ints[:E], ints[E:2 * E], ints[2 * E:3 * E + 1], ints[3 * E + 1:]
+    probsum = torch.empty(E, device=dev, dtype=torch.float32)
+    _hip.call("walsh_moe_scatter", r.topk_idx.data_ptr(), r.M, E, r.k, r.count_part.data_ptr(),
+              r.probsum_part.data_ptr(), r.parts, count.data_ptr(), probsum.data_ptr(), cursor.data_ptr(),
               lst.data_ptr(), offset.data_ptr(), tile_off.data_ptr(), _hip.stream(dev), kernel="moe_scatter_kernel",
               nbytes=r.M * r.k * 8)
+    r._count, r._probsum = count, probsum
     return lst, offset, tile_off
 
 
@@ -470,3 +500,50 @@ def moe_experts(x: torch.Tensor, y: torch.Tensor, r: MoERoute, lists, frags, gam
               r.count.data_ptr(), r.topk_w.data_ptr(), _hip.dtype_code(x.dtype), _hip.dtype_code(y.dtype),
               _hip.stream(x.device), kernel="moe_experts_kernel<%s>" % tag, nbytes=nbytes,
               flops=2 * pairs * 3 * 32 * H)
+
+
+def moe_ffn_supported(x2d: torch.Tensor, E: int, H: int, k: int) -> bool:
+    """Whether walsh_moe_ffn_fwd (single-launch MoE) handles this call."""
+    return (x2d.dtype == torch.bfloat16 and x2d.shape[-1] == 512 and E == 16 and H in (64, 128) and 1 <= k <= 8)
+
+
+def moe_ffn_fragments(w1: torch.Tensor, w2: torch.Tensor, gate_packed: torch.Tensor, up_packed: torch.Tensor,
+                      down_packed: torch.Tensor):
+    """Operand layouts of walsh_moe_ffn_fwd from the router weights and the
+    packed expert codes."""
+    H1, C = w1.shape
+    E, H = gate_packed.shape[0], gate_packed.shape[1]
+    f1 = w1.detach().to(torch.bfloat16).reshape(H1 // 16, 16, C // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous()
+    w2p = torch.zeros(16, H1, device=w2.device, dtype=torch.bfloat16)
+    w2p[:E] = w2.detach().to(torch.bfloat16)
+    f2 = w2p.reshape(16, H1 // 16, 4, 4).permute(1, 2, 0, 3).contiguous()  # [c][kq][m][s]
+
+    def gu(p):  # [E][nt][m][kq][2] -> [E][kq][m][nt][2]
+        return p.reshape(E, H // 16, 16, 4, 2).permute(0, 3, 2, 1, 4).contiguous().view(torch.int16)
+
+    # [E][mt][m][c][half][kq] -> [E][kq][m][mt][c][half]
+    dn = down_packed.reshape(E, 2, 16, H // 32, 2, 4).permute(0, 5, 2, 1, 3, 4).contiguous().view(torch.int16)
+    return f1, f2, gu(gate_packed), gu(up_packed), dn
+
+
+def moe_ffn(x: torch.Tensor, y: torch.Tensor, frags, gammas: torch.Tensor, E: int, k: int, H: int) -> MoERoute:
+    """Single-launch HadamardMoE forward (walsh_moe_ffn_fwd): writes y [M, 512]
+    (float32 or bf16) and returns the routing (topk_idx, topk_w, count, probsum)."""
+    _hip.require_device(x, "input")
+    xv, M, ldx = _rows_view(x, x.shape[-1])
+    C = x.shape[-1]
+    assert y.shape[-1] == C and y.stride(-1) == 1, "output layout"
+    ldy = y.stride(0) if y.dim() == 2 else C
+    parts = max(1, min((M + 63) // 64, _hip.cu_count(x.device)))
+    r = MoERoute(M, E, k, x.device, dense=False, parts=parts)
+    f1, f2, gf, uf, df = frags
+    g = gammas.detach().float().contiguous()
+    nbytes = M * C * (2 + y.element_size()) + M * k * 8 + (f1.numel() + f2.numel()) * 2 + 3 * E * H * 8
+    flops = 2 * M * (C * (C // 4) + (C // 4) * E) + 2 * M * k * 3 * 32 * H
+    _hip.call("walsh_moe_ffn_fwd", xv.data_ptr(), ldx, M, C, f1.data_ptr(), f2.data_ptr(), E, k, H, gf.data_ptr(),
+              uf.data_ptr(), df.data_ptr(), g.data_ptr(), r.topk_idx.data_ptr(), r.topk_w.data_ptr(),
+              r.count_part.data_ptr(), r.probsum_part.data_ptr(), parts, y.data_ptr(), ldy, _hip.dtype_code(x.dtype),
+              _hip.dtype_code(y.dtype), _hip.stream(x.device),
+              kernel="moe_ffn_kernel<%s>" % ("f32out" if y.dtype == torch.float32 else "bf16out"), nbytes=nbytes,
+              flops=flops)
+    return r

@@ -3,16 +3,19 @@
 ``HadamardMoE`` keeps the reference's constructor, submodules and parameter
 names (``router.gate.{0,2}.weight``, ``experts.{gate,up,down}_weights``) and
 its side state (``_aux_loss``, ``_last_expert_mask``, ``_expert_counts``,
-``_total_tokens``), but runs on four HIP launches instead of a dense einsum
-over all experts (moe.py:363-374):
+``_total_tokens``), but computes only the selected (token, expert) pairs
+instead of a dense einsum over all experts (moe.py:363-374):
 
-  1. walsh_moe_route_fwd   router MLP + softmax + top-k + weights + per-expert
-                           counts, zero-filling the blocks of unselected
-                           experts (or, for a large router, torch GEMMs for
-                           the two Linears and walsh_moe_topk_fwd);
-  2. walsh_moe_scatter     per-expert pair lists;
-  3. walsh_moe_experts_fwd ternary SwiGLU on the selected (token, expert)
-                           pairs only, weighted by the routing weight.
+  * bf16 at n_embd 512 (16 experts): one launch, walsh_moe_ffn_fwd (router,
+    routing and experts fused, the input tile read once into LDS);
+  * otherwise three launches:
+      1. walsh_moe_route_fwd   router MLP + softmax + top-k + weights +
+                               per-expert counts, zero-filling the blocks of
+                               unselected experts (for a wide router: torch
+                               GEMMs for the two Linears + walsh_moe_topk_fwd);
+      2. walsh_moe_scatter     per-expert pair lists;
+      3. walsh_moe_experts_fwd ternary SwiGLU on the routed pairs, weighted
+                               by the routing weight.
 
 Routing semantics are the reference's: top-k with k = min(max_experts, E)
 for every token (moe.py:434-436); ``threshold`` and ``min_experts`` are
@@ -81,6 +84,7 @@ class FastMoEExperts(nn.Module):
         nn.init.uniform_(self.gate_weights, -1, 1)
         nn.init.uniform_(self.up_weights, -1, 1)
         nn.init.uniform_(self.down_weights, -1, 1)
+        self._q = WeightCache()
         self._prep = WeightCache()
 
     def _check(self):
@@ -90,18 +94,31 @@ class FastMoEExperts(nn.Module):
             raise NotImplementedError(f"experts need dim 32 and expansion 2, 4 or 8 (dim={self.dim}, "
                                       f"hidden={self.hidden})")
 
-    def ternary_state(self, dtype: torch.dtype):
-        """(gammas float32 [3], fragments) of the three weight tensors; under
-        bf16 the gammas are rounded to bf16 as autocast rounds code * gamma."""
+    def quantized(self):
+        """(gammas float32 [3], packed codes (gate, up, down)) of the three
+        weight tensors (2-bit pack_ternary_weights layout)."""
         self._check()
         ws = (self.gate_weights, self.up_weights, self.down_weights)
 
         def build():
             qs = [kernels.ternary_quantize(w, packed=True) for w in ws]
-            g = torch.cat([q["gamma"] for q in qs])
-            if dtype == torch.bfloat16:
-                g = g.to(torch.bfloat16).float()
-            return g, kernels.moe_expert_fragments(*(q["packed"] for q in qs))
+            return torch.cat([q["gamma"] for q in qs]), tuple(q["packed"] for q in qs)
+
+        return self._q.get(ws, build)
+
+    @staticmethod
+    def operand_gammas(gammas: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        """Under bf16 autocast the einsum operand code * gamma is a bf16
+        tensor, i.e. code * bf16(gamma)."""
+        return gammas.to(torch.bfloat16).float() if dtype == torch.bfloat16 else gammas
+
+    def ternary_state(self, dtype: torch.dtype):
+        """(operand gammas [3], fragments for walsh_moe_experts_fwd)."""
+        ws = (self.gate_weights, self.up_weights, self.down_weights)
+
+        def build():
+            g, packed = self.quantized()
+            return self.operand_gammas(g, dtype), kernels.moe_expert_fragments(*packed)
 
         return self._prep.get(ws, build, extra=(dtype,))
 
@@ -123,11 +140,11 @@ class FastMoEExperts(nn.Module):
         y = torch.empty(M, E * D, device=x.device, dtype=_output_dtype(x, expert_weights.dtype))
         if M:
             # every (token, expert) pair, weighted by the given weights
-            r = kernels.MoERoute(M, E, E, x.device, dense=False)
+            r = kernels.MoERoute(M, E, E, x.device, dense=False, parts=1)
             r.topk_idx.copy_(torch.arange(E, device=x.device, dtype=torch.int32).expand(M, E))
             r.topk_w.copy_(expert_weights.reshape(M, E))
-            r.count.fill_(M)
-            r.cursor.zero_()
+            r.count_part.fill_(M)
+            r.probsum_part.zero_()
             self.routed(x2d, r, y)
         return y.view(B, T, E, D)
 
@@ -217,6 +234,7 @@ class HadamardMoE(nn.Module):
         self.experts = FastMoEExperts(n_experts=n_experts, dim=self.block_dim, expansion=expansion)
         self.register_buffer('_expert_counts', torch.zeros(n_experts), persistent=False)
         self.register_buffer('_total_tokens', torch.zeros(1), persistent=False)
+        self._ffn = WeightCache()   # single-launch operand layouts
         self._route = None          # routing of the last forward (device tensors)
         self._route_shape = None
         self._aux_value = None
@@ -262,16 +280,34 @@ class HadamardMoE(nn.Module):
         if dt == torch.float32:
             ydt = torch.float32
         y = torch.empty(M, C, device=x.device, dtype=ydt)
-        r = self.router.route(x2d, y2d=y)
+        ex = self.experts
+        if kernels.moe_ffn_supported(x2d, self.n_experts, ex.hidden, self.router.top_k) and self.use_fused:
+            # router, routing and experts in one launch
+            g, frags = self._ffn_state()
+            r = kernels.moe_ffn(x2d, y, frags, g, self.n_experts, self.router.top_k, ex.hidden)
+        else:
+            r = self.router.route(x2d, y2d=y)
+            if M:
+                ex.routed(x2d, r, y)
         self._route, self._route_shape = r, (B, T)
         self._aux_value = self._mask_value = None
         if self.training:
             with torch.no_grad():
                 self._expert_counts += r.count.float()
                 self._total_tokens += M
-        if M:
-            self.experts.routed(x2d, r, y)
         return y.view(B, T, C)
+
+    use_fused = True   # single-launch kernel where supported (tests switch it off to compare paths)
+
+    def _ffn_state(self):
+        ex, w1, w2 = self.experts, self.router.gate[0].weight, self.router.gate[2].weight
+        ws = (w1, w2, ex.gate_weights, ex.up_weights, ex.down_weights)
+
+        def build():
+            g, packed = ex.quantized()
+            return (ex.operand_gammas(g, torch.bfloat16), kernels.moe_ffn_fragments(w1, w2, *packed))
+
+        return self._ffn.get(ws, build)
 
     def get_aux_loss(self) -> Optional[torch.Tensor]:
         a = self._aux_loss
