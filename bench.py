@@ -38,7 +38,42 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-roofline", action="store_true", help="skip the instrumented pass (profiling runs)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy 5 times (reference for HBM byte counters)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mhcwalsh_forward_hbm_traffic.txt")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` measured with rocprofv3 counters
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), from
+    the committed summary; None when that kernel was not measured."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("kernel=") and "traffic_bytes=" in line:
+                    fields = dict(kv.split("=", 1) for kv in line.split())
+                    if fields["kernel"] == kernel:
+                        return int(float(fields["traffic_bytes"]))
+    except OSError:
+        pass
+    return None
+
+
+def calibrate_copy(torch):
+    """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE readings
+    give the scale factor from counter units to bytes."""
+    n = 256 << 20
+    src = torch.ones(n // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read_per_launch": n, "bytes_written_per_launch": n,
+                      "launches": 5}), flush=True)
 
 
 def build_model(torch, batch, seq):
@@ -85,6 +120,9 @@ def main():
     from src.model import _hip
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
     _hip.lib()
     cfg, model, idx = build_model(torch, args.batch, args.seq)
     tokens = args.batch * args.seq
@@ -117,7 +155,7 @@ def main():
         bytes_per_launch = d["bytes"] / d["launches"]
         achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
         roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                        frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None, kernel=dom,
+                        frac=round(achieved / HBM_PEAK_GBS, 4), traffic=measured_traffic(dom), kernel=dom,
                         avg_launch_us=round(avg_ms * 1000, 2), launches_per_step=d["launches"] // args.steps,
                         algorithmic_bytes_per_launch=int(bytes_per_launch))
 

@@ -44,6 +44,20 @@ const char *walsh_last_error(void);
 /* Binary name of the device code this library carries ("gfx950"). */
 const char *walsh_device_arch(void);
 
+/* Kernel timing -- a measurement hook with no counterpart in the reference,
+ * for callers that report per-kernel time (benchmarks, profilers).
+ * walsh_timing_begin(capacity): from now on every kernel launch records its
+ *   own start/stop timestamps (hipExtLaunchKernelGGL) into the next of
+ *   `capacity` event pairs, labelled with the tag last set by
+ *   walsh_timing_tag (initially -1).  Launches beyond capacity are untimed.
+ * walsh_timing_end(tags, ms, capacity): stops timing, waits for the timed
+ *   kernels and writes up to `capacity` (tag, milliseconds) pairs in launch
+ *   order; returns how many were written (negative on error).
+ * Not thread-safe while timing is on. */
+int walsh_timing_begin(int capacity);
+void walsh_timing_tag(int tag);
+int walsh_timing_end(int *tags, float *ms, int capacity);
+
 /* ------------------------------------------------------------------ A1 / A11
  * Absmean ternary quantisation.
  * Replaces TernaryAbsmeanSTE.forward / quantize_ternary

@@ -204,3 +204,25 @@ def test_hadamard_swiglu_and_padded_down(K, dtype, in_o, hid_o):
     y = K.hadamard_linear(h, hid_o, in_o, _prepare(K, cd), t(ad), t(bd), gsx=gsh)
     hq = hv[:, :, :hid_o].reshape(M, -1).astype(np.float64)
     assert_close(y.float().cpu().numpy(), ohad.hadamard_linear_f64(hq, cd, ad, bd), dtype, f"down {dtype}")
+
+
+def test_launch_timer_records_kernel_time(K):
+    """walsh_timing_*: every entry-point call inside LaunchTimer gets its
+    kernel's own duration (hipExtLaunchKernelGGL events)."""
+    from src.model import _hip
+    from src.model.hadamard import HadamardLinear
+    torch.manual_seed(0)
+    lin = HadamardLinear(512, 512).cuda()
+    x = torch.randn(4096, 512, device="cuda")
+    lin(x)
+    with _hip.LaunchTimer() as lt:
+        for _ in range(3):
+            lin(x)
+    s = lt.summary()
+    assert len(s) == 1
+    (name, d), = s.items()
+    assert name.startswith("hadamard_fwd_kernel") and d["launches"] == 3
+    assert 0.0 < d["ms"] < 100.0
+    # timing is off again: untimed launches still work
+    lin(x)
+    torch.cuda.synchronize()

@@ -48,7 +48,59 @@ const DeviceInfo &device_info() {
     return cache[dev];
 }
 
+Timing &timing() {
+    static Timing t{false, -1, 0, 0, nullptr, nullptr};
+    return t;
+}
+
 }  // namespace walsh
+
+WALSH_EXPORT int walsh_timing_begin(int capacity) {
+    using namespace walsh;
+    Timing &t = timing();
+    if (capacity < 1 || capacity > (1 << 20)) return set_error(WALSH_EINVAL, "walsh_timing_begin: capacity");
+    if (t.cap < capacity) {
+        for (int i = 0; i < 2 * t.cap; ++i) (void)hipEventDestroy(t.ev[i]);
+        delete[] t.ev;
+        delete[] t.tags;
+        t.ev = new hipEvent_t[2 * capacity];
+        t.tags = new int[capacity];
+        for (int i = 0; i < 2 * capacity; ++i) {
+            const hipError_t e = hipEventCreate(&t.ev[i]);
+            if (e != hipSuccess) {
+                for (int j = 0; j < i; ++j) (void)hipEventDestroy(t.ev[j]);
+                delete[] t.ev;
+                delete[] t.tags;
+                t.ev = nullptr;
+                t.tags = nullptr;
+                t.cap = 0;
+                return check_hip(e, "walsh_timing_begin: hipEventCreate");
+            }
+        }
+        t.cap = capacity;
+    }
+    t.n = 0;
+    t.tag = -1;
+    t.on = true;
+    return WALSH_OK;
+}
+
+WALSH_EXPORT void walsh_timing_tag(int tag) { walsh::timing().tag = tag; }
+
+WALSH_EXPORT int walsh_timing_end(int *tags, float *ms, int capacity) {
+    using namespace walsh;
+    Timing &t = timing();
+    t.on = false;
+    const int n = t.n < capacity ? t.n : capacity;
+    for (int i = 0; i < n; ++i) {
+        hipError_t e = hipEventSynchronize(t.ev[2 * i + 1]);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms[i], t.ev[2 * i], t.ev[2 * i + 1]);
+        if (e != hipSuccess) return check_hip(e, "walsh_timing_end");
+        tags[i] = t.tags[i];
+    }
+    t.n = 0;
+    return n;
+}
 
 WALSH_EXPORT int walsh_abi_version(void) { return WALSH_ABI_VERSION; }
 WALSH_EXPORT const char *walsh_last_error(void) { return walsh::g_err; }

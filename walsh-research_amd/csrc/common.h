@@ -1,6 +1,7 @@
 // Shared helpers for the Walsh HIP kernels (gfx950 / CDNA4, wave64).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -28,6 +29,30 @@ struct DeviceInfo {
     int max_shared_per_block;
 };
 const DeviceInfo &device_info();
+
+// ---------------------------------------------------------------- timing
+// Optional per-launch timing (walsh_timing_begin / _end): while it is on,
+// every launch records the kernel's own start and stop timestamps
+// (hipExtLaunchKernelGGL) into the next event pair of a pool, labelled with
+// the tag the caller set last.  Not thread-safe while on.
+struct Timing {
+    bool on;
+    int tag, n, cap;
+    hipEvent_t *ev;  // 2 * cap events
+    int *tags;       // cap
+};
+Timing &timing();
+
+template <typename F, typename... Args>
+inline void launch(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t s, Args... args) {
+    Timing &t = timing();
+    if (t.on && t.n < t.cap) {
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, s, t.ev[2 * t.n], t.ev[2 * t.n + 1], 0, args...);
+        t.tags[t.n++] = t.tag;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+    }
+}
 
 // ---------------------------------------------------------------- bf16
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {

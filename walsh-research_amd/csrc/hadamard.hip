@@ -498,7 +498,7 @@ WALSH_EXPORT int walsh_hadamard_prepare(const uint8_t *packed, int64_t in_o, int
     const int block = 256;
     int grid = (int)ceil_div(total, block);
     if (grid > 4096) grid = 4096;
-    hipLaunchKernelGGL(hadamard_prepare_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, packed, (int)in_o,
+    launch(hadamard_prepare_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, packed, (int)in_o,
                        (int)out_o, Nt, Kc, kweight);
     return check_hip(hipGetLastError(), "walsh_hadamard_prepare launch");
 }
@@ -552,7 +552,7 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
             ua.x = a.x;
             ua.y = a.y;
             ua.M = a.M;
-#define WALSH_SW_LAUNCH(T, MMA, V, K1) hipLaunchKernelGGL((hadamard_swiglu_kernel<T, MMA, V, K1>), G, B, lds, s, a, ua)
+#define WALSH_SW_LAUNCH(T, MMA, V, K1) launch((hadamard_swiglu_kernel<T, MMA, V, K1>), G, B, lds, s, a, ua)
             const bool one = Kc == 1;
             if (bf16) {
                 if (vec) { if (one) WALSH_SW_LAUNCH(uint16_t, true, true, true); else WALSH_SW_LAUNCH(uint16_t, true, true, false); }
@@ -563,7 +563,7 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
             }
 #undef WALSH_SW_LAUNCH
         } else {
-#define WALSH_HAD_LAUNCH(T, MMA, V, K1) hipLaunchKernelGGL((hadamard_fwd_kernel<T, MMA, V, K1>), G, B, lds, s, a)
+#define WALSH_HAD_LAUNCH(T, MMA, V, K1) launch((hadamard_fwd_kernel<T, MMA, V, K1>), G, B, lds, s, a)
             if (bf16) {
                 if (vec) { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, true, true); else WALSH_HAD_LAUNCH(uint16_t, true, true, false); }
                 else     { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, false, true); else WALSH_HAD_LAUNCH(uint16_t, true, false, false); }
@@ -649,10 +649,10 @@ WALSH_EXPORT int walsh_fht_fwd(const void *x, int64_t rows, int64_t n, int norma
     const float scale = normalize ? (float)(1.0 / sqrt((double)n)) : 1.0f;
     const dim3 G((unsigned)ceil_div(rows, rpb)), B(256);
     if (dtype == WALSH_BF16)
-        hipLaunchKernelGGL(fht_kernel<uint16_t>, G, B, lds, (hipStream_t)stream, (const uint16_t *)x, rows, logN,
+        launch(fht_kernel<uint16_t>, G, B, lds, (hipStream_t)stream, (const uint16_t *)x, rows, logN,
                            scale, (uint16_t *)y);
     else
-        hipLaunchKernelGGL(fht_kernel<float>, G, B, lds, (hipStream_t)stream, (const float *)x, rows, logN, scale,
+        launch(fht_kernel<float>, G, B, lds, (hipStream_t)stream, (const float *)x, rows, logN, scale,
                            (float *)y);
     return check_hip(hipGetLastError(), "walsh_fht_fwd launch");
 }

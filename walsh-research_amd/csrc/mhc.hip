@@ -559,7 +559,7 @@ WALSH_EXPORT int walsh_sinkhorn_fwd(const float *h, int64_t batch, int64_t n, in
     const int block = 128;
     int64_t grid = ceil_div(batch, block);
     if (grid > (int64_t)device_info().cu_count * 8) grid = (int64_t)device_info().cu_count * 8;
-    hipLaunchKernelGGL(sinkhorn_kernel, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream, h, batch, (int)n,
+    launch(sinkhorn_kernel, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream, h, batch, (int)n,
                        (int)n_iter, eps, out);
     return check_hip(hipGetLastError(), "walsh_sinkhorn_fwd launch");
 }
@@ -609,9 +609,9 @@ WALSH_EXPORT int walsh_mhc_pre_fwd(const void *x, int64_t ldx, int64_t M, int64_
         a.ld_in = ld_in;
         const dim3 G((unsigned)ceil_div(rows, kPreTok)), B(kPreThreads);
         if (dtype == WALSH_BF16)
-            hipLaunchKernelGGL((mhc_pre_kernel<uint16_t, true>), G, B, 0, (hipStream_t)stream, a);
+            launch((mhc_pre_kernel<uint16_t, true>), G, B, 0, (hipStream_t)stream, a);
         else
-            hipLaunchKernelGGL((mhc_pre_kernel<float, false>), G, B, 0, (hipStream_t)stream, a);
+            launch((mhc_pre_kernel<float, false>), G, B, 0, (hipStream_t)stream, a);
         const int rc = check_hip(hipGetLastError(), "walsh_mhc_pre_fwd launch");
         if (rc) return rc;
     }
@@ -646,12 +646,12 @@ WALSH_EXPORT int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out,
         if (grid > cap) grid = cap;
         hipStream_t s = (hipStream_t)stream;
         if (dtype == WALSH_BF16)
-            hipLaunchKernelGGL(mhc_post_kernel<uint16_t>, dim3((unsigned)grid), dim3(block), 0, s,
+            launch(mhc_post_kernel<uint16_t>, dim3((unsigned)grid), dim3(block), 0, s,
                                (const uint16_t *)x + r0 * ldx, ldx, (const uint16_t *)out + r0 * ld_out, ld_out,
                                h_res + r0 * n * n, h_post + r0 * n, (uint16_t *)x_new + r0 * ld_new, ld_new, (int)rows,
                                (int)n, (int)C);
         else
-            hipLaunchKernelGGL(mhc_post_kernel<float>, dim3((unsigned)grid), dim3(block), 0, s,
+            launch(mhc_post_kernel<float>, dim3((unsigned)grid), dim3(block), 0, s,
                                (const float *)x + r0 * ldx, ldx, (const float *)out + r0 * ld_out, ld_out,
                                h_res + r0 * n * n, h_post + r0 * n, (float *)x_new + r0 * ld_new, ld_new, (int)rows,
                                (int)n, (int)C);
@@ -717,11 +717,11 @@ WALSH_EXPORT int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, i
         const dim3 G((unsigned)ceil_div(rows, TT)), B(kPreThreads);
         hipStream_t s = (hipStream_t)stream;
         if (dtype == WALSH_BF16) {
-            if (MT == 2) hipLaunchKernelGGL((mhc_pre2_kernel<uint16_t, true, 2>), G, B, lds, s, a);
-            else hipLaunchKernelGGL((mhc_pre2_kernel<uint16_t, true, 1>), G, B, lds, s, a);
+            if (MT == 2) launch((mhc_pre2_kernel<uint16_t, true, 2>), G, B, lds, s, a);
+            else launch((mhc_pre2_kernel<uint16_t, true, 1>), G, B, lds, s, a);
         } else {
-            if (MT == 2) hipLaunchKernelGGL((mhc_pre2_kernel<float, false, 2>), G, B, lds, s, a);
-            else hipLaunchKernelGGL((mhc_pre2_kernel<float, false, 1>), G, B, lds, s, a);
+            if (MT == 2) launch((mhc_pre2_kernel<float, false, 2>), G, B, lds, s, a);
+            else launch((mhc_pre2_kernel<float, false, 1>), G, B, lds, s, a);
         }
         const int rc = check_hip(hipGetLastError(), "walsh_mhc_pre_norm_fwd launch");
         if (rc) return rc;

@@ -888,7 +888,7 @@ WALSH_EXPORT int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int6
     if (M * ldx * esz > (int64_t)kMaxBufferBytes) return set_error(WALSH_ENOTSUP, "%s: input too large", fn);
     hipStream_t s = (hipStream_t)stream;
     if (M == 0) {
-        hipLaunchKernelGGL(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
+        launch(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
         return check_hip(hipGetLastError(), fn);
     }
     RouterArgs a;
@@ -903,8 +903,8 @@ WALSH_EXPORT int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int6
                    topk_w,   count,   probsum,  (int)n_part, y, ldy, ydtype == WALSH_BF16};
     const dim3 G(grid_cap(ceil_div(M, 16), n_part)), B(kMoeThreads);
 #define WALSH_ROUTE(NE)                                                                               \
-    if (dtype == WALSH_BF16) hipLaunchKernelGGL((moe_route_kernel<uint16_t, true, NE>), G, B, 0, s, a); \
-    else hipLaunchKernelGGL((moe_route_kernel<float, false, NE>), G, B, 0, s, a);
+    if (dtype == WALSH_BF16) launch((moe_route_kernel<uint16_t, true, NE>), G, B, 0, s, a); \
+    else launch((moe_route_kernel<float, false, NE>), G, B, 0, s, a);
     if (a.net <= 1) { WALSH_ROUTE(1) } else if (a.net <= 2) { WALSH_ROUTE(2) } else { WALSH_ROUTE(4) }
 #undef WALSH_ROUTE
     return check_hip(hipGetLastError(), fn);
@@ -919,17 +919,17 @@ WALSH_EXPORT int walsh_moe_topk_fwd(const float *logits, int64_t M, int64_t E, i
     if (M > 0 && !logits) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
     hipStream_t s = (hipStream_t)stream;
     if (M == 0) {
-        hipLaunchKernelGGL(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
+        launch(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
         return check_hip(hipGetLastError(), fn);
     }
     RouteOut o{(int)M, (int)E, (int)k, probs, mask, weights_dense, topk_idx, topk_w, count, probsum, (int)n_part,
                nullptr, 0, 0};
     const int net = (int)ceil_div(E, 16);
     const dim3 G(grid_cap(ceil_div(M, 16), n_part)), B(kMoeThreads);
-    if (net <= 1) hipLaunchKernelGGL(moe_topk_kernel<1>, G, B, 0, s, logits, net, o);
-    else if (net <= 2) hipLaunchKernelGGL(moe_topk_kernel<2>, G, B, 0, s, logits, net, o);
-    else if (net <= 4) hipLaunchKernelGGL(moe_topk_kernel<4>, G, B, 0, s, logits, net, o);
-    else hipLaunchKernelGGL(moe_topk_kernel<8>, G, B, 0, s, logits, net, o);
+    if (net <= 1) launch(moe_topk_kernel<1>, G, B, 0, s, logits, net, o);
+    else if (net <= 2) launch(moe_topk_kernel<2>, G, B, 0, s, logits, net, o);
+    else if (net <= 4) launch(moe_topk_kernel<4>, G, B, 0, s, logits, net, o);
+    else launch(moe_topk_kernel<8>, G, B, 0, s, logits, net, o);
     return check_hip(hipGetLastError(), fn);
 }
 
@@ -944,12 +944,12 @@ WALSH_EXPORT int walsh_moe_scatter(const int *topk_idx, int64_t M, int64_t E, in
         return set_error(WALSH_EINVAL, "%s: bad shape (M=%lld E=%lld k=%lld n_part=%lld)", fn, (long long)M,
                          (long long)E, (long long)k, (long long)n_part);
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(moe_finalize_kernel, dim3(1), dim3(kMaxE), 0, s, count_part, probsum_part, (int)n_part,
+    launch(moe_finalize_kernel, dim3(1), dim3(kMaxE), 0, s, count_part, probsum_part, (int)n_part,
                        (int)E, count, probsum, cursor, offset, tile_off);
     const int64_t n_pairs = M * k;
     if (n_pairs > 0) {
         const int64_t grid = ceil_div(n_pairs, 256 * kScatterPerThread);
-        hipLaunchKernelGGL(moe_scatter_kernel, dim3((unsigned)grid), dim3(256), 0, s, topk_idx, n_pairs, (int)E,
+        launch(moe_scatter_kernel, dim3((unsigned)grid), dim3(256), 0, s, topk_idx, n_pairs, (int)E,
                            offset, cursor, list);
     }
     return check_hip(hipGetLastError(), fn);
@@ -997,10 +997,10 @@ WALSH_EXPORT int walsh_moe_experts_fwd(const void *x, int64_t ldx, void *y, int6
     const dim3 G(grid_cap(ceil_div(M * k, 16) + E)), B(kMoeThreads);
     hipStream_t s = (hipStream_t)stream;
 #define WALSH_EXP_LAUNCH(NH)                                                                                  \
-    if (dtype == WALSH_F32) hipLaunchKernelGGL((moe_experts_kernel<float, float, false, NH>), G, B, 0, s, a);  \
+    if (dtype == WALSH_F32) launch((moe_experts_kernel<float, float, false, NH>), G, B, 0, s, a);  \
     else if (ydtype == WALSH_BF16)                                                                            \
-        hipLaunchKernelGGL((moe_experts_kernel<uint16_t, uint16_t, true, NH>), G, B, 0, s, a);                \
-    else hipLaunchKernelGGL((moe_experts_kernel<uint16_t, float, true, NH>), G, B, 0, s, a);
+        launch((moe_experts_kernel<uint16_t, uint16_t, true, NH>), G, B, 0, s, a);                \
+    else launch((moe_experts_kernel<uint16_t, float, true, NH>), G, B, 0, s, a);
     if (H == 64) { WALSH_EXP_LAUNCH(4) } else if (H == 128) { WALSH_EXP_LAUNCH(8) } else { WALSH_EXP_LAUNCH(16) }
 #undef WALSH_EXP_LAUNCH
     return check_hip(hipGetLastError(), fn);
@@ -1025,7 +1025,7 @@ WALSH_EXPORT int walsh_moe_ffn_fwd(const void *x, int64_t ldx, int64_t M, int64_
     if (n_part < 1 || n_part > 65536) return set_error(WALSH_EINVAL, "%s: n_part must be in [1, 65536]", fn);
     hipStream_t s = (hipStream_t)stream;
     if (M == 0) {
-        hipLaunchKernelGGL(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
+        launch(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
         return check_hip(hipGetLastError(), fn);
     }
     FfnArgs a;
@@ -1052,8 +1052,8 @@ WALSH_EXPORT int walsh_moe_ffn_fwd(const void *x, int64_t ldx, int64_t M, int64_
     if (g > n_part) g = n_part;
     const dim3 G((unsigned)g), B(kFfnThreads);
 #define WALSH_FFN(NHV)                                                                 \
-    if (ydtype == WALSH_F32) hipLaunchKernelGGL((moe_ffn_kernel<float, NHV>), G, B, 0, s, a); \
-    else hipLaunchKernelGGL((moe_ffn_kernel<uint16_t, NHV>), G, B, 0, s, a);
+    if (ydtype == WALSH_F32) launch((moe_ffn_kernel<float, NHV>), G, B, 0, s, a); \
+    else launch((moe_ffn_kernel<uint16_t, NHV>), G, B, 0, s, a);
     if (H == 64) { WALSH_FFN(4) } else { WALSH_FFN(8) }
 #undef WALSH_FFN
     return check_hip(hipGetLastError(), fn);

@@ -189,10 +189,10 @@ WALSH_EXPORT int walsh_octonion_prepare(const uint8_t *packed, int64_t in_o, int
     int64_t grid = ceil_div(total, block);
     if (grid > 8192) grid = 8192;
     if (dtype == WALSH_BF16)
-        hipLaunchKernelGGL(octonion_expand_kernel<uint16_t>, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream,
+        launch(octonion_expand_kernel<uint16_t>, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream,
                            packed, (int)in_o, (int)out_o, Kp, (uint16_t *)B);
     else
-        hipLaunchKernelGGL(octonion_expand_kernel<float>, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream,
+        launch(octonion_expand_kernel<float>, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream,
                            packed, (int)in_o, (int)out_o, Kp, (float *)B);
     return check_hip(hipGetLastError(), "walsh_octonion_prepare launch");
 }
@@ -231,9 +231,9 @@ WALSH_EXPORT int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M
         a.ldy = ldy;
         const dim3 G((unsigned)ceil_div(rows, kBM), (unsigned)ceil_div(N, kBN)), Bk(kGemmThreads);
         if (dtype == WALSH_BF16)
-            hipLaunchKernelGGL(octonion_gemm_kernel<uint16_t>, G, Bk, 0, (hipStream_t)stream, a);
+            launch(octonion_gemm_kernel<uint16_t>, G, Bk, 0, (hipStream_t)stream, a);
         else
-            hipLaunchKernelGGL(octonion_gemm_kernel<float>, G, Bk, 0, (hipStream_t)stream, a);
+            launch(octonion_gemm_kernel<float>, G, Bk, 0, (hipStream_t)stream, a);
         const int rc = check_hip(hipGetLastError(), "walsh_octonion_linear_fwd launch");
         if (rc) return rc;
     }

@@ -100,7 +100,7 @@ using namespace walsh;
 WALSH_EXPORT int walsh_ternary_gamma(const float *w, int64_t n, float *gamma, void *stream) {
     if (!w || !gamma) return set_error(WALSH_EINVAL, "walsh_ternary_gamma: null pointer");
     if (n <= 0) return set_error(WALSH_EINVAL, "walsh_ternary_gamma: n must be positive (got %lld)", (long long)n);
-    hipLaunchKernelGGL(gamma_kernel, dim3(1), dim3(kGammaThreads), 0, (hipStream_t)stream, w, n, gamma);
+    launch(gamma_kernel, dim3(1), dim3(kGammaThreads), 0, (hipStream_t)stream, w, n, gamma);
     return check_hip(hipGetLastError(), "walsh_ternary_gamma launch");
 }
 
@@ -111,7 +111,7 @@ WALSH_EXPORT int walsh_ternary_quantize(const float *w, int64_t rows, int64_t K,
         return set_error(WALSH_EINVAL, "walsh_ternary_quantize: rows and K must be positive");
     const int block = 256;
     const int grid = grid_for(rows * ceil_div(K, 4), block);
-    hipLaunchKernelGGL(quantize_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, w, rows, K, gamma,
+    launch(quantize_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, w, rows, K, gamma,
                        codes, packed, scaled);
     return check_hip(hipGetLastError(), "walsh_ternary_quantize launch");
 }
@@ -122,6 +122,6 @@ WALSH_EXPORT int walsh_ternary_unpack(const uint8_t *packed, int64_t rows, int64
     if (rows <= 0 || K <= 0) return set_error(WALSH_EINVAL, "walsh_ternary_unpack: rows and K must be positive");
     const int block = 256;
     const int grid = grid_for(rows * K, block);
-    hipLaunchKernelGGL(unpack_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, packed, rows, K, codes);
+    launch(unpack_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, packed, rows, K, codes);
     return check_hip(hipGetLastError(), "walsh_ternary_unpack launch");
 }

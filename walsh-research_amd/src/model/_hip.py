@@ -24,6 +24,9 @@ SIGNATURES = {
     "walsh_abi_version": (_I, []),
     "walsh_last_error": (ctypes.c_char_p, []),
     "walsh_device_arch": (ctypes.c_char_p, []),
+    "walsh_timing_begin": (_I, [_I]),
+    "walsh_timing_tag": (None, [_I]),
+    "walsh_timing_end": (_I, [_P, _P, _I]),
     "walsh_ternary_gamma": (_I, [_P, _I64, _P, _P]),
     "walsh_ternary_quantize": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
     "walsh_ternary_unpack": (_I, [_P, _I64, _I64, _P, _P]),
@@ -87,30 +90,51 @@ _timer = None
 
 
 class LaunchTimer:
-    """Context manager that brackets every hot-path launch with HIP events on
-    the launching (current torch) stream and records (kernel, bytes, flops,
-    start, end).  Used by bench.py to time the dominant kernel."""
+    """Context manager that times every hot-path kernel launch with the
+    kernel's own start/stop timestamps (walsh_timing_begin: the library
+    launches through hipExtLaunchKernelGGL with an event pair per launch, on
+    the launching stream), labelled with the (kernel, bytes, flops) of the
+    entry-point call that made it.  Used by bench.py for the roofline."""
+
+    CAPACITY = 1 << 16
 
     def __init__(self):
-        self.records = []
+        self.meta = []
+        self.records = None
 
     def __enter__(self):
         global _timer
+        check(lib().walsh_timing_begin(self.CAPACITY), "walsh_timing_begin")
         _timer = self
         return self
 
     def __exit__(self, *exc):
         global _timer
         _timer = None
+        self.records = self._collect()
+
+    def _collect(self):
+        cap = self.CAPACITY
+        tags = (ctypes.c_int * cap)()
+        ms = (ctypes.c_float * cap)()
+        n = lib().walsh_timing_end(tags, ms, cap)
+        if n < 0:
+            check(n, "walsh_timing_end")
+        return [(tags[i], ms[i]) for i in range(n)]
 
     def summary(self):
-        """{kernel: dict(launches, ms, bytes, flops)} (synchronises first)."""
-        torch.cuda.synchronize()
+        """{kernel: dict(launches, ms, bytes, flops)}: kernel time summed per
+        entry-point call (available after the with-block)."""
+        per_call = {}
+        for tag, ms in self.records:
+            if tag >= 0:
+                per_call[tag] = per_call.get(tag, 0.0) + ms
         out = {}
-        for kname, nbytes, flops, s, e in self.records:
+        for tag, ms in per_call.items():
+            kname, nbytes, flops = self.meta[tag]
             d = out.setdefault(kname, dict(launches=0, ms=0.0, bytes=0, flops=0))
             d["launches"] += 1
-            d["ms"] += s.elapsed_time(e)
+            d["ms"] += ms
             d["bytes"] += nbytes
             d["flops"] += flops
         return out
@@ -118,16 +142,13 @@ class LaunchTimer:
 
 def call(name: str, *args, kernel: str = None, nbytes: int = 0, flops: int = 0) -> None:
     t = _timer
-    if t is None or kernel is None:
-        check(getattr(lib(), name)(*args), name)
-        return
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
-    s.record()
-    rc = getattr(lib(), name)(*args)
-    e.record()
-    check(rc, name)
-    t.records.append((kernel, int(nbytes), int(flops), s, e))
+    if t is not None:
+        if kernel is None:
+            lib().walsh_timing_tag(-1)
+        else:
+            lib().walsh_timing_tag(len(t.meta))
+            t.meta.append((kernel, int(nbytes), int(flops)))
+    check(getattr(lib(), name)(*args), name)
 
 
 def require_device(t: torch.Tensor, what: str = "tensor") -> None:
