@@ -6,6 +6,14 @@ n_embd 512, Hadamard algebra with head mixing, 4 mHC streams, MoE and channel
 modulation off, tokens uniform over a 50257 vocabulary, batch 8 x seq 1024.
 A step is one forward over that batch (inputs resident in HBM).
 
+Other workloads (``--workload``), each printing one JSON line of its own:
+  moe       HadamardMoE alone, bf16 autocast, n_embd 512 (16 experts, k = 6),
+            x [16, 1024, 512]; inputs and outputs rotate over buffers larger
+            than the 256 MB Infinity Cache so reads come from HBM;
+  octonion  8 OctonionFusedLinear(1024, 1024) layers, bf16, x [32, 2048, 1024];
+  hadamard  one HadamardLinear(512, 512), fp32, x [4, 256, 512] and a
+            token sweep up to 262144 rows (rotated).
+
 Prints ONE JSON line.  Besides the timed region it
   * repeats the K steps with HIP events around every hot-path launch (on the
     launching stream) to find the dominant kernel and its achieved
@@ -25,6 +33,7 @@ for p in (ROOT, os.path.join(ROOT, "walsh-research_amd")):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "tokens/sec through Walsh layer stack at 1 GPU; % of HBM roofline (GB/s)"
 
 
@@ -38,6 +47,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-roofline", action="store_true", help="skip the instrumented pass (profiling runs)")
+    ap.add_argument("--workload", default="mhcwalsh", choices=["mhcwalsh", "moe", "octonion", "hadamard"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (reference for HBM byte counters)")
     return ap.parse_args()
@@ -123,6 +133,10 @@ def main():
     if args.calibrate_copy:
         calibrate_copy(torch)
         return
+    if args.workload != "mhcwalsh":
+        line = {"moe": bench_moe, "octonion": bench_octonion, "hadamard": bench_hadamard}[args.workload](torch, args)
+        print(json.dumps(line), flush=True)
+        return
     _hip.lib()
     cfg, model, idx = build_model(torch, args.batch, args.seq)
     tokens = args.batch * args.seq
@@ -186,6 +200,183 @@ def main():
                                    gbs=round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1),
                                    ms_per_step=round(v["ms"] / args.steps, 3)) for k, v in kernels.items()}
     print(json.dumps(line), flush=True)
+
+
+def _time_steps(torch, step, steps, warmup):
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def _roofline_of(kernels, steps, bound="hbm"):
+    from src.model import _hip  # noqa: F401
+    dom = max(kernels, key=lambda k: kernels[k]["ms"])
+    d = kernels[dom]
+    avg_ms = d["ms"] / d["launches"]
+    if bound == "mfma":
+        achieved = d["flops"] / d["launches"] / (avg_ms * 1e-3) / 1e12
+        peak, unit = MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        achieved = d["bytes"] / d["launches"] / (avg_ms * 1e-3) / 1e9
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+    return dict(bound=bound, achieved=round(achieved, 1), peak=peak, unit=unit, frac=round(achieved / peak, 4),
+                traffic=measured_traffic(dom), kernel=dom, avg_launch_us=round(avg_ms * 1000, 2),
+                launches_per_step=d["launches"] // steps,
+                algorithmic_bytes_per_launch=int(d["bytes"] / d["launches"]),
+                flops_per_launch=int(d["flops"] / d["launches"]))
+
+
+def _line(metric, value, unit, steps, warmup, ms, dtype, data, config, roofline, cpu, higher=True):
+    return {"metric": metric, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": round(ms, 4), "higher_is_better": higher, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype, "data": data, "config": config, "roofline": roofline,
+            "cpu_baseline": cpu}
+
+
+def bench_moe(torch, args):
+    """HadamardMoE forward (config 3): router N(0, 0.02), k = 6 for every token
+    (the reference's top-k routing), reference output dtype (float32)."""
+    from src.model import _hip
+    from src.model.moe import HadamardMoE
+
+    class Cfg:
+        n_embd = 512
+    torch.manual_seed(0)
+    m = HadamardMoE(Cfg(), max_experts=6).cuda().eval()
+    with torch.no_grad():
+        for lin in (m.router.gate[0], m.router.gate[2]):
+            lin.weight.normal_(0.0, 0.02)
+    B, T, C = 16, 1024, 512
+    nbuf = 8   # 8 x (16 MB in + 32 MB out) = 384 MB > 256 MB Infinity Cache
+    gen = torch.Generator().manual_seed(0)
+    xs = [torch.randn(B, T, C, generator=gen).bfloat16().cuda() for _ in range(nbuf)]
+
+    def step(i):
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return m(xs[i % nbuf])
+    dt = _time_steps(torch, step, args.steps, args.warmup)
+    with _hip.LaunchTimer() as lt:
+        for i in range(args.steps):
+            step(i)
+    roof = _roofline_of(lt.summary(), args.steps)
+    cpu = None
+    if not args.no_cpu:
+        from oracle.moe import moe_forward
+        sd = {k: v.detach().cpu().float().numpy() for k, v in m.state_dict().items()}
+        xc = xs[0].float().cpu().numpy().reshape(-1, C)[:1024]
+        t0, reps = time.perf_counter(), 0
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0) or reps == 0:
+            moe_forward(xc, sd["router.gate.0.weight"], sd["router.gate.2.weight"], sd["experts.gate_weights"],
+                        sd["experts.up_weights"], sd["experts.down_weights"], 6)
+            reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(reps * 1024 / el, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   sample=f"{reps} x 1024 tokens through oracle/moe.py (numpy float64, all-expert einsum as the "
+                          f"reference), {el:.1f} s")
+    return _line("tokens/sec through the Hadamard MoE FFN at 1 GPU; % of HBM roofline (GB/s)", B * T / dt,
+                 "tokens/s", args.steps, args.warmup, dt * 1e3, "bf16",
+                 "synthetic: x N(0,1), router N(0,0.02), experts U(-1,1) latents",
+                 {"workload": "HadamardMoE n_embd 512, 16 experts, k 6, expansion 4", "global_batch": B,
+                  "seq_len": T, "parallelism": "single GPU", "rotated_buffers": nbuf}, roof, cpu)
+
+
+def bench_octonion(torch, args):
+    """8 octonion ternary linear layers (config 4), bf16, x [32, 2048, 1024]."""
+    from src.model import _hip
+    from src.model.octonion import OctonionFusedLinear
+    torch.manual_seed(0)
+    layers = [OctonionFusedLinear(1024, 1024).cuda() for _ in range(8)]
+    with torch.no_grad():
+        for l in layers:
+            l.weight.normal_(0.0, 0.02)
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(32 * 2048, 1024, generator=gen).bfloat16().cuda()
+
+    def step(i):
+        with torch.no_grad():
+            h = x
+            for l in layers:
+                h = l.forward_full(h)
+            return h
+    dt = _time_steps(torch, step, args.steps, args.warmup)
+    with _hip.LaunchTimer() as lt:
+        for i in range(args.steps):
+            step(i)
+    roof = _roofline_of(lt.summary(), args.steps, bound="mfma")
+    cpu = None
+    if not args.no_cpu:
+        import numpy as np
+        from oracle.octonion import octonion_linear_f64
+        codes = np.sign(layers[0].weight.detach().cpu().numpy())  # timing only: any ternary matrix
+        beta = layers[0].beta.detach().cpu().numpy()
+        xp = x[:2048].float().cpu().numpy().reshape(2048, 8, 128).transpose(1, 0, 2)
+        t0, reps = time.perf_counter(), 0
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0) or reps == 0:
+            octonion_linear_f64(xp, codes, beta)
+            reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(reps * 2048 / 8 / el, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   sample=f"{reps} x one layer on 2048 tokens (oracle/octonion.py, 64 block matmuls as the reference "
+                          f"CPU path), {el:.1f} s; tokens/s of the 8-layer stack = layer rate / 8")
+    return _line("tokens/sec through the octonion ternary linear stack at 1 GPU; % of MFMA roofline",
+                 32 * 2048 / dt, "tokens/s", args.steps, args.warmup, dt * 1e3, "bf16",
+                 "synthetic: x N(0,1), weights N(0,0.02) latents",
+                 {"workload": "8 x OctonionFusedLinear(1024, 1024)", "global_batch": 32, "seq_len": 2048,
+                  "parallelism": "single GPU"}, roof, cpu)
+
+
+def bench_hadamard(torch, args):
+    """One HadamardLinear(512, 512) in fp32 (config 1: x [4, 256, 512]) and a
+    token sweep with rotated buffers (> 256 MB) for the HBM figure."""
+    from src.model import _hip
+    from src.model.hadamard import HadamardLinear
+    torch.manual_seed(0)
+    lin = HadamardLinear(512, 512).cuda()
+    sweep = []
+    for rows in (1024, 8192, 65536, 262144):
+        nbuf = max(1, min(64, (512 << 20) // (rows * 512 * 4 * 2)))
+        gen = torch.Generator().manual_seed(0)
+        xs = [torch.randn(rows, 512, generator=gen).cuda() for _ in range(nbuf)]
+
+        def step(i):
+            with torch.no_grad():
+                return lin(xs[i % nbuf])
+        iters = max(args.steps, 200 if rows <= 8192 else 20)
+        dt = _time_steps(torch, step, iters, args.warmup)
+        with _hip.LaunchTimer() as lt:
+            for i in range(iters):
+                step(i)
+        r = _roofline_of(lt.summary(), iters)
+        sweep.append(dict(rows=rows, us_per_call=round(dt * 1e6, 2), kernel_us=r["avg_launch_us"],
+                          kernel_gbs=r["achieved"], frac=r["frac"], rotated_buffers=nbuf))
+        if rows == 1024:
+            roof, dt1 = r, dt
+    cpu = None
+    if not args.no_cpu:
+        import numpy as np
+        from oracle.hadamard import hadamard_linear_torch32
+        codes = np.sign(lin.weight.detach().cpu().numpy())
+        xc = torch.randn(1024, 512)
+        t0, reps = time.perf_counter(), 0
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 5.0) or reps == 0:
+            hadamard_linear_torch32(xc, codes, lin.alpha.detach().cpu(), lin.beta.detach().cpu())
+            reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(reps * 1024 / el, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   sample=f"{reps} x [4, 256, 512] float32 through oracle/hadamard.py (the reference CPU einsums), "
+                          f"{el:.1f} s")
+    line = _line("tokens/sec through one Hadamard ternary linear at 1 GPU; % of HBM roofline (GB/s)",
+                 1024 / dt1, "tokens/s", max(args.steps, 200), args.warmup, dt1 * 1e3, "f32",
+                 "synthetic: x N(0,1), weights N(0,0.02) latents",
+                 {"workload": "HadamardLinear(512, 512), x [4, 256, 512]", "global_batch": 4, "seq_len": 256,
+                  "parallelism": "single GPU"}, roof, cpu)
+    line["sweep"] = sweep
+    return line
 
 
 if __name__ == "__main__":
