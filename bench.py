@@ -12,7 +12,11 @@ Other workloads (``--workload``), each printing one JSON line of its own:
             than the 256 MB Infinity Cache so reads come from HBM;
   octonion  8 OctonionFusedLinear(1024, 1024) layers, bf16, x [32, 2048, 1024];
   hadamard  one HadamardLinear(512, 512), fp32, x [4, 256, 512] and a
-            token sweep up to 262144 rows (rotated).
+            token sweep up to 262144 rows (rotated);
+  prefill5  scaled model: n_embd 4096 (32 heads of 128), 24 layers, MoE with
+            128 experts (k = 6), 4 streams, bf16, prefill of 64 x 1024 tokens;
+  decode5   the same model decoding one token per sequence against a
+            synthetic KV cache of length 4096, at batch 1, 16 and 64.
 
 Prints ONE JSON line.  Besides the timed region it
   * repeats the K steps with HIP events around every hot-path launch (on the
@@ -47,7 +51,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-roofline", action="store_true", help="skip the instrumented pass (profiling runs)")
-    ap.add_argument("--workload", default="mhcwalsh", choices=["mhcwalsh", "moe", "octonion", "hadamard"])
+    ap.add_argument("--workload", default="mhcwalsh",
+                    choices=["mhcwalsh", "moe", "octonion", "hadamard", "prefill5", "decode5"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (reference for HBM byte counters)")
     return ap.parse_args()
@@ -56,10 +61,13 @@ def parse():
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mhcwalsh_forward_hbm_traffic.txt")
 
 
-def measured_traffic(kernel: str):
+def measured_traffic(kernel: str, workload: str = "mhcwalsh"):
     """HBM bytes per launch of ``kernel`` measured with rocprofv3 counters
     (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), from
-    the committed summary; None when that kernel was not measured."""
+    the committed summary of the default workload; None when that kernel
+    was not measured at this workload's shapes."""
+    if workload != "mhcwalsh":
+        return None
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
@@ -134,7 +142,8 @@ def main():
         calibrate_copy(torch)
         return
     if args.workload != "mhcwalsh":
-        line = {"moe": bench_moe, "octonion": bench_octonion, "hadamard": bench_hadamard}[args.workload](torch, args)
+        line = {"moe": bench_moe, "octonion": bench_octonion, "hadamard": bench_hadamard, "prefill5": bench_prefill5,
+                "decode5": bench_decode5}[args.workload](torch, args)
         print(json.dumps(line), flush=True)
         return
     _hip.lib()
@@ -225,7 +234,7 @@ def _roofline_of(kernels, steps, bound="hbm"):
         achieved = d["bytes"] / d["launches"] / (avg_ms * 1e-3) / 1e9
         peak, unit = HBM_PEAK_GBS, "GB/s"
     return dict(bound=bound, achieved=round(achieved, 1), peak=peak, unit=unit, frac=round(achieved / peak, 4),
-                traffic=measured_traffic(dom), kernel=dom, avg_launch_us=round(avg_ms * 1000, 2),
+                traffic=None, kernel=dom, avg_launch_us=round(avg_ms * 1000, 2),
                 launches_per_step=d["launches"] // steps,
                 algorithmic_bytes_per_launch=int(d["bytes"] / d["launches"]),
                 flops_per_launch=int(d["flops"] / d["launches"]))
@@ -375,6 +384,100 @@ def bench_hadamard(torch, args):
                  "synthetic: x N(0,1), weights N(0,0.02) latents",
                  {"workload": "HadamardLinear(512, 512), x [4, 256, 512]", "global_batch": 4, "seq_len": 256,
                   "parallelism": "single GPU"}, roof, cpu)
+    line["sweep"] = sweep
+    return line
+
+
+def _config5(torch, block_size):
+    from src.model import WalshConfig, mHCWalsh
+    torch.manual_seed(0)
+    cfg = WalshConfig(block_size=block_size, vocab_size=50257, n_layer=24, n_head=32, n_embd=4096,
+                      algebra="hadamard", head_mixing=True, use_moe=True, moe_max_experts=6, use_channel_mod=False)
+    with torch.device("cuda"):
+        model = mHCWalsh(cfg, n_streams=4).eval()
+    return cfg, model
+
+
+def _config5_cpu(torch, model, cfg, args, tokens):
+    """Oracle float32 forward of the first layer on a bounded token sample,
+    scaled to the 24-layer stack (layers cost the same)."""
+    from oracle.model import Oracle
+    keep = ("tok_embeddings.", "output.", "stream_proj.", "stream_merge.", "norm.", "freqs_cis", "layers.0.")
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items() if k.startswith(keep)}
+    orc = Oracle(sd, cfg.n_embd, cfg.n_head, 1, n_streams=4, use_moe=True, moe_max_experts=6)
+    idx = torch.randint(0, cfg.vocab_size, (1, tokens), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        orc.forward(idx[:, :8])
+        t0, reps = time.perf_counter(), 0
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 15.0) or reps == 0:
+            orc.forward(idx)
+            reps += 1
+    el = time.perf_counter() - t0
+    rate = reps * tokens / el / cfg.n_layer
+    return dict(value=round(rate, 2), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{reps} x (1 x {tokens} tokens) through one layer of the oracle float32 forward "
+                       f"(oracle/model.py) in {el:.1f} s; rate divided by the 24 layers (extrapolated)")
+
+
+def bench_prefill5(torch, args):
+    from src.model import _hip
+    cfg, model = _config5(torch, 1024)
+    B, T = 64, 1024
+    idx = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(0)).cuda()
+
+    def step(i):
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return model(idx)[0]
+    steps, warm = min(args.steps, 3), min(args.warmup, 1)
+    dt = _time_steps(torch, step, steps, warm)
+    with _hip.LaunchTimer() as lt:
+        step(0)
+    roof = _roofline_of(lt.summary(), 1)
+    cpu = None if args.no_cpu else _config5_cpu(torch, model, cfg, args, 64)
+    line = _line("tokens/sec through Walsh layer stack at 1 GPU; % of HBM roofline (GB/s)", B * T / dt, "tokens/s",
+                 steps, warm, dt * 1e3, "bf16", "synthetic: random-init weights, tokens uniform over 50257",
+                 {"workload": "mHCWalsh prefill, n_layer 24, n_embd 4096, n_head 32 (head_dim 128), hadamard + head "
+                              "mixing, MoE 128 experts k 6, 4 mHC streams", "global_batch": B, "seq_len": T,
+                  "parallelism": "single GPU"}, roof, cpu)
+    line["kernels"] = {k: dict(launches=v["launches"], us_per_launch=round(v["ms"] * 1000 / v["launches"], 2),
+                               gbs=round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1), ms=round(v["ms"], 3))
+                       for k, v in lt.summary().items()}
+    return line
+
+
+def bench_decode5(torch, args):
+    from src.model import KVCache, _hip
+    cfg, model = _config5(torch, 4096)
+    kv_len = 4095     # cached tokens; the decoded token is position 4096
+    bmax = 64
+    kv = KVCache(cfg.n_layer, 4096, cfg.n_head, cfg.n_embd // cfg.n_head, torch.device("cuda"),
+                 dtype=torch.bfloat16, batch=bmax)
+    sweep = []
+    for b in (1, 16, 64):
+        idx = torch.randint(0, cfg.vocab_size, (b, 1), generator=torch.Generator().manual_seed(b)).cuda()
+
+        def step(i):
+            kv.cached_len = kv_len   # synthetic cache content; every step decodes position kv_len
+            with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+                return model(idx, kv_cache=kv, start_pos=kv_len)[0]
+        steps = max(args.steps, 10)
+        dt = _time_steps(torch, step, steps, args.warmup)
+        with _hip.LaunchTimer() as lt:
+            for i in range(steps):
+                step(i)
+        k = lt.summary()
+        hot_ms = sum(v["ms"] for v in k.values()) / steps
+        sweep.append(dict(batch=b, ms_per_step=round(dt * 1e3, 3), tokens_per_s=round(b / dt, 1),
+                          hot_path_kernel_ms_per_step=round(hot_ms, 3)))
+        if b == bmax:
+            roof = _roofline_of(k, steps)
+            dt64 = dt
+    cpu = None if args.no_cpu else _config5_cpu(torch, model, cfg, args, 16)
+    line = _line("tokens/sec through Walsh layer stack at 1 GPU; % of HBM roofline (GB/s)", bmax / dt64, "tokens/s",
+                 max(args.steps, 10), args.warmup, dt64 * 1e3, "bf16",
+                 "synthetic: random-init weights, zero KV cache of length 4095",
+                 {"workload": "mHCWalsh decode, n_layer 24, n_embd 4096, MoE 128 experts, KV 4096", "global_batch": bmax,
+                  "seq_len": 1, "parallelism": "single GPU"}, roof, cpu)
     line["sweep"] = sweep
     return line
 

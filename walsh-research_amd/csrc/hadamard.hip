@@ -56,21 +56,24 @@ __global__ void hadamard_prepare_kernel(const uint8_t *__restrict__ packed, int 
 // ---------------------------------------------------------------- helpers
 
 // Unnormalised 32-point Walsh-Hadamard transform along the group index of
-// 4 independent columns held as v[g][j] (Sylvester ordering, in place).
-__device__ __forceinline__ void fht32x4(f32x4 (&v)[32]) {
+// independent columns held as v[g][j] (Sylvester ordering, in place).
+template <typename V>
+__device__ __forceinline__ void fht32(V (&v)[32]) {
 #pragma unroll
     for (int h = 1; h < 32; h <<= 1) {
 #pragma unroll
         for (int g = 0; g < 32; ++g) {
             if (g & h) continue;
-            const f32x4 a = v[g];
-            const f32x4 b = v[g + h];
+            const V a = v[g];
+            const V b = v[g + h];
             v[g] = a + b;
             v[g + h] = a - b;
         }
         __builtin_amdgcn_sched_barrier(0);
     }
 }
+
+__device__ __forceinline__ void fht32x4(f32x4 (&v)[32]) { fht32<f32x4>(v); }
 
 struct HadArgs {
     const void *x;      // first row of this launch
@@ -97,12 +100,12 @@ template <> struct XM<true> { uint2 b[32]; };
 //   beta_l  [Nt][4][32]      beta[h, 16nt+4q .. +3]/32 (0 past out_o)
 template <bool BF16MMA> constexpr int lut_bytes() { return BF16MMA ? 256 * 8 : 256 * 16; }
 
-template <typename T, bool BF16MMA, bool VEC>
-__device__ __forceinline__ void load_transform(const HadArgs &a, __amdgpu_buffer_rsrc_t xr, uint32_t row_off,
-                                               bool row_ok, int c, int q, const f32x4 *__restrict__ alpha_l,
-                                               XM<BF16MMA> &out) {
+// The lane's 4 columns 16c+4q.. of all 32 groups of its row (zeros past
+// in_o / M).
+template <typename T, bool VEC>
+__device__ __forceinline__ void load_x(const HadArgs &a, __amdgpu_buffer_rsrc_t xr, uint32_t row_off, bool row_ok,
+                                       int c, int q, f32x4 (&v)[32]) {
     constexpr uint32_t esz = sizeof(T);
-    f32x4 v[32];
     const int i0 = kKChunk * c + 4 * q;
     const uint32_t gstride = (uint32_t)a.gsx * esz;
     if (VEC) {
@@ -118,6 +121,14 @@ __device__ __forceinline__ void load_transform(const HadArgs &a, __amdgpu_buffer
 #pragma unroll
             for (int j = 0; j < 4; ++j) v[g][j] = Buf4<T>::load1(xr, voff[j], (uint32_t)g * gstride);
     }
+}
+
+template <typename T, bool BF16MMA, bool VEC>
+__device__ __forceinline__ void load_transform(const HadArgs &a, __amdgpu_buffer_rsrc_t xr, uint32_t row_off,
+                                               bool row_ok, int c, int q, const f32x4 *__restrict__ alpha_l,
+                                               XM<BF16MMA> &out) {
+    f32x4 v[32];
+    load_x<T, VEC>(a, xr, row_off, row_ok, c, q, v);
     const f32x4 *al = alpha_l + (c * 4 + q) * 32;
 #pragma unroll
     for (int g = 0; g < 32; ++g) {
@@ -138,10 +149,8 @@ __device__ __forceinline__ void load_transform(const HadArgs &a, __amdgpu_buffer
 }
 
 template <bool BF16MMA>
-__device__ __forceinline__ void contract(const HadArgs &a, int nt, int c, int lane, const XM<BF16MMA> &xm,
-                                         const void *__restrict__ lut, f32x4 (&acc)[32]) {
-    const uint4 *src = (const uint4 *)(a.kw + (((int64_t)nt * a.Kc + c) * 64 + lane) * 32);
-    const uint4 w0 = src[0], w1 = src[1];
+__device__ __forceinline__ void contract_w(uint4 w0, uint4 w1, const XM<BF16MMA> &xm, const void *__restrict__ lut,
+                                           f32x4 (&acc)[32]) {
     const uint32_t wb[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
     for (int g = 0; g < 32; ++g) {
@@ -158,6 +167,21 @@ __device__ __forceinline__ void contract(const HadArgs &a, int nt, int c, int la
         }
         if ((g & 7) == 7) __builtin_amdgcn_sched_barrier(0);
     }
+}
+
+// The lane's 32 code bytes of weight tile (nt, c).
+__device__ __forceinline__ void load_w(const HadArgs &a, int nt, int c, int lane, uint4 &w0, uint4 &w1) {
+    const uint4 *src = (const uint4 *)(a.kw + (((int64_t)nt * a.Kc + c) * 64 + lane) * 32);
+    w0 = src[0];
+    w1 = src[1];
+}
+
+template <bool BF16MMA>
+__device__ __forceinline__ void contract(const HadArgs &a, int nt, int c, int lane, const XM<BF16MMA> &xm,
+                                         const void *__restrict__ lut, f32x4 (&acc)[32]) {
+    uint4 w0, w1;
+    load_w(a, nt, c, lane, w0, w1);
+    contract_w<BF16MMA>(w0, w1, xm, lut, acc);
 }
 
 template <typename T, bool VEC>
@@ -271,6 +295,152 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
                 transform_store<T, VEC>(a, acc, yr, yoff, row_ok, nt, q, beta_l);
             }
         }
+    }
+}
+
+// ---------------------------------------------------------------- wide layers
+// in_o > 16 with several output tiles (n_embd 4096: in_o = out_o = 128).  One
+// workgroup of 8 waves takes a (16-token tile, group of 8 output tiles): the
+// transformed input of up to S chunks of 16 columns is staged in LDS (wave w
+// transforms chunk s0 + w), then wave w contracts output tile nt0 + w over
+// the staged chunks, so the input transform is done once per workgroup
+// rather than once per output tile, and 8 waves share a token tile.
+constexpr int kWideWaves = 8;
+constexpr int kWideThreads = 64 * kWideWaves;
+template <bool BF16MMA> constexpr int wide_stage() { return BF16MMA ? 8 : 4; }
+template <bool BF16MMA> struct XElem;
+template <> struct XElem<true> { typedef uint2 type; };
+template <> struct XElem<false> { typedef f32x4 type; };
+
+template <bool BF16MMA> constexpr size_t wide_lds_bytes() {
+    return (size_t)lut_bytes<BF16MMA>() + (size_t)kWideWaves * 128 * 16 +
+           (size_t)wide_stage<BF16MMA>() * 32 * 64 * sizeof(typename XElem<BF16MMA>::type);
+}
+
+// alpha[g, i0], alpha[g, i0 + 1] (zeros past in_o); A2: in_o is even.
+template <bool A2>
+__device__ __forceinline__ f32x2 alpha2(const HadArgs &a, int g, int i0) {
+    const float *p = a.alpha + (int64_t)g * a.in_o + i0;
+    if (A2) return i0 < a.in_o ? *(const f32x2 *)p : f32x2{0.f, 0.f};
+    return f32x2{i0 < a.in_o ? p[0] : 0.f, i0 + 1 < a.in_o ? p[1] : 0.f};
+}
+
+template <typename T, bool BF16MMA, bool A4>
+__global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide_kernel(HadArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int S = wide_stage<BF16MMA>();
+    typedef typename XElem<BF16MMA>::type XE;
+    void *lut = smem;
+    f32x4 *beta_l = (f32x4 *)(smem + lut_bytes<BF16MMA>());  // [8 local tiles][4][32]
+    XE *xs = (XE *)(beta_l + kWideWaves * 128);             // [S][32 g][64 lanes]
+    constexpr uint32_t esz = sizeof(T);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane & 15, q = lane >> 4;
+    if (tid < 256) {
+        const uint32_t byte = (uint32_t)tid;
+        float val[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) val[j] = (float)((int)((byte >> (6 - 2 * j)) & 3u) - 1);
+        if constexpr (BF16MMA) {
+            ((uint2 *)lut)[byte] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
+        } else {
+            ((f32x4 *)lut)[byte] = f32x4{val[0], val[1], val[2], val[3]};
+        }
+    }
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * esz));
+    const int n_tiles = (int)ceil_div(a.M, kTile);
+    const int ngroups = (int)ceil_div(a.Nt, kWideWaves);
+    for (int item = blockIdx.x; item < n_tiles * ngroups; item += gridDim.x) {
+        const int tile = item / ngroups, nt0 = (item % ngroups) * kWideWaves, nt = nt0 + wave;
+        const int row = tile * kTile + t;
+        const bool row_ok = row < a.M;
+        const uint32_t xoff = (uint32_t)((int64_t)row * a.ldx * esz);
+        const uint32_t yoff = (uint32_t)((int64_t)row * a.ldy * esz);
+        __syncthreads();  // LUT ready / previous item done with beta_l and xs
+        for (int e = tid; e < kWideWaves * 128; e += kWideThreads) {
+            const int lw = e >> 7, h = e & 31, qq = (e >> 5) & 3;
+            const int o0 = kNTile * (nt0 + lw) + 4 * qq;
+            f32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = (o0 + j < a.out_o) ? a.beta[h * a.out_o + o0 + j] * 0.03125f : 0.f;
+            beta_l[e] = v;
+        }
+        f32x4 acc[32];
+#pragma unroll
+        for (int g = 0; g < 32; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < a.Kc; s0 += S) {
+            // transform chunk s0 + wave into LDS slot `wave`
+            if (wave < S && s0 + wave < a.Kc) {
+                // two passes of 2 columns keep the transform at 64 registers
+                // beside the 128 of accumulators
+                const int c = s0 + wave;
+                const int i0 = kKChunk * c + 4 * q;
+                const uint32_t gstride = (uint32_t)a.gsx * esz;
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const int ip = i0 + 2 * p;
+                    const uint32_t voff = (row_ok && ip < a.in_o) ? xoff + (uint32_t)ip * esz : kOOB;
+                    f32x2 v[32];
+#pragma unroll
+                    for (int g = 0; g < 32; ++g) {
+                        if constexpr (sizeof(T) == 2) {
+                            const uint32_t u = __builtin_amdgcn_raw_buffer_load_b32(xr, voff, (uint32_t)g * gstride, 0);
+                            v[g] = f32x2{__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u)};
+                        } else {
+                            v[g] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                                 xr, voff, (uint32_t)g * gstride, 0));
+                        }
+                    }
+#pragma unroll
+                    for (int g = 0; g < 32; ++g) {
+                        v[g] = v[g] * alpha2<A4>(a, g, ip);
+                        if ((g & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+                    }
+                    fht32<f32x2>(v);
+                    XE *dst = xs + (size_t)wave * 32 * 64 + lane;
+#pragma unroll
+                    for (int g = 0; g < 32; ++g) {
+                        if constexpr (BF16MMA)
+                            ((uint32_t *)&dst[g * 64])[p] = pack_bf16x2(v[g][0], v[g][1]);
+                        else
+                            ((f32x2 *)&dst[g * 64])[p] = v[g];
+                    }
+                }
+            }
+            __syncthreads();
+            if (nt < a.Nt) {
+                const int nc = a.Kc - s0 < S ? a.Kc - s0 : S;
+                uint4 w0, w1;
+                load_w(a, nt, s0, lane, w0, w1);
+                for (int j = 0; j < nc; ++j) {
+                    uint4 n0 = w0, n1 = w1;
+                    if (j + 1 < nc) load_w(a, nt, s0 + j + 1, lane, n0, n1);
+                    // staged operands are read group by group next to their products
+                    const XE *src = xs + (size_t)j * 32 * 64 + lane;
+                    const uint32_t wb[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                    for (int g = 0; g < 32; ++g) {
+                        const uint32_t byte = (wb[g >> 2] >> (8 * (g & 3))) & 0xffu;
+                        const XE xg = src[g * 64];
+                        if constexpr (BF16MMA) {
+                            const uint2 wa = ((const uint2 *)lut)[byte];
+                            acc[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                                __builtin_bit_cast(i16x4, wa), __builtin_bit_cast(i16x4, xg), acc[g], 0, 0, 0);
+                        } else {
+                            const f32x4 wa = ((const f32x4 *)lut)[byte];
+#pragma unroll
+                            for (int u = 0; u < 4; ++u)
+                                acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[u], xg[u], acc[g], 0, 0, 0);
+                        }
+                        if ((g & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+                    }
+                    w0 = n0;
+                    w1 = n1;
+                }
+            }
+            __syncthreads();
+        }
+        if (nt < a.Nt) transform_store<T, true>(a, acc, yr, yoff, row_ok, nt, q, beta_l + (wave - nt) * 128);
     }
 }
 
@@ -532,6 +702,9 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
     // float32 operands keep 128 registers of transformed input; with several
     // output tiles they are recomputed per tile instead of kept live.
     const bool kc1 = Kc == 1 && (bf16 || Nt == 1);
+    // several input chunks and output tiles: the workgroup-wide kernel
+    const size_t wide_lds = bf16 ? wide_lds_bytes<true>() : wide_lds_bytes<false>();
+    const bool wide = !swiglu && vec && Kc >= 2 && Nt >= 4 && wide_lds <= (size_t)device_info().max_shared_per_block;
     const int64_t ld = base.ldx > base.ldy ? base.ldx : base.ldy;
     int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz);
     rows_max = rows_max / kTile * kTile;
@@ -562,6 +735,18 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
                 else     { if (one) WALSH_SW_LAUNCH(float, false, false, true); else WALSH_SW_LAUNCH(float, false, false, false); }
             }
 #undef WALSH_SW_LAUNCH
+        } else if (wide) {
+            const int64_t items = ceil_div(rows, kTile) * ceil_div(Nt, kWideWaves);
+            const int64_t wcap = (int64_t)device_info().cu_count;
+            const dim3 GW((unsigned)(items < wcap ? items : wcap)), BW(kWideThreads);
+            const bool a4 = base.in_o % 2 == 0;
+            if (bf16) {
+                if (a4) launch((hadamard_wide_kernel<uint16_t, true, true>), GW, BW, wide_lds, s, a);
+                else launch((hadamard_wide_kernel<uint16_t, true, false>), GW, BW, wide_lds, s, a);
+            } else {
+                if (a4) launch((hadamard_wide_kernel<float, false, true>), GW, BW, wide_lds, s, a);
+                else launch((hadamard_wide_kernel<float, false, false>), GW, BW, wide_lds, s, a);
+            }
         } else {
 #define WALSH_HAD_LAUNCH(T, MMA, V, K1) launch((hadamard_fwd_kernel<T, MMA, V, K1>), G, B, lds, s, a)
             if (bf16) {
