@@ -7,6 +7,8 @@
 //   walsh_mhc_post_fwd  x_new = H_res @ x + H_post^T (x) out (mhc.py:366-381)
 //
 // Stream tensors are [M tokens][n streams][C] (row stride ldx >= n*C).
+#include <type_traits>
+
 #include "common.h"
 
 namespace walsh {
@@ -299,6 +301,7 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     float *part = (float *)(smem + TT * stride);              // [4][TT][33]
     float *ssp = part + kPreWaves * TT * (kPhiRows + 1);     // [4][TT]
     float *hpre = ssp + kPreWaves * TT;                      // [TT][4]
+    f32x4 *nw_l = (f32x4 *)(hpre + TT * 4);                  // [C/4]
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tok0 = blockIdx.x * TT;
@@ -311,17 +314,27 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     const int ks0 = wave * ks_per, ks1 = min(nks, ks0 + ks_per);
     const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.phi_frag, (uint32_t)((int64_t)nks * 2 * 64 * 4 * esz));
     constexpr int kPf = 8;                    // K steps of phi per batch
-    f32x4 pa[kPf][2], pbb[kPf][2];            // ping-pong buffers (static indexing keeps them in VGPRs)
-    auto load_phi = [&](int kb, f32x4 (&dst)[kPf][2]) {
+    // phi fragments stay in the operand format: 4 bf16 (8 bytes) or 4 f32
+    typedef typename std::conditional<BF16MMA, u32x2, f32x4>::type PhiT;
+    PhiT pa[kPf][2], pbb[kPf][2];             // ping-pong buffers (static indexing keeps them in VGPRs)
+    auto load_phi = [&](int kb, PhiT (&dst)[kPf][2]) {
 #pragma unroll
         for (int u = 0; u < kPf; ++u)
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 const int ks = kb + u;
-                dst[u][nt] = Buf4<T>::load(
-                    pr, ks < ks1 ? (uint32_t)((((int64_t)ks * 2 + nt) * 64 + lane) * 4 * esz) : kOOB, 0);
+                const uint32_t off = ks < ks1 ? (uint32_t)((((int64_t)ks * 2 + nt) * 64 + lane) * 4 * esz) : kOOB;
+                if constexpr (BF16MMA)
+                    dst[u][nt] = __builtin_amdgcn_raw_buffer_load_b64(pr, off, 0, 0);
+                else
+                    dst[u][nt] = Buf4<T>::load(pr, off, 0);
             }
     };
+    constexpr int kTpt = kPreThreads / TT;    // threads per token in phase 3
+    constexpr int kMaxQ = 1024 / 4 / kTpt;    // C <= 1024
+    // the norm weights (or ones) go to LDS with the tile
+    for (int c4 = tid; c4 < C / 4; c4 += kPreThreads)
+        nw_l[c4] = a.norm_w ? *(const f32x4 *)(a.norm_w + 4 * c4) : f32x4{1.f, 1.f, 1.f, 1.f};
 
     // phase 0: tile -> LDS, all 16-byte loads in flight together
     {
@@ -354,27 +367,31 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     __syncthreads();
 
     // phase 1: projection on matrix cores, K split over the 4 wavefronts
-    f32x4 acc[MT][2];
+    f32x4 acc[MT][2], accss[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < MT; ++i) acc[i][0] = acc[i][1] = accss[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float ss[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) ss[i] = 0.f;
-    auto compute = [&](int kb, const f32x4 (&p)[kPf][2]) {
+    auto compute = [&](int kb, const PhiT (&p)[kPf][2]) {
 #pragma unroll
         for (int u = 0; u < kPf; ++u) {
             const int ks = kb + u;
             if (ks >= ks1) break;
             const int k = ks * 16 + 4 * kq;
-            uint2 bv[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                bv[nt].x = pack_bf16x2(p[u][nt].x, p[u][nt].y);
-                bv[nt].y = pack_bf16x2(p[u][nt].z, p[u][nt].w);
-            }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const unsigned char *src = xs + (16 * mt + m) * stride + k * esz;
+                if constexpr (BF16MMA) {
+                    // raw bf16 operands; the sum of squares is the diagonal of x x^T
+                    const i16x4 xr4 = __builtin_bit_cast(i16x4, *(const u32x2 *)src);
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                            xr4, __builtin_bit_cast(i16x4, p[u][nt]), acc[mt][nt], 0, 0, 0);
+                    accss[mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(xr4, xr4, accss[mt], 0, 0, 0);
+                    continue;
+                }
                 f32x4 xa;
                 if constexpr (sizeof(T) == 2) {
                     const u32x2 u2 = *(const u32x2 *)src;
@@ -387,20 +404,13 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
                     xa = __builtin_bit_cast(f32x4, u32x4{lo.x, lo.y, hi.x, hi.y});
                 }
                 ss[mt] += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w;
+                if constexpr (!BF16MMA) {
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    if constexpr (BF16MMA) {
-                        uint2 av;
-                        av.x = pack_bf16x2(xa.x, xa.y);
-                        av.y = pack_bf16x2(xa.z, xa.w);
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-                            __builtin_bit_cast(i16x4, av), __builtin_bit_cast(i16x4, bv[nt]), acc[mt][nt], 0, 0, 0);
-                    } else {
+                    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                         for (int s2 = 0; s2 < 4; ++s2)
                             acc[mt][nt] =
                                 __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s2], p[u][nt][s2], acc[mt][nt], 0, 0, 0);
-                    }
                 }
             }
         }
@@ -415,9 +425,15 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        ss[mt] += __shfl_xor(ss[mt], 16);
-        ss[mt] += __shfl_xor(ss[mt], 32);
-        if (kq == 0) ssp[wave * TT + 16 * mt + m] = ss[mt];
+        if constexpr (BF16MMA) {
+            // lane (n = m, q = kq) holds rows 4kq..4kq+3 of column m of x x^T
+            const int j = m - 4 * kq;
+            if (j >= 0 && j < 4) ssp[wave * TT + 16 * mt + m] = accss[mt][j];
+        } else {
+            ss[mt] += __shfl_xor(ss[mt], 16);
+            ss[mt] += __shfl_xor(ss[mt], 32);
+            if (kq == 0) ssp[wave * TT + 16 * mt + m] = ss[mt];
+        }
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
@@ -444,64 +460,57 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     }
     __syncthreads();
 
-    // phase 3: layer_in = sum_s H_pre[s] x[s, :] (8 threads per token, 4 values per
-    // item), optional RMS normalisation over the row with weight norm_w
+    // phase 3: layer_in = sum_s H_pre[s] x[s, :] (kTpt threads per token, 4
+    // values per item), optional RMS normalisation over the row with weight norm_w
     {
-        const int t = tid >> 3, sub = tid & 7;
+        const int tt = tid / kTpt, sub = tid % kTpt;
         const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
-        constexpr int kMaxQ = 1024 / 4 / 8;   // C <= 1024: at most 32 quads per thread
-        for (int tb = 0; tb < TT; tb += kPreThreads / 8) {
-            const int tt = tb + t;
-            if (tt >= TT) continue;           // whole 8-lane groups skip together
-            const int tok = tok0 + tt;
-            const int nq = C / 4;
-            f32x4 v[kMaxQ];
-            float sq = 0.f;
-            float hp[kMaxStreams];
+        const int tok = tok0 + tt;
+        const int nq = C / 4;
+        f32x4 v[kMaxQ];
+        float sq = 0.f;
+        float hp[kMaxStreams];
 #pragma unroll
-            for (int s = 0; s < kMaxStreams; ++s) hp[s] = hpre[tt * 4 + s];
+        for (int s = 0; s < kMaxStreams; ++s) hp[s] = hpre[tt * 4 + s];
 #pragma unroll
-            for (int j = 0; j < kMaxQ; ++j) {
-                const int q = sub + 8 * j;
-                f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
-                if (q < nq) {
+        for (int j = 0; j < kMaxQ; ++j) {
+            const int q = sub + kTpt * j;
+            f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
+            if (q < nq) {
 #pragma unroll
-                    for (int s = 0; s < kMaxStreams; ++s) {
-                        if (s >= n) continue;
-                        const unsigned char *src = xs + tt * stride + (s * C + 4 * q) * esz;
-                        f32x4 xv;
-                        if constexpr (sizeof(T) == 2) {
-                            const u32x2 u2 = *(const u32x2 *)src;
-                            xv.x = __uint_as_float(u2.x << 16);
-                            xv.y = __uint_as_float(u2.x & 0xffff0000u);
-                            xv.z = __uint_as_float(u2.y << 16);
-                            xv.w = __uint_as_float(u2.y & 0xffff0000u);
-                        } else {
-                            const u32x2 lo = *(const u32x2 *)src, hi = *(const u32x2 *)(src + 8);
-                            xv = __builtin_bit_cast(f32x4, u32x4{lo.x, lo.y, hi.x, hi.y});
-                        }
-                        acc4 += hp[s] * xv;
+                for (int s = 0; s < kMaxStreams; ++s) {
+                    if (s >= n) continue;
+                    const unsigned char *src = xs + tt * stride + (s * C + 4 * q) * esz;
+                    f32x4 xv;
+                    if constexpr (sizeof(T) == 2) {
+                        const u32x2 u2 = *(const u32x2 *)src;
+                        xv.x = __uint_as_float(u2.x << 16);
+                        xv.y = __uint_as_float(u2.x & 0xffff0000u);
+                        xv.z = __uint_as_float(u2.y << 16);
+                        xv.w = __uint_as_float(u2.y & 0xffff0000u);
+                    } else {
+                        const u32x2 lo = *(const u32x2 *)src, hi = *(const u32x2 *)(src + 8);
+                        xv = __builtin_bit_cast(f32x4, u32x4{lo.x, lo.y, hi.x, hi.y});
                     }
+                    acc4 += hp[s] * xv;
                 }
-                v[j] = acc4;
-                sq += acc4.x * acc4.x + acc4.y * acc4.y + acc4.z * acc4.z + acc4.w * acc4.w;
             }
-            float scale = 1.f;
-            if (a.norm_w) {
-                sq += __shfl_xor(sq, 1);
-                sq += __shfl_xor(sq, 2);
-                sq += __shfl_xor(sq, 4);
-                scale = 1.0f / sqrtf(__fdiv_rn(sq, (float)C) + a.norm_eps);
-            }
-            const bool ok = tok < a.M;
+            v[j] = acc4;
+            sq += acc4.x * acc4.x + acc4.y * acc4.y + acc4.z * acc4.z + acc4.w * acc4.w;
+        }
+        float scale = 1.f;
+        if (a.norm_w) {
 #pragma unroll
-            for (int j = 0; j < kMaxQ; ++j) {
-                const int q = sub + 8 * j;
-                if (q >= nq) continue;
-                f32x4 o = v[j] * scale;
-                if (a.norm_w) o *= *(const f32x4 *)(a.norm_w + 4 * q);
-                Buf4<T>::store(o, lr, ok ? (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz) : kOOB, 0);
-            }
+            for (int sh = 1; sh < kTpt; sh <<= 1) sq += __shfl_xor(sq, sh);
+            scale = 1.0f / sqrtf(__fdiv_rn(sq, (float)C) + a.norm_eps);
+        }
+        const bool ok = tok < a.M;
+#pragma unroll
+        for (int j = 0; j < kMaxQ; ++j) {
+            const int q = sub + kTpt * j;
+            if (q >= nq) continue;
+            const f32x4 o = v[j] * scale * nw_l[q];
+            Buf4<T>::store(o, lr, ok ? (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz) : kOOB, 0);
         }
     }
 }
@@ -687,7 +696,7 @@ WALSH_EXPORT int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, i
     const int MT = 1;
     const int TT = 16 * MT;
     const size_t lds = (size_t)TT * (rowb + 8) + (size_t)kPreWaves * TT * (kPhiRows + 1) * 4 + kPreWaves * TT * 4 +
-                       TT * 16;
+                       TT * 16 + (size_t)C * 4;
     if (lds > (size_t)device_info().max_shared_per_block)
         return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: needs %zu B of LDS", lds);
     const int64_t ld = ldx > ld_in ? ldx : ld_in;
