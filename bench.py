@@ -456,19 +456,34 @@ def bench_decode5(torch, args):
     for b in (1, 16, 64):
         idx = torch.randint(0, cfg.vocab_size, (b, 1), generator=torch.Generator().manual_seed(b)).cuda()
 
-        def step(i):
+        def eager(i=0):
             kv.cached_len = kv_len   # synthetic cache content; every step decodes position kv_len
             with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
                 return model(idx, kv_cache=kv, start_pos=kv_len)[0]
         steps = max(args.steps, 10)
-        dt = _time_steps(torch, step, steps, args.warmup)
+        dt_eager = _time_steps(torch, eager, steps, args.warmup)
         with _hip.LaunchTimer() as lt:
             for i in range(steps):
-                step(i)
+                eager(i)
         k = lt.summary()
         hot_ms = sum(v["ms"] for v in k.values()) / steps
+        # the step as one HIP graph: removes the per-launch host cost of the
+        # ~40 launches per layer (the eager step is launch-bound at small batch)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                eager()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            eager()
+        dt = _time_steps(torch, lambda i: graph.replay(), steps, args.warmup)
+        del graph
         sweep.append(dict(batch=b, ms_per_step=round(dt * 1e3, 3), tokens_per_s=round(b / dt, 1),
-                          hot_path_kernel_ms_per_step=round(hot_ms, 3)))
+                          eager_ms_per_step=round(dt_eager * 1e3, 3),
+                          hot_path_kernel_ms_per_step=round(hot_ms, 3),
+                          kernels={n: round(v["ms"] * 1000 / v["launches"], 2) for n, v in k.items()}))
         if b == bmax:
             roof = _roofline_of(k, steps)
             dt64 = dt

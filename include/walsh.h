@@ -209,6 +209,21 @@ int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int
                            float *h_pre, float *h_post, float *h_res, void *layer_in, int64_t ld_in,
                            const float *norm_w, float norm_eps, int dtype, void *stream);
 
+/* walsh_mhc_pre_wide_fwd: the same results as walsh_mhc_pre_norm_fwd for
+ *   rows too long for an LDS tile (n*C % 32 == 0, C <= 4096; n_embd 4096),
+ *   in two launches: a split-K projection on 16x16x32 matrix cores writing
+ *   partial sums to `workspace`, then per token the constraints and
+ *   layer_in (with its RMSNorm when norm_w is given).  phi_frag32 is the
+ *   [32, n*C] projection in fragment order [n*C/32][2][64][8] (lane
+ *   16*kq + r holds phi[16*tile + r][32*ks + 8*kq .. +7]).  workspace:
+ *   device memory of at least walsh_mhc_pre_wide_workspace(M, n, C) bytes. */
+int64_t walsh_mhc_pre_wide_workspace(int64_t M, int64_t n, int64_t C);
+int walsh_mhc_pre_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C, const void *phi_frag32,
+                           const float *coef, const float *bias, float rms_eps, int64_t n_iter, float sk_eps,
+                           float *h_pre, float *h_post, float *h_res, void *layer_in, int64_t ld_in,
+                           const float *norm_w, float norm_eps, void *workspace, int64_t workspace_bytes, int dtype,
+                           void *stream);
+
 /* walsh_mhc_post_fwd: x_new = H_res @ x + H_post^T (x) out
  *   (src/model/mhc.py:366-381).  out [M, C] row stride ld_out; x_new may not
  *   alias x. */

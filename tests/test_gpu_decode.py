@@ -76,3 +76,41 @@ def test_config5_layer_fp32_vs_oracle():
     r = rel(logits.cpu(), ref_logits)
     print(f"config-5 layer logits rel={r}")
     assert max(r) <= 1e-5
+
+
+@pytest.mark.parametrize("C,use_moe", [(512, True), (4096, True)])
+def test_decode_step_hip_graph_replays_match_eager(C, use_moe):
+    """One decode step captured as a HIP graph (how the decode benchmark runs
+    it): every replay, with eager work and synchronisation in between, equals
+    the eager step."""
+    from src.model import KVCache
+    n_layer = 2 if C == 512 else 1
+    cfg, model = make(C, n_layer, 32, use_moe, block=64, seed=11)
+    B, pos = 4, 16
+    kv = KVCache(n_layer, cfg.block_size, 32, C // 32, torch.device("cuda"), dtype=torch.bfloat16, batch=B)
+    gen = torch.Generator().manual_seed(5)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        model(torch.randint(0, cfg.vocab_size, (B, pos), generator=gen).cuda(), kv_cache=kv, start_pos=0)
+    idx = torch.randint(0, cfg.vocab_size, (B, 1), generator=gen).cuda()
+
+    def step():
+        kv.cached_len = pos
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return model(idx, kv_cache=kv, start_pos=pos)[0]
+    eager = step().float().clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = step()
+    for r in range(3):
+        junk = torch.randn(1024, 1024, device="cuda") @ torch.randn(1024, 1024, device="cuda")  # eager work between
+        g.replay()
+        torch.cuda.synchronize()
+        diff = (out.float() - eager).abs().max().item()
+        print(f"replay {r}: max |graph - eager| = {diff:.3e} (junk {junk.norm().item():.1f})")
+        assert torch.equal(out.float(), eager)

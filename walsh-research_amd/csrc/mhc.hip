@@ -515,6 +515,208 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     }
 }
 
+// ---------------------------------------------------------------- pre, wide rows
+// ResidualStreamMapping x3 + H_pre @ x (+ the block's RMSNorm) for rows too
+// long for an LDS tile (n*C up to 16384: n_embd 4096), in two launches:
+//   mhc_proj_kernel   one wavefront per (16-token tile, K split): streams the
+//                     rows through 16x16x32 matrix-core steps against the
+//                     projection (phi fragments [K/32][2][64][8]) and the
+//                     x x^T diagonal (sum of squares); writes partial sums
+//                     [split][M][25] (24 projections + sum of squares);
+//   mhc_apply_kernel  one wavefront per token: sums the splits, RMS scale,
+//                     the constraints (4-lane Sinkhorn), then layer_in =
+//                     sum_s H_pre[s] x[s, :] with its RMS norm over C.
+// Small batches (decode) split K across many wavefronts; prefill uses one
+// split, so each row is read twice (projection, apply).
+constexpr int kProjOut = kPhiRows - 8 + 1;  // 24 projection outputs + sum of squares
+
+struct ProjArgs {
+    const void *x;
+    int64_t ldx;
+    int M, K, splits, kper;   // kper: K per split (multiple of 32)
+    const void *phi32;        // [K/32][2][64][8] activation dtype
+    float *part;              // [splits][M][25]
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void mhc_proj_kernel(ProjArgs a) {
+    constexpr uint32_t esz = sizeof(T);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+    const int n_tiles = (int)ceil_div(a.M, 16);
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= n_tiles * a.splits) return;
+    const int tile = item / a.splits, split = item % a.splits;
+    const int k0 = split * a.kper, k1 = min(a.K, k0 + a.kper);
+    const int tok = tile * 16 + m;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.phi32, (uint32_t)((int64_t)a.K * 32 * esz));
+    const uint32_t xrow = tok < a.M ? (uint32_t)((int64_t)tok * a.ldx * esz) : kOOB;
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, accss = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (sizeof(T) == 2) {
+        // batches of kU steps: all loads of a batch are issued before its products
+        constexpr int kU = 8;
+        for (int kb = k0; kb < k1; kb += 32 * kU) {
+            u32x4 xv[kU], pv[kU][2];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int k = kb + 32 * u;
+                const bool ok = k < k1;
+                const uint32_t xo = (xrow == kOOB || !ok) ? kOOB : xrow + (uint32_t)(k + 8 * kq) * esz;
+                xv[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    const uint32_t po =
+                        ok ? (uint32_t)((((int64_t)(k / 32) * 2 + nt) * 64 + lane) * 8 * esz) : kOOB;
+                    pv[u][nt] = __builtin_amdgcn_raw_buffer_load_b128(pr, po, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const bf16x8 x8 = __builtin_bit_cast(bf16x8, xv[u]);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, __builtin_bit_cast(bf16x8, pv[u][nt]),
+                                                                      acc[nt], 0, 0, 0);
+                accss = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, x8, accss, 0, 0, 0);
+            }
+        }
+    } else
+    for (int k = k0; k < k1; k += 32) {
+        const uint32_t xo = xrow == kOOB ? kOOB : xrow + (uint32_t)(k + 8 * kq) * esz;
+        const uint32_t po = (uint32_t)(((int64_t)(k / 32) * 2 * 64 + lane) * 8 * esz);
+        {
+            const f32x4 x0 = Buf4<float>::load(xr, xo, 0), x1 = Buf4<float>::load(xr, xo, 16);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint32_t pn = po + (uint32_t)nt * 64 * 8 * esz;
+                const f32x4 p0 = Buf4<float>::load(pr, pn, 0), p1 = Buf4<float>::load(pr, pn, 16);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(x0[u], p0[u], acc[nt], 0, 0, 0);
+                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(x1[u], p1[u], acc[nt], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                accss = __builtin_amdgcn_mfma_f32_16x16x4f32(x0[u], x0[u], accss, 0, 0, 0);
+                accss = __builtin_amdgcn_mfma_f32_16x16x4f32(x1[u], x1[u], accss, 0, 0, 0);
+            }
+        }
+    }
+    // lane (n = m, q = kq) holds rows 4kq..4kq+3 (tokens) of column m (output)
+    float *dst = a.part + (int64_t)split * a.M * kProjOut;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const int o = 16 * nt + m;
+        if (o >= kProjOut - 1) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = tile * 16 + 4 * kq + j;
+            if (t < a.M) dst[(int64_t)t * kProjOut + o] = acc[nt][j];
+        }
+    }
+    const int j = m - 4 * kq;
+    if (j >= 0 && j < 4 && tile * 16 + m < a.M) dst[(int64_t)(tile * 16 + m) * kProjOut + kProjOut - 1] = accss[j];
+}
+
+struct ApplyArgs {
+    const void *x;
+    int64_t ldx;
+    int M, n, C, splits;
+    const float *part;        // [splits][M][25]
+    const float *coef, *bias;
+    float rms_eps, sk_eps;
+    int n_iter;
+    float *h_pre, *h_post, *h_res;
+    void *layer_in;
+    int64_t ld_in;
+    const float *norm_w;
+    float norm_eps;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void mhc_apply_kernel(ApplyArgs a) {
+    constexpr uint32_t esz = sizeof(T);
+    constexpr int kMaxQ = 16;                 // C <= 4096: 16 quads per lane
+    __shared__ float dyn_s[4][kProjOut + 7];
+    __shared__ float hpre_s[4][4];
+    __shared__ float red_s[4][64][kProjOut];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tok = blockIdx.x * 4 + wave;
+    const bool live = tok < a.M;
+    const int n = a.n, C = a.C, K = n * C;
+    // sum the K splits: lane l loads splits l, l+64, ... (all loads in flight
+    // together), then lane o < 25 adds the 64 lane sums from LDS in lane order
+    {
+        float v[kProjOut];
+#pragma unroll
+        for (int o = 0; o < kProjOut; ++o) v[o] = 0.f;
+        if (live)
+            for (int sp = lane; sp < a.splits; sp += 64) {
+                const float *src = a.part + ((int64_t)sp * a.M + tok) * kProjOut;
+#pragma unroll
+                for (int o = 0; o < kProjOut; ++o) v[o] += src[o];
+            }
+#pragma unroll
+        for (int o = 0; o < kProjOut; ++o) red_s[wave][lane][o] = v[o];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < kProjOut) {
+        const int nl = a.splits < 64 ? a.splits : 64;
+        float v = 0.f;
+        for (int l = 0; l < nl; ++l) v += red_s[wave][l][lane];
+        dyn_s[wave][lane] = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < 4) {
+        const float rs = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(dyn_s[wave][kProjOut - 1], (float)K) + a.rms_eps));
+        auto dynf = [&](int o) { return dyn_s[wave][o] * rs; };
+        token_constraints_quad(wave, lane, live ? tok : a.M, a.M, n, a.coef, a.bias, a.n_iter, a.sk_eps, dynf,
+                               &hpre_s[0][0], a.h_pre, a.h_post, a.h_res);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (!live) return;
+    float hp[kMaxStreams];
+#pragma unroll
+    for (int s = 0; s < kMaxStreams; ++s) hp[s] = hpre_s[wave][s];
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
+    const uint32_t xrow = (uint32_t)((int64_t)tok * a.ldx * esz);
+    const int nq = C / 4;
+    f32x4 v[kMaxQ];
+    float sq = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxQ; ++j) {
+        const int q = lane + 64 * j;
+        f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < kMaxStreams; ++s)
+            if (s < n) acc4 += hp[s] * Buf4<T>::load(xr, q < nq ? xrow + (uint32_t)(s * C + 4 * q) * esz : kOOB, 0);
+        v[j] = acc4;
+        sq += acc4.x * acc4.x + acc4.y * acc4.y + acc4.z * acc4.z + acc4.w * acc4.w;
+    }
+    float scale = 1.f;
+    if (a.norm_w) {
+#pragma unroll
+        for (int sh = 1; sh < 64; sh <<= 1) sq += __shfl_xor(sq, sh);
+        scale = 1.0f / sqrtf(__fdiv_rn(sq, (float)C) + a.norm_eps);
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxQ; ++j) {
+        const int q = lane + 64 * j;
+        if (q >= nq) continue;
+        f32x4 o = v[j] * scale;
+        if (a.norm_w) o *= *(const f32x4 *)(a.norm_w + 4 * q);
+        Buf4<T>::store(o, lr, (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz), 0);
+    }
+}
+
 // ---------------------------------------------------------------- post (apply)
 // x_new[t, r, :] = sum_s H_res[t, r, s] x[t, s, :] + H_post[t, r] out[t, :]
 template <typename T>
@@ -733,6 +935,95 @@ WALSH_EXPORT int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, i
             else launch((mhc_pre2_kernel<float, false, 1>), G, B, lds, s, a);
         }
         const int rc = check_hip(hipGetLastError(), "walsh_mhc_pre_norm_fwd launch");
+        if (rc) return rc;
+    }
+    return WALSH_OK;
+}
+
+// Splits of K for the wide-row projection: enough wavefronts to fill the
+// chip when there are few tokens (decode), one split otherwise.
+static int mhc_wide_splits(int64_t M, int64_t K) {
+    const int64_t tiles = ceil_div(M, 16);
+    const int64_t want = (int64_t)device_info().cu_count * 8;
+    int64_t s = tiles >= want ? 1 : ceil_div(want, tiles);
+    const int64_t smax = K / 256;             // at least 256 columns per split
+    if (s > smax) s = smax;
+    return (int)(s < 1 ? 1 : s);
+}
+
+WALSH_EXPORT int64_t walsh_mhc_pre_wide_workspace(int64_t M, int64_t n, int64_t C) {
+    if (M < 0 || n < 1 || C < 1) return 0;
+    return (int64_t)mhc_wide_splits(M, n * C) * M * kProjOut * 4;
+}
+
+WALSH_EXPORT int walsh_mhc_pre_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C,
+                                        const void *phi_frag32, const float *coef, const float *bias, float rms_eps,
+                                        int64_t n_iter, float sk_eps, float *h_pre, float *h_post, float *h_res,
+                                        void *layer_in, int64_t ld_in, const float *norm_w, float norm_eps,
+                                        void *workspace, int64_t workspace_bytes, int dtype, void *stream) {
+    const char *fn = "walsh_mhc_pre_wide_fwd";
+    if (!x || !phi_frag32 || !coef || !bias || !h_pre || !h_post || !h_res || !layer_in)
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (M < 0 || n < 1 || C < 4 || ldx < n * C || ld_in < C || n_iter < 0)
+        return set_error(WALSH_EINVAL, "%s: bad shape M=%lld n=%lld C=%lld", fn, (long long)M, (long long)n,
+                         (long long)C);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype", fn);
+    const int64_t esz = dtype == WALSH_BF16 ? 2 : 4, K = n * C;
+    if (n > kMaxStreams || K % 32 || C % 4 || C > 4096 || ldx % (32 / esz) || ld_in % 4)
+        return set_error(WALSH_ENOTSUP, "%s: needs n <= %d, n*C %% 32 == 0, C <= 4096", fn, kMaxStreams);
+    if ((uintptr_t)x % 16 || (uintptr_t)layer_in % 16 || (uintptr_t)phi_frag32 % 16 ||
+        (norm_w && (uintptr_t)norm_w % 16))
+        return set_error(WALSH_ENOTSUP, "%s: pointers must be 16-byte aligned", fn);
+    if (M == 0) return WALSH_OK;
+    const int splits = mhc_wide_splits(M, K);
+    const int64_t need = (int64_t)splits * M * kProjOut * 4;
+    if (!workspace || workspace_bytes < need)
+        return set_error(WALSH_EINVAL, "%s: workspace of %lld bytes needed", fn, (long long)need);
+    // row chunks keep every buffer below 2^31 bytes
+    const int64_t ld = ldx > ld_in ? ldx : ld_in;
+    const int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / 16 * 16;
+    if (rows_max < 16) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
+    hipStream_t s = (hipStream_t)stream;
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        const void *xc = (const char *)x + r0 * ldx * esz;
+        ProjArgs pa;
+        pa.x = xc;
+        pa.ldx = ldx;
+        pa.M = (int)rows;
+        pa.K = (int)K;
+        pa.splits = splits;
+        pa.kper = (int)(ceil_div(ceil_div(K, splits), 32) * 32);
+        pa.phi32 = phi_frag32;
+        pa.part = (float *)workspace;
+        const int64_t items = ceil_div(rows, 16) * splits;
+        const dim3 G1((unsigned)ceil_div(items, 4)), B(256);
+        if (dtype == WALSH_BF16) launch(mhc_proj_kernel<uint16_t>, G1, B, 0, s, pa);
+        else launch(mhc_proj_kernel<float>, G1, B, 0, s, pa);
+        ApplyArgs aa;
+        aa.x = xc;
+        aa.ldx = ldx;
+        aa.M = (int)rows;
+        aa.n = (int)n;
+        aa.C = (int)C;
+        aa.splits = splits;
+        aa.part = (const float *)workspace;
+        aa.coef = coef;
+        aa.bias = bias;
+        aa.rms_eps = rms_eps;
+        aa.sk_eps = sk_eps;
+        aa.n_iter = (int)n_iter;
+        aa.h_pre = h_pre + r0 * n;
+        aa.h_post = h_post + r0 * n;
+        aa.h_res = h_res + r0 * n * n;
+        aa.layer_in = (char *)layer_in + r0 * ld_in * esz;
+        aa.ld_in = ld_in;
+        aa.norm_w = norm_w;
+        aa.norm_eps = norm_eps;
+        const dim3 G2((unsigned)ceil_div(rows, 4));
+        if (dtype == WALSH_BF16) launch(mhc_apply_kernel<uint16_t>, G2, B, 0, s, aa);
+        else launch(mhc_apply_kernel<float>, G2, B, 0, s, aa);
+        const int rc = check_hip(hipGetLastError(), fn);
         if (rc) return rc;
     }
     return WALSH_OK;

@@ -17,6 +17,7 @@ WALSH_BF16 = 1
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
+_F = ctypes.c_float
 _I = ctypes.c_int
 
 # name -> (restype, argtypes); mirrors include/walsh.h
@@ -46,6 +47,9 @@ SIGNATURES = {
     "walsh_mhc_pre_norm_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float, _I64, ctypes.c_float,
                                     _P, _P, _P, _P, _I64, _P, ctypes.c_float, _I, _P]),
     "walsh_mhc_post_fwd": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P]),
+    "walsh_mhc_pre_wide_workspace": (_I64, [_I64, _I64, _I64]),
+    "walsh_mhc_pre_wide_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _I64, _F, _P, _P, _P, _P, _I64, _P, _F,
+                                    _P, _I64, _I, _P]),
     "walsh_moe_route_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64,
                                  _P, _I64, _I, _I, _P]),
     "walsh_moe_topk_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),

@@ -83,8 +83,9 @@ class RMSNorm(nn.Module):
 
 class KVCache:
     """Per-layer K/V cache (chassis.py:262-330), extended to a batch
-    dimension: tensors [batch, max_seq_len, n_head, head_dim] (batch=1 is the
-    reference's layout with the batch axis kept)."""
+    dimension.  Storage is [batch, n_head, max_seq_len, head_dim] so that the
+    attention reads each head's keys contiguously; ``update`` returns the
+    reference's [batch, total_len, n_head, head_dim] view of it."""
 
     def __init__(self, n_layers: int, max_seq_len: int, n_head: int, head_dim: int,
                  device: torch.device, dtype: torch.dtype = torch.bfloat16, batch: int = 1):
@@ -94,9 +95,9 @@ class KVCache:
         self.head_dim = head_dim
         self.batch = batch
         self.k_cache: List[torch.Tensor] = [
-            torch.zeros(batch, max_seq_len, n_head, head_dim, device=device, dtype=dtype) for _ in range(n_layers)]
+            torch.zeros(batch, n_head, max_seq_len, head_dim, device=device, dtype=dtype) for _ in range(n_layers)]
         self.v_cache: List[torch.Tensor] = [
-            torch.zeros(batch, max_seq_len, n_head, head_dim, device=device, dtype=dtype) for _ in range(n_layers)]
+            torch.zeros(batch, n_head, max_seq_len, head_dim, device=device, dtype=dtype) for _ in range(n_layers)]
         self.cached_len = 0
 
     def update(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -104,9 +105,11 @@ class KVCache:
         assert b <= self.batch, f"batch {b} exceeds cache batch {self.batch}"
         s, e = self.cached_len, self.cached_len + new_len
         assert e <= self.max_seq_len, "KV cache overflow"
-        self.k_cache[layer_idx][:b, s:e] = k.to(self.k_cache[layer_idx].dtype)
-        self.v_cache[layer_idx][:b, s:e] = v.to(self.v_cache[layer_idx].dtype)
-        return self.k_cache[layer_idx][:b, :e], self.v_cache[layer_idx][:b, :e]
+        kc = self.k_cache[layer_idx].transpose(1, 2)   # [batch, max_seq_len, n_head, head_dim] view
+        vc = self.v_cache[layer_idx].transpose(1, 2)
+        kc[:b, s:e] = k.to(kc.dtype)
+        vc[:b, s:e] = v.to(vc.dtype)
+        return kc[:b, :e], vc[:b, :e]
 
     def increment(self, n: int = 1):
         self.cached_len += n
@@ -175,7 +178,10 @@ class CausalSelfAttention(nn.Module):
         k = k.transpose(1, 2).to(q.dtype)
         v = v.transpose(1, 2).to(q.dtype)
         drop = self.dropout if self.training else 0
-        if kv_cache is not None and kv_cache.cached_len > 0:
+        if kv_cache is not None and kv_cache.cached_len > 0 and T == 1:
+            # one new position attends to every cached one: no mask needed
+            y = F.scaled_dot_product_attention(q, k, v, dropout_p=drop)
+        elif kv_cache is not None and kv_cache.cached_len > 0:
             total = k.size(2)
             mask = torch.ones(T, total, dtype=torch.bool, device=q.device).tril(diagonal=total - T)
             y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=drop)

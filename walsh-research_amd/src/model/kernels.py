@@ -322,6 +322,56 @@ def mhc_pre_norm(x: torch.Tensor, phi_frag: torch.Tensor, coef: torch.Tensor, bi
     return layer_in, h_pre, h_post, h_res
 
 
+def phi_fragments32(phi_cat: torch.Tensor) -> torch.Tensor:
+    """phi_cat [32, K] -> 16x16x32 matrix-core fragment order [K/32][2][64][8]
+    (lane = 16*kq + n holds phi[16*tile + n][32*ks + 8*kq .. +7])."""
+    K = phi_cat.shape[1]
+    return phi_cat.view(2, 16, K // 32, 4, 8).permute(2, 0, 3, 1, 4).contiguous()
+
+
+def mhc_pre_wide_supported(n: int, C: int) -> bool:
+    """Whether walsh_mhc_pre_wide_fwd handles this shape (rows too long for
+    the LDS-tile kernel, up to n_embd 4096)."""
+    return n <= 4 and (n * C) % 32 == 0 and C % 4 == 0 and C <= 4096
+
+
+def mhc_pre_wide(x: torch.Tensor, phi_frag32: torch.Tensor, coef: torch.Tensor, bias_cat: torch.Tensor,
+                 rms_eps: float, norm_w: torch.Tensor = None, norm_eps: float = 1e-6, n_iter: int = 20,
+                 sk_eps: float = 1e-8):
+    """mhc_pre_norm for long rows: split-K projection, then per-token
+    constraints and layer input (two launches; workspace from the caching
+    allocator)."""
+    _hip.require_device(x, "stream input")
+    n, C = x.shape[-2], x.shape[-1]
+    lead = x.shape[:-2]
+    xv = x if x.is_contiguous() else x.contiguous()
+    M = xv.numel() // (n * C)
+    dev = x.device
+    layer_in = torch.empty(lead + (C,), device=dev, dtype=x.dtype)
+    h_pre = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_post = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_res = torch.empty(lead + (n, n), device=dev, dtype=torch.float32)
+    if M == 0:
+        return layer_in, h_pre, h_post, h_res
+    assert phi_frag32.dtype == x.dtype and phi_frag32.numel() == 32 * n * C, "phi_frag32 layout"
+    nw = None
+    if norm_w is not None:
+        nw = norm_w.detach().float().contiguous()
+        assert nw.numel() == C
+    wsb = _hip.lib().walsh_mhc_pre_wide_workspace(M, n, C)
+    ws = torch.empty(max(wsb, 4), device=dev, dtype=torch.uint8)
+    esz = x.element_size()
+    nbytes = 2 * M * n * C * esz + M * C * esz + M * (2 * n + n * n) * 4 + 32 * n * C * esz
+    flops = M * (2 * n * C * 32 + 2 * n * C + 2 * n * C)
+    _hip.call("walsh_mhc_pre_wide_fwd", xv.data_ptr(), n * C, M, n, C, phi_frag32.data_ptr(), coef.data_ptr(),
+              bias_cat.data_ptr(), float(rms_eps), int(n_iter), float(sk_eps), h_pre.data_ptr(), h_post.data_ptr(),
+              h_res.data_ptr(), layer_in.data_ptr(), C, _hip.ptr(nw), float(norm_eps), ws.data_ptr(), ws.numel(),
+              _hip.dtype_code(x.dtype), _hip.stream(dev),
+              kernel="mhc_proj+apply<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"), nbytes=nbytes,
+              flops=flops)
+    return layer_in, h_pre, h_post, h_res
+
+
 def mhc_post(x: torch.Tensor, out: torch.Tensor, h_res: torch.Tensor, h_post: torch.Tensor) -> torch.Tensor:
     """x_new = H_res @ x + H_post^T (x) out (mhc.py:366-381); x [..., n, C], out [..., C]."""
     _hip.require_device(x, "stream input")

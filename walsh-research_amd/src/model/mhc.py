@@ -126,7 +126,12 @@ class mHCResidualStream(nn.Module):
                                     (self.H_res.phi.weight, n * n)], dtype, device)
             coef = torch.stack([m.alpha.detach().float() for m in maps]).to(device)
             bias = torch.cat([m.bias.detach().float().reshape(-1) for m in maps]).to(device)
-            frag = kernels.phi_fragments(phi) if (n * C) % 16 == 0 else None
+            if kernels.mhc_pre_supported(n, C, dtype) and (n * C) % 16 == 0:
+                frag = kernels.phi_fragments(phi)
+            elif kernels.mhc_pre_wide_supported(n, C):
+                frag = kernels.phi_fragments32(phi)
+            else:
+                frag = None
             return phi, coef, bias, frag
 
         tensors = [t for m in maps for t in (m.phi.weight, m.alpha, m.bias)]
@@ -137,10 +142,12 @@ class mHCResidualStream(nn.Module):
         if n > _MAX_STREAMS:
             raise NotImplementedError(f"n_streams={n} > {_MAX_STREAMS} is not supported by this build")
         phi, coef, bias, frag = self.fused_params(dt, x.device)
+        nw = None if norm is None else norm.weight
+        neps = 1e-6 if norm is None else norm.eps
         if frag is not None and kernels.mhc_pre_supported(n, C, dt):
-            return kernels.mhc_pre_norm(x, frag, coef, bias, _rms_eps(dt),
-                                        norm_w=None if norm is None else norm.weight,
-                                        norm_eps=1e-6 if norm is None else norm.eps)
+            return kernels.mhc_pre_norm(x, frag, coef, bias, _rms_eps(dt), norm_w=nw, norm_eps=neps)
+        if frag is not None and kernels.mhc_pre_wide_supported(n, C):
+            return kernels.mhc_pre_wide(x, frag, coef, bias, _rms_eps(dt), norm_w=nw, norm_eps=neps)
         li, hp, hq, hr = kernels.mhc_pre(x, phi, coef, bias, _rms_eps(dt))
         if norm is not None:
             li = norm(li).to(dt)
@@ -282,7 +289,7 @@ class mHCWalsh(nn.Module):
             logits = self.output(h_out)
             loss = F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1), ignore_index=-1)
         else:
-            logits = self.output(h_out[:, [-1], :])
+            logits = self.output(h_out[:, -1:, :])
             loss = None
         if return_hidden:
             return logits, loss, h_out
