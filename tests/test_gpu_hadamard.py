@@ -137,6 +137,23 @@ def test_hadamard_linear_shapes(K, dtype, in_o, out_o):
     assert_close(y, ref, dtype, f"{dtype} in_o={in_o} out_o={out_o}")
 
 
+@pytest.mark.parametrize("in_o,out_o,M", [(128, 128, 1), (128, 128, 17), (128, 128, 4200), (64, 64, 300),
+                                          (100, 128, 77), (128, 68, 77), (36, 64, 77), (128, 112, 33)])
+def test_hadamard_wide_bf16(K, in_o, out_o, M):
+    # bf16 layers with 16 < in_o <= 128 and 64 <= out_o <= 128 run the base-3
+    # 16x16x32 kernel: partial 32-column chunks (in_o 100, 36), a partial last
+    # output tile (68), fewer than 8 output tiles (112, 64), and more 16-row
+    # tiles than workgroups (4200 rows)
+    rng = np.random.default_rng(in_o * 7 + out_o + M)
+    codes = rng.integers(-1, 2, size=(32, out_o, in_o)).astype(np.int8)
+    alpha = rng.uniform(0.5, 1.5, size=(32, in_o)).astype(np.float32)
+    beta = rng.uniform(0.05, 0.3, size=(32, out_o)).astype(np.float32)
+    x = rng.standard_normal((M, 32 * in_o)).astype(np.float32)
+    y, xq = _run(K, x, codes, alpha, beta, torch.bfloat16)
+    ref = ohad.hadamard_linear_f64(xq, codes, alpha, beta)
+    assert_close(y, ref, torch.bfloat16, f"wide in_o={in_o} out_o={out_o} M={M}")
+
+
 @pytest.mark.parametrize("M", [1, 15, 16, 17, 1000])
 def test_hadamard_linear_row_tails(K, M):
     rng = np.random.default_rng(M)

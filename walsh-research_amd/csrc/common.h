@@ -101,6 +101,15 @@ __device__ __forceinline__ void store4(uint16_t *p, f32x4 v) {
     *(uint2 *)p = u;
 }
 
+// Workgroup barrier ordering LDS only: global loads and stores issued before
+// it stay in flight instead of being drained at every phase boundary (as the
+// full __syncthreads() fence does).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---------------------------------------------------------------- buffer access

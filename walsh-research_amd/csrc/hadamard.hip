@@ -19,6 +19,8 @@
 // into beta (exact: a power of two).
 #include "common.h"
 
+#include <type_traits>
+
 namespace walsh {
 
 constexpr int kTile = 16;       // tokens per wavefront tile
@@ -82,6 +84,7 @@ struct HadArgs {
     int in_o, out_o, Nt, Kc;
     int gsx, gsy;       // group strides of x / y rows (>= in_o / out_o)
     const uint8_t *kw;
+    const uint8_t *kw3;  // base-3 layout (wide bf16 kernel), or null
     const float *alpha;
     const float *beta;
     void *y;
@@ -444,6 +447,242 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide_kernel(HadArgs 
     }
 }
 
+// ---------------------------------------------------------------- wide bf16 layers
+// bf16 layers with 16 < in_o <= 128 and out_o <= 128 (n_embd 4096: in_o =
+// out_o = 128) on 16x16x32 matrix-core products.  A workgroup of 8 waves
+// takes one 16-token tile at a time:
+//   1. wave w transforms columns 16w..16w+15 of all 32 groups (alpha, FHT
+//      over the groups in registers) and writes them to an LDS stage laid out
+//      as the products' B operand: [32-column chunk][group][lane] x 16 bytes,
+//      so every later read is one contiguous 1 KB per wave;
+//   2. wave w contracts output tile w against the whole stage (32 groups x
+//      in_o/32 chunks);
+//   3. wave w runs the output transform and beta into an LDS output tile
+//      (the stage's space), which leaves as whole contiguous rows (16 bytes
+//      per lane, 1 KB per wave and store) instead of 32-byte row pieces.
+// The next tile's x is loaded during the last chunk's products and the
+// output phase.  Weight codes are stored 4 per byte in base 3 (byte =
+// sum_j (code_j + 1) 3^j) and expanded through an 81-entry byte -> 4 x bf16
+// table of +-1/32 (the two transforms' 1/sqrt(32)^2, exact in bf16), held in
+// 16 copies, entry-major with one 8-byte copy per lane of a 16-lane group.
+// (A 9-entry table of bf16 pairs in 64 conflict-free copies was measured
+// slower: twice the LDS instructions.)  alpha and beta stay in LDS for the
+// whole launch as fp16 (11-bit significand, 2^-12 relative rounding against
+// the 2^-9 of the bf16 activations): with the 128 KB stage, float32 copies of
+// both would not fit in 160 KB.
+constexpr int kW3Copies = 16;
+constexpr int kW3Entries = 81;
+constexpr int kW3MaxO = 128;  // in_o and out_o limit
+constexpr size_t kW3LutBytes = (size_t)kW3Entries * kW3Copies * 8;
+constexpr size_t kW3AlphaBytes = (size_t)32 * kW3MaxO * 2;             // [32 g][128 cols] fp16
+constexpr size_t kW3BetaBytes = (size_t)32 * kW3MaxO * 2;              // [8 tiles][32 h][16 o] fp16
+
+constexpr int kW3ORow = 32 * kW3MaxO * 2 + 16;                        // output tile row stride (bytes)
+
+static size_t wide3_lds_bytes(int Kc32) {
+    const size_t stage = (size_t)Kc32 * 32 * 64 * 16, otile = (size_t)kTile * kW3ORow;
+    return kW3LutBytes + kW3AlphaBytes + kW3BetaBytes + (stage > otile ? stage : otile);
+}
+
+// Base-3 weight layout [Nt][Kc32][64 lanes][32 groups][2] bytes: lane l of
+// (nt, c) holds for group g the bytes of codes
+// W[g, 16nt + l%16, 32c + 8(l/16) + 4h .. +3], h = 0, 1 (40 = four zero codes,
+// used past out_o / in_o).  Packed code 0b11 is never written by the packer;
+// it saturates to +1 here.
+__global__ void hadamard_prepare3_kernel(const uint8_t *__restrict__ packed, int in_o, int out_o, int Nt, int Kc32,
+                                         uint8_t *__restrict__ kw3) {
+    const int64_t total = (int64_t)Nt * Kc32 * 64 * 64;
+    const int kp4 = (int)ceil_div(in_o, 4);
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int h = (int)(e & 1);
+        const int g = (int)((e >> 1) & 31);
+        const int lane = (int)((e >> 6) & 63);
+        const int64_t tc = e >> 12;
+        const int c = (int)(tc % Kc32);
+        const int nt = (int)(tc / Kc32);
+        const int o = kNTile * nt + (lane & 15);
+        const int i0 = 32 * c + 8 * (lane >> 4) + 4 * h;
+        int b = 40;
+        if (o < out_o && i0 < in_o) {
+            const uint32_t p = packed[((int64_t)g * out_o + o) * kp4 + i0 / 4];
+            b = 0;
+            int w3 = 1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = (int)((p >> (6 - 2 * j)) & 3u);
+                b += (d > 2 ? 2 : d) * w3;
+                w3 *= 3;
+            }
+        }
+        kw3[e] = (uint8_t)b;
+    }
+}
+
+// Groups G0..G1-1 of the lane's 4 transform columns as raw bf16.
+template <int G0 = 0, int G1 = 32>
+__device__ __forceinline__ void wide3_load_x(__amdgpu_buffer_rsrc_t xr, uint32_t voff, uint32_t gstride,
+                                             u32x2 (&r)[32]) {
+#pragma unroll
+    for (int g = G0; g < G1; ++g) r[g] = __builtin_amdgcn_raw_buffer_load_b64(xr, voff, (uint32_t)g * gstride, 0);
+}
+
+// GS: 128 for in_o = out_o = 128 with unpadded groups (the n_embd 4096
+// layers: strides fixed at compile time), 0 for any other shape.
+template <int GS>
+__global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint2 *lut = (uint2 *)smem;                                          // [81 entries][16 copies]
+    _Float16 *alpha_l = (_Float16 *)(smem + kW3LutBytes);                // [32 g][128 cols]
+    _Float16 *beta_l = (_Float16 *)(smem + kW3LutBytes + kW3AlphaBytes); // [8 tiles][32 h][16 o]
+    uint4 *xs = (uint4 *)(smem + kW3LutBytes + kW3AlphaBytes + kW3BetaBytes);  // [Kc32][32 g][64 lanes]
+    unsigned char *ostage = (unsigned char *)xs;  // after the products: the output tile
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane & 15, q = lane >> 4;
+    for (int e = tid; e < kW3Entries * kW3Copies; e += kWideThreads) {
+        int r = e / kW3Copies;
+        float val[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            val[j] = (float)(r % 3 - 1) * 0.03125f;
+            r /= 3;
+        }
+        lut[e] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
+    }
+    for (int e = tid; e < 32 * kW3MaxO; e += kWideThreads) {
+        const int g = e / kW3MaxO, i = e % kW3MaxO;
+        alpha_l[e] = (_Float16)(i < a.in_o ? a.alpha[g * a.in_o + i] : 0.f);
+        const int o = kNTile * (e >> 9) + (e & 15), h = (e >> 4) & 31;  // e = (nt*32 + h)*16 + o%16
+        beta_l[e] = (_Float16)(o < a.out_o ? a.beta[h * a.out_o + o] : 0.f);
+    }
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * 2));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
+    const int n_tiles = (int)ceil_div(a.M, kTile);
+    const int Kc32 = (a.in_o + 31) >> 5;
+    const uint2 *lut_l = lut + (lane & 15);
+    const uint32_t gstride = (uint32_t)(GS ? GS : a.gsx) * 2;
+    // this wave's transform columns and their place in the stage
+    const int i0 = 16 * wave + 4 * q;
+    uint2 *xdst = (uint2 *)(xs + (size_t)(i0 >> 5) * 32 * 64 + t + 16 * ((i0 >> 3) & 3)) + ((i0 >> 2) & 1);
+    const bool xwave = wave < 2 * Kc32;
+    // every wave runs the products (uniform control flow keeps the
+    // accumulators in registers across the barriers); a wave past the last
+    // output tile reads tile 0's weights and its results are never stored
+    const int wt = wave < a.Nt ? wave : 0;
+    const uint4 *wsrc = (const uint4 *)(a.kw3 + ((int64_t)wt * Kc32 * 64 + lane) * 64);
+    const _Float16 *bl = beta_l + wave * 512 + 4 * q;
+    const _Float16 *al = alpha_l + i0;
+    auto x_off = [&](int tile) -> uint32_t {
+        const int row = tile * kTile + t;
+        return (row < a.M && i0 < a.in_o) ? (uint32_t)((int64_t)row * a.ldx * 2) + (uint32_t)i0 * 2 : kOOB;
+    };
+    // x of the first tile; later tiles are loaded during the contraction of
+    // the one before, so their load latency overlaps the matrix work
+    u32x2 xraw[32];
+    if (xwave && (int)blockIdx.x < n_tiles) wide3_load_x(xr, x_off(blockIdx.x), gstride, xraw);
+    for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const int next = tile + gridDim.x;
+        lds_barrier();  // tables ready / previous tile done with the stage
+        if (xwave) {
+            // two passes of 2 columns keep the transform at 64 registers
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                f32x2 v[32];
+#pragma unroll
+                for (int g = 0; g < 32; ++g) {
+                    const uint32_t u = p ? xraw[g].y : xraw[g].x;
+                    const _Float16 *ag = al + g * kW3MaxO + 2 * p;
+                    v[g] = f32x2{__uint_as_float(u << 16) * (float)ag[0], __uint_as_float(u & 0xffff0000u) * (float)ag[1]};
+                }
+                fht32<f32x2>(v);
+#pragma unroll
+                for (int g = 0; g < 32; ++g) ((uint32_t *)&xdst[g * 128])[p] = pack_bf16x2(v[g][0], v[g][1]);
+            }
+        }
+        lds_barrier();
+        f32x4 acc[32];
+        const bool pf = xwave && next < n_tiles;
+        const uint32_t pf_off = pf ? x_off(next) : kOOB;
+        {
+#pragma unroll
+            for (int g = 0; g < 32; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+            // one 32-column chunk: 32 products
+            auto chunk = [&](int c, const uint4 (&w)[4]) {
+                const uint4 *xsrc = xs + (size_t)c * 32 * 64 + lane;
+#pragma unroll
+                for (int g = 0; g < 32; ++g) {
+                    const uint32_t word = w[g >> 3][(g >> 1) & 3] >> (16 * (g & 1));
+                    const uint2 lo = lut_l[(word & 0xffu) * kW3Copies];
+                    const uint2 hi = lut_l[((word >> 8) & 0xffu) * kW3Copies];
+                    const uint4 xb = xsrc[g * 64];
+                    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y}), __builtin_bit_cast(bf16x8, xb),
+                        acc[g], 0, 0, 0);
+                }
+            };
+            uint4 w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = wsrc[j];
+            for (int c = 0; c + 1 < Kc32; ++c) {
+                uint4 wn[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wn[j] = wsrc[(c + 1) * 256 + j];
+                chunk(c, w);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[j] = wn[j];
+            }
+            // the next tile's x: groups 0-15 behind the last chunk (whose
+            // weights are already in registers, so no weight load waits
+            // behind them), groups 16-31 once the output tile is written and
+            // the accumulators are free
+            __builtin_amdgcn_sched_barrier(0);
+            if (pf) wide3_load_x<0, 16>(xr, pf_off, gstride, xraw);
+            chunk(Kc32 - 1, w);
+        }
+        lds_barrier();  // every wave is done with the stage: it now takes the output tile
+        {
+            // output transform over h and beta, into the LDS output tile
+            // [16 rows][32 h][128 o] (rows padded by 16 bytes: the 16 rows
+            // of a write fall on different banks)
+            fht32x4(acc);
+            unsigned char *od = ostage + t * kW3ORow + (kNTile * wave + 4 * q) * 2;
+#pragma unroll
+            for (int h0 = 0; h0 < 32; h0 += 8) {
+                uint2 b8[8];  // beta of 8 output groups, read together
+#pragma unroll
+                for (int j = 0; j < 8; ++j) b8[j] = *(const uint2 *)(bl + (h0 + j) * 16);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const _Float16 *b = (const _Float16 *)&b8[j];
+                    const f32x4 r = acc[h0 + j] * f32x4{(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
+                    *(uint2 *)(od + (h0 + j) * kW3MaxO * 2) = uint2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (pf) wide3_load_x<16, 32>(xr, pf_off, gstride, xraw);
+        }
+        lds_barrier();
+        // the whole tile leaves as contiguous rows: each lane takes 8 outputs
+        // (16 bytes) of a row, 1 KB per wave and instruction
+#pragma unroll 4
+        for (int r = 0; r < kTile; ++r) {
+            const int orow = tile * kTile + r;
+            const uint4 v = *(const uint4 *)(ostage + r * kW3ORow + tid * 16);
+            if (GS == kW3MaxO) {
+                const uint32_t voff = orow < a.M ? (uint32_t)((int64_t)orow * a.ldy * 2) + (uint32_t)tid * 16 : kOOB;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yr, voff, 0, 0);
+            } else {
+                // group stride gsy: two 4-output stores at h*gsy + o
+                const int h = tid >> 4, o = (tid & 15) * 8;
+                const uint32_t base = (uint32_t)((int64_t)orow * a.ldy * 2) + (uint32_t)(h * a.gsy + o) * 2;
+                const uint32_t v0 = (orow < a.M && o < a.out_o) ? base : kOOB;
+                const uint32_t v1 = (orow < a.M && o + 4 < a.out_o) ? base + 8 : kOOB;
+                __builtin_amdgcn_raw_buffer_store_b64(u32x2{v.x, v.y}, yr, v0, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b64(u32x2{v.z, v.w}, yr, v1, 0, 0);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- fused SwiGLU
 // h = silu(gate(x)) * up(x) for two Hadamard linears sharing the input x
 // (SwiGLUMLP.forward, src/model/chassis.py:498-504, whose gate_proj/up_proj
@@ -652,9 +891,21 @@ static size_t hadamard_lds_bytes(bool bf16, int Kc, int Nt) {
 
 using namespace walsh;
 
+// Shapes that also get the base-3 layout of the wide bf16 kernel.
+static bool wide3_shape(int64_t in_o, int64_t out_o) {
+    return in_o > kKChunk && in_o <= kW3MaxO && out_o <= kW3MaxO;
+}
+
+static int64_t weight_bytes1(int64_t in_o, int64_t out_o) {
+    return ceil_div(out_o, kNTile) * ceil_div(in_o, kKChunk) * 64 * 32;
+}
+
+// The first layout, followed by the base-3 one for wide3_shape.
 WALSH_EXPORT int64_t walsh_hadamard_weight_bytes(int64_t in_o, int64_t out_o) {
     if (in_o <= 0 || out_o <= 0) return 0;
-    return ceil_div(out_o, kNTile) * ceil_div(in_o, kKChunk) * 64 * 32;
+    int64_t n = weight_bytes1(in_o, out_o);
+    if (wide3_shape(in_o, out_o)) n += ceil_div(out_o, kNTile) * ceil_div(in_o, 32) * 4096;
+    return n;
 }
 
 WALSH_EXPORT int walsh_hadamard_prepare(const uint8_t *packed, int64_t in_o, int64_t out_o, uint8_t *kweight,
@@ -670,6 +921,14 @@ WALSH_EXPORT int walsh_hadamard_prepare(const uint8_t *packed, int64_t in_o, int
     if (grid > 4096) grid = 4096;
     launch(hadamard_prepare_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, packed, (int)in_o,
                        (int)out_o, Nt, Kc, kweight);
+    if (wide3_shape(in_o, out_o)) {
+        const int Kc32 = (int)ceil_div(in_o, 32);
+        const int64_t total3 = (int64_t)Nt * Kc32 * 4096;
+        int grid3 = (int)ceil_div(total3, block);
+        if (grid3 > 4096) grid3 = 4096;
+        launch(hadamard_prepare3_kernel, dim3(grid3), dim3(block), 0, (hipStream_t)stream, packed, (int)in_o,
+               (int)out_o, Nt, Kc32, kweight + weight_bytes1(in_o, out_o));
+    }
     return check_hip(hipGetLastError(), "walsh_hadamard_prepare launch");
 }
 
@@ -705,6 +964,9 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
     // several input chunks and output tiles: the workgroup-wide kernel
     const size_t wide_lds = bf16 ? wide_lds_bytes<true>() : wide_lds_bytes<false>();
     const bool wide = !swiglu && vec && Kc >= 2 && Nt >= 4 && wide_lds <= (size_t)device_info().max_shared_per_block;
+    // bf16 with in_o <= 128 and out_o <= 128: the base-3 16x16x32 kernel
+    const size_t wide3_lds = wide3_lds_bytes((base.in_o + 31) / 32);
+    const bool wide3 = wide && bf16 && base.kw3 != nullptr && wide3_lds <= (size_t)device_info().max_shared_per_block;
     const int64_t ld = base.ldx > base.ldy ? base.ldx : base.ldy;
     int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz);
     rows_max = rows_max / kTile * kTile;
@@ -735,6 +997,13 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
                 else     { if (one) WALSH_SW_LAUNCH(float, false, false, true); else WALSH_SW_LAUNCH(float, false, false, false); }
             }
 #undef WALSH_SW_LAUNCH
+        } else if (wide3) {
+            const int64_t items = ceil_div(rows, kTile);
+            const int64_t wcap = (int64_t)device_info().cu_count;
+            const dim3 G3((unsigned)(items < wcap ? items : wcap)), B3(kWideThreads);
+            if (a.gsx == 128 && a.gsy == 128 && a.in_o == 128 && a.out_o == 128)
+                launch(hadamard_wide3_kernel<128>, G3, B3, wide3_lds, s, a);
+            else launch(hadamard_wide3_kernel<0>, G3, B3, wide3_lds, s, a);
         } else if (wide) {
             const int64_t items = ceil_div(rows, kTile) * ceil_div(Nt, kWideWaves);
             const int64_t wcap = (int64_t)device_info().cu_count;
@@ -777,6 +1046,7 @@ static HadArgs had_args(const void *x, int64_t ldx, int64_t gsx, int64_t in_o, i
     a.gsx = (int)gsx;
     a.gsy = (int)gsy;
     a.kw = kw;
+    a.kw3 = wide3_shape(in_o, out_o) ? kw + weight_bytes1(in_o, out_o) : nullptr;
     a.alpha = alpha;
     a.beta = beta;
     a.y = y;

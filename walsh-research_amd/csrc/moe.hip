@@ -587,15 +587,6 @@ __global__ __launch_bounds__(kMoeThreads, 2) void moe_experts_kernel(ExpArgs a) 
 constexpr int kFfnC = 512, kFfnE = 16, kFfnTok = 64, kFfnWaves = 8, kFfnThreads = 64 * kFfnWaves;
 constexpr int kXsStride = kFfnC * 2 + 16;  // bytes per token row of the LDS tile (padded)
 
-// Workgroup barrier ordering LDS only: global stores issued before it (the
-// zeroed output blocks, routing outputs) stay in flight instead of being
-// drained at every phase boundary.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 __device__ __forceinline__ f32x4 mma32(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);

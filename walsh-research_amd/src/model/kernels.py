@@ -146,7 +146,10 @@ def hadamard_linear(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tenso
     kc1 = in_o <= 16 and (dt == torch.bfloat16 or out_o <= 16)
     kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, vec, kc1)
     if vec and in_o > 16 and out_o > 48:
-        kname = "hadamard_wide_kernel<%s>" % ("bf16" if dt == torch.bfloat16 else "f32")
+        if dt == torch.bfloat16 and in_o <= 128 and out_o <= 128:
+            kname = "hadamard_wide3_kernel<bf16>"
+        else:
+            kname = "hadamard_wide_kernel<%s>" % ("bf16" if dt == torch.bfloat16 else "f32")
     _hip.call("walsh_hadamard_linear_ex_fwd", xv.data_ptr(), ldx, gsx, rows, in_o, out_o, kweight.data_ptr(),
               alpha.data_ptr(), beta.data_ptr(), y.data_ptr(), 32 * gsy, gsy, code, _hip.stream(x.device),
               kernel=kname, nbytes=nbytes, flops=flops)
