@@ -112,6 +112,16 @@ __device__ __forceinline__ void lds_barrier() {
 
 __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Rows per launch when M rows must be split into launches of at most
+// rows_max (a multiple of align): equal chunks rounded up to align, so no
+// launch is a small tail.
+inline int64_t balanced_rows(int64_t M, int64_t rows_max, int64_t align) {
+    if (M <= rows_max) return rows_max;
+    const int64_t n = ceil_div(M, rows_max);
+    const int64_t r = ceil_div(ceil_div(M, n), align) * align;
+    return r < rows_max ? r : rows_max;
+}
+
 // ---------------------------------------------------------------- buffer access
 // Raw buffer resources (gfx9 descriptor word 3 = 0x00020000).  A lane whose
 // byte offset is >= the buffer size reads zeros and its stores are dropped,

@@ -971,6 +971,7 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
     int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz);
     rows_max = rows_max / kTile * kTile;
     if (rows_max < kTile) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
+    rows_max = balanced_rows(M, rows_max, kTile);
     const int64_t cap = (int64_t)device_info().cu_count * (swiglu ? 8 : 2);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;

@@ -799,6 +799,7 @@ WALSH_EXPORT int walsh_mhc_pre_fwd(const void *x, int64_t ldx, int64_t M, int64_
     const int64_t ld = ldx > ld_in ? ldx : ld_in;
     int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / kPreTok * kPreTok;
     if (rows_max < kPreTok) return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_fwd: row stride too large");
+    rows_max = balanced_rows(M, rows_max, kPreTok);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
         PreArgs a;
@@ -847,8 +848,9 @@ WALSH_EXPORT int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out,
         return set_error(WALSH_ENOTSUP, "walsh_mhc_post_fwd: tensors must be %zu-byte aligned", valign);
     int64_t ld = ldx > ld_new ? ldx : ld_new;
     if (ld_out > ld) ld = ld_out;
-    const int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz);
+    int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz);
     if (rows_max < 1) return set_error(WALSH_ENOTSUP, "walsh_mhc_post_fwd: row stride too large");
+    rows_max = balanced_rows(M, rows_max, 1);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
         const int block = 256;
@@ -904,6 +906,7 @@ WALSH_EXPORT int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, i
     const int64_t ld = ldx > ld_in ? ldx : ld_in;
     int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / TT * TT;
     if (rows_max < TT) return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: row stride too large");
+    rows_max = balanced_rows(M, rows_max, TT);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
         Pre2Args a;
@@ -981,8 +984,9 @@ WALSH_EXPORT int walsh_mhc_pre_wide_fwd(const void *x, int64_t ldx, int64_t M, i
         return set_error(WALSH_EINVAL, "%s: workspace of %lld bytes needed", fn, (long long)need);
     // row chunks keep every buffer below 2^31 bytes
     const int64_t ld = ldx > ld_in ? ldx : ld_in;
-    const int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / 16 * 16;
+    int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / 16 * 16;
     if (rows_max < 16) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
+    rows_max = balanced_rows(M, rows_max, 16);
     hipStream_t s = (hipStream_t)stream;
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;

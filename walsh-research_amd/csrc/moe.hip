@@ -405,36 +405,68 @@ __global__ void moe_zero_kernel(int *count, float *probsum, int n) {
 }
 
 // ------------------------------------------------------------------ scatter
-// moe_finalize_kernel (one workgroup): totals of the per-workgroup partial
-// sums, offset = exclusive scan of the counts, tile_off = exclusive scan of
+// moe_finalize_kernel (one workgroup of kFinSlices threads per expert):
+// totals of the per-workgroup partial sums (each slice sums every
+// kFinSlices-th row, 8 loads in flight, then the slices add in LDS),
+// offset = exclusive scan of the counts, tile_off = exclusive scan of
 // ceil(count / 16), cursor cleared.
-__global__ __launch_bounds__(kMaxE) void moe_finalize_kernel(const int *__restrict__ count_part,
-                                                             const float *__restrict__ probsum_part, int n_part, int E,
-                                                             int *__restrict__ count, float *__restrict__ probsum,
-                                                             int *__restrict__ cursor, int *__restrict__ offset,
-                                                             int *__restrict__ tile_off) {
-    __shared__ int c_s[kMaxE];
-    const int e = threadIdx.x;
+constexpr int kFinSlices = 8;
+__global__ __launch_bounds__(kMaxE * kFinSlices) void moe_finalize_kernel(const int *__restrict__ count_part,
+                                                                          const float *__restrict__ probsum_part,
+                                                                          int n_part, int E, int *__restrict__ count,
+                                                                          float *__restrict__ probsum,
+                                                                          int *__restrict__ cursor,
+                                                                          int *__restrict__ offset,
+                                                                          int *__restrict__ tile_off) {
+    __shared__ int c_s[kFinSlices][kMaxE];
+    __shared__ float p_s[kFinSlices][kMaxE];
+    const int e = threadIdx.x % kMaxE, sl = threadIdx.x / kMaxE;
     int c = 0;
     float ps = 0.f;
     if (e < E) {
-        for (int r = 0; r < n_part; ++r) {
+        int r = sl;
+        for (; r + 7 * kFinSlices < n_part; r += 8 * kFinSlices) {
+            int cv[8];
+            float pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                cv[j] = count_part[(int64_t)(r + j * kFinSlices) * E + e];
+                pv[j] = probsum_part[(int64_t)(r + j * kFinSlices) * E + e];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                c += cv[j];
+                ps += pv[j];
+            }
+        }
+        for (; r < n_part; r += kFinSlices) {
             c += count_part[(int64_t)r * E + e];
             ps += probsum_part[(int64_t)r * E + e];
         }
-        count[e] = c;
-        probsum[e] = ps;
-        cursor[e] = 0;
     }
-    c_s[e] = c;
+    c_s[sl][e] = c;
+    p_s[sl][e] = ps;
     __syncthreads();
-    if (e == 0) {
+    if (sl == 0) {
+        for (int j = 1; j < kFinSlices; ++j) {
+            c += c_s[j][e];
+            ps += p_s[j][e];
+        }
+        if (e < E) {
+            count[e] = c;
+            probsum[e] = ps;
+            cursor[e] = 0;
+        }
+        c_s[0][e] = e < E ? c : 0;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
         int acc = 0, tacc = 0;
         for (int i = 0; i < E; ++i) {
             offset[i] = acc;
             tile_off[i] = tacc;
-            acc += c_s[i];
-            tacc += (c_s[i] + 15) / 16;
+            acc += c_s[0][i];
+            tacc += (c_s[0][i] + 15) / 16;
         }
         offset[E] = acc;
         tile_off[E] = tacc;
@@ -935,7 +967,7 @@ WALSH_EXPORT int walsh_moe_scatter(const int *topk_idx, int64_t M, int64_t E, in
         return set_error(WALSH_EINVAL, "%s: bad shape (M=%lld E=%lld k=%lld n_part=%lld)", fn, (long long)M,
                          (long long)E, (long long)k, (long long)n_part);
     hipStream_t s = (hipStream_t)stream;
-    launch(moe_finalize_kernel, dim3(1), dim3(kMaxE), 0, s, count_part, probsum_part, (int)n_part,
+    launch(moe_finalize_kernel, dim3(1), dim3(kMaxE * kFinSlices), 0, s, count_part, probsum_part, (int)n_part,
                        (int)E, count, probsum, cursor, offset, tile_off);
     const int64_t n_pairs = M * k;
     if (n_pairs > 0) {

@@ -215,6 +215,7 @@ WALSH_EXPORT int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M
     const int64_t ld = ldx > ldy ? ldx : ldy;
     int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / kBM * kBM;
     if (rows_max < kBM) return set_error(WALSH_ENOTSUP, "walsh_octonion_linear_fwd: row stride too large");
+    rows_max = balanced_rows(M, rows_max, kBM);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
         OctArgs a;
