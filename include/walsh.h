@@ -140,6 +140,29 @@ int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t gsx, int64_t M
                               const uint8_t *kw_up, const float *alpha_up, const float *beta_up, void *h,
                               int64_t ldh, int64_t gsh, int dtype, void *stream);
 
+/* walsh_hadamard_dense_weight_bytes / walsh_hadamard_dense_prepare: float32
+ *   weights of a Hadamard-structured layer with dense per-group matrices
+ *   (HadamardHeadMixerFused.W [32, head_dim, head_dim], fht_cuda.py:627-648)
+ *   in the kernel's matrix-core layout, bf16 or float32 (dtype).  w is
+ *   [32][out_o][in_o], or [32][in_o][out_o] when w_io (the head mixer's
+ *   x @ W[h]).  Re-run after every weight update. */
+int64_t walsh_hadamard_dense_weight_bytes(int64_t in_o, int64_t out_o, int dtype);
+int walsh_hadamard_dense_prepare(const float *w, int64_t in_o, int64_t out_o, int w_io, int dtype, uint8_t *kweight,
+                                 void *stream);
+
+/* walsh_head_mixer_fwd: HadamardHeadMixerFused.forward (fht_cuda.py:650-662)
+ *   on one group of 32 attention heads: x element (b, h, t, d) at
+ *   b*x_bstride + h*x_hstride + t*x_tstride + d (the [B, 32, T, D] output of
+ *   scaled_dot_product_attention, or a view into more heads); the result is
+ *   written token-major, y row b*T + t at (b*T + t)*ldy holding head h at
+ *   h*D: the layout the output projection reads, so no transpose copy is
+ *   needed.  y = beta[d] * H (H x W[h]) over the head axis, H the normalised
+ *   32-point Hadamard matrix.  kweight from walsh_hadamard_dense_prepare with
+ *   w_io = 1 and the same dtype.  head_dim (D) <= 32. */
+int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64_t D, int64_t x_bstride, int64_t x_hstride,
+                         int64_t x_tstride, const uint8_t *kweight, const float *beta, void *y, int64_t ldy, int dtype,
+                         void *stream);
+
 /* walsh_fht_fwd: fast Walsh-Hadamard transform of `rows` contiguous rows of
  *   length n (power of two <= 16384), Sylvester order, scaled by 1/sqrt(n)
  *   when `normalize` (fht_butterfly / fht, src/model/fht_cuda.py:281-337). */

@@ -70,6 +70,24 @@ def hadamard_linear_f64(x, codes, alpha, beta) -> np.ndarray:
     return y.reshape(M, G * out_o)
 
 
+def head_mixer_f64(x, W, beta) -> np.ndarray:
+    """Float64 HadamardHeadMixerFused.forward (``fht_cuda.py:650-662``).
+
+    x [B, 32, T, D] (32 attention heads); x_fht[g] = sum_h H[h, g] x[h]
+    (``:655``), y[h] = x_fht[h] @ W[h] with W [32, D, D] dense (``:658``),
+    y_fht[g] = sum_h H[h, g] y[h] (``:661``), times beta [D] broadcast over
+    heads and tokens (``:662``); H the normalised Sylvester matrix.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    B, G, T, D = x.shape
+    assert G == ALGEBRA_DIM
+    H = sylvester(G)
+    xf = np.einsum('bhti,hg->bgti', x, H)
+    y = np.einsum('bhti,hio->bhto', xf, np.asarray(W, np.float64))
+    yf = np.einsum('bhti,hg->bgti', y, H)
+    return yf * np.asarray(beta, np.float64)
+
+
 def hadamard_linear_torch32(x, codes, alpha, beta) -> torch.Tensor:
     """The reference CPU float32 evaluation order (``fht_cuda.py:497-519``).
 

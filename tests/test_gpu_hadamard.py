@@ -243,3 +243,60 @@ def test_launch_timer_records_kernel_time(K):
     # timing is off again: untimed launches still work
     lin(x)
     torch.cuda.synchronize()
+
+
+# --------------------------------------------------------------- head mixer
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,T,D", [(2, 64, 16), (1, 17, 16), (3, 5, 8), (2, 9, 12), (1, 33, 32), (2, 7, 5)])
+def test_head_mixer_vs_oracle(K, dtype, B, T, D):
+    rng = np.random.default_rng(B * 100 + T * 10 + D)
+    x = rng.standard_normal((B, 32, T, D)).astype(np.float32)
+    W = (rng.standard_normal((32, D, D)) * 0.2).astype(np.float32)
+    beta = rng.uniform(0.1, 0.5, size=D).astype(np.float32)
+    xt = torch.from_numpy(x).cuda().to(dtype)
+    Wt = torch.from_numpy(W).cuda()
+    kw = K.head_mixer_prepare(Wt, dtype)
+    y = K.head_mixer(xt, kw, torch.from_numpy(beta).cuda())
+    torch.cuda.synchronize()
+    assert y.shape == (B, T, 32 * D)
+    Wq = Wt.to(dtype).float().cpu().numpy()   # the weights the matrix cores see
+    ref = ohad.head_mixer_f64(xt.float().cpu().numpy(), Wq, beta).transpose(0, 2, 1, 3).reshape(B, T, 32 * D)
+    assert_close(y.float().cpu().numpy(), ref, dtype, f"mixer {dtype} B={B} T={T} D={D}")
+
+
+def test_head_mixer_group_view_and_output_slice(K):
+    # heads 32..63 of a 64-head attention output, written into the second
+    # half of token-major [B, T, 64*D] rows
+    rng = np.random.default_rng(11)
+    B, T, D = 2, 40, 16
+    x = rng.standard_normal((B, 64, T, D)).astype(np.float32)
+    W = (rng.standard_normal((32, D, D)) * 0.2).astype(np.float32)
+    beta = rng.uniform(0.1, 0.5, size=D).astype(np.float32)
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    kw = K.head_mixer_prepare(torch.from_numpy(W).cuda(), torch.bfloat16)
+    out = torch.zeros(B, T, 64 * D, device="cuda", dtype=torch.bfloat16)
+    K.head_mixer(xt.view(B, 2, 32, T, D)[:, 1], kw, torch.from_numpy(beta).cuda(), out=out[:, :, 32 * D:])
+    torch.cuda.synchronize()
+    Wq = torch.from_numpy(W).to(torch.bfloat16).float().numpy()
+    ref = ohad.head_mixer_f64(xt[:, 32:].float().cpu().numpy(), Wq, beta).transpose(0, 2, 1, 3).reshape(B, T, 32 * D)
+    o = out.float().cpu().numpy()
+    assert np.all(o[:, :, :32 * D] == 0)
+    assert_close(o[:, :, 32 * D:], ref, torch.bfloat16, "mixer group view")
+
+
+def test_head_mixer_module_matches_torch_path():
+    from src.model.hadamard import HadamardHeadMixerFused
+    torch.manual_seed(3)
+    m = HadamardHeadMixerFused(16)
+    x = torch.randn(2, 32, 24, 16)
+    ref = m(x)                       # CPU: the reference's three products in torch
+    mg = m.cuda()
+    y = mg(x.cuda())                 # GPU: walsh_head_mixer_fwd (float32)
+    torch.cuda.synchronize()
+    assert y.shape == ref.shape
+    assert_close(y.cpu().numpy(), ref.detach().numpy(), torch.float32, "mixer module f32")
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        yb = mg(x.cuda().to(torch.bfloat16))
+    assert yb.dtype == torch.bfloat16
+    assert_close(yb.float().cpu().numpy(), ref.detach().numpy(), torch.bfloat16, "mixer module bf16")

@@ -92,3 +92,27 @@ def test_init_weight_quantises_to_thirds():
     c = ternary.ternary_codes(w, ternary.absmean_gamma(w))
     frac = np.bincount(c.reshape(-1) + 1, minlength=3) / c.size
     assert np.all(np.abs(frac - np.array([0.345, 0.31, 0.345])) < 0.04)
+
+
+def test_head_mixer_identity_weights():
+    # W[h] = I: H H = I (normalised Sylvester), so the mixer is beta * x
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((2, 32, 5, 8))
+    beta = rng.uniform(0.1, 0.9, size=8)
+    W = np.broadcast_to(np.eye(8), (32, 8, 8))
+    assert np.allclose(hadamard.head_mixer_f64(x, W, beta), x * beta, atol=1e-12)
+
+
+def test_head_mixer_equals_hadamard_linear_on_rows():
+    # with ternary W the mixer is a Hadamard linear on the token rows
+    # [32 heads x D]: codes[g, o, i] = W[g, i, o], alpha = 1, beta per column
+    rng = np.random.default_rng(8)
+    B, T, D = 2, 3, 12
+    x = rng.standard_normal((B, 32, T, D))
+    W = rng.integers(-1, 2, size=(32, D, D)).astype(np.float64)
+    beta = rng.uniform(0.1, 0.9, size=D)
+    y = hadamard.head_mixer_f64(x, W, beta)
+    rows = x.transpose(0, 2, 1, 3).reshape(B * T, 32 * D)
+    ref = hadamard.hadamard_linear_f64(rows, W.transpose(0, 2, 1).astype(np.int8), np.ones((32, D)),
+                                       np.broadcast_to(beta, (32, D)))
+    assert np.allclose(y.transpose(0, 2, 1, 3).reshape(B * T, 32 * D), ref, atol=1e-10)

@@ -85,11 +85,26 @@ struct HadArgs {
     int gsx, gsy;       // group strides of x / y rows (>= in_o / out_o)
     const uint8_t *kw;
     const uint8_t *kw3;  // base-3 layout (wide bf16 kernel), or null
-    const float *alpha;
-    const float *beta;
+    const float *alpha;  // [32][in_o]; null: all ones
+    const float *beta;   // row h of beta at beta + h * beta_h
+    int beta_h;          // out_o, or 0 for one beta row shared by all groups
     void *y;
     int64_t ldy;
+    // x rows in batches (0: plain rows at ldx): row r sits at
+    // (r / tpb) * bstride + (r % tpb) * ldx elements
+    int tpb;
+    int64_t bstride;
 };
+
+__device__ __forceinline__ uint32_t x_row_off(const HadArgs &a, int row, uint32_t esz) {
+    const int64_t e = a.tpb ? (int64_t)(row / a.tpb) * a.bstride + (int64_t)(row % a.tpb) * a.ldx : (int64_t)row * a.ldx;
+    return (uint32_t)(e * esz);
+}
+
+__device__ __forceinline__ uint32_t x_bytes(const HadArgs &a, uint32_t esz) {
+    const int64_t e = a.tpb ? ceil_div(a.M, a.tpb) * a.bstride : (int64_t)a.M * a.ldx;
+    return (uint32_t)(e * esz);
+}
 
 // Transformed inputs of the lane's 4 columns over the 32 groups.
 template <bool BF16MMA> struct XM;
@@ -220,15 +235,43 @@ __device__ __forceinline__ void transform_store(const HadArgs &a, f32x4 (&acc)[3
 // VEC: in_o % 4 == 0 and out_o % 4 == 0 with aligned rows (4-wide loads and
 // stores).  KC1: a single input chunk (in_o <= 16); the transformed inputs
 // are computed once per tile and reused for every output tile.
-template <typename T, bool BF16MMA, bool VEC, bool KC1>
+// DENSE: float weights instead of ternary codes (the Hadamard head mixer),
+// as matrix-core A fragments [Nt][Kc][32 g][64 lanes] (bf16x4 or f32x4)
+// copied into LDS in place of the code table.
+template <bool BF16MMA> constexpr int dense_frag_bytes() { return BF16MMA ? 8 : 16; }
+
+template <bool BF16MMA>
+__device__ __forceinline__ void contract_dense(const unsigned char *__restrict__ wf, const XM<BF16MMA> &xm,
+                                               f32x4 (&acc)[32]) {
+#pragma unroll
+    for (int g = 0; g < 32; ++g) {
+        if constexpr (BF16MMA) {
+            const uint2 wa = ((const uint2 *)wf)[g * 64];
+            acc[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, wa),
+                                                                __builtin_bit_cast(i16x4, xm.b[g]), acc[g], 0, 0, 0);
+        } else {
+            const f32x4 wa = ((const f32x4 *)wf)[g * 64];
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[s], xm.v[g][s], acc[g], 0, 0, 0);
+        }
+        if ((g & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE = false>
 __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void hadamard_fwd_kernel(HadArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     void *lut = smem;
-    f32x4 *alpha_l = (f32x4 *)(smem + lut_bytes<BF16MMA>());
+    const size_t wbytes = DENSE ? (size_t)a.Nt * a.Kc * 32 * 64 * dense_frag_bytes<BF16MMA>() : lut_bytes<BF16MMA>();
+    f32x4 *alpha_l = (f32x4 *)(smem + wbytes);
     f32x4 *beta_l = alpha_l + a.Kc * 128;
 
     const int tid = threadIdx.x;
-    {
+    if constexpr (DENSE) {
+        const uint4 *src = (const uint4 *)a.kw;
+        for (int e = tid; e < (int)(wbytes / 16); e += kThreads) ((uint4 *)smem)[e] = src[e];
+    } else {
         const uint32_t byte = (uint32_t)tid;  // kThreads == 256 table entries
         float val[4];
 #pragma unroll
@@ -247,7 +290,8 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
         const int i0 = 4 * cq;  // 16c + 4q
         f32x4 v;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = (i0 + j < a.in_o) ? a.alpha[g * a.in_o + i0 + j] : 0.f;
+        for (int j = 0; j < 4; ++j)
+            v[j] = (i0 + j < a.in_o) ? (a.alpha ? a.alpha[g * a.in_o + i0 + j] : 1.f) : 0.f;
         alpha_l[e] = v;
     }
     for (int e = tid; e < a.Nt * 128; e += kThreads) {
@@ -255,7 +299,7 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
         const int o0 = 4 * nq;
         f32x4 v;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = (o0 + j < a.out_o) ? a.beta[h * a.out_o + o0 + j] * 0.03125f : 0.f;
+        for (int j = 0; j < 4; ++j) v[j] = (o0 + j < a.out_o) ? a.beta[h * a.beta_h + o0 + j] * 0.03125f : 0.f;
         beta_l[e] = v;
     }
     __syncthreads();
@@ -265,15 +309,22 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
     const int lane = tid & 63;
     const int t = lane & 15;
     const int q = lane >> 4;
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a, esz));
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * esz));
     const int n_tiles = (int)ceil_div(a.M, kTile);
     const int stride = gridDim.x * kWaves;
+    auto contract_any = [&](int nt, int c, const XM<BF16MMA> &xm, f32x4 (&acc)[32]) {
+        if constexpr (DENSE)
+            contract_dense<BF16MMA>(smem + ((size_t)(nt * a.Kc + c) * 32 * 64 + lane) * dense_frag_bytes<BF16MMA>(),
+                                    xm, acc);
+        else
+            contract<BF16MMA>(a, nt, c, lane, xm, lut, acc);
+    };
 
     for (int tile = blockIdx.x * kWaves + wave; tile < n_tiles; tile += stride) {
         const int row = tile * kTile + t;
         const bool row_ok = row < a.M;
-        const uint32_t xoff = (uint32_t)((int64_t)row * a.ldx * esz);
+        const uint32_t xoff = row_ok ? x_row_off(a, row, esz) : 0u;
         const uint32_t yoff = (uint32_t)((int64_t)row * a.ldy * esz);
         if constexpr (KC1) {
             XM<BF16MMA> xm;
@@ -282,7 +333,7 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
                 f32x4 acc[32];
 #pragma unroll
                 for (int g = 0; g < 32; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-                contract<BF16MMA>(a, nt, 0, lane, xm, lut, acc);
+                contract_any(nt, 0, xm, acc);
                 transform_store<T, VEC>(a, acc, yr, yoff, row_ok, nt, q, beta_l);
             }
         } else {
@@ -293,7 +344,7 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
                 for (int c = 0; c < a.Kc; ++c) {
                     XM<BF16MMA> xm;
                     load_transform<T, BF16MMA, VEC>(a, xr, xoff, row_ok, c, q, alpha_l, xm);
-                    contract<BF16MMA>(a, nt, c, lane, xm, lut, acc);
+                    contract_any(nt, c, xm, acc);
                 }
                 transform_store<T, VEC>(a, acc, yr, yoff, row_ok, nt, q, beta_l);
             }
@@ -883,6 +934,38 @@ __global__ __launch_bounds__(256) void fht_kernel(const T *__restrict__ x, int64
     for (int e = threadIdx.x; e < tot; e += blockDim.x) Act<T>::store(y + row0 * N + e, buf[e] * scale);
 }
 
+// Dense weights as A fragments [Nt][Kc][32 g][64 lanes] x 4 values: lane l
+// of (nt, c) holds for group g the weights W[g, o, i..i+3] with
+// o = 16nt + l%16, i = 16c + 4(l/16) (0 past out_o / in_o).  w_io: the
+// source is stored [32][in_o][out_o] (the head mixer's x @ W) instead of
+// [32][out_o][in_o].
+__global__ void hadamard_dense_prepare_kernel(const float *__restrict__ w, int in_o, int out_o, int w_io, int Nt,
+                                              int Kc, int bf16, unsigned char *__restrict__ kw) {
+    const int64_t total = (int64_t)Nt * Kc * 32 * 64;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(e & 63);
+        const int g = (int)((e >> 6) & 31);
+        const int64_t tc = e >> 11;
+        const int c = (int)(tc % Kc);
+        const int nt = (int)(tc / Kc);
+        const int o = kNTile * nt + (lane & 15);
+        const int i0 = kKChunk * c + 4 * (lane >> 4);
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = i0 + j;
+            v[j] = (o < out_o && i < in_o)
+                       ? w[w_io ? ((int64_t)g * in_o + i) * out_o + o : ((int64_t)g * out_o + o) * in_o + i]
+                       : 0.f;
+        }
+        if (bf16)
+            ((uint2 *)kw)[e] = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        else
+            ((f32x4 *)kw)[e] = f32x4{v[0], v[1], v[2], v[3]};
+    }
+}
+
 static size_t hadamard_lds_bytes(bool bf16, int Kc, int Nt) {
     return (bf16 ? lut_bytes<true>() : lut_bytes<false>()) + (size_t)16 * 128 * (Kc + Nt);
 }
@@ -1050,8 +1133,11 @@ static HadArgs had_args(const void *x, int64_t ldx, int64_t gsx, int64_t in_o, i
     a.kw3 = wide3_shape(in_o, out_o) ? kw + weight_bytes1(in_o, out_o) : nullptr;
     a.alpha = alpha;
     a.beta = beta;
+    a.beta_h = (int)out_o;
     a.y = y;
     a.ldy = ldy;
+    a.tpb = 0;
+    a.bstride = 0;
     return a;
 }
 
@@ -1089,6 +1175,80 @@ WALSH_EXPORT int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t g
     const HadArgs ga = had_args(x, ldx, gsx, in_o, hid_o, kw_gate, alpha_gate, beta_gate, h, ldh, gsh);
     const HadArgs ua = had_args(x, ldx, gsx, in_o, hid_o, kw_up, alpha_up, beta_up, h, ldh, gsh);
     return hadamard_launch(fn, ga, &ua, M, dtype == WALSH_BF16, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------- head mixer
+
+constexpr int kDenseMaxO = 32;  // head_dim limit of the dense (LDS-resident) path
+
+WALSH_EXPORT int64_t walsh_hadamard_dense_weight_bytes(int64_t in_o, int64_t out_o, int dtype) {
+    if (in_o <= 0 || out_o <= 0 || (dtype != WALSH_F32 && dtype != WALSH_BF16)) return 0;
+    return ceil_div(out_o, kNTile) * ceil_div(in_o, kKChunk) * 32 * 64 * (dtype == WALSH_BF16 ? 8 : 16);
+}
+
+WALSH_EXPORT int walsh_hadamard_dense_prepare(const float *w, int64_t in_o, int64_t out_o, int w_io, int dtype,
+                                              uint8_t *kweight, void *stream) {
+    const char *fn = "walsh_hadamard_dense_prepare";
+    if (!w || !kweight) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (in_o <= 0 || out_o <= 0 || in_o > 65536 || out_o > 65536)
+        return set_error(WALSH_EINVAL, "%s: bad shape in_o=%lld out_o=%lld", fn, (long long)in_o, (long long)out_o);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype %d", fn, dtype);
+    const int Nt = (int)ceil_div(out_o, kNTile), Kc = (int)ceil_div(in_o, kKChunk);
+    const int64_t total = (int64_t)Nt * Kc * 2048;
+    int grid = (int)ceil_div(total, 256);
+    if (grid > 4096) grid = 4096;
+    launch(hadamard_dense_prepare_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, w, (int)in_o, (int)out_o,
+           w_io ? 1 : 0, Nt, Kc, dtype == WALSH_BF16 ? 1 : 0, (unsigned char *)kweight);
+    return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64_t D, int64_t x_bstride,
+                                      int64_t x_hstride, int64_t x_tstride, const uint8_t *kweight,
+                                      const float *beta, void *y, int64_t ldy, int dtype, void *stream) {
+    const char *fn = "walsh_head_mixer_fwd";
+    if (!x || !y || !kweight || !beta) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (B < 0 || T < 0 || D <= 0 || ldy < 32 * D || x_tstride < D || x_hstride < D)
+        return set_error(WALSH_EINVAL, "%s: bad shape B=%lld T=%lld D=%lld", fn, (long long)B, (long long)T,
+                         (long long)D);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype %d", fn, dtype);
+    if (D > kDenseMaxO) return set_error(WALSH_ENOTSUP, "%s: head_dim %lld > %d", fn, (long long)D, kDenseMaxO);
+    const int64_t M = B * T;
+    if (M == 0) return WALSH_OK;
+    const bool bf16 = dtype == WALSH_BF16;
+    const int64_t esz = bf16 ? 2 : 4;
+    // every offset of x and y stays inside a 31-bit buffer range
+    const int64_t xspan = (B - 1) * x_bstride + 31 * x_hstride + (T - 1) * x_tstride + D;
+    if (xspan * esz > (int64_t)kMaxBufferBytes || M * ldy * esz > (int64_t)kMaxBufferBytes || M > INT32_MAX)
+        return set_error(WALSH_ENOTSUP, "%s: tensors above 2^31 bytes", fn);
+    HadArgs a = had_args(x, x_tstride, x_hstride, D, D, kweight, nullptr, beta, y, ldy, D);
+    a.kw3 = nullptr;
+    a.beta_h = 0;  // one beta row for all heads
+    a.M = (int)M;
+    a.tpb = (int)T;
+    a.bstride = x_bstride;
+    const int Nt = a.Nt, Kc = a.Kc;
+    const size_t lds = (size_t)Nt * Kc * 32 * 64 * (bf16 ? 8 : 16) + (size_t)16 * 128 * (Kc + Nt);
+    if (lds > (size_t)device_info().max_shared_per_block)
+        return set_error(WALSH_ENOTSUP, "%s: head_dim %lld needs %zu B of LDS", fn, (long long)D, lds);
+    const size_t valign = bf16 ? 8 : 16;
+    const bool vec = D % 4 == 0 && x_hstride % 4 == 0 && x_tstride % 4 == 0 && x_bstride % 4 == 0 &&
+                     (uintptr_t)x % valign == 0 && ldy % 4 == 0 && (uintptr_t)y % valign == 0;
+    const bool kc1 = Kc == 1 && (bf16 || Nt == 1);
+    int64_t grid = ceil_div(ceil_div(M, kTile), kWaves);
+    const int64_t cap = (int64_t)device_info().cu_count * 2;
+    if (grid > cap) grid = cap;
+    const dim3 G((unsigned)grid), Bk(kThreads);
+    hipStream_t s = (hipStream_t)stream;
+#define WALSH_MIX_LAUNCH(T_, MMA, V, K1) launch((hadamard_fwd_kernel<T_, MMA, V, K1, true>), G, Bk, lds, s, a)
+    if (bf16) {
+        if (vec) { if (kc1) WALSH_MIX_LAUNCH(uint16_t, true, true, true); else WALSH_MIX_LAUNCH(uint16_t, true, true, false); }
+        else     { if (kc1) WALSH_MIX_LAUNCH(uint16_t, true, false, true); else WALSH_MIX_LAUNCH(uint16_t, true, false, false); }
+    } else {
+        if (vec) { if (kc1) WALSH_MIX_LAUNCH(float, false, true, true); else WALSH_MIX_LAUNCH(float, false, true, false); }
+        else     { if (kc1) WALSH_MIX_LAUNCH(float, false, false, true); else WALSH_MIX_LAUNCH(float, false, false, false); }
+    }
+#undef WALSH_MIX_LAUNCH
+    return check_hip(hipGetLastError(), fn);
 }
 
 WALSH_EXPORT int walsh_fht_fwd(const void *x, int64_t rows, int64_t n, int normalize, void *y, int dtype,

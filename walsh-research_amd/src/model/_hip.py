@@ -38,6 +38,9 @@ SIGNATURES = {
     "walsh_hadamard_swiglu_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                        _I, _P]),
     "walsh_fht_fwd": (_I, [_P, _I64, _I64, _I, _P, _I, _P]),
+    "walsh_hadamard_dense_weight_bytes": (_I64, [_I64, _I64, _I]),
+    "walsh_hadamard_dense_prepare": (_I, [_P, _I64, _I64, _I, _I, _P, _P]),
+    "walsh_head_mixer_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I, _P]),
     "walsh_octonion_weight_elems": (_I64, [_I64, _I64]),
     "walsh_octonion_prepare": (_I, [_P, _I64, _I64, _P, _I, _P]),
     "walsh_octonion_linear_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I, _P]),

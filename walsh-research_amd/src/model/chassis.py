@@ -190,6 +190,14 @@ class CausalSelfAttention(nn.Module):
         if self.head_mixer is not None:
             n_groups = self.n_head // self.mixer_dim
             yg = y.view(B, n_groups, self.mixer_dim, T, self.head_dim)
+            if hasattr(self.head_mixer, "forward_rows") and self.head_mixer.uses_kernel(y):
+                # the mixer kernel writes each group's heads straight into
+                # the token-major rows: no cat and no transpose copy
+                gw = self.mixer_dim * self.head_dim
+                yr = torch.empty(B, T, C, device=y.device, dtype=y.dtype)
+                for g in range(n_groups):
+                    self.head_mixer.forward_rows(yg[:, g], out=yr[:, :, g * gw:(g + 1) * gw])
+                return _full(self.wo, yr.to(dt))
             y = torch.cat([self.head_mixer(yg[:, g]) for g in range(n_groups)], dim=1)
         y = y.transpose(1, 2).contiguous().view(B, T, C).to(dt)
         return _full(self.wo, y)

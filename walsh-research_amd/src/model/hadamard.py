@@ -164,8 +164,13 @@ def fht_reference(x: torch.Tensor) -> torch.Tensor:
 
 
 class HadamardHeadMixerFused(nn.Module):
-    """Hadamard head mixer (fht_cuda.py:627-670), same parameters; runs as
-    torch einsums on the GPU (outside the hot path of this build)."""
+    """Hadamard head mixer (fht_cuda.py:627-662), same parameters.
+
+    On the GPU with head_dim <= 32 it runs walsh_head_mixer_fwd: H over the
+    32 heads, the per-head dense W (bf16 matrix cores under autocast, as the
+    reference's einsums), H again and beta, in one kernel that writes the
+    token-major rows the output projection reads.  Larger head_dim and CPU
+    tensors run the reference's three products as torch matmuls."""
 
     ALGEBRA_DIM = ALGEBRA_DIM
 
@@ -175,10 +180,34 @@ class HadamardHeadMixerFused(nn.Module):
         self.W = nn.Parameter(torch.randn(ALGEBRA_DIM, head_dim, head_dim) * 0.02)
         self.beta = nn.Parameter(torch.ones(head_dim) * math.sqrt(3.0 / (2.0 * head_dim)))
         self.register_buffer('H', hadamard_matrix(ALGEBRA_DIM, normalize=True))
+        self._wcache = WeightCache()
+
+    def uses_kernel(self, x: torch.Tensor) -> bool:
+        return x.is_cuda and self.head_dim <= kernels.HEAD_MIXER_MAX_D
+
+    def _kweight(self, dt: torch.dtype) -> torch.Tensor:
+        return self._wcache.get([self.W], lambda: kernels.head_mixer_prepare(self.W, dt), extra=(dt,))
+
+    def forward_rows(self, x: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+        """x [B, 32, T, D] -> the mixed heads as token-major rows [B, T, 32*D]
+        (written into ``out`` when given, see kernels.head_mixer)."""
+        B, Hh, T, D = x.shape
+        assert Hh == ALGEBRA_DIM
+        if self.uses_kernel(x):
+            dt = x.dtype if x.dtype in (torch.float32, torch.bfloat16) else torch.float32
+            return kernels.head_mixer(x.to(dt), self._kweight(dt), self.beta, out=out)
+        r = self.forward(x).transpose(1, 2).reshape(B, T, Hh * D)
+        if out is not None:
+            out.copy_(r)
+            return out
+        return r
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         B, Hh, T, D = x.shape
         assert Hh == ALGEBRA_DIM
+        if self.uses_kernel(x):
+            # a [B, 32, T, D] view of the token-major result
+            return self.forward_rows(x).view(B, T, Hh, D).transpose(1, 2)
         dt = x.dtype
         H = self.H.to(dt).contiguous()          # symmetric: H^T x == H x
         xf = torch.matmul(H, x.reshape(B, Hh, T * D).contiguous()).view(B, Hh, T, D)

@@ -194,6 +194,55 @@ def fht(x: torch.Tensor, normalize: bool = True) -> torch.Tensor:
     return y
 
 
+# ------------------------------------------------------------------ head mixer
+
+HEAD_MIXER_MAX_D = 32
+
+
+def head_mixer_prepare(W: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Matrix-core fragments of the head mixer's dense W [32, D, D] (applied as
+    x @ W[h]) in ``dtype`` (bf16 or float32)."""
+    _hip.require_device(W, "head mixer weight")
+    assert W.dim() == 3 and W.shape[0] == 32 and W.shape[1] == W.shape[2], f"W shape {tuple(W.shape)}"
+    D = W.shape[1]
+    code = _hip.dtype_code(dtype)
+    n = _hip.lib().walsh_hadamard_dense_weight_bytes(D, D, code)
+    kw = torch.empty(n, device=W.device, dtype=torch.uint8)
+    wf = W.detach().float().contiguous()
+    _hip.call("walsh_hadamard_dense_prepare", wf.data_ptr(), D, D, 1, code, kw.data_ptr(), _hip.stream(W.device))
+    return kw
+
+
+def head_mixer(x: torch.Tensor, kweight: torch.Tensor, beta: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+    """HadamardHeadMixerFused.forward (fht_cuda.py:650-662) on x [B, 32, T, D]
+    (any strides with a unit inner one); returns the token-major [B, T, 32*D]
+    rows (the layout after transpose(1, 2)), written into ``out`` if given (a
+    [B, T, 32*D] view with unit inner stride and stride(0) == T*stride(1),
+    e.g. one head group's columns of a [B, T, n_embd] tensor)."""
+    _hip.require_device(x, "input")
+    B, Hh, T, D = x.shape
+    assert Hh == 32, f"the head mixer takes 32 heads, got {Hh}"
+    dt = x.dtype
+    if x.stride(3) != 1:
+        x = x.contiguous()
+    if out is None:
+        y = torch.empty(B, T, 32 * D, device=x.device, dtype=dt)
+    else:
+        y = out
+        assert tuple(y.shape) == (B, T, 32 * D) and y.dtype == dt and y.stride(2) == 1, "head mixer output view"
+        assert B == 1 or y.stride(0) == T * y.stride(1), "head mixer output rows must be evenly spaced"
+    if B * T == 0:
+        return y
+    b = beta.detach().float().contiguous()
+    esz = x.element_size()
+    nbytes = 2 * B * T * 32 * D * esz + kweight.numel() + 4 * D
+    flops = B * T * (2 * 32 * D * D + 10 * 32 * D + 32 * D)
+    _hip.call("walsh_head_mixer_fwd", x.data_ptr(), B, T, D, x.stride(0), x.stride(1), x.stride(2),
+              kweight.data_ptr(), b.data_ptr(), y.data_ptr(), y.stride(1), _hip.dtype_code(dt), _hip.stream(x.device),
+              kernel="head_mixer<%s>" % ("bf16" if dt == torch.bfloat16 else "f32"), nbytes=nbytes, flops=flops)
+    return y
+
+
 # ------------------------------------------------------------------ octonion
 
 def octonion_prepare(packed: torch.Tensor, in_o: int, out_o: int, dtype: torch.dtype) -> torch.Tensor:
