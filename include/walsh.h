@@ -129,6 +129,17 @@ int walsh_hadamard_linear_ex_fwd(const void *x, int64_t ldx, int64_t gsx, int64_
                                  const uint8_t *kweight, const float *alpha, const float *beta, void *y, int64_t ldy,
                                  int64_t gsy, int dtype, void *stream);
 
+/* walsh_hadamard_linear_rope_fwd: walsh_hadamard_linear_fwd followed by
+ *   apply_rotary_emb (src/model/chassis.py:339-345) on its output, in the
+ *   store: output row r is token t = r % rope_T of a sequence, split into
+ *   heads of head_dim features whose pairs (2i, 2i+1) turn by rope[t][i] =
+ *   (cos, sin) (float32 [rope_T][head_dim/2][2], the view_as_real of the
+ *   freqs_cis rows of the call).  head_dim % 4 == 0 and divides out_o; rows
+ *   and in_o 4-aligned.  Used for the q and k projections. */
+int walsh_hadamard_linear_rope_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                                   const uint8_t *kweight, const float *alpha, const float *beta, const float *rope,
+                                   int64_t rope_T, int64_t head_dim, void *y, int64_t ldy, int dtype, void *stream);
+
 /* walsh_hadamard_swiglu_fwd: h = silu(gate(x)) * up(x) for two Hadamard
  *   linears of the same shape (in_o -> hid_o) on the same input, fused
  *   (SwiGLUMLP.forward, src/model/chassis.py:498-504, gate_proj/up_proj).

@@ -88,6 +88,23 @@ def head_mixer_f64(x, W, beta) -> np.ndarray:
     return yf * np.asarray(beta, np.float64)
 
 
+def rope_f64(y, freqs_cis, head_dim: int) -> np.ndarray:
+    """apply_rotary_emb (``chassis.py:339-345``) on y [B, T, C] in float64:
+    C is split into heads of head_dim features; pair (2i, 2i+1) of a head at
+    token t turns by freqs_cis[t, i] = cos + i sin (complex [T, head_dim/2]):
+    (a, b) -> (a cos - b sin, a sin + b cos).
+    """
+    y = np.asarray(y, dtype=np.float64)
+    B, T, C = y.shape
+    f = np.asarray(freqs_cis)[:T]
+    c = np.real(f).astype(np.float64)[None, :, None, :]
+    s = np.imag(f).astype(np.float64)[None, :, None, :]
+    v = y.reshape(B, T, C // head_dim, head_dim // 2, 2)
+    a, b = v[..., 0], v[..., 1]
+    out = np.stack([a * c - b * s, a * s + b * c], axis=-1)
+    return out.reshape(B, T, C)
+
+
 def hadamard_linear_torch32(x, codes, alpha, beta) -> torch.Tensor:
     """The reference CPU float32 evaluation order (``fht_cuda.py:497-519``).
 

@@ -300,3 +300,31 @@ def test_head_mixer_module_matches_torch_path():
         yb = mg(x.cuda().to(torch.bfloat16))
     assert yb.dtype == torch.bfloat16
     assert_close(yb.float().cpu().numpy(), ref.detach().numpy(), torch.bfloat16, "mixer module bf16")
+
+
+# --------------------------------------------------------------- fused rotary embedding
+
+def _freqs_cis(T, D, start=0):
+    f = 1.0 / (10000.0 ** (torch.arange(0, D, 2)[: D // 2].float() / D))
+    ang = torch.outer(torch.arange(start, start + T).float(), f)
+    return torch.polar(torch.ones_like(ang), ang)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("in_o,out_o,D,B,T", [(16, 16, 16, 2, 40), (16, 16, 8, 3, 7), (128, 128, 128, 2, 37),
+                                                (16, 32, 16, 1, 20), (64, 64, 64, 2, 17)])
+def test_hadamard_linear_rope(K, dtype, in_o, out_o, D, B, T):
+    rng = np.random.default_rng(in_o + out_o + D + T)
+    codes = rng.integers(-1, 2, size=(32, out_o, in_o)).astype(np.int8)
+    alpha = rng.uniform(0.5, 1.5, size=(32, in_o)).astype(np.float32)
+    beta = rng.uniform(0.05, 0.3, size=(32, out_o)).astype(np.float32)
+    x = rng.standard_normal((B, T, 32 * in_o)).astype(np.float32)
+    kw = _prepare(K, codes)
+    xt = torch.from_numpy(x).cuda().to(dtype)
+    fc = _freqs_cis(T, D, start=5)
+    y = K.hadamard_linear_rope(xt, in_o, out_o, kw, torch.from_numpy(alpha).cuda(), torch.from_numpy(beta).cuda(),
+                               fc.cuda(), D)
+    torch.cuda.synchronize()
+    lin = ohad.hadamard_linear_f64(xt.float().cpu().numpy().reshape(B * T, -1), codes, alpha, beta)
+    ref = ohad.rope_f64(lin.reshape(B, T, -1), fc.numpy(), D)
+    assert_close(y.float().cpu().numpy(), ref, dtype, f"rope {dtype} in_o={in_o} out_o={out_o} D={D}")

@@ -116,3 +116,32 @@ def test_head_mixer_equals_hadamard_linear_on_rows():
     ref = hadamard.hadamard_linear_f64(rows, W.transpose(0, 2, 1).astype(np.int8), np.ones((32, D)),
                                        np.broadcast_to(beta, (32, D)))
     assert np.allclose(y.transpose(0, 2, 1, 3).reshape(B * T, 32 * D), ref, atol=1e-10)
+
+
+def _freqs(T, D, theta=10000.0):
+    import torch
+    f = 1.0 / (theta ** (torch.arange(0, D, 2)[: D // 2].float() / D))
+    ang = torch.outer(torch.arange(T).float(), f)
+    return torch.polar(torch.ones_like(ang), ang)
+
+
+def test_rope_matches_complex_multiply():
+    # the real-arithmetic rotation equals torch's complex product
+    import torch
+    rng = np.random.default_rng(9)
+    B, T, H, D = 2, 6, 3, 8
+    y = rng.standard_normal((B, T, H * D)).astype(np.float32)
+    fc = _freqs(T, D)
+    yc = torch.view_as_complex(torch.from_numpy(y).reshape(B, T, H, D // 2, 2))
+    ref = torch.view_as_real(yc * fc[:T].unsqueeze(0).unsqueeze(2)).reshape(B, T, H * D).numpy()
+    assert np.allclose(hadamard.rope_f64(y, fc.numpy(), D), ref, atol=1e-6)
+
+
+def test_rope_position_zero_identity_and_norm():
+    rng = np.random.default_rng(10)
+    y = rng.standard_normal((1, 5, 16))
+    fc = _freqs(5, 8).numpy()
+    r = hadamard.rope_f64(y, fc, 8)
+    assert np.allclose(r[:, 0], y[:, 0])
+    pn = lambda v: np.hypot(v.reshape(1, 5, 8, 2)[..., 0], v.reshape(1, 5, 8, 2)[..., 1])
+    assert np.allclose(pn(r), pn(y))

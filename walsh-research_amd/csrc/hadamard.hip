@@ -94,7 +94,24 @@ struct HadArgs {
     // (r / tpb) * bstride + (r % tpb) * ldx elements
     int tpb;
     int64_t bstride;
+    // rotary embedding on the outputs (null: none): pairs (2i, 2i+1) of each
+    // rope_D-wide head turn by rope[t][i] = (cos, sin), t = row % rope_T
+    const float *rope;
+    int rope_T, rope_D;
+    int rope_row0;  // row 0 of this launch is row rope_row0 of a sequence
 };
+
+// The (cos, sin) of the lane's two output pairs o0..o0+3 (o0 % 4 == 0,
+// rope_D % 4 == 0, out_o % rope_D == 0: the same pairs in every group).
+__device__ __forceinline__ f32x4 rope_cs(const HadArgs &a, int row, int o0) {
+    const int t = (row + a.rope_row0) % a.rope_T, i0 = (o0 % a.rope_D) >> 1;
+    return *(const f32x4 *)(a.rope + ((int64_t)t * (a.rope_D >> 1) + i0) * 2);
+}
+
+__device__ __forceinline__ f32x4 rope_apply(f32x4 r, f32x4 cs) {
+    return f32x4{r[0] * cs[0] - r[1] * cs[1], r[0] * cs[1] + r[1] * cs[0], r[2] * cs[2] - r[3] * cs[3],
+                 r[2] * cs[3] + r[3] * cs[2]};
+}
 
 __device__ __forceinline__ uint32_t x_row_off(const HadArgs &a, int row, uint32_t esz) {
     const int64_t e = a.tpb ? (int64_t)(row / a.tpb) * a.bstride + (int64_t)(row % a.tpb) * a.ldx : (int64_t)row * a.ldx;
@@ -205,18 +222,29 @@ __device__ __forceinline__ void contract(const HadArgs &a, int nt, int c, int la
 template <typename T, bool VEC>
 __device__ __forceinline__ void transform_store(const HadArgs &a, f32x4 (&acc)[32], __amdgpu_buffer_rsrc_t yr,
                                                 uint32_t row_off, bool row_ok, int nt, int q,
-                                                const f32x4 *__restrict__ beta_l) {
+                                                const f32x4 *__restrict__ beta_l, int row) {
     constexpr uint32_t esz = sizeof(T);
     fht32x4(acc);
     const int o0 = kNTile * nt + 4 * q;
     const uint32_t hstride = (uint32_t)a.gsy * esz;
     const f32x4 *bl = beta_l + (nt * 4 + q) * 32;
     if (VEC) {
-        const uint32_t voff = (row_ok && o0 < a.out_o) ? row_off + (uint32_t)o0 * esz : kOOB;
+        const bool ok = row_ok && o0 < a.out_o;
+        const uint32_t voff = ok ? row_off + (uint32_t)o0 * esz : kOOB;
+        if (a.rope) {
+            // the same two (cos, sin) pairs for all 32 groups of the row
+            const f32x4 cs = ok ? rope_cs(a, row, o0) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int h = 0; h < 32; ++h) {
-            Buf4<T>::store(acc[h] * bl[h], yr, voff, (uint32_t)h * hstride);
-            if ((h & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+            for (int h = 0; h < 32; ++h) {
+                Buf4<T>::store(rope_apply(acc[h] * bl[h], cs), yr, voff, (uint32_t)h * hstride);
+                if ((h & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 32; ++h) {
+                Buf4<T>::store(acc[h] * bl[h], yr, voff, (uint32_t)h * hstride);
+                if ((h & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+            }
         }
     } else {
         uint32_t voff[4];
@@ -334,7 +362,7 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
 #pragma unroll
                 for (int g = 0; g < 32; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
                 contract_any(nt, 0, xm, acc);
-                transform_store<T, VEC>(a, acc, yr, yoff, row_ok, nt, q, beta_l);
+                transform_store<T, VEC>(a, acc, yr, yoff, row_ok, nt, q, beta_l, row);
             }
         } else {
             for (int nt = 0; nt < a.Nt; ++nt) {
@@ -346,7 +374,7 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
                     load_transform<T, BF16MMA, VEC>(a, xr, xoff, row_ok, c, q, alpha_l, xm);
                     contract_any(nt, c, xm, acc);
                 }
-                transform_store<T, VEC>(a, acc, yr, yoff, row_ok, nt, q, beta_l);
+                transform_store<T, VEC>(a, acc, yr, yoff, row_ok, nt, q, beta_l, row);
             }
         }
     }
@@ -494,7 +522,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide_kernel(HadArgs 
             }
             __syncthreads();
         }
-        if (nt < a.Nt) transform_store<T, true>(a, acc, yr, yoff, row_ok, nt, q, beta_l + (wave - nt) * 128);
+        if (nt < a.Nt) transform_store<T, true>(a, acc, yr, yoff, row_ok, nt, q, beta_l + (wave - nt) * 128, row);
     }
 }
 
@@ -696,6 +724,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs
             // of a write fall on different banks)
             fht32x4(acc);
             unsigned char *od = ostage + t * kW3ORow + (kNTile * wave + 4 * q) * 2;
+            const int orow = tile * kTile + t, o0 = kNTile * wave + 4 * q;
+            // rotary embedding: the same two (cos, sin) pairs for all 32 groups
+            const bool rope = a.rope != nullptr;
+            const f32x4 cs = (rope && orow < a.M && o0 < a.out_o) ? rope_cs(a, orow, o0) : f32x4{1.f, 0.f, 1.f, 0.f};
 #pragma unroll
             for (int h0 = 0; h0 < 32; h0 += 8) {
                 uint2 b8[8];  // beta of 8 output groups, read together
@@ -704,7 +736,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const _Float16 *b = (const _Float16 *)&b8[j];
-                    const f32x4 r = acc[h0 + j] * f32x4{(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
+                    f32x4 r = acc[h0 + j] * f32x4{(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
+                    if (rope) r = rope_apply(r, cs);
                     *(uint2 *)(od + (h0 + j) * kW3MaxO * 2) = uint2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
                 }
             }
@@ -1060,6 +1093,7 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
         HadArgs a = base;
         a.x = (const char *)base.x + r0 * base.ldx * esz;
+        a.rope_row0 = (int)(r0 % base.rope_T);
         a.y = (char *)base.y + r0 * base.ldy * esz;
         a.M = (int)rows;
         int64_t work = ceil_div(rows, kTile) * (swiglu ? Nt : 1);
@@ -1138,6 +1172,10 @@ static HadArgs had_args(const void *x, int64_t ldx, int64_t gsx, int64_t in_o, i
     a.ldy = ldy;
     a.tpb = 0;
     a.bstride = 0;
+    a.rope = nullptr;
+    a.rope_T = 1;
+    a.rope_D = 4;
+    a.rope_row0 = 0;
     return a;
 }
 
@@ -1159,6 +1197,27 @@ WALSH_EXPORT int walsh_hadamard_linear_fwd(const void *x, int64_t ldx, int64_t M
                                            int64_t ldy, int dtype, void *stream) {
     return walsh_hadamard_linear_ex_fwd(x, ldx, in_o, M, in_o, out_o, kweight, alpha, beta, y, ldy, out_o, dtype,
                                         stream);
+}
+
+WALSH_EXPORT int walsh_hadamard_linear_rope_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                                                const uint8_t *kweight, const float *alpha, const float *beta,
+                                                const float *rope, int64_t rope_T, int64_t head_dim, void *y,
+                                                int64_t ldy, int dtype, void *stream) {
+    const char *fn = "walsh_hadamard_linear_rope_fwd";
+    int rc = hadamard_check(fn, x, ldx, in_o, M, in_o, out_o, y, ldy, out_o, dtype);
+    if (rc) return rc;
+    if (!kweight || !alpha || !beta || !rope) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (rope_T < 1 || head_dim < 4 || head_dim % 4 || out_o % head_dim || (uintptr_t)rope % 16)
+        return set_error(WALSH_ENOTSUP, "%s: needs head_dim %% 4 == 0 dividing out_o, 16-byte aligned table", fn);
+    const size_t valign = dtype == WALSH_BF16 ? 8 : 16;
+    if (ldx % 4 || ldy % 4 || in_o % 4 || (uintptr_t)x % valign || (uintptr_t)y % valign)
+        return set_error(WALSH_ENOTSUP, "%s: needs 4-aligned rows and in_o", fn);
+    if (M == 0) return WALSH_OK;
+    HadArgs a = had_args(x, ldx, in_o, in_o, out_o, kweight, alpha, beta, y, ldy, out_o);
+    a.rope = rope;
+    a.rope_T = (int)rope_T;
+    a.rope_D = (int)head_dim;
+    return hadamard_launch(fn, a, nullptr, M, dtype == WALSH_BF16, (hipStream_t)stream);
 }
 
 WALSH_EXPORT int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t gsx, int64_t M, int64_t in_o,

@@ -168,10 +168,20 @@ class CausalSelfAttention(nn.Module):
         B, T, C = x.size()
         dt = act_dtype(x)
         x = x.to(dt)
-        q = _full(self.wq, x).view(B, T, self.n_head, self.head_dim)
-        k = _full(self.wk, x).view(B, T, self.n_head, self.head_dim)
-        v = _full(self.wv, x).view(B, T, self.n_head, self.head_dim)
-        q, k = apply_rotary_emb(q, k, freqs_cis)
+        q = k = None
+        if hasattr(self.wq, "forward_full_rope") and freqs_cis.shape[0] >= T:
+            # the rotary embedding rides on the q and k projections' stores
+            q = self.wq.forward_full_rope(x, freqs_cis, self.head_dim)
+            k = self.wk.forward_full_rope(x, freqs_cis, self.head_dim) if q is not None else None
+        if q is not None and k is not None:
+            q = q.view(B, T, self.n_head, self.head_dim)
+            k = k.view(B, T, self.n_head, self.head_dim)
+            v = _full(self.wv, x).view(B, T, self.n_head, self.head_dim)
+        else:
+            q = _full(self.wq, x).view(B, T, self.n_head, self.head_dim)
+            k = _full(self.wk, x).view(B, T, self.n_head, self.head_dim)
+            v = _full(self.wv, x).view(B, T, self.n_head, self.head_dim)
+            q, k = apply_rotary_emb(q, k, freqs_cis)
         if kv_cache is not None:
             k, v = kv_cache.update(layer_idx, k, v)
         q = q.transpose(1, 2)

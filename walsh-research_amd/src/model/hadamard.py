@@ -138,6 +138,17 @@ class HadamardTernaryLinearTuple(nn.Module):
         (the same result as split -> forward -> cat, without the copies)."""
         return self.inner._apply_2d(x, act_dtype(x))
 
+    def forward_full_rope(self, x: torch.Tensor, freqs_cis: torch.Tensor, head_dim: int):
+        """forward_full on x [B, T, C] with apply_rotary_emb (chassis.py:339-345)
+        fused into the store, or None when the shapes do not allow it."""
+        inner = self.inner
+        if x.dim() != 3 or not kernels.rope_supported(x, inner.out_o, head_dim):
+            return None
+        dt = act_dtype(x)
+        _, _, kw = inner.ternary_state()
+        return kernels.hadamard_linear_rope(x if x.dtype == dt else x.to(dt), inner.in_o, inner.out_o, kw,
+                                           inner.alpha, inner.beta, freqs_cis, head_dim)
+
     def forward(self, x_parts: tuple) -> tuple:
         assert len(x_parts) == ALGEBRA_DIM, f"Expected {ALGEBRA_DIM} parts, got {len(x_parts)}"
         x = adjacent_parts_view(x_parts, self.in_o)

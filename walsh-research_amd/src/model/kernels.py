@@ -117,6 +117,42 @@ def _had_meta(rows, in_o, out_o, dt, vec, kc1, swiglu=False):
     return kname, nbytes, flops
 
 
+def rope_supported(x: torch.Tensor, out_o: int, head_dim: int) -> bool:
+    """Can the rotary embedding ride on a Hadamard linear's store?"""
+    return (x.is_cuda and head_dim >= 4 and head_dim % 4 == 0 and out_o % head_dim == 0
+            and x.shape[-1] % 4 == 0 and x.stride(-1) == 1)
+
+
+def hadamard_linear_rope(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tensor, alpha: torch.Tensor,
+                         beta: torch.Tensor, freqs_cis: torch.Tensor, head_dim: int) -> torch.Tensor:
+    """HadamardLinear forward followed by apply_rotary_emb (chassis.py:339-345)
+    on x [B, T, C]: row (b, t) turns by freqs_cis[t] (complex [T, head_dim/2])."""
+    _hip.require_device(x, "input")
+    dt = x.dtype
+    B, T = x.shape[0], x.shape[1]
+    xv, rows, ldx = _rows_view(x, 32 * in_o)
+    if xv.data_ptr() % (4 * x.element_size()) or ldx % 4:
+        xv = xv.contiguous()
+        ldx = xv.stride(0)
+    y = torch.empty(x.shape[:-1] + (32 * out_o,), device=x.device, dtype=dt)
+    if rows == 0:
+        return y
+    table = torch.view_as_real(freqs_cis[:T].contiguous())
+    assert table.shape == (T, head_dim // 2, 2) and table.dtype == torch.float32, "freqs_cis shape"
+    alpha = alpha.detach().float().contiguous()
+    beta = beta.detach().float().contiguous()
+    vec = True
+    kc1 = in_o <= 16
+    kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, vec, kc1)
+    if in_o > 16 and out_o > 48:
+        kname = "hadamard_wide3_kernel<bf16>" if dt == torch.bfloat16 and in_o <= 128 and out_o <= 128 else \
+            "hadamard_wide_kernel<%s>" % ("bf16" if dt == torch.bfloat16 else "f32")
+    _hip.call("walsh_hadamard_linear_rope_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, kweight.data_ptr(),
+              alpha.data_ptr(), beta.data_ptr(), table.data_ptr(), T, head_dim, y.data_ptr(), 32 * out_o,
+              _hip.dtype_code(dt), _hip.stream(x.device), kernel=kname, nbytes=nbytes, flops=flops)
+    return y
+
+
 def hadamard_linear(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tensor, alpha: torch.Tensor,
                     beta: torch.Tensor, out_dtype: torch.dtype = None, gsx: int = None,
                     gsy: int = None) -> torch.Tensor:
