@@ -169,7 +169,8 @@ int walsh_hadamard_dense_prepare(const float *w, int64_t in_o, int64_t out_o, in
  *   h*D: the layout the output projection reads, so no transpose copy is
  *   needed.  y = beta[d] * H (H x W[h]) over the head axis, H the normalised
  *   32-point Hadamard matrix.  kweight from walsh_hadamard_dense_prepare with
- *   w_io = 1 and the same dtype.  head_dim (D) <= 32. */
+ *   w_io = 1 and the same dtype.  head_dim (D) <= 32, or, in bf16,
+ *   D <= 128 with 4-aligned strides (the wide kernel streams the weights). */
 int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64_t D, int64_t x_bstride, int64_t x_hstride,
                          int64_t x_tstride, const uint8_t *kweight, const float *beta, void *y, int64_t ldy, int dtype,
                          void *stream);

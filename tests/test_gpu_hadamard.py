@@ -328,3 +328,20 @@ def test_hadamard_linear_rope(K, dtype, in_o, out_o, D, B, T):
     lin = ohad.hadamard_linear_f64(xt.float().cpu().numpy().reshape(B * T, -1), codes, alpha, beta)
     ref = ohad.rope_f64(lin.reshape(B, T, -1), fc.numpy(), D)
     assert_close(y.float().cpu().numpy(), ref, dtype, f"rope {dtype} in_o={in_o} out_o={out_o} D={D}")
+
+
+@pytest.mark.parametrize("B,T,D", [(2, 40, 128), (1, 17, 64), (3, 5, 96), (1, 300, 128)])
+def test_head_mixer_wide_bf16(K, B, T, D):
+    # head_dim above 32 in bf16: the wide kernel with streamed dense weights
+    rng = np.random.default_rng(B + T + D)
+    x = rng.standard_normal((B, 32, T, D)).astype(np.float32)
+    W = (rng.standard_normal((32, D, D)) * 0.05).astype(np.float32)
+    beta = rng.uniform(0.1, 0.5, size=D).astype(np.float32)
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    Wt = torch.from_numpy(W).cuda()
+    kw = K.head_mixer_prepare(Wt, torch.bfloat16)
+    y = K.head_mixer(xt, kw, torch.from_numpy(beta).cuda())
+    torch.cuda.synchronize()
+    Wq = Wt.to(torch.bfloat16).float().cpu().numpy()
+    ref = ohad.head_mixer_f64(xt.float().cpu().numpy(), Wq, beta).transpose(0, 2, 1, 3).reshape(B, T, 32 * D)
+    assert_close(y.float().cpu().numpy(), ref, torch.bfloat16, f"wide mixer B={B} T={T} D={D}")

@@ -608,7 +608,10 @@ __device__ __forceinline__ void wide3_load_x(__amdgpu_buffer_rsrc_t xr, uint32_t
 
 // GS: 128 for in_o = out_o = 128 with unpadded groups (the n_embd 4096
 // layers: strides fixed at compile time), 0 for any other shape.
-template <int GS>
+// DENSE: dense bf16 weights (the head mixer at head_dim 128) as 16x16x32
+// A fragments [Nt][Kc32][32 g][64 lanes] x 16 bytes, streamed from global
+// memory a few groups ahead of their products, instead of the code table.
+template <int GS, bool DENSE = false>
 __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     uint2 *lut = (uint2 *)smem;                                          // [81 entries][16 copies]
@@ -617,7 +620,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs
     uint4 *xs = (uint4 *)(smem + kW3LutBytes + kW3AlphaBytes + kW3BetaBytes);  // [Kc32][32 g][64 lanes]
     unsigned char *ostage = (unsigned char *)xs;  // after the products: the output tile
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane & 15, q = lane >> 4;
-    for (int e = tid; e < kW3Entries * kW3Copies; e += kWideThreads) {
+    for (int e = tid; e < (DENSE ? 0 : kW3Entries * kW3Copies); e += kWideThreads) {
         int r = e / kW3Copies;
         float val[4];
 #pragma unroll
@@ -629,11 +632,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs
     }
     for (int e = tid; e < 32 * kW3MaxO; e += kWideThreads) {
         const int g = e / kW3MaxO, i = e % kW3MaxO;
-        alpha_l[e] = (_Float16)(i < a.in_o ? a.alpha[g * a.in_o + i] : 0.f);
+        // the two transforms' 1/32 rides on the code table; dense weights
+        // carry no such factor, so it goes on alpha (exact: a power of two)
+        const float a32 = DENSE ? 0.03125f : 1.f;
+        alpha_l[e] = (_Float16)(i < a.in_o ? (a.alpha ? a.alpha[g * a.in_o + i] : 1.f) * a32 : 0.f);
         const int o = kNTile * (e >> 9) + (e & 15), h = (e >> 4) & 31;  // e = (nt*32 + h)*16 + o%16
-        beta_l[e] = (_Float16)(o < a.out_o ? a.beta[h * a.out_o + o] : 0.f);
+        beta_l[e] = (_Float16)(o < a.out_o ? a.beta[h * a.beta_h + o] : 0.f);
     }
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * 2));
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a, 2));
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
     const int n_tiles = (int)ceil_div(a.M, kTile);
     const int Kc32 = (a.in_o + 31) >> 5;
@@ -647,12 +653,15 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs
     // accumulators in registers across the barriers); a wave past the last
     // output tile reads tile 0's weights and its results are never stored
     const int wt = wave < a.Nt ? wave : 0;
-    const uint4 *wsrc = (const uint4 *)(a.kw3 + ((int64_t)wt * Kc32 * 64 + lane) * 64);
+    const uint4 *wsrc = DENSE ? nullptr : (const uint4 *)(a.kw3 + ((int64_t)wt * Kc32 * 64 + lane) * 64);
+    const uint4 *wdn = DENSE ? (const uint4 *)a.kw + (int64_t)wt * Kc32 * 32 * 64 + lane : nullptr;  // + (c*32+g)*64
+    constexpr int RD = 4;  // DENSE: fragments in flight ahead of their products
+    uint4 ring[RD];
     const _Float16 *bl = beta_l + wave * 512 + 4 * q;
     const _Float16 *al = alpha_l + i0;
     auto x_off = [&](int tile) -> uint32_t {
         const int row = tile * kTile + t;
-        return (row < a.M && i0 < a.in_o) ? (uint32_t)((int64_t)row * a.ldx * 2) + (uint32_t)i0 * 2 : kOOB;
+        return (row < a.M && i0 < a.in_o) ? x_row_off(a, row, 2) + (uint32_t)i0 * 2 : kOOB;
     };
     // x of the first tile; later tiles are loaded during the contraction of
     // the one before, so their load latency overlaps the matrix work
@@ -677,13 +686,40 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs
                 for (int g = 0; g < 32; ++g) ((uint32_t *)&xdst[g * 128])[p] = pack_bf16x2(v[g][0], v[g][1]);
             }
         }
+        if (DENSE) {
+            // the first fragments load while the other waves finish their
+            // transforms
+#pragma unroll
+            for (int j = 0; j < RD; ++j) ring[j] = wdn[j * 64];
+        }
         lds_barrier();
         f32x4 acc[32];
         const bool pf = xwave && next < n_tiles;
         const uint32_t pf_off = pf ? x_off(next) : kOOB;
-        {
 #pragma unroll
-            for (int g = 0; g < 32; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int g = 0; g < 32; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (DENSE) {
+            for (int c = 0; c < Kc32; ++c) {
+                const uint4 *xsrc = xs + (size_t)c * 32 * 64 + lane;
+                const bool more = c + 1 < Kc32;
+#pragma unroll
+                for (int g = 0; g < 32; ++g) {
+                    const uint4 wa = ring[g % RD];
+                    if (g == 32 - RD && !more) {
+                        // the tile's last weight load is issued: the next
+                        // tile's x (groups 0-15) follows without holding
+                        // up any weight wait
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (pf) wide3_load_x<0, 16>(xr, pf_off, gstride, xraw);
+                    }
+                    if (g < 32 - RD) ring[g % RD] = wdn[(c * 32 + g + RD) * 64];
+                    else if (more) ring[g % RD] = wdn[((c + 1) * 32 + g - (32 - RD)) * 64];
+                    const uint4 xb = xsrc[g * 64];
+                    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wa),
+                                                                     __builtin_bit_cast(bf16x8, xb), acc[g], 0, 0, 0);
+                }
+            }
+        } else {
             // one 32-column chunk: 32 products
             auto chunk = [&](int c, const uint4 (&w)[4]) {
                 const uint4 *xsrc = xs + (size_t)c * 32 * 64 + lane;
@@ -972,6 +1008,34 @@ __global__ __launch_bounds__(256) void fht_kernel(const T *__restrict__ x, int64
 // o = 16nt + l%16, i = 16c + 4(l/16) (0 past out_o / in_o).  w_io: the
 // source is stored [32][in_o][out_o] (the head mixer's x @ W) instead of
 // [32][out_o][in_o].
+// Wide layout (bf16 with 32 < in_o <= 128, out_o <= 128: the wide kernel's
+// 16x16x32 products): [Nt][in_o/32][32 g][64 lanes] x 8 values, lane l of
+// (nt, c) holding W[g, 16nt + l%16, 32c + 8(l/16) .. +7].
+__global__ void hadamard_dense_prepare32_kernel(const float *__restrict__ w, int in_o, int out_o, int w_io, int Nt,
+                                                int Kc32, uint4 *__restrict__ kw) {
+    const int64_t total = (int64_t)Nt * Kc32 * 32 * 64;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(e & 63);
+        const int g = (int)((e >> 6) & 31);
+        const int64_t tc = e >> 11;
+        const int c = (int)(tc % Kc32);
+        const int nt = (int)(tc / Kc32);
+        const int o = kNTile * nt + (lane & 15);
+        const int i0 = 32 * c + 8 * (lane >> 4);
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = i0 + j;
+            v[j] = (o < out_o && i < in_o)
+                       ? w[w_io ? ((int64_t)g * in_o + i) * out_o + o : ((int64_t)g * out_o + o) * in_o + i]
+                       : 0.f;
+        }
+        kw[e] = uint4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                      pack_bf16x2(v[6], v[7])};
+    }
+}
+
 __global__ void hadamard_dense_prepare_kernel(const float *__restrict__ w, int in_o, int out_o, int w_io, int Nt,
                                               int Kc, int bf16, unsigned char *__restrict__ kw) {
     const int64_t total = (int64_t)Nt * Kc * 32 * 64;
@@ -1238,10 +1302,16 @@ WALSH_EXPORT int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t g
 
 // ---------------------------------------------------------------- head mixer
 
-constexpr int kDenseMaxO = 32;  // head_dim limit of the dense (LDS-resident) path
+constexpr int kDenseMaxO = 32;  // head_dim limit of the LDS-resident dense path
+
+// bf16 shapes that take the wide kernel (weights streamed from memory)
+static bool dense_wide(int64_t in_o, int64_t out_o, int dtype) {
+    return dtype == WALSH_BF16 && in_o > kDenseMaxO && in_o <= kW3MaxO && out_o > kDenseMaxO && out_o <= kW3MaxO;
+}
 
 WALSH_EXPORT int64_t walsh_hadamard_dense_weight_bytes(int64_t in_o, int64_t out_o, int dtype) {
     if (in_o <= 0 || out_o <= 0 || (dtype != WALSH_F32 && dtype != WALSH_BF16)) return 0;
+    if (dense_wide(in_o, out_o, dtype)) return ceil_div(out_o, kNTile) * ceil_div(in_o, 32) * 32 * 64 * 16;
     return ceil_div(out_o, kNTile) * ceil_div(in_o, kKChunk) * 32 * 64 * (dtype == WALSH_BF16 ? 8 : 16);
 }
 
@@ -1256,8 +1326,12 @@ WALSH_EXPORT int walsh_hadamard_dense_prepare(const float *w, int64_t in_o, int6
     const int64_t total = (int64_t)Nt * Kc * 2048;
     int grid = (int)ceil_div(total, 256);
     if (grid > 4096) grid = 4096;
-    launch(hadamard_dense_prepare_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, w, (int)in_o, (int)out_o,
-           w_io ? 1 : 0, Nt, Kc, dtype == WALSH_BF16 ? 1 : 0, (unsigned char *)kweight);
+    if (dense_wide(in_o, out_o, dtype))
+        launch(hadamard_dense_prepare32_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, w, (int)in_o,
+               (int)out_o, w_io ? 1 : 0, Nt, (int)ceil_div(in_o, 32), (uint4 *)kweight);
+    else
+        launch(hadamard_dense_prepare_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, w, (int)in_o,
+               (int)out_o, w_io ? 1 : 0, Nt, Kc, dtype == WALSH_BF16 ? 1 : 0, (unsigned char *)kweight);
     return check_hip(hipGetLastError(), fn);
 }
 
@@ -1270,7 +1344,10 @@ WALSH_EXPORT int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64
         return set_error(WALSH_EINVAL, "%s: bad shape B=%lld T=%lld D=%lld", fn, (long long)B, (long long)T,
                          (long long)D);
     if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype %d", fn, dtype);
-    if (D > kDenseMaxO) return set_error(WALSH_ENOTSUP, "%s: head_dim %lld > %d", fn, (long long)D, kDenseMaxO);
+    const bool wide = dense_wide(D, D, dtype);
+    if (D > kDenseMaxO && !wide)
+        return set_error(WALSH_ENOTSUP, "%s: head_dim %lld needs bf16 and <= %d (or <= %d)", fn, (long long)D,
+                         kW3MaxO, kDenseMaxO);
     const int64_t M = B * T;
     if (M == 0) return WALSH_OK;
     const bool bf16 = dtype == WALSH_BF16;
@@ -1285,6 +1362,18 @@ WALSH_EXPORT int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64
     a.M = (int)M;
     a.tpb = (int)T;
     a.bstride = x_bstride;
+    if (wide) {
+        if (D % 4 || x_hstride % 4 || x_tstride % 4 || x_bstride % 4 || ldy % 4 || (uintptr_t)x % 8 ||
+            (uintptr_t)y % 8)
+            return set_error(WALSH_ENOTSUP, "%s: head_dim %lld needs 4-aligned strides", fn, (long long)D);
+        const size_t lds = wide3_lds_bytes((int)ceil_div(D, 32));
+        if (lds > (size_t)device_info().max_shared_per_block)
+            return set_error(WALSH_ENOTSUP, "%s: needs %zu B of LDS", fn, lds);
+        const int64_t items = ceil_div(M, kTile), cap = (int64_t)device_info().cu_count;
+        launch(hadamard_wide3_kernel<0, true>, dim3((unsigned)(items < cap ? items : cap)), dim3(kWideThreads), lds,
+               (hipStream_t)stream, a);
+        return check_hip(hipGetLastError(), fn);
+    }
     const int Nt = a.Nt, Kc = a.Kc;
     const size_t lds = (size_t)Nt * Kc * 32 * 64 * (bf16 ? 8 : 16) + (size_t)16 * 128 * (Kc + Nt);
     if (lds > (size_t)device_info().max_shared_per_block)

@@ -177,11 +177,12 @@ def fht_reference(x: torch.Tensor) -> torch.Tensor:
 class HadamardHeadMixerFused(nn.Module):
     """Hadamard head mixer (fht_cuda.py:627-662), same parameters.
 
-    On the GPU with head_dim <= 32 it runs walsh_head_mixer_fwd: H over the
-    32 heads, the per-head dense W (bf16 matrix cores under autocast, as the
-    reference's einsums), H again and beta, in one kernel that writes the
-    token-major rows the output projection reads.  Larger head_dim and CPU
-    tensors run the reference's three products as torch matmuls."""
+    On the GPU with head_dim <= 32 (or <= 128 in bf16) it runs
+    walsh_head_mixer_fwd: H over the 32 heads, the per-head dense W (bf16
+    matrix cores under autocast, as the reference's einsums), H again and
+    beta, in one kernel that writes the token-major rows the output
+    projection reads.  Other shapes and CPU tensors run the reference's three
+    products as torch matmuls."""
 
     ALGEBRA_DIM = ALGEBRA_DIM
 
@@ -194,7 +195,8 @@ class HadamardHeadMixerFused(nn.Module):
         self._wcache = WeightCache()
 
     def uses_kernel(self, x: torch.Tensor) -> bool:
-        return x.is_cuda and self.head_dim <= kernels.HEAD_MIXER_MAX_D
+        dt = x.dtype if x.dtype in (torch.float32, torch.bfloat16) else torch.float32
+        return x.is_cuda and kernels.head_mixer_supported(self.head_dim, dt)
 
     def _kweight(self, dt: torch.dtype) -> torch.Tensor:
         return self._wcache.get([self.W], lambda: kernels.head_mixer_prepare(self.W, dt), extra=(dt,))

@@ -232,7 +232,12 @@ def fht(x: torch.Tensor, normalize: bool = True) -> torch.Tensor:
 
 # ------------------------------------------------------------------ head mixer
 
-HEAD_MIXER_MAX_D = 32
+HEAD_MIXER_MAX_D = 32        # any dtype (weights resident in LDS)
+HEAD_MIXER_MAX_D_BF16 = 128  # bf16 (weights streamed, the wide kernel)
+
+
+def head_mixer_supported(D: int, dtype: torch.dtype) -> bool:
+    return D <= HEAD_MIXER_MAX_D or (dtype == torch.bfloat16 and D <= HEAD_MIXER_MAX_D_BF16 and D % 4 == 0)
 
 
 def head_mixer_prepare(W: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
