@@ -175,6 +175,40 @@ int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64_t D, int64_t
                          int64_t x_tstride, const uint8_t *kweight, const float *beta, void *y, int64_t ldy, int dtype,
                          void *stream);
 
+/* ------------------------------------------------------------------ backward
+ * Autograd of HadamardLinear.forward (src/model/fht_cuda.py:489-519) through
+ * FHTFunction.backward (fht_cuda.py:328-332, H self-adjoint) and the
+ * straight-through estimator of physics.quantize_ternary
+ * (src/model/physics.py:43-50): replaces the torch autograd graph the
+ * reference builds for the layer.
+ *
+ * walsh_hadamard_pack_transpose: the reference 2-bit packing (fht_cuda.py:
+ *   65-93) of the transposed codes, packed_t [32][in_o][ceil(out_o/4)] from
+ *   packed [32][out_o][ceil(in_o/4)].  walsh_hadamard_prepare(packed_t,
+ *   out_o, in_o, kweight_t) then gives the transposed layer's kernel layout.
+ * walsh_hadamard_bwd_workspace_bytes: device scratch walsh_hadamard_linear_bwd
+ *   needs for M dense rows (row strides 32*in_o / 32*out_o).
+ * walsh_hadamard_linear_bwd: for the output gradient gy [M, ldg] of
+ *   y = beta .* H W H (alpha .* x), x [M, ldx]:
+ *     gx     = alpha .* H W^T H (beta .* gy)          [M, ldgx], x's dtype
+ *     dalpha = sum_rows x .* H W^T H (beta .* gy)      float [32][in_o]
+ *     dbeta  = sum_rows gy .* H W H (alpha .* x)       float [32][out_o]
+ *     dweight = sum_rows H(beta .* gy)_g (x) H(alpha .* x)_g, times
+ *              [-1.5 <= latent <= 1.5] when latent (float [32][out_o][in_o])
+ *              is given (the STE's clamp): float [32][out_o][in_o]
+ *   Any of gx / dalpha / dbeta / dweight may be null (not computed).
+ *   kweight (forward layout) is needed for dbeta, kweight_t for gx / dalpha.
+ *   Sums run in a fixed order (identical results run to run).  The outputs
+ *   are overwritten, not accumulated. */
+int walsh_hadamard_pack_transpose(const uint8_t *packed, int64_t in_o, int64_t out_o, uint8_t *packed_t,
+                                  void *stream);
+int64_t walsh_hadamard_bwd_workspace_bytes(int64_t M, int64_t in_o, int64_t out_o, int dtype);
+int walsh_hadamard_linear_bwd(const void *x, int64_t ldx, const void *gy, int64_t ldg, int64_t M, int64_t in_o,
+                              int64_t out_o, const uint8_t *kweight, const uint8_t *kweight_t, const float *alpha,
+                              const float *beta, const float *latent, void *gx, int64_t ldgx, float *dalpha,
+                              float *dbeta, float *dweight, int dtype, void *workspace, int64_t workspace_bytes,
+                              void *stream);
+
 /* walsh_fht_fwd: fast Walsh-Hadamard transform of `rows` contiguous rows of
  *   length n (power of two <= 16384), Sylvester order, scaled by 1/sqrt(n)
  *   when `normalize` (fht_butterfly / fht, src/model/fht_cuda.py:281-337). */

@@ -154,3 +154,40 @@ def init_weight(out_o: int, in_o: int, gen: torch.Generator) -> torch.Tensor:
 def beta_init(in_o: int) -> float:
     """Variance-preserving beta init sqrt(3 / (2 in_o)) (``fht_cuda.py:475-476``)."""
     return math.sqrt(3.0 / (2.0 * in_o))
+
+
+def hadamard_linear_bwd_f64(x, codes, alpha, beta, gy, latent=None):
+    """Float64 gradients of ``hadamard_linear_f64`` for the output gradient gy.
+
+    The autograd the reference builds for ``fht_cuda.py:497-519``:
+    FHTFunction.backward is the same normalised transform (``:328-332``, H
+    symmetric), the einsum's gradients are the transposed contractions, and
+    the weight gradient passes physics.quantize_ternary's STE, whose only
+    differentiable path is ``w.clamp(-1.5, 1.5)`` (``physics.py:48-50``):
+    dlatent = dW_q * [-1.5 <= latent <= 1.5] when ``latent`` is given.
+
+    Returns (dx [M, 32*in_o], dalpha [32, in_o], dbeta [32, out_o],
+    dW [32, out_o, in_o]).
+    """
+    x = np.asarray(x, dtype=np.float64)
+    gy = np.asarray(gy, dtype=np.float64)
+    M = x.shape[0]
+    G, out_o, in_o = codes.shape
+    W = codes.astype(np.float64)
+    a = np.asarray(alpha, np.float64)
+    b = np.asarray(beta, np.float64)
+    H = sylvester(G)
+    xs = x.reshape(M, G, in_o)
+    g = gy.reshape(M, G, out_o)
+    xm = np.einsum('mgi,gh->mhi', xs * a, H)
+    ym = np.einsum('mgo,gh->mho', np.einsum('mgi,goi->mgo', xm, W), H)
+    dbeta = (g * ym).sum(0)
+    dyp = np.einsum('mgo,gh->mho', g * b, H)
+    dW = np.einsum('mgo,mgi->goi', dyp, xm)
+    dxs = np.einsum('mgi,gh->mhi', np.einsum('mgo,goi->mgi', dyp, W), H)
+    dalpha = (dxs * xs).sum(0)
+    dx = (dxs * a).reshape(M, G * in_o)
+    if latent is not None:
+        lat = np.asarray(latent, np.float64)
+        dW = dW * ((lat >= -1.5) & (lat <= 1.5))
+    return dx, dalpha, dbeta, dW

@@ -145,3 +145,103 @@ def test_rope_position_zero_identity_and_norm():
     assert np.allclose(r[:, 0], y[:, 0])
     pn = lambda v: np.hypot(v.reshape(1, 5, 8, 2)[..., 0], v.reshape(1, 5, 8, 2)[..., 1])
     assert np.allclose(pn(r), pn(y))
+
+
+# ---------------------------------------------------------------- backward
+
+def _torch_layer_f64(x, latent, alpha, beta):
+    """fht_cuda.py:489-519 with physics.quantize_ternary (physics.py:43-50),
+    written with torch float64 ops so that autograd derives the gradients."""
+    import torch
+    M = x.shape[0]
+    G, out_o, in_o = latent.shape
+    gamma = latent.abs().mean() + 1e-8
+    wq = torch.clamp(torch.round(latent / gamma), -1, 1)
+    wc = latent.clamp(-1.5, 1.5)
+    w = wc + (wq - wc).detach()
+    H = torch.tensor(hadamard.sylvester(G), dtype=torch.float64)
+    xs = x.view(M, G, in_o) * alpha
+    xm = (xs.transpose(-2, -1) @ H).transpose(-2, -1)
+    yp = torch.einsum('mgi,goi->mgo', xm, w)
+    ym = (yp.transpose(-2, -1) @ H).transpose(-2, -1)
+    return (ym * beta).reshape(M, G * out_o), wq
+
+
+def _bwd_case(M, in_o, out_o, seed, big=0.0):
+    import torch
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, 32 * in_o, generator=gen, dtype=torch.float64)
+    latent = hadamard.init_weight(out_o, in_o, gen).double()
+    if big:
+        # push some latent weights past the STE clamp at +-1.5
+        sel = torch.rand(latent.shape, generator=gen) < 0.2
+        latent = torch.where(sel, latent.sign() * (1.5 + big * torch.rand(latent.shape, generator=gen,
+                                                                               dtype=torch.float64)), latent)
+    alpha = 1 + 0.5 * torch.randn(32, in_o, generator=gen, dtype=torch.float64)
+    beta = 0.3 * torch.randn(32, out_o, generator=gen, dtype=torch.float64)
+    gy = torch.randn(M, 32 * out_o, generator=gen, dtype=torch.float64)
+    return x, latent, alpha, beta, gy
+
+
+def test_bwd_oracle_matches_torch_autograd():
+    for (M, in_o, out_o, seed, big) in ((7, 3, 5, 0, 0.0), (20, 4, 4, 1, 2.0), (5, 16, 8, 2, 0.5)):
+        x, latent, alpha, beta, gy = _bwd_case(M, in_o, out_o, seed, big)
+        xr, lr, ar, br = (t.clone().requires_grad_(True) for t in (x, latent, alpha, beta))
+        y, wq = _torch_layer_f64(xr, lr, ar, br)
+        y.backward(gy)
+        codes = wq.detach().numpy().astype(np.int8)
+        if big:
+            assert (np.abs(latent.numpy()) > 1.5).any()
+        dx, da, db, dw = hadamard.hadamard_linear_bwd_f64(x.numpy(), codes, alpha.numpy(), beta.numpy(), gy.numpy(),
+                                                         latent=latent.numpy())
+        for got, ref in ((dx, xr.grad), (da, ar.grad), (db, br.grad), (dw, lr.grad)):
+            ref = ref.numpy()
+            assert got.shape == ref.shape
+            assert np.max(np.abs(got - ref)) <= 1e-12 * max(1.0, np.max(np.abs(ref)))
+
+
+def test_bwd_dx_is_transpose_of_dense_matrix():
+    # dx = gy A with A the layer's dense matrix (Kronecker construction)
+    rng = np.random.default_rng(3)
+    in_o, out_o, M = 3, 2, 6
+    codes = rng.integers(-1, 2, size=(32, out_o, in_o)).astype(np.int8)
+    alpha = rng.normal(size=(32, in_o))
+    beta = rng.normal(size=(32, out_o))
+    x = rng.normal(size=(M, 32 * in_o))
+    gy = rng.normal(size=(M, 32 * out_o))
+    A = hadamard.dense_matrix(codes, alpha, beta)
+    dx, _, _, _ = hadamard.hadamard_linear_bwd_f64(x, codes, alpha, beta, gy)
+    assert np.allclose(dx, gy @ A, rtol=1e-12, atol=1e-12)
+
+
+def test_bwd_finite_differences():
+    # central differences of the float64 forward in alpha, beta and the
+    # (continuous) per-group matrices
+    rng = np.random.default_rng(4)
+    in_o, out_o, M = 2, 3, 4
+    W = rng.normal(size=(32, out_o, in_o))
+    alpha = rng.normal(size=(32, in_o))
+    beta = rng.normal(size=(32, out_o))
+    x = rng.normal(size=(M, 32 * in_o))
+    gy = rng.normal(size=(M, 32 * out_o))
+    _, da, db, dw = hadamard.hadamard_linear_bwd_f64(x, W, alpha, beta, gy)
+
+    def loss(W_, a_, b_):
+        return float(np.sum(hadamard.hadamard_linear_f64(x, W_, a_, b_) * gy))
+
+    h = 1e-6
+    for (idx, ref) in (((5, 1), da), ((31, 0), da)):
+        e = np.zeros_like(alpha)
+        e[idx] = h
+        fd = (loss(W, alpha + e, beta) - loss(W, alpha - e, beta)) / (2 * h)
+        assert abs(fd - ref[idx]) <= 1e-6 * max(1.0, abs(fd))
+    for idx in ((0, 0), (17, 2)):
+        e = np.zeros_like(beta)
+        e[idx] = h
+        fd = (loss(W, alpha, beta + e) - loss(W, alpha, beta - e)) / (2 * h)
+        assert abs(fd - db[idx]) <= 1e-6 * max(1.0, abs(fd))
+    for idx in ((0, 0, 0), (9, 2, 1), (31, 1, 0)):
+        e = np.zeros_like(W)
+        e[idx] = h
+        fd = (loss(W + e, alpha, beta) - loss(W - e, alpha, beta)) / (2 * h)
+        assert abs(fd - dw[idx]) <= 1e-6 * max(1.0, abs(fd))

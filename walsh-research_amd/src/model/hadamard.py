@@ -54,6 +54,33 @@ def _init_latent(out_o: int, in_o: int) -> torch.Tensor:
     return w / (norms + 1e-8) * 0.02 * math.sqrt(out_o * in_o)
 
 
+class HadamardLinearFunction(torch.autograd.Function):
+    """Autograd of the Hadamard linear on the HIP kernels: forward
+    walsh_hadamard_linear_fwd, backward walsh_hadamard_linear_bwd (dx through
+    the transposed layer, dalpha / dbeta / dW as fixed-order reductions, the
+    weight gradient through physics.quantize_ternary's STE clamp,
+    physics.py:48-50).  Replaces the graph the reference's einsum + FHTFunction
+    (fht_cuda.py:316-337, :497-519) builds."""
+
+    @staticmethod
+    def forward(ctx, x, weight, alpha, beta, layer):
+        y = layer._apply_2d(x, x.dtype)
+        ctx.layer = layer
+        ctx.save_for_backward(x, weight, alpha, beta)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, weight, alpha, beta = ctx.saved_tensors
+        layer = ctx.layer
+        nx, nw, na, nb, _ = ctx.needs_input_grad
+        _, packed, kw = layer.ternary_state()
+        kwt = layer.ternary_state_t() if (nx or na) else None
+        gx, da, db, dw = kernels.hadamard_linear_bwd(x, gy.to(x.dtype).contiguous(), layer.in_o, layer.out_o, kw,
+                                                      kwt, alpha, beta, latent=weight, need=(nx, na, nb, nw))
+        return gx, dw, da, db, None
+
+
 class _HadamardBase(nn.Module):
     """Parameters and the HIP forward shared by the Hadamard linear classes."""
 
@@ -68,6 +95,7 @@ class _HadamardBase(nn.Module):
         self.alpha = nn.Parameter(torch.ones(ALGEBRA_DIM, self.in_o))
         self.beta = nn.Parameter(torch.ones(ALGEBRA_DIM, self.out_o) * math.sqrt(3.0 / (2.0 * self.in_o)))
         self._wcache = WeightCache()
+        self._wcache_t = WeightCache()
 
     def ternary_state(self):
         """(gamma, packed codes, kernel layout) of the current weight, cached."""
@@ -79,14 +107,36 @@ class _HadamardBase(nn.Module):
 
         return self._wcache.get([w], build)
 
+    def ternary_state_t(self):
+        """Kernel layout of the transposed codes (the input-gradient pass), cached."""
+        w = self.weight
+
+        def build():
+            _, packed, _ = self.ternary_state()
+            return kernels.hadamard_prepare_t(packed, self.in_o, self.out_o)
+
+        return self._wcache_t.get([w], build)
+
     def _apply_2d(self, x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
         _, _, kw = self.ternary_state()
         return kernels.hadamard_linear(x if x.dtype == dtype else x.to(dtype), self.in_o, self.out_o, kw,
                                        self.alpha, self.beta)
 
+    def _needs_grad(self, x: torch.Tensor) -> bool:
+        return torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad
+                                            or self.alpha.requires_grad or self.beta.requires_grad)
+
+    def apply_rows(self, x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        """The layer on x [..., 32*in_o] in ``dtype``, differentiable when
+        autograd needs it."""
+        xin = x if x.dtype == dtype else x.to(dtype)
+        if self._needs_grad(xin):
+            return HadamardLinearFunction.apply(xin, self.weight, self.alpha, self.beta, self)
+        return self._apply_2d(xin, dtype)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         assert x.shape[-1] == self.in_o * ALGEBRA_DIM, f"expected last dim {self.in_o * ALGEBRA_DIM}, got {x.shape[-1]}"
-        y = self._apply_2d(x, act_dtype(x))
+        y = self.apply_rows(x, act_dtype(x))
         return y.to(x.dtype)
 
 
@@ -136,13 +186,15 @@ class HadamardTernaryLinearTuple(nn.Module):
     def forward_full(self, x: torch.Tensor) -> torch.Tensor:
         """Whole rows [..., 32*in_o] -> [..., 32*out_o] in the activation dtype
         (the same result as split -> forward -> cat, without the copies)."""
-        return self.inner._apply_2d(x, act_dtype(x))
+        return self.inner.apply_rows(x, act_dtype(x))
 
     def forward_full_rope(self, x: torch.Tensor, freqs_cis: torch.Tensor, head_dim: int):
         """forward_full on x [B, T, C] with apply_rotary_emb (chassis.py:339-345)
-        fused into the store, or None when the shapes do not allow it."""
+        fused into the store, or None when the shapes do not allow it or
+        autograd needs the linear's own graph (the caller then applies the
+        rotation separately)."""
         inner = self.inner
-        if x.dim() != 3 or not kernels.rope_supported(x, inner.out_o, head_dim):
+        if x.dim() != 3 or not kernels.rope_supported(x, inner.out_o, head_dim) or inner._needs_grad(x):
             return None
         dt = act_dtype(x)
         _, _, kw = inner.ternary_state()
@@ -164,9 +216,22 @@ def fht_butterfly(x: torch.Tensor) -> torch.Tensor:
     return kernels.fht(x, normalize=True)
 
 
+class FHTFunction(torch.autograd.Function):
+    """Normalised FHT with its backward (fht_cuda.py:316-332): H is symmetric
+    and orthonormal, so the gradient is the same transform of grad_y."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor) -> torch.Tensor:
+        return kernels.fht(x, normalize=True)
+
+    @staticmethod
+    def backward(ctx, grad_y: torch.Tensor) -> torch.Tensor:
+        return kernels.fht(grad_y, normalize=True)
+
+
 def fht(x: torch.Tensor) -> torch.Tensor:
-    """fht (fht_cuda.py:316-337): forward-only here."""
-    return kernels.fht(x, normalize=True)
+    """fht (fht_cuda.py:335-337): FHTFunction.apply."""
+    return FHTFunction.apply(x)
 
 
 def fht_reference(x: torch.Tensor) -> torch.Tensor:

@@ -217,6 +217,71 @@ def hadamard_swiglu(x: torch.Tensor, in_o: int, hid_o: int, gate, up, gsh: int =
     return h
 
 
+def hadamard_pack_transpose(packed: torch.Tensor, in_o: int, out_o: int) -> torch.Tensor:
+    """Packed codes of the transposed layer: [32, in_o, ceil(out_o/4)] from
+    [32, out_o, ceil(in_o/4)] (fht_cuda.py:65-93 packing of W^T)."""
+    _hip.require_device(packed, "packed weight")
+    assert tuple(packed.shape) == (32, out_o, (in_o + 3) // 4), f"packed shape {tuple(packed.shape)}"
+    pt = torch.empty(32, in_o, (out_o + 3) // 4, device=packed.device, dtype=torch.uint8)
+    _hip.call("walsh_hadamard_pack_transpose", packed.contiguous().data_ptr(), in_o, out_o, pt.data_ptr(),
+              _hip.stream(packed.device))
+    return pt
+
+
+def hadamard_prepare_t(packed: torch.Tensor, in_o: int, out_o: int) -> torch.Tensor:
+    """Kernel weight layout of the transposed layer (in_o <-> out_o), the
+    weights of the input-gradient pass."""
+    return hadamard_prepare(hadamard_pack_transpose(packed, in_o, out_o), out_o, in_o)
+
+
+def hadamard_linear_bwd(x: torch.Tensor, gy: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tensor,
+                        kweight_t: torch.Tensor, alpha: torch.Tensor, beta: torch.Tensor,
+                        latent: torch.Tensor = None, need=(True, True, True, True)):
+    """Backward of hadamard_linear for the output gradient ``gy``.
+
+    Returns (gx, dalpha, dbeta, dweight); entries not requested in ``need``
+    (same order) are None.  gx has x's shape and dtype; the others are
+    float32 [32, in_o], [32, out_o], [32, out_o, in_o].  With ``latent`` the
+    weight gradient passes the straight-through estimator's clamp
+    (physics.py:48-50): zero where |latent| > 1.5."""
+    _hip.require_device(x, "input")
+    _hip.require_device(gy, "output gradient")
+    dt = x.dtype
+    code = _hip.dtype_code(dt)
+    assert gy.dtype == dt, f"gradient dtype {gy.dtype} != input dtype {dt}"
+    assert x.shape[-1] == 32 * in_o and gy.shape[-1] == 32 * out_o, "x / gy widths"
+    assert x.shape[:-1] == gy.shape[:-1], "x / gy leading shapes differ"
+    xc = x.reshape(-1, 32 * in_o).contiguous()
+    gc = gy.reshape(-1, 32 * out_o).contiguous()
+    M = xc.shape[0]
+    dev = x.device
+    want_x, want_a, want_b, want_w = need
+    gx = torch.empty_like(xc) if want_x else None
+    da = torch.empty(32, in_o, device=dev, dtype=torch.float32) if want_a else None
+    db = torch.empty(32, out_o, device=dev, dtype=torch.float32) if want_b else None
+    dw = torch.empty(32, out_o, in_o, device=dev, dtype=torch.float32) if want_w else None
+    nws = _hip.lib().walsh_hadamard_bwd_workspace_bytes(M, in_o, out_o, code)
+    ws = torch.empty(max(nws, 1), device=dev, dtype=torch.uint8)
+    alpha = alpha.detach().float().contiguous()
+    beta = beta.detach().float().contiguous()
+    lat = None
+    if latent is not None and want_w:
+        lat = latent.detach().float().contiguous()
+        assert lat.shape == (32, out_o, in_o), "latent weight shape"
+    ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+    esz = x.element_size()
+    nbytes = M * 32 * (in_o + out_o) * esz * 4 + M * 32 * in_o * esz
+    flops = M * 2 * 32 * in_o * out_o * 3
+    _hip.call("walsh_hadamard_linear_bwd", xc.data_ptr(), 32 * in_o, gc.data_ptr(), 32 * out_o, M, in_o, out_o,
+              ptr(kweight), ptr(kweight_t), alpha.data_ptr(), beta.data_ptr(), ptr(lat), ptr(gx), 32 * in_o,
+              ptr(da), ptr(db), ptr(dw), code, ws.data_ptr(), nws, _hip.stream(dev),
+              kernel="hadamard_linear_bwd<%s>" % ("bf16" if dt == torch.bfloat16 else "f32"), nbytes=nbytes,
+              flops=flops)
+    if gx is not None:
+        gx = gx.view(x.shape)
+    return gx, da, db, dw
+
+
 def fht(x: torch.Tensor, normalize: bool = True) -> torch.Tensor:
     """Fast Walsh-Hadamard transform along the last dim (fht_cuda.py:281-309)."""
     _hip.require_device(x, "input")
