@@ -16,7 +16,10 @@ Other workloads (``--workload``), each printing one JSON line of its own:
   prefill5  scaled model: n_embd 4096 (32 heads of 128), 24 layers, MoE with
             128 experts (k = 6), 4 streams, bf16, prefill of 64 x 1024 tokens;
   decode5   the same model decoding one token per sequence against a
-            synthetic KV cache of length 4096, at batch 1, 16 and 64.
+            synthetic KV cache of length 4096, at batch 1, 16 and 64;
+  hadamard_bwd  backward of one HadamardLinear(512, 512), bf16, x and the
+            output gradient [8192, 512] (the headline model's layer shape),
+            and a token sweep up to 262144 rows (rotated).
 
 Prints ONE JSON line.  Besides the timed region it
   * repeats the K steps with HIP events around every hot-path launch (on the
@@ -52,7 +55,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-roofline", action="store_true", help="skip the instrumented pass (profiling runs)")
     ap.add_argument("--workload", default="mhcwalsh",
-                    choices=["mhcwalsh", "moe", "octonion", "hadamard", "prefill5", "decode5"])
+                    choices=["mhcwalsh", "moe", "octonion", "hadamard", "prefill5", "decode5", "hadamard_bwd"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (reference for HBM byte counters)")
     return ap.parse_args()
@@ -143,7 +146,7 @@ def main():
         return
     if args.workload != "mhcwalsh":
         line = {"moe": bench_moe, "octonion": bench_octonion, "hadamard": bench_hadamard, "prefill5": bench_prefill5,
-                "decode5": bench_decode5}[args.workload](torch, args)
+                "decode5": bench_decode5, "hadamard_bwd": bench_hadamard_bwd}[args.workload](torch, args)
         print(json.dumps(line), flush=True)
         return
     _hip.lib()
@@ -384,6 +387,78 @@ def bench_hadamard(torch, args):
                  "synthetic: x N(0,1), weights N(0,0.02) latents",
                  {"workload": "HadamardLinear(512, 512), x [4, 256, 512]", "global_batch": 4, "seq_len": 256,
                   "parallelism": "single GPU"}, roof, cpu)
+    line["sweep"] = sweep
+    return line
+
+
+def bench_hadamard_bwd(torch, args):
+    """Backward of one HadamardLinear(512, 512) in bf16 at the per-layer shape
+    of the headline model (8 x 1024 tokens): gx, dalpha, dbeta and the STE
+    weight gradient in one walsh_hadamard_linear_bwd call, plus a token sweep
+    with rotated buffers (> 256 MB) for the HBM figure."""
+    from src.model import _hip, kernels
+    from src.model.hadamard import HadamardLinear
+    torch.manual_seed(0)
+    lin = HadamardLinear(512, 512).cuda()
+    with torch.no_grad():
+        lin.alpha.add_(0.1 * torch.randn_like(lin.alpha))
+    _, _, kw = lin.ternary_state()
+    kwt = lin.ternary_state_t()
+    sweep = []
+    for rows in (8192, 65536, 262144):
+        nbuf = max(1, min(32, (768 << 20) // (rows * 512 * 2 * 3)))
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        xs = [torch.randn(rows, 512, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(nbuf)]
+        gs = [torch.randn(rows, 512, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(nbuf)]
+
+        def step(i):
+            return kernels.hadamard_linear_bwd(xs[i % nbuf], gs[i % nbuf], 16, 16, kw, kwt, lin.alpha, lin.beta,
+                                               latent=lin.weight)
+        iters = max(args.steps, 100 if rows <= 8192 else 20)
+        dt = _time_steps(torch, step, iters, args.warmup)
+        with _hip.LaunchTimer() as lt:
+            for i in range(iters):
+                step(i)
+        r = _roofline_of(lt.summary(), iters)
+        sweep.append(dict(rows=rows, us_per_call=round(dt * 1e6, 2), kernels_us=r["avg_launch_us"],
+                          gbs=r["achieved"], frac=r["frac"], rotated_buffers=nbuf))
+        if rows == 8192:
+            roof, dt1 = r, dt
+        del xs, gs
+    roof["note"] = ("all four launches of one walsh_hadamard_linear_bwd call (dx+dalpha pass, dbeta pass, dW pass, "
+                    "reduction) against the minimal traffic: x and gy read once, gx written once")
+    cpu = None
+    if not args.no_cpu:
+        import numpy as np
+        from oracle.hadamard import sylvester
+        torch.manual_seed(1)
+        M = 1024
+        H = torch.tensor(sylvester(32), dtype=torch.float32)
+        w = torch.tensor(np.sign(lin.weight.detach().cpu().numpy()), requires_grad=True)
+        a = lin.alpha.detach().cpu().requires_grad_(True)
+        b = lin.beta.detach().cpu().requires_grad_(True)
+        x = torch.randn(M, 512, requires_grad=True)
+        gy = torch.randn(M, 512)
+        t_bwd, reps, t0 = 0.0, 0, time.perf_counter()
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0) or reps == 0:
+            # the reference's float32 CPU graph (fht_cuda.py:497-519)
+            xs_ = x.view(M, 32, 16) * a
+            xm = torch.einsum('mgi,gh->mhi', xs_, H)
+            ym = torch.einsum('mgo,gh->mho', torch.einsum('mgi,goi->mgo', xm, w), H)
+            y = (ym * b).reshape(M, 512)
+            t1 = time.perf_counter()
+            y.backward(gy)
+            t_bwd += time.perf_counter() - t1
+            x.grad = a.grad = b.grad = w.grad = None
+            reps += 1
+        cpu = dict(value=round(reps * M / t_bwd, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   sample=f"{reps} backward passes of [1024, 512] float32 through the reference's CPU einsum graph "
+                          f"(torch autograd), {t_bwd:.1f} s of backward")
+    line = _line("tokens/sec through one Hadamard ternary linear backward at 1 GPU; % of HBM roofline (GB/s)",
+                 8192 / dt1, "tokens/s", max(args.steps, 100), args.warmup, dt1 * 1e3, "bf16",
+                 "synthetic: x, gy N(0,1); weights N(0,0.02) latents",
+                 {"workload": "HadamardLinear(512, 512) backward, x and gy [8192, 512]", "global_batch": 8,
+                  "seq_len": 1024, "parallelism": "single GPU"}, roof, cpu)
     line["sweep"] = sweep
     return line
 

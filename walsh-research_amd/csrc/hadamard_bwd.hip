@@ -17,21 +17,21 @@
 // Every product above is H0 ... H0 / 32, so the kernels run unnormalised
 // transforms and the reduction applies the 1/32.
 //
-// Kernels.
-//   hadamard_bwd_red_kernel  one forward-style pass (transform, ternary
-//     contraction on matrix cores, transform) whose epilogue multiplies the
-//     result by an auxiliary row tensor and keeps per-lane sums over the
-//     wave's tiles (dalpha with aux = x while storing dx; dbeta with
-//     aux = gy without a store).  The sums of a wave are reduced over its 16
+// Kernel: hadamard_bwd_kernel, one launch with three workgroup roles.
+//   dW role: per (token range, output tile, input chunk), H0(beta .* gy) and
+//     H0(alpha .* x) in the forward lane layout (lane = token, 4 columns),
+//     turned into token-major fragments by a matrix-core product with the
+//     identity, then dW_g += dyp_g^T xm_g on matrix cores with the 16 tokens
+//     of a tile as the contraction.  The four waves of a workgroup add their
+//     dW in LDS in a fixed order and write one partial.
+//   dx / dalpha role and dbeta role: a forward-style pass (transform,
+//     ternary contraction on matrix cores, transform) whose epilogue
+//     multiplies the result by an auxiliary row tensor and keeps per-lane
+//     sums over the wave's tiles (dalpha with aux = x while storing dx;
+//     dbeta with aux = gy, no store); a wave's sums are reduced over its 16
 //     token lanes with DPP row rotations and written as one partial row.
-//   hadamard_bwd_dw_kernel   per (token range, output tile, input chunk):
-//     H0(beta .* gy) and H0(alpha .* x) in the forward lane layout (lane =
-//     token, 4 columns), turned into token-major fragments by a matrix-core
-//     product with the identity, then dW_g += dyp_g^T xm_g on matrix cores
-//     with the 16 tokens of a tile as the contraction.  The four waves of a
-//     workgroup add their dW in LDS in a fixed order.
-//   hadamard_bwd_reduce_kernel  fixed-order sums of the partials, the 1/32
-//     and the STE mask.
+// hadamard_bwd_reduce_kernel: fixed-order column sums of the partials, the
+//   1/32 and the STE mask.
 // All sums run in a fixed order: results are identical from run to run.
 #include "hadamard_core.h"
 
@@ -114,8 +114,7 @@ struct BwdRed {
 };
 
 template <typename T, bool BF16MMA, bool VEC, bool STORE>
-__global__ __launch_bounds__(kThreads, 1) void hadamard_bwd_red_kernel(HadArgs a, BwdRed r) {
-    extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ void bwd_red_role(const HadArgs &a, const BwdRed &r, int blk, unsigned char *smem) {
     void *lut = smem;
     f32x4 *alpha_l = (f32x4 *)(smem + lut_bytes<BF16MMA>());
     f32x4 *beta_l = alpha_l + a.Kc * 128;
@@ -127,7 +126,7 @@ __global__ __launch_bounds__(kThreads, 1) void hadamard_bwd_red_kernel(HadArgs a
 
     constexpr uint32_t esz = sizeof(T);
     const int wave = tid >> 6, lane = tid & 63, t = lane & 15, q = lane >> 4;
-    const int wid = blockIdx.x * kWaves + wave;
+    const int wid = blk * kWaves + wave;
     if (wid >= r.S * a.Nt) return;  // no barrier follows
     const int nt = wid % a.Nt, s = wid / a.Nt;
     const int n_tiles = (int)ceil_div(a.M, kTile);
@@ -220,8 +219,8 @@ __device__ __forceinline__ f32x4 transpose_f32(f32x4 tile, f32x4 ident) {
 }
 
 template <typename T, bool BF16MMA, bool VEC>
-__global__ __launch_bounds__(kThreads, 1) void hadamard_bwd_dw_kernel(HadArgs ax, HadArgs ag, BwdDW d) {
-    extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ void bwd_dw_role(const HadArgs &ax, const HadArgs &ag, const BwdDW &d, int blk,
+                                            unsigned char *smem) {
     f32x4 *alpha_l = (f32x4 *)smem;             // [Kc][4][32]
     f32x4 *beta_l = alpha_l + ax.Kc * 128;      // [Nt][4][32]
     f32x4 *sum_l = beta_l + ag.Kc * 128;        // [32][64]
@@ -233,7 +232,7 @@ __global__ __launch_bounds__(kThreads, 1) void hadamard_bwd_dw_kernel(HadArgs ax
     constexpr uint32_t esz = sizeof(T);
     const int wave = tid >> 6, lane = tid & 63, t = lane & 15, q = lane >> 4;
     const int Kc = ax.Kc, Nt = ag.Kc;
-    const int item = blockIdx.x;
+    const int item = blk;
     const int c = item % Kc, nt = (item / Kc) % Nt, s = item / (Kc * Nt);
     const int n_tiles = (int)ceil_div(ax.M, kTile);
     const int t0 = s * d.tps;
@@ -305,6 +304,38 @@ __global__ __launch_bounds__(kThreads, 1) void hadamard_bwd_dw_kernel(HadArgs ax
     }
 }
 
+// ---------------------------------------------------------------- one launch, three roles
+
+// The three passes read the same rows and are independent, so they run as
+// one launch: workgroups [0, nW) take the dW role, the next nA the dx/dalpha
+// role, the last nB the dbeta role (the longest role first, so its
+// workgroups are dispatched first).
+struct BwdJob {
+    HadArgs a;   // transposed layer on gy (dx / dalpha)
+    BwdRed ra;
+    HadArgs b;   // the layer on x (dbeta)
+    BwdRed rb;
+    HadArgs wx, wg;  // x and gy as transform inputs (dW)
+    BwdDW dw;
+    int nW, nA, nB;
+};
+
+template <typename T, bool BF16MMA, bool VEC, bool STORE>
+__global__ __launch_bounds__(kThreads, 1) void hadamard_bwd_kernel(BwdJob j) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    int blk = blockIdx.x;
+    if (blk < j.nW) {
+        bwd_dw_role<T, BF16MMA, VEC>(j.wx, j.wg, j.dw, blk, smem);
+        return;
+    }
+    blk -= j.nW;
+    if (blk < j.nA) {
+        bwd_red_role<T, BF16MMA, VEC, STORE>(j.a, j.ra, blk, smem);
+        return;
+    }
+    bwd_red_role<T, BF16MMA, VEC, false>(j.b, j.rb, blk - j.nA, smem);
+}
+
 // ---------------------------------------------------------------- final reduction
 
 struct BwdSum {
@@ -317,38 +348,67 @@ struct BwdSum {
     float *da, *db, *dw;  // null: not wanted
 };
 
-__global__ __launch_bounds__(256) void hadamard_bwd_reduce_kernel(BwdSum r) {
-    const int64_t na = r.da ? 32 * r.in_o : 0, nb = r.db ? 32 * r.out_o : 0;
-    const int64_t nw = r.dw ? (int64_t)32 * r.out_o * r.in_o : 0;
-    const int64_t total = na + nb + nw;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-         e += (int64_t)gridDim.x * blockDim.x) {
-        double acc = 0.0;
-        if (e < na) {
-            const int g = (int)(e / r.in_o), i = (int)(e % r.in_o);
-            const float *p = r.pa + (int64_t)g * r.Ap + i;
-            for (int s = 0; s < r.Sa; ++s) acc += (double)p[(int64_t)s * 32 * r.Ap];
-            r.da[e] = (float)(acc * 0.03125);
-        } else if (e < na + nb) {
-            const int64_t f = e - na;
-            const int g = (int)(f / r.out_o), o = (int)(f % r.out_o);
-            const float *p = r.pb + (int64_t)g * r.Bp + o;
-            for (int s = 0; s < r.Sb; ++s) acc += (double)p[(int64_t)s * 32 * r.Bp];
-            r.db[f] = (float)(acc * 0.03125);
-        } else {
-            const int64_t f = e - na - nb;
-            const int i = (int)(f % r.in_o);
-            const int64_t go = f / r.in_o;
-            const int o = (int)(go % r.out_o), g = (int)(go / r.out_o);
-            const float *p = r.pw + ((int64_t)g * r.Op + o) * r.Ip + i;
-            for (int s = 0; s < r.Sw; ++s) acc += (double)p[(int64_t)s * 32 * r.Op * r.Ip];
-            float v = (float)(acc * 0.03125);
-            if (r.latent) {
-                const float w = r.latent[f];
-                v = (w >= -1.5f && w <= 1.5f) ? v : 0.f;
-            }
-            r.dw[f] = v;
+constexpr int kSumCols = 64;     // partial columns per workgroup
+constexpr int kSumPhases = 16;   // partial rows summed in parallel, s = phase mod 16
+
+__host__ __device__ inline int64_t sum_blocks(const BwdSum &r, int64_t *bw, int64_t *ba) {
+    *bw = r.dw ? ceil_div((int64_t)32 * r.Op * r.Ip, kSumCols) : 0;
+    *ba = r.da ? ceil_div((int64_t)32 * r.Ap, kSumCols) : 0;
+    const int64_t bb = r.db ? ceil_div((int64_t)32 * r.Bp, kSumCols) : 0;
+    return *bw + *ba + bb;
+}
+
+// Column sums of the partial arrays P[S][N] (each partial row contiguous):
+// thread (column, phase) sums rows phase, phase + 16, ... in order, then
+// phase 0 adds the 16 phase sums in order; then the 1/32, the output
+// mapping (padded columns dropped) and the STE mask.
+__global__ __launch_bounds__(kSumCols * kSumPhases) void hadamard_bwd_reduce_kernel(BwdSum r) {
+    __shared__ double part[kSumPhases][kSumCols];
+    int64_t bw, ba;
+    sum_blocks(r, &bw, &ba);
+    int64_t blk = blockIdx.x;
+    int kind;  // 0 dW, 1 dalpha, 2 dbeta
+    const float *P;
+    int64_t N;
+    int S;
+    if (blk < bw) {
+        kind = 0, P = r.pw, N = (int64_t)32 * r.Op * r.Ip, S = r.Sw;
+    } else if ((blk -= bw) < ba) {
+        kind = 1, P = r.pa, N = (int64_t)32 * r.Ap, S = r.Sa;
+    } else {
+        blk -= ba;
+        kind = 2, P = r.pb, N = (int64_t)32 * r.Bp, S = r.Sb;
+    }
+    const int cx = threadIdx.x % kSumCols, ph = threadIdx.x / kSumCols;
+    const int64_t n = blk * kSumCols + cx;
+    double acc = 0.0;
+    if (n < N)
+        for (int s = ph; s < S; s += kSumPhases) acc += (double)P[(int64_t)s * N + n];
+    part[ph][cx] = acc;
+    __syncthreads();
+    if (ph != 0 || n >= N) return;
+    double tot = 0.0;
+#pragma unroll
+    for (int p = 0; p < kSumPhases; ++p) tot += part[p][cx];
+    const float v = (float)(tot * 0.03125);
+    if (kind == 0) {
+        const int i = (int)(n % r.Ip);
+        const int64_t go = n / r.Ip;
+        const int o = (int)(go % r.Op), g = (int)(go / r.Op);
+        if (o >= r.out_o || i >= r.in_o) return;
+        const int64_t f = ((int64_t)g * r.out_o + o) * r.in_o + i;
+        float out = v;
+        if (r.latent) {
+            const float w = r.latent[f];
+            out = (w >= -1.5f && w <= 1.5f) ? v : 0.f;
         }
+        r.dw[f] = out;
+    } else if (kind == 1) {
+        const int i = (int)(n % r.Ap), g = (int)(n / r.Ap);
+        if (i < r.in_o) r.da[g * r.in_o + i] = v;
+    } else {
+        const int o = (int)(n % r.Bp), g = (int)(n / r.Bp);
+        if (o < r.out_o) r.db[g * r.out_o + o] = v;
     }
 }
 
@@ -372,11 +432,11 @@ static int split_count(int n_tiles, int per_split_min, int64_t target, int *tps)
 static BwdChunk plan_chunk(int64_t rows, int in_o, int out_o) {
     const int n_tiles = (int)ceil_div(rows, kTile);
     const int Nt = (int)ceil_div(out_o, kNTile), Kc = (int)ceil_div(in_o, kKChunk);
-    const int64_t waves = (int64_t)device_info().cu_count * kWaves * 2;
+    const int64_t waves = (int64_t)device_info().cu_count;  // per red role
     BwdChunk p;
     p.Sa = split_count(n_tiles, 1, ceil_div(waves, Kc), &p.tpa);  // transposed layer: Kc output tiles
     p.Sb = split_count(n_tiles, 1, ceil_div(waves, Nt), &p.tpb);
-    p.Sw = split_count(n_tiles, 2 * kWaves, ceil_div((int64_t)device_info().cu_count * 2, (int64_t)Nt * Kc), &p.tpw);
+    p.Sw = split_count(n_tiles, kWaves, ceil_div((int64_t)device_info().cu_count / 2, (int64_t)Nt * Kc), &p.tpw);
     return p;
 }
 
@@ -474,79 +534,67 @@ WALSH_EXPORT int walsh_hadamard_linear_bwd(const void *x, int64_t ldx, const voi
     auto lut = [&](void) { return (size_t)(bf16 ? lut_bytes<true>() : lut_bytes<false>()); };
 
     int64_t ia = 0, ib = 0, iw = 0;  // partial rows written so far
+    const size_t lds_red = lut() + (size_t)16 * 128 * (Nt + Kc);
+    const size_t lds_dw = (size_t)16 * 128 * (Nt + Kc) + (size_t)32 * 64 * 16;
+    const size_t lds = need_w && lds_dw > lds_red ? lds_dw : lds_red;
+    if ((int64_t)lds > maxlds) return set_error(WALSH_ENOTSUP, "%s: shape needs %zu B of LDS", fn, lds);
     for (int64_t r0 = 0; r0 < M; r0 += L.rows_max) {
         const int64_t rows = (M - r0) < L.rows_max ? (M - r0) : L.rows_max;
         const BwdChunk p = plan_chunk(rows, (int)in_o, (int)out_o);
         const char *xc = (const char *)x + r0 * ldx * esz;
         const char *gc = (const char *)gy + r0 * ldg * esz;
-        if (need_a) {
-            // transposed layer on gy: in' = out_o, out' = in_o, alpha' = beta,
-            // beta' = alpha (stores dx), aux = x (dalpha)
-            HadArgs a{};
-            a.x = gc; a.ldx = ldg; a.M = (int)rows; a.in_o = (int)out_o; a.out_o = (int)in_o;
-            a.Nt = Kc; a.Kc = Nt; a.gsx = (int)out_o; a.gsy = (int)in_o; a.kw = kweight_t; a.kw3 = nullptr;
-            a.alpha = beta; a.beta = alpha; a.beta_h = (int)in_o;
-            a.y = gx ? (void *)((char *)gx + r0 * ldgx * esz) : nullptr; a.ldy = gx ? ldgx : 0;
-            a.tpb = 0; a.bstride = 0; a.rope = nullptr; a.rope_T = 1; a.rope_D = 4; a.rope_row0 = 0;
-            BwdRed r{xc, ldx, (int)in_o, pa + ia * 32 * Ap, p.Sa, p.tpa};
-            const size_t lds = lut() + (size_t)16 * 128 * (Nt + Kc);
-            if ((int64_t)lds > maxlds) return set_error(WALSH_ENOTSUP, "%s: shape needs %zu B of LDS", fn, lds);
-            const bool vec = out_o % 4 == 0 && in_o % 4 == 0 && ldx % 4 == 0 && ldg % 4 == 0 &&
-                             (!gx || ldgx % 4 == 0) && (uintptr_t)gc % valign == 0 && (uintptr_t)xc % valign == 0 &&
-                             (!gx || (uintptr_t)a.y % valign == 0);
-            const dim3 G((unsigned)ceil_div((int64_t)p.Sa * Kc, kWaves)), B(kThreads);
-#define WALSH_RED(T, MMA, V, ST) launch((hadamard_bwd_red_kernel<T, MMA, V, ST>), G, B, lds, s, a, r)
-            if (bf16) {
-                if (vec) { if (gx) WALSH_RED(uint16_t, true, true, true); else WALSH_RED(uint16_t, true, true, false); }
-                else     { if (gx) WALSH_RED(uint16_t, true, false, true); else WALSH_RED(uint16_t, true, false, false); }
-            } else {
-                if (vec) { if (gx) WALSH_RED(float, false, true, true); else WALSH_RED(float, false, true, false); }
-                else     { if (gx) WALSH_RED(float, false, false, true); else WALSH_RED(float, false, false, false); }
-            }
-            const int rc = check_hip(hipGetLastError(), fn);
-            if (rc) return rc;
-            ia += p.Sa;
+        char *gxc = gx ? (char *)gx + r0 * ldgx * esz : nullptr;
+        BwdJob j{};
+        auto base = [&](HadArgs &h) {
+            h.M = (int)rows;
+            h.kw3 = nullptr;
+            h.tpb = 0;
+            h.bstride = 0;
+            h.rope = nullptr;
+            h.rope_T = 1;
+            h.rope_D = 4;
+            h.rope_row0 = 0;
+        };
+        // transposed layer on gy: in' = out_o, out' = in_o, alpha' = beta,
+        // beta' = alpha (stores dx), aux = x (dalpha)
+        base(j.a);
+        j.a.x = gc; j.a.ldx = ldg; j.a.in_o = (int)out_o; j.a.out_o = (int)in_o; j.a.Nt = Kc; j.a.Kc = Nt;
+        j.a.gsx = (int)out_o; j.a.gsy = (int)in_o; j.a.kw = kweight_t; j.a.alpha = beta; j.a.beta = alpha;
+        j.a.beta_h = (int)in_o; j.a.y = gxc; j.a.ldy = gx ? ldgx : 0;
+        j.ra = BwdRed{xc, ldx, (int)in_o, pa + ia * 32 * Ap, p.Sa, p.tpa};
+        j.nA = need_a ? (int)ceil_div((int64_t)p.Sa * Kc, kWaves) : 0;
+        // the layer on x without beta or store, aux = gy (dbeta)
+        base(j.b);
+        j.b.x = xc; j.b.ldx = ldx; j.b.in_o = (int)in_o; j.b.out_o = (int)out_o; j.b.Nt = Nt; j.b.Kc = Kc;
+        j.b.gsx = (int)in_o; j.b.gsy = (int)out_o; j.b.kw = kweight; j.b.alpha = alpha; j.b.beta = nullptr;
+        j.b.beta_h = 0; j.b.y = nullptr; j.b.ldy = 0;
+        j.rb = BwdRed{gc, ldg, (int)out_o, pb + ib * 32 * Bp, p.Sb, p.tpb};
+        j.nB = need_b ? (int)ceil_div((int64_t)p.Sb * Nt, kWaves) : 0;
+        // x and gy as transform inputs (dW)
+        base(j.wx);
+        j.wx.x = xc; j.wx.ldx = ldx; j.wx.in_o = (int)in_o; j.wx.Kc = Kc; j.wx.gsx = (int)in_o; j.wx.alpha = alpha;
+        base(j.wg);
+        j.wg.x = gc; j.wg.ldx = ldg; j.wg.in_o = (int)out_o; j.wg.Kc = Nt; j.wg.gsx = (int)out_o; j.wg.alpha = beta;
+        j.dw = BwdDW{pw + iw * 32 * (int64_t)Bp * Ap, p.Sw, p.tpw};
+        j.nW = need_w ? p.Sw * Nt * Kc : 0;
+        const bool vec = out_o % 4 == 0 && in_o % 4 == 0 && ldx % 4 == 0 && ldg % 4 == 0 &&
+                         (!gx || ldgx % 4 == 0) && (uintptr_t)gc % valign == 0 && (uintptr_t)xc % valign == 0 &&
+                         (!gx || (uintptr_t)gxc % valign == 0);
+        const dim3 G((unsigned)(j.nW + j.nA + j.nB)), B(kThreads);
+#define WALSH_BWD(T, MMA, V, ST) launch((hadamard_bwd_kernel<T, MMA, V, ST>), G, B, lds, s, j)
+        if (bf16) {
+            if (vec) { if (gx) WALSH_BWD(uint16_t, true, true, true); else WALSH_BWD(uint16_t, true, true, false); }
+            else     { if (gx) WALSH_BWD(uint16_t, true, false, true); else WALSH_BWD(uint16_t, true, false, false); }
+        } else {
+            if (vec) { if (gx) WALSH_BWD(float, false, true, true); else WALSH_BWD(float, false, true, false); }
+            else     { if (gx) WALSH_BWD(float, false, false, true); else WALSH_BWD(float, false, false, false); }
         }
-        if (need_b) {
-            // the layer on x without beta or store, aux = gy (dbeta)
-            HadArgs a{};
-            a.x = xc; a.ldx = ldx; a.M = (int)rows; a.in_o = (int)in_o; a.out_o = (int)out_o;
-            a.Nt = Nt; a.Kc = Kc; a.gsx = (int)in_o; a.gsy = (int)out_o; a.kw = kweight; a.kw3 = nullptr;
-            a.alpha = alpha; a.beta = nullptr; a.beta_h = 0; a.y = nullptr; a.ldy = 0;
-            a.tpb = 0; a.bstride = 0; a.rope = nullptr; a.rope_T = 1; a.rope_D = 4; a.rope_row0 = 0;
-            BwdRed r{gc, ldg, (int)out_o, pb + ib * 32 * Bp, p.Sb, p.tpb};
-            const size_t lds = lut() + (size_t)16 * 128 * (Nt + Kc);
-            if ((int64_t)lds > maxlds) return set_error(WALSH_ENOTSUP, "%s: shape needs %zu B of LDS", fn, lds);
-            const bool vec = out_o % 4 == 0 && in_o % 4 == 0 && ldx % 4 == 0 && ldg % 4 == 0 &&
-                             (uintptr_t)gc % valign == 0 && (uintptr_t)xc % valign == 0;
-            const dim3 G((unsigned)ceil_div((int64_t)p.Sb * Nt, kWaves)), B(kThreads);
-            if (bf16) { if (vec) WALSH_RED(uint16_t, true, true, false); else WALSH_RED(uint16_t, true, false, false); }
-            else      { if (vec) WALSH_RED(float, false, true, false); else WALSH_RED(float, false, false, false); }
-#undef WALSH_RED
-            const int rc = check_hip(hipGetLastError(), fn);
-            if (rc) return rc;
-            ib += p.Sb;
-        }
-        if (need_w) {
-            HadArgs ax{}, ag{};
-            ax.x = xc; ax.ldx = ldx; ax.M = (int)rows; ax.in_o = (int)in_o; ax.Kc = Kc; ax.gsx = (int)in_o;
-            ax.alpha = alpha; ax.tpb = 0;
-            ag.x = gc; ag.ldx = ldg; ag.M = (int)rows; ag.in_o = (int)out_o; ag.Kc = Nt; ag.gsx = (int)out_o;
-            ag.alpha = beta; ag.tpb = 0;
-            BwdDW dd{pw + iw * 32 * (int64_t)Bp * Ap, p.Sw, p.tpw};
-            const size_t lds = (size_t)16 * 128 * (Nt + Kc) + (size_t)32 * 64 * 16;
-            if ((int64_t)lds > maxlds) return set_error(WALSH_ENOTSUP, "%s: shape needs %zu B of LDS", fn, lds);
-            const bool vec = out_o % 4 == 0 && in_o % 4 == 0 && ldx % 4 == 0 && ldg % 4 == 0 &&
-                             (uintptr_t)gc % valign == 0 && (uintptr_t)xc % valign == 0;
-            const dim3 G((unsigned)((int64_t)p.Sw * Nt * Kc)), B(kThreads);
-#define WALSH_DW(T, MMA, V) launch((hadamard_bwd_dw_kernel<T, MMA, V>), G, B, lds, s, ax, ag, dd)
-            if (bf16) { if (vec) WALSH_DW(uint16_t, true, true); else WALSH_DW(uint16_t, true, false); }
-            else      { if (vec) WALSH_DW(float, false, true); else WALSH_DW(float, false, false); }
-#undef WALSH_DW
-            const int rc = check_hip(hipGetLastError(), fn);
-            if (rc) return rc;
-            iw += p.Sw;
-        }
+#undef WALSH_BWD
+        const int rc = check_hip(hipGetLastError(), fn);
+        if (rc) return rc;
+        if (need_a) ia += p.Sa;
+        if (need_b) ib += p.Sb;
+        if (need_w) iw += p.Sw;
     }
     // with M == 0 every sum is empty: the reduction writes zeros
     BwdSum r{};
@@ -554,11 +602,8 @@ WALSH_EXPORT int walsh_hadamard_linear_bwd(const void *x, int64_t ldx, const voi
     r.Sa = (int)ia; r.Ap = Ap; r.Sb = (int)ib; r.Bp = Bp; r.Sw = (int)iw; r.Op = Bp; r.Ip = Ap;
     r.in_o = (int)in_o; r.out_o = (int)out_o; r.latent = latent;
     r.da = dalpha; r.db = dbeta; r.dw = dweight;
-    const int64_t total = (dalpha ? 32 * in_o : 0) + (dbeta ? 32 * out_o : 0) + (dweight ? 32 * in_o * out_o : 0);
-    if (total > 0) {
-        int grid = (int)ceil_div(total, 256);
-        if (grid > 4096) grid = 4096;
-        launch(hadamard_bwd_reduce_kernel, dim3(grid), dim3(256), 0, s, r);
-    }
+    int64_t bw, ba;
+    const int64_t nblk = sum_blocks(r, &bw, &ba);
+    if (nblk > 0) launch(hadamard_bwd_reduce_kernel, dim3((unsigned)nblk), dim3(kSumCols * kSumPhases), 0, s, r);
     return check_hip(hipGetLastError(), fn);
 }

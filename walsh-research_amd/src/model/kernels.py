@@ -270,8 +270,9 @@ def hadamard_linear_bwd(x: torch.Tensor, gy: torch.Tensor, in_o: int, out_o: int
         assert lat.shape == (32, out_o, in_o), "latent weight shape"
     ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
     esz = x.element_size()
-    nbytes = M * 32 * (in_o + out_o) * esz * 4 + M * 32 * in_o * esz
-    flops = M * 2 * 32 * in_o * out_o * 3
+    # algorithmic: x and gy read once, gx written once (+ the parameters)
+    nbytes = M * 32 * (2 * in_o + out_o) * esz + 4 * 32 * (in_o + out_o) * 3 + 4 * 32 * in_o * out_o * 2
+    flops = M * 32 * (3 * 2 * in_o * out_o + 20 * (in_o + out_o))
     _hip.call("walsh_hadamard_linear_bwd", xc.data_ptr(), 32 * in_o, gc.data_ptr(), 32 * out_o, M, in_o, out_o,
               ptr(kweight), ptr(kweight_t), alpha.data_ptr(), beta.data_ptr(), ptr(lat), ptr(gx), 32 * in_o,
               ptr(da), ptr(db), ptr(dw), code, ws.data_ptr(), nws, _hip.stream(dev),
