@@ -230,11 +230,32 @@ int walsh_fht_fwd(const void *x, int64_t rows, int64_t n, int normalize, void *y
  * walsh_octonion_linear_fwd: y[M, ldy] = (x[M, ldx] B^T) * beta[n % out_o];
  *   beta float [out_o]; x rows 16-byte aligned.  WALSH_BF16 multiplies bf16
  *   operands (the reference's kernel casts x to bf16 too, :402) with float32
- *   accumulation; WALSH_F32 uses float32 matrix cores. */
+ *   accumulation; WALSH_F32 uses float32 matrix cores.  beta may be null
+ *   (all ones).
+ *
+ * Backward (CayleyDicksonFunction.backward, src/model/cayley_dickson_cuda.py:
+ * 500-567, with physics.quantize_ternary's STE, physics.py:43-50):
+ * walsh_octonion_prepare_t: Bt[j*in_o + m][i*out_o + n] = S[i][j] *
+ *   W[i^j][n][m] * beta[n], rows of length roundup(8*out_o, 32); then
+ *   gx = walsh_octonion_linear_fwd(gy, in_o' = out_o, out_o' = in_o, Bt,
+ *   beta = null) is the input gradient (gy .* beta) B.
+ * walsh_octonion_bwd_fold: parameter gradients from C = gy^T x (float
+ *   [8*out_o][ldc], the sum of n_parts partial matrices part_stride floats
+ *   apart, e.g. split-K results of any GEMM):
+ *     dweight[w][n][m] = beta[n] sum_i S[i][i^w] C[i*out_o + n][(i^w)*in_o + m],
+ *       zeroed where latent (float [8][out_o][in_o], optional) is outside
+ *       [-1.5, 1.5];
+ *     dbeta[n] = sum_{i,j,m} S[i][j] W[i^j][n][m] C[i*out_o + n][j*in_o + m].
+ *   Either output may be null.  Fixed-order sums (float64). */
 int64_t walsh_octonion_weight_elems(int64_t in_o, int64_t out_o);
 int walsh_octonion_prepare(const uint8_t *packed, int64_t in_o, int64_t out_o, void *B, int dtype, void *stream);
 int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o, const void *B,
                               const float *beta, void *y, int64_t ldy, int dtype, void *stream);
+int walsh_octonion_prepare_t(const uint8_t *packed, int64_t in_o, int64_t out_o, const float *beta, void *Bt,
+                             int dtype, void *stream);
+int walsh_octonion_bwd_fold(const float *C, int64_t ldc, int64_t n_parts, int64_t part_stride, const uint8_t *packed,
+                            int64_t in_o, int64_t out_o, const float *beta, const float *latent, float *dweight,
+                            float *dbeta, void *stream);
 
 /* ------------------------------------------------------------------ A14-A17
  * mHC residual streams.  Stream tensors are [M tokens][n streams][C] with row
@@ -246,6 +267,14 @@ int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_
  *   [batch, n, n], n <= 8.
  */
 int walsh_sinkhorn_fwd(const float *h, int64_t batch, int64_t n, int64_t n_iter, float eps, float *out,
+                       void *stream);
+
+/* walsh_sinkhorn_bwd: gradient of walsh_sinkhorn_fwd (the autograd torch
+ *   derives for SinkhornKnopp.forward, src/model/mhc.py:214-229): dh = the
+ *   gradient wrt h for the output gradient g, float32 [batch, n, n], n <= 8.
+ *   The forward's intermediates are recomputed bit-identically per iteration
+ *   (O(n_iter^2) small steps per matrix), so nothing is saved between passes. */
+int walsh_sinkhorn_bwd(const float *h, const float *g, int64_t batch, int64_t n, int64_t n_iter, float eps, float *dh,
                        void *stream);
 
 /* walsh_mhc_pre_fwd: the three ResidualStreamMapping.forward calls of one

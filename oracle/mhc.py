@@ -20,6 +20,29 @@ def sinkhorn(h, n_iter: int = 20, eps: float = 1e-8, dtype=np.float64) -> np.nda
     return m
 
 
+def sinkhorn_bwd(h, g, n_iter: int = 20, eps: float = 1e-8) -> np.ndarray:
+    """Float64 reverse-mode gradient of ``sinkhorn`` wrt h for the output
+    gradient g (the autograd torch derives for ``mhc.py:214-229``): the
+    forward is taped, then each normalisation Y = X / (sum + eps) is undone
+    with dX = (dY - sum(dY * Y)) / (sum + eps) along the normalised axis, and
+    exp with dh = dM0 * M0."""
+    m0 = np.exp(np.asarray(h, np.float64))
+    tape = []
+    m = m0
+    for _ in range(n_iter):
+        c = m.sum(axis=-2, keepdims=True) + eps
+        t = m / c
+        r = t.sum(axis=-1, keepdims=True) + eps
+        u = t / r
+        tape.append((t, c, u, r))
+        m = u
+    G = np.asarray(g, np.float64)
+    for t, c, u, r in reversed(tape):
+        dT = (G - (G * u).sum(axis=-1, keepdims=True)) / r
+        G = (dT - (dT * t).sum(axis=-2, keepdims=True)) / c
+    return G * m0
+
+
 def sigmoid(a):
     return 1.0 / (1.0 + np.exp(-a))
 

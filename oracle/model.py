@@ -36,9 +36,30 @@ def sylvester(n=32):
 
 
 class Oracle:
+    """``grad=True`` turns the oracle into the gradient reference: every
+    floating entry of the state dict becomes a float64 leaf (tensors that
+    share storage in the model, like the tied embedding / output weight,
+    share one leaf), the Hadamard weights go through the STE of
+    physics.quantize_ternary (physics.py:43-50) instead of fixed codes, and
+    ``loss`` gives the cross-entropy whose backward fills ``leaf.grad``."""
+
     def __init__(self, sd, n_embd, n_head, n_layer, n_streams=4, head_mixing=True, block_size=256,
-                 use_moe=False, moe_max_experts=4):
-        self.sd = {k: (v.detach().cpu() if v.is_complex() else v.detach().float().cpu()) for k, v in sd.items()}
+                 use_moe=False, moe_max_experts=4, grad=False):
+        self.grad = grad
+        self.dt = torch.float64 if grad else torch.float32
+        if grad:
+            leaves, by_ptr = {}, {}
+            for k, v in sd.items():
+                if v.is_complex():
+                    leaves[k] = v.detach().cpu()
+                    continue
+                key = (v.data_ptr(), v.dtype, tuple(v.shape))
+                if key not in by_ptr:
+                    by_ptr[key] = v.detach().double().cpu().requires_grad_(v.is_floating_point())
+                leaves[k] = by_ptr[key]
+            self.sd = leaves
+        else:
+            self.sd = {k: (v.detach().cpu() if v.is_complex() else v.detach().float().cpu()) for k, v in sd.items()}
         self.C = n_embd
         self.n_head = n_head
         self.n_layer = n_layer
@@ -46,10 +67,14 @@ class Oracle:
         self.head_mixing = head_mixing
         self.use_moe = use_moe
         self.moe_k = moe_max_experts
-        self.H = sylvester(32)
+        self.H = sylvester(32).to(self.dt)
         self._codes = {}
 
     def codes(self, key):
+        if self.grad:
+            w = self.sd[key]
+            wc = w.clamp(-1.5, 1.5)
+            return wc + (ternary_codes(w.detach()) - wc).detach()
         if key not in self._codes:
             self._codes[key] = ternary_codes(self.sd[key])
         return self._codes[key]
@@ -61,7 +86,7 @@ class Oracle:
         G, out_o, in_o = w.shape
         lead = x.shape[:-1]
         xs = x.reshape(*lead, G, in_o) * self.sd[p + '.alpha']
-        xm = torch.einsum('...gi,gh->...hi', xs.float(), self.H)
+        xm = torch.einsum('...gi,gh->...hi', xs.to(self.dt), self.H)
         yp = torch.einsum('...gi,goi->...go', xm, w)
         ym = torch.einsum('...go,gh->...ho', yp, self.H)
         return (ym * self.sd[p + '.beta']).reshape(*lead, G * out_o)
@@ -120,12 +145,12 @@ class Oracle:
 
     # ---------------------------------------------------------------- harness
     def rmsnorm(self, x, w, eps=1e-6):
-        xf = x.float()
+        xf = x.to(self.dt)
         return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)) * w
 
     def rope(self, xq, xk, freqs):
-        xq_ = torch.view_as_complex(xq.float().reshape(*xq.shape[:-1], -1, 2))
-        xk_ = torch.view_as_complex(xk.float().reshape(*xk.shape[:-1], -1, 2))
+        xq_ = torch.view_as_complex(xq.to(self.dt).reshape(*xq.shape[:-1], -1, 2))
+        xk_ = torch.view_as_complex(xk.to(self.dt).reshape(*xk.shape[:-1], -1, 2))
         f = freqs[:xq.shape[1]].unsqueeze(0).unsqueeze(2)
         return torch.view_as_real(xq_ * f).flatten(3), torch.view_as_real(xk_ * f).flatten(3)
 
@@ -154,6 +179,13 @@ class Oracle:
         g = self.hadamard_linear(x, p + '.gate_proj.inner')
         u = self.hadamard_linear(x, p + '.up_proj.inner')
         return self.hadamard_linear(F.silu(g) * u, p + '.down_proj.inner')
+
+    def loss(self, idx, targets):
+        """mHCWalsh.forward's loss with targets (mhc.py:668-672): logits of
+        every position, cross-entropy with ignore_index -1."""
+        _, ho = self.forward(idx, return_hidden=True)
+        logits = ho @ self.sd['output.weight'].t()
+        return F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1), ignore_index=-1)
 
     def forward(self, idx, return_hidden=False):
         """Logits of the last position [B, 1, V] (mhc.py:617-681, targets=None)."""

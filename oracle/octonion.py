@@ -77,3 +77,35 @@ def dense_matrix(codes, beta) -> np.ndarray:
         for j in range(8):
             A[i * out_o:(i + 1) * out_o, j * in_o:(j + 1) * in_o] = SIGN_TABLE[i, j] * w[WEIGHT_IDX[i, j]]
     return np.asarray(beta, np.float64).reshape(1, -1).repeat(8, 0).reshape(-1)[:, None] * A
+
+
+def octonion_linear_bwd_f64(x_parts, codes, beta, gy_parts, latent=None):
+    """Float64 gradients of ``octonion_linear_f64`` for output gradients gy
+    [8, M, out_o]: the exact transpose of the forward's block structure (what
+    CayleyDicksonFunction.backward computes, ``cayley_dickson_cuda.py:500-567``)
+    and the STE of physics.quantize_ternary (``physics.py:48-50``): the weight
+    gradient is zero where the latent weight lies outside [-1.5, 1.5].
+
+    Returns (dx [8, M, in_o], dW [8, out_o, in_o], dbeta [out_o]).
+    """
+    x = np.asarray(x_parts, dtype=np.float64)
+    w = np.asarray(codes, dtype=np.float64)
+    gy = np.asarray(gy_parts, dtype=np.float64)
+    b = np.asarray(beta, np.float64)
+    g = gy * b
+    dx = np.zeros_like(x)
+    dW = np.zeros_like(w)
+    dbeta = np.zeros(w.shape[1])
+    for i in range(8):
+        ypre = np.zeros(gy.shape[1:])
+        for j in range(8):
+            k = WEIGHT_IDX[i, j]
+            s = SIGN_TABLE[i, j]
+            dx[j] += s * (g[i] @ w[k])
+            dW[k] += s * (g[i].T @ x[j])
+            ypre += s * (x[j] @ w[k].T)
+        dbeta += (gy[i] * ypre).sum(0)
+    if latent is not None:
+        lat = np.asarray(latent, np.float64)
+        dW = dW * ((lat >= -1.5) & (lat <= 1.5))
+    return dx, dW, dbeta

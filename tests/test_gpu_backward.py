@@ -148,3 +148,144 @@ def test_fht_function_backward():
     H = torch.tensor(ohad.sylvester(64), dtype=torch.float64)
     ref = (g.double().cpu() @ H).numpy()
     assert_close(x.grad.cpu().numpy(), ref, torch.float32, "fht grad")
+
+
+# ---------------------------------------------------------------- octonion
+
+def _oct_parts(rows, n_o):
+    return np.stack(np.split(np.asarray(rows, np.float64), 8, axis=-1))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("in_o,out_o,M", [(128, 128, 300), (16, 8, 100), (5, 3, 33), (64, 128, 1)])
+def test_octonion_bwd_vs_oracle(K, in_o, out_o, M, dtype):
+    from oracle import octonion as ooct
+    print(f"case octonion in_o={in_o} out_o={out_o} M={M} dtype={dtype}", flush=True)
+    gen = torch.Generator().manual_seed(in_o + 3 * out_o + M)
+    latent = torch.rand(8, out_o, in_o, generator=gen) * 4 - 2
+    beta = torch.randn(out_o, generator=gen)
+    x = torch.randn(M, 8 * in_o, generator=gen).to(dtype)
+    gy = torch.randn(M, 8 * out_o, generator=gen).to(dtype)
+    q = K.ternary_quantize(latent.cuda(), codes=True, packed=True)
+    gx, dw, db = K.octonion_linear_bwd(x.cuda(), gy.cuda(), in_o, out_o, q["packed"], beta.cuda(),
+                                       latent=latent.cuda())
+    torch.cuda.synchronize()
+    ref = ooct.octonion_linear_bwd_f64(_oct_parts(x.double().numpy(), in_o), q["codes"].cpu().numpy(),
+                                       beta.double().numpy(), _oct_parts(gy.double().numpy(), out_o),
+                                       latent=latent.double().numpy())
+    assert gx.dtype == dtype and gx.shape == x.shape
+    assert_close(np.concatenate(list(_oct_parts(gx.float().cpu().numpy(), in_o)), axis=1),
+                 np.concatenate(list(ref[0]), axis=1), dtype, f"oct gx {in_o}x{out_o} M={M}")
+    assert_close(dw.cpu().numpy(), ref[1], dtype, f"oct dweight {in_o}x{out_o} M={M}")
+    assert_close(db.cpu().numpy(), ref[2], dtype, f"oct dbeta {in_o}x{out_o} M={M}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_octonion_module_autograd(dtype):
+    from oracle import octonion as ooct
+    from src.model import kernels
+    from src.model.cayley_dickson_cuda import OctonionFusedLinear
+    torch.manual_seed(11)
+    layer = OctonionFusedLinear(256, 512).cuda()
+    xr = torch.randn(2, 40, 256, device="cuda", dtype=dtype)
+    parts = tuple(p.detach().requires_grad_(True) for p in xr.split(32, dim=-1))
+    ys = layer(parts)
+    gys = [torch.randn_like(y) for y in ys]
+    sum((y * g).sum() for y, g in zip(ys, gys)).backward()
+    torch.cuda.synchronize()
+    codes = kernels.ternary_quantize(layer.weight.detach(), codes=True)["codes"].cpu().numpy()
+    ref = ooct.octonion_linear_bwd_f64(np.stack([p.detach().double().cpu().numpy().reshape(-1, 32) for p in parts]),
+                                       codes, layer.beta.detach().double().cpu().numpy(),
+                                       np.stack([g.double().cpu().numpy().reshape(-1, 64) for g in gys]),
+                                       latent=layer.weight.detach().double().cpu().numpy())
+    gx = np.stack([p.grad.float().cpu().numpy().reshape(-1, 32) for p in parts])
+    assert_close(gx, ref[0], dtype, "oct module x.grad")
+    assert_close(layer.weight.grad.cpu().numpy(), ref[1], dtype, "oct module weight.grad")
+    assert_close(layer.beta.grad.cpu().numpy(), ref[2], dtype, "oct module beta.grad")
+
+
+# ---------------------------------------------------------------- Sinkhorn
+
+@pytest.mark.parametrize("n", [1, 2, 4, 7])
+def test_sinkhorn_bwd_vs_oracle(K, n):
+    from oracle import mhc as omhc
+    rng = np.random.default_rng(n)
+    h = rng.normal(0, 1.5, (300, n, n)).astype(np.float32)
+    g = rng.normal(0, 1, (300, n, n)).astype(np.float32)
+    dh = K.sinkhorn_bwd(torch.from_numpy(h).cuda(), torch.from_numpy(g).cuda()).cpu().numpy()
+    ref = omhc.sinkhorn_bwd(h.astype(np.float64), g.astype(np.float64))
+    if n == 1:
+        # a 1x1 projection is exp(h) / (exp(h) + eps) ~ 1: the exact gradient
+        # is O(eps) and rounds to 0 in float32
+        assert np.abs(ref).max() < 1e-6 and np.abs(dh).max() < 1e-6
+        return
+    assert_close(dh, ref, torch.float32, f"sinkhorn bwd n={n}")
+
+
+def test_sinkhorn_function_autograd():
+    from oracle import mhc as omhc
+    from src.model.mhc import SinkhornKnopp
+    rng = np.random.default_rng(3)
+    h = torch.from_numpy(rng.normal(0, 1, (2, 8, 4, 4)).astype(np.float32)).cuda().requires_grad_(True)
+    g = torch.from_numpy(rng.normal(0, 1, (2, 8, 4, 4)).astype(np.float32)).cuda()
+    (SinkhornKnopp()(h) * g).sum().backward()
+    ref = omhc.sinkhorn_bwd(h.detach().double().cpu().numpy(), g.double().cpu().numpy())
+    assert_close(h.grad.cpu().numpy(), ref, torch.float32, "SinkhornKnopp grad")
+
+
+# ---------------------------------------------------------------- whole model
+
+def _grad_rel(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    nb = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / nb) if nb > 0 else float(np.linalg.norm(a - b))
+
+
+@pytest.mark.parametrize("C,n_layer,vocab,T", [(64, 2, 256, 16), (256, 2, 512, 32)])
+def test_mhcwalsh_backward_matches_oracle(C, n_layer, vocab, T):
+    """One training backward of mHCWalsh (float32) through the HIP backward
+    kernels (Hadamard linears, Sinkhorn) and the differentiable training
+    composition, against float64 autograd of the oracle model with the
+    reference's STE; every parameter's gradient is compared."""
+    from oracle.model import Oracle
+    from src.model import WalshConfig, mHCWalsh
+    torch.manual_seed(0)
+    cfg = WalshConfig(block_size=64, vocab_size=vocab, n_layer=n_layer, n_head=32, n_embd=C, algebra='hadamard',
+                      head_mixing=True)
+    model = mHCWalsh(cfg, n_streams=4).cuda().eval()
+    g = torch.Generator().manual_seed(1)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith(('.alpha', '.beta', 'norm.weight')) and p.dim() > 0:
+                p.mul_(1 + 0.2 * torch.randn(p.shape, generator=g).to(p.device))
+    idx = torch.randint(0, vocab, (2, T), generator=g)
+    tgt = torch.randint(0, vocab, (2, T), generator=g)
+    _, loss = model(idx.cuda(), targets=tgt.cuda())
+    loss.backward()
+    torch.cuda.synchronize()
+    orc = Oracle(model.state_dict(), C, 32, n_layer, grad=True)
+    ref_loss = orc.loss(idx, tgt)
+    ref_loss.backward()
+    print(f"loss gpu={loss.item():.6f} oracle={ref_loss.item():.6f}", flush=True)
+    assert abs(loss.item() - ref_loss.item()) <= 1e-5 * abs(ref_loss.item())
+    got, ref = {}, {}
+    for name, p in model.named_parameters():
+        assert p.grad is not None, f"{name}: no gradient"
+        assert orc.sd[name].grad is not None, f"{name}: no oracle gradient"
+        got[name] = p.grad.double().cpu().numpy().ravel()
+        ref[name] = orc.sd[name].grad.numpy().ravel()
+    # all gradients together at the float32 bar; each parameter within 1e-4
+    # of its own norm plus 1e-6 of the largest gradient norm (some exact
+    # gradients are ~0, e.g. H_res of layer 0 mixes identical streams, and
+    # only a floor relative to the model's gradient scale is meaningful there)
+    total = _grad_rel(np.concatenate(list(got.values())), np.concatenate(list(ref.values())))
+    G = max(np.linalg.norm(v) for v in ref.values())
+    bad = [(name, float(np.linalg.norm(got[name] - ref[name])), float(np.linalg.norm(ref[name])))
+           for name in got if np.linalg.norm(got[name] - ref[name]) > 1e-4 * np.linalg.norm(ref[name]) + 1e-6 * G]
+    worst = max((_grad_rel(got[n], ref[n]), n) for n in got if np.linalg.norm(ref[n]) > 1e-3 * G)
+    print(f"C={C} L={n_layer}: {len(got)} parameters, all-gradient rel_norm {total:.2e}, worst rel_norm of the "
+          f"{sum(np.linalg.norm(ref[n]) > 1e-3 * G for n in got)} with norm > 1e-3 max: {worst[0]:.2e} ({worst[1]})",
+          flush=True)
+    assert total <= 1e-5, total
+    assert not bad, bad

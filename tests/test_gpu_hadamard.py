@@ -285,6 +285,7 @@ def test_head_mixer_group_view_and_output_slice(K):
     assert_close(o[:, :, 32 * D:], ref, torch.bfloat16, "mixer group view")
 
 
+@torch.no_grad()
 def test_head_mixer_module_matches_torch_path():
     from src.model.hadamard import HadamardHeadMixerFused
     torch.manual_seed(3)

@@ -96,7 +96,15 @@ def test_mhc_pre_post_match_oracle(K, dtype, M, n, C):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_stream_module_matches_oracle(dtype):
+@pytest.mark.parametrize("tracked", [False, True])
+def test_stream_module_matches_oracle(dtype, tracked):
+    """The fused inference kernels (untracked) and the differentiable
+    training composition (autograd tracking the call) both match the oracle."""
+    with torch.set_grad_enabled(tracked):
+        _stream_module_case(dtype)
+
+
+def _stream_module_case(dtype):
     from src.model import mHCResidualStream
     torch.manual_seed(0)
     n, C, B, T = 4, 64, 2, 9
@@ -115,15 +123,15 @@ def test_stream_module_matches_oracle(dtype):
     xq = x.float().cpu().numpy().reshape(B * T, n, C).astype(np.float64)
     L = lin.double().cpu().numpy()
     ref, *_ = omhc.stream_forward(xq, maps, lambda v: v @ L, float(torch.finfo(dtype).eps))
-    assert_close(y.float().cpu().numpy().reshape(B * T, n, C), ref, dtype, f"stream {dtype}")
+    assert_close(y.detach().float().cpu().numpy().reshape(B * T, n, C), ref, dtype, f"stream {dtype}")
     # standalone mappings agree with the fused path
     xf = x.reshape(B, T, n * C)
     hr = s.H_res(xf)
     hp = s.H_pre(xf)
     _, hp_ref, _, hr_ref, _ = omhc.stream_forward(xq, maps, lambda v: v, float(torch.finfo(dtype).eps))
     tol = 1e-5 if dtype == torch.float32 else 1e-2
-    assert np.max(np.abs(hr.cpu().numpy().reshape(-1, n, n) - hr_ref)) < tol
-    assert np.max(np.abs(hp.cpu().numpy().reshape(-1, n) - hp_ref[:, 0])) < tol
+    assert np.max(np.abs(hr.detach().cpu().numpy().reshape(-1, n, n) - hr_ref)) < tol
+    assert np.max(np.abs(hp.detach().cpu().numpy().reshape(-1, n) - hp_ref[:, 0])) < tol
 
 
 # ------------------------------------------------------------------ octonion
@@ -147,6 +155,7 @@ def test_octonion_linear_matches_oracle(K, dtype, M, in_o, out_o):
     assert_close(y.float().cpu().numpy(), ref, dtype, f"octonion {dtype} M={M} {in_o}x{out_o}")
 
 
+@torch.no_grad()
 def test_octonion_module_tuple_interface():
     from src.model.cayley_dickson_cuda import OctonionFusedLinear, cayley_dickson_fused
     from src.model.physics import OctonionTernaryLinearRef

@@ -30,11 +30,11 @@ def test_hadamard_layer_classes(cls_name):
     assert y.shape == (3, 7, 1376) and y.dtype == torch.float32
     ref = ohad.hadamard_linear_f64(x.reshape(-1, 512).cpu().numpy(), _codes(layer.weight),
                                    layer.alpha.detach().cpu().numpy(), layer.beta.detach().cpu().numpy())
-    assert_close(y.reshape(-1, 1376).cpu().numpy(), ref, torch.float32, cls_name)
+    assert_close(y.detach().reshape(-1, 1376).cpu().numpy(), ref, torch.float32, cls_name)
     with torch.autocast("cuda", dtype=torch.bfloat16):
         yb = layer(x)
     assert yb.dtype == torch.float32          # cast back to the input dtype, as the reference does
-    assert_close(yb.reshape(-1, 1376).cpu().numpy(), ref, torch.bfloat16, cls_name + " autocast")
+    assert_close(yb.detach().reshape(-1, 1376).cpu().numpy(), ref, torch.bfloat16, cls_name + " autocast")
 
 
 def test_tuple_interface_in_place_and_copy():

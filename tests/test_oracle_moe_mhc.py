@@ -173,3 +173,32 @@ def test_stream_identity_layer_closed_form():
 def test_rms_eps_values():
     assert mhc.rms_eps(np.float32) == float(torch.finfo(torch.float32).eps)
     assert mhc.rms_eps('bfloat16') == float(torch.finfo(torch.bfloat16).eps)
+
+
+def test_sinkhorn_bwd_matches_torch_autograd_and_finite_differences():
+    """oracle.mhc.sinkhorn_bwd against torch float64 autograd of the
+    reference loop (mhc.py:214-229) and central differences."""
+    import torch
+    from oracle import mhc as omhc
+    rng = np.random.default_rng(12)
+    for n in (1, 2, 4, 7):
+        h = rng.normal(0, 1.5, (5, n, n))
+        g = rng.normal(0, 1, (5, n, n))
+        ht = torch.tensor(h, requires_grad=True)
+        M = torch.exp(ht)
+        for _ in range(20):
+            M = M / (M.sum(dim=-2, keepdim=True) + 1e-8)
+            M = M / (M.sum(dim=-1, keepdim=True) + 1e-8)
+        (M * torch.tensor(g)).sum().backward()
+        dh = omhc.sinkhorn_bwd(h, g)
+        assert np.allclose(dh, ht.grad.numpy(), rtol=1e-10, atol=1e-12)
+        eps = 1e-6
+        for idx in ((0, 0, 0), (3, n - 1, 0), (4, n // 2, n - 1)):
+            e = np.zeros_like(h)
+            e[idx] = eps
+            fd = ((omhc.sinkhorn(h + e) * g).sum() - (omhc.sinkhorn(h - e) * g).sum()) / (2 * eps)
+            assert abs(fd - dh[idx]) <= 1e-6 * max(1.0, abs(fd))
+    # rows and columns of the output sum to ~1, so a constant gradient has
+    # (almost) no effect: the gradient of sum(M) is ~0
+    h = rng.normal(0, 1, (3, 4, 4))
+    assert np.abs(omhc.sinkhorn_bwd(h, np.ones_like(h))).max() < 1e-6

@@ -89,3 +89,45 @@ def test_bf16_round_matches_torch():
     v = np.random.default_rng(7).standard_normal(1000).astype(np.float32)
     t = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
     assert np.array_equal(octonion.bf16_round(v), t)
+
+
+def test_bwd_oracle_matches_torch_autograd():
+    """The gradient oracle against torch float64 autograd of the table-driven
+    forward with physics.quantize_ternary's STE (physics.py:43-50)."""
+    import torch
+    gen = torch.Generator().manual_seed(7)
+    M, in_o, out_o = 9, 5, 3
+    x = torch.randn(8, M, in_o, generator=gen, dtype=torch.float64, requires_grad=True)
+    latent = (torch.rand(8, out_o, in_o, generator=gen, dtype=torch.float64) * 4 - 2).requires_grad_(True)
+    beta = torch.randn(out_o, generator=gen, dtype=torch.float64, requires_grad=True)
+    gy = torch.randn(8, M, out_o, generator=gen, dtype=torch.float64)
+    gamma = latent.abs().mean() + 1e-8
+    wq = torch.clamp(torch.round(latent / gamma), -1, 1)
+    wc = latent.clamp(-1.5, 1.5)
+    w = wc + (wq - wc).detach()
+    ys = []
+    for i in range(8):
+        yi = 0
+        for j in range(8):
+            yi = yi + int(octonion.SIGN_TABLE[i, j]) * (x[j] @ w[int(octonion.WEIGHT_IDX[i, j])].T)
+        ys.append(yi * beta)
+    (torch.stack(ys) * gy).sum().backward()
+    assert (latent.abs() > 1.5).any()
+    dx, dW, db = octonion.octonion_linear_bwd_f64(x.detach().numpy(), wq.detach().numpy(), beta.detach().numpy(),
+                                                  gy.numpy(), latent=latent.detach().numpy())
+    for got, ref in ((dx, x.grad), (dW, latent.grad), (db, beta.grad)):
+        assert np.allclose(got, ref.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_bwd_dx_is_transpose_of_dense_matrix():
+    rng = np.random.default_rng(8)
+    M, in_o, out_o = 4, 3, 2
+    codes = rng.integers(-1, 2, size=(8, out_o, in_o)).astype(np.int8)
+    beta = rng.normal(size=out_o)
+    x = rng.normal(size=(8, M, in_o))
+    gy = rng.normal(size=(8, M, out_o))
+    A = octonion.dense_matrix(codes, beta)
+    dx, _, _ = octonion.octonion_linear_bwd_f64(x, codes, beta, gy)
+    g_rows = np.concatenate(list(gy), axis=1)           # [M, 8*out_o], part-major
+    dx_rows = np.concatenate(list(dx), axis=1)
+    assert np.allclose(dx_rows, g_rows @ A, rtol=1e-12, atol=1e-12)

@@ -105,6 +105,84 @@ __device__ __forceinline__ void token_constraints_quad(int t, int r, int tok, in
 }
 
 // ---------------------------------------------------------------- sinkhorn
+// Backward of sinkhorn_regs for the output gradient g (the autograd of
+// SinkhornKnopp.forward, src/model/mhc.py:214-229, which the reference leaves
+// to torch): per matrix, walking the iterations backwards, the state S_k
+// before iteration k is recomputed from exp(h) with the forward's own
+// operations (so every intermediate is bit-identical to the forward's), then
+//   row step    U = T / r,  r_i = sum_j T_ij + eps:  dT_ij = (G_ij - sum_j' G_ij' U_ij') / r_i
+//   column step T = S / c,  c_j = sum_i S_ij + eps:  dS_ij = (dT_ij - sum_i' dT_i'j T_i'j) / c_j
+// and finally dh = G .* exp(h).  O(n_iter^2) small iterations per matrix.
+template <int NMAX>
+__global__ void sinkhorn_bwd_kernel(const float *__restrict__ h, const float *__restrict__ g, int64_t batch, int n,
+                                    int n_iter, float eps, float *__restrict__ dh) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < batch; b += (int64_t)gridDim.x * blockDim.x) {
+        float m0[NMAX][NMAX], G[NMAX][NMAX];
+        const float *src = h + b * n * n;
+        const float *gs = g + b * n * n;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i)
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) {
+                m0[i][j] = (i < n && j < n) ? expf(src[i * n + j]) : 0.f;
+                G[i][j] = (i < n && j < n) ? gs[i * n + j] : 0.f;
+            }
+        for (int k = n_iter - 1; k >= 0; --k) {
+            float S[NMAX][NMAX], T[NMAX][NMAX], c[NMAX], r[NMAX];
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i)
+#pragma unroll
+                for (int j = 0; j < NMAX; ++j) S[i][j] = m0[i][j];
+            for (int it = 0; it <= k; ++it) {
+#pragma unroll
+                for (int j = 0; j < NMAX; ++j) {
+                    float sum = 0.f;
+#pragma unroll
+                    for (int i = 0; i < NMAX; ++i) sum += (i < n) ? S[i][j] : 0.f;
+                    c[j] = sum + eps;
+#pragma unroll
+                    for (int i = 0; i < NMAX; ++i) T[i][j] = (j < n) ? __fdiv_rn(S[i][j], c[j]) : 0.f;
+                }
+#pragma unroll
+                for (int i = 0; i < NMAX; ++i) {
+                    float sum = 0.f;
+#pragma unroll
+                    for (int j = 0; j < NMAX; ++j) sum += (j < n) ? T[i][j] : 0.f;
+                    r[i] = sum + eps;
+                    if (it < k) {
+#pragma unroll
+                        for (int j = 0; j < NMAX; ++j) S[i][j] = (i < n) ? __fdiv_rn(T[i][j], r[i]) : 0.f;
+                    }
+                }
+            }
+            // now T, c, r are iteration k's; U = T / r
+            float dT[NMAX][NMAX];
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) {
+                float dot = 0.f;
+#pragma unroll
+                for (int j = 0; j < NMAX; ++j) dot += (i < n && j < n) ? G[i][j] * __fdiv_rn(T[i][j], r[i]) : 0.f;
+#pragma unroll
+                for (int j = 0; j < NMAX; ++j) dT[i][j] = (i < n && j < n) ? __fdiv_rn(G[i][j] - dot, r[i]) : 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) {
+                float dot = 0.f;
+#pragma unroll
+                for (int i = 0; i < NMAX; ++i) dot += (i < n && j < n) ? dT[i][j] * T[i][j] : 0.f;
+#pragma unroll
+                for (int i = 0; i < NMAX; ++i) G[i][j] = (i < n && j < n) ? __fdiv_rn(dT[i][j] - dot, c[j]) : 0.f;
+            }
+        }
+        float *dst = dh + b * n * n;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i)
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j)
+                if (i < n && j < n) dst[i * n + j] = G[i][j] * m0[i][j];
+    }
+}
+
 __global__ void sinkhorn_kernel(const float *__restrict__ h, int64_t batch, int n, int n_iter, float eps,
                                 float *__restrict__ out) {
     for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < batch; b += (int64_t)gridDim.x * blockDim.x) {
@@ -773,6 +851,26 @@ WALSH_EXPORT int walsh_sinkhorn_fwd(const float *h, int64_t batch, int64_t n, in
     launch(sinkhorn_kernel, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream, h, batch, (int)n,
                        (int)n_iter, eps, out);
     return check_hip(hipGetLastError(), "walsh_sinkhorn_fwd launch");
+}
+
+WALSH_EXPORT int walsh_sinkhorn_bwd(const float *h, const float *g, int64_t batch, int64_t n, int64_t n_iter, float eps,
+                                    float *dh, void *stream) {
+    if (batch > 0 && (!h || !g || !dh)) return set_error(WALSH_EINVAL, "walsh_sinkhorn_bwd: null pointer");
+    if (batch < 0 || n < 1 || n > 8 || n_iter < 0)
+        return set_error(n > 8 ? WALSH_ENOTSUP : WALSH_EINVAL,
+                         "walsh_sinkhorn_bwd: batch=%lld n=%lld n_iter=%lld (n must be 1..8)", (long long)batch,
+                         (long long)n, (long long)n_iter);
+    if (batch == 0) return WALSH_OK;
+    const int block = 64;
+    int64_t grid = ceil_div(batch, block);
+    if (grid > (int64_t)device_info().cu_count * 16) grid = (int64_t)device_info().cu_count * 16;
+    if (n <= 4)
+        launch(sinkhorn_bwd_kernel<4>, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream, h, g, batch, (int)n,
+               (int)n_iter, eps, dh);
+    else
+        launch(sinkhorn_bwd_kernel<8>, dim3((unsigned)grid), dim3(block), 0, (hipStream_t)stream, h, g, batch, (int)n,
+               (int)n_iter, eps, dh);
+    return check_hip(hipGetLastError(), "walsh_sinkhorn_bwd launch");
 }
 
 WALSH_EXPORT int walsh_mhc_pre_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C, const void *phi,

@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int n = n0 + wn * 64 + j * 16 + fr;
-        const float b = n < a.N ? a.beta[n % a.out_o] : 0.f;
+        const float b = n < a.N ? (a.beta ? a.beta[n % a.out_o] : 1.f) : 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -168,9 +168,131 @@ __global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs 
     }
 }
 
+// ------------------------------------------------------------------ backward
+// The layer is y = (x B^T) .* beta~ with beta~[i*out_o + n] = beta[n].  For an
+// output gradient gy:
+//   gx = (gy .* beta~) B = gy Bt^T with Bt[j*in_o + m][i*out_o + n] =
+//        S[i][j] W[i^j][n][m] beta[n]    (the forward GEMM on Bt, no beta)
+//   C  = gy^T x                          [8*out_o][8*in_o], K = tokens
+//   dW[w][n][m] = beta[n] sum_i S[i][i^w] C[i*out_o + n][(i^w)*in_o + m]
+//   dbeta[n]    = sum_{i,j,m} S[i][j] W[i^j][n][m] C[i*out_o + n][j*in_o + m]
+// (each weight block w = i^j appears once per output part i).  The STE of
+// physics.quantize_ternary passes dW where -1.5 <= latent <= 1.5.
+
+// Bt rows j*in_o + m, row length Np (>= 8*out_o, zero padded).
+template <typename T>
+__global__ void octonion_expand_t_kernel(const uint8_t *__restrict__ packed, int in_o, int out_o,
+                                         const float *__restrict__ beta, int Np, T *__restrict__ Bt) {
+    const int64_t R = 8LL * in_o;
+    const int64_t total = R * Np;
+    const int kp4 = (int)ceil_div(in_o, 4);
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = e / Np;
+        const int col = (int)(e - row * Np);
+        float v = 0.f;
+        if (col < 8 * out_o) {
+            const int j = (int)(row / in_o), m = (int)(row - (int64_t)j * in_o);
+            const int i = col / out_o, n = col - i * out_o;
+            const int w = i ^ j;
+            const uint32_t byte = packed[((int64_t)w * out_o + n) * kp4 + m / 4];
+            const int code = (int)((byte >> (6 - 2 * (m & 3))) & 3u) - 1;
+            v = (float)(kOctSign[i][j] * code) * beta[n];
+        }
+        Act<T>::store(Bt + e, v);
+    }
+}
+
+// dW and dbeta from C.  Threads [0, 8*out_o*in_o) take one dW element each;
+// workgroups past that take one dbeta[n] each (256 threads, fixed-order tree).
+__global__ __launch_bounds__(256) void octonion_fold_kernel(const float *__restrict__ C, int64_t ldc, int Sc,
+                                                            int64_t cstride, const uint8_t *__restrict__ packed,
+                                                            int in_o, int out_o, const float *__restrict__ beta,
+                                                            const float *__restrict__ latent, float *__restrict__ dw,
+                                                            float *__restrict__ db, int dw_blocks) {
+    const int kp4 = (int)ceil_div(in_o, 4);
+    if ((int)blockIdx.x < dw_blocks) {
+        const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (!dw || e >= 8LL * out_o * in_o) return;
+        const int m = (int)(e % in_o);
+        const int64_t wn = e / in_o;
+        const int n = (int)(wn % out_o), w = (int)(wn / out_o);
+        double acc = 0.0;
+        for (int i = 0; i < 8; ++i) {
+            const int j = i ^ w;
+            const int64_t off = (int64_t)(i * out_o + n) * ldc + (int64_t)j * in_o + m;
+            double c = 0.0;
+            for (int s = 0; s < Sc; ++s) c += (double)C[s * cstride + off];
+            acc += kOctSign[i][j] * c;
+        }
+        float v = (float)(acc * (double)beta[n]);
+        if (latent) {
+            const float lw = latent[e];
+            v = (lw >= -1.5f && lw <= 1.5f) ? v : 0.f;
+        }
+        dw[e] = v;
+        return;
+    }
+    if (!db) return;
+    __shared__ double part[256];
+    const int n = (int)blockIdx.x - dw_blocks;
+    double acc = 0.0;
+    for (int e = threadIdx.x; e < 64 * in_o; e += blockDim.x) {  // e = (i*8 + j)*in_o + m
+        const int m = e % in_o, ij = e / in_o, i = ij >> 3, j = ij & 7;
+        const uint32_t byte = packed[((int64_t)(i ^ j) * out_o + n) * kp4 + m / 4];
+        const int code = (int)((byte >> (6 - 2 * (m & 3))) & 3u) - 1;
+        if (!code) continue;
+        const int64_t off = (int64_t)(i * out_o + n) * ldc + (int64_t)j * in_o + m;
+        double c = 0.0;
+        for (int s = 0; s < Sc; ++s) c += (double)C[s * cstride + off];
+        acc += (double)(kOctSign[i][j] * code) * c;
+    }
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) part[threadIdx.x] += part[threadIdx.x + st];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) db[n] = (float)part[0];
+}
+
 }  // namespace walsh
 
 using namespace walsh;
+
+WALSH_EXPORT int walsh_octonion_prepare_t(const uint8_t *packed, int64_t in_o, int64_t out_o, const float *beta,
+                                          void *Bt, int dtype, void *stream) {
+    if (!packed || !beta || !Bt) return set_error(WALSH_EINVAL, "walsh_octonion_prepare_t: null pointer");
+    if (in_o <= 0 || out_o <= 0 || in_o > 65536 || out_o > 65536)
+        return set_error(WALSH_EINVAL, "walsh_octonion_prepare_t: bad shape");
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "walsh_octonion_prepare_t: dtype");
+    const int Np = (int)(ceil_div(8 * out_o, 32) * 32);
+    const int64_t total = 8 * in_o * (int64_t)Np;
+    int64_t grid = ceil_div(total, 256);
+    if (grid > 8192) grid = 8192;
+    if (dtype == WALSH_BF16)
+        launch(octonion_expand_t_kernel<uint16_t>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, packed,
+               (int)in_o, (int)out_o, beta, Np, (uint16_t *)Bt);
+    else
+        launch(octonion_expand_t_kernel<float>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, packed,
+               (int)in_o, (int)out_o, beta, Np, (float *)Bt);
+    return check_hip(hipGetLastError(), "walsh_octonion_prepare_t launch");
+}
+
+WALSH_EXPORT int walsh_octonion_bwd_fold(const float *C, int64_t ldc, int64_t n_parts, int64_t part_stride,
+                                         const uint8_t *packed, int64_t in_o, int64_t out_o, const float *beta,
+                                         const float *latent, float *dweight, float *dbeta, void *stream) {
+    if (!C || !packed || !beta) return set_error(WALSH_EINVAL, "walsh_octonion_bwd_fold: null pointer");
+    if (in_o <= 0 || out_o <= 0 || in_o > 65536 || out_o > 65536 || ldc < 8 * in_o || n_parts < 1 ||
+        (n_parts > 1 && part_stride < 8 * out_o * ldc))
+        return set_error(WALSH_EINVAL, "walsh_octonion_bwd_fold: bad shape");
+    const int64_t nw = 8 * out_o * in_o;
+    const int dw_blocks = dweight ? (int)ceil_div(nw, 256) : 0;
+    const int64_t grid = dw_blocks + (dbeta ? out_o : 0);
+    if (grid == 0) return WALSH_OK;
+    launch(octonion_fold_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, C, ldc, (int)n_parts,
+           part_stride, packed, (int)in_o, (int)out_o, beta, latent, dweight, dbeta, dw_blocks);
+    return check_hip(hipGetLastError(), "walsh_octonion_bwd_fold launch");
+}
 
 WALSH_EXPORT int64_t walsh_octonion_weight_elems(int64_t in_o, int64_t out_o) {
     if (in_o <= 0 || out_o <= 0) return 0;
@@ -200,7 +322,7 @@ WALSH_EXPORT int walsh_octonion_prepare(const uint8_t *packed, int64_t in_o, int
 WALSH_EXPORT int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
                                            const void *B, const float *beta, void *y, int64_t ldy, int dtype,
                                            void *stream) {
-    if (!x || !B || !beta || !y) return set_error(WALSH_EINVAL, "walsh_octonion_linear_fwd: null pointer");
+    if (!x || !B || !y) return set_error(WALSH_EINVAL, "walsh_octonion_linear_fwd: null pointer");
     if (M < 0 || in_o <= 0 || out_o <= 0 || ldx < 8 * in_o || ldy < 8 * out_o)
         return set_error(WALSH_EINVAL, "walsh_octonion_linear_fwd: bad shape M=%lld in_o=%lld out_o=%lld",
                          (long long)M, (long long)in_o, (long long)out_o);

@@ -39,7 +39,11 @@ class WeightCache:
 def adjacent_parts_view(parts, width: int):
     """If ``parts`` are equal-shape slices laid side by side along the last
     dim of one tensor (what ``x.split(width, -1)`` returns), return the
-    covering view without copying; otherwise None."""
+    covering view without copying; otherwise None.  Also None when autograd
+    tracks the parts: a view built from the first part's storage would not
+    carry the other parts' gradients, so the caller concatenates."""
+    if torch.is_grad_enabled() and any(p.requires_grad for p in parts):
+        return None
     p0 = parts[0]
     if p0.shape[-1] != width or p0.stride(-1) != 1:
         return None

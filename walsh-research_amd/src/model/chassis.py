@@ -228,9 +228,11 @@ class SwiGLUMLP(nn.Module):
 
     def forward(self, x):
         x = x.to(act_dtype(x))
-        if isinstance(self.gate_proj, HadamardTernaryLinearTuple):
-            # fused gate/up/silu*mul; the hidden activation stays in a
-            # group-padded layout (stride roundup(hid_o, 4)) read in place by down_proj
+        if isinstance(self.gate_proj, HadamardTernaryLinearTuple) and not (
+                torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))):
+            # fused gate/up/silu*mul (inference; under autograd the three
+            # differentiable linears below run); the hidden activation stays in
+            # a group-padded layout (stride roundup(hid_o, 4)) read in place by down_proj
             g, u, d = self.gate_proj.inner, self.up_proj.inner, self.down_proj.inner
             hid_o = g.out_o
             h = kernels.hadamard_swiglu(x, g.in_o, hid_o, (g.ternary_state()[2], g.alpha, g.beta),

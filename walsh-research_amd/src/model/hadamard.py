@@ -260,7 +260,11 @@ class HadamardHeadMixerFused(nn.Module):
         self._wcache = WeightCache()
 
     def uses_kernel(self, x: torch.Tensor) -> bool:
+        """The mixer kernel serves inference; when autograd tracks the call
+        the torch products (differentiable) run instead."""
         dt = x.dtype if x.dtype in (torch.float32, torch.bfloat16) else torch.float32
+        if torch.is_grad_enabled() and (x.requires_grad or self.W.requires_grad or self.beta.requires_grad):
+            return False
         return x.is_cuda and kernels.head_mixer_supported(self.head_dim, dt)
 
     def _kweight(self, dt: torch.dtype) -> torch.Tensor:

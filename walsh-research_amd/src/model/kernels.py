@@ -366,7 +366,7 @@ def octonion_prepare(packed: torch.Tensor, in_o: int, out_o: int, dtype: torch.d
 
 def octonion_linear(x: torch.Tensor, in_o: int, out_o: int, B: torch.Tensor, beta: torch.Tensor) -> torch.Tensor:
     """Cayley-Dickson ternary linear on full rows x [..., 8*in_o] -> [..., 8*out_o]
-    (physics.py:66-82); B from octonion_prepare in x.dtype."""
+    (physics.py:66-82); B from octonion_prepare in x.dtype; beta None = ones."""
     _hip.require_device(x, "input")
     assert B.dtype == x.dtype, "prepared weight dtype must match the activation dtype"
     K = 8 * in_o
@@ -379,15 +379,66 @@ def octonion_linear(x: torch.Tensor, in_o: int, out_o: int, B: torch.Tensor, bet
     if ldx % vec or xv.data_ptr() % 16:
         xv = xv.reshape(rows, -1)[:, :K].contiguous()
         ldx = K
-    beta = beta.detach().float().contiguous()
+    beta_p = 0 if beta is None else beta.detach().float().contiguous().data_ptr()
     esz = x.element_size()
     nbytes = rows * 8 * (in_o + out_o) * esz + 8 * out_o * ((in_o + 3) // 4) + 4 * out_o
     flops = 2 * rows * (8 * in_o) * (8 * out_o)
-    _hip.call("walsh_octonion_linear_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, B.data_ptr(), beta.data_ptr(),
+    _hip.call("walsh_octonion_linear_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, B.data_ptr(), beta_p,
               y.data_ptr(), 8 * out_o, _hip.dtype_code(x.dtype), _hip.stream(x.device),
               kernel="octonion_gemm_kernel<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"),
               nbytes=nbytes, flops=flops)
     return y
+
+
+def octonion_prepare_t(packed: torch.Tensor, in_o: int, out_o: int, beta: torch.Tensor,
+                       dtype: torch.dtype) -> torch.Tensor:
+    """Transposed block matrix with beta folded in, [8*in_o, roundup(8*out_o, 32)]:
+    the weights of the input-gradient GEMM."""
+    _hip.require_device(packed, "packed weight")
+    assert tuple(packed.shape) == (8, out_o, (in_o + 3) // 4), f"packed shape {tuple(packed.shape)}"
+    Np = (8 * out_o + 31) // 32 * 32
+    Bt = torch.empty(8 * in_o * Np, device=packed.device, dtype=dtype)
+    beta = beta.detach().float().contiguous()
+    _hip.call("walsh_octonion_prepare_t", packed.contiguous().data_ptr(), in_o, out_o, beta.data_ptr(),
+              Bt.data_ptr(), _hip.dtype_code(dtype), _hip.stream(packed.device))
+    return Bt
+
+
+def octonion_linear_bwd(x: torch.Tensor, gy: torch.Tensor, in_o: int, out_o: int, packed: torch.Tensor,
+                        beta: torch.Tensor, latent: torch.Tensor = None, need=(True, True, True)):
+    """Backward of octonion_linear (CayleyDicksonFunction.backward,
+    cayley_dickson_cuda.py:500-567, with the STE of physics.py:48-50).
+
+    Returns (gx, dweight, dbeta); entries not requested in ``need`` are None.
+    gx = (gy .* beta) B on the HIP GEMM (transposed block matrix); the
+    parameter gradients fold C = gy^T x ([8*out_o, 8*in_o], one library GEMM
+    with float32 output, K = tokens) in walsh_octonion_bwd_fold."""
+    _hip.require_device(x, "input")
+    dt = x.dtype
+    assert gy.dtype == dt, f"gradient dtype {gy.dtype} != input dtype {dt}"
+    xr = x.reshape(-1, 8 * in_o)
+    gr = gy.reshape(-1, 8 * out_o)
+    want_x, want_w, want_b = need
+    gx = dw = db = None
+    if want_x:
+        Bt = octonion_prepare_t(packed, in_o, out_o, beta, dt)
+        gx = octonion_linear(gr, out_o, in_o, Bt, None).view(x.shape)
+    if want_w or want_b:
+        if gr.shape[0] == 0:
+            C = torch.zeros(8 * out_o, 8 * in_o, device=x.device, dtype=torch.float32)
+        elif dt == torch.float32:
+            C = torch.mm(gr.t(), xr)
+        else:
+            C = torch.mm(gr.t(), xr, out_dtype=torch.float32)
+        C = C.contiguous()
+        dw = torch.empty(8, out_o, in_o, device=x.device, dtype=torch.float32) if want_w else None
+        db = torch.empty(out_o, device=x.device, dtype=torch.float32) if want_b else None
+        lat = latent.detach().float().contiguous() if (latent is not None and want_w) else None
+        beta = beta.detach().float().contiguous()
+        ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+        _hip.call("walsh_octonion_bwd_fold", C.data_ptr(), 8 * in_o, 1, 0, packed.contiguous().data_ptr(), in_o,
+                  out_o, beta.data_ptr(), ptr(lat), ptr(dw), ptr(db), _hip.stream(x.device))
+    return gx, dw, db
 
 
 # ------------------------------------------------------------------ mHC
@@ -403,6 +454,20 @@ def sinkhorn(h: torch.Tensor, n_iter: int = 20, eps: float = 1e-8) -> torch.Tens
     _hip.call("walsh_sinkhorn_fwd", hf.data_ptr(), batch, n, int(n_iter), float(eps), out.data_ptr(),
               _hip.stream(h.device))
     return out
+
+
+def sinkhorn_bwd(h: torch.Tensor, g: torch.Tensor, n_iter: int = 20, eps: float = 1e-8) -> torch.Tensor:
+    """Gradient of ``sinkhorn`` wrt h for the output gradient g (float32, h's shape)."""
+    _hip.require_device(h, "H")
+    n = h.shape[-1]
+    hf = h.detach().float().contiguous()
+    gf = g.float().contiguous()
+    assert gf.shape == hf.shape, "gradient shape"
+    dh = torch.empty_like(hf)
+    batch = hf.numel() // (n * n)
+    _hip.call("walsh_sinkhorn_bwd", hf.data_ptr(), gf.data_ptr(), batch, n, int(n_iter), float(eps), dh.data_ptr(),
+              _hip.stream(h.device))
+    return dh
 
 
 def mhc_pre(x: torch.Tensor, phi_cat: torch.Tensor, coef: torch.Tensor, bias_cat: torch.Tensor, rms_eps: float,

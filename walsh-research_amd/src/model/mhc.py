@@ -17,9 +17,32 @@ from ._common import WeightCache, act_dtype
 _MAX_STREAMS = 4
 
 
+class SinkhornFunction(torch.autograd.Function):
+    """Sinkhorn projection with its backward on the GPU (walsh_sinkhorn_fwd /
+    walsh_sinkhorn_bwd); the reference differentiates its torch loop
+    (mhc.py:214-229) with autograd."""
+
+    @staticmethod
+    def forward(ctx, H, n_iter, eps):
+        ctx.save_for_backward(H)
+        ctx.n_iter, ctx.eps = n_iter, eps
+        return kernels.sinkhorn(H, n_iter=n_iter, eps=eps)
+
+    @staticmethod
+    def backward(ctx, g):
+        (H,) = ctx.saved_tensors
+        return kernels.sinkhorn_bwd(H, g, n_iter=ctx.n_iter, eps=ctx.eps).to(H.dtype), None, None
+
+
+def _sinkhorn(H, n_iter, eps):
+    if torch.is_grad_enabled() and H.requires_grad:
+        return SinkhornFunction.apply(H, n_iter, eps)
+    return kernels.sinkhorn(H, n_iter=n_iter, eps=eps)
+
+
 def sinkhorn_knopp_fused(H_tilde, n_iter=20):
     """Doubly-stochastic projection of [..., n, n] (mhc.py:152-195), float32."""
-    return kernels.sinkhorn(H_tilde, n_iter=n_iter, eps=1e-8)
+    return _sinkhorn(H_tilde, n_iter, 1e-8)
 
 
 class SinkhornKnopp(nn.Module):
@@ -31,7 +54,7 @@ class SinkhornKnopp(nn.Module):
         self.eps = eps
 
     def forward(self, H):
-        return kernels.sinkhorn(H, n_iter=self.n_iter, eps=self.eps)
+        return _sinkhorn(H, self.n_iter, self.eps)
 
 
 def _rms_eps(dtype: torch.dtype) -> float:
@@ -82,6 +105,15 @@ class ResidualStreamMapping(nn.Module):
         if n > _MAX_STREAMS:
             raise NotImplementedError(f"n_streams={n} > {_MAX_STREAMS} is not supported by this build")
         B, T, _ = x.shape
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            # differentiable form for training (the fused kernel has no backward)
+            xn = F.rms_norm(x, (x.size(-1),))
+            dyn = F.linear(xn, self.phi.weight.to(xn.dtype))
+            if self.mapping_type == 'res':
+                h = (self.alpha * dyn.view(B, T, n, n) + self.bias).float()
+                return _sinkhorn(h, self.sinkhorn.n_iter, self.sinkhorn.eps)
+            s = torch.sigmoid(self.alpha * dyn + self.bias).unsqueeze(2)
+            return s if self.mapping_type == 'pre' else 2.0 * s
         dt = act_dtype(x)
         slot = {'pre': 0, 'post': 1, 'res': 2}[self.mapping_type]
 
@@ -153,8 +185,36 @@ class mHCResidualStream(nn.Module):
             li = norm(li).to(dt)
         return li, hp, hq, hr
 
+    def _tracked(self, x) -> bool:
+        return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+
+    def _forward_autograd(self, x, norm, layer_fn):
+        """The stream update as differentiable operations, for training
+        (mhc.py:345-381 with the mappings of :283-318): one projection for
+        the three mappings' phi rows, sigmoid / 2*sigmoid, the Sinkhorn
+        projection as SinkhornFunction (its backward on the GPU), then
+        H_pre @ x, the layer, H_res @ x + H_post^T out.  The fused inference
+        kernels (walsh_mhc_pre_fwd / walsh_mhc_post_fwd) have no backward."""
+        B, T, n, C = x.shape
+        xn = F.rms_norm(x.reshape(B, T, n * C), (n * C,))
+        phi = torch.cat([self.H_pre.phi.weight, self.H_post.phi.weight, self.H_res.phi.weight], 0)
+        d_pre, d_post, d_res = F.linear(xn, phi.to(xn.dtype)).split([n, n, n * n], dim=-1)
+        h_pre = torch.sigmoid(self.H_pre.alpha * d_pre + self.H_pre.bias).unsqueeze(2)
+        h_post = 2.0 * torch.sigmoid(self.H_post.alpha * d_post + self.H_post.bias).unsqueeze(2)
+        sk = self.H_res.sinkhorn
+        h_res = _sinkhorn((self.H_res.alpha * d_res.reshape(B, T, n, n) + self.H_res.bias).float(), sk.n_iter,
+                          sk.eps)
+        # the mixing products in the stream dtype (what autocast gives the
+        # reference's matmuls under bf16)
+        layer_in = torch.matmul(h_pre.to(x.dtype), x).squeeze(2)
+        out = layer_fn(layer_in if norm is None else norm(layer_in))
+        return torch.matmul(h_res.to(x.dtype), x) + torch.matmul(h_post.transpose(-2, -1).to(out.dtype),
+                                                                 out.unsqueeze(2))
+
     def forward(self, x, layer_fn):
         """x [B, T, n, C]; layer_fn maps [B, T, C] -> [B, T, C]."""
+        if self._tracked(x):
+            return self._forward_autograd(x, None, layer_fn)
         dt = act_dtype(x)
         x = x.to(dt)
         layer_in, _, h_post, h_res = self._pre(x, dt)
@@ -164,6 +224,8 @@ class mHCResidualStream(nn.Module):
     def forward_normed(self, x, norm, layer_fn):
         """forward(x, lambda v: layer_fn(norm(v))) with the RMSNorm ``norm``
         (chassis.RMSNorm) fused into the mapping kernel."""
+        if self._tracked(x):
+            return self._forward_autograd(x, norm, layer_fn)
         dt = act_dtype(x)
         x = x.to(dt)
         layer_in, _, h_post, h_res = self._pre(x, dt, norm=norm)

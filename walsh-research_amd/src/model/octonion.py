@@ -47,6 +47,31 @@ def cayley_dickson_fused(x_parts, weight: torch.Tensor) -> tuple:
     return tuple(y.split(N, dim=-1))
 
 
+class OctonionLinearFunction(torch.autograd.Function):
+    """Autograd of the octonion layer on the HIP kernels (the role of
+    CayleyDicksonFunction, cayley_dickson_cuda.py:428-567): the exact
+    transpose of the forward's signed-permutation block matrix for dx, and
+    dW / dbeta folded from gy^T x; the weight gradient passes the STE clamp
+    of physics.quantize_ternary (physics.py:48-50)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, beta, layer):
+        y = kernels.octonion_linear(x, layer.in_o, layer.out_o, layer.block_matrix(x.dtype), beta)
+        ctx.layer = layer
+        ctx.save_for_backward(x, weight, beta)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, weight, beta = ctx.saved_tensors
+        layer = ctx.layer
+        nx, nw, nb, _ = ctx.needs_input_grad
+        packed = layer.ternary_state()[1]
+        gx, dw, db = kernels.octonion_linear_bwd(x, gy.to(x.dtype).contiguous(), layer.in_o, layer.out_o, packed,
+                                                 beta, latent=weight, need=(nx, nw, nb))
+        return gx, dw, db, None
+
+
 class OctonionFusedLinear(nn.Module):
     """Octonion ternary linear (cayley_dickson_cuda.py:622-668): 8 parts
     [..., in_o] in, 8 parts [..., out_o] out, y_i scaled by beta [out_o].
@@ -82,6 +107,8 @@ class OctonionFusedLinear(nn.Module):
         """Rows x [..., 8*in_o] (parts side by side) -> [..., 8*out_o] in the activation dtype."""
         dt = act_dtype(x)
         x = x if x.dtype == dt else x.to(dt)
+        if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad or self.beta.requires_grad):
+            return OctonionLinearFunction.apply(x, self.weight, self.beta, self)
         return kernels.octonion_linear(x, self.in_o, self.out_o, self.block_matrix(dt), self.beta)
 
     def forward(self, x_parts):
