@@ -85,6 +85,15 @@ int walsh_ternary_gamma(const float *w, int64_t n, float *gamma, void *stream);
 int walsh_ternary_quantize(const float *w, int64_t rows, int64_t K, const float *gamma,
                            int8_t *codes, uint8_t *packed, float *scaled, void *stream);
 
+/* walsh_ternary_ste_bwd: backward of the two straight-through estimators,
+ *   elementwise over n float32 gradients (out may alias grad):
+ *   mode 0, TernaryAbsmeanSTE of src/model/physics.py:13-50 as used through
+ *     quantize_ternary (w_clamped + (w_quant - w_clamped).detach()):
+ *     out = grad where -1.5 <= w <= 1.5, else 0 (w: the latent weights);
+ *   mode 1, TernaryAbsmeanSTE.backward of src/model/moe.py:289-294:
+ *     out = clamp(grad, -2, 2) (w unused, may be NULL). */
+int walsh_ternary_ste_bwd(const float *grad, const float *w, int64_t n, int mode, float *out, void *stream);
+
 /* walsh_ternary_unpack: inverse of the packed layout -> int8 codes [rows, K]
  *   (unpack_ternary_weights, src/model/fht_cuda.py:96-117). */
 int walsh_ternary_unpack(const uint8_t *packed, int64_t rows, int64_t K, int8_t *codes,

@@ -35,6 +35,20 @@ def sylvester(n=32):
     return H / math.sqrt(n)
 
 
+class _MoESTE(torch.autograd.Function):
+    """moe.TernaryAbsmeanSTE (moe.py:276-294): value clamp(round(w/g), -1, 1)*g
+    with g = mean|w| + 1e-8; gradient clamp(grad, -2, 2)."""
+
+    @staticmethod
+    def forward(ctx, w):
+        g = w.abs().mean() + 1e-8
+        return torch.clamp(torch.round(w / g), -1, 1) * g
+
+    @staticmethod
+    def backward(ctx, grad):
+        return torch.clamp(grad, -2.0, 2.0)
+
+
 class Oracle:
     """``grad=True`` turns the oracle into the gradient reference: every
     floating entry of the state dict becomes a float64 leaf (tensors that
@@ -134,6 +148,8 @@ class Oracle:
 
         def q(key):
             w = self.sd[key]
+            if self.grad:
+                return _MoESTE.apply(w)
             g = w.abs().mean() + 1e-8
             return torch.clamp(torch.round(w / g), -1, 1) * g
 

@@ -289,3 +289,55 @@ def test_mhcwalsh_backward_matches_oracle(C, n_layer, vocab, T):
           flush=True)
     assert total <= 1e-5, total
     assert not bad, bad
+
+
+# ---------------------------------------------------------------- MoE
+
+def test_ternary_ste_bwd_modes(K):
+    g = torch.tensor([-3.0, -2.0, -0.5, 0.0, 1.9, 2.5, float("nan")], device="cuda")
+    w = torch.tensor([-1.6, -1.5, 0.3, 1.5, 1.51, -3.0, 0.0], device="cuda")
+    m1 = K.ternary_ste_bwd(g, mode=1).cpu()
+    assert torch.equal(m1[:6], torch.tensor([-2.0, -2.0, -0.5, 0.0, 1.9, 2.0])) and torch.isnan(m1[6])
+    m0 = K.ternary_ste_bwd(g, w, mode=0).cpu()
+    assert torch.equal(m0[:6], torch.tensor([0.0, -2.0, -0.5, 0.0, 0.0, 0.0])) and torch.isnan(m0[6])
+
+
+@pytest.mark.parametrize("C,k", [(256, 4), (512, 6)])
+def test_moe_backward_matches_oracle(C, k):
+    """HadamardMoE training backward (routing, balance loss, experts with the
+    MoE STE) against float64 autograd of the oracle's MoE (moe.py:418-447,
+    :337-380, :544-560) on the same parameters."""
+    from oracle.model import Oracle
+    from src.model import WalshConfig
+    from src.model.moe import HadamardMoE
+    torch.manual_seed(4)
+    cfg = WalshConfig(n_embd=C, n_head=32, n_layer=1, vocab_size=64, block_size=64)
+    m = HadamardMoE(cfg, max_experts=k).cuda().train()
+    with torch.no_grad():
+        for lin in (m.router.gate[0], m.router.gate[2]):
+            lin.weight.normal_(0, 0.2)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 24, C, generator=g).cuda().requires_grad_(True)
+    gy = torch.randn(2, 24, C, generator=g).cuda()
+    y = m(x)
+    loss = (y * gy).sum() + 0.3 * m.get_aux_loss()
+    loss.backward()
+    torch.cuda.synchronize()
+    orc = Oracle({"m." + n: t for n, t in m.state_dict().items()}, C, 32, 1, moe_max_experts=k, grad=True)
+    x64 = x.detach().double().cpu().requires_grad_(True)
+    out, info = orc.moe(x64, "m")
+    E = C // 32
+    aux = (info["mask"].reshape(-1, E).mean(0) * info["probs"].reshape(-1, E).mean(0)).sum() * E
+    ref_loss = (out * gy.double().cpu()).sum() + 0.3 * aux
+    ref_loss.backward()
+    assert np.array_equal(m._last_expert_mask.cpu().numpy(), info["mask"].detach().numpy()), "routing differs"
+    got = {"x": x.grad}
+    ref = {"x": x64.grad}
+    for n, p in m.named_parameters():
+        got[n], ref[n] = p.grad, orc.sd["m." + n].grad
+    G = max(float(v.norm()) for v in ref.values())
+    for n in got:
+        a, b = got[n].double().cpu().numpy().ravel(), ref[n].numpy().ravel()
+        err, nb = float(np.linalg.norm(a - b)), float(np.linalg.norm(b))
+        print(f"moe C={C} k={k} {n}: rel_norm {err / max(nb, 1e-300):.2e} (|ref| {nb:.3e})", flush=True)
+        assert err <= 1e-5 * nb + 1e-6 * G, (n, err, nb)

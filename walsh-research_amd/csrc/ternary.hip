@@ -93,9 +93,43 @@ static int grid_for(int64_t work, int block) {
     return (int)(g < 1 ? 1 : g);
 }
 
+// Straight-through estimators' backward, elementwise over n weights:
+//   mode 0 (physics.quantize_ternary, physics.py:43-50): the value
+//     w_clamped + (w_quant - w_clamped).detach() passes gradient only through
+//     w.clamp(-1.5, 1.5): g_latent = g * [-1.5 <= w <= 1.5];
+//   mode 1 (moe.TernaryAbsmeanSTE.backward, moe.py:289-294):
+//     g_latent = clamp(g, -2, 2).
+__global__ void ste_bwd_kernel(const float *__restrict__ g, const float *__restrict__ w, int64_t n, int mode,
+                               float *__restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = g[i];
+        float r;
+        if (mode == 0) {
+            const float x = w[i];
+            r = (x >= -1.5f && x <= 1.5f) ? v : 0.f;
+        } else {
+            r = fminf(fmaxf(v, -2.f), 2.f);
+            if (v != v) r = v;  // NaN passes through, as torch.clamp does
+        }
+        out[i] = r;
+    }
+}
+
 }  // namespace walsh
 
 using namespace walsh;
+
+WALSH_EXPORT int walsh_ternary_ste_bwd(const float *grad, const float *w, int64_t n, int mode, float *out,
+                                       void *stream) {
+    if (n < 0 || (mode != 0 && mode != 1)) return set_error(WALSH_EINVAL, "walsh_ternary_ste_bwd: n=%lld mode=%d",
+                                                            (long long)n, mode);
+    if (n == 0) return WALSH_OK;
+    if (!grad || !out || (mode == 0 && !w)) return set_error(WALSH_EINVAL, "walsh_ternary_ste_bwd: null pointer");
+    const int block = 256;
+    const int grid = grid_for(n, block);
+    launch(ste_bwd_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, grad, w, n, mode, out);
+    return check_hip(hipGetLastError(), "walsh_ternary_ste_bwd launch");
+}
 
 WALSH_EXPORT int walsh_ternary_gamma(const float *w, int64_t n, float *gamma, void *stream) {
     if (!w || !gamma) return set_error(WALSH_EINVAL, "walsh_ternary_gamma: null pointer");

@@ -13,6 +13,15 @@ def act_dtype(x: torch.Tensor) -> torch.dtype:
     return x.dtype
 
 
+def tracked_dtype(dt: torch.dtype) -> torch.dtype:
+    """Compute dtype for batched products that autograd tracks: float32 in
+    place of bfloat16.  The backward of a bf16 batched product multiplies by
+    a transposed view of its right operand, a form of torch.bmm that has
+    faulted the GPU here, so training-path batched products run in float32
+    (their results are cast back to the activation dtype)."""
+    return torch.float32 if dt == torch.bfloat16 else dt
+
+
 class WeightCache:
     """Caches a device-side derivative of a parameter (its ternary codes,
     packed layouts, concatenations ...) until the parameter changes.

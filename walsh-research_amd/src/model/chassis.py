@@ -20,7 +20,7 @@ from .hadamard import HadamardLinear, HadamardTernaryLinear, HadamardTernaryLine
 from .hadamard import HadamardHeadMixer, HadamardHeadMixerFused
 from .octonion import OctonionHeadMixerFused, OctonionTernaryLinear
 from . import kernels
-from ._common import act_dtype
+from ._common import act_dtype, tracked_dtype
 
 _HADAMARD_AVAILABLE = True
 _HADAMARD_HEAD_MIXER_AVAILABLE = True
@@ -187,16 +187,24 @@ class CausalSelfAttention(nn.Module):
         q = q.transpose(1, 2)
         k = k.transpose(1, 2).to(q.dtype)
         v = v.transpose(1, 2).to(q.dtype)
+        att_dt = q.dtype
+        tracked = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+        if tracked:
+            # training: attention (and its backward) in float32, see tracked_dtype
+            q, k, v = (t.to(tracked_dtype(att_dt)) for t in (q, k, v))
         drop = self.dropout if self.training else 0
-        if kv_cache is not None and kv_cache.cached_len > 0 and T == 1:
-            # one new position attends to every cached one: no mask needed
-            y = F.scaled_dot_product_attention(q, k, v, dropout_p=drop)
-        elif kv_cache is not None and kv_cache.cached_len > 0:
-            total = k.size(2)
-            mask = torch.ones(T, total, dtype=torch.bool, device=q.device).tril(diagonal=total - T)
-            y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=drop)
-        else:
-            y = F.scaled_dot_product_attention(q, k, v, is_causal=True, dropout_p=drop)
+        with torch.autocast("cuda", dtype=torch.get_autocast_dtype("cuda"),
+                            enabled=torch.is_autocast_enabled("cuda") and not tracked):
+            if kv_cache is not None and kv_cache.cached_len > 0 and T == 1:
+                # one new position attends to every cached one: no mask needed
+                y = F.scaled_dot_product_attention(q, k, v, dropout_p=drop)
+            elif kv_cache is not None and kv_cache.cached_len > 0:
+                total = k.size(2)
+                mask = torch.ones(T, total, dtype=torch.bool, device=q.device).tril(diagonal=total - T)
+                y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=drop)
+            else:
+                y = F.scaled_dot_product_attention(q, k, v, is_causal=True, dropout_p=drop)
+        y = y.to(att_dt)
         if self.head_mixer is not None:
             n_groups = self.n_head // self.mixer_dim
             yg = y.view(B, n_groups, self.mixer_dim, T, self.head_dim)

@@ -12,7 +12,7 @@ import torch
 import torch.nn as nn
 
 from . import kernels
-from ._common import WeightCache, act_dtype, adjacent_parts_view
+from ._common import WeightCache, act_dtype, adjacent_parts_view, tracked_dtype
 
 ALGEBRA_DIM = 32
 
@@ -290,12 +290,17 @@ class HadamardHeadMixerFused(nn.Module):
         if self.uses_kernel(x):
             # a [B, 32, T, D] view of the token-major result
             return self.forward_rows(x).view(B, T, Hh, D).transpose(1, 2)
-        dt = x.dtype
-        H = self.H.to(dt).contiguous()          # symmetric: H^T x == H x
-        xf = torch.matmul(H, x.reshape(B, Hh, T * D).contiguous()).view(B, Hh, T, D)
-        y = torch.matmul(xf, self.W.to(dt).contiguous())
-        yf = torch.matmul(H, y.reshape(B, Hh, T * D).contiguous()).view(B, Hh, T, D)
-        return yf * self.beta.to(dt)
+        out_dt = x.dtype
+        tracked = torch.is_grad_enabled()
+        dt = tracked_dtype(out_dt) if tracked else out_dt
+        x = x.to(dt)
+        dev = x.device.type
+        with torch.autocast(dev, dtype=torch.get_autocast_dtype(dev), enabled=torch.is_autocast_enabled(dev) and not tracked):
+            H = self.H.to(dt).contiguous()          # symmetric: H^T x == H x
+            xf = torch.matmul(H, x.reshape(B, Hh, T * D).contiguous()).view(B, Hh, T, D)
+            y = torch.matmul(xf, self.W.to(dt).contiguous())
+            yf = torch.matmul(H, y.reshape(B, Hh, T * D).contiguous()).view(B, Hh, T, D)
+        return (yf * self.beta.to(dt)).to(out_dt)
 
 
 HadamardHeadMixer = HadamardHeadMixerFused

@@ -79,6 +79,23 @@ def ternary_quantize(w: torch.Tensor, gamma: torch.Tensor = None, codes=False, p
     return out
 
 
+def ternary_ste_bwd(grad: torch.Tensor, w: torch.Tensor = None, mode: int = 1) -> torch.Tensor:
+    """Straight-through gradient of the ternary quantisers: mode 1 clamps to
+    [-2, 2] (TernaryAbsmeanSTE.backward, physics.py:35-39, moe.py:289-294);
+    mode 0 passes the gradient where -1.5 <= w <= 1.5 (quantize_ternary's
+    clamp path, physics.py:48-50).  float32, grad's shape."""
+    _hip.require_device(grad, "gradient")
+    g = grad.float().contiguous()
+    out = torch.empty_like(g)
+    wp = 0
+    if mode == 0:
+        assert w is not None and w.numel() == g.numel(), "mode 0 needs the latent weights"
+        wf = w.detach().float().contiguous()
+        wp = wf.data_ptr()
+    _hip.call("walsh_ternary_ste_bwd", g.data_ptr(), wp, g.numel(), int(mode), out.data_ptr(), _hip.stream(g.device))
+    return out
+
+
 def ternary_unpack(packed: torch.Tensor, K: int) -> torch.Tensor:
     """int8 codes [.., K] from the 2-bit layout (fht_cuda.py:96-117)."""
     _hip.require_device(packed, "packed")

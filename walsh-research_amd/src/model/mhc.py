@@ -204,12 +204,15 @@ class mHCResidualStream(nn.Module):
         sk = self.H_res.sinkhorn
         h_res = _sinkhorn((self.H_res.alpha * d_res.reshape(B, T, n, n) + self.H_res.bias).float(), sk.n_iter,
                           sk.eps)
-        # the mixing products in the stream dtype (what autocast gives the
-        # reference's matmuls under bf16)
-        layer_in = torch.matmul(h_pre.to(x.dtype), x).squeeze(2)
+        # the n x n mixing as broadcast products summed in float32, rounded
+        # to the stream dtype (what the reference's autocast matmuls give),
+        # without batched matmuls (see tracked_dtype)
+        xw = x.float()
+        layer_in = (h_pre.transpose(-2, -1).float() * xw).sum(2).to(x.dtype)
         out = layer_fn(layer_in if norm is None else norm(layer_in))
-        return torch.matmul(h_res.to(x.dtype), x) + torch.matmul(h_post.transpose(-2, -1).to(out.dtype),
-                                                                 out.unsqueeze(2))
+        res = (h_res.float().unsqueeze(-1) * xw.unsqueeze(2)).sum(3)
+        post = h_post.transpose(-2, -1).float() * out.float().unsqueeze(2)
+        return res.to(x.dtype) + post.to(x.dtype)
 
     def forward(self, x, layer_fn):
         """x [B, T, n, C]; layer_fn maps [B, T, C] -> [B, T, C]."""

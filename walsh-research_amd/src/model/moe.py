@@ -30,7 +30,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import kernels
-from ._common import WeightCache, act_dtype
+from ._common import WeightCache, act_dtype, tracked_dtype
 
 # A fused router keeps W1 in each wavefront's working set; beyond this width
 # the two Linears run as library GEMMs (plain dense products) instead.
@@ -50,7 +50,7 @@ class TernaryAbsmeanSTE(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        return torch.clamp(grad_output, -2.0, 2.0)
+        return kernels.ternary_ste_bwd(grad_output, mode=1).to(grad_output.dtype)
 
 
 def quantize_ternary(w: torch.Tensor) -> torch.Tensor:
@@ -128,12 +128,33 @@ class FastMoEExperts(nn.Module):
         lists = kernels.moe_scatter(route)
         kernels.moe_experts(x2d, y2d, route, lists, frags, gammas, self.hidden)
 
+    def forward_autograd(self, x: torch.Tensor, expert_weights: torch.Tensor) -> torch.Tensor:
+        """The experts as differentiable products for training (moe.py:337-380):
+        quantize_ternary (HIP quantiser, straight-through gradient clipped to
+        [-2, 2] on the GPU), then per-expert matrix products in float32 (see
+        tracked_dtype), times the routing weights; float32 result."""
+        self._check()
+        B, T, E, D = x.shape
+        gw, uw, dw = (quantize_ternary(w) for w in (self.gate_weights, self.up_weights, self.down_weights))
+        dt = tracked_dtype(act_dtype(x))
+        dev = x.device.type
+        with torch.autocast(dev, dtype=torch.get_autocast_dtype(dev), enabled=False):
+            xe = x.to(dt).reshape(B * T, E, D).transpose(0, 1).contiguous()            # [E, M, D]
+            g = torch.matmul(xe, gw.to(dt).transpose(1, 2).contiguous())               # [E, M, H]
+            u = torch.matmul(xe, uw.to(dt).transpose(1, 2).contiguous())
+            o = torch.matmul(F.silu(g) * u, dw.to(dt).transpose(1, 2).contiguous())     # [E, M, D]
+            out = o.transpose(0, 1).reshape(B, T, E, D) * expert_weights.to(dt).unsqueeze(-1)
+        return out
+
     def forward(self, x: torch.Tensor, expert_weights: torch.Tensor) -> torch.Tensor:
         """x [B, T, E, dim], expert_weights [B, T, E] -> [B, T, E, dim]: every
         expert on its block, times its weight (moe.py:337-380)."""
         B, T, E, D = x.shape
         assert E == self.n_experts and D == self.dim, f"expert input shape {tuple(x.shape)}"
         assert tuple(expert_weights.shape) == (B, T, E), "expert_weights shape"
+        if torch.is_grad_enabled() and (x.requires_grad or expert_weights.requires_grad
+                                        or any(p.requires_grad for p in self.parameters())):
+            return self.forward_autograd(x, expert_weights)
         dt = act_dtype(x)
         M = B * T
         x2d = x.to(dt).reshape(M, E * D)
@@ -196,10 +217,23 @@ class HadamardRouter(nn.Module):
             _zero_unselected(y2d, r)
         return r
 
+    def route_autograd(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """moe.py:418-447 as differentiable operations (training): the router
+        MLP, softmax, top-k mask and the renormalised weights; the gradient
+        reaches the router through the probabilities of the selected experts."""
+        logits = self.gate(x)
+        probs = F.softmax(logits, dim=-1)
+        _, idx = probs.topk(self.top_k, dim=-1)
+        mask = torch.zeros_like(probs).scatter_(-1, idx, 1.0)
+        mp = probs * mask
+        return mp / mp.sum(dim=-1, keepdim=True).clamp(min=1e-8), mask, probs
+
     def forward(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """x [B, T, C] -> (expert_weights, expert_mask, router_probs), each
         [B, T, E] float32."""
         B, T, C = x.shape
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return self.route_autograd(x)
         dt = act_dtype(x)
         r = self.route(x.to(dt).reshape(B * T, C), dense=True)
         E = self.n_experts
@@ -275,6 +309,8 @@ class HadamardMoE(nn.Module):
         ``out_dtype`` overrides it for callers that round the result anyway."""
         B, T, C = x.shape
         assert C == self.n_embd, f"expected n_embd {self.n_embd}, got {C}"
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return self._forward_autograd(x, out_dtype)
         dt = act_dtype(x)
         M = B * T
         x2d = x.to(dt).reshape(M, C)
@@ -300,6 +336,26 @@ class HadamardMoE(nn.Module):
         return y.view(B, T, C)
 
     use_fused = True   # single-launch kernel where supported (tests switch it off to compare paths)
+
+    def _forward_autograd(self, x: torch.Tensor, out_dtype: Optional[torch.dtype]) -> torch.Tensor:
+        """Training form (moe.py:512-542): differentiable routing, the
+        balance loss kept as a differentiable tensor, and every expert on its
+        block (FastMoEExperts.forward_autograd)."""
+        B, T, C = x.shape
+        E = self.n_experts
+        dt = act_dtype(x)
+        xr = x.to(dt)
+        weights, mask, probs = self.router.route_autograd(xr)
+        self._route, self._route_shape = None, (B, T)
+        self._aux_value = (mask.reshape(-1, E).mean(0) * probs.reshape(-1, E).mean(0)).sum() * E
+        self._mask_value = mask.detach()
+        if self.training:
+            with torch.no_grad():
+                self._expert_counts += mask.reshape(-1, E).sum(0)
+                self._total_tokens += B * T
+        out = self.experts.forward_autograd(xr.reshape(B, T, E, self.block_dim), weights).reshape(B, T, C)
+        ydt = _output_dtype(x) if out_dtype is None else out_dtype
+        return out.to(torch.float32 if dt == torch.float32 else ydt)
 
     def _ffn_state(self):
         ex, w1, w2 = self.experts, self.router.gate[0].weight, self.router.gate[2].weight
