@@ -341,3 +341,33 @@ def test_moe_backward_matches_oracle(C, k):
         err, nb = float(np.linalg.norm(a - b)), float(np.linalg.norm(b))
         print(f"moe C={C} k={k} {n}: rel_norm {err / max(nb, 1e-300):.2e} (|ref| {nb:.3e})", flush=True)
         assert err <= 1e-5 * nb + 1e-6 * G, (n, err, nb)
+
+
+def test_mhcwalsh_backward_bf16_autocast():
+    """A bf16-autocast training backward runs and lands near the float64
+    gradients: bf16 activations round at every layer, so the bar is the
+    all-gradient relative error <= 3e-2 (the float32 run meets 1e-5)."""
+    from oracle.model import Oracle
+    from src.model import WalshConfig, mHCWalsh
+    torch.manual_seed(0)
+    C, n_layer, vocab, T = 256, 2, 512, 32
+    cfg = WalshConfig(block_size=64, vocab_size=vocab, n_layer=n_layer, n_head=32, n_embd=C, algebra='hadamard',
+                      head_mixing=True)
+    model = mHCWalsh(cfg, n_streams=4).cuda().eval()
+    g = torch.Generator().manual_seed(1)
+    idx = torch.randint(0, vocab, (2, T), generator=g)
+    tgt = torch.randint(0, vocab, (2, T), generator=g)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        _, loss = model(idx.cuda(), targets=tgt.cuda())
+    loss.backward()
+    torch.cuda.synchronize()
+    orc = Oracle(model.state_dict(), C, 32, n_layer, grad=True)
+    ref_loss = orc.loss(idx, tgt)
+    ref_loss.backward()
+    got = np.concatenate([p.grad.double().cpu().numpy().ravel() for _, p in model.named_parameters()])
+    ref = np.concatenate([orc.sd[n].grad.numpy().ravel() for n, _ in model.named_parameters()])
+    rel = _grad_rel(got, ref)
+    print(f"bf16 autocast: loss gpu={loss.item():.5f} oracle={ref_loss.item():.5f}, all-gradient rel_norm {rel:.2e}",
+          flush=True)
+    assert abs(loss.item() - ref_loss.item()) <= 1e-2 * abs(ref_loss.item())
+    assert rel <= 3e-2, rel
