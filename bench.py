@@ -19,7 +19,9 @@ Other workloads (``--workload``), each printing one JSON line of its own:
             synthetic KV cache of length 4096, at batch 1, 16 and 64;
   hadamard_bwd  backward of one HadamardLinear(512, 512), bf16, x and the
             output gradient [8192, 512] (the headline model's layer shape),
-            and a token sweep up to 262144 rows (rotated).
+            and a token sweep up to 262144 rows (rotated);
+  train2    one training step of the headline model (bf16 autocast forward
+            with targets, backward, AdamW), batch x seq tokens.
 
 Prints ONE JSON line.  Besides the timed region it
   * repeats the K steps with HIP events around every hot-path launch (on the
@@ -55,7 +57,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-roofline", action="store_true", help="skip the instrumented pass (profiling runs)")
     ap.add_argument("--workload", default="mhcwalsh",
-                    choices=["mhcwalsh", "moe", "octonion", "hadamard", "prefill5", "decode5", "hadamard_bwd"])
+                    choices=["mhcwalsh", "moe", "octonion", "hadamard", "prefill5", "decode5", "hadamard_bwd",
+                             "train2"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (reference for HBM byte counters)")
     return ap.parse_args()
@@ -146,7 +149,8 @@ def main():
         return
     if args.workload != "mhcwalsh":
         line = {"moe": bench_moe, "octonion": bench_octonion, "hadamard": bench_hadamard, "prefill5": bench_prefill5,
-                "decode5": bench_decode5, "hadamard_bwd": bench_hadamard_bwd}[args.workload](torch, args)
+                "decode5": bench_decode5, "hadamard_bwd": bench_hadamard_bwd,
+                "train2": bench_train2}[args.workload](torch, args)
         print(json.dumps(line), flush=True)
         return
     _hip.lib()
@@ -461,6 +465,63 @@ def bench_hadamard_bwd(torch, args):
                   "seq_len": 1024, "parallelism": "single GPU"}, roof, cpu)
     line["sweep"] = sweep
     return line
+
+
+def bench_train2(torch, args):
+    """One training step of the headline model (n_layer 16, n_embd 512,
+    hadamard + head mixing, 4 streams) at batch x seq tokens: bf16 autocast
+    forward with targets, backward through the HIP backward kernels, and an
+    AdamW step (torch, foreach) on every parameter."""
+    from src.model import _hip
+    cfg, model, idx = build_model(torch, args.batch, args.seq)
+    model.train()
+    gen = torch.Generator().manual_seed(2)
+    tgt = torch.randint(0, cfg.vocab_size, idx.shape, generator=gen).cuda()
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True)
+    tokens = args.batch * args.seq
+
+    def step(i=0):
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            _, loss = model(idx, targets=tgt)
+        loss.backward()
+        opt.step()
+        return loss
+
+    steps = max(1, min(args.steps, 10))
+    dt = _time_steps(torch, step, steps, max(1, min(args.warmup, 2)))
+    roof = None
+    if not args.no_roofline:
+        with _hip.LaunchTimer() as lt:
+            for i in range(steps):
+                step(i)
+        summ = lt.summary()
+        roof = _roofline_of(summ, steps)
+        roof["hip_kernels"] = {k: dict(launches_per_step=v["launches"] // steps,
+                                       us_per_launch=round(v["ms"] * 1000 / v["launches"], 2),
+                                       ms_per_step=round(v["ms"] / steps, 3)) for k, v in summ.items()}
+    cpu = None
+    if not args.no_cpu:
+        from oracle.model import Oracle
+        sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+        orc = Oracle(sd, cfg.n_embd, cfg.n_head, cfg.n_layer, n_streams=4, grad=True, grad_dtype=torch.float32)
+        seq = 128
+        x, y = idx[:1, :seq].cpu(), tgt[:1, :seq].cpu()
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 20.0) or reps == 0:
+            orc.loss(x, y).backward()
+            reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(reps * seq / el, 2), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   sample=f"{reps} x (1 x {seq} tokens) forward + backward of the same 16-layer model in float32 "
+                          f"through the oracle (the reference's torch CPU graph, autograd), {el:.1f} s; no "
+                          f"optimizer step")
+    return _line("training tokens/sec of the Walsh layer stack at 1 GPU (forward + backward + AdamW)",
+                 tokens / dt, "tokens/s", steps, max(1, min(args.warmup, 2)), dt * 1e3, "bf16",
+                 "synthetic: random-init weights, tokens and targets uniform over 50257",
+                 {"workload": "mHCWalsh training step, n_layer 16, n_head 32, n_embd 512, hadamard + head mixing, "
+                              "4 mHC streams, MoE off, bf16 autocast, AdamW", "global_batch": args.batch,
+                  "seq_len": args.seq, "parallelism": "single GPU"}, roof, cpu)
 
 
 def _config5(torch, block_size):

@@ -217,6 +217,17 @@ int walsh_hadamard_linear_bwd(const void *x, int64_t ldx, const void *gy, int64_
                               const float *beta, const float *latent, void *gx, int64_t ldgx, float *dalpha,
                               float *dbeta, float *dweight, int dtype, void *workspace, int64_t workspace_bytes,
                               void *stream);
+/* walsh_hadamard_linear_ex_bwd: walsh_hadamard_linear_bwd with the group
+ *   strides of walsh_hadamard_linear_ex_fwd: x and gx rows hold group g at
+ *   g*gsx (gsx >= in_o), gy rows at g*gsy (gsy >= out_o); gx slots in
+ *   [in_o, roundup(in_o, 4)) are written as zeros (slots past that are not
+ *   written), pad slots of x and gy are not read.  The backward of the
+ *   group-padded SwiGLU hidden layout. */
+int walsh_hadamard_linear_ex_bwd(const void *x, int64_t ldx, int64_t gsx, const void *gy, int64_t ldg, int64_t gsy,
+                                 int64_t M, int64_t in_o, int64_t out_o, const uint8_t *kweight,
+                                 const uint8_t *kweight_t, const float *alpha, const float *beta, const float *latent,
+                                 void *gx, int64_t ldgx, float *dalpha, float *dbeta, float *dweight, int dtype,
+                                 void *workspace, int64_t workspace_bytes, void *stream);
 
 /* walsh_fht_fwd: fast Walsh-Hadamard transform of `rows` contiguous rows of
  *   length n (power of two <= 16384), Sylvester order, scaled by 1/sqrt(n)

@@ -51,16 +51,16 @@ class _MoESTE(torch.autograd.Function):
 
 class Oracle:
     """``grad=True`` turns the oracle into the gradient reference: every
-    floating entry of the state dict becomes a float64 leaf (tensors that
+    floating entry of the state dict becomes a ``grad_dtype`` (float64) leaf (tensors that
     share storage in the model, like the tied embedding / output weight,
     share one leaf), the Hadamard weights go through the STE of
     physics.quantize_ternary (physics.py:43-50) instead of fixed codes, and
     ``loss`` gives the cross-entropy whose backward fills ``leaf.grad``."""
 
     def __init__(self, sd, n_embd, n_head, n_layer, n_streams=4, head_mixing=True, block_size=256,
-                 use_moe=False, moe_max_experts=4, grad=False):
+                 use_moe=False, moe_max_experts=4, grad=False, grad_dtype=torch.float64):
         self.grad = grad
-        self.dt = torch.float64 if grad else torch.float32
+        self.dt = grad_dtype if grad else torch.float32
         if grad:
             leaves, by_ptr = {}, {}
             for k, v in sd.items():
@@ -69,7 +69,7 @@ class Oracle:
                     continue
                 key = (v.data_ptr(), v.dtype, tuple(v.shape))
                 if key not in by_ptr:
-                    by_ptr[key] = v.detach().double().cpu().requires_grad_(v.is_floating_point())
+                    by_ptr[key] = v.detach().to(self.dt).cpu().requires_grad_(v.is_floating_point())
                 leaves[k] = by_ptr[key]
             self.sd = leaves
         else:

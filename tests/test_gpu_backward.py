@@ -371,3 +371,29 @@ def test_mhcwalsh_backward_bf16_autocast():
           flush=True)
     assert abs(loss.item() - ref_loss.item()) <= 1e-2 * abs(ref_loss.item())
     assert rel <= 3e-2, rel
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("in_o,gsx,out_o,gsy", [(16, 16, 43, 44), (43, 44, 16, 16), (43, 48, 43, 44)])
+def test_hadamard_bwd_group_padded(K, in_o, gsx, out_o, gsy, dtype):
+    """walsh_hadamard_linear_ex_bwd on group-padded rows (the training SwiGLU
+    hidden layout) against the oracle on the unpadded rows; gx pad slots are
+    zeros, x / gy pad slots are ignored (filled with junk here)."""
+    c = make_case(K, 130, in_o, out_o, dtype, seed=in_o + gsx + out_o + gsy)
+    M = 130
+    xp = torch.full((M, 32, gsx), 7.0, dtype=dtype)
+    xp[:, :, :in_o] = c["x"].view(M, 32, in_o)
+    gp = torch.full((M, 32, gsy), -5.0, dtype=dtype)
+    gp[:, :, :out_o] = c["gy"].view(M, 32, out_o)
+    gx, da, db, dw = K.hadamard_linear_bwd(xp.view(M, -1).cuda(), gp.view(M, -1).cuda(), in_o, out_o, c["kw"],
+                                           c["kwt"], c["alpha"].cuda(), c["beta"].cuda(), latent=c["lc"], gsx=gsx,
+                                           gsy=gsy)
+    torch.cuda.synchronize()
+    ref = ohad.hadamard_linear_bwd_f64(c["x"].double().numpy(), c["codes"], c["alpha"].double().numpy(),
+                                       c["beta"].double().numpy(), c["gy"].double().numpy(),
+                                       latent=c["latent"].double().numpy())
+    gx3 = gx.float().cpu().view(M, 32, gsx)
+    assert torch.count_nonzero(gx3[:, :, in_o:]) == 0
+    assert_close(gx3[:, :, :in_o].reshape(M, -1).numpy(), ref[0], dtype, f"padded gx {in_o}/{gsx}x{out_o}/{gsy}")
+    for name, got, r in (("dalpha", da, ref[1]), ("dbeta", db, ref[2]), ("dweight", dw, ref[3])):
+        assert_close(got.cpu().numpy(), r, dtype, f"padded {name}")

@@ -495,21 +495,21 @@ WALSH_EXPORT int64_t walsh_hadamard_bwd_workspace_bytes(int64_t M, int64_t in_o,
     return plan(M, in_o, out_o, ld, esz).bytes;
 }
 
-WALSH_EXPORT int walsh_hadamard_linear_bwd(const void *x, int64_t ldx, const void *gy, int64_t ldg, int64_t M,
-                                           int64_t in_o, int64_t out_o, const uint8_t *kweight,
-                                           const uint8_t *kweight_t, const float *alpha, const float *beta,
-                                           const float *latent, void *gx, int64_t ldgx, float *dalpha, float *dbeta,
-                                           float *dweight, int dtype, void *workspace, int64_t workspace_bytes,
-                                           void *stream) {
-    const char *fn = "walsh_hadamard_linear_bwd";
+WALSH_EXPORT int walsh_hadamard_linear_ex_bwd(const void *x, int64_t ldx, int64_t gsx, const void *gy, int64_t ldg,
+                                              int64_t gsy, int64_t M, int64_t in_o, int64_t out_o,
+                                              const uint8_t *kweight, const uint8_t *kweight_t, const float *alpha,
+                                              const float *beta, const float *latent, void *gx, int64_t ldgx,
+                                              float *dalpha, float *dbeta, float *dweight, int dtype, void *workspace,
+                                              int64_t workspace_bytes, void *stream) {
+    const char *fn = "walsh_hadamard_linear_ex_bwd";
     if ((M > 0 && (!x || !gy)) || !alpha || !beta) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
     if (M < 0 || in_o <= 0 || out_o <= 0 || in_o > 65536 || out_o > 65536)
         return set_error(WALSH_EINVAL, "%s: bad shape M=%lld in_o=%lld out_o=%lld", fn, (long long)M,
                          (long long)in_o, (long long)out_o);
     if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype %d not supported", fn, dtype);
-    if (ldx < 32 * in_o || ldg < 32 * out_o || (gx && ldgx < 32 * in_o))
-        return set_error(WALSH_EINVAL, "%s: row strides too small (ldx=%lld ldg=%lld ldgx=%lld)", fn, (long long)ldx,
-                         (long long)ldg, (long long)ldgx);
+    if (gsx < in_o || gsy < out_o || ldx < 32 * gsx || ldg < 32 * gsy || (gx && ldgx < 32 * gsx))
+        return set_error(WALSH_EINVAL, "%s: strides too small (ldx=%lld gsx=%lld ldg=%lld gsy=%lld ldgx=%lld)", fn,
+                         (long long)ldx, (long long)gsx, (long long)ldg, (long long)gsy, (long long)ldgx);
     const bool need_a = gx || dalpha, need_b = dbeta != nullptr, need_w = dweight != nullptr;
     if (need_a && !kweight_t) return set_error(WALSH_EINVAL, "%s: dx / dalpha need kweight_t", fn);
     if (need_b && !kweight) return set_error(WALSH_EINVAL, "%s: dbeta needs kweight", fn);
@@ -559,25 +559,25 @@ WALSH_EXPORT int walsh_hadamard_linear_bwd(const void *x, int64_t ldx, const voi
         // beta' = alpha (stores dx), aux = x (dalpha)
         base(j.a);
         j.a.x = gc; j.a.ldx = ldg; j.a.in_o = (int)out_o; j.a.out_o = (int)in_o; j.a.Nt = Kc; j.a.Kc = Nt;
-        j.a.gsx = (int)out_o; j.a.gsy = (int)in_o; j.a.kw = kweight_t; j.a.alpha = beta; j.a.beta = alpha;
+        j.a.gsx = (int)gsy; j.a.gsy = (int)gsx; j.a.kw = kweight_t; j.a.alpha = beta; j.a.beta = alpha;
         j.a.beta_h = (int)in_o; j.a.y = gxc; j.a.ldy = gx ? ldgx : 0;
-        j.ra = BwdRed{xc, ldx, (int)in_o, pa + ia * 32 * Ap, p.Sa, p.tpa};
+        j.ra = BwdRed{xc, ldx, (int)gsx, pa + ia * 32 * Ap, p.Sa, p.tpa};
         j.nA = need_a ? (int)ceil_div((int64_t)p.Sa * Kc, kWaves) : 0;
         // the layer on x without beta or store, aux = gy (dbeta)
         base(j.b);
         j.b.x = xc; j.b.ldx = ldx; j.b.in_o = (int)in_o; j.b.out_o = (int)out_o; j.b.Nt = Nt; j.b.Kc = Kc;
-        j.b.gsx = (int)in_o; j.b.gsy = (int)out_o; j.b.kw = kweight; j.b.alpha = alpha; j.b.beta = nullptr;
+        j.b.gsx = (int)gsx; j.b.gsy = (int)gsy; j.b.kw = kweight; j.b.alpha = alpha; j.b.beta = nullptr;
         j.b.beta_h = 0; j.b.y = nullptr; j.b.ldy = 0;
-        j.rb = BwdRed{gc, ldg, (int)out_o, pb + ib * 32 * Bp, p.Sb, p.tpb};
+        j.rb = BwdRed{gc, ldg, (int)gsy, pb + ib * 32 * Bp, p.Sb, p.tpb};
         j.nB = need_b ? (int)ceil_div((int64_t)p.Sb * Nt, kWaves) : 0;
         // x and gy as transform inputs (dW)
         base(j.wx);
-        j.wx.x = xc; j.wx.ldx = ldx; j.wx.in_o = (int)in_o; j.wx.Kc = Kc; j.wx.gsx = (int)in_o; j.wx.alpha = alpha;
+        j.wx.x = xc; j.wx.ldx = ldx; j.wx.in_o = (int)in_o; j.wx.Kc = Kc; j.wx.gsx = (int)gsx; j.wx.alpha = alpha;
         base(j.wg);
-        j.wg.x = gc; j.wg.ldx = ldg; j.wg.in_o = (int)out_o; j.wg.Kc = Nt; j.wg.gsx = (int)out_o; j.wg.alpha = beta;
+        j.wg.x = gc; j.wg.ldx = ldg; j.wg.in_o = (int)out_o; j.wg.Kc = Nt; j.wg.gsx = (int)gsy; j.wg.alpha = beta;
         j.dw = BwdDW{pw + iw * 32 * (int64_t)Bp * Ap, p.Sw, p.tpw};
         j.nW = need_w ? p.Sw * Nt * Kc : 0;
-        const bool vec = out_o % 4 == 0 && in_o % 4 == 0 && ldx % 4 == 0 && ldg % 4 == 0 &&
+        const bool vec = gsy % 4 == 0 && gsx % 4 == 0 && ldx % 4 == 0 && ldg % 4 == 0 &&
                          (!gx || ldgx % 4 == 0) && (uintptr_t)gc % valign == 0 && (uintptr_t)xc % valign == 0 &&
                          (!gx || (uintptr_t)gxc % valign == 0);
         const dim3 G((unsigned)(j.nW + j.nA + j.nB)), B(kThreads);
@@ -606,4 +606,15 @@ WALSH_EXPORT int walsh_hadamard_linear_bwd(const void *x, int64_t ldx, const voi
     const int64_t nblk = sum_blocks(r, &bw, &ba);
     if (nblk > 0) launch(hadamard_bwd_reduce_kernel, dim3((unsigned)nblk), dim3(kSumCols * kSumPhases), 0, s, r);
     return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int walsh_hadamard_linear_bwd(const void *x, int64_t ldx, const void *gy, int64_t ldg, int64_t M,
+                                           int64_t in_o, int64_t out_o, const uint8_t *kweight,
+                                           const uint8_t *kweight_t, const float *alpha, const float *beta,
+                                           const float *latent, void *gx, int64_t ldgx, float *dalpha, float *dbeta,
+                                           float *dweight, int dtype, void *workspace, int64_t workspace_bytes,
+                                           void *stream) {
+    return walsh_hadamard_linear_ex_bwd(x, ldx, in_o, gy, ldg, out_o, M, in_o, out_o, kweight, kweight_t, alpha, beta,
+                                        latent, gx, ldgx, dalpha, dbeta, dweight, dtype, workspace, workspace_bytes,
+                                        stream);
 }

@@ -183,6 +183,100 @@ __global__ void sinkhorn_bwd_kernel(const float *__restrict__ h, const float *__
     }
 }
 
+// The same gradient with the states S_k kept in LDS (one column per thread,
+// [n_iter][NMAX*NMAX][threads]): one forward sweep stores them, one backward
+// sweep reads them, O(n_iter) per matrix.  Used when the states fit.
+constexpr int kSkBwdThreads = 64;
+template <int NMAX>
+__global__ __launch_bounds__(kSkBwdThreads) void sinkhorn_bwd_lds_kernel(const float *__restrict__ h,
+                                                                         const float *__restrict__ g, int64_t batch,
+                                                                         int n, int n_iter, float eps,
+                                                                         float *__restrict__ dh) {
+    extern __shared__ float st[];
+    const int tid = threadIdx.x;
+    const int64_t b = (int64_t)blockIdx.x * kSkBwdThreads + tid;
+    if (b >= batch) return;  // no barrier: each thread uses only its own LDS column
+    auto at = [&](int k, int e) -> float & { return st[((int64_t)k * NMAX * NMAX + e) * kSkBwdThreads + tid]; };
+    float m0[NMAX][NMAX], S[NMAX][NMAX];
+    const float *src = h + b * n * n;
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i)
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) S[i][j] = m0[i][j] = (i < n && j < n) ? expf(src[i * n + j]) : 0.f;
+    for (int k = 0; k < n_iter; ++k) {
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i)
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) at(k, i * NMAX + j) = S[i][j];
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) {
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) sum += (i < n) ? S[i][j] : 0.f;
+            const float c = sum + eps;
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) S[i][j] = (j < n) ? __fdiv_rn(S[i][j], c) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) sum += (j < n) ? S[i][j] : 0.f;
+            const float r = sum + eps;
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) S[i][j] = (i < n) ? __fdiv_rn(S[i][j], r) : 0.f;
+        }
+    }
+    float G[NMAX][NMAX];
+    const float *gs = g + b * n * n;
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i)
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) G[i][j] = (i < n && j < n) ? gs[i * n + j] : 0.f;
+    for (int k = n_iter - 1; k >= 0; --k) {
+        float T[NMAX][NMAX], c[NMAX], r[NMAX];
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) {
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) sum += (i < n) ? at(k, i * NMAX + j) : 0.f;
+            c[j] = sum + eps;
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) T[i][j] = (j < n) ? __fdiv_rn(at(k, i * NMAX + j), c[j]) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) sum += (j < n) ? T[i][j] : 0.f;
+            r[i] = sum + eps;
+        }
+        float dT[NMAX][NMAX];
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+            float dot = 0.f;
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) dot += (i < n && j < n) ? G[i][j] * __fdiv_rn(T[i][j], r[i]) : 0.f;
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) dT[i][j] = (i < n && j < n) ? __fdiv_rn(G[i][j] - dot, r[i]) : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) {
+            float dot = 0.f;
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) dot += (i < n && j < n) ? dT[i][j] * T[i][j] : 0.f;
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) G[i][j] = (i < n && j < n) ? __fdiv_rn(dT[i][j] - dot, c[j]) : 0.f;
+        }
+    }
+    float *dst = dh + b * n * n;
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i)
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j)
+            if (i < n && j < n) dst[i * n + j] = G[i][j] * m0[i][j];
+}
+
 __global__ void sinkhorn_kernel(const float *__restrict__ h, int64_t batch, int n, int n_iter, float eps,
                                 float *__restrict__ out) {
     for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < batch; b += (int64_t)gridDim.x * blockDim.x) {
@@ -861,6 +955,13 @@ WALSH_EXPORT int walsh_sinkhorn_bwd(const float *h, const float *g, int64_t batc
                          "walsh_sinkhorn_bwd: batch=%lld n=%lld n_iter=%lld (n must be 1..8)", (long long)batch,
                          (long long)n, (long long)n_iter);
     if (batch == 0) return WALSH_OK;
+    const size_t lds = (size_t)n_iter * 16 * kSkBwdThreads * sizeof(float);
+    if (n <= 4 && n_iter > 0 && lds <= (size_t)device_info().max_shared_per_block / 2) {
+        const int64_t grid = ceil_div(batch, kSkBwdThreads);
+        launch(sinkhorn_bwd_lds_kernel<4>, dim3((unsigned)grid), dim3(kSkBwdThreads), (uint32_t)lds,
+               (hipStream_t)stream, h, g, batch, (int)n, (int)n_iter, eps, dh);
+        return check_hip(hipGetLastError(), "walsh_sinkhorn_bwd launch");
+    }
     const int block = 64;
     int64_t grid = ceil_div(batch, block);
     if (grid > (int64_t)device_info().cu_count * 16) grid = (int64_t)device_info().cu_count * 16;

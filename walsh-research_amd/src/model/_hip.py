@@ -47,6 +47,8 @@ SIGNATURES = {
     "walsh_hadamard_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I]),
     "walsh_hadamard_linear_bwd": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P, _P,
                                        _P, _I, _P, _I64, _P]),
+    "walsh_hadamard_linear_ex_bwd": (_I, [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P,
+                                          _I64, _P, _P, _P, _I, _P, _I64, _P]),
     "walsh_octonion_weight_elems": (_I64, [_I64, _I64]),
     "walsh_octonion_prepare": (_I, [_P, _I64, _I64, _P, _I, _P]),
     "walsh_octonion_linear_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I, _P]),

@@ -17,10 +17,11 @@ import torch.nn as nn
 from torch.nn import functional as F
 
 from .hadamard import HadamardLinear, HadamardTernaryLinear, HadamardTernaryLinearTuple  # noqa: F401
+from .hadamard import HadamardLinearFunction
 from .hadamard import HadamardHeadMixer, HadamardHeadMixerFused
 from .octonion import OctonionHeadMixerFused, OctonionTernaryLinear
 from . import kernels
-from ._common import act_dtype, tracked_dtype
+from ._common import act_dtype
 
 _HADAMARD_AVAILABLE = True
 _HADAMARD_HEAD_MIXER_AVAILABLE = True
@@ -140,6 +141,19 @@ class OctonionHeadMixer(OctonionHeadMixerFused):
     """chassis.py:347-399: same parameters and result as the fused mixer."""
 
 
+def _attention_backends(tracked: bool):
+    """Under autograd with 16-bit operands, scaled_dot_product_attention may
+    use only the fused flash / memory-efficient kernels: the math
+    fallback's backward makes bf16 batched products with transposed right
+    operands (see _common.tracked_dtype), so a case those kernels cannot
+    take raises instead."""
+    import contextlib
+    if not tracked:
+        return contextlib.nullcontext()
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    return sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION])
+
+
 def _full(layer, x):
     """Apply a tuple-interface ternary linear to a full [.., C] tensor."""
     return layer.forward_full(x)
@@ -189,12 +203,8 @@ class CausalSelfAttention(nn.Module):
         v = v.transpose(1, 2).to(q.dtype)
         att_dt = q.dtype
         tracked = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
-        if tracked:
-            # training: attention (and its backward) in float32, see tracked_dtype
-            q, k, v = (t.to(tracked_dtype(att_dt)) for t in (q, k, v))
         drop = self.dropout if self.training else 0
-        with torch.autocast("cuda", dtype=torch.get_autocast_dtype("cuda"),
-                            enabled=torch.is_autocast_enabled("cuda") and not tracked):
+        with _attention_backends(tracked and q.is_cuda and q.dtype != torch.float32):
             if kv_cache is not None and kv_cache.cached_len > 0 and T == 1:
                 # one new position attends to every cached one: no mask needed
                 y = F.scaled_dot_product_attention(q, k, v, dropout_p=drop)
@@ -247,6 +257,15 @@ class SwiGLUMLP(nn.Module):
                                         (u.ternary_state()[2], u.alpha, u.beta))
             return kernels.hadamard_linear(h, d.in_o, d.out_o, d.ternary_state()[2], d.alpha, d.beta,
                                            gsx=h.shape[-1] // 32)
+        if isinstance(self.gate_proj, HadamardTernaryLinearTuple):
+            # training: the three linears with their backward kernels, the
+            # hidden activation in the same group-padded layout (stride
+            # roundup(hid_o, 4); pad slots are zeros and stay zero)
+            g, u, d = self.gate_proj.inner, self.up_proj.inner, self.down_proj.inner
+            gsh = (g.out_o + 3) // 4 * 4
+            hg = HadamardLinearFunction.apply(x, g.weight, g.alpha, g.beta, g, None, gsh)
+            hu = HadamardLinearFunction.apply(x, u.weight, u.alpha, u.beta, u, None, gsh)
+            return HadamardLinearFunction.apply(F.silu(hg) * hu, d.weight, d.alpha, d.beta, d, gsh, None)
         h = F.silu(_full(self.gate_proj, x)) * _full(self.up_proj, x)
         return _full(self.down_proj, h)
 

@@ -63,9 +63,10 @@ class HadamardLinearFunction(torch.autograd.Function):
     (fht_cuda.py:316-337, :497-519) builds."""
 
     @staticmethod
-    def forward(ctx, x, weight, alpha, beta, layer):
-        y = layer._apply_2d(x, x.dtype)
-        ctx.layer = layer
+    def forward(ctx, x, weight, alpha, beta, layer, gsx=None, gsy=None):
+        _, _, kw = layer.ternary_state()
+        y = kernels.hadamard_linear(x, layer.in_o, layer.out_o, kw, alpha, beta, gsx=gsx, gsy=gsy)
+        ctx.layer, ctx.gs = layer, (gsx, gsy)
         ctx.save_for_backward(x, weight, alpha, beta)
         return y
 
@@ -73,12 +74,14 @@ class HadamardLinearFunction(torch.autograd.Function):
     def backward(ctx, gy):
         x, weight, alpha, beta = ctx.saved_tensors
         layer = ctx.layer
-        nx, nw, na, nb, _ = ctx.needs_input_grad
+        nx, nw, na, nb = ctx.needs_input_grad[:4]
         _, packed, kw = layer.ternary_state()
         kwt = layer.ternary_state_t() if (nx or na) else None
+        gsx, gsy = ctx.gs
         gx, da, db, dw = kernels.hadamard_linear_bwd(x, gy.to(x.dtype).contiguous(), layer.in_o, layer.out_o, kw,
-                                                      kwt, alpha, beta, latent=weight, need=(nx, na, nb, nw))
-        return gx, dw, da, db, None
+                                                      kwt, alpha, beta, latent=weight, need=(nx, na, nb, nw),
+                                                      gsx=gsx, gsy=gsy)
+        return gx, dw, da, db, None, None, None
 
 
 class _HadamardBase(nn.Module):

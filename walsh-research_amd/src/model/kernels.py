@@ -253,31 +253,36 @@ def hadamard_prepare_t(packed: torch.Tensor, in_o: int, out_o: int) -> torch.Ten
 
 def hadamard_linear_bwd(x: torch.Tensor, gy: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tensor,
                         kweight_t: torch.Tensor, alpha: torch.Tensor, beta: torch.Tensor,
-                        latent: torch.Tensor = None, need=(True, True, True, True)):
+                        latent: torch.Tensor = None, need=(True, True, True, True), gsx: int = None,
+                        gsy: int = None):
     """Backward of hadamard_linear for the output gradient ``gy``.
 
     Returns (gx, dalpha, dbeta, dweight); entries not requested in ``need``
     (same order) are None.  gx has x's shape and dtype; the others are
     float32 [32, in_o], [32, out_o], [32, out_o, in_o].  With ``latent`` the
     weight gradient passes the straight-through estimator's clamp
-    (physics.py:48-50): zero where |latent| > 1.5."""
+    (physics.py:48-50): zero where |latent| > 1.5.  gsx / gsy are the group
+    strides of x (and gx) and gy rows, as in hadamard_linear."""
     _hip.require_device(x, "input")
     _hip.require_device(gy, "output gradient")
     dt = x.dtype
     code = _hip.dtype_code(dt)
+    gsx = in_o if gsx is None else gsx
+    gsy = out_o if gsy is None else gsy
     assert gy.dtype == dt, f"gradient dtype {gy.dtype} != input dtype {dt}"
-    assert x.shape[-1] == 32 * in_o and gy.shape[-1] == 32 * out_o, "x / gy widths"
+    assert x.shape[-1] == 32 * gsx and gy.shape[-1] == 32 * gsy, "x / gy widths"
     assert x.shape[:-1] == gy.shape[:-1], "x / gy leading shapes differ"
-    xc = x.reshape(-1, 32 * in_o).contiguous()
-    gc = gy.reshape(-1, 32 * out_o).contiguous()
+    xc = x.reshape(-1, 32 * gsx).contiguous()
+    gc = gy.reshape(-1, 32 * gsy).contiguous()
     M = xc.shape[0]
     dev = x.device
     want_x, want_a, want_b, want_w = need
-    gx = torch.empty_like(xc) if want_x else None
+    # the kernel writes pad slots up to roundup(in_o, 4); wider pads start at zero
+    gx = (torch.zeros_like(xc) if gsx > (in_o + 3) // 4 * 4 else torch.empty_like(xc)) if want_x else None
     da = torch.empty(32, in_o, device=dev, dtype=torch.float32) if want_a else None
     db = torch.empty(32, out_o, device=dev, dtype=torch.float32) if want_b else None
     dw = torch.empty(32, out_o, in_o, device=dev, dtype=torch.float32) if want_w else None
-    nws = _hip.lib().walsh_hadamard_bwd_workspace_bytes(M, in_o, out_o, code)
+    nws = _hip.lib().walsh_hadamard_bwd_workspace_bytes(M, gsx, gsy, code)
     ws = torch.empty(max(nws, 1), device=dev, dtype=torch.uint8)
     alpha = alpha.detach().float().contiguous()
     beta = beta.detach().float().contiguous()
@@ -290,8 +295,8 @@ def hadamard_linear_bwd(x: torch.Tensor, gy: torch.Tensor, in_o: int, out_o: int
     # algorithmic: x and gy read once, gx written once (+ the parameters)
     nbytes = M * 32 * (2 * in_o + out_o) * esz + 4 * 32 * (in_o + out_o) * 3 + 4 * 32 * in_o * out_o * 2
     flops = M * 32 * (3 * 2 * in_o * out_o + 20 * (in_o + out_o))
-    _hip.call("walsh_hadamard_linear_bwd", xc.data_ptr(), 32 * in_o, gc.data_ptr(), 32 * out_o, M, in_o, out_o,
-              ptr(kweight), ptr(kweight_t), alpha.data_ptr(), beta.data_ptr(), ptr(lat), ptr(gx), 32 * in_o,
+    _hip.call("walsh_hadamard_linear_ex_bwd", xc.data_ptr(), 32 * gsx, gsx, gc.data_ptr(), 32 * gsy, gsy, M, in_o,
+              out_o, ptr(kweight), ptr(kweight_t), alpha.data_ptr(), beta.data_ptr(), ptr(lat), ptr(gx), 32 * gsx,
               ptr(da), ptr(db), ptr(dw), code, ws.data_ptr(), nws, _hip.stream(dev),
               kernel="hadamard_linear_bwd<%s>" % ("bf16" if dt == torch.bfloat16 else "f32"), nbytes=nbytes,
               flops=flops)

@@ -204,14 +204,17 @@ class mHCResidualStream(nn.Module):
         sk = self.H_res.sinkhorn
         h_res = _sinkhorn((self.H_res.alpha * d_res.reshape(B, T, n, n) + self.H_res.bias).float(), sk.n_iter,
                           sk.eps)
-        # the n x n mixing as broadcast products summed in float32, rounded
-        # to the stream dtype (what the reference's autocast matmuls give),
-        # without batched matmuls (see tracked_dtype)
-        xw = x.float()
-        layer_in = (h_pre.transpose(-2, -1).float() * xw).sum(2).to(x.dtype)
+        # the n x n mixing as float32 products rounded to the stream dtype
+        # (what the reference's autocast matmuls give); float32 keeps the
+        # batched products out of bf16 (see tracked_dtype)
+        dev = x.device.type
+        with torch.autocast(dev, dtype=torch.get_autocast_dtype(dev), enabled=False):
+            xw = x.float()
+            layer_in = torch.matmul(h_pre.float(), xw).squeeze(2).to(x.dtype)
         out = layer_fn(layer_in if norm is None else norm(layer_in))
-        res = (h_res.float().unsqueeze(-1) * xw.unsqueeze(2)).sum(3)
-        post = h_post.transpose(-2, -1).float() * out.float().unsqueeze(2)
+        with torch.autocast(dev, dtype=torch.get_autocast_dtype(dev), enabled=False):
+            res = torch.matmul(h_res.float(), xw)
+            post = h_post.transpose(-2, -1).float() * out.float().unsqueeze(2)
         return res.to(x.dtype) + post.to(x.dtype)
 
     def forward(self, x, layer_fn):
