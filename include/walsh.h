@@ -349,6 +349,24 @@ int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out, int64_t ld_o
                        const float *h_post, void *x_new, int64_t ld_new, int64_t M, int64_t n, int64_t C, int dtype,
                        void *stream);
 
+/* Training (the autograd torch derives for mHCResidualStream.forward,
+ * src/model/mhc.py:366-381); dense rows: x, dx, d_new [M][n][C];
+ * layer_in, d_layer_in, out, d_out [M][C] (all of dtype); h_pre, h_post
+ * [M][n], h_res [M][n][n] and their gradients float32; n <= 4, C % 4 == 0.
+ * walsh_mhc_aggregate_fwd: layer_in = H_pre @ x (mhc.py:366), float32 sums.
+ * walsh_mhc_aggregate_bwd: dx = H_pre^T d_layer_in, dh_pre[s] = <d_layer_in, x_s>.
+ * walsh_mhc_post_bwd: for x_new = H_res @ x + H_post^T (x) out:
+ *   dx_s = sum_i H_res[i][s] d_new_i, d_out = sum_i H_post[i] d_new_i,
+ *   dh_res[i][s] = <d_new_i, x_s>, dh_post[i] = <d_new_i, out>.
+ *   One wavefront per token; sums over C in a fixed order. */
+int walsh_mhc_aggregate_fwd(const void *x, const float *h_pre, void *layer_in, int64_t M, int64_t n, int64_t C,
+                            int dtype, void *stream);
+int walsh_mhc_aggregate_bwd(const void *x, const float *h_pre, const void *d_layer_in, void *dx, float *dh_pre,
+                            int64_t M, int64_t n, int64_t C, int dtype, void *stream);
+int walsh_mhc_post_bwd(const void *x, const void *out, const float *h_res, const float *h_post, const void *d_new,
+                       void *dx, void *d_out, float *dh_res, float *dh_post, int64_t M, int64_t n, int64_t C,
+                       int dtype, void *stream);
+
 /* ------------------------------------------------------------------ A10-A13
  * Hadamard mixture-of-experts FFN (src/model/moe.py:306-560).  Expert e owns
  * the 32-wide feature block x[:, 32e:32e+32]; E <= 128 experts; each token

@@ -397,3 +397,34 @@ def test_hadamard_bwd_group_padded(K, in_o, gsx, out_o, gsy, dtype):
     assert_close(gx3[:, :, :in_o].reshape(M, -1).numpy(), ref[0], dtype, f"padded gx {in_o}/{gsx}x{out_o}/{gsy}")
     for name, got, r in (("dalpha", da, ref[1]), ("dbeta", db, ref[2]), ("dweight", dw, ref[3])):
         assert_close(got.cpu().numpy(), r, dtype, f"padded {name}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,C", [(4, 512), (3, 44), (1, 260)])
+def test_stream_mixing_bwd(K, n, C, dtype):
+    """walsh_mhc_aggregate_fwd/_bwd and walsh_mhc_post_bwd against float64
+    autograd of layer_in = H_pre @ x and x_new = H_res @ x + H_post^T out
+    (mhc.py:366-381) on the same (rounded) inputs."""
+    g = torch.Generator().manual_seed(n * 1000 + C)
+    M = 37
+    x = torch.randn(M, n, C, generator=g).to(dtype)
+    out = torch.randn(M, C, generator=g).to(dtype)
+    hp = torch.rand(M, 1, n, generator=g)
+    hr = torch.rand(M, n, n, generator=g)
+    hq = 2 * torch.rand(M, 1, n, generator=g)
+    gli = torch.randn(M, C, generator=g).to(dtype)
+    gnew = torch.randn(M, n, C, generator=g).to(dtype)
+    li = K.mhc_aggregate(x.cuda(), hp.cuda())
+    dx1, dhp = K.mhc_aggregate_bwd(x.cuda(), hp.cuda(), gli.cuda())
+    dx2, dout, dhr, dhq = K.mhc_post_bwd(x.cuda(), out.cuda(), hr.cuda(), hq.cuda(), gnew.cuda())
+    torch.cuda.synchronize()
+    xr, orr, hpr, hrr, hqr = (t.double().requires_grad_(True) for t in (x, out, hp, hr, hq))
+    li_ref = torch.matmul(hpr, xr).squeeze(1)
+    new_ref = torch.matmul(hrr, xr) + hqr.transpose(-2, -1) * orr.unsqueeze(1)
+    torch.autograd.backward([li_ref, new_ref], [gli.double(), gnew.double()])
+    assert_close(li.float().cpu().numpy(), li_ref.detach().numpy(), dtype, f"aggregate n={n} C={C}")
+    assert_close(dhp.cpu().numpy(), hpr.grad.numpy(), dtype, "dh_pre")
+    assert_close(dhr.cpu().numpy(), hrr.grad.numpy(), dtype, "dh_res")
+    assert_close(dhq.cpu().numpy(), hqr.grad.numpy(), dtype, "dh_post")
+    assert_close(dout.float().cpu().numpy(), orr.grad.numpy(), dtype, "d_out")
+    assert_close((dx1.float() + dx2.float()).cpu().numpy(), xr.grad.numpy(), dtype, "dx")

@@ -277,6 +277,135 @@ __global__ __launch_bounds__(kSkBwdThreads) void sinkhorn_bwd_lds_kernel(const f
             if (i < n && j < n) dst[i * n + j] = G[i][j] * m0[i][j];
 }
 
+// ---------------------------------------------------------------- stream mixing for training
+// Dense rows: x / dx / dnew [M][n][C], li / dli / out / dout [M][C] (one
+// dtype T), h_pre / h_post [M][n], h_res [M][n][n] float32.  One wavefront
+// per token; lane l covers columns 4l + 256k; sums over the C columns are
+// per-lane partials reduced across the wavefront with xor shuffles.
+constexpr int kMixWaves = 4;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * kMixWaves) void mhc_agg_fwd_kernel(const T *__restrict__ x,
+                                                                     const float *__restrict__ h_pre,
+                                                                     T *__restrict__ li, int64_t M, int n, int C) {
+    const int lane = threadIdx.x & 63;
+    for (int64_t t = (int64_t)blockIdx.x * kMixWaves + (threadIdx.x >> 6); t < M; t += (int64_t)gridDim.x * kMixWaves) {
+        float hp[kMaxStreams];
+#pragma unroll
+        for (int s = 0; s < kMaxStreams; ++s) hp[s] = s < n ? h_pre[t * n + s] : 0.f;
+        for (int c = 4 * lane; c < C; c += 256) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < kMaxStreams; ++s)
+                if (s < n) acc += hp[s] * load4(x + (t * n + s) * C + c);
+            store4(li + t * C + c, acc);
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * kMixWaves) void mhc_agg_bwd_kernel(const T *__restrict__ x,
+                                                                     const float *__restrict__ h_pre,
+                                                                     const T *__restrict__ dli, T *__restrict__ dx,
+                                                                     float *__restrict__ dh_pre, int64_t M, int n,
+                                                                     int C) {
+    const int lane = threadIdx.x & 63;
+    for (int64_t t = (int64_t)blockIdx.x * kMixWaves + (threadIdx.x >> 6); t < M; t += (int64_t)gridDim.x * kMixWaves) {
+        float hp[kMaxStreams], dh[kMaxStreams];
+#pragma unroll
+        for (int s = 0; s < kMaxStreams; ++s) {
+            hp[s] = s < n ? h_pre[t * n + s] : 0.f;
+            dh[s] = 0.f;
+        }
+        for (int c = 4 * lane; c < C; c += 256) {
+            const f32x4 g = load4(dli + t * C + c);
+#pragma unroll
+            for (int s = 0; s < kMaxStreams; ++s) {
+                if (s >= n) continue;
+                const f32x4 xv = load4(x + (t * n + s) * C + c);
+                dh[s] += g[0] * xv[0] + g[1] * xv[1] + g[2] * xv[2] + g[3] * xv[3];
+                store4(dx + (t * n + s) * C + c, hp[s] * g);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kMaxStreams; ++s) {
+            if (s >= n) continue;
+            const float v = wave_sum(dh[s]);
+            if (lane == 0) dh_pre[t * n + s] = v;
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * kMixWaves) void mhc_post_bwd_kernel(const T *__restrict__ x, const T *__restrict__ out,
+                                                                      const float *__restrict__ h_res,
+                                                                      const float *__restrict__ h_post,
+                                                                      const T *__restrict__ dnew, T *__restrict__ dx,
+                                                                      T *__restrict__ dout, float *__restrict__ dh_res,
+                                                                      float *__restrict__ dh_post, int64_t M, int n,
+                                                                      int C) {
+    const int lane = threadIdx.x & 63;
+    for (int64_t t = (int64_t)blockIdx.x * kMixWaves + (threadIdx.x >> 6); t < M; t += (int64_t)gridDim.x * kMixWaves) {
+        float hr[kMaxStreams][kMaxStreams], hq[kMaxStreams];
+        float dr[kMaxStreams][kMaxStreams], dq[kMaxStreams];
+#pragma unroll
+        for (int i = 0; i < kMaxStreams; ++i) {
+            hq[i] = i < n ? h_post[t * n + i] : 0.f;
+            dq[i] = 0.f;
+#pragma unroll
+            for (int s = 0; s < kMaxStreams; ++s) {
+                hr[i][s] = (i < n && s < n) ? h_res[(t * n + i) * n + s] : 0.f;
+                dr[i][s] = 0.f;
+            }
+        }
+        for (int c = 4 * lane; c < C; c += 256) {
+            f32x4 g[kMaxStreams], xv[kMaxStreams];
+#pragma unroll
+            for (int i = 0; i < kMaxStreams; ++i) {
+                g[i] = i < n ? load4(dnew + (t * n + i) * C + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+                xv[i] = i < n ? load4(x + (t * n + i) * C + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            const f32x4 o = load4(out + t * C + c);
+            f32x4 go = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < kMaxStreams; ++i) {
+                go += hq[i] * g[i];
+                dq[i] += g[i][0] * o[0] + g[i][1] * o[1] + g[i][2] * o[2] + g[i][3] * o[3];
+#pragma unroll
+                for (int s = 0; s < kMaxStreams; ++s)
+                    dr[i][s] += g[i][0] * xv[s][0] + g[i][1] * xv[s][1] + g[i][2] * xv[s][2] + g[i][3] * xv[s][3];
+            }
+            store4(dout + t * C + c, go);
+#pragma unroll
+            for (int s = 0; s < kMaxStreams; ++s) {
+                if (s >= n) continue;
+                f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < kMaxStreams; ++i) d += hr[i][s] * g[i];
+                store4(dx + (t * n + s) * C + c, d);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxStreams; ++i) {
+            if (i >= n) continue;
+            const float vq = wave_sum(dq[i]);
+            if (lane == 0) dh_post[t * n + i] = vq;
+#pragma unroll
+            for (int s = 0; s < kMaxStreams; ++s) {
+                if (s >= n) continue;
+                const float v = wave_sum(dr[i][s]);
+                if (lane == 0) dh_res[(t * n + i) * n + s] = v;
+            }
+        }
+    }
+}
+
 __global__ void sinkhorn_kernel(const float *__restrict__ h, int64_t batch, int n, int n_iter, float eps,
                                 float *__restrict__ out) {
     for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < batch; b += (int64_t)gridDim.x * blockDim.x) {
@@ -1230,4 +1359,70 @@ WALSH_EXPORT int walsh_mhc_pre_wide_fwd(const void *x, int64_t ldx, int64_t M, i
         if (rc) return rc;
     }
     return WALSH_OK;
+}
+
+static int mix_check(const char *fn, int64_t M, int64_t n, int64_t C, int dtype) {
+    if (M < 0 || n < 1 || n > kMaxStreams || C < 4 || C % 4)
+        return set_error(WALSH_EINVAL, "%s: bad shape M=%lld n=%lld C=%lld (n <= %d, C a multiple of 4)", fn,
+                         (long long)M, (long long)n, (long long)C, kMaxStreams);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype %d", fn, dtype);
+    return WALSH_OK;
+}
+
+static dim3 mix_grid(int64_t M) {
+    int64_t g = ceil_div(M, kMixWaves);
+    const int64_t cap = (int64_t)device_info().cu_count * 16;
+    return dim3((unsigned)(g < cap ? g : cap));
+}
+
+WALSH_EXPORT int walsh_mhc_aggregate_fwd(const void *x, const float *h_pre, void *layer_in, int64_t M, int64_t n,
+                                         int64_t C, int dtype, void *stream) {
+    const char *fn = "walsh_mhc_aggregate_fwd";
+    int rc = mix_check(fn, M, n, C, dtype);
+    if (rc) return rc;
+    if (M == 0) return WALSH_OK;
+    if (!x || !h_pre || !layer_in) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (dtype == WALSH_BF16)
+        launch(mhc_agg_fwd_kernel<uint16_t>, mix_grid(M), dim3(64 * kMixWaves), 0, (hipStream_t)stream,
+               (const uint16_t *)x, h_pre, (uint16_t *)layer_in, M, (int)n, (int)C);
+    else
+        launch(mhc_agg_fwd_kernel<float>, mix_grid(M), dim3(64 * kMixWaves), 0, (hipStream_t)stream, (const float *)x,
+               h_pre, (float *)layer_in, M, (int)n, (int)C);
+    return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int walsh_mhc_aggregate_bwd(const void *x, const float *h_pre, const void *d_layer_in, void *dx,
+                                         float *dh_pre, int64_t M, int64_t n, int64_t C, int dtype, void *stream) {
+    const char *fn = "walsh_mhc_aggregate_bwd";
+    int rc = mix_check(fn, M, n, C, dtype);
+    if (rc) return rc;
+    if (M == 0) return WALSH_OK;
+    if (!x || !h_pre || !d_layer_in || !dx || !dh_pre) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (dtype == WALSH_BF16)
+        launch(mhc_agg_bwd_kernel<uint16_t>, mix_grid(M), dim3(64 * kMixWaves), 0, (hipStream_t)stream,
+               (const uint16_t *)x, h_pre, (const uint16_t *)d_layer_in, (uint16_t *)dx, dh_pre, M, (int)n, (int)C);
+    else
+        launch(mhc_agg_bwd_kernel<float>, mix_grid(M), dim3(64 * kMixWaves), 0, (hipStream_t)stream, (const float *)x,
+               h_pre, (const float *)d_layer_in, (float *)dx, dh_pre, M, (int)n, (int)C);
+    return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int walsh_mhc_post_bwd(const void *x, const void *out, const float *h_res, const float *h_post,
+                                    const void *d_new, void *dx, void *d_out, float *dh_res, float *dh_post, int64_t M,
+                                    int64_t n, int64_t C, int dtype, void *stream) {
+    const char *fn = "walsh_mhc_post_bwd";
+    int rc = mix_check(fn, M, n, C, dtype);
+    if (rc) return rc;
+    if (M == 0) return WALSH_OK;
+    if (!x || !out || !h_res || !h_post || !d_new || !dx || !d_out || !dh_res || !dh_post)
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (dtype == WALSH_BF16)
+        launch(mhc_post_bwd_kernel<uint16_t>, mix_grid(M), dim3(64 * kMixWaves), 0, (hipStream_t)stream,
+               (const uint16_t *)x, (const uint16_t *)out, h_res, h_post, (const uint16_t *)d_new, (uint16_t *)dx,
+               (uint16_t *)d_out, dh_res, dh_post, M, (int)n, (int)C);
+    else
+        launch(mhc_post_bwd_kernel<float>, mix_grid(M), dim3(64 * kMixWaves), 0, (hipStream_t)stream, (const float *)x,
+               (const float *)out, h_res, h_post, (const float *)d_new, (float *)dx, (float *)d_out, dh_res, dh_post,
+               M, (int)n, (int)C);
+    return check_hip(hipGetLastError(), fn);
 }

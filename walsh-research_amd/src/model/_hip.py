@@ -61,6 +61,9 @@ SIGNATURES = {
     "walsh_mhc_pre_norm_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float, _I64, ctypes.c_float,
                                     _P, _P, _P, _P, _I64, _P, ctypes.c_float, _I, _P]),
     "walsh_mhc_post_fwd": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P]),
+    "walsh_mhc_aggregate_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
+    "walsh_mhc_aggregate_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P]),
+    "walsh_mhc_post_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P]),
     "walsh_mhc_pre_wide_workspace": (_I64, [_I64, _I64, _I64]),
     "walsh_mhc_pre_wide_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _I64, _F, _P, _P, _P, _P, _I64, _P, _F,
                                     _P, _I64, _I, _P]),

@@ -642,6 +642,63 @@ def mhc_post(x: torch.Tensor, out: torch.Tensor, h_res: torch.Tensor, h_post: to
     return x_new
 
 
+def _dense(t: torch.Tensor, dtype=None) -> torch.Tensor:
+    t = t if dtype is None else t.to(dtype)
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def mhc_aggregate(x: torch.Tensor, h_pre: torch.Tensor) -> torch.Tensor:
+    """layer_in = H_pre @ x (mhc.py:366) for x [..., n, C], h_pre [..., 1, n] or
+    [..., n]; float32 sums, result in x.dtype [..., C]."""
+    _hip.require_device(x, "stream input")
+    n, C = x.shape[-2], x.shape[-1]
+    xv = _dense(x)
+    M = xv.numel() // (n * C)
+    hp = _dense(h_pre.detach(), torch.float32)
+    assert hp.numel() == M * n, "h_pre shape"
+    li = torch.empty(x.shape[:-2] + (C,), device=x.device, dtype=x.dtype)
+    _hip.call("walsh_mhc_aggregate_fwd", xv.data_ptr(), hp.data_ptr(), li.data_ptr(), M, n, C,
+              _hip.dtype_code(x.dtype), _hip.stream(x.device))
+    return li
+
+
+def mhc_aggregate_bwd(x: torch.Tensor, h_pre: torch.Tensor, d_li: torch.Tensor):
+    """(dx [..., n, C] in x.dtype, dh_pre float32 h_pre's shape) of mhc_aggregate."""
+    n, C = x.shape[-2], x.shape[-1]
+    xv = _dense(x)
+    M = xv.numel() // (n * C)
+    hp = _dense(h_pre.detach(), torch.float32)
+    g = _dense(d_li, x.dtype)
+    dx = torch.empty_like(xv)
+    dh = torch.empty(hp.shape, device=x.device, dtype=torch.float32)
+    _hip.call("walsh_mhc_aggregate_bwd", xv.data_ptr(), hp.data_ptr(), g.data_ptr(), dx.data_ptr(), dh.data_ptr(),
+              M, n, C, _hip.dtype_code(x.dtype), _hip.stream(x.device))
+    return dx, dh
+
+
+def mhc_post_bwd(x: torch.Tensor, out: torch.Tensor, h_res: torch.Tensor, h_post: torch.Tensor,
+                 d_new: torch.Tensor):
+    """Gradients (dx, d_out, dh_res, dh_post) of mhc_post; dx / d_out in
+    x.dtype, the mappings' gradients float32 in their input shapes."""
+    n, C = x.shape[-2], x.shape[-1]
+    xv = _dense(x)
+    M = xv.numel() // (n * C)
+    o = _dense(out, x.dtype)
+    hr = _dense(h_res.detach(), torch.float32)
+    hq = _dense(h_post.detach(), torch.float32)
+    g = _dense(d_new, x.dtype)
+    dx = torch.empty_like(xv)
+    dout = torch.empty_like(o)
+    dhr = torch.empty(hr.shape, device=x.device, dtype=torch.float32)
+    dhq = torch.empty(hq.shape, device=x.device, dtype=torch.float32)
+    esz = x.element_size()
+    _hip.call("walsh_mhc_post_bwd", xv.data_ptr(), o.data_ptr(), hr.data_ptr(), hq.data_ptr(), g.data_ptr(),
+              dx.data_ptr(), dout.data_ptr(), dhr.data_ptr(), dhq.data_ptr(), M, n, C, _hip.dtype_code(x.dtype),
+              _hip.stream(x.device), kernel="mhc_post_bwd_kernel<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"),
+              nbytes=M * (3 * n * C + 2 * C) * esz + M * (n * n + n) * 8, flops=M * n * C * (4 * n + 4))
+    return dx, dout, dhr, dhq
+
+
 # ------------------------------------------------------------------ MoE
 
 def moe_router_fragments(w1: torch.Tensor, w2: torch.Tensor, dtype: torch.dtype):

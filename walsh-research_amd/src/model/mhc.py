@@ -17,6 +17,38 @@ from ._common import WeightCache, act_dtype
 _MAX_STREAMS = 4
 
 
+class StreamAggregateFunction(torch.autograd.Function):
+    """layer_in = H_pre @ x (mhc.py:366) with its backward on the GPU
+    (walsh_mhc_aggregate_fwd / _bwd)."""
+
+    @staticmethod
+    def forward(ctx, x, h_pre):
+        ctx.save_for_backward(x, h_pre)
+        return kernels.mhc_aggregate(x, h_pre)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, h_pre = ctx.saved_tensors
+        dx, dh = kernels.mhc_aggregate_bwd(x, h_pre, g)
+        return dx, dh.to(h_pre.dtype)
+
+
+class StreamUpdateFunction(torch.autograd.Function):
+    """x_new = H_res @ x + H_post^T (x) out (mhc.py:366-381) with its
+    backward on the GPU (walsh_mhc_post_fwd / walsh_mhc_post_bwd)."""
+
+    @staticmethod
+    def forward(ctx, x, out, h_res, h_post):
+        ctx.save_for_backward(x, out, h_res, h_post)
+        return kernels.mhc_post(x, out, h_res, h_post)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, out, h_res, h_post = ctx.saved_tensors
+        dx, dout, dhr, dhq = kernels.mhc_post_bwd(x, out, h_res, h_post, g)
+        return dx, dout.to(out.dtype), dhr.to(h_res.dtype), dhq.to(h_post.dtype)
+
+
 class SinkhornFunction(torch.autograd.Function):
     """Sinkhorn projection with its backward on the GPU (walsh_sinkhorn_fwd /
     walsh_sinkhorn_bwd); the reference differentiates its torch loop
@@ -204,18 +236,11 @@ class mHCResidualStream(nn.Module):
         sk = self.H_res.sinkhorn
         h_res = _sinkhorn((self.H_res.alpha * d_res.reshape(B, T, n, n) + self.H_res.bias).float(), sk.n_iter,
                           sk.eps)
-        # the n x n mixing as float32 products rounded to the stream dtype
-        # (what the reference's autocast matmuls give); float32 keeps the
-        # batched products out of bf16 (see tracked_dtype)
-        dev = x.device.type
-        with torch.autocast(dev, dtype=torch.get_autocast_dtype(dev), enabled=False):
-            xw = x.float()
-            layer_in = torch.matmul(h_pre.float(), xw).squeeze(2).to(x.dtype)
+        # the n x n mixing on the GPU kernels (float32 sums, results in the
+        # stream dtype, as the reference's autocast matmuls give)
+        layer_in = StreamAggregateFunction.apply(x, h_pre)
         out = layer_fn(layer_in if norm is None else norm(layer_in))
-        with torch.autocast(dev, dtype=torch.get_autocast_dtype(dev), enabled=False):
-            res = torch.matmul(h_res.float(), xw)
-            post = h_post.transpose(-2, -1).float() * out.float().unsqueeze(2)
-        return res.to(x.dtype) + post.to(x.dtype)
+        return StreamUpdateFunction.apply(x, out, h_res, h_post)
 
     def forward(self, x, layer_fn):
         """x [B, T, n, C]; layer_fn maps [B, T, C] -> [B, T, C]."""
