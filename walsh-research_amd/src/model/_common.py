@@ -67,16 +67,3 @@ def adjacent_parts_view(parts, width: int):
     if p0.dim() >= 2 and p0.stride(-2) < full:
         return None
     return torch.as_strided(p0, p0.shape[:-1] + (full,), p0.stride(), p0.storage_offset())
-
-
-class NoBackward(torch.autograd.Function):
-    """Marks outputs of forward-only HIP ops: calling backward raises."""
-
-    @staticmethod
-    def forward(ctx, name, *tensors):
-        ctx.name = name
-        return tensors[0] if len(tensors) == 1 else tensors
-
-    @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError(f"{ctx.name}: this build implements the forward pass only")
