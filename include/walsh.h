@@ -277,6 +277,25 @@ int walsh_octonion_bwd_fold(const float *C, int64_t ldc, int64_t n_parts, int64_
                             int64_t in_o, int64_t out_o, const float *beta, const float *latent, float *dweight,
                             float *dbeta, void *stream);
 
+/* ------------------------------------------------------------------ decode attention
+ * CausalSelfAttention.forward with a KV cache at T == 1
+ * (src/model/chassis.py:441-478, cache :262-330): o = softmax(q K^T * scale) V
+ * over the L cached positions, no mask.
+ *
+ * walsh_decode_attention_workspace_bytes: float scratch for the split-K
+ *   partials of one call.
+ * walsh_decode_attention: q element (b, h, d) at b*q_bs + h*q_hs + d; cache
+ *   element (b, h, j, d) at b*kv_bs + h*kv_hs + j*kv_rs + d for k and v (the
+ *   KV cache's [batch, n_head, max_seq_len, head_dim] storage); o element
+ *   (b, h, d) at b*o_bs + h*o_hs + d.  head_dim D in {16, 32, 64, 128};
+ *   strides multiples of 8 elements, q / k / v 16-byte aligned.  dtype is
+ *   that of q, k, v and o; scores, softmax and sums in float32. */
+int64_t walsh_decode_attention_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t D);
+int walsh_decode_attention(const void *q, int64_t q_bs, int64_t q_hs, const void *k, const void *v, int64_t kv_bs,
+                           int64_t kv_hs, int64_t kv_rs, int64_t B, int64_t H, int64_t L, int64_t D, float scale,
+                           void *o, int64_t o_bs, int64_t o_hs, int dtype, void *workspace, int64_t workspace_bytes,
+                           void *stream);
+
 /* ------------------------------------------------------------------ A14-A17
  * mHC residual streams.  Stream tensors are [M tokens][n streams][C] with row
  * stride ldx >= n*C (elements); n <= 4 and C % 4 == 0 in this build.

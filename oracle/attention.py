@@ -1,0 +1,26 @@
+"""Oracle: decode attention over a KV cache.
+
+Test infrastructure only (see ``oracle/__init__.py``).
+
+``src/model/chassis.py:441-478`` with a cache (``:262-330``) at T == 1:
+F.scaled_dot_product_attention(q, k, v) without a mask, i.e. for every
+(sequence, head) o = softmax(q . k_j * scale over the L cached j) @ V with
+scale = 1/sqrt(head_dim).
+"""
+import math
+
+import numpy as np
+
+
+def decode_attention_f64(q, k, v, scale=None) -> np.ndarray:
+    """q [B, H, D], k / v [B, H, L, D] -> o [B, H, D] in float64."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    D = q.shape[-1]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    s = np.einsum('bhd,bhjd->bhj', q, k) * scale
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p = p / p.sum(axis=-1, keepdims=True)
+    return np.einsum('bhj,bhjd->bhd', p, v)

@@ -206,8 +206,12 @@ class CausalSelfAttention(nn.Module):
         drop = self.dropout if self.training else 0
         with _attention_backends(tracked and q.is_cuda and q.dtype != torch.float32):
             if kv_cache is not None and kv_cache.cached_len > 0 and T == 1:
-                # one new position attends to every cached one: no mask needed
-                y = F.scaled_dot_product_attention(q, k, v, dropout_p=drop)
+                # one new position attends to every cached one: no mask needed;
+                # the split-K decode kernel reads the cache in place
+                if not tracked and drop == 0 and kernels.decode_attention_supported(q, k, v):
+                    y = kernels.decode_attention(q, k, v)
+                else:
+                    y = F.scaled_dot_product_attention(q, k, v, dropout_p=drop)
             elif kv_cache is not None and kv_cache.cached_len > 0:
                 total = k.size(2)
                 mask = torch.ones(T, total, dtype=torch.bool, device=q.device).tril(diagonal=total - T)

@@ -463,6 +463,43 @@ def octonion_linear_bwd(x: torch.Tensor, gy: torch.Tensor, in_o: int, out_o: int
     return gx, dw, db
 
 
+# ------------------------------------------------------------------ decode attention
+
+DECODE_HEAD_DIMS = (16, 32, 64, 128)
+
+
+def decode_attention_supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """q [B, H, 1, D]; k, v [B, H, L, D] views with unit inner stride."""
+    if not (q.is_cuda and q.dim() == 4 and q.shape[2] == 1 and q.shape[-1] in DECODE_HEAD_DIMS):
+        return False
+    if q.dtype not in (torch.float32, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        return False
+    if k.stride() != v.stride() or k.stride(-1) != 1 or q.stride(-1) != 1 or k.shape != v.shape:
+        return False
+    ok = all(st % 8 == 0 for st in (q.stride(0), q.stride(1), k.stride(0), k.stride(1), k.stride(2)))
+    return ok and all(t.data_ptr() % 16 == 0 for t in (q, k, v))
+
+
+def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = None) -> torch.Tensor:
+    """softmax(q k^T * scale) v for one query per (sequence, head) over the
+    L cached positions (no mask): q [B, H, 1, D], k / v [B, H, L, D] (the KV
+    cache's head-major storage, read in place) -> [B, H, 1, D] in q.dtype."""
+    _hip.require_device(q, "query")
+    B, H, _, D = q.shape
+    L = k.shape[2]
+    scale = 1.0 / (D ** 0.5) if scale is None else scale
+    o = torch.empty(B, H, 1, D, device=q.device, dtype=q.dtype)
+    nws = _hip.lib().walsh_decode_attention_workspace_bytes(B, H, L, D)
+    ws = torch.empty(max(nws, 4) // 4, device=q.device, dtype=torch.float32)
+    esz = q.element_size()
+    _hip.call("walsh_decode_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+              k.stride(0), k.stride(1), k.stride(2), B, H, L, D, float(scale), o.data_ptr(), o.stride(0), o.stride(1),
+              _hip.dtype_code(q.dtype), ws.data_ptr(), nws, _hip.stream(q.device),
+              kernel="decode_attn_partial_kernel<%s,%d>" % ("bf16" if q.dtype == torch.bfloat16 else "f32", D),
+              nbytes=2 * B * H * L * D * esz + 2 * B * H * D * esz, flops=4 * B * H * L * D)
+    return o
+
+
 # ------------------------------------------------------------------ mHC
 
 def sinkhorn(h: torch.Tensor, n_iter: int = 20, eps: float = 1e-8) -> torch.Tensor:
