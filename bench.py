@@ -21,7 +21,9 @@ Other workloads (``--workload``), each printing one JSON line of its own:
             output gradient [8192, 512] (the headline model's layer shape),
             and a token sweep up to 262144 rows (rotated);
   train2    one training step of the headline model (bf16 autocast forward
-            with targets, backward, AdamW), batch x seq tokens.
+            with targets, backward, AdamW), batch x seq tokens;
+  walsh_load  a .walsh v4 file of config-5 ternary weights decoded on the
+            GPU straight into 2-bit packed buffers.
 
 Prints ONE JSON line.  Besides the timed region it
   * repeats the K steps with HIP events around every hot-path launch (on the
@@ -58,7 +60,7 @@ def parse():
     ap.add_argument("--no-roofline", action="store_true", help="skip the instrumented pass (profiling runs)")
     ap.add_argument("--workload", default="mhcwalsh",
                     choices=["mhcwalsh", "moe", "octonion", "hadamard", "prefill5", "decode5", "hadamard_bwd",
-                             "train2"])
+                             "train2", "walsh_load"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (reference for HBM byte counters)")
     return ap.parse_args()
@@ -150,7 +152,7 @@ def main():
     if args.workload != "mhcwalsh":
         line = {"moe": bench_moe, "octonion": bench_octonion, "hadamard": bench_hadamard, "prefill5": bench_prefill5,
                 "decode5": bench_decode5, "hadamard_bwd": bench_hadamard_bwd,
-                "train2": bench_train2}[args.workload](torch, args)
+                "train2": bench_train2, "walsh_load": bench_walsh_load}[args.workload](torch, args)
         print(json.dumps(line), flush=True)
         return
     _hip.lib()
@@ -522,6 +524,71 @@ def bench_train2(torch, args):
                  {"workload": "mHCWalsh training step, n_layer 16, n_head 32, n_embd 512, hadamard + head mixing, "
                               "4 mHC streams, MoE off, bf16 autocast, AdamW", "global_batch": args.batch,
                   "seq_len": args.seq, "parallelism": "single GPU"}, roof, cpu)
+
+
+def bench_walsh_load(torch, args):
+    """Loading a .walsh v4 file (compress.py format) of config-5 ternary
+    weights -- 24 layers of wq/wk/wv/wo [32, 128, 128] and gate/up
+    [32, 342, 128], down [32, 128, 342] latents -- straight into 2-bit packed
+    device buffers: the bitmask + sign decode runs on the GPU
+    (walsh_ternary_from_bitmask).  value = packed ternary bytes produced per
+    second by the decode kernels; the whole load (file read, host parse,
+    host-to-device copies, decode) is reported beside it."""
+    import tempfile
+    from src.model import _hip
+    from src.walsh_format import load_walsh, save_walsh
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    sd = {}
+    for l in range(24):
+        for n in ("wq", "wk", "wv", "wo"):
+            sd[f"layers.{l}.attention.{n}.inner.weight"] = torch.randn(32, 128, 128, device="cuda", generator=gen)
+        for n, shp in (("gate_proj", (32, 342, 128)), ("up_proj", (32, 342, 128)), ("down_proj", (32, 128, 342))):
+            sd[f"layers.{l}.feed_forward.{n}.inner.weight"] = torch.randn(*shp, device="cuda", generator=gen)
+    values = sum(t.numel() for t in sd.values())
+    path = os.path.join(tempfile.mkdtemp(), "config5.walsh")
+    save_walsh(path, sd, {"n_embd": 4096, "n_layer": 24})
+    fsize = os.path.getsize(path)
+    load_walsh(path, packed_ternary=True)          # warm up (allocator, file cache)
+    torch.cuda.synchronize()
+    steps = max(1, min(args.steps, 5))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out, _ = load_walsh(path, packed_ternary=True)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    with _hip.LaunchTimer() as lt:
+        for _ in range(steps):
+            load_walsh(path, packed_ternary=True)
+    k = lt.summary()["bitmask_decode"]
+    dec_ms = k["ms"] / steps
+    packed_bytes = sum(t.numel() for t in out.values())
+    roof = _roofline_of({"bitmask_decode": k}, steps)
+    roof["note"] = ("bytes per call: bitmask + sign bytes read, 2-bit packed bytes written; the three launches of "
+                    "one call (word counts + scan, block-sum scan, decode) timed together")
+    cpu = None
+    if not args.no_cpu:
+        import numpy as np
+        from oracle import ternary as otern
+        from oracle import walsh_format as owf
+        name = "layers.0.feed_forward.gate_proj.inner.weight"
+        codes = np.sign(sd[name].cpu().numpy()).astype(np.int8)
+        bm, sg, nnz = owf.encode_codes(codes)
+        reps, t1 = 0, time.perf_counter()
+        while time.perf_counter() - t1 < min(args.cpu_seconds, 10.0) or reps == 0:
+            otern.pack_codes(owf.decode_codes(bm, sg, codes.shape, nnz))
+            reps += 1
+        el = time.perf_counter() - t1
+        cpu = dict(value=round(reps * codes.size / 4 / el / 1e9, 4), unit="GB/s of packed output", cores=1,
+                   kind="port", sample=f"{reps} decodes of one [32, 342, 128] tensor (numpy restatement of "
+                                       f"generate_compressed.py:70-105, then the 2-bit pack), {el:.1f} s")
+    line = _line("packed ternary bytes per second decoded from .walsh v4 on 1 GPU", packed_bytes / (dec_ms * 1e-3) / 1e9,
+                 "GB/s", steps, 1, dec_ms, "u8", "synthetic: N(0,1) latents, absmean codes (about 1/3 zeros)",
+                 {"workload": ".walsh v4 load, config-5 ternary weights (24 layers x 7 matrices, "
+                              f"{values / 1e6:.0f} M values, file {fsize / 1e6:.1f} MB)", "global_batch": 1,
+                  "seq_len": 0, "parallelism": "single GPU"}, roof, cpu)
+    line["whole_load_ms"] = round(dt * 1e3, 2)
+    line["decode_kernel_ms"] = round(dec_ms, 3)
+    return line
 
 
 def _config5(torch, block_size):

@@ -94,6 +94,20 @@ int walsh_ternary_quantize(const float *w, int64_t rows, int64_t K, const float 
  *     out = clamp(grad, -2, 2) (w unused, may be NULL). */
 int walsh_ternary_ste_bwd(const float *grad, const float *w, int64_t n, int mode, float *out, void *stream);
 
+/* walsh_bitmask_workspace_bytes / walsh_ternary_from_bitmask: decode the
+ *   .walsh v4 bitmask + sign storage of a ternary tensor (written by
+ *   compress.py:36-93, read by generate_compressed.py:70-105) on the GPU,
+ *   straight into the 2-bit packed layout and/or int8 codes of the tensor
+ *   viewed as [rows, K] (K = last dim):
+ *     bitmask: bit p (LSB first) set <=> value p is non-zero;
+ *     sign_bits: bit r set <=> the r-th non-zero is +1 (clear: -1);
+ *   non-zeros past num_nonzero decode as 0, as the reference loader leaves
+ *   them.  rows*K < 2^32; workspace: walsh_bitmask_workspace_bytes(rows*K). */
+int64_t walsh_bitmask_workspace_bytes(int64_t total);
+int walsh_ternary_from_bitmask(const uint8_t *bitmask, int64_t bitmask_bytes, const uint8_t *sign_bits,
+                               int64_t sign_bytes, int64_t num_nonzero, int64_t rows, int64_t K, uint8_t *packed,
+                               int8_t *codes, void *workspace, int64_t workspace_bytes, void *stream);
+
 /* walsh_ternary_unpack: inverse of the packed layout -> int8 codes [rows, K]
  *   (unpack_ternary_weights, src/model/fht_cuda.py:96-117). */
 int walsh_ternary_unpack(const uint8_t *packed, int64_t rows, int64_t K, int8_t *codes,

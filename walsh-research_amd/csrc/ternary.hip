@@ -93,6 +93,112 @@ static int grid_for(int64_t work, int block) {
     return (int)(g < 1 ? 1 : g);
 }
 
+// ---------------------------------------------------------------- .walsh v4 bitmask + sign
+// A ternary tensor of `total` values stored as a bitmask (bit p of the
+// little-endian bit stream: value p is non-zero) and a sign stream (bit r:
+// the r-th non-zero is +1 when set, -1 when clear) (compress.py:36-93,
+// generate_compressed.py:70-105).  The value at position p is therefore
+// sign[rank(p)] with rank(p) = the number of set mask bits before p, a prefix
+// popcount.  Three passes over 32-bit mask words: per-word counts with a
+// workgroup exclusive scan, a scan of the workgroup sums, then the decode,
+// one output byte (4 codes of the 2-bit packed layout) per thread.
+constexpr int kMaskWordsPerBlock = 256;
+
+__device__ __forceinline__ uint32_t mask_word(const uint8_t *__restrict__ m, int64_t nb, int64_t w) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t b = 4 * w + i;
+        if (b < nb) v |= (uint32_t)m[b] << (8 * i);
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(kMaskWordsPerBlock) void bitmask_count_kernel(const uint8_t *__restrict__ mask, int64_t nb,
+                                                                           int64_t nwords, int64_t total,
+                                                                           uint32_t *__restrict__ word_pref,
+                                                                           uint32_t *__restrict__ block_sum) {
+    __shared__ uint32_t sc[kMaskWordsPerBlock];
+    const int t = threadIdx.x;
+    const int64_t w = (int64_t)blockIdx.x * kMaskWordsPerBlock + t;
+    uint32_t c = 0;
+    if (w < nwords) {
+        uint32_t v = mask_word(mask, nb, w);
+        const int64_t valid = total - 32 * w;  // bits past `total` are ignored
+        if (valid < 32) v &= (1u << valid) - 1u;
+        c = (uint32_t)__popc(v);
+    }
+    sc[t] = c;
+    __syncthreads();
+    for (int off = 1; off < kMaskWordsPerBlock; off <<= 1) {  // inclusive Hillis-Steele scan
+        const uint32_t add = t >= off ? sc[t - off] : 0u;
+        __syncthreads();
+        sc[t] += add;
+        __syncthreads();
+    }
+    if (w < nwords) word_pref[w] = sc[t] - c;
+    if (t == kMaskWordsPerBlock - 1) block_sum[blockIdx.x] = sc[t];
+}
+
+// Exclusive scan of the workgroup sums in place, one workgroup, chunks of 1024.
+__global__ __launch_bounds__(1024) void bitmask_scan_kernel(uint32_t *__restrict__ block_sum, int64_t nblk) {
+    __shared__ uint32_t sc[1024];
+    __shared__ uint32_t carry;
+    const int t = threadIdx.x;
+    if (t == 0) carry = 0;
+    __syncthreads();
+    for (int64_t base = 0; base < nblk; base += 1024) {
+        const int64_t i = base + t;
+        const uint32_t c = i < nblk ? block_sum[i] : 0u;
+        sc[t] = c;
+        __syncthreads();
+        for (int off = 1; off < 1024; off <<= 1) {
+            const uint32_t add = t >= off ? sc[t - off] : 0u;
+            __syncthreads();
+            sc[t] += add;
+            __syncthreads();
+        }
+        if (i < nblk) block_sum[i] = carry + sc[t] - c;
+        __syncthreads();
+        if (t == 1023) carry += sc[1023];
+        __syncthreads();
+    }
+}
+
+__global__ void bitmask_decode_kernel(const uint8_t *__restrict__ mask, int64_t nb, const uint8_t *__restrict__ sign,
+                                      int64_t ns, int64_t nnz, const uint32_t *__restrict__ word_pref,
+                                      const uint32_t *__restrict__ block_pref, int64_t rows, int64_t K,
+                                      uint8_t *__restrict__ packed, int8_t *__restrict__ codes) {
+    const int64_t kp4 = ceil_div(K, 4);
+    const int64_t total_b = rows * kp4;
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < total_b;
+         b += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = b / kp4;
+        const int64_t k0 = (b - r * kp4) * 4;
+        uint32_t byte = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t k = k0 + j;
+            int c = 0;
+            if (k < K) {
+                const int64_t p = r * K + k;
+                const int64_t w = p >> 5;
+                const int bit = (int)(p & 31);
+                const uint32_t v = mask_word(mask, nb, w);
+                if ((v >> bit) & 1u) {
+                    const int64_t rank = (int64_t)block_pref[w / kMaskWordsPerBlock] + word_pref[w] +
+                                         __popc(v & ((1u << bit) - 1u));
+                    // non-zeros past num_nonzero keep the value 0, as the reference loader does
+                    if (rank < nnz && (rank >> 3) < ns) c = ((sign[rank >> 3] >> (rank & 7)) & 1u) ? 1 : -1;
+                }
+                if (codes) codes[p] = (int8_t)c;
+            }
+            byte |= (uint32_t)(c + 1) << (6 - 2 * j);
+        }
+        if (packed) packed[b] = (uint8_t)byte;
+    }
+}
+
 // Straight-through estimators' backward, elementwise over n weights:
 //   mode 0 (physics.quantize_ternary, physics.py:43-50): the value
 //     w_clamped + (w_quant - w_clamped).detach() passes gradient only through
@@ -158,4 +264,38 @@ WALSH_EXPORT int walsh_ternary_unpack(const uint8_t *packed, int64_t rows, int64
     const int grid = grid_for(rows * K, block);
     launch(unpack_kernel, dim3(grid), dim3(block), 0, (hipStream_t)stream, packed, rows, K, codes);
     return check_hip(hipGetLastError(), "walsh_ternary_unpack launch");
+}
+
+WALSH_EXPORT int64_t walsh_bitmask_workspace_bytes(int64_t total) {
+    if (total <= 0) return 0;
+    const int64_t nwords = ceil_div(total, 32), nblk = ceil_div(nwords, kMaskWordsPerBlock);
+    return (nwords + nblk) * (int64_t)sizeof(uint32_t);
+}
+
+WALSH_EXPORT int walsh_ternary_from_bitmask(const uint8_t *bitmask, int64_t bitmask_bytes, const uint8_t *sign_bits,
+                                            int64_t sign_bytes, int64_t num_nonzero, int64_t rows, int64_t K,
+                                            uint8_t *packed, int8_t *codes, void *workspace, int64_t workspace_bytes,
+                                            void *stream) {
+    const char *fn = "walsh_ternary_from_bitmask";
+    if (rows <= 0 || K <= 0 || bitmask_bytes < 0 || sign_bytes < 0 || num_nonzero < 0)
+        return set_error(WALSH_EINVAL, "%s: bad sizes", fn);
+    const int64_t total = rows * K;
+    if (total >= (int64_t)1 << 32) return set_error(WALSH_ENOTSUP, "%s: more than 2^32 values", fn);
+    if ((!bitmask && bitmask_bytes) || (!sign_bits && sign_bytes) || (!packed && !codes))
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    const int64_t need = walsh_bitmask_workspace_bytes(total);
+    if (!workspace || workspace_bytes < need)
+        return set_error(WALSH_EINVAL, "%s: workspace of %lld bytes < %lld", fn, (long long)workspace_bytes,
+                         (long long)need);
+    const int64_t nwords = ceil_div(total, 32), nblk = ceil_div(nwords, kMaskWordsPerBlock);
+    uint32_t *word_pref = (uint32_t *)workspace;
+    uint32_t *block_pref = word_pref + nwords;
+    hipStream_t s = (hipStream_t)stream;
+    launch(bitmask_count_kernel, dim3((unsigned)nblk), dim3(kMaskWordsPerBlock), 0, s, bitmask, bitmask_bytes, nwords,
+           total, word_pref, block_pref);
+    launch(bitmask_scan_kernel, dim3(1), dim3(1024), 0, s, block_pref, nblk);
+    const int block = 256;
+    launch(bitmask_decode_kernel, dim3(grid_for(rows * ceil_div(K, 4), block)), dim3(block), 0, s, bitmask,
+           bitmask_bytes, sign_bits, sign_bytes, num_nonzero, word_pref, block_pref, rows, K, packed, codes);
+    return check_hip(hipGetLastError(), fn);
 }

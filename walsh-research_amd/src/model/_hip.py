@@ -32,6 +32,8 @@ SIGNATURES = {
     "walsh_ternary_quantize": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
     "walsh_ternary_unpack": (_I, [_P, _I64, _I64, _P, _P]),
     "walsh_ternary_ste_bwd": (_I, [_P, _P, _I64, _I, _P, _P]),
+    "walsh_bitmask_workspace_bytes": (_I64, [_I64]),
+    "walsh_ternary_from_bitmask": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "walsh_hadamard_weight_bytes": (_I64, [_I64, _I64]),
     "walsh_hadamard_prepare": (_I, [_P, _I64, _I64, _P, _P]),
     "walsh_hadamard_linear_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I, _P]),

@@ -213,6 +213,78 @@ class HadamardTernaryLinearTuple(nn.Module):
         return tuple(y.split(self.out_o, dim=-1))
 
 
+class HadamardPackedLinear(nn.Module):
+    """Inference Hadamard linear holding 2-bit packed codes (fht_cuda.py:751-840):
+    buffer ``weight_packed`` [32, out_o, ceil(in_o/4)] uint8 in the
+    pack_ternary_weights layout, ``H`` as there, and the trained layer's
+    diagonals.  Two defects of the reference class are fixed: ``beta`` keeps
+    the trained layer's [32, out_o] shape (the reference holds [out_o] and
+    repeats it over the groups, :780, :838-840) and ``alpha`` [32, in_o] is
+    applied (the reference drops it, :806, :826-835), so the result equals
+    HadamardLinear.forward on the same codes.  Runs the forward kernel on a
+    layout prepared once per weight_packed version."""
+
+    ALGEBRA_DIM = ALGEBRA_DIM
+
+    def __init__(self, in_features: int, out_features: int):
+        super().__init__()
+        assert in_features % ALGEBRA_DIM == 0 and out_features % ALGEBRA_DIM == 0
+        self.in_o = in_features // ALGEBRA_DIM
+        self.out_o = out_features // ALGEBRA_DIM
+        self.in_features = in_features
+        self.out_features = out_features
+        self.register_buffer('weight_packed', torch.zeros(ALGEBRA_DIM, self.out_o, (self.in_o + 3) // 4,
+                                                          dtype=torch.uint8))
+        self.register_buffer('alpha', torch.ones(ALGEBRA_DIM, self.in_o))
+        self.register_buffer('beta', torch.ones(ALGEBRA_DIM, self.out_o))
+        self.register_buffer('H', hadamard_matrix(ALGEBRA_DIM, normalize=True))
+        self._wcache = WeightCache()
+
+    @classmethod
+    def from_trained(cls, trained_layer) -> 'HadamardPackedLinear':
+        """Packed copy of a trained HadamardLinear / HadamardTernaryLinear."""
+        layer = getattr(trained_layer, 'inner', trained_layer)
+        packed = cls(layer.in_o * ALGEBRA_DIM, layer.out_o * ALGEBRA_DIM).to(layer.weight.device)
+        _, pk, _ = layer.ternary_state()
+        packed.weight_packed.copy_(pk)
+        packed.alpha.copy_(layer.alpha.detach())
+        packed.beta.copy_(layer.beta.detach())
+        return packed
+
+    def ternary_state(self):
+        """(None, packed codes, kernel layout): the HadamardLinear interface."""
+        wp = self.weight_packed
+        return self._wcache.get([wp], lambda: (None, wp, kernels.hadamard_prepare(wp, self.in_o, self.out_o)))
+
+    def _needs_grad(self, x: torch.Tensor) -> bool:
+        return False
+
+    def _apply_2d(self, x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        _, _, kw = self.ternary_state()
+        return kernels.hadamard_linear(x if x.dtype == dtype else x.to(dtype), self.in_o, self.out_o, kw,
+                                       self.alpha, self.beta)
+
+    apply_rows = _apply_2d
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        assert x.shape[-1] == self.in_features, f"expected last dim {self.in_features}, got {x.shape[-1]}"
+        return self._apply_2d(x, act_dtype(x)).to(x.dtype)
+
+
+def optimize_for_inference(model: nn.Module) -> nn.Module:
+    """Swap every HadamardLinear / HadamardTernaryLinear (also the inner layer
+    of a HadamardTernaryLinearTuple) for a HadamardPackedLinear with the same
+    codes and diagonals, in place (fht_cuda.py:843-866)."""
+    def replace(module):
+        for name, child in module.named_children():
+            if isinstance(child, _HadamardBase):
+                setattr(module, name, HadamardPackedLinear.from_trained(child))
+            else:
+                replace(child)
+    replace(model)
+    return model
+
+
 def fht_butterfly(x: torch.Tensor) -> torch.Tensor:
     """Normalised fast Hadamard transform along the last dim (any power of
     two N <= 16384), fht_cuda.py:281-309, on the GPU."""

@@ -96,6 +96,36 @@ def ternary_ste_bwd(grad: torch.Tensor, w: torch.Tensor = None, mode: int = 1) -
     return out
 
 
+def ternary_from_bitmask(bitmask: torch.Tensor, sign_bits: torch.Tensor, num_nonzero: int, shape,
+                         packed: bool = True, codes: bool = False) -> dict:
+    """Decode a .walsh v4 bitmask + sign tensor (uint8 device buffers) on
+    the GPU into the 2-bit packed layout [.., ceil(K/4)] and/or int8 codes of
+    ``shape`` (generate_compressed.py:70-105 semantics)."""
+    _hip.require_device(bitmask, "bitmask")
+    shape = tuple(int(d) for d in shape)
+    K = shape[-1]
+    rows = 1
+    for d in shape[:-1]:
+        rows *= d
+    dev = bitmask.device
+    out = {}
+    pk = torch.empty(shape[:-1] + ((K + 3) // 4,), device=dev, dtype=torch.uint8) if packed else None
+    cd = torch.empty(shape, device=dev, dtype=torch.int8) if codes else None
+    nws = _hip.lib().walsh_bitmask_workspace_bytes(rows * K)
+    ws = torch.empty(max(nws, 4), device=dev, dtype=torch.uint8)
+    bm = bitmask.contiguous()
+    sg = sign_bits.contiguous()
+    _hip.call("walsh_ternary_from_bitmask", bm.data_ptr() if bm.numel() else 0, bm.numel(),
+              sg.data_ptr() if sg.numel() else 0, sg.numel(), int(num_nonzero), rows, K,
+              0 if pk is None else pk.data_ptr(), 0 if cd is None else cd.data_ptr(), ws.data_ptr(), nws,
+              _hip.stream(dev), kernel="bitmask_decode", nbytes=bm.numel() + sg.numel() + rows * ((K + 3) // 4))
+    if pk is not None:
+        out["packed"] = pk
+    if cd is not None:
+        out["codes"] = cd
+    return out
+
+
 def ternary_unpack(packed: torch.Tensor, K: int) -> torch.Tensor:
     """int8 codes [.., K] from the 2-bit layout (fht_cuda.py:96-117)."""
     _hip.require_device(packed, "packed")
