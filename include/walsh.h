@@ -163,6 +163,18 @@ int walsh_hadamard_linear_rope_fwd(const void *x, int64_t ldx, int64_t M, int64_
                                    const uint8_t *kweight, const float *alpha, const float *beta, const float *rope,
                                    int64_t rope_T, int64_t head_dim, void *y, int64_t ldy, int dtype, void *stream);
 
+/* walsh_hadamard_linear_multi_fwd: n (<= 4) Hadamard linears of one shape on
+ *   the same input rows x, in one launch where the shape allows (the q, k and
+ *   v projections of CausalSelfAttention.forward, chassis.py:441-452): layer i
+ *   uses kweights[i], alphas[i], betas[i] and writes ys[i] (row stride ldy);
+ *   layers with bit i of rope_mask also apply the rotary embedding of
+ *   walsh_hadamard_linear_rope_fwd (rope, rope_T, head_dim).  Shapes the
+ *   single-tile kernel does not take run as n launches. */
+int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o, int64_t n,
+                                    const uint8_t *const *kweights, const float *const *alphas,
+                                    const float *const *betas, void *const *ys, int64_t ldy, const float *rope,
+                                    int64_t rope_T, int64_t head_dim, int rope_mask, int dtype, void *stream);
+
 /* walsh_hadamard_swiglu_fwd: h = silu(gate(x)) * up(x) for two Hadamard
  *   linears of the same shape (in_o -> hid_o) on the same input, fused
  *   (SwiGLUMLP.forward, src/model/chassis.py:498-504, gate_proj/up_proj).

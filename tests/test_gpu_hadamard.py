@@ -346,3 +346,28 @@ def test_head_mixer_wide_bf16(K, B, T, D):
     Wq = Wt.to(torch.bfloat16).float().cpu().numpy()
     ref = ohad.head_mixer_f64(xt.float().cpu().numpy(), Wq, beta).transpose(0, 2, 1, 3).reshape(B, T, 32 * D)
     assert_close(y.float().cpu().numpy(), ref, torch.bfloat16, f"wide mixer B={B} T={T} D={D}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("in_o,out_o,T", [(16, 16, 1024), (16, 16, 37), (64, 64, 20)])
+def test_hadamard_linear_multi_equals_single_launches(K, dtype, in_o, out_o, T):
+    """walsh_hadamard_linear_multi_fwd (q, k with RoPE, v in one launch) is
+    bitwise the three single-layer calls."""
+    torch.manual_seed(in_o + T)
+    B, D = 2, 16
+    x = torch.randn(B, T, 32 * in_o, device="cuda").to(dtype)
+    f = _freqs_cis(T, D).cuda()
+    layers, singles = [], []
+    for i, rope in enumerate((True, True, False)):
+        w = torch.randn(32, out_o, in_o) * 0.02
+        q = K.ternary_quantize(w.cuda(), packed=True)
+        kw = K.hadamard_prepare(q["packed"], in_o, out_o)
+        a = (1 + 0.3 * torch.randn(32, in_o)).cuda()
+        b = (0.2 * torch.randn(32, out_o)).cuda()
+        layers.append((kw, a, b, rope))
+        singles.append(K.hadamard_linear_rope(x, in_o, out_o, kw, a, b, f, D) if rope
+                       else K.hadamard_linear(x, in_o, out_o, kw, a, b))
+    outs = K.hadamard_linear_multi(x, in_o, out_o, layers, f, D)
+    torch.cuda.synchronize()
+    for o, s in zip(outs, singles):
+        assert torch.equal(o, s)

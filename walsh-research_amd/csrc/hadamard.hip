@@ -53,8 +53,8 @@ __global__ void hadamard_prepare_kernel(const uint8_t *__restrict__ packed, int 
 // DENSE: float weights instead of ternary codes (the Hadamard head mixer),
 // as matrix-core A fragments [Nt][Kc][32 g][64 lanes] (bf16x4 or f32x4)
 // copied into LDS in place of the code table.
-template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE = false>
-__global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void hadamard_fwd_kernel(HadArgs a) {
+template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE>
+__device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int nblk) {
     extern __shared__ __align__(16) unsigned char smem[];
     void *lut = smem;
     const size_t wbytes = DENSE ? (size_t)a.Nt * a.Kc * 32 * 64 * dense_frag_bytes<BF16MMA>() : lut_bytes<BF16MMA>();
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a, esz));
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * esz));
     const int n_tiles = (int)ceil_div(a.M, kTile);
-    const int stride = gridDim.x * kWaves;
+    const int stride = nblk * kWaves;
     auto contract_any = [&](int nt, int c, const XM<BF16MMA> &xm, f32x4 (&acc)[32]) {
         if constexpr (DENSE)
             contract_dense<BF16MMA>(smem + ((size_t)(nt * a.Kc + c) * 32 * 64 + lane) * dense_frag_bytes<BF16MMA>(),
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
             contract<BF16MMA>(a, nt, c, lane, xm, lut, acc);
     };
 
-    for (int tile = blockIdx.x * kWaves + wave; tile < n_tiles; tile += stride) {
+    for (int tile = blk * kWaves + wave; tile < n_tiles; tile += stride) {
         const int row = tile * kTile + t;
         const bool row_ok = row < a.M;
         const uint32_t xoff = row_ok ? x_row_off(a, row, esz) : 0u;
@@ -144,6 +144,27 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
             }
         }
     }
+}
+
+template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE = false>
+__global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void hadamard_fwd_kernel(HadArgs a) {
+    hadamard_fwd_body<T, BF16MMA, VEC, KC1, DENSE>(a, blockIdx.x, gridDim.x);
+}
+
+// Several Hadamard linears of one shape on the same input rows in one launch
+// (the q, k and v projections): workgroup b runs layer b % n over the tiles
+// of slot b / n, so the n layers' waves fill the machine together and the
+// shared input is fetched from HBM once (later reads hit the caches).
+constexpr int kMaxMulti = 4;
+struct HadArgsN {
+    HadArgs p[kMaxMulti];
+    int n;
+};
+
+template <typename T, bool BF16MMA, bool VEC, bool KC1>
+__global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void hadamard_fwdn_kernel(HadArgsN an) {
+    const int l = blockIdx.x % an.n;
+    hadamard_fwd_body<T, BF16MMA, VEC, KC1, false>(an.p[l], blockIdx.x / an.n, gridDim.x / an.n);
 }
 
 // ---------------------------------------------------------------- wide layers
@@ -1048,6 +1069,75 @@ WALSH_EXPORT int walsh_hadamard_linear_rope_fwd(const void *x, int64_t ldx, int6
     a.rope_T = (int)rope_T;
     a.rope_D = (int)head_dim;
     return hadamard_launch(fn, a, nullptr, M, dtype == WALSH_BF16, (hipStream_t)stream);
+}
+
+WALSH_EXPORT int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                                                 int64_t n, const uint8_t *const *kweights, const float *const *alphas,
+                                                 const float *const *betas, void *const *ys, int64_t ldy,
+                                                 const float *rope, int64_t rope_T, int64_t head_dim, int rope_mask,
+                                                 int dtype, void *stream) {
+    const char *fn = "walsh_hadamard_linear_multi_fwd";
+    if (n < 1 || n > kMaxMulti || !kweights || !alphas || !betas || !ys)
+        return set_error(WALSH_EINVAL, "%s: n=%lld (1..%d) or null array", fn, (long long)n, kMaxMulti);
+    if (rope_mask & ~((1 << n) - 1)) return set_error(WALSH_EINVAL, "%s: rope_mask 0x%x past n", fn, rope_mask);
+    HadArgs base[kMaxMulti];
+    for (int i = 0; i < n; ++i) {
+        int rc = hadamard_check(fn, x, ldx, in_o, M, in_o, out_o, ys[i], ldy, out_o, dtype);
+        if (rc) return rc;
+        if (!kweights[i] || !alphas[i] || !betas[i]) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+        base[i] = had_args(x, ldx, in_o, in_o, out_o, kweights[i], alphas[i], betas[i], ys[i], ldy, out_o);
+        if (rope_mask & (1 << i)) {
+            if (!rope || rope_T < 1 || head_dim < 4 || head_dim % 4 || out_o % head_dim || (uintptr_t)rope % 16)
+                return set_error(WALSH_ENOTSUP, "%s: RoPE needs head_dim %% 4 == 0 dividing out_o, 16-byte aligned "
+                                 "table", fn);
+            base[i].rope = rope;
+            base[i].rope_T = (int)rope_T;
+            base[i].rope_D = (int)head_dim;
+        }
+    }
+    if (M == 0) return WALSH_OK;
+    const bool bf16 = dtype == WALSH_BF16;
+    const int64_t esz = bf16 ? 2 : 4;
+    const size_t valign = bf16 ? 8 : 16;
+    const int Nt = base[0].Nt, Kc = base[0].Kc;
+    bool vec = in_o % 4 == 0 && out_o % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && (uintptr_t)x % valign == 0;
+    for (int i = 0; i < n; ++i) vec = vec && (uintptr_t)ys[i] % valign == 0;
+    const bool kc1 = Kc == 1 && (bf16 || Nt == 1);
+    const size_t lds = hadamard_lds_bytes(bf16, Kc, Nt);
+    hipStream_t s = (hipStream_t)stream;
+    if (!kc1 || !vec || lds > (size_t)device_info().max_shared_per_block) {
+        // shapes served by the other kernels: one launch per layer
+        for (int i = 0; i < n; ++i) {
+            const int rc = hadamard_launch(fn, base[i], nullptr, M, bf16, s);
+            if (rc) return rc;
+        }
+        return WALSH_OK;
+    }
+    const int64_t ld = ldx > ldy ? ldx : ldy;
+    int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / kTile * kTile;
+    if (rows_max < kTile) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
+    rows_max = balanced_rows(M, rows_max, kTile);
+    const int64_t cap = (int64_t)device_info().cu_count * 2;
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        HadArgsN an;
+        an.n = (int)n;
+        for (int i = 0; i < n; ++i) {
+            an.p[i] = base[i];
+            an.p[i].x = (const char *)x + r0 * ldx * esz;
+            an.p[i].y = (char *)ys[i] + r0 * ldy * esz;
+            an.p[i].M = (int)rows;
+            an.p[i].rope_row0 = (int)(r0 % base[i].rope_T);
+        }
+        int64_t grid = ceil_div(ceil_div(rows, kTile), kWaves);
+        if (grid > cap) grid = cap;
+        const dim3 G((unsigned)(grid * n)), B(kThreads);
+        if (bf16) launch((hadamard_fwdn_kernel<uint16_t, true, true, true>), G, B, lds, s, an);
+        else launch((hadamard_fwdn_kernel<float, false, true, true>), G, B, lds, s, an);
+        const int rc = check_hip(hipGetLastError(), fn);
+        if (rc) return rc;
+    }
+    return WALSH_OK;
 }
 
 WALSH_EXPORT int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t gsx, int64_t M, int64_t in_o,

@@ -42,6 +42,8 @@ SIGNATURES = {
                                        _I, _P]),
     "walsh_fht_fwd": (_I, [_P, _I64, _I64, _I, _P, _I, _P]),
     "walsh_hadamard_linear_rope_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I, _P]),
+    "walsh_hadamard_linear_multi_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _I64, _I64,
+                                             _I, _I, _P]),
     "walsh_hadamard_dense_weight_bytes": (_I64, [_I64, _I64, _I]),
     "walsh_hadamard_dense_prepare": (_I, [_P, _I64, _I64, _I, _I, _P, _P]),
     "walsh_head_mixer_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I, _P]),

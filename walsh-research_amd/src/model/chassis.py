@@ -141,6 +141,17 @@ class OctonionHeadMixer(OctonionHeadMixerFused):
     """chassis.py:347-399: same parameters and result as the fused mixer."""
 
 
+def _qkv_layers(attn):
+    """The inner Hadamard layers of wq, wk, wv when all three are Hadamard
+    tuples of one shape (else None)."""
+    inner = [getattr(m, "inner", None) for m in (attn.wq, attn.wk, attn.wv)]
+    if any(i is None or not hasattr(i, "ternary_state") for i in inner):
+        return None
+    if len({(i.in_o, i.out_o) for i in inner}) != 1:
+        return None
+    return inner
+
+
 def _attention_backends(tracked: bool):
     """Under autograd with 16-bit operands, scaled_dot_product_attention may
     use only the fused flash / memory-efficient kernels: the math
@@ -178,16 +189,32 @@ class CausalSelfAttention(nn.Module):
         self.dropout = config.dropout
         self.head_mixer = get_head_mixer(config, self.head_dim)
 
+    def _qkv_multi(self, x, freqs_cis, T):
+        """q (roped), k (roped), v in one launch (walsh_hadamard_linear_multi_fwd),
+        or None when the layers, shapes or autograd do not allow it."""
+        inner = _qkv_layers(self)
+        if inner is None or x.dim() != 3 or freqs_cis.shape[0] < T:
+            return None
+        if any(i._needs_grad(x) for i in inner) or not kernels.rope_supported(x, inner[0].out_o, self.head_dim):
+            return None
+        layers = [(i.ternary_state()[2], i.alpha, i.beta, r) for i, r in zip(inner, (True, True, False))]
+        return kernels.hadamard_linear_multi(x, inner[0].in_o, inner[0].out_o, layers, freqs_cis, self.head_dim)
+
     def forward(self, x, freqs_cis, kv_cache: Optional[KVCache] = None, layer_idx: int = 0):
         B, T, C = x.size()
         dt = act_dtype(x)
         x = x.to(dt)
         q = k = None
-        if hasattr(self.wq, "forward_full_rope") and freqs_cis.shape[0] >= T:
+        fused = self._qkv_multi(x, freqs_cis, T)
+        if fused is not None:
+            q, k, v = (t.view(B, T, self.n_head, self.head_dim) for t in fused)
+        elif hasattr(self.wq, "forward_full_rope") and freqs_cis.shape[0] >= T:
             # the rotary embedding rides on the q and k projections' stores
             q = self.wq.forward_full_rope(x, freqs_cis, self.head_dim)
             k = self.wk.forward_full_rope(x, freqs_cis, self.head_dim) if q is not None else None
-        if q is not None and k is not None:
+        if fused is not None:
+            pass
+        elif q is not None and k is not None:
             q = q.view(B, T, self.n_head, self.head_dim)
             k = k.view(B, T, self.n_head, self.head_dim)
             v = _full(self.wv, x).view(B, T, self.n_head, self.head_dim)

@@ -200,6 +200,51 @@ def hadamard_linear_rope(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.
     return y
 
 
+def hadamard_linear_multi(x: torch.Tensor, in_o: int, out_o: int, layers, freqs_cis: torch.Tensor = None,
+                          head_dim: int = None):
+    """Several Hadamard linears of one shape on the same rows x [B, T, C] in
+    one launch: ``layers`` = [(kweight, alpha, beta, rope)], rope True applies
+    the rotary embedding (freqs_cis rows, head_dim) on that layer's store.
+    Returns the outputs [B, T, 32*out_o] in x.dtype."""
+    import ctypes
+    _hip.require_device(x, "input")
+    n = len(layers)
+    dt = x.dtype
+    B, T = x.shape[0], x.shape[1]
+    xv, rows, ldx = _rows_view(x, 32 * in_o)
+    if xv.data_ptr() % (4 * x.element_size()) or ldx % 4:
+        xv = xv.contiguous()
+        ldx = xv.stride(0)
+    ys = [torch.empty(x.shape[:-1] + (32 * out_o,), device=x.device, dtype=dt) for _ in range(n)]
+    if rows == 0:
+        return ys
+    keep = []
+    kws, als, bes, yps = [], [], [], []
+    mask = 0
+    for i, (kw, a, b, rope) in enumerate(layers):
+        a = a.detach().float().contiguous()
+        b = b.detach().float().contiguous()
+        keep += [a, b]
+        kws.append(kw.data_ptr())
+        als.append(a.data_ptr())
+        bes.append(b.data_ptr())
+        yps.append(ys[i].data_ptr())
+        mask |= (1 << i) if rope else 0
+    table = None
+    if mask:
+        table = torch.view_as_real(freqs_cis[:T].contiguous())
+        assert table.shape == (T, head_dim // 2, 2) and table.dtype == torch.float32, "freqs_cis shape"
+    arrs = [(ctypes.c_void_p * n)(*v) for v in (kws, als, bes, yps)]
+    kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, True, in_o <= 16)
+    nbytes = rows * 32 * (in_o + n * out_o) * x.element_size()
+    _hip.call("walsh_hadamard_linear_multi_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, n,
+              *[ctypes.addressof(a) for a in arrs], 32 * out_o, 0 if table is None else table.data_ptr(),
+              T, head_dim or 4, mask, _hip.dtype_code(dt), _hip.stream(x.device),
+              kernel="hadamard_fwdn_kernel<%s,x%d>" % ("bf16" if dt == torch.bfloat16 else "f32", n),
+              nbytes=nbytes, flops=flops * n)
+    return ys
+
+
 def hadamard_linear(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tensor, alpha: torch.Tensor,
                     beta: torch.Tensor, out_dtype: torch.dtype = None, gsx: int = None,
                     gsy: int = None) -> torch.Tensor:
