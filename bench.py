@@ -23,7 +23,10 @@ Other workloads (``--workload``), each printing one JSON line of its own:
   train2    one training step of the headline model (bf16 autocast forward
             with targets, backward, AdamW), batch x seq tokens;
   walsh_load  a .walsh v4 file of config-5 ternary weights decoded on the
-            GPU straight into 2-bit packed buffers.
+            GPU straight into 2-bit packed buffers;
+  chanmod   the block's channel modulation x + cm(RMSNorm(x)) on the
+            headline model's streams ([8, 1024, 4, 512] bf16, viewed as 32
+            groups of 1024 rows), and a sweep with rotated buffers.
 
 Prints ONE JSON line.  Besides the timed region it
   * repeats the K steps with HIP events around every hot-path launch (on the
@@ -60,7 +63,7 @@ def parse():
     ap.add_argument("--no-roofline", action="store_true", help="skip the instrumented pass (profiling runs)")
     ap.add_argument("--workload", default="mhcwalsh",
                     choices=["mhcwalsh", "moe", "octonion", "hadamard", "prefill5", "decode5", "hadamard_bwd",
-                             "train2", "walsh_load"])
+                             "train2", "walsh_load", "chanmod"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (reference for HBM byte counters)")
     return ap.parse_args()
@@ -152,7 +155,8 @@ def main():
     if args.workload != "mhcwalsh":
         line = {"moe": bench_moe, "octonion": bench_octonion, "hadamard": bench_hadamard, "prefill5": bench_prefill5,
                 "decode5": bench_decode5, "hadamard_bwd": bench_hadamard_bwd,
-                "train2": bench_train2, "walsh_load": bench_walsh_load}[args.workload](torch, args)
+                "train2": bench_train2, "walsh_load": bench_walsh_load,
+                "chanmod": bench_chanmod}[args.workload](torch, args)
         print(json.dumps(line), flush=True)
         return
     _hip.lib()
@@ -465,6 +469,70 @@ def bench_hadamard_bwd(torch, args):
                  "synthetic: x, gy N(0,1); weights N(0,0.02) latents",
                  {"workload": "HadamardLinear(512, 512) backward, x and gy [8192, 512]", "global_batch": 8,
                   "seq_len": 1024, "parallelism": "single GPU"}, roof, cpu)
+    line["sweep"] = sweep
+    return line
+
+
+def bench_chanmod(torch, args):
+    """mHCLlamaBlock's channel modulation (mhc.py:528-532) at the headline
+    model's stream shape: x [8, 1024, 4, 512] bf16 viewed as [32, 1024, 512],
+    y = x + cm(RMSNorm(x)) with the ternary context MLP, one
+    walsh_chanmod_fwd call (column sums, MLP, apply).  A sweep over more
+    groups rotates buffers beyond the 256 MB Infinity Cache."""
+    from src.model import _hip
+    from src.model.chassis import RMSNorm
+    from src.model.moe import HadamardChannelModulation
+    torch.manual_seed(0)
+    C = 512
+    cm = HadamardChannelModulation(n_embd=C, residual_scale=0.5).cuda()
+    norm = RMSNorm(C).cuda()
+    sweep = []
+    for G in (32, 128, 512):
+        T = 1024
+        nbuf = max(1, min(16, (768 << 20) // (G * T * C * 2 * 2)))
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        xs = [torch.randn(G, T, C, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(nbuf)]
+
+        def step(i):
+            with torch.no_grad():
+                return cm.fused_residual(xs[i % nbuf], norm)
+        iters = max(args.steps, 50)
+        dt = _time_steps(torch, step, iters, args.warmup)
+        with _hip.LaunchTimer() as lt:
+            for i in range(iters):
+                step(i)
+        r = _roofline_of(lt.summary(), iters)
+        sweep.append(dict(groups=G, rows=G * T, us_per_call=round(dt * 1e6, 2), kernels_us=r["avg_launch_us"],
+                          gbs=r["achieved"], frac=r["frac"], rotated_buffers=nbuf))
+        if G == 32:
+            roof, dt1 = r, dt
+        del xs
+    roof["note"] = ("the three launches of one walsh_chanmod_fwd call (column sums, MLP, apply) against the "
+                    "minimal traffic: x read once and y written once (the kernels read x twice)")
+    cpu = None
+    if not args.no_cpu:
+        from oracle.model import Oracle
+        sd = {"cm." + k: v.detach().float().cpu() for k, v in cm.state_dict().items()}
+        orc = Oracle(sd, C, 1, 0)
+        nw = norm.weight.detach().float().cpu()
+        G, T = 32, 1024
+        x = torch.randn(G, T, C)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0) or reps == 0:
+            with torch.no_grad():
+                xn = orc.rmsnorm(x, nw)
+                _ = x + orc.channel_mod(xn, "cm")
+            reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(reps * G * T / el, 1), unit="rows/s", cores=torch.get_num_threads(), kind="port",
+                   sample=f"{reps} passes of the reference's float32 CPU graph (RMSNorm, mean, ternary MLP, "
+                          f"per-block modulation, residual) over [32, 1024, 512], {el:.1f} s")
+    line = _line("rows/sec through the block's channel modulation at 1 GPU; % of HBM roofline (GB/s)",
+                 32 * 1024 / dt1, "rows/s", max(args.steps, 50), args.warmup, dt1 * 1e3, "bf16",
+                 "synthetic: x N(0,1); context MLP N(0,0.02) / N(0,0.01) ternary latents",
+                 {"workload": "mHC block channel modulation x + cm(RMSNorm(x)), streams [8, 1024, 4, 512] as "
+                              "[32, 1024, 512]", "global_batch": 8, "seq_len": 1024, "parallelism": "single GPU"},
+                 roof, cpu)
     line["sweep"] = sweep
     return line
 

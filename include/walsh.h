@@ -501,6 +501,54 @@ int walsh_moe_ffn_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, const vo
                       const uint16_t *down_frag, const float *gammas, int *topk_idx, float *topk_w, int *count,
                       float *probsum, int64_t n_part, void *y, int64_t ldy, int dtype, int ydtype, void *stream);
 
+/* ------------------------------------------------------------------ channel modulation
+ * HadamardChannelModulation (src/model/moe.py:610-771).  Rows come in G
+ * groups of T rows (the module's [B, T, C] input, G = B; mHCLlamaBlock
+ * passes the [B*n, T, C] view of its streams, src/model/mhc.py:528-532):
+ * row (g, t) at x + (g*T + t)*ldx.  C % 4 == 0, C <= 4096; n_blocks divides
+ * C (block b = columns [b*C/n_blocks, (b+1)*C/n_blocks)).  bf16 rows 8-byte
+ * aligned, float32 rows 16-byte aligned, strides multiples of 4.
+ *
+ * walsh_chanmod_workspace_bytes: float scratch for the per-chunk column
+ *   sums of walsh_chanmod_fwd / walsh_chanmod_bwd.
+ * walsh_chanmod_fwd: the module's forward with the scale / shift MLP
+ *   (moe.py:676-727, ternary branch :753-762), for xn = x, or, if norm_w
+ *   (float32 [C], 16-byte aligned) is non-NULL, xn = x * rsqrt(mean(x^2) +
+ *   eps) * norm_w (the RMSNorm in front of it, chassis.py:96-106):
+ *     bulk[g] = mean_t xn[g, t];  h = silu(w1 bulk[g]);  m = w2 h
+ *     scale[g][b] = 1 + clamp(*scale_temp, 0.1, 0.5) * tanh(m[b]);
+ *     shift[g][b] = m[n_blocks + b]
+ *     y = (add_input ? x : 0) + xn + residual_scale * (xn*scale + shift_scale*shift - xn)
+ *   w1 float32 [hidden][C], w2 float32 [2*n_blocks][hidden] (the context
+ *   MLP's weights: code * gamma for the ternary module, walsh_ternary_quantize's
+ *   `scaled`, or the latent weights for use_ternary=False); scale_temp a
+ *   device float.  scale_shift float32 [G][2*n_blocks] receives scale then
+ *   shift of each group (the module's statistics come from it).  y may not
+ *   alias x.  Everything is computed in float32; y is rounded to dtype once.
+ * walsh_chanmod_apply: the per-block modulation alone, ChannelModFunction's
+ *   forward (moe.py:116-153, :202-233): y = x + residual_scale * (x*scale +
+ *   shift_scale*shift - x) with scale / shift float32, element (g, b) at
+ *   g*ld_ss + b.
+ * walsh_chanmod_bwd: ChannelModFunction's backward (moe.py:155-199,
+ *   :235-256) for the output gradient gy:
+ *     gx = gy * (1 + residual_scale * (scale - 1))
+ *     dscale[g][b] = residual_scale * sum over the group's rows and block b of gy*x
+ *     dshift[g][b] = shift_scale * residual_scale * sum of gy
+ *   gy, x and gx share dtype; the sums are float32 in a fixed order
+ *   (deterministic). */
+int64_t walsh_chanmod_workspace_bytes(int64_t G, int64_t T, int64_t C);
+int walsh_chanmod_fwd(const void *x, int64_t ldx, int64_t G, int64_t T, int64_t C, const float *norm_w, float eps,
+                      const float *w1, int64_t hidden, const float *w2, int64_t n_blocks, const float *scale_temp,
+                      float residual_scale, float shift_scale, int add_input, void *y, int64_t ldy,
+                      float *scale_shift, int dtype, void *workspace, int64_t workspace_bytes, void *stream);
+int walsh_chanmod_apply(const void *x, int64_t ldx, int64_t G, int64_t T, int64_t C, int64_t n_blocks,
+                        const float *scale, const float *shift, int64_t ld_ss, float residual_scale,
+                        float shift_scale, void *y, int64_t ldy, int dtype, void *stream);
+int walsh_chanmod_bwd(const void *gy, int64_t ldg, const void *x, int64_t ldx, int64_t G, int64_t T, int64_t C,
+                      int64_t n_blocks, const float *scale, int64_t ld_ss, float residual_scale, float shift_scale,
+                      void *gx, int64_t ldgx, float *dscale, float *dshift, int dtype, void *workspace,
+                      int64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

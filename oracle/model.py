@@ -13,6 +13,7 @@ reference's order (generate.py:134 runs the CPU path without autocast):
   HadamardLinear.forward       src/model/fht_cuda.py:489-519 (quantiser physics.py:13-51)
   HadamardHeadMixerFused       fht_cuda.py:652-670
   HadamardMoE.forward          src/model/moe.py:512-542 (router :418-447, experts :337-380)
+  HadamardChannelModulation    src/model/moe.py:676-762 (its use in the block: mhc.py:528-532)
 
 It also serves as the timed CPU baseline of the full forward.
 """
@@ -58,7 +59,7 @@ class Oracle:
     ``loss`` gives the cross-entropy whose backward fills ``leaf.grad``."""
 
     def __init__(self, sd, n_embd, n_head, n_layer, n_streams=4, head_mixing=True, block_size=256,
-                 use_moe=False, moe_max_experts=4, grad=False, grad_dtype=torch.float64):
+                 use_moe=False, moe_max_experts=4, grad=False, grad_dtype=torch.float64, use_channel_mod=False):
         self.grad = grad
         self.dt = grad_dtype if grad else torch.float32
         if grad:
@@ -80,6 +81,7 @@ class Oracle:
         self.n = n_streams
         self.head_mixing = head_mixing
         self.use_moe = use_moe
+        self.use_channel_mod = use_channel_mod
         self.moe_k = moe_max_experts
         self.H = sylvester(32).to(self.dt)
         self._codes = {}
@@ -146,18 +148,36 @@ class Oracle:
         mp = probs * mask
         wts = mp / mp.sum(-1, keepdim=True).clamp(min=1e-8)
 
-        def q(key):
-            w = self.sd[key]
-            if self.grad:
-                return _MoESTE.apply(w)
-            g = w.abs().mean() + 1e-8
-            return torch.clamp(torch.round(w / g), -1, 1) * g
-
+        q = self.moe_quantized
         xb = x.view(B, T, E, C // E)
         g = torch.einsum('bted,ehd->bteh', xb, q(p + '.experts.gate_weights'))
         u = torch.einsum('bted,ehd->bteh', xb, q(p + '.experts.up_weights'))
         out = torch.einsum('bteh,edh->bted', F.silu(g) * u, q(p + '.experts.down_weights'))
         return (out * wts.unsqueeze(-1)).reshape(B, T, C), dict(probs=probs, mask=mask, weights=wts, idx=idx)
+
+    def moe_quantized(self, key):
+        """quantize_ternary of moe.py:276-303: clamp(round(w/g), -1, 1)*g."""
+        w = self.sd[key]
+        if self.grad:
+            return _MoESTE.apply(w)
+        g = w.abs().mean() + 1e-8
+        return torch.clamp(torch.round(w / g), -1, 1) * g
+
+    def channel_mod(self, x, p, n_blocks=None, residual_scale=0.5):
+        """HadamardChannelModulation.forward with the ternary MLP
+        (moe.py:676-727, :753-762) and the per-block modulation of
+        _forward_pytorch (:729-744); x [G, T, C]."""
+        G, T, C = x.shape
+        nb = n_blocks or C // 32
+        q = self.moe_quantized
+        bulk = x.mean(dim=1)
+        h = F.silu(bulk @ q(p + '.context_mlp.0.weight').t())
+        mods = h @ q(p + '.context_mlp.2.weight').t()
+        raw, shift = mods.chunk(2, dim=-1)
+        scale = 1.0 + torch.clamp(self.sd[p + '.scale_temp'], 0.1, 0.5) * torch.tanh(raw)
+        xb = x.view(G, T, nb, C // nb)
+        xm = xb * scale.view(G, 1, nb, 1) + shift.view(G, 1, nb, 1) * 0.1
+        return (xb + residual_scale * (xm - xb)).view(G, T, C)
 
     # ---------------------------------------------------------------- harness
     def rmsnorm(self, x, w, eps=1e-6):
@@ -221,6 +241,11 @@ class Oracle:
             else:
                 ffn = lambda v: self.swiglu(self.rmsnorm(v, sd[p + '.ffn_norm.weight']), p + '.feed_forward')  # noqa: E731
             h = self.stream(h, p + '.ffn_stream', ffn)
+            if self.use_channel_mod:
+                # the [B*n, T, C] view of the streams (mhc.py:528-532)
+                hf = h.reshape(B * self.n, T, self.C)
+                hn = self.rmsnorm(hf, sd[p + '.channel_mod_norm.weight'])
+                h = (hf + self.channel_mod(hn, p + '.channel_mod')).view(B, T, self.n, self.C)
         hm = h.reshape(B, T, self.n * self.C) @ sd['stream_merge.weight'].t() + sd['stream_merge.bias']
         ho = self.rmsnorm(hm, sd['norm.weight'])
         logits = ho[:, [-1], :] @ sd['output.weight'].t()

@@ -575,6 +575,91 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
     return o
 
 
+# ------------------------------------------------------------------ channel modulation
+
+def _groups(x: torch.Tensor) -> torch.Tensor:
+    """[G, T, C] with unit column stride, 4-aligned row stride and the groups
+    laid out one after another (what the channel-modulation kernels read)."""
+    assert x.dim() == 3, "channel modulation takes [groups, T, C]"
+    G, T, C = x.shape
+    ok = x.stride(-1) == 1 and x.stride(1) % 4 == 0 and x.stride(1) >= C and x.stride(0) == T * x.stride(1)
+    ok = ok and x.data_ptr() % (8 if x.dtype == torch.bfloat16 else 16) == 0
+    return x if ok else x.contiguous()
+
+
+def chanmod_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, scale_temp: torch.Tensor, n_blocks: int,
+                residual_scale: float, shift_scale: float = 0.1, norm_w: torch.Tensor = None, eps: float = 1e-6,
+                add_input: bool = False):
+    """HadamardChannelModulation.forward (moe.py:676-727) on x [G, T, C]
+    (float32 or bfloat16), with the context MLP weights w1 [hidden, C] and
+    w2 [2*n_blocks, hidden] as float32 values (ternary code*gamma, or the
+    latent weights).  With ``norm_w`` the input is RMSNorm(x)*norm_w first;
+    with ``add_input`` x is added to the result (the block's residual,
+    mhc.py:531).  Returns (y [G, T, C] in x.dtype, scale_shift float32
+    [G, 2*n_blocks] = scale then shift per group)."""
+    _hip.require_device(x, "input")
+    x = _groups(x)
+    G, T, C = x.shape
+    dev = x.device
+    w1f = w1.detach().float().contiguous()
+    w2f = w2.detach().float().contiguous()
+    hidden = w1f.shape[0]
+    assert w1f.shape == (hidden, C) and w2f.shape == (2 * n_blocks, hidden), "context MLP shapes"
+    st = scale_temp.detach().float().reshape(-1)[:1].contiguous()
+    nw = None if norm_w is None else norm_w.detach().float().contiguous()
+    y = torch.empty(G, T, C, device=dev, dtype=x.dtype)
+    ss = torch.empty(G, 2 * n_blocks, device=dev, dtype=torch.float32)
+    nws = _hip.lib().walsh_chanmod_workspace_bytes(G, T, C)
+    ws = torch.empty(max(nws, 4) // 4, device=dev, dtype=torch.float32)
+    esz = x.element_size()
+    _hip.call("walsh_chanmod_fwd", x.data_ptr(), x.stride(1), G, T, C, _hip.ptr(nw), float(eps), w1f.data_ptr(),
+              hidden, w2f.data_ptr(), int(n_blocks), st.data_ptr(), float(residual_scale), float(shift_scale),
+              int(bool(add_input)), y.data_ptr(), C, ss.data_ptr(), _hip.dtype_code(x.dtype), ws.data_ptr(), nws,
+              _hip.stream(dev), kernel="chanmod<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"),
+              nbytes=2 * G * T * C * esz, flops=0)
+    return y, ss
+
+
+def chanmod_apply(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, residual_scale: float,
+                  shift_scale: float = 0.1) -> torch.Tensor:
+    """ChannelModFunction's forward (moe.py:116-153): x [G, T, C], scale /
+    shift [G, n_blocks] -> x + r*(x*scale + shift_scale*shift - x) per block."""
+    _hip.require_device(x, "input")
+    x = _groups(x)
+    G, T, C = x.shape
+    sc = scale.detach().float().contiguous()
+    sh = shift.detach().float().contiguous()
+    nb = sc.shape[-1]
+    assert sc.shape == (G, nb) and sh.shape == (G, nb), "scale / shift must be [groups, n_blocks]"
+    y = torch.empty(G, T, C, device=x.device, dtype=x.dtype)
+    _hip.call("walsh_chanmod_apply", x.data_ptr(), x.stride(1), G, T, C, nb, sc.data_ptr(), sh.data_ptr(), nb,
+              float(residual_scale), float(shift_scale), y.data_ptr(), C, _hip.dtype_code(x.dtype),
+              _hip.stream(x.device))
+    return y
+
+
+def chanmod_bwd(gy: torch.Tensor, x: torch.Tensor, scale: torch.Tensor, residual_scale: float,
+                shift_scale: float = 0.1):
+    """ChannelModFunction's backward (moe.py:155-199, :235-256): returns
+    (gx in x.dtype, dscale, dshift float32 [G, n_blocks])."""
+    _hip.require_device(x, "input")
+    x = _groups(x)
+    G, T, C = x.shape
+    g = _groups(gy.to(x.dtype))
+    assert g.shape == x.shape, "gradient shape"
+    sc = scale.detach().float().contiguous()
+    nb = sc.shape[-1]
+    gx = torch.empty(G, T, C, device=x.device, dtype=x.dtype)
+    ds = torch.empty(G, nb, device=x.device, dtype=torch.float32)
+    dh = torch.empty(G, nb, device=x.device, dtype=torch.float32)
+    nws = _hip.lib().walsh_chanmod_workspace_bytes(G, T, C)
+    ws = torch.empty(max(nws, 4) // 4, device=x.device, dtype=torch.float32)
+    _hip.call("walsh_chanmod_bwd", g.data_ptr(), g.stride(1), x.data_ptr(), x.stride(1), G, T, C, nb, sc.data_ptr(),
+              nb, float(residual_scale), float(shift_scale), gx.data_ptr(), C, ds.data_ptr(), dh.data_ptr(),
+              _hip.dtype_code(x.dtype), ws.data_ptr(), nws, _hip.stream(x.device))
+    return gx, ds, dh
+
+
 # ------------------------------------------------------------------ mHC
 
 def sinkhorn(h: torch.Tensor, n_iter: int = 20, eps: float = 1e-8) -> torch.Tensor:

@@ -309,7 +309,10 @@ class mHCLlamaBlock(nn.Module):
         self._moe = getattr(config, 'use_moe', False)
         self.use_channel_mod = getattr(config, 'use_channel_mod', False)
         if self.use_channel_mod:
-            raise NotImplementedError("channel modulation (use_channel_mod) is outside this build's scope")
+            from .moe import HadamardChannelModulation
+            self.channel_mod = HadamardChannelModulation(n_embd=config.n_embd, n_blocks=None, use_ternary=True,
+                                                         residual_scale=0.5)
+            self.channel_mod_norm = RMSNorm(config.n_embd)
         self.attn_stream = mHCResidualStream(config.n_embd, n_streams)
         self.ffn_stream = mHCResidualStream(config.n_embd, n_streams)
 
@@ -324,8 +327,18 @@ class mHCLlamaBlock(nn.Module):
         if self._moe:
             # the stream update rounds the FFN output to the stream dtype
             # (autocast matmul, mhc.py:374-377), so produce it in that dtype
-            return self.ffn_stream.forward_normed(x, self.ffn_norm, lambda v: ff(v, out_dtype=v.dtype))
-        return self.ffn_stream.forward_normed(x, self.ffn_norm, ff)
+            x = self.ffn_stream.forward_normed(x, self.ffn_norm, lambda v: ff(v, out_dtype=v.dtype))
+        else:
+            x = self.ffn_stream.forward_normed(x, self.ffn_norm, ff)
+        if self.use_channel_mod:
+            # x + channel_mod(norm(x)) on the [B*n, T, C] view of the
+            # contiguous [B, T, n, C] streams (mhc.py:528-532): a "group" of T
+            # rows is that view's, as there, not one stream's.  The result
+            # stays in the stream dtype.
+            B, T, n, C = x.shape
+            x = self.channel_mod.fused_residual(x.contiguous().view(B * n, T, C), self.channel_mod_norm)
+            x = x.view(B, T, n, C)
+        return x
 
 
 class mHCWalsh(nn.Module):
@@ -417,7 +430,11 @@ class mHCWalsh(nn.Module):
                 layer.feed_forward.reset_stats()
 
     def get_channel_mod_stats(self) -> dict:
-        return {}
+        """Channel-modulation statistics averaged over the layers (mhc.py:733-751)."""
+        stats = [l.channel_mod.get_modulation_stats() for l in self.layers if hasattr(l, 'channel_mod')]
+        if not stats:
+            return {}
+        return {k: sum(s[k] for s in stats) / len(stats) for k in ('scale_mean', 'scale_std', 'shift_mean')}
 
     @torch.no_grad()
     def generate(self, idx, max_new_tokens, temperature=1.0, top_k=None):

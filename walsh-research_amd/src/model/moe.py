@@ -401,12 +401,168 @@ def should_use_channel_mod(config) -> bool:
     return getattr(config, 'use_channel_mod', False)
 
 
+class ChannelModFunction(torch.autograd.Function):
+    """Per-block modulation out = x + r*(x*scale + shift_scale*shift - x)
+    with its backward (moe.py:202-256), both on HIP kernels
+    (walsh_chanmod_apply / walsh_chanmod_bwd)."""
+
+    @staticmethod
+    def forward(ctx, x, scale, shift, n_blocks, block_dim, residual_scale, shift_scale):
+        if x.dim() != 3:
+            raise ValueError(f"Expected 3D input, got {x.shape}")
+        assert scale.shape[-1] == n_blocks and n_blocks * block_dim == x.shape[-1], "block layout"
+        y = kernels.chanmod_apply(x, scale, shift, residual_scale, shift_scale)
+        ctx.save_for_backward(x, scale)
+        ctx.residual_scale = residual_scale
+        ctx.shift_scale = shift_scale
+        ctx.shift_dtype = shift.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, scale = ctx.saved_tensors
+        gx, ds, dh = kernels.chanmod_bwd(grad_out, x, scale, ctx.residual_scale, ctx.shift_scale)
+        return gx, ds.to(scale.dtype), dh.to(ctx.shift_dtype), None, None, None, None
+
+
 class HadamardChannelModulation(nn.Module):
-    """Channel modulation (moe.py:610-771) is outside this build's scope."""
+    """Bulk-state channel modulation (moe.py:610-771): per group (batch row)
+    the mean over T of the input drives a two-layer MLP whose outputs give a
+    scale in [1 - t, 1 + t] (t = clamp(scale_temp, 0.1, 0.5)) and a shift for
+    each block of C / n_blocks channels:
+        out = x + residual_scale * (x * scale + 0.1 * shift - x).
+    Parameter names are the reference's (``context_mlp.{0,2}.weight``,
+    ``scale_temp``).
 
-    def __init__(self, *args, **kwargs):
-        raise NotImplementedError("channel modulation (HadamardChannelModulation) is outside this build's scope")
+    Inference runs walsh_chanmod_fwd: a column-sum kernel for the bulk state,
+    the MLP kernel and the apply kernel (the input is read twice and the
+    output written once).  ``fused_residual(x, norm)`` computes
+    x + self(norm(x)) in the same three kernels with the RMSNorm folded into
+    both passes over x.  With autograd on, the MLP runs as float32 torch
+    operations (the ternary weights through TernaryAbsmeanSTE) and the
+    modulation through ChannelModFunction.
+
+    The MLP runs in float32 also under bfloat16 autocast, where the
+    reference's F.linear rounds its inputs to bfloat16 (moe.py:753-762)."""
+
+    BLOCK_DIM = 32
+
+    def __init__(self, n_embd: int = 256, n_blocks: int = None, use_ternary: bool = True,
+                 residual_scale: float = 0.5):
+        super().__init__()
+        if n_blocks is None:
+            n_blocks = n_embd // self.BLOCK_DIM
+        self.n_blocks = n_blocks
+        self.block_dim = n_embd // n_blocks
+        self.residual_scale = residual_scale
+        self.use_ternary = use_ternary
+        hidden = n_embd // 4
+        self.context_mlp = nn.Sequential(
+            nn.Linear(n_embd, hidden, bias=False),
+            nn.SiLU(),
+            nn.Linear(hidden, n_blocks * 2, bias=False),
+        )
+        nn.init.normal_(self.context_mlp[0].weight, std=0.02)
+        nn.init.normal_(self.context_mlp[-1].weight, std=0.01)
+        self.scale_temp = nn.Parameter(torch.ones(1) * 1.0)
+        self._wcache = WeightCache()
+        self._last_ss = None   # float32 [G, 2*n_blocks]: scale then shift of the last forward
+
+    # statistics of the last forward (moe.py:711-715), computed when read
+    def _stat(self, which):
+        ss = self._last_ss
+        if ss is None:
+            return 0.0
+        nb = self.n_blocks
+        if which == 'scale_mean':
+            return ss[:, :nb].mean().item()
+        if which == 'scale_std':
+            return ss[:, :nb].std().item()
+        return ss[:, nb:].abs().mean().item()
+
+    @property
+    def _last_scale_mean(self):
+        return self._stat('scale_mean')
+
+    @property
+    def _last_scale_std(self):
+        return self._stat('scale_std')
+
+    @property
+    def _last_shift_mean(self):
+        return self._stat('shift_mean')
+
+    def get_modulation_stats(self) -> dict:
+        return {
+            'scale_mean': self._last_scale_mean,
+            'scale_std': self._last_scale_std,
+            'shift_mean': self._last_shift_mean,
+            'scale_temp': self.scale_temp.item(),
+        }
+
+    def _tracked(self, x) -> bool:
+        return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+
+    def _mlp_weights(self):
+        """(w1, w2) float32 as the MLP uses them: code * gamma (moe.py:288)
+        for the ternary module, the weights themselves otherwise."""
+        l1, l2 = self.context_mlp[0].weight, self.context_mlp[2].weight
+
+        def build():
+            if not self.use_ternary:
+                return l1.detach().float().contiguous(), l2.detach().float().contiguous()
+            return (kernels.ternary_quantize(l1, packed=False, scaled=True)["scaled"],
+                    kernels.ternary_quantize(l2, packed=False, scaled=True)["scaled"])
+        return self._wcache.get((l1, l2), build, extra=(self.use_ternary,))
+
+    def _forward_autograd(self, x):
+        with torch.autocast("cuda", enabled=False):
+            h = x.float().mean(dim=1)
+            for layer in self.context_mlp:
+                if isinstance(layer, nn.Linear):
+                    w = quantize_ternary(layer.weight) if self.use_ternary else layer.weight
+                    h = F.linear(h, w.float())
+                else:
+                    h = layer(h)
+            raw_scale, shift = h.chunk(2, dim=-1)
+            scale = 1.0 + torch.clamp(self.scale_temp, 0.1, 0.5) * torch.tanh(raw_scale)
+        self._last_ss = torch.cat([scale, shift], -1).detach()
+        return ChannelModFunction.apply(x, scale, shift.contiguous(), self.n_blocks, self.block_dim,
+                                        self.residual_scale, 0.1)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """x [B, T, n_embd] -> modulated x, same shape and dtype."""
+        if self._tracked(x):
+            return self._forward_autograd(x)
+        w1, w2 = self._mlp_weights()
+        y, self._last_ss = kernels.chanmod_fwd(x, w1, w2, self.scale_temp, self.n_blocks, self.residual_scale, 0.1)
+        return y
+
+    def fused_residual(self, x: torch.Tensor, norm) -> torch.Tensor:
+        """x + self(norm(x)) for an RMSNorm module ``norm`` (mhc.py:531,
+        moe.py:796-798), in x's dtype."""
+        if self._tracked(x):
+            return (x + self(norm(x))).to(x.dtype)
+        w1, w2 = self._mlp_weights()
+        y, self._last_ss = kernels.chanmod_fwd(x, w1, w2, self.scale_temp, self.n_blocks, self.residual_scale, 0.1,
+                                               norm_w=norm.weight, eps=norm.eps, add_input=True)
+        return y
 
 
-class HadamardChannelModulationBlock(HadamardChannelModulation):
-    pass
+class HadamardChannelModulationBlock(nn.Module):
+    """x + channel_mod(norm(x)) (moe.py:774-798): n_blocks 8 and residual
+    scale 0.1 by default, as there."""
+
+    def __init__(self, config, n_blocks: int = 8):
+        super().__init__()
+        from .chassis import RMSNorm
+        self.norm = RMSNorm(config.n_embd)
+        self.channel_mod = HadamardChannelModulation(
+            n_embd=config.n_embd,
+            n_blocks=n_blocks,
+            use_ternary=getattr(config, 'use_ternary', True),
+            residual_scale=0.1,
+        )
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.channel_mod.fused_residual(x, self.norm)
