@@ -372,6 +372,23 @@ int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int
                            float *h_pre, float *h_post, float *h_res, void *layer_in, int64_t ld_in,
                            const float *norm_w, float norm_eps, int dtype, void *stream);
 
+/* walsh_mhc_post_pre_norm_fwd: the stream update of one mHCResidualStream
+ *   (src/model/mhc.py:366-381) fused with the mappings of the next one
+ *   (walsh_mhc_pre_norm_fwd): the tile of the next stream's input
+ *     x_new[t, r, :] = sum_s h_res_prev[t, r, s] x_old[t, s, :] + h_post_prev[t, r] out[t, :]
+ *   is formed while it is loaded (x_old read once, the separate pre pass's
+ *   read of x_new saved), written to x_new (row stride ld_new) and used for
+ *   h_pre / h_post / h_res / layer_in exactly as walsh_mhc_pre_norm_fwd uses
+ *   x.  x_new is bitwise what walsh_mhc_post_fwd writes.  Same limits as
+ *   walsh_mhc_pre_norm_fwd, plus C*esize % 16 == 0 and 16-byte aligned rows;
+ *   x_new may not alias x_old, nor the new h_post / h_res the previous ones. */
+int walsh_mhc_post_pre_norm_fwd(const void *x_old, int64_t ld_old, const void *out, int64_t ld_out,
+                                const float *h_res_prev, const float *h_post_prev, void *x_new, int64_t ld_new,
+                                int64_t M, int64_t n, int64_t C, const void *phi_frag, const float *coef,
+                                const float *bias, float rms_eps, int64_t n_iter, float sk_eps, float *h_pre,
+                                float *h_post, float *h_res, void *layer_in, int64_t ld_in, const float *norm_w,
+                                float norm_eps, int dtype, void *stream);
+
 /* walsh_mhc_pre_wide_fwd: the same results as walsh_mhc_pre_norm_fwd for
  *   rows too long for an LDS tile (n*C % 32 == 0, C <= 4096; n_embd 4096),
  *   in two launches: a split-K projection on 16x16x32 matrix cores writing

@@ -219,3 +219,31 @@ def test_mhc_pre_norm_matches_oracle(K, dtype, M, n, C, with_norm):
     # identical H to the one-pass-per-K-slice kernel
     _, hp1, hq1, hr1 = K.mhc_pre(xt, phi, coef, bias, eps)
     assert torch.allclose(hr, hr1, atol=1e-6) and torch.allclose(hp, hp1, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,n,C", [(100, 4, 512), (33, 4, 64), (7, 2, 32), (40, 3, 96), (1, 4, 512), (50, 4, 1024)])
+def test_mhc_post_pre_norm_equals_separate_kernels(K, dtype, M, n, C):
+    """The fused stream update + next mappings (walsh_mhc_post_pre_norm_fwd)
+    give bitwise the results of walsh_mhc_post_fwd followed by
+    walsh_mhc_pre_norm_fwd (which the oracle tests pin)."""
+    if not K.mhc_post_pre_supported(n, C, dtype):
+        pytest.skip("shape outside the fused kernel (LDS tile or 16-byte chunks)")
+    print(f"post+pre fused M={M} n={n} C={C} {dtype}", flush=True)
+    rng = np.random.default_rng(M * 5 + n + C)
+    x_old = torch.from_numpy(rng.normal(0, 1, (M, n, C)).astype(np.float32)).cuda().to(dtype)
+    out = torch.from_numpy(rng.normal(0, 1, (M, C)).astype(np.float32)).cuda().to(dtype)
+    h_res_prev = torch.from_numpy(rng.uniform(0, 0.5, (M, n, n)).astype(np.float32)).cuda()
+    h_post_prev = torch.from_numpy(rng.uniform(0, 2, (M, n)).astype(np.float32)).cuda()
+    maps = _maps(rng, n, C)
+    phi, coef, bias = _fused_params(maps, n, C, dtype)
+    frag = K.phi_fragments(phi)
+    eps = float(torch.finfo(dtype).eps)
+    w = torch.from_numpy(rng.uniform(0.5, 1.5, C).astype(np.float32)).cuda()
+    x_new, li, hp, hq, hr = K.mhc_post_pre_norm(x_old, out, h_res_prev, h_post_prev, frag, coef, bias, eps,
+                                                norm_w=w, norm_eps=1e-6)
+    x_ref = K.mhc_post(x_old, out, h_res_prev, h_post_prev)
+    li_r, hp_r, hq_r, hr_r = K.mhc_pre_norm(x_ref, frag, coef, bias, eps, norm_w=w, norm_eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(x_new, x_ref)
+    assert torch.equal(li, li_r) and torch.equal(hp, hp_r) and torch.equal(hq, hq_r) and torch.equal(hr, hr_r)

@@ -586,11 +586,22 @@ struct Pre2Args {
     int64_t ld_in;
     const float *norm_w;    // nullable: layer_in = rmsnorm(layer_in) * norm_w
     float norm_eps;
+    // POST variant: the tile is the previous stream's update
+    //   x_new[t, r, :] = sum_s hr_prev[t, r, s] xo[t, s, :] + hp_prev[t, r] out[t, :]
+    // formed while it is loaded, kept in LDS and written to x_new (x unused)
+    const void *xo;
+    int64_t ld_xo;
+    const void *out;
+    int64_t ld_out;
+    const float *hr_prev, *hp_prev;
+    void *x_new;
+    int64_t ld_new;
 };
 
 constexpr int kTileBytes = 128 * 1024;
+constexpr int kPostItems = 4;             // POST: (token, 16-byte column chunk) items per thread per round
 
-template <typename T, bool BF16MMA, int MT>
+template <typename T, bool BF16MMA, int MT, bool POST = false>
 __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     constexpr int TT = 16 * MT;
     constexpr uint32_t esz = sizeof(T);
@@ -637,6 +648,103 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     for (int c4 = tid; c4 < C / 4; c4 += kPreThreads)
         nw_l[c4] = a.norm_w ? *(const f32x4 *)(a.norm_w + 4 * c4) : f32x4{1.f, 1.f, 1.f, 1.f};
 
+    // phase 0 (POST): the stream update of the previous layer, formed per
+    // (token, 16-byte column chunk) from the n old stream chunks and the
+    // layer output chunk, in mhc_post_kernel's operation order (so x_new is
+    // bitwise what that kernel writes); rounded to T, kept in LDS, stored.
+    if constexpr (POST) {
+        const int cpc = C * (int)esz / 16;    // chunks per stream row
+        const int nit = TT * cpc;
+        const int nh = n * n + n;
+        float *hprev = part;                  // [TT][n*n + n]; part is free until phase 1 ends
+        const __amdgpu_buffer_rsrc_t xor_ = make_rsrc(a.xo, (uint32_t)((int64_t)a.M * a.ld_xo * esz));
+        const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.out, (uint32_t)((int64_t)a.M * a.ld_out * esz));
+        const __amdgpu_buffer_rsrc_t nr = make_rsrc(a.x_new, (uint32_t)((int64_t)a.M * a.ld_new * esz));
+        u32x4 xv[kPostItems][kMaxStreams], ov[kPostItems];
+        auto load_round = [&](int it0) {
+#pragma unroll
+            for (int i = 0; i < kPostItems; ++i) {
+                const int it = it0 + tid + i * kPreThreads;
+                const int r = it / cpc, cc = it - r * cpc;
+                const bool ok = it < nit && tok0 + r < a.M;
+#pragma unroll
+                for (int st = 0; st < kMaxStreams; ++st)
+                    xv[i][st] = __builtin_amdgcn_raw_buffer_load_b128(
+                        xor_, ok && st < n ? (uint32_t)(((int64_t)(tok0 + r) * a.ld_xo + st * C) * esz + cc * 16) : kOOB,
+                        0, 0);
+                ov[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                    orr, ok ? (uint32_t)((int64_t)(tok0 + r) * a.ld_out * esz + cc * 16) : kOOB, 0, 0);
+            }
+        };
+        load_round(0);
+        for (int e = tid; e < TT * nh; e += kPreThreads) {
+            const int r = e / nh, k = e - r * nh;
+            const bool ok = tok0 + r < a.M;
+            hprev[e] = !ok ? 0.f : k < n * n ? a.hr_prev[(int64_t)(tok0 + r) * n * n + k]
+                                             : a.hp_prev[(int64_t)(tok0 + r) * n + (k - n * n)];
+        }
+        load_phi(ks0, pa);
+        __syncthreads();
+        constexpr int VE = 16 / (int)esz;     // values per chunk: 8 bf16 or 4 f32
+        for (int it0 = 0; it0 < nit; it0 += kPostItems * kPreThreads) {
+            if (it0) load_round(it0);
+#pragma unroll
+            for (int i = 0; i < kPostItems; ++i) {
+                const int it = it0 + tid + i * kPreThreads;
+                if (it >= nit) continue;
+                const int r = it / cpc, cc = it - r * cpc;
+                const bool ok = tok0 + r < a.M;
+                const float *hr = hprev + r * nh, *hp = hr + n * n;
+                float xf[kMaxStreams][8], of[8];
+                auto unpack = [&](const u32x4 &u, float (&f)[8]) {
+                    if constexpr (sizeof(T) == 2) {
+                        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            f[2 * q] = __uint_as_float(w[q] << 16);
+                            f[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+                        }
+                    } else {
+                        f[0] = __uint_as_float(u.x);
+                        f[1] = __uint_as_float(u.y);
+                        f[2] = __uint_as_float(u.z);
+                        f[3] = __uint_as_float(u.w);
+                    }
+                };
+#pragma unroll
+                for (int st = 0; st < kMaxStreams; ++st) unpack(xv[i][st], xf[st]);
+                unpack(ov[i], of);
+#pragma unroll
+                for (int rr = 0; rr < kMaxStreams; ++rr) {
+                    if (rr >= n) continue;
+                    float acc[8];
+#pragma unroll
+                    for (int e = 0; e < VE; ++e) acc[e] = hp[rr] * of[e];
+#pragma unroll
+                    for (int st = 0; st < kMaxStreams; ++st) {
+                        if (st >= n) continue;
+                        const float h = hr[rr * n + st];
+#pragma unroll
+                        for (int e = 0; e < VE; ++e) acc[e] += h * xf[st][e];
+                    }
+                    u32x4 pk;
+                    if constexpr (sizeof(T) == 2) {
+                        pk = u32x4{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
+                                   pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7])};
+                    } else {
+                        pk = u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
+                                   __float_as_uint(acc[3])};
+                    }
+                    u32x2 *d = (u32x2 *)(xs + r * stride + rr * C * esz + cc * 16);
+                    d[0] = u32x2{pk.x, pk.y};
+                    d[1] = u32x2{pk.z, pk.w};
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        pk, nr, ok ? (uint32_t)(((int64_t)(tok0 + r) * a.ld_new + rr * C) * esz + cc * 16) : kOOB,
+                        0, 0);
+                }
+            }
+        }
+    } else
     // phase 0: tile -> LDS, all 16-byte loads in flight together
     {
         const int cpr = rowb / 16;            // chunks per row
@@ -1202,26 +1310,46 @@ WALSH_EXPORT int walsh_mhc_post_fwd(const void *x, int64_t ldx, const void *out,
     return WALSH_OK;
 }
 
-WALSH_EXPORT int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C,
-                                        const void *phi_frag, const float *coef, const float *bias, float rms_eps,
-                                        int64_t n_iter, float sk_eps, float *h_pre, float *h_post, float *h_res,
-                                        void *layer_in, int64_t ld_in, const float *norm_w, float norm_eps,
-                                        int dtype, void *stream) {
-    if (!x || !phi_frag || !coef || !bias || !h_pre || !h_post || !h_res || !layer_in)
-        return set_error(WALSH_EINVAL, "walsh_mhc_pre_norm_fwd: null pointer");
-    if (M < 0 || n < 1 || C < 4 || ldx < n * C || ld_in < C || n_iter < 0)
-        return set_error(WALSH_EINVAL, "walsh_mhc_pre_norm_fwd: bad shape M=%lld n=%lld C=%lld", (long long)M,
-                         (long long)n, (long long)C);
-    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: dtype");
+struct PostIn {
+    const void *xo;
+    int64_t ld_xo;
+    const void *out;
+    int64_t ld_out;
+    const float *hr_prev, *hp_prev;
+    void *x_new;
+    int64_t ld_new;
+};
+
+static int mhc_pre_norm_impl(const char *fn, const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C,
+                             const void *phi_frag, const float *coef, const float *bias, float rms_eps, int64_t n_iter,
+                             float sk_eps, float *h_pre, float *h_post, float *h_res, void *layer_in, int64_t ld_in,
+                             const float *norm_w, float norm_eps, int dtype, void *stream, const PostIn *post) {
+    if ((!post && !x) || !phi_frag || !coef || !bias || !h_pre || !h_post || !h_res || !layer_in)
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (M < 0 || n < 1 || C < 4 || (!post && ldx < n * C) || ld_in < C || n_iter < 0)
+        return set_error(WALSH_EINVAL, "%s: bad shape M=%lld n=%lld C=%lld", fn, (long long)M, (long long)n,
+                         (long long)C);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype", fn);
     const int64_t esz = dtype == WALSH_BF16 ? 2 : 4;
     const int64_t rowb = n * C * esz;
-    if (n > kMaxStreams || (n * C) % 16 || C % 4 || C > 1024 || rowb % 16 || ldx % (16 / esz) || ld_in % 4 ||
-        rowb * 16 > kTileBytes)
-        return set_error(WALSH_ENOTSUP,
-                         "walsh_mhc_pre_norm_fwd: needs n <= %d, n*C %% 16 == 0, C <= 1024, 16 rows in 128 KB",
+    if (n > kMaxStreams || (n * C) % 16 || C % 4 || C > 1024 || rowb % 16 || (!post && ldx % (16 / esz)) ||
+        ld_in % 4 || rowb * 16 > kTileBytes)
+        return set_error(WALSH_ENOTSUP, "%s: needs n <= %d, n*C %% 16 == 0, C <= 1024, 16 rows in 128 KB", fn,
                          kMaxStreams);
-    if ((uintptr_t)x % 16 || (uintptr_t)layer_in % 16 || (uintptr_t)phi_frag % 16 || (norm_w && (uintptr_t)norm_w % 16))
-        return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: pointers must be 16-byte aligned");
+    if ((!post && (uintptr_t)x % 16) || (uintptr_t)layer_in % 16 || (uintptr_t)phi_frag % 16 ||
+        (norm_w && (uintptr_t)norm_w % 16))
+        return set_error(WALSH_ENOTSUP, "%s: pointers must be 16-byte aligned", fn);
+    if (post) {
+        if (!post->xo || !post->out || !post->hr_prev || !post->hp_prev || !post->x_new)
+            return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+        const int64_t v = 16 / esz;
+        if ((C * esz) % 16 || post->ld_xo < n * C || post->ld_new < n * C || post->ld_out < C || post->ld_xo % v ||
+            post->ld_new % v || post->ld_out % v || (uintptr_t)post->xo % 16 || (uintptr_t)post->out % 16 ||
+            (uintptr_t)post->x_new % 16)
+            return set_error(WALSH_ENOTSUP, "%s: stream rows need C*esize %% 16 == 0, 16-byte aligned rows", fn);
+        if (post->x_new == post->xo || (const float *)post->hr_prev == h_res || (const float *)post->hp_prev == h_post)
+            return set_error(WALSH_EINVAL, "%s: outputs may not alias the previous stream's tensors", fn);
+    }
     if (M == 0) return WALSH_OK;
     // 16-token tiles: ~74 KB of LDS at 4 KB rows, so two workgroups share a
     // CU and overlap their load / projection / write phases
@@ -1230,15 +1358,21 @@ WALSH_EXPORT int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, i
     const size_t lds = (size_t)TT * (rowb + 8) + (size_t)kPreWaves * TT * (kPhiRows + 1) * 4 + kPreWaves * TT * 4 +
                        TT * 16 + (size_t)C * 4;
     if (lds > (size_t)device_info().max_shared_per_block)
-        return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: needs %zu B of LDS", lds);
-    const int64_t ld = ldx > ld_in ? ldx : ld_in;
+        return set_error(WALSH_ENOTSUP, "%s: needs %zu B of LDS", fn, lds);
+    int64_t ld = ld_in;
+    if (!post && ldx > ld) ld = ldx;
+    if (post) {
+        if (post->ld_xo > ld) ld = post->ld_xo;
+        if (post->ld_new > ld) ld = post->ld_new;
+        if (post->ld_out > ld) ld = post->ld_out;
+    }
     int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / TT * TT;
-    if (rows_max < TT) return set_error(WALSH_ENOTSUP, "walsh_mhc_pre_norm_fwd: row stride too large");
+    if (rows_max < TT) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
     rows_max = balanced_rows(M, rows_max, TT);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
-        Pre2Args a;
-        a.x = (const char *)x + r0 * ldx * esz;
+        Pre2Args a{};
+        a.x = post ? nullptr : (const char *)x + r0 * ldx * esz;
         a.ldx = ldx;
         a.M = (int)rows;
         a.n = (int)n;
@@ -1256,19 +1390,51 @@ WALSH_EXPORT int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, i
         a.ld_in = ld_in;
         a.norm_w = norm_w;
         a.norm_eps = norm_eps;
+        if (post) {
+            a.xo = (const char *)post->xo + r0 * post->ld_xo * esz;
+            a.ld_xo = post->ld_xo;
+            a.out = (const char *)post->out + r0 * post->ld_out * esz;
+            a.ld_out = post->ld_out;
+            a.hr_prev = post->hr_prev + r0 * n * n;
+            a.hp_prev = post->hp_prev + r0 * n;
+            a.x_new = (char *)post->x_new + r0 * post->ld_new * esz;
+            a.ld_new = post->ld_new;
+        }
         const dim3 G((unsigned)ceil_div(rows, TT)), B(kPreThreads);
         hipStream_t s = (hipStream_t)stream;
         if (dtype == WALSH_BF16) {
-            if (MT == 2) launch((mhc_pre2_kernel<uint16_t, true, 2>), G, B, lds, s, a);
+            if (post) launch((mhc_pre2_kernel<uint16_t, true, 1, true>), G, B, lds, s, a);
             else launch((mhc_pre2_kernel<uint16_t, true, 1>), G, B, lds, s, a);
         } else {
-            if (MT == 2) launch((mhc_pre2_kernel<float, false, 2>), G, B, lds, s, a);
+            if (post) launch((mhc_pre2_kernel<float, false, 1, true>), G, B, lds, s, a);
             else launch((mhc_pre2_kernel<float, false, 1>), G, B, lds, s, a);
         }
-        const int rc = check_hip(hipGetLastError(), "walsh_mhc_pre_norm_fwd launch");
+        const int rc = check_hip(hipGetLastError(), fn);
         if (rc) return rc;
     }
     return WALSH_OK;
+}
+
+WALSH_EXPORT int walsh_mhc_pre_norm_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C,
+                                        const void *phi_frag, const float *coef, const float *bias, float rms_eps,
+                                        int64_t n_iter, float sk_eps, float *h_pre, float *h_post, float *h_res,
+                                        void *layer_in, int64_t ld_in, const float *norm_w, float norm_eps,
+                                        int dtype, void *stream) {
+    return mhc_pre_norm_impl("walsh_mhc_pre_norm_fwd", x, ldx, M, n, C, phi_frag, coef, bias, rms_eps, n_iter, sk_eps,
+                             h_pre, h_post, h_res, layer_in, ld_in, norm_w, norm_eps, dtype, stream, nullptr);
+}
+
+WALSH_EXPORT int walsh_mhc_post_pre_norm_fwd(const void *x_old, int64_t ld_old, const void *out, int64_t ld_out,
+                                             const float *h_res_prev, const float *h_post_prev, void *x_new,
+                                             int64_t ld_new, int64_t M, int64_t n, int64_t C, const void *phi_frag,
+                                             const float *coef, const float *bias, float rms_eps, int64_t n_iter,
+                                             float sk_eps, float *h_pre, float *h_post, float *h_res, void *layer_in,
+                                             int64_t ld_in, const float *norm_w, float norm_eps, int dtype,
+                                             void *stream) {
+    const PostIn post{x_old, ld_old, out, ld_out, h_res_prev, h_post_prev, x_new, ld_new};
+    return mhc_pre_norm_impl("walsh_mhc_post_pre_norm_fwd", nullptr, 0, M, n, C, phi_frag, coef, bias, rms_eps,
+                             n_iter, sk_eps, h_pre, h_post, h_res, layer_in, ld_in, norm_w, norm_eps, dtype, stream,
+                             &post);
 }
 
 // Splits of K for the wide-row projection: enough wavefronts to fill the

@@ -72,6 +72,9 @@ SIGNATURES = {
     "walsh_sinkhorn_bwd": (_I, [_P, _P, _I64, _I64, _I64, ctypes.c_float, _P, _P]),
     "walsh_mhc_pre_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float, _I64, ctypes.c_float,
                                _P, _P, _P, _P, _I64, _I, _P]),
+    "walsh_mhc_post_pre_norm_fwd": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P,
+                                         ctypes.c_float, _I64, ctypes.c_float, _P, _P, _P, _P, _I64, _P,
+                                         ctypes.c_float, _I, _P]),
     "walsh_mhc_pre_norm_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float, _I64, ctypes.c_float,
                                     _P, _P, _P, _P, _I64, _P, ctypes.c_float, _I, _P]),
     "walsh_mhc_post_fwd": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P]),

@@ -765,6 +765,56 @@ def mhc_pre_norm(x: torch.Tensor, phi_frag: torch.Tensor, coef: torch.Tensor, bi
     return layer_in, h_pre, h_post, h_res
 
 
+def mhc_post_pre_supported(n: int, C: int, dtype: torch.dtype) -> bool:
+    """Shapes walsh_mhc_post_pre_norm_fwd takes (the LDS tile of
+    walsh_mhc_pre_norm_fwd, stream rows of whole 16-byte chunks)."""
+    esz = 2 if dtype == torch.bfloat16 else 4
+    return mhc_pre_supported(n, C, dtype) and (n * C) % 16 == 0 and (C * esz) % 16 == 0
+
+
+def mhc_post_pre_norm(x_old: torch.Tensor, out: torch.Tensor, h_res_prev: torch.Tensor, h_post_prev: torch.Tensor,
+                      phi_frag: torch.Tensor, coef: torch.Tensor, bias_cat: torch.Tensor, rms_eps: float,
+                      norm_w: torch.Tensor = None, norm_eps: float = 1e-6, n_iter: int = 20, sk_eps: float = 1e-8):
+    """mhc_post of the previous stream fused with mhc_pre_norm of the next:
+    x_new = H_res_prev @ x_old + H_post_prev^T (x) out is formed as the
+    mapping kernel loads its tile (mhc.py:366-381 then :283-318, :345-364).
+    Returns (x_new, layer_in, h_pre, h_post, h_res); x_new is bitwise
+    mhc_post's result."""
+    _hip.require_device(x_old, "stream input")
+    n, C = x_old.shape[-2], x_old.shape[-1]
+    lead = x_old.shape[:-2]
+    xo = x_old if x_old.is_contiguous() else x_old.contiguous()
+    M = xo.numel() // (n * C)
+    dev = x_old.device
+    o = out.to(x_old.dtype)
+    o = o if o.is_contiguous() else o.contiguous()
+    assert o.numel() == M * C, "layer output shape"
+    hr = h_res_prev.detach().float().contiguous()
+    hp = h_post_prev.detach().float().contiguous()
+    x_new = torch.empty_like(xo)
+    layer_in = torch.empty(lead + (C,), device=dev, dtype=x_old.dtype)
+    h_pre = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_post = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_res = torch.empty(lead + (n, n), device=dev, dtype=torch.float32)
+    if M == 0:
+        return x_new, layer_in, h_pre, h_post, h_res
+    assert phi_frag.dtype == x_old.dtype and phi_frag.numel() == 32 * n * C, "phi_frag layout"
+    nw = None
+    if norm_w is not None:
+        nw = norm_w.detach().float().contiguous()
+        assert nw.numel() == C
+    esz = x_old.element_size()
+    nbytes = M * (2 * n * C + 2 * C) * esz + M * (3 * n + 2 * n * n) * 4 + 32 * n * C * esz
+    flops = M * (2 * n * C * 32 + 2 * n * C + 2 * n * C + n * C * (2 * n + 2))
+    _hip.call("walsh_mhc_post_pre_norm_fwd", xo.data_ptr(), n * C, o.data_ptr(), C, hr.data_ptr(), hp.data_ptr(),
+              x_new.data_ptr(), n * C, M, n, C, phi_frag.data_ptr(), coef.data_ptr(), bias_cat.data_ptr(),
+              float(rms_eps), int(n_iter), float(sk_eps), h_pre.data_ptr(), h_post.data_ptr(), h_res.data_ptr(),
+              layer_in.data_ptr(), C, _hip.ptr(nw), float(norm_eps), _hip.dtype_code(x_old.dtype), _hip.stream(dev),
+              kernel="mhc_post_pre2_kernel<%s>" % ("bf16" if x_old.dtype == torch.bfloat16 else "f32"),
+              nbytes=nbytes, flops=flops)
+    return x_new, layer_in, h_pre, h_post, h_res
+
+
 def phi_fragments32(phi_cat: torch.Tensor) -> torch.Tensor:
     """phi_cat [32, K] -> 16x16x32 matrix-core fragment order [K/32][2][64][8]
     (lane = 16*kq + n holds phi[16*tile + n][32*ks + 8*kq .. +7])."""

@@ -168,6 +168,28 @@ class ResidualStreamMapping(nn.Module):
         return (hp if self.mapping_type == 'pre' else hq).unsqueeze(2)
 
 
+class PendingUpdate:
+    """A stream update x_new = H_res @ x + H_post^T (x) out (mhc.py:366-381)
+    that has not been applied yet.  The next stream's mapping kernel forms it
+    while loading its tile (walsh_mhc_post_pre_norm_fwd), which saves one
+    pass over the streams; ``materialize`` applies it on its own."""
+    __slots__ = ('x', 'out', 'h_res', 'h_post')
+
+    def __init__(self, x, out, h_res, h_post):
+        self.x, self.out, self.h_res, self.h_post = x, out, h_res, h_post
+
+    @property
+    def shape(self):
+        return self.x.shape
+
+    def materialize(self) -> torch.Tensor:
+        return kernels.mhc_post(self.x, self.out, self.h_res, self.h_post)
+
+
+def materialize(x):
+    return x.materialize() if isinstance(x, PendingUpdate) else x
+
+
 class mHCResidualStream(nn.Module):
     """x_{l+1} = H_res @ x_l + H_post^T F(H_pre @ x_l) (mhc.py:321-381)."""
 
@@ -252,15 +274,43 @@ class mHCResidualStream(nn.Module):
         out = layer_fn(layer_in)
         return kernels.mhc_post(x, out, h_res, h_post)
 
-    def forward_normed(self, x, norm, layer_fn):
+    def _post_pre(self, p: PendingUpdate, dt, norm):
+        """The pending update of the previous stream fused with this stream's
+        mappings, or None when the fused kernel does not take the shape."""
+        n, C = self.n_streams, self.n_embd
+        if p.x.dtype != dt or n > _MAX_STREAMS or not kernels.mhc_post_pre_supported(n, C, dt):
+            return None
+        _, coef, bias, frag = self.fused_params(dt, p.x.device)
+        if frag is None:
+            return None
+        return kernels.mhc_post_pre_norm(p.x, p.out, p.h_res, p.h_post, frag, coef, bias, _rms_eps(dt),
+                                         norm_w=None if norm is None else norm.weight,
+                                         norm_eps=1e-6 if norm is None else norm.eps)
+
+    def forward_normed(self, x, norm, layer_fn, defer: bool = False):
         """forward(x, lambda v: layer_fn(norm(v))) with the RMSNorm ``norm``
-        (chassis.RMSNorm) fused into the mapping kernel."""
-        if self._tracked(x):
+        (chassis.RMSNorm) fused into the mapping kernel.  ``x`` may be a
+        PendingUpdate of the previous stream; with ``defer`` the result is
+        returned as one (inference only)."""
+        if isinstance(x, PendingUpdate) and self._tracked(x.x):
+            x = x.materialize()
+        if not isinstance(x, PendingUpdate) and self._tracked(x):
             return self._forward_autograd(x, norm, layer_fn)
-        dt = act_dtype(x)
-        x = x.to(dt)
-        layer_in, _, h_post, h_res = self._pre(x, dt, norm=norm)
+        fused = None
+        if isinstance(x, PendingUpdate):
+            dt = act_dtype(x.x)
+            fused = self._post_pre(x, dt, norm)
+            if fused is None:
+                x = x.materialize()
+        if fused is not None:
+            x, layer_in, _, h_post, h_res = fused
+        else:
+            dt = act_dtype(x)
+            x = x.to(dt)
+            layer_in, _, h_post, h_res = self._pre(x, dt, norm=norm)
         out = layer_fn(layer_in)
+        if defer:
+            return PendingUpdate(x, out, h_res, h_post)
         return kernels.mhc_post(x, out, h_res, h_post)
 
 
@@ -317,19 +367,27 @@ class mHCLlamaBlock(nn.Module):
         self.ffn_stream = mHCResidualStream(config.n_embd, n_streams)
 
     def forward(self, x, freqs_cis, kv_cache=None, layer_idx=0):
+        return materialize(self.forward_deferred(x, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx))
+
+    def forward_deferred(self, x, freqs_cis, kv_cache=None, layer_idx=0):
+        """forward() for x a tensor or a PendingUpdate; the FFN stream's
+        update may come back pending (applied by the next block's first
+        mapping kernel)."""
         # attn_stream(x, attention(attention_norm(.))) then
         # ffn_stream(x, feed_forward(ffn_norm(.))) (mhc.py:507-534), with each
-        # RMSNorm fused into its stream's mapping kernel
+        # RMSNorm fused into its stream's mapping kernel and each stream
+        # update fused into the next stream's mapping kernel
         x = self.attn_stream.forward_normed(
             x, self.attention_norm,
-            lambda v: self.attention(v, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx))
+            lambda v: self.attention(v, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx), defer=True)
         ff = self.feed_forward
+        defer = not self.use_channel_mod
         if self._moe:
             # the stream update rounds the FFN output to the stream dtype
             # (autocast matmul, mhc.py:374-377), so produce it in that dtype
-            x = self.ffn_stream.forward_normed(x, self.ffn_norm, lambda v: ff(v, out_dtype=v.dtype))
+            x = self.ffn_stream.forward_normed(x, self.ffn_norm, lambda v: ff(v, out_dtype=v.dtype), defer=defer)
         else:
-            x = self.ffn_stream.forward_normed(x, self.ffn_norm, ff)
+            x = self.ffn_stream.forward_normed(x, self.ffn_norm, ff, defer=defer)
         if self.use_channel_mod:
             # x + channel_mod(norm(x)) on the [B*n, T, C] view of the
             # contiguous [B, T, n, C] streams (mhc.py:528-532): a "group" of T
@@ -388,7 +446,8 @@ class mHCWalsh(nn.Module):
         h = h.to(dt).view(B, T, self.n_streams, self.config.n_embd)
         freqs_cis = self.freqs_cis[start_pos:start_pos + T]
         for layer_idx, layer in enumerate(self.layers):
-            h = layer(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
+            h = layer.forward_deferred(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
+        h = materialize(h)
         h_flat = h.reshape(B, T, self.n_streams * self.config.n_embd)
         h_out = self.norm(self.stream_merge(h_flat))
         if targets is not None:
