@@ -322,6 +322,20 @@ int walsh_decode_attention(const void *q, int64_t q_bs, int64_t q_hs, const void
                            void *o, int64_t o_bs, int64_t o_hs, int dtype, void *workspace, int64_t workspace_bytes,
                            void *stream);
 
+/* walsh_prefill_attention: causal self-attention of T queries against the
+ *   same T keys per (sequence, head), F.scaled_dot_product_attention(q, k,
+ *   v, is_causal=True) of CausalSelfAttention.forward without a cache
+ *   (src/model/chassis.py:465): o = softmax(q k^T * scale, key <= query) v.
+ *   Element (b, h, t, d) of q at b*q_sb + h*q_sh + t*q_st + d, of k and v at
+ *   b*kv_sb + h*kv_sh + t*kv_st + d, of o at b*o_sb + h*o_sh + t*o_st + d
+ *   (any of the [B, T, H, D] or [B, H, T, D] layouts).  bf16 only; head_dim
+ *   D in {16, 32, 64, 128}; strides multiples of 8 elements, pointers
+ *   16-byte aligned.  Scores, softmax and sums in float32, the
+ *   probabilities rounded to bf16 for the product with v. */
+int walsh_prefill_attention(const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void *k, const void *v,
+                            int64_t kv_sb, int64_t kv_sh, int64_t kv_st, int64_t B, int64_t H, int64_t T, int64_t D,
+                            float scale, void *o, int64_t o_sb, int64_t o_sh, int64_t o_st, int dtype, void *stream);
+
 /* ------------------------------------------------------------------ A14-A17
  * mHC residual streams.  Stream tensors are [M tokens][n streams][C] with row
  * stride ldx >= n*C (elements); n <= 4 and C % 4 == 0 in this build.

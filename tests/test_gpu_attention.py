@@ -59,3 +59,29 @@ def test_decode_attention_matches_sdpa_in_model_view():
     o = kernels.decode_attention(q, k, v)
     ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float())
     assert_close(o.float().cpu().numpy(), ref.cpu().numpy(), torch.bfloat16, "model view vs SDPA")
+
+
+@pytest.mark.parametrize("B,H,T,D,layout", [(2, 32, 1024, 16, "bthd"), (1, 4, 37, 16, "bthd"), (2, 3, 64, 32, "bhtd"),
+                                            (1, 8, 200, 64, "bthd"), (1, 4, 130, 128, "bhtd"), (2, 2, 1, 16, "bthd"),
+                                            (1, 8, 1024, 128, "bthd"), (1, 2, 3000, 16, "bthd")])
+def test_prefill_attention_vs_oracle(B, H, T, D, layout):
+    """Causal prefill attention (walsh_prefill_attention) against the float64
+    oracle on the bf16-rounded inputs; q/k/v read in place from the
+    projections' [B, T, H, D] rows or from [B, H, T, D] tensors.  head_dim 16
+    up to about 2,300 positions runs the whole-head kernel, the rest (T =
+    3000 included) the chunked one."""
+    from src.model import kernels
+    print(f"prefill case B={B} H={H} T={T} D={D} {layout}", flush=True)
+    g = torch.Generator().manual_seed(B * 11 + T + D)
+    shape = (B, T, H, D) if layout == "bthd" else (B, H, T, D)
+    q, k, v = (torch.randn(*shape, generator=g).to(torch.bfloat16).cuda() for _ in range(3))
+    if layout == "bthd":
+        q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+    assert kernels.prefill_attention_supported(q, k, v)
+    o = kernels.prefill_attention(q, k, v)
+    o2 = kernels.prefill_attention(q, k, v)
+    torch.cuda.synchronize()
+    assert o.shape == (B, H, T, D) and o.is_contiguous()
+    assert torch.equal(o, o2)
+    ref = oatt.causal_attention_f64(*(t.double().cpu().numpy() for t in (q, k, v)))
+    assert_close(o.double().cpu().numpy(), ref, torch.bfloat16, f"prefill B={B} H={H} T={T} D={D}")

@@ -181,6 +181,293 @@ static int dec_split(int64_t L, int64_t BH, int *chunk) {
     return (int)ceil_div(L, *chunk);
 }
 
+// ---------------------------------------------------------------- causal prefill
+// softmax(q k^T / sqrt(D) + causal mask) v for T queries against the same T
+// keys per (sequence, head): CausalSelfAttention.forward without a cache
+// (chassis.py:465, F.scaled_dot_product_attention(..., is_causal=True)).
+//
+// Flash-style, bf16 on 16x16x16 matrix cores.  A workgroup takes 64 queries
+// (16 per wave) of one (sequence, head) and walks the keys up to its last
+// query in chunks staged in LDS (K row-major, V transposed).  Each
+// wave computes S^T = K Q^T, so a lane holds 4 keys of ONE query (query =
+// lane % 16): the running max / sum of a query live in its 4 lanes and the
+// probabilities are already the B operand of O^T = V^T P^T, whose output a
+// lane again holds for its own query, as it does the row sums (a product of
+// a ones matrix with P^T on the matrix core).  No shuffles beyond the two of
+// the row max per 64 keys.  Keys are staged 256 (D = 16) to 64 (D >= 64) at
+// a time, the next chunk's loads in flight while the current one is used.
+// Scores are float32; the probabilities are rounded to bf16 for the
+// products with V and with ones (the normalisation uses the weights that
+// are applied), as the reference's bf16 SDPA rounds them.  The softmax
+// is VALU-bound at small head_dim (one exponential per score).
+constexpr int kPfQ = 64;   // queries per workgroup
+
+struct PfArgs {
+    const uint16_t *q, *k, *v;
+    uint16_t *o;
+    int64_t q_sb, q_sh, q_st;        // element (b, h, t, d) at b*sb + h*sh + t*st + d
+    int64_t kv_sb, kv_sh, kv_st;
+    int64_t o_sb, o_sh, o_st;
+    int T, nqt;
+    float sl2;                       // scale * log2(e)
+};
+
+// One 64-key step of the online softmax for a wave's 16 queries.  K rows
+// kl[key * ks + d], V transposed vt[d * vs + key] (LDS); key index kbase +
+// r for LDS row r.  FULL: every key of the step is at or before the wave's
+// first query (no mask); otherwise keys past each query are masked and
+// 16-key blocks wholly after the wave's last query are skipped.
+struct AttnState {
+    f32x4 acc[8];      // O^T tiles (D / 16 used)
+    f32x4 lacc;        // every entry: this lane's query's sum of p
+    float m_run;
+};
+
+template <int D, bool FULL>
+__device__ __forceinline__ void attn_step(AttnState &st, const u32x2 (&qf)[D / 16], const uint16_t *kl, int ks,
+                                          const uint16_t *vt, int vs, int r0, int k0, int qw, int qi, int n, int kq,
+                                          float sl2) {
+    constexpr int ND = D / 16;
+    const u32x2 ones = {0x3f803f80u, 0x3f803f80u};   // four bf16 1.0
+    f32x4 s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int kb = k0 + 16 * j;
+        if (!FULL && kb > qw + 15) {           // wave-uniform
+            s[j] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            continue;
+        }
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < ND; ++c) {
+            const u32x2 kf = *(const u32x2 *)(kl + (r0 + 16 * j + n) * ks + 16 * c + 4 * kq);
+            t = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, kf),
+                                                         __builtin_bit_cast(i16x4, qf[c]), t, 0, 0, 0);
+        }
+        // t[i]: S[query qi][key kb + 4kq + i], unscaled (the scale is folded
+        // into the exponent; scale > 0 keeps the max)
+        if (!FULL && kb + 15 > qw) {           // the diagonal block: mask keys past the query
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (kb + 4 * kq + i > qi) t[i] = -INFINITY;
+        }
+        s[j] = t;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0].x, s[0].y), fmaxf(s[0].z, s[0].w)),
+                     fmaxf(fmaxf(s[1].x, s[1].y), fmaxf(s[1].z, s[1].w)));
+    mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[2].x, s[2].y), fmaxf(s[2].z, s[2].w)),
+                         fmaxf(fmaxf(s[3].x, s[3].y), fmaxf(s[3].z, s[3].w))));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(st.m_run, mx);
+    // v_exp_f32 directly: arguments are <= 0 (or -inf -> 0); results below
+    // the float32 normal range flush to zero
+    const float alpha = __builtin_amdgcn_exp2f((st.m_run - m_new) * sl2);
+    st.m_run = m_new;
+    const float moff = -m_new * sl2;
+    u32x2 pf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(fmaf(s[j][i], sl2, moff));
+        pf[j] = u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+    }
+    st.lacc *= alpha;
+#pragma unroll
+    for (int c = 0; c < ND; ++c) st.acc[c] *= alpha;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (!FULL && k0 + 16 * j > qw + 15) continue;
+        // row sums of the (bf16) probabilities on the matrix core:
+        // ones(16 x 16 keys) P^T puts sum_k P[query][k] in every row
+        st.lacc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, ones),
+                                                           __builtin_bit_cast(i16x4, pf[j]), st.lacc, 0, 0, 0);
+#pragma unroll
+        for (int c = 0; c < ND; ++c) {
+            const u32x2 vf = *(const u32x2 *)(vt + (16 * c + n) * vs + r0 + 16 * j + 4 * kq);
+            st.acc[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, vf),
+                                                                 __builtin_bit_cast(i16x4, pf[j]), st.acc[c], 0, 0, 0);
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void attn_store(const AttnState &st, uint16_t *op, int kq) {
+    const float inv = 1.0f / st.lacc[0];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        // acc[c][i]: O[query][d = 16c + 4kq + i]
+        const f32x4 r = st.acc[c] * inv;
+        *(u32x2 *)(op + 16 * c + 4 * kq) = u32x2{pack_bf16x2(r.x, r.y), pack_bf16x2(r.z, r.w)};
+    }
+}
+
+// Keys per LDS chunk: as many as keep the tile near 20 KB, so a chunk's
+// global loads are few round trips per workgroup.
+template <int D> struct PfKC { static constexpr int value = D == 16 ? 256 : D == 32 ? 128 : 64; };
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_attn_kernel(PfArgs a) {
+    constexpr int ND = D / 16;
+    constexpr int KC = PfKC<D>::value;
+    constexpr int KS = D + 4;                        // padded K row (bank spread)
+    constexpr int VS = KC + 4;                       // padded row of the transposed V tile
+    constexpr int PIECES = KC * D / 8;               // 16-byte pieces per tensor per chunk
+    constexpr int PPT = (2 * PIECES + 255) / 256;    // pieces per thread
+    __shared__ __align__(16) uint16_t k_l[KC * KS];
+    __shared__ __align__(16) uint16_t vt_l[D * VS];
+    const int qt = a.nqt - 1 - (int)blockIdx.x;      // longest query tiles first
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, kq = lane >> 4;
+    const int qw = qt * kPfQ + wave * 16;            // this wave's first query
+    const int qi = qw + n;                           // this lane's query
+    const int qc = qi < a.T ? qi : a.T - 1;
+    const int kend = (qt + 1) * kPfQ;                // keys this workgroup can need
+
+    u32x2 qf[ND];
+    {
+        const uint16_t *qp = a.q + b * a.q_sb + h * a.q_sh + (int64_t)qc * a.q_st;
+#pragma unroll
+        for (int c = 0; c < ND; ++c) qf[c] = *(const u32x2 *)(qp + 16 * c + 4 * kq);
+    }
+    AttnState st;
+#pragma unroll
+    for (int c = 0; c < ND; ++c) st.acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.lacc = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m_run = -INFINITY;
+
+    const uint16_t *kbase = a.k + b * a.kv_sb + h * a.kv_sh;
+    const uint16_t *vbase = a.v + b * a.kv_sb + h * a.kv_sh;
+    uint4 stg[PPT];
+    // keys at or past kend are neither loaded nor read; keys past T are
+    // loaded from row T - 1 (finite values that the causal mask zeroes)
+    auto gload = [&](int ch) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int p = tid + 256 * i;
+            const int tensor = p >= PIECES, pp = p - tensor * PIECES;
+            const int key = pp / (D / 8), part = pp - key * (D / 8);
+            int kidx = ch * KC + key;
+            if (p < 2 * PIECES && kidx < kend) {
+                kidx = kidx < a.T ? kidx : a.T - 1;
+                stg[i] = *(const uint4 *)((tensor ? vbase : kbase) + (int64_t)kidx * a.kv_st + part * 8);
+            }
+        }
+    };
+    auto lstore = [&](int ch) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int p = tid + 256 * i;
+            const int tensor = p >= PIECES, pp = p - tensor * PIECES;
+            const int key = pp / (D / 8), part = pp - key * (D / 8);
+            if (p < 2 * PIECES && ch * KC + key < kend) {
+                if (!tensor) {
+                    u32x2 *d = (u32x2 *)(k_l + key * KS + part * 8);
+                    d[0] = u32x2{stg[i].x, stg[i].y};
+                    d[1] = u32x2{stg[i].z, stg[i].w};
+                } else {
+                    const uint32_t w[4] = {stg[i].x, stg[i].y, stg[i].z, stg[i].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        vt_l[(part * 8 + 2 * e) * VS + key] = (uint16_t)(w[e] & 0xffffu);
+                        vt_l[(part * 8 + 2 * e + 1) * VS + key] = (uint16_t)(w[e] >> 16);
+                    }
+                }
+            }
+        }
+    };
+
+    const int nch = (kend + KC - 1) / KC;
+    gload(0);
+    for (int ch = 0; ch < nch; ++ch) {
+        __syncthreads();       // the previous chunk's readers are done
+        lstore(ch);
+        __syncthreads();
+        if (ch + 1 < nch) gload(ch + 1);   // next chunk in flight during this one
+        // 64-key steps.  Steps wholly at or before this wave's first query
+        // (all but the last one or two) take the unmasked path; the step
+        // holding the diagonal masks keys past each query and skips 16-key
+        // blocks wholly after the wave's last query.
+#pragma unroll 1
+        for (int sb = 0; sb < KC / 64; ++sb) {
+            const int k0 = ch * KC + sb * 64;
+            if (k0 > qw + 15) break;                   // wave-uniform
+            if (k0 + 63 <= qw) attn_step<D, true>(st, qf, k_l, KS, vt_l, VS, sb * 64, k0, qw, qi, n, kq, a.sl2);
+            else attn_step<D, false>(st, qf, k_l, KS, vt_l, VS, sb * 64, k0, qw, qi, n, kq, a.sl2);
+        }
+    }
+    if (qi < a.T) attn_store<D>(st, a.o + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st, kq);
+}
+
+// Whole-head variant, for heads whose K and V fit in LDS together (T_pad *
+// D * 4 bytes plus padding; head_dim 16 up to about 2,300 positions): one
+// workgroup of 16 waves per (sequence, head) stages K (row-major) and V
+// (transposed) once, then each wave takes 16-query sub-tiles in a snake
+// order (w, 31 - w, 32 + w, 63 - w, ...) so every wave gets about the same
+// number of key steps.  No barriers after the staging.  (gridDim.z
+// workgroups may share a head, each taking its share of the sub-tiles; one
+// measured fastest at head_dim 16, T = 1024: 51 us against 60 us for two.)
+constexpr int kPhWaves = 16;
+
+template <int D>
+__global__ __launch_bounds__(64 * kPhWaves) void prefill_attn_head_kernel(PfArgs a, int tpad) {
+    constexpr int ND = D / 16;
+    extern __shared__ __align__(16) uint16_t ph_smem[];
+    const int ks = D;                    // K row: D / 2 dwords (16 B-aligned rows, bank-spread at D = 16)
+    const int vs = tpad + 16;            // V^T row: (tpad + 16) / 2 dwords = 8 mod 64 banks
+    uint16_t *k_l = ph_smem;                         // [tpad][D]
+    uint16_t *vt_l = ph_smem + tpad * D;             // [D][vs]
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // gridDim.z workgroups share a head: global wave index over them
+    const int nw = kPhWaves * (int)gridDim.z, wave = (int)blockIdx.z * kPhWaves + (tid >> 6);
+    const int n = lane & 15, kq = lane >> 4;
+    const uint16_t *kbase = a.k + b * a.kv_sb + h * a.kv_sh;
+    const uint16_t *vbase = a.v + b * a.kv_sb + h * a.kv_sh;
+    // stage K and V^T; rows T .. tpad - 1 are zeros (finite, masked)
+    for (int p = tid; p < tpad * (D / 8); p += 64 * kPhWaves) {
+        const int key = p / (D / 8), part = p - key * (D / 8);
+        uint4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+        if (key < a.T) {
+            kv = *(const uint4 *)(kbase + (int64_t)key * a.kv_st + part * 8);
+            vv = *(const uint4 *)(vbase + (int64_t)key * a.kv_st + part * 8);
+        }
+        *(uint4 *)(k_l + key * ks + part * 8) = kv;
+        const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            vt_l[(part * 8 + 2 * e) * vs + key] = (uint16_t)(w[e] & 0xffffu);
+            vt_l[(part * 8 + 2 * e + 1) * vs + key] = (uint16_t)(w[e] >> 16);
+        }
+    }
+    __syncthreads();
+    const int nst = tpad / 16;
+    for (int i = 0;; ++i) {
+        const int stile = nw * i + ((i & 1) ? nw - 1 - wave : wave);
+        if (nw * i >= nst) break;
+        if (stile >= nst) continue;
+        const int qw = 16 * stile, qi = qw + n;
+        const int qc = qi < a.T ? qi : a.T - 1;
+        u32x2 qf[ND];
+        const uint16_t *qp = a.q + b * a.q_sb + h * a.q_sh + (int64_t)qc * a.q_st;
+#pragma unroll
+        for (int c = 0; c < ND; ++c) qf[c] = *(const u32x2 *)(qp + 16 * c + 4 * kq);
+        AttnState st;
+#pragma unroll
+        for (int c = 0; c < ND; ++c) st.acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        st.lacc = f32x4{0.f, 0.f, 0.f, 0.f};
+        st.m_run = -INFINITY;
+#pragma unroll 1
+        for (int k0 = 0; k0 <= qw + 15; k0 += 64) {
+            if (k0 + 63 <= qw) attn_step<D, true>(st, qf, k_l, ks, vt_l, vs, k0, k0, qw, qi, n, kq, a.sl2);
+            else attn_step<D, false>(st, qf, k_l, ks, vt_l, vs, k0, k0, qw, qi, n, kq, a.sl2);
+        }
+        if (qi < a.T) attn_store<D>(st, a.o + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st, kq);
+    }
+}
+
 }  // namespace walsh
 
 using namespace walsh;
@@ -234,5 +521,43 @@ WALSH_EXPORT int walsh_decode_attention(const void *q, int64_t q_bs, int64_t q_h
         else WALSH_DEC(float, 16);
     }
 #undef WALSH_DEC
+    return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int walsh_prefill_attention(const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void *k,
+                                         const void *v, int64_t kv_sb, int64_t kv_sh, int64_t kv_st, int64_t B,
+                                         int64_t H, int64_t T, int64_t D, float scale, void *o, int64_t o_sb,
+                                         int64_t o_sh, int64_t o_st, int dtype, void *stream) {
+    const char *fn = "walsh_prefill_attention";
+    if (B < 0 || H <= 0 || T < 0 || B > 65535 || H > 65535 || T > (1 << 24))
+        return set_error(WALSH_EINVAL, "%s: bad shape B=%lld H=%lld T=%lld", fn, (long long)B, (long long)H,
+                         (long long)T);
+    if (D != 16 && D != 32 && D != 64 && D != 128)
+        return set_error(WALSH_ENOTSUP, "%s: head_dim %lld (16, 32, 64 or 128)", fn, (long long)D);
+    if (dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype %d (bf16 only)", fn, dtype);
+    if (B == 0 || T == 0) return WALSH_OK;
+    if (!q || !k || !v || !o) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    const int64_t st[9] = {q_sb, q_sh, q_st, kv_sb, kv_sh, kv_st, o_sb, o_sh, o_st};
+    for (int i = 0; i < 9; ++i)
+        if (st[i] % 8 || st[i] < 0)
+            return set_error(WALSH_ENOTSUP, "%s: strides must be non-negative multiples of 8 elements", fn);
+    if ((uintptr_t)q % 16 || (uintptr_t)k % 16 || (uintptr_t)v % 16 || (uintptr_t)o % 16)
+        return set_error(WALSH_ENOTSUP, "%s: q, k, v, o must be 16-byte aligned", fn);
+    PfArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o, q_sb, q_sh, q_st,
+             kv_sb, kv_sh, kv_st, o_sb, o_sh, o_st, (int)T, (int)ceil_div(T, kPfQ), scale * 1.4426950408889634f};
+    hipStream_t s = (hipStream_t)stream;
+    // whole heads in LDS when they fit (tpad rows of K and of V^T, padded)
+    const int64_t tpad = ceil_div(T, 64) * 64;
+    const int64_t head_lds = (tpad * D + D * (tpad + 16)) * 2;
+    if (D == 16 && head_lds <= device_info().max_shared_per_block) {
+        launch(prefill_attn_head_kernel<16>, dim3((unsigned)H, (unsigned)B, 1u), dim3(64 * kPhWaves),
+               (uint32_t)head_lds, s, a, (int)tpad);
+        return check_hip(hipGetLastError(), fn);
+    }
+    const dim3 G((unsigned)a.nqt, (unsigned)H, (unsigned)B);
+    if (D == 16) launch(prefill_attn_kernel<16>, G, dim3(256), 0, s, a);
+    else if (D == 32) launch(prefill_attn_kernel<32>, G, dim3(256), 0, s, a);
+    else if (D == 64) launch(prefill_attn_kernel<64>, G, dim3(256), 0, s, a);
+    else launch(prefill_attn_kernel<128>, G, dim3(256), 0, s, a);
     return check_hip(hipGetLastError(), fn);
 }

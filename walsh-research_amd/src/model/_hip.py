@@ -68,6 +68,8 @@ SIGNATURES = {
                                  _P, _I64, _I, _P]),
     "walsh_chanmod_bwd": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, ctypes.c_float,
                                ctypes.c_float, _P, _I64, _P, _P, _I, _P, _I64, _P]),
+    "walsh_prefill_attention": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                     ctypes.c_float, _P, _I64, _I64, _I64, _I, _P]),
     "walsh_sinkhorn_fwd": (_I, [_P, _I64, _I64, _I64, ctypes.c_float, _P, _P]),
     "walsh_sinkhorn_bwd": (_I, [_P, _P, _I64, _I64, _I64, ctypes.c_float, _P, _P]),
     "walsh_mhc_pre_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float, _I64, ctypes.c_float,

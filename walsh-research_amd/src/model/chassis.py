@@ -243,6 +243,10 @@ class CausalSelfAttention(nn.Module):
                 total = k.size(2)
                 mask = torch.ones(T, total, dtype=torch.bool, device=q.device).tril(diagonal=total - T)
                 y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=drop)
+            elif (not tracked and drop == 0 and kernels.prefill_attention_preferred(q)
+                  and kernels.prefill_attention_supported(q, k, v)):
+                # causal prefill on the matrix cores, q / k / v read in place
+                y = kernels.prefill_attention(q, k, v)
             else:
                 y = F.scaled_dot_product_attention(q, k, v, is_causal=True, dropout_p=drop)
         y = y.to(att_dt)
