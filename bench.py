@@ -4,7 +4,8 @@ Workload (the configuration the headline metric is quoted on): full
 mHCWalsh forward, random init, bf16 autocast, n_layer 16, n_head 32,
 n_embd 512, Hadamard algebra with head mixing, 4 mHC streams, MoE and channel
 modulation off, tokens uniform over a 50257 vocabulary, batch 8 x seq 1024.
-A step is one forward over that batch (inputs resident in HBM).
+A step is one forward over that batch (inputs resident in HBM), replayed
+as one captured HIP graph (``--eager`` times the launches one by one).
 
 Other workloads (``--workload``), each printing one JSON line of its own:
   moe       HadamardMoE alone, bf16 autocast, n_embd 512 (16 experts, k = 6),
@@ -61,6 +62,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-roofline", action="store_true", help="skip the instrumented pass (profiling runs)")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
     ap.add_argument("--workload", default="mhcwalsh",
                     choices=["mhcwalsh", "moe", "octonion", "hadamard", "prefill5", "decode5", "hadamard_bwd",
                              "train2", "walsh_load", "chanmod"])
@@ -170,9 +172,21 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    run = step
+    graph = None
+    if not args.eager:
+        # the forward as one HIP graph (captured once, after the warmup has
+        # built the weight caches): the same kernels, without the host's
+        # per-launch cost between them
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        run = graph.replay
+        run()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        run()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms = dt * 1000.0 / args.steps
@@ -215,6 +229,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "execution": "eager launches" if graph is None else "one HIP graph per forward (captured after warmup)",
     }
     if kernels is not None:
         line["kernels"] = {k: dict(launches_per_step=v["launches"] // args.steps,

@@ -91,3 +91,29 @@ def test_state_dict_roundtrip_and_weight_cache():
     m2.load_state_dict(sd)
     with torch.no_grad():
         assert torch.equal(m2(idx)[0], a)
+
+
+def test_forward_hip_graph_replays_match_eager():
+    """The bf16 forward captured as one HIP graph (how bench.py times it):
+    every replay, with eager work and synchronisation in between, gives
+    bitwise the eager logits and hidden states."""
+    C, n_layer, vocab, T = 512, 2, 256, 128
+    cfg, model = _model(C, n_layer, vocab, T)
+    _perturb(model)
+    idx = torch.randint(0, vocab, (2, T), generator=torch.Generator().manual_seed(5)).cuda()
+
+    def fwd():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return model(idx, return_hidden=True)
+    ref_logits, _, ref_hid = fwd()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out_logits, _, out_hid = fwd()
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_logits, ref_logits), f"replay {i}: logits"
+        assert torch.equal(out_hid, ref_hid), f"replay {i}: hidden"
+        fwd()   # eager work between replays
+        torch.cuda.synchronize()
