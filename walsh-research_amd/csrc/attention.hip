@@ -193,8 +193,8 @@ static int dec_split(int64_t L, int64_t BH, int *chunk) {
 // lane % 16): the running max / sum of a query live in its 4 lanes and the
 // probabilities are already the B operand of O^T = V^T P^T, whose output a
 // lane again holds for its own query, as it does the row sums (a product of
-// a ones matrix with P^T on the matrix core).  No shuffles beyond the two of
-// the row max per 64 keys.  Keys are staged 256 (D = 16) to 64 (D >= 64) at
+// a ones matrix with P^T on the matrix core).  The row max per 64 keys takes
+// two lane swaps.  Keys are staged 256 (D = 16) to 64 (D >= 64) at
 // a time, the next chunk's loads in flight while the current one is used.
 // Scores are float32; the probabilities are rounded to bf16 for the
 // products with V and with ones (the normalisation uses the weights that
@@ -217,6 +217,19 @@ struct PfArgs {
 // r for LDS row r.  FULL: every key of the step is at or before the wave's
 // first query (no mask); otherwise keys past each query are masked and
 // 16-key blocks wholly after the wave's last query are skipped.
+// max over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (a query's lanes) with
+// the gfx950 row / half swaps (VALU; no LDS traffic as ds_bpermute has):
+// permlane16_swap exchanges odd rows of one operand with even rows of the
+// other, permlane32_swap the upper half of one with the lower half of the
+// other, so with both operands equal each pair of results covers the pair.
+__device__ __forceinline__ float max_over_rows(float v) {
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    const u2 a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a.x), __uint_as_float(a.y));
+    const u2 b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b.x), __uint_as_float(b.y));
+}
+
 struct AttnState {
     f32x4 acc[8];      // O^T tiles (D / 16 used)
     f32x4 lacc;        // every entry: this lane's query's sum of p
@@ -257,8 +270,7 @@ __device__ __forceinline__ void attn_step(AttnState &st, const u32x2 (&qf)[D / 1
                      fmaxf(fmaxf(s[1].x, s[1].y), fmaxf(s[1].z, s[1].w)));
     mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[2].x, s[2].y), fmaxf(s[2].z, s[2].w)),
                          fmaxf(fmaxf(s[3].x, s[3].y), fmaxf(s[3].z, s[3].w))));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_over_rows(mx);
     const float m_new = fmaxf(st.m_run, mx);
     // v_exp_f32 directly: arguments are <= 0 (or -inf -> 0); results below
     // the float32 normal range flush to zero
