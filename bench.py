@@ -413,6 +413,26 @@ def bench_hadamard(torch, args):
                  {"workload": "HadamardLinear(512, 512), x [4, 256, 512]", "global_batch": 4, "seq_len": 256,
                   "parallelism": "single GPU"}, roof, cpu)
     line["sweep"] = sweep
+    # the same layer in bf16 (the dtype of the model configs) at prefill row counts
+    sweep16 = []
+    for rows in (65536, 262144, 1048576):
+        nbuf = max(1, min(16, (768 << 20) // (rows * 512 * 2 * 2)))
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        xs = [torch.randn(rows, 512, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(nbuf)]
+
+        def step16(i):
+            with torch.no_grad():
+                return lin(xs[i % nbuf])
+        iters = max(args.steps, 20)
+        dt = _time_steps(torch, step16, iters, args.warmup)
+        with _hip.LaunchTimer() as lt:
+            for i in range(iters):
+                step16(i)
+        r = _roofline_of(lt.summary(), iters)
+        sweep16.append(dict(rows=rows, us_per_call=round(dt * 1e6, 2), kernel_us=r["avg_launch_us"],
+                            kernel_gbs=r["achieved"], frac=r["frac"], rotated_buffers=nbuf))
+        del xs
+    line["sweep_bf16"] = sweep16
     return line
 
 
