@@ -106,7 +106,9 @@ __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a, esz));
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * esz));
     const int n_tiles = (int)ceil_div(a.M, kTile);
-    const int stride = nblk * kWaves;
+    const int wt = a.wave_tiles > 0 ? a.wave_tiles : kWaves;
+    if (wave >= wt) return;   // after the set-up barrier; the tile loop has none
+    const int stride = nblk * wt;
     auto contract_any = [&](int nt, int c, const XM<BF16MMA> &xm, f32x4 (&acc)[32]) {
         if constexpr (DENSE)
             contract_dense<BF16MMA>(smem + ((size_t)(nt * a.Kc + c) * 32 * 64 + lane) * dense_frag_bytes<BF16MMA>(),
@@ -115,7 +117,7 @@ __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int
             contract<BF16MMA>(a, nt, c, lane, xm, lut, acc);
     };
 
-    for (int tile = blk * kWaves + wave; tile < n_tiles; tile += stride) {
+    for (int tile = blk * wt + wave; tile < n_tiles; tile += stride) {
         const int row = tile * kTile + t;
         const bool row_ok = row < a.M;
         const uint32_t xoff = row_ok ? x_row_off(a, row, esz) : 0u;
@@ -665,9 +667,11 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1) ? 2 : 1) void hadamard_s
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)g.M * g.ldx * esz));
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(g.y, (uint32_t)((int64_t)g.M * g.ldy * esz));
     const int n_items = (int)ceil_div(g.M, kTile) * g.Nt;
-    const int stride = gridDim.x * kWaves;
+    const int wt = g.wave_tiles > 0 ? g.wave_tiles : kWaves;
+    if (wave >= wt) return;   // after the set-up barrier; the item loop has none
+    const int stride = gridDim.x * wt;
 
-    for (int item = blockIdx.x * kWaves + wave; item < n_items; item += stride) {
+    for (int item = blockIdx.x * wt + wave; item < n_items; item += stride) {
         const int tile = item / g.Nt, nt = item - tile * g.Nt;
         const int row = tile * kTile + t;
         const bool row_ok = row < g.M;
@@ -949,6 +953,15 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
         a.M = (int)rows;
         int64_t work = ceil_div(rows, kTile) * (swiglu ? Nt : 1);
         int64_t grid = ceil_div(work, kWaves);
+        const int64_t resident = (int64_t)device_info().cu_count * 2;   // two workgroups per CU
+        if (Kc == 1 && vec && bf16 && work <= resident * kWaves) {
+            // all the work fits in one residency round of this variant: give
+            // each workgroup ceil(work / resident) working waves, so every CU
+            // holds the same number of them
+            const int64_t wt = ceil_div(work, resident);
+            a.wave_tiles = (int)wt;
+            grid = ceil_div(work, wt);
+        }
         if (grid > cap) grid = cap;
         const dim3 G((unsigned)grid), B(kThreads);
         if (swiglu) {
@@ -1004,7 +1017,7 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
 
 static HadArgs had_args(const void *x, int64_t ldx, int64_t gsx, int64_t in_o, int64_t out_o, const uint8_t *kw,
                         const float *alpha, const float *beta, void *y, int64_t ldy, int64_t gsy) {
-    HadArgs a;
+    HadArgs a{};
     a.x = x;
     a.ldx = ldx;
     a.M = 0;
@@ -1027,6 +1040,7 @@ static HadArgs had_args(const void *x, int64_t ldx, int64_t gsx, int64_t in_o, i
     a.rope_T = 1;
     a.rope_D = 4;
     a.rope_row0 = 0;
+    a.wave_tiles = 0;
     return a;
 }
 

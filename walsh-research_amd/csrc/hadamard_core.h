@@ -60,6 +60,10 @@ struct HadArgs {
     const float *rope;
     int rope_T, rope_D;
     int rope_row0;  // row 0 of this launch is row rope_row0 of a sequence
+    // waves of a workgroup that take tiles (1..4; 0 means all 4).  With
+    // fewer tiles than wavefronts on the chip, one working wave per
+    // workgroup spreads the tiles over every CU instead of a quarter of them.
+    int wave_tiles;
 };
 
 // The (cos, sin) of the lane's two output pairs o0..o0+3 (o0 % 4 == 0,
