@@ -953,8 +953,10 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
         a.M = (int)rows;
         int64_t work = ceil_div(rows, kTile) * (swiglu ? Nt : 1);
         int64_t grid = ceil_div(work, kWaves);
-        const int64_t resident = (int64_t)device_info().cu_count * 2;   // two workgroups per CU
-        if (Kc == 1 && vec && bf16 && work <= resident * kWaves) {
+        // workgroups per CU these bf16 variants hold (register-bound: two for
+        // one input chunk, one for the chunk loop)
+        const int64_t resident = (int64_t)device_info().cu_count * (Kc == 1 ? 2 : 1);
+        if (vec && bf16 && work <= resident * kWaves) {
             // all the work fits in one residency round of this variant: give
             // each workgroup ceil(work / resident) working waves, so every CU
             // holds the same number of them
