@@ -582,7 +582,7 @@ def bench_train2(torch, args):
     model.train()
     gen = torch.Generator().manual_seed(2)
     tgt = torch.randint(0, cfg.vocab_size, idx.shape, generator=gen).cuda()
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True, capturable=not args.eager)
     tokens = args.batch * args.seq
 
     def step(i=0):
@@ -594,7 +594,31 @@ def bench_train2(torch, args):
         return loss
 
     steps = max(1, min(args.steps, 10))
-    dt = _time_steps(torch, step, steps, max(1, min(args.warmup, 2)))
+    run, execution = step, "eager launches"
+    if not args.eager:
+        # the whole step (forward, backward, AdamW) as one HIP graph: the
+        # step is host-bound eagerly (57 ms of kernels in ~64 ms); warmup on
+        # a side stream of default priority, then capture
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    step()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            opt.zero_grad(set_to_none=True)
+            with torch.cuda.graph(graph):
+                with torch.autocast("cuda", dtype=torch.bfloat16):
+                    _, static_loss = model(idx, targets=tgt)
+                static_loss.backward()
+                opt.step()
+            run = lambda i=0: graph.replay()  # noqa: E731
+            execution = "one HIP graph per training step (captured after warmup)"
+        except Exception as e:  # capture is an optimisation: fall back to eager steps
+            torch.cuda.synchronize()
+            execution = f"eager launches (graph capture failed: {type(e).__name__}: {e})"[:200]
+    dt = _time_steps(torch, run, steps, max(1, min(args.warmup, 2)))
     roof = None
     if not args.no_roofline:
         with _hip.LaunchTimer() as lt:
@@ -626,7 +650,7 @@ def bench_train2(torch, args):
                  "synthetic: random-init weights, tokens and targets uniform over 50257",
                  {"workload": "mHCWalsh training step, n_layer 16, n_head 32, n_embd 512, hadamard + head mixing, "
                               "4 mHC streams, MoE off, bf16 autocast, AdamW", "global_batch": args.batch,
-                  "seq_len": args.seq, "parallelism": "single GPU"}, roof, cpu)
+                  "seq_len": args.seq, "parallelism": "single GPU"}, roof, cpu) | {"execution": execution}
 
 
 def bench_walsh_load(torch, args):

@@ -428,3 +428,54 @@ def test_stream_mixing_bwd(K, n, C, dtype):
     assert_close(dhq.cpu().numpy(), hqr.grad.numpy(), dtype, "dh_post")
     assert_close(dout.float().cpu().numpy(), orr.grad.numpy(), dtype, "d_out")
     assert_close((dx1.float() + dx2.float()).cpu().numpy(), xr.grad.numpy(), dtype, "dx")
+
+
+def test_training_step_hip_graph_matches_eager():
+    """A training step (forward with targets, backward, AdamW) captured as one
+    HIP graph, how bench.py's train2 runs it: three replays move the
+    parameters as three eager steps do (float32; torch's embedding backward
+    sums with atomics, so the bar is a relative 1e-5 over all parameters),
+    with eager work and synchronisation between the replays."""
+    from src.model import WalshConfig, mHCWalsh
+    C, n_layer, vocab, T = 64, 2, 256, 32
+    cfg = WalshConfig(block_size=64, vocab_size=vocab, n_layer=n_layer, n_head=32, n_embd=C, algebra='hadamard',
+                      head_mixing=True)
+    g = torch.Generator().manual_seed(3)
+    idx = torch.randint(0, vocab, (2, T), generator=g).cuda()
+    tgt = torch.randint(0, vocab, (2, T), generator=g).cuda()
+    models = []
+    for _ in range(2):
+        torch.manual_seed(0)
+        m = mHCWalsh(cfg, n_streams=4).cuda().train()
+        models.append((m, torch.optim.AdamW(m.parameters(), lr=1e-3, foreach=True, capturable=True)))
+
+    def step(m, opt):
+        opt.zero_grad(set_to_none=True)
+        _, loss = m(idx, targets=tgt)
+        loss.backward()
+        opt.step()
+
+    (ma, oa), (mb, ob) = models
+    for _ in range(3):
+        step(ma, oa)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step(mb, ob)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    ob.zero_grad(set_to_none=True)
+    with torch.cuda.graph(graph):
+        _, loss = mb(idx, targets=tgt)
+        loss.backward()
+        ob.step()
+    for i in range(3):
+        step(ma, oa)
+        graph.replay()
+        torch.cuda.synchronize()
+        pa = torch.cat([p.detach().reshape(-1) for p in ma.parameters()])
+        pb = torch.cat([p.detach().reshape(-1) for p in mb.parameters()])
+        rel = ((pa - pb).norm() / pa.norm()).item()
+        print(f"replay {i}: parameter rel diff {rel:.2e}", flush=True)
+        assert rel <= 1e-5, (i, rel)
