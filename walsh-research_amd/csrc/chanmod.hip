@@ -12,16 +12,20 @@
 // where xn is the module input or, fused for the block (mhc.py:531,
 // moe.py:796-798), RMSNorm(x) * w, with x + out written.
 //
-// Three kernels:
-//   colsum  per-column sums of a T-chunk of a group (the bulk state, or in
-//           the backward the sums of g*x and g), one float partial per
-//           (group, chunk): deterministic, no atomics;
-//   mlp     sums the partials in a fixed order and runs the two small
-//           products for up to 4 groups per workgroup (W1/W2 rows are read
-//           once per workgroup, not once per group);
-//   apply   one wave per row, per-column scale/shift tables in LDS.
-// The bulk and the apply each read the input once: 2 reads + 1 write of it
-// in all, HBM-bound.
+// Kernels (all sums in a fixed order: deterministic, no atomics):
+//   colsum     per-column sums of a T-chunk of a group (the bulk state, or
+//              in the backward the sums of g*x and g), one float partial per
+//              (group, chunk); each wave keeps 1-8 rows' loads in flight;
+//   mlp_fused  one 16-wave workgroup per group: the partials summed, then
+//              both products of the MLP (used while hidden * C <= 2^19);
+//   bulk + mlp the same in three launches for a wide MLP: partial sums,
+//              then each product for 4 groups x 16 rows per workgroup (W1 /
+//              W2 rows read once per workgroup, not once per group);
+//   apply      RB rows per wave, per-column scale / shift / norm tables in
+//              LDS built while the rows' loads are in flight;
+//   bwd_reduce the backward's per-(group, block) sums of the partials.
+// The colsum and the apply each read the input once: 2 reads + 1 write of
+// it in all, HBM- (at small sizes latency-) bound.
 #include "common.h"
 
 namespace walsh {
