@@ -31,6 +31,12 @@ Pinning (what makes each function trustworthy, checked in
 * ``mhc``      -- Sinkhorn invariants (row sums 1 after the last step,
   column sums -> 1, n=1 gives [[1]]), float64 closed-form iteration,
   sigmoid bounds, stream update with an identity layer.
-* ``model``    -- assembled from the pinned pieces; pinned end to end by
-  the golden fixture in ``tests/golden`` where one exists.
+* ``model``    -- assembled from the pinned pieces, and pinned end to end
+  by the golden fixtures of ``tests/golden`` (written from the reference's
+  own modules on the CPU by ``tests/golden/make_fixtures.py``): two small
+  mHCWalsh models (SwiGLU with head mixing; MoE with channel modulation),
+  HadamardMoE, the three stream mappings and one stream, Sinkhorn,
+  HadamardLinear and the octonion layer (``tests/test_oracle_model.py``).
+  Each method of ``Oracle`` is also checked against the function-level
+  oracle of the same step.
 """
