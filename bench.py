@@ -55,8 +55,8 @@ METRIC = "tokens/sec through Walsh layer stack at 1 GPU; % of HBM roofline (GB/s
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--batch", type=int, default=8)
     ap.add_argument("--seq", type=int, default=1024)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
@@ -118,10 +118,48 @@ def build_model(torch, batch, seq):
     return cfg, model, idx
 
 
+def cpu_setup(torch):
+    """Run the CPU baseline on the physical cores this process may use: the
+    affinity set's distinct (package, core) pairs from sysfs, capped by
+    OMP_NUM_THREADS when set; torch.set_num_threads to that count.  Returns
+    the host record reported beside every CPU figure."""
+    import subprocess
+    aff = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in aff:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                core = f.read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", str(c)))
+    host = {"affinity_cpus": len(aff), "physical_cores_in_affinity": len(cores)}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        f = {k.strip(): v.strip() for k, v in (ln.split(":", 1) for ln in out.splitlines() if ":" in ln)}
+        host["lscpu_model"] = f.get("Model name")
+        host["lscpu_n_phys"] = int(f.get("Socket(s)", "0")) * int(f.get("Core(s) per socket", "0"))
+        host["lscpu_threads_per_core"] = int(f.get("Thread(s) per core", "1"))
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    n = len(cores)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        host["omp_num_threads"] = int(omp)
+        n = min(n, int(omp))
+    torch.set_num_threads(max(1, n))
+    host["torch_threads"] = torch.get_num_threads()
+    return host
+
+
 def cpu_baseline(torch, model, cfg, seq, budget_s):
     """Oracle float32 forward on the host cores: 1 x seq tokens per call,
     repeated until the budget is spent (at least once)."""
     from oracle.model import Oracle
+    host = cpu_setup(torch)
     threads = torch.get_num_threads()
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     orc = Oracle(sd, cfg.n_embd, cfg.n_head, cfg.n_layer, n_streams=4)
@@ -138,7 +176,7 @@ def cpu_baseline(torch, model, cfg, seq, budget_s):
                 break
     return dict(value=round(reps * seq / el, 2), unit="tokens/s", cores=threads, kind="port",
                 sample=f"{reps} x (1 x {seq} tokens) of the same 16-layer forward in float32 "
-                       f"(oracle/model.py), {el:.1f} s on {threads} threads")
+                       f"(oracle/model.py), {el:.1f} s on {threads} threads", host=host)
 
 
 def main():
@@ -191,6 +229,7 @@ def main():
     dt = time.perf_counter() - t0
     ms = dt * 1000.0 / args.steps
     value = tokens * args.steps / dt
+    sustained = _sustained(torch, run)
 
     roofline = None
     kernels = None
@@ -208,6 +247,15 @@ def main():
                         frac=round(achieved / HBM_PEAK_GBS, 4), traffic=measured_traffic(dom), kernel=dom,
                         avg_launch_us=round(avg_ms * 1000, 2), launches_per_step=d["launches"] // args.steps,
                         algorithmic_bytes_per_launch=int(bytes_per_launch))
+        # the whole forward: every hot-path kernel's algorithmic bytes per
+        # step over the measured time per step (torch's embedding, stream
+        # projection / merge and LM head are not counted)
+        fwd_bytes = sum(v["bytes"] for v in kernels.values()) / args.steps
+        whole = fwd_bytes / (ms * 1e-3) / 1e9
+        roofline["whole_forward"] = dict(algorithmic_bytes_per_step=int(fwd_bytes), achieved=round(whole, 1),
+                                         frac=round(whole / HBM_PEAK_GBS, 4),
+                                         kernel_ms_per_step=round(sum(v["ms"] for v in kernels.values())
+                                                                  / args.steps, 3))
 
     cpu = None if args.no_cpu else cpu_baseline(torch, model, cfg, args.seq, args.cpu_seconds)
 
@@ -230,6 +278,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "execution": "eager launches" if graph is None else "one HIP graph per forward (captured after warmup)",
+        "sustained": sustained,
     }
     if kernels is not None:
         line["kernels"] = {k: dict(launches_per_step=v["launches"] // args.steps,
@@ -237,6 +286,24 @@ def main():
                                    gbs=round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1),
                                    ms_per_step=round(v["ms"] / args.steps, 3)) for k, v in kernels.items()}
     print(json.dumps(line), flush=True)
+
+
+def _sustained(torch, run, min_s=1.0, min_reps=50, block=10):
+    """Steps timed in blocks of ``block`` until at least ``min_s`` seconds and
+    ``min_reps`` steps have run: median and spread of ms per step over the
+    blocks (a steadier figure beside the K-step timed region)."""
+    per, t_all, n = [], time.perf_counter(), 0
+    while time.perf_counter() - t_all < min_s or n < min_reps:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(block):
+            run()
+        torch.cuda.synchronize()
+        per.append((time.perf_counter() - t0) * 1000.0 / block)
+        n += block
+    per.sort()
+    return dict(steps=n, seconds=round(time.perf_counter() - t_all, 2), median_ms_per_step=round(per[len(per) // 2], 4),
+                min_ms_per_step=round(per[0], 4), max_ms_per_step=round(per[-1], 4))
 
 
 def _time_steps(torch, step, steps, warmup):
@@ -303,6 +370,7 @@ def bench_moe(torch, args):
     roof = _roofline_of(lt.summary(), args.steps)
     cpu = None
     if not args.no_cpu:
+        host = cpu_setup(torch)
         from oracle.moe import moe_forward
         sd = {k: v.detach().cpu().float().numpy() for k, v in m.state_dict().items()}
         xc = xs[0].float().cpu().numpy().reshape(-1, C)[:1024]
@@ -313,6 +381,7 @@ def bench_moe(torch, args):
             reps += 1
         el = time.perf_counter() - t0
         cpu = dict(value=round(reps * 1024 / el, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   host=host,
                    sample=f"{reps} x 1024 tokens through oracle/moe.py (numpy float64, all-expert einsum as the "
                           f"reference), {el:.1f} s")
     return _line("tokens/sec through the Hadamard MoE FFN at 1 GPU; % of HBM roofline (GB/s)", B * T / dt,
@@ -347,6 +416,7 @@ def bench_octonion(torch, args):
     roof = _roofline_of(lt.summary(), args.steps, bound="mfma")
     cpu = None
     if not args.no_cpu:
+        host = cpu_setup(torch)
         import numpy as np
         from oracle.octonion import octonion_linear_f64
         codes = np.sign(layers[0].weight.detach().cpu().numpy())  # timing only: any ternary matrix
@@ -358,6 +428,7 @@ def bench_octonion(torch, args):
             reps += 1
         el = time.perf_counter() - t0
         cpu = dict(value=round(reps * 2048 / 8 / el, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   host=host,
                    sample=f"{reps} x one layer on 2048 tokens (oracle/octonion.py, 64 block matmuls as the reference "
                           f"CPU path), {el:.1f} s; tokens/s of the 8-layer stack = layer rate / 8")
     return _line("tokens/sec through the octonion ternary linear stack at 1 GPU; % of MFMA roofline",
@@ -395,6 +466,7 @@ def bench_hadamard(torch, args):
             roof, dt1 = r, dt
     cpu = None
     if not args.no_cpu:
+        host = cpu_setup(torch)
         import numpy as np
         from oracle.hadamard import hadamard_linear_torch32
         codes = np.sign(lin.weight.detach().cpu().numpy())
@@ -405,6 +477,7 @@ def bench_hadamard(torch, args):
             reps += 1
         el = time.perf_counter() - t0
         cpu = dict(value=round(reps * 1024 / el, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   host=host,
                    sample=f"{reps} x [4, 256, 512] float32 through oracle/hadamard.py (the reference CPU einsums), "
                           f"{el:.1f} s")
     line = _line("tokens/sec through one Hadamard ternary linear at 1 GPU; % of HBM roofline (GB/s)",
@@ -474,6 +547,7 @@ def bench_hadamard_bwd(torch, args):
                     "reduction) against the minimal traffic: x and gy read once, gx written once")
     cpu = None
     if not args.no_cpu:
+        host = cpu_setup(torch)
         import numpy as np
         from oracle.hadamard import sylvester
         torch.manual_seed(1)
@@ -497,6 +571,7 @@ def bench_hadamard_bwd(torch, args):
             x.grad = a.grad = b.grad = w.grad = None
             reps += 1
         cpu = dict(value=round(reps * M / t_bwd, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   host=host,
                    sample=f"{reps} backward passes of [1024, 512] float32 through the reference's CPU einsum graph "
                           f"(torch autograd), {t_bwd:.1f} s of backward")
     line = _line("tokens/sec through one Hadamard ternary linear backward at 1 GPU; % of HBM roofline (GB/s)",
@@ -546,6 +621,7 @@ def bench_chanmod(torch, args):
                     "minimal traffic: x read once and y written once (the kernels read x twice)")
     cpu = None
     if not args.no_cpu:
+        host = cpu_setup(torch)
         from oracle.model import Oracle
         sd = {"cm." + k: v.detach().float().cpu() for k, v in cm.state_dict().items()}
         orc = Oracle(sd, C, 1, 0)
@@ -560,6 +636,7 @@ def bench_chanmod(torch, args):
             reps += 1
         el = time.perf_counter() - t0
         cpu = dict(value=round(reps * G * T / el, 1), unit="rows/s", cores=torch.get_num_threads(), kind="port",
+                   host=host,
                    sample=f"{reps} passes of the reference's float32 CPU graph (RMSNorm, mean, ternary MLP, "
                           f"per-block modulation, residual) over [32, 1024, 512], {el:.1f} s")
     line = _line("rows/sec through the block's channel modulation at 1 GPU; % of HBM roofline (GB/s)",
@@ -631,6 +708,7 @@ def bench_train2(torch, args):
                                        ms_per_step=round(v["ms"] / steps, 3)) for k, v in summ.items()}
     cpu = None
     if not args.no_cpu:
+        host = cpu_setup(torch)
         from oracle.model import Oracle
         sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
         orc = Oracle(sd, cfg.n_embd, cfg.n_head, cfg.n_layer, n_streams=4, grad=True, grad_dtype=torch.float32)
@@ -642,6 +720,7 @@ def bench_train2(torch, args):
             reps += 1
         el = time.perf_counter() - t0
         cpu = dict(value=round(reps * seq / el, 2), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   host=host,
                    sample=f"{reps} x (1 x {seq} tokens) forward + backward of the same 16-layer model in float32 "
                           f"through the oracle (the reference's torch CPU graph, autograd), {el:.1f} s; no "
                           f"optimizer step")
@@ -694,6 +773,7 @@ def bench_walsh_load(torch, args):
                     "one call (word counts + scan, block-sum scan, decode) timed together")
     cpu = None
     if not args.no_cpu:
+        host = cpu_setup(torch)
         import numpy as np
         from oracle import ternary as otern
         from oracle import walsh_format as owf
@@ -732,6 +812,7 @@ def _config5_cpu(torch, model, cfg, args, tokens):
     """Oracle float32 forward of the first layer on a bounded token sample,
     scaled to the 24-layer stack (layers cost the same)."""
     from oracle.model import Oracle
+    host = cpu_setup(torch)
     keep = ("tok_embeddings.", "output.", "stream_proj.", "stream_merge.", "norm.", "freqs_cis", "layers.0.")
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items() if k.startswith(keep)}
     orc = Oracle(sd, cfg.n_embd, cfg.n_head, 1, n_streams=4, use_moe=True, moe_max_experts=6)
@@ -744,7 +825,7 @@ def _config5_cpu(torch, model, cfg, args, tokens):
             reps += 1
     el = time.perf_counter() - t0
     rate = reps * tokens / el / cfg.n_layer
-    return dict(value=round(rate, 2), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+    return dict(value=round(rate, 2), unit="tokens/s", cores=torch.get_num_threads(), kind="port", host=host,
                 sample=f"{reps} x (1 x {tokens} tokens) through one layer of the oracle float32 forward "
                        f"(oracle/model.py) in {el:.1f} s; rate divided by the 24 layers (extrapolated)")
 

@@ -48,9 +48,12 @@ def sigmoid(a):
 
 
 def rms_eps(dtype) -> float:
-    """``F.rms_norm`` with eps=None uses finfo(input dtype).eps
-    (``mhc.py:291``): 2^-23 for float32, 2^-7 for bfloat16."""
-    return {np.float32: 2.0 ** -23, 'bfloat16': 2.0 ** -7, np.float64: 2.0 ** -52}[dtype]
+    """The epsilon ``F.rms_norm(x, shape)`` adds when eps is None
+    (``mhc.py:291``): torch normalises in the op-math type (float32 for a
+    bfloat16 input) and uses that type's epsilon, so 2^-23 for float32 and
+    bfloat16 inputs alike, 2^-52 for float64 (checked bit for bit against
+    torch's own rms_norm in the oracle tests)."""
+    return {np.float32: 2.0 ** -23, 'bfloat16': 2.0 ** -23, np.float64: 2.0 ** -52}[dtype]
 
 
 def mapping(x_flat, phi, alpha, bias, kind: str, n: int, eps: float, n_iter: int = 20) -> np.ndarray:

@@ -27,6 +27,58 @@ def absmean_gamma_exact(w) -> float:
     return float(np.abs(np.asarray(w, dtype=np.float64)).mean() + EPS_GAMMA)
 
 
+def exact_abs_sum(w):
+    """sum(|W|) of float32 values as an exact rational (numerator, denominator).
+
+    Every float32 is m * 2^(s - 149) with an integer m < 2^24 and
+    0 <= s < 255, so the sum is an integer over 2^149: the mantissas are
+    summed per exponent (float64 sums of at most 2^29 integers below 2^24
+    are exact) and combined as Python integers."""
+    a = np.abs(np.ascontiguousarray(w, dtype=np.float32)).ravel()
+    bits = a.view(np.uint32).astype(np.int64)
+    exp = (bits >> 23) & 0xFF
+    man = bits & 0x7FFFFF
+    man = np.where(exp > 0, man | 0x800000, man)
+    shift = np.where(exp > 0, exp - 1, 0)
+    assert a.size < (1 << 29) and not np.any(exp == 0xFF), "finite inputs below 2^29 elements"
+    per = np.bincount(shift, weights=man.astype(np.float64), minlength=1)
+    total = 0
+    for s, v in enumerate(per):
+        if v:
+            total += int(v) << s
+    return total, 1 << 149
+
+
+def round_to_f32(num: int, den: int) -> np.float32:
+    """num/den rounded to the nearest float32, ties to even (exact rational
+    comparison of the candidates around the double quotient)."""
+    from fractions import Fraction
+    q = Fraction(num, den)
+    f = np.float32(num / den)            # Python int division is correctly rounded to double
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    best = None
+    for c in cands:
+        d = abs(Fraction(float(c)) - q)
+        if best is None or d < best[0] or (d == best[0] and int(np.float32(c).view(np.uint32)) % 2 == 0):
+            best = (d, c)
+    return np.float32(best[1])
+
+
+def absmean_gamma_rounded(w) -> np.float32:
+    """gamma = mean(|W|) + 1e-8 (``physics.py:24``, ``moe.py:279``) with the
+    mean rounded correctly: the exact mean of the float32 weights rounded to
+    the nearest float32, then the float32 addition of 1e-8 (torch casts the
+    Python scalar to the tensor's float32 first).
+
+    This is the value a float32 reduction approximates; torch-CPU's own
+    ``abs().mean()`` lands within an ulp of it, and which ulp depends on
+    the reduction order and on the number of threads torch uses."""
+    num, den = exact_abs_sum(w)
+    n = int(np.asarray(w).size)
+    mean = round_to_f32(num, den * n)
+    return np.float32(mean + np.float32(EPS_GAMMA))
+
+
 def ternary_codes(w, gamma) -> np.ndarray:
     """codes = clamp(round_half_even(W / gamma), -1, 1) as int8.
 

@@ -479,3 +479,33 @@ def test_training_step_hip_graph_matches_eager():
         rel = ((pa - pb).norm() / pa.norm()).item()
         print(f"replay {i}: parameter rel diff {rel:.2e}", flush=True)
         assert rel <= 1e-5, (i, rel)
+
+
+@pytest.mark.parametrize("use_moe", [False, True])
+def test_gradient_checkpointing_matches_plain_backward(use_moe):
+    """mHCWalsh(gradient_checkpointing=True) in training recomputes each
+    layer in the backward (mhc.py:647-649): the loss and every parameter's
+    gradient equal the run without checkpointing (float32, the backward
+    kernels are deterministic)."""
+    from src.model import WalshConfig, mHCWalsh
+    C, n_layer, vocab, T = 64, 2, 256, 16
+    grads = []
+    for ckpt in (False, True):
+        torch.manual_seed(0)
+        cfg = WalshConfig(block_size=64, vocab_size=vocab, n_layer=n_layer, n_head=32, n_embd=C,
+                          algebra='hadamard', head_mixing=True, use_moe=use_moe, moe_max_experts=2)
+        model = mHCWalsh(cfg, n_streams=4, gradient_checkpointing=ckpt).cuda().train()
+        g = torch.Generator().manual_seed(1)
+        idx = torch.randint(0, vocab, (2, T), generator=g).cuda()
+        tgt = torch.randint(0, vocab, (2, T), generator=g).cuda()
+        _, loss = model(idx, targets=tgt)
+        loss.backward()
+        torch.cuda.synchronize()
+        grads.append((loss.item(), {n: p.grad.detach().clone() for n, p in model.named_parameters()}))
+    (l0, g0), (l1, g1) = grads
+    print(f"moe={use_moe}: loss {l0:.7f} / checkpointed {l1:.7f}")
+    assert abs(l0 - l1) <= 1e-6 * abs(l0)
+    assert g0.keys() == g1.keys()
+    for n in g0:
+        d = (g0[n] - g1[n]).norm().item()
+        assert d <= 1e-6 * g0[n].norm().item() + 1e-12, f"{n}: |diff| {d:.3e}"

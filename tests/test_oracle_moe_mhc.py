@@ -171,8 +171,25 @@ def test_stream_identity_layer_closed_form():
 
 
 def test_rms_eps_values():
+    """F.rms_norm(x, shape) with eps=None, the mappings' normalisation
+    (mhc.py:291): for float32 and bfloat16 inputs alike it equals
+    x * rsqrt(mean(x.float()^2) + 2^-23) rounded to the input dtype, bit for
+    bit -- torch normalises in float32 and takes float32's epsilon, not the
+    bfloat16 epsilon 2^-7 (which would differ by up to a factor of 4 on
+    rows of RMS ~0.02, the scale of the embedding-initialised streams)."""
     assert mhc.rms_eps(np.float32) == float(torch.finfo(torch.float32).eps)
-    assert mhc.rms_eps('bfloat16') == float(torch.finfo(torch.bfloat16).eps)
+    assert mhc.rms_eps('bfloat16') == float(torch.finfo(torch.float32).eps)
+    gen = torch.Generator().manual_seed(0)
+    for dtype in (torch.float32, torch.bfloat16):
+        for scale in (1e-3, 0.02, 1.0, 30.0):
+            x = (torch.randn(64, 512, generator=gen) * scale).to(dtype)
+            eps = mhc.rms_eps(np.float32 if dtype == torch.float32 else 'bfloat16')
+            xf = x.float()
+            ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(dtype)
+            assert torch.equal(torch.nn.functional.rms_norm(x, (512,)), ref), (dtype, scale)
+            if dtype == torch.bfloat16 and scale <= 0.02:
+                wrong = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 2.0 ** -7)).to(dtype)
+                assert not torch.equal(torch.nn.functional.rms_norm(x, (512,)), wrong)
 
 
 def test_sinkhorn_bwd_matches_torch_autograd_and_finite_differences():

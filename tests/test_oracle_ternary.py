@@ -36,6 +36,57 @@ def test_gamma_matches_exact_mean():
         assert abs(float(g) - exact) <= 4 * np.spacing(np.float32(exact)), (n, g, exact)
 
 
+def test_rounded_gamma_closed_forms():
+    """Correct rounding of the mean, ties to even: mean(1, 1 + 2^-23) =
+    1 + 2^-24 lies halfway between 1 and 1 + 2^-23 and rounds to 1;
+    mean(1, 1 + 3*2^-23) = 1 + 3*2^-24 rounds up to 1 + 2^-22 (even);
+    equal values give themselves; subnormals are summed exactly."""
+    one = np.float32(1.0)
+    u = np.float32(2.0 ** -23)
+    m = lambda a: ternary.round_to_f32(*_mean_rational(a))  # noqa: E731
+    assert m(np.array([one, one + u], np.float32)) == one
+    assert m(np.array([one, one + 3 * u], np.float32)) == np.float32(1 + 2.0 ** -22)
+    assert m(np.full(1000, np.float32(0.0123), np.float32)) == np.float32(0.0123)
+    tiny = np.float32(2.0 ** -149)
+    assert m(np.array([tiny, tiny, tiny, -tiny], np.float32)) == tiny
+    g = ternary.absmean_gamma_rounded(np.array([one, -one - u], np.float32))
+    assert g == np.float32(one + np.float32(1e-8))
+
+
+def _mean_rational(a):
+    num, den = ternary.exact_abs_sum(a)
+    return num, den * a.size
+
+
+def test_rounded_gamma_brute_force_and_torch():
+    """The exact integer sum equals a Fraction sum of the same floats; the
+    rounded mean is the float32 nearest to the exact mean; torch-CPU's
+    float32 abs().mean() (the reference's CPU expression) is within one ulp
+    of it at every thread count, and which ulp it lands on varies."""
+    from fractions import Fraction
+    import torch
+    rng = np.random.default_rng(11)
+    for n in (3, 100, 5000):
+        w = (rng.standard_normal(n) * 0.02).astype(np.float32)
+        num, den = ternary.exact_abs_sum(w)
+        assert Fraction(num, den) == sum(Fraction(float(abs(v))) for v in w)
+        q = Fraction(num, den * n)
+        r = ternary.round_to_f32(num, den * n)
+        for c in (np.nextafter(r, np.float32(-1)), np.nextafter(r, np.float32(1))):
+            assert abs(Fraction(float(r)) - q) <= abs(Fraction(float(c)) - q)
+    threads = torch.get_num_threads()
+    try:
+        for seed in range(4):
+            w = (np.random.default_rng(seed).standard_normal((128, 128, 32)) * 0.02).astype(np.float32)
+            g = ternary.absmean_gamma_rounded(w)
+            for nt in (1, 2, 4, 8):
+                torch.set_num_threads(nt)
+                gt = ternary.absmean_gamma(w)
+                assert abs(int(gt.view(np.int32)) - int(g.view(np.int32))) <= 1, (seed, nt, gt, g)
+    finally:
+        torch.set_num_threads(threads)
+
+
 def test_gamma_zero_tensor():
     w = np.zeros(64, np.float32)
     g = ternary.absmean_gamma(w)

@@ -1038,6 +1038,7 @@ static HadArgs had_args(const void *x, int64_t ldx, int64_t gsx, int64_t in_o, i
     a.ldy = ldy;
     a.tpb = 0;
     a.bstride = 0;
+    a.xspan = 0;
     a.rope = nullptr;
     a.rope_T = 1;
     a.rope_D = 4;
@@ -1234,6 +1235,7 @@ WALSH_EXPORT int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64
     a.M = (int)M;
     a.tpb = (int)T;
     a.bstride = x_bstride;
+    a.xspan = xspan;
     if (wide) {
         if (D % 4 || x_hstride % 4 || x_tstride % 4 || x_bstride % 4 || ldy % 4 || (uintptr_t)x % 8 ||
             (uintptr_t)y % 8)

@@ -550,6 +550,7 @@ WALSH_EXPORT int walsh_hadamard_linear_ex_bwd(const void *x, int64_t ldx, int64_
             h.kw3 = nullptr;
             h.tpb = 0;
             h.bstride = 0;
+            h.xspan = 0;
             h.rope = nullptr;
             h.rope_T = 1;
             h.rope_D = 4;

@@ -52,9 +52,12 @@ struct HadArgs {
     void *y;
     int64_t ldy;
     // x rows in batches (0: plain rows at ldx): row r sits at
-    // (r / tpb) * bstride + (r % tpb) * ldx elements
+    // (r / tpb) * bstride + (r % tpb) * ldx elements; xspan is the element
+    // extent of x those rows cover (the batch stride alone says nothing of
+    // it: a size-1 batch dimension may carry any stride)
     int tpb;
     int64_t bstride;
+    int64_t xspan;
     // rotary embedding on the outputs (null: none): pairs (2i, 2i+1) of each
     // rope_D-wide head turn by rope[t][i] = (cos, sin), t = row % rope_T
     const float *rope;
@@ -84,7 +87,7 @@ __device__ __forceinline__ uint32_t x_row_off(const HadArgs &a, int row, uint32_
 }
 
 __device__ __forceinline__ uint32_t x_bytes(const HadArgs &a, uint32_t esz) {
-    const int64_t e = a.tpb ? ceil_div(a.M, a.tpb) * a.bstride : (int64_t)a.M * a.ldx;
+    const int64_t e = a.tpb ? a.xspan : (int64_t)a.M * a.ldx;
     return (uint32_t)(e * esz);
 }
 

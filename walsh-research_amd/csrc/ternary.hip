@@ -10,13 +10,30 @@ namespace walsh {
 
 constexpr int kGammaThreads = 1024;
 
+// Error-free sum of two doubles (Knuth's TwoSum): s + e == a + b exactly.
+__device__ inline void two_sum(double a, double b, double &s, double &e) {
+    s = a + b;
+    const double z = s - a;
+    e = (a - (s - z)) + (b - z);
+}
+
 // One workgroup; fixed element->thread assignment and a fixed-shape tree, so
-// the float64 sum (and the float32 gamma) is identical on every run.
+// the result is identical on every run.  The sum of |w| is carried as a
+// double-double (hi + lo, TwoSum at every addition), about 100 bits, so the
+// float32 mean is the correctly rounded mean of the exact sum (the division
+// keeps the remainder through an fma) -- a value that does not depend on the
+// reduction order, unlike a float32 or plain float64 sum.
 __global__ __launch_bounds__(kGammaThreads) void gamma_kernel(const float *__restrict__ w, int64_t n,
                                                               float *__restrict__ gamma) {
-    __shared__ double part[kGammaThreads];
+    __shared__ double part_hi[kGammaThreads];
+    __shared__ double part_lo[kGammaThreads];
     const int t = threadIdx.x;
-    double acc = 0.0;
+    double hi = 0.0, lo = 0.0;
+    auto add = [&](float v) {
+        double e;
+        two_sum(hi, (double)fabsf(v), hi, e);
+        lo += e;
+    };
     const bool vec = ((uintptr_t)w & 15) == 0;
     int64_t head = 0;
     if (vec) {
@@ -24,22 +41,32 @@ __global__ __launch_bounds__(kGammaThreads) void gamma_kernel(const float *__res
         const f32x4 *w4 = (const f32x4 *)w;
         for (int64_t i = t; i < n4; i += kGammaThreads) {
             f32x4 v = w4[i];
-            acc += (double)fabsf(v.x);
-            acc += (double)fabsf(v.y);
-            acc += (double)fabsf(v.z);
-            acc += (double)fabsf(v.w);
+            add(v.x);
+            add(v.y);
+            add(v.z);
+            add(v.w);
         }
         head = n4 * 4;
     }
-    for (int64_t i = head + t; i < n; i += kGammaThreads) acc += (double)fabsf(w[i]);
-    part[t] = acc;
+    for (int64_t i = head + t; i < n; i += kGammaThreads) add(w[i]);
+    part_hi[t] = hi;
+    part_lo[t] = lo;
     __syncthreads();
     for (int s = kGammaThreads / 2; s > 0; s >>= 1) {
-        if (t < s) part[t] += part[t + s];
+        if (t < s) {
+            double h, e;
+            two_sum(part_hi[t], part_hi[t + s], h, e);
+            part_lo[t] = part_lo[t] + part_lo[t + s] + e;
+            part_hi[t] = h;
+        }
         __syncthreads();
     }
     if (t == 0) {
-        const float mean = (float)(part[0] / (double)n);
+        const double nd = (double)n, h = part_hi[0], l = part_lo[0];
+        double q = h / nd;
+        const double r = fma(-q, nd, h);  // h - q*n exactly
+        q += (r + l) / nd;
+        const float mean = (float)q;
         gamma[0] = mean + 1e-8f;
     }
 }

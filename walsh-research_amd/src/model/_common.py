@@ -22,12 +22,30 @@ def tracked_dtype(dt: torch.dtype) -> torch.dtype:
     return torch.float32 if dt == torch.bfloat16 else dt
 
 
+_EPOCH = [0]
+
+
+def invalidate_weight_caches() -> None:
+    """Drop every cached weight derivative (ternary codes, packed kernel
+    layouts, concatenated projections) of every module.
+
+    Needed after a parameter is written in a way autograd's version counter
+    does not see: through ``.data`` (``p.data.copy_(...)``,
+    ``p.data.clamp_(...)``) or by another process or library writing its
+    memory.  Optimizer steps, in-place writes on the parameter itself,
+    ``load_state_dict`` and ``.to()`` are detected without it."""
+    _EPOCH[0] += 1
+
+
 class WeightCache:
     """Caches a device-side derivative of a parameter (its ternary codes,
     packed layouts, concatenations ...) until the parameter changes.
 
-    The key is (data_ptr, _version, device, shape): an optimizer step bumps
-    ``_version`` and a ``.to()`` moves ``data_ptr``, so either rebuilds."""
+    The key is (data_ptr, _version, device, shape, dtype) plus a global
+    epoch: an optimizer step bumps ``_version``, a ``.to()`` moves
+    ``data_ptr``, and ``invalidate_weight_caches()`` bumps the epoch, so any
+    of them rebuilds.  A write through ``.data`` bumps none of these: call
+    ``invalidate_weight_caches()`` after one."""
 
     def __init__(self):
         self._key = None
@@ -35,6 +53,7 @@ class WeightCache:
 
     def get(self, tensors, build, extra=()):
         key = tuple((t.data_ptr(), t._version, t.device, tuple(t.shape), t.dtype) for t in tensors) + tuple(extra)
+        key = (_EPOCH[0],) + key
         if key != self._key:
             self._val = build()
             self._key = key

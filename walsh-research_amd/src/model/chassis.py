@@ -13,6 +13,7 @@ from dataclasses import dataclass
 from typing import List, Optional, Tuple
 
 import torch
+import torch.utils.checkpoint
 import torch.nn as nn
 from torch.nn import functional as F
 
@@ -359,7 +360,11 @@ class Walsh(nn.Module):
         h = self.tok_embeddings(idx)
         freqs_cis = self.freqs_cis[start_pos:start_pos + T]
         for layer_idx, layer in enumerate(self.layers):
-            h = layer(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
+            if self.training and torch.is_grad_enabled():
+                # every layer checkpointed in training (chassis.py:570-572)
+                h = torch.utils.checkpoint.checkpoint(layer, h, freqs_cis, use_reentrant=False)
+            else:
+                h = layer(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
         h = self.norm(h)
         if targets is not None:
             logits = self.output(h)

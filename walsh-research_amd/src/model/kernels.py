@@ -894,7 +894,10 @@ def mhc_pre_wide(x: torch.Tensor, phi_frag32: torch.Tensor, coef: torch.Tensor, 
     wsb = _hip.lib().walsh_mhc_pre_wide_workspace(M, n, C)
     ws = torch.empty(max(wsb, 4), device=dev, dtype=torch.uint8)
     esz = x.element_size()
-    nbytes = 2 * M * n * C * esz + M * C * esz + M * (2 * n + n * n) * 4 + 32 * n * C * esz
+    # algorithmic bytes: the stream rows read once (the projection and the
+    # apply launch each read them; the second read is measured traffic, not
+    # algorithmic), the layer input and the mappings written once, phi once
+    nbytes = M * n * C * esz + M * C * esz + M * (2 * n + n * n) * 4 + 32 * n * C * esz
     flops = M * (2 * n * C * 32 + 2 * n * C + 2 * n * C)
     _hip.call("walsh_mhc_pre_wide_fwd", xv.data_ptr(), n * C, M, n, C, phi_frag32.data_ptr(), coef.data_ptr(),
               bias_cat.data_ptr(), float(rms_eps), int(n_iter), float(sk_eps), h_pre.data_ptr(), h_post.data_ptr(),

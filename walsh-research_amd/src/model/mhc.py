@@ -8,11 +8,12 @@ layer function, then walsh_mhc_post_fwd (H_res @ x + H_post^T (x) out).
 import math
 
 import torch
+import torch.utils.checkpoint
 import torch.nn as nn
 import torch.nn.functional as F
 
 from . import kernels
-from ._common import WeightCache, act_dtype
+from ._common import WeightCache, act_dtype, invalidate_weight_caches
 
 _MAX_STREAMS = 4
 
@@ -90,9 +91,12 @@ class SinkhornKnopp(nn.Module):
 
 
 def _rms_eps(dtype: torch.dtype) -> float:
-    # F.rms_norm(x, ...) with eps=None uses finfo(x.dtype).eps (mhc.py:291);
-    # rms_norm has no autocast rule, so x keeps the activation dtype
-    return float(torch.finfo(dtype).eps)
+    # F.rms_norm(x, ...) with eps=None (mhc.py:291) normalises in the op-math
+    # type (float32 for bf16 / fp16 inputs) and takes that type's epsilon:
+    # 2^-23 for bf16 and fp32 activations, bit for bit the same as
+    # rsqrt(mean(x.float()^2) + 2^-23) rounded back to the input dtype.
+    # rms_norm has no autocast rule, so x keeps the activation dtype.
+    return float(torch.finfo(torch.float64 if dtype == torch.float64 else torch.float32).eps)
 
 
 def _phi_block(n: int, C: int, parts, dtype, device):
@@ -445,8 +449,16 @@ class mHCWalsh(nn.Module):
         dt = act_dtype(h)
         h = h.to(dt).view(B, T, self.n_streams, self.config.n_embd)
         freqs_cis = self.freqs_cis[start_pos:start_pos + T]
+        checkpointed = self.gradient_checkpointing and self.training and torch.is_grad_enabled()
         for layer_idx, layer in enumerate(self.layers):
-            h = layer.forward_deferred(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
+            if checkpointed:
+                # activation checkpointing per layer (mhc.py:647-649): the
+                # layer's forward is recomputed in the backward; it takes and
+                # returns plain tensors (no pending stream update crosses it)
+                h = torch.utils.checkpoint.checkpoint(layer.forward, materialize(h), freqs_cis, kv_cache, layer_idx,
+                                                      use_reentrant=False)
+            else:
+                h = layer.forward_deferred(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
         h = materialize(h)
         h_flat = h.reshape(B, T, self.n_streams * self.config.n_embd)
         h_out = self.norm(self.stream_merge(h_flat))
@@ -459,6 +471,12 @@ class mHCWalsh(nn.Module):
         if return_hidden:
             return logits, loss, h_out
         return logits, loss
+
+    def invalidate_weight_caches(self) -> None:
+        """Rebuild the ternary codes and kernel layouts on the next forward:
+        call after writing parameters through ``.data`` (which autograd's
+        version counter, the caches' change detector, does not see)."""
+        invalidate_weight_caches()
 
     @property
     def num_parameters(self):
