@@ -322,6 +322,22 @@ int walsh_decode_attention(const void *q, int64_t q_bs, int64_t q_hs, const void
                            void *o, int64_t o_bs, int64_t o_hs, int dtype, void *workspace, int64_t workspace_bytes,
                            void *stream);
 
+/* walsh_decode_attention_static: walsh_decode_attention without the
+ *   workspace; it allocates nothing.  No counterpart in the reference: it is
+ *   for callers that cannot allocate device memory (code under HIP graph
+ *   capture, serving loops, harnesses that forbid hipMalloc).  The split-K
+ *   partials live in a file-scope device array of the library, 8 MiB per GPU
+ *   (held until the process ends); a call whose partials need more
+ *   (B * H * S * (D + 2) * 4 bytes, the size walsh_decode_attention_workspace_bytes
+ *   reports) returns WALSH_ENOTSUP without launching.  Every call on one GPU
+ *   shares that GPU's array: calls that overlap on one GPU (other streams or
+ *   host threads) race and must be serialised by the caller.  Same arguments,
+ *   layouts and results as walsh_decode_attention (the same kernels). */
+int walsh_decode_attention_static(const void *q, int64_t q_bs, int64_t q_hs, const void *k, const void *v,
+                                  int64_t kv_bs, int64_t kv_hs, int64_t kv_rs, int64_t B, int64_t H, int64_t L,
+                                  int64_t D, float scale, void *o, int64_t o_bs, int64_t o_hs, int dtype,
+                                  void *stream);
+
 /* walsh_prefill_attention: causal self-attention of T queries against the
  *   same T keys per (sequence, head), F.scaled_dot_product_attention(q, k,
  *   v, is_causal=True) of CausalSelfAttention.forward without a cache

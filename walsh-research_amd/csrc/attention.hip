@@ -11,6 +11,8 @@
 // and divides by the global sum.  D/8 lanes share a key row, each reading 16
 // contiguous bytes (bf16) of it, so a wavefront reads 64/(D/8) whole rows per
 // load instruction.  The cache is read exactly once: the kernel is HBM-bound.
+#include <mutex>
+
 #include "common.h"
 
 namespace walsh {
@@ -491,11 +493,13 @@ WALSH_EXPORT int64_t walsh_decode_attention_workspace_bytes(int64_t B, int64_t H
     return B * H * S * (D + 2) * (int64_t)sizeof(float);
 }
 
-WALSH_EXPORT int walsh_decode_attention(const void *q, int64_t q_bs, int64_t q_hs, const void *k, const void *v,
-                                        int64_t kv_bs, int64_t kv_hs, int64_t kv_rs, int64_t B, int64_t H, int64_t L,
-                                        int64_t D, float scale, void *o, int64_t o_bs, int64_t o_hs, int dtype,
-                                        void *workspace, int64_t workspace_bytes, void *stream) {
-    const char *fn = "walsh_decode_attention";
+// The checks and the two launches of a decode attention call, with the
+// split-K partials at ``part`` (B * H * S * (D + 2) floats, every slot written
+// by the partial kernel before the combine reads it).
+static int decode_attention_run(const char *fn, const void *q, int64_t q_bs, int64_t q_hs, const void *k,
+                                const void *v, int64_t kv_bs, int64_t kv_hs, int64_t kv_rs, int64_t B, int64_t H,
+                                int64_t L, int64_t D, float scale, void *o, int64_t o_bs, int64_t o_hs, int dtype,
+                                float *part, int64_t part_bytes, bool static_part, void *stream) {
     if (B < 0 || H <= 0 || L <= 0 || B > 65535 || H > 65535 || L > (1 << 30))
         return set_error(WALSH_EINVAL, "%s: bad shape B=%lld H=%lld L=%lld", fn, (long long)B, (long long)H,
                          (long long)L);
@@ -503,22 +507,29 @@ WALSH_EXPORT int walsh_decode_attention(const void *q, int64_t q_bs, int64_t q_h
         return set_error(WALSH_ENOTSUP, "%s: head_dim %lld (16, 32, 64 or 128)", fn, (long long)D);
     if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype %d", fn, dtype);
     if (B == 0) return WALSH_OK;
-    if (!q || !k || !v || !o || !workspace) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (!q || !k || !v || !o || !part) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
     const int64_t vec = 8;
     if (q_bs % vec || q_hs % vec || kv_bs % vec || kv_hs % vec || kv_rs % vec || kv_rs < D ||
         (uintptr_t)q % 16 || (uintptr_t)k % 16 || (uintptr_t)v % 16)
         return set_error(WALSH_ENOTSUP, "%s: q / cache rows must be 16-byte aligned with strides multiple of 8", fn);
     int chunk;
     const int S = dec_split(L, B * H, &chunk);
-    if (workspace_bytes < B * H * S * (D + 2) * (int64_t)sizeof(float))
+    const int64_t need = B * H * S * (D + 2) * (int64_t)sizeof(float);
+    if (part_bytes < need) {
+        if (static_part)
+            return set_error(WALSH_ENOTSUP, "%s: B=%lld H=%lld L=%lld D=%lld need %lld bytes of split-K scratch, above "
+                             "the static maximum of %lld (use walsh_decode_attention with a workspace)", fn,
+                             (long long)B, (long long)H, (long long)L, (long long)D, (long long)need,
+                             (long long)part_bytes);
         return set_error(WALSH_EINVAL, "%s: workspace too small", fn);
-    DecArgs a{q, q_bs, q_hs, k, v, kv_bs, kv_hs, kv_rs, (int)L, chunk, S, scale, (float *)workspace};
+    }
+    DecArgs a{q, q_bs, q_hs, k, v, kv_bs, kv_hs, kv_rs, (int)L, chunk, S, scale, part};
     hipStream_t s = (hipStream_t)stream;
     const dim3 G((unsigned)S, (unsigned)H, (unsigned)B);
 #define WALSH_DEC(T, DD)                                                                                          \
     do {                                                                                                          \
         launch(decode_attn_partial_kernel<T, DD>, G, dim3(kDecThreads), 0, s, a);                                 \
-        launch(decode_attn_combine_kernel<T, DD>, dim3((unsigned)(B * H)), dim3(DD), 0, s, (const float *)workspace, \
+        launch(decode_attn_combine_kernel<T, DD>, dim3((unsigned)(B * H)), dim3(DD), 0, s, (const float *)part,     \
                S, (int)H, o, o_bs, o_hs);                                                                         \
     } while (0)
     if (dtype == WALSH_BF16) {
@@ -534,6 +545,58 @@ WALSH_EXPORT int walsh_decode_attention(const void *q, int64_t q_bs, int64_t q_h
     }
 #undef WALSH_DEC
     return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int walsh_decode_attention(const void *q, int64_t q_bs, int64_t q_hs, const void *k, const void *v,
+                                        int64_t kv_bs, int64_t kv_hs, int64_t kv_rs, int64_t B, int64_t H, int64_t L,
+                                        int64_t D, float scale, void *o, int64_t o_bs, int64_t o_hs, int dtype,
+                                        void *workspace, int64_t workspace_bytes, void *stream) {
+    return decode_attention_run("walsh_decode_attention", q, q_bs, q_hs, k, v, kv_bs, kv_hs, kv_rs, B, H, L, D, scale,
+                                o, o_bs, o_hs, dtype, (float *)workspace, workspace_bytes, false, stream);
+}
+
+// ---------------------------------------------------------------- allocation-free decode attention
+// walsh_decode_attention_static keeps the split-K partials in this file-scope
+// device array instead of a caller workspace, for callers that cannot
+// allocate.  Each GPU the library runs on holds its own copy until the
+// process ends; every call on one GPU shares it, so calls that overlap on one
+// GPU (other streams, other host threads) race on it.  Host code never passes
+// the array's name to a kernel: its device address comes from
+// hipGetSymbolAddress, looked up once per device on the first call there.
+constexpr int64_t kDecScratchBytes = 8ll << 20;
+constexpr int kScratchMaxDevices = 64;
+static __device__ __align__(256) float scratch[kDecScratchBytes / sizeof(float)];
+
+static int dec_scratch(const char *fn, float **out) {
+    static std::mutex mu;
+    static float *ptrs[kScratchMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return check_hip(e, fn);
+    if (dev < 0 || dev >= kScratchMaxDevices)
+        return set_error(WALSH_ENOTSUP, "%s: device %d beyond the %d this build tracks", fn, dev, kScratchMaxDevices);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptrs[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return check_hip(e, fn);
+        if (!p) return set_error(WALSH_EHIP, "%s: no device address for the scratch array", fn);
+        ptrs[dev] = (float *)p;
+    }
+    *out = ptrs[dev];
+    return WALSH_OK;
+}
+
+WALSH_EXPORT int walsh_decode_attention_static(const void *q, int64_t q_bs, int64_t q_hs, const void *k, const void *v,
+                                               int64_t kv_bs, int64_t kv_hs, int64_t kv_rs, int64_t B, int64_t H,
+                                               int64_t L, int64_t D, float scale, void *o, int64_t o_bs, int64_t o_hs,
+                                               int dtype, void *stream) {
+    const char *fn = "walsh_decode_attention_static";
+    float *part = nullptr;
+    const int rc = dec_scratch(fn, &part);
+    if (rc) return rc;
+    return decode_attention_run(fn, q, q_bs, q_hs, k, v, kv_bs, kv_hs, kv_rs, B, H, L, D, scale, o, o_bs, o_hs, dtype,
+                                part, kDecScratchBytes, true, stream);
 }
 
 WALSH_EXPORT int walsh_prefill_attention(const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void *k,

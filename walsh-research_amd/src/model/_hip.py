@@ -61,6 +61,8 @@ SIGNATURES = {
     "walsh_decode_attention_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "walsh_decode_attention": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
                                     _P, _I64, _I64, _I, _P, _I64, _P]),
+    "walsh_decode_attention_static": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                           ctypes.c_float, _P, _I64, _I64, _I, _P]),
     "walsh_chanmod_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "walsh_chanmod_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, ctypes.c_float, _P, _I64, _P, _I64, _P,
                                ctypes.c_float, ctypes.c_float, _I, _P, _I64, _P, _I, _P, _I64, _P]),

@@ -575,6 +575,27 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
     return o
 
 
+def decode_attention_static(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                            scale: float = None) -> torch.Tensor:
+    """decode_attention through walsh_decode_attention_static: the split-K
+    partials stay in the library's fixed per-GPU scratch array, so the call
+    allocates nothing (``out`` [B, H, 1, D] in q.dtype is the caller's).
+    Calls that overlap on one GPU race on that array; shapes whose partials
+    exceed it raise WalshHipError."""
+    _hip.require_device(q, "query")
+    B, H, _, D = q.shape
+    L = k.shape[2]
+    assert tuple(out.shape) == (B, H, 1, D) and out.dtype == q.dtype and out.stride(-1) == 1, "output view"
+    scale = 1.0 / (D ** 0.5) if scale is None else scale
+    esz = q.element_size()
+    _hip.call("walsh_decode_attention_static", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+              k.stride(0), k.stride(1), k.stride(2), B, H, L, D, float(scale), out.data_ptr(), out.stride(0),
+              out.stride(1), _hip.dtype_code(q.dtype), _hip.stream(q.device),
+              kernel="decode_attn_partial_kernel<%s,%d>" % ("bf16" if q.dtype == torch.bfloat16 else "f32", D),
+              nbytes=2 * B * H * L * D * esz + 2 * B * H * D * esz, flops=4 * B * H * L * D)
+    return out
+
+
 PREFILL_HEAD_DIMS = (16, 32, 64, 128)
 
 
