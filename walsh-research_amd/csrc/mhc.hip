@@ -1126,6 +1126,90 @@ __global__ __launch_bounds__(256) void mhc_apply_kernel(ApplyArgs a) {
     }
 }
 
+// The same per-token work for few tokens (decode): one 256-thread workgroup
+// per token.  The split partials are summed in a fixed two-level order (8
+// thread groups over strided splits, then the 8 group sums in order), the
+// constraints run on lanes 0..3 as above, and the row (C <= 4096) is spread
+// 16 columns per thread with the sum of squares reduced through LDS.
+template <typename T>
+__global__ __launch_bounds__(256) void mhc_apply_tok_kernel(ApplyArgs a) {
+    constexpr uint32_t esz = sizeof(T);
+    __shared__ float grp_s[8][32];
+    __shared__ float dyn_s[kProjOut + 7];
+    __shared__ float hpre_s[4];
+    __shared__ float sq_s[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tok = blockIdx.x;
+    const int n = a.n, C = a.C, K = n * C;
+    {
+        // splits <= 64 (K / 256 with K <= 16384): each thread's 8 loads are
+        // issued together, then added in split order
+        const int o = tid & 31, g = tid >> 5;
+        float pv[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int sp = g + 8 * r;
+            pv[r] = (o < kProjOut && sp < a.splits) ? a.part[((int64_t)sp * a.M + tok) * kProjOut + o] : 0.f;
+        }
+        float v = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v += pv[r];
+        grp_s[g][o] = v;
+    }
+    __syncthreads();
+    if (tid < kProjOut) {
+        float v = 0.f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) v += grp_s[g][tid];
+        dyn_s[tid] = v;
+    }
+    __syncthreads();
+    if (tid < 4) {
+        const float rs = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(dyn_s[kProjOut - 1], (float)K) + a.rms_eps));
+        auto dynf = [&](int o) { return dyn_s[o] * rs; };
+        token_constraints_quad(0, tid, tok, a.M, n, a.coef, a.bias, a.n_iter, a.sk_eps, dynf, hpre_s, a.h_pre,
+                               a.h_post, a.h_res);
+    }
+    __syncthreads();
+    float hp[kMaxStreams];
+#pragma unroll
+    for (int st = 0; st < kMaxStreams; ++st) hp[st] = hpre_s[st];
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
+    const uint32_t xrow = (uint32_t)((int64_t)tok * a.ldx * esz);
+    const int nq = C / 4;
+    constexpr int kQ = 4;  // quads per thread: 256 x 4 x 4 = 4096 columns
+    f32x4 v[kQ];
+    float sq = 0.f;
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) {
+        const int q = tid + 256 * j;
+        f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < kMaxStreams; ++st)
+            if (st < n) acc4 += hp[st] * Buf4<T>::load(xr, q < nq ? xrow + (uint32_t)(st * C + 4 * q) * esz : kOOB, 0);
+        v[j] = acc4;
+        sq += acc4.x * acc4.x + acc4.y * acc4.y + acc4.z * acc4.z + acc4.w * acc4.w;
+    }
+    float scale = 1.f;
+    if (a.norm_w) {
+#pragma unroll
+        for (int sh = 1; sh < 64; sh <<= 1) sq += __shfl_xor(sq, sh);
+        if (lane == 0) sq_s[wave] = sq;
+        __syncthreads();
+        sq = (sq_s[0] + sq_s[1]) + (sq_s[2] + sq_s[3]);
+        scale = 1.0f / sqrtf(__fdiv_rn(sq, (float)C) + a.norm_eps);
+    }
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) {
+        const int q = tid + 256 * j;
+        if (q >= nq) continue;
+        f32x4 o = v[j] * scale;
+        if (a.norm_w) o *= *(const f32x4 *)(a.norm_w + 4 * q);
+        Buf4<T>::store(o, lr, (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz), 0);
+    }
+}
+
 // ---------------------------------------------------------------- post (apply)
 // x_new[t, r, :] = sum_s H_res[t, r, s] x[t, s, :] + H_post[t, r] out[t, :]
 template <typename T>
@@ -1439,6 +1523,9 @@ WALSH_EXPORT int walsh_mhc_post_pre_norm_fwd(const void *x_old, int64_t ld_old, 
 
 // Splits of K for the wide-row projection: enough wavefronts to fill the
 // chip when there are few tokens (decode), one split otherwise.
+// row counts up to which the apply step runs a workgroup per token
+constexpr int64_t kApplyTokRows = 1024;
+
 static int mhc_wide_splits(int64_t M, int64_t K) {
     const int64_t tiles = ceil_div(M, 16);
     const int64_t want = (int64_t)device_info().cu_count * 8;
@@ -1518,9 +1605,16 @@ WALSH_EXPORT int walsh_mhc_pre_wide_fwd(const void *x, int64_t ldx, int64_t M, i
         aa.ld_in = ld_in;
         aa.norm_w = norm_w;
         aa.norm_eps = norm_eps;
-        const dim3 G2((unsigned)ceil_div(rows, 4));
-        if (dtype == WALSH_BF16) launch(mhc_apply_kernel<uint16_t>, G2, B, 0, s, aa);
-        else launch(mhc_apply_kernel<float>, G2, B, 0, s, aa);
+        if (rows <= kApplyTokRows && splits <= 64) {
+            // few tokens: a workgroup per token
+            const dim3 G2((unsigned)rows);
+            if (dtype == WALSH_BF16) launch(mhc_apply_tok_kernel<uint16_t>, G2, B, 0, s, aa);
+            else launch(mhc_apply_tok_kernel<float>, G2, B, 0, s, aa);
+        } else {
+            const dim3 G2((unsigned)ceil_div(rows, 4));
+            if (dtype == WALSH_BF16) launch(mhc_apply_kernel<uint16_t>, G2, B, 0, s, aa);
+            else launch(mhc_apply_kernel<float>, G2, B, 0, s, aa);
+        }
         const int rc = check_hip(hipGetLastError(), fn);
         if (rc) return rc;
     }

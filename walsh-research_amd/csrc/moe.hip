@@ -397,6 +397,94 @@ __global__ __launch_bounds__(kMoeThreads) void moe_topk_kernel(const float *__re
     part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
 }
 
+// Top-k routing for 16 < E <= 128 experts: one wavefront per token, lane l
+// holding experts l and l + 64.  Softmax by wave reductions (max, then a
+// fixed-order sum); the probabilities go to LDS and each lane ranks its own
+// experts by counting the entries that beat them (larger probability, ties to
+// the lower index), so the k selected experts and their order need no
+// sequential rounds.  Same outputs as moe_topk_kernel.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int sh = 32; sh > 0; sh >>= 1) v = fmaxf(v, __shfl_xor(v, sh));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int sh = 32; sh > 0; sh >>= 1) v += __shfl_xor(v, sh);
+    return v;
+}
+
+__global__ __launch_bounds__(kMoeThreads) void moe_topk_rank_kernel(const float *__restrict__ logits, RouteOut o) {
+    __shared__ int cnt_l[kMaxE];
+    __shared__ float ps_l[kMaxE];
+    __shared__ __align__(16) float pl[kMoeWaves][kMaxE];
+    part_init(cnt_l, ps_l);
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int E = o.E, k = o.k;
+    for (int tok = blockIdx.x * kMoeWaves + wave; tok < o.M; tok += gridDim.x * kMoeWaves) {
+        float p[2], lg[2];
+        int e[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            e[h] = lane + 64 * h;
+            lg[h] = e[h] < E ? logits[(int64_t)tok * E + e[h]] : -INFINITY;
+        }
+        const float mx = wave_max(fmaxf(lg[0], lg[1]));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) p[h] = (lg[h] == -INFINITY) ? 0.f : expf(lg[h] - mx);
+        const float sum = wave_sum(p[0] + p[1]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            p[h] = __fdiv_rn(p[h], sum);
+            pl[wave][e[h]] = e[h] < E ? p[h] : -1.f;  // probabilities are >= 0: -1 never beats
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // ranks: the token's probabilities read back 32 at a time (8 x 16-byte
+        // broadcast reads in flight together); entries past E hold -1
+        int rank[2] = {0, 0};
+        const int E32 = (E + 31) & ~31;
+        for (int j0 = 0; j0 < E32; j0 += 32) {
+            f32x4 pv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) pv[u] = *(const f32x4 *)&pl[wave][j0 + 4 * u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int j = j0 + 4 * u + c;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) rank[h] += beats(pv[u][c], p[h], j < e[h]);
+                }
+        }
+        bool sel[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) sel[h] = e[h] < E && rank[h] < k;
+        const float den = fmaxf(wave_sum((sel[0] ? p[0] : 0.f) + (sel[1] ? p[1] : 0.f)), 1e-8f);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (e[h] >= E) continue;
+            const int64_t pe = (int64_t)tok * E + e[h];
+            if (sel[h]) {
+                const int64_t at = (int64_t)tok * k + rank[h];
+                o.topk_idx[at] = e[h];
+                o.topk_w[at] = __fdiv_rn(p[h], den);
+                atomicAdd(cnt_l + e[h], 1);
+            }
+            atomicAdd(ps_l + e[h], p[h]);
+            if (o.probs) o.probs[pe] = p[h];
+            if (o.mask) o.mask[pe] = sel[h] ? 1.f : 0.f;
+            if (o.wdense) o.wdense[pe] = sel[h] ? __fdiv_rn(p[h], den) : 0.f;
+            if (o.y && !sel[h]) zero_block(o.y, o.y_bf16, tok * o.ldy + 32 * e[h]);
+        }
+        // the next token of this wave overwrites pl only after every lane read it
+        __builtin_amdgcn_wave_barrier();
+    }
+    part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
+}
+
 __global__ void moe_zero_kernel(int *count, float *probsum, int n) {
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         count[e] = 0;
@@ -948,11 +1036,14 @@ WALSH_EXPORT int walsh_moe_topk_fwd(const float *logits, int64_t M, int64_t E, i
     RouteOut o{(int)M, (int)E, (int)k, probs, mask, weights_dense, topk_idx, topk_w, count, probsum, (int)n_part,
                nullptr, 0, 0};
     const int net = (int)ceil_div(E, 16);
-    const dim3 G(grid_cap(ceil_div(M, 16), n_part)), B(kMoeThreads);
-    if (net <= 1) launch(moe_topk_kernel<1>, G, B, 0, s, logits, net, o);
-    else if (net <= 2) launch(moe_topk_kernel<2>, G, B, 0, s, logits, net, o);
-    else if (net <= 4) launch(moe_topk_kernel<4>, G, B, 0, s, logits, net, o);
-    else launch(moe_topk_kernel<8>, G, B, 0, s, logits, net, o);
+    if (net <= 1) {
+        const dim3 G(grid_cap(ceil_div(M, 16), n_part)), B(kMoeThreads);
+        launch(moe_topk_kernel<1>, G, B, 0, s, logits, net, o);
+    } else {
+        // one wavefront per token
+        const dim3 G(grid_cap(M, n_part)), B(kMoeThreads);
+        launch(moe_topk_rank_kernel, G, B, 0, s, logits, o);
+    }
     return check_hip(hipGetLastError(), fn);
 }
 

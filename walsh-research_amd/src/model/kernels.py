@@ -1120,7 +1120,9 @@ def moe_topk(logits: torch.Tensor, k: int, dense: bool = False) -> MoERoute:
     _hip.require_device(logits, "logits")
     lg = logits.detach().float().contiguous()
     M, E = lg.shape
-    r = MoERoute(M, E, k, lg.device, dense, _parts(M, 64, lg.device))
+    # partial-count rows: one per workgroup (16 tokens per wave up to 16
+    # experts; one token per wave, 8 per workgroup, above)
+    r = MoERoute(M, E, k, lg.device, dense, _parts(M, 64 if E <= 16 else 8, lg.device))
     _hip.call("walsh_moe_topk_fwd", lg.data_ptr(), M, E, k, _hip.ptr(r.probs), _hip.ptr(r.mask),
               _hip.ptr(r.weights), r.topk_idx.data_ptr(), r.topk_w.data_ptr(), r.count_part.data_ptr(),
               r.probsum_part.data_ptr(), r.parts, _hip.stream(lg.device), kernel="moe_topk_kernel",
