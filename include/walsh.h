@@ -494,6 +494,21 @@ int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_
                         int *topk_idx, float *topk_w, int *count, float *probsum, int64_t n_part, void *y,
                         int64_t ldy, int dtype, int ydtype, void *stream);
 
+/* walsh_moe_router_wide_fwd: HadamardRouter.forward (src/model/moe.py:
+ *   418-447) for wide models (n_embd 4096: W1 4096 -> 1024, W2 -> 128
+ *   experts), bf16 only, on matrix cores in two launches: h = silu(x W1^T)
+ *   [M, H] into the caller's bf16 workspace h (row stride ldh), then
+ *   logits = h W2^T with the softmax / top-k / routing outputs of
+ *   walsh_moe_route_fwd.  W1 [H, C] and W2 [E, H] are plain row-major bf16
+ *   matrices (the Linear weights cast to bf16).  The first product, SiLU's
+ *   result and the logits are rounded to bfloat16 where torch.autocast
+ *   rounds them.  Needs C % 256 == 0, H % 32 == 0, H <= 1024, 16-byte
+ *   aligned operands and rows. */
+int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_t H, const void *w1,
+                              const void *w2, int64_t E, int64_t k, void *h, int64_t ldh, float *probs, float *mask,
+                              float *weights_dense, int *topk_idx, float *topk_w, int *count, float *probsum,
+                              int64_t n_part, void *y, int64_t ldy, int ydtype, void *stream);
+
 /* walsh_moe_topk_fwd: the softmax / top-k / renormalisation part of
  *   HadamardRouter.forward (src/model/moe.py:432-445) from given float32
  *   logits [M, E] (contiguous). */

@@ -423,3 +423,50 @@ def test_hadamard_linear_multi_equals_single_launches(K, dtype, in_o, out_o, T):
     torch.cuda.synchronize()
     for o, s in zip(outs, singles):
         assert torch.equal(o, s)
+
+
+# --------------------------------------------------------------- decode-sized batches
+
+@pytest.mark.parametrize("in_o,out_o", [(128, 128), (100, 128), (128, 68), (36, 64)])
+def test_split_kernel_bitwise_equals_wide_kernel(K, in_o, out_o):
+    """Row counts up to 256 of the bf16 wide shapes run the split kernel
+    (one workgroup per token tile and output tile), larger ones the wide3
+    kernel: both round and sum in the same order, so the first k rows of a
+    512-row call equal a k-row call bitwise, for the plain linear, the RoPE
+    variant and the three-layer q/k/v launch."""
+    torch.manual_seed(in_o + out_o)
+    T, D = 512, 4 if out_o % 128 else 128
+    x = torch.randn(1, T, 32 * in_o, device="cuda").to(torch.bfloat16)
+    f = _freqs_cis(T, D).cuda()
+    layers = []
+    for rope in (True, True, False):
+        w = torch.randn(32, out_o, in_o) * 0.02
+        q = K.ternary_quantize(w.cuda(), packed=True)
+        kw = K.hadamard_prepare(q["packed"], in_o, out_o)
+        layers.append((kw, (1 + 0.3 * torch.randn(32, in_o)).cuda(), (0.2 * torch.randn(32, out_o)).cuda(), rope))
+    kw, a, b, _ = layers[0]
+    big = K.hadamard_linear(x, in_o, out_o, kw, a, b)
+    big_rope = K.hadamard_linear_rope(x, in_o, out_o, kw, a, b, f, D)
+    big_multi = K.hadamard_linear_multi(x, in_o, out_o, layers, f, D)
+    for k in (1, 5, 16, 33, 256):
+        xs = x[:, :k]
+        assert torch.equal(K.hadamard_linear(xs, in_o, out_o, kw, a, b), big[:, :k]), k
+        assert torch.equal(K.hadamard_linear_rope(xs, in_o, out_o, kw, a, b, f[:k], D), big_rope[:, :k]), k
+        for o, ref in zip(K.hadamard_linear_multi(xs, in_o, out_o, layers, f[:k], D), big_multi):
+            assert torch.equal(o, ref[:, :k]), k
+
+
+@pytest.mark.parametrize("B,D", [(1, 128), (3, 96)])
+def test_split_head_mixer_bitwise_equals_wide_kernel(K, B, D):
+    """The head mixer at head_dim above 32 in bf16: B * T rows up to 256 run
+    the split kernel; the first k positions of a 512-position call equal a
+    k-position call (a strided view of the same tensor) bitwise."""
+    rng = np.random.default_rng(B * D)
+    T = 512 // B + 1
+    x = torch.from_numpy(rng.standard_normal((B, 32, T, D)).astype(np.float32)).cuda().to(torch.bfloat16)
+    W = torch.from_numpy((rng.standard_normal((32, D, D)) * 0.05).astype(np.float32)).cuda()
+    beta = torch.from_numpy(rng.uniform(0.1, 0.5, size=D).astype(np.float32)).cuda()
+    kw = K.head_mixer_prepare(W, torch.bfloat16)
+    big = K.head_mixer(x, kw, beta)
+    for k in (1, 7, 16, 256 // B):
+        assert torch.equal(K.head_mixer(x[:, :, :k], kw, beta), big[:, :k]), k

@@ -120,9 +120,11 @@ def test_topk_rejects_bad_k(K):
 
 # ------------------------------------------------------------ scatter
 
-def test_scatter_groups_pairs_by_expert(K):
-    rng = np.random.default_rng(5)
-    M, E, k = 1000, 16, 6
+@pytest.mark.parametrize("M", [1000, 100, 1])
+def test_scatter_groups_pairs_by_expert(K, M):
+    # 6000 pairs take the two-launch form, 600 and 6 the one-workgroup form
+    rng = np.random.default_rng(5 + M)
+    E, k = 16, 6
     lg = rng.standard_normal((M, E)).astype(np.float32)
     r = K.moe_topk(torch.from_numpy(lg).cuda(), k)
     lst, off, toff = K.moe_scatter(r)
@@ -134,6 +136,83 @@ def test_scatter_groups_pairs_by_expert(K):
     assert np.array_equal(np.sort(lst), np.arange(M * k))
     for e in range(E):
         assert np.all(idx[lst[off[e]:off[e + 1]]] == e)
+
+
+# ------------------------------------------------------------ wide router (n_embd 4096)
+
+def _router_bf16_ref(x, w1, w2):
+    """The router on bf16 operands with autocast's roundings (the first
+    product, SiLU's result and the logits rounded to bf16), float64 in
+    between: (hidden, logits)."""
+    xb, w1b, w2b = (_bf16(a).astype(np.float64) for a in (x, w1, w2))
+    h = _bf16(xb @ w1b.T)
+    s = _bf16(omoe.silu(h.astype(np.float64)))
+    return s, _bf16(s.astype(np.float64) @ w2b.T)
+
+
+def _bf16_ulp(a):
+    e = np.floor(np.log2(np.maximum(np.abs(a), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+@pytest.mark.parametrize("M,C,E,k", [(1, 4096, 128, 6), (17, 4096, 128, 6), (64, 512, 40, 4), (300, 4096, 128, 6),
+                                     (700, 1024, 128, 8), (0, 4096, 128, 6)])
+def test_router_wide_bf16(K, M, C, E, k):
+    """walsh_moe_router_wide_fwd (split-K first product up to 256 rows, the
+    256 x 256 GEMM above) against the float64 router on the same bf16
+    operands with autocast's roundings.  Bars: the hidden activations within
+    1e-2; the routing bit-exact on the kernel's own probabilities (top-k,
+    counts); probabilities within 1e-2 of the oracle's; assignments equal
+    to the oracle's except where the oracle's k-th and (k+1)-th bf16 logits
+    lie within 4 bf16 ulps (counted and reported); unselected output blocks
+    zeroed, selected ones untouched."""
+    H = C // 4
+    rng = np.random.default_rng(M + C + E)
+    x = rng.standard_normal((M, C)).astype(np.float32)
+    w1 = (rng.standard_normal((H, C)) * 0.02).astype(np.float32)
+    w2 = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    xt = torch.from_numpy(x).cuda().bfloat16()
+    w1t, w2t = (torch.from_numpy(a).cuda().bfloat16().contiguous() for a in (w1, w2))
+    y = torch.full((M, 32 * E), 7.0, device="cuda")
+    assert K.moe_router_wide_supported(xt, H, E, k)
+    r, h = K.moe_router_wide(xt, w1t, w2t, E, k, dense=True, y=y, return_hidden=True)
+    torch.cuda.synchronize()
+    if M == 0:
+        assert int(r.count.sum()) == 0
+        return
+    h_ref, lg_ref = _router_bf16_ref(x, w1, w2)
+    check(h.float().cpu().numpy(), h_ref, TOL[torch.bfloat16], f"router hidden M={M} C={C}")
+    probs = r.probs.cpu().numpy()
+    idx = r.topk_idx.cpu().numpy()
+    assert np.array_equal(idx, omoe.topk_indices(probs, k).astype(np.int32))
+    assert np.array_equal(r.count.cpu().numpy(), np.bincount(idx.reshape(-1), minlength=E).astype(np.int32))
+    p_ref = omoe.softmax(lg_ref)
+    check(probs, p_ref, TOL[torch.bfloat16], f"router probs M={M} C={C}")
+    _, _, idx_ref = omoe.route_from_probs(p_ref, k)
+    same = np.all(np.sort(idx, -1) == np.sort(idx_ref, -1), axis=-1)
+    srt = -np.sort(-lg_ref, axis=-1)
+    gap = srt[:, k - 1] - srt[:, k] if k < E else np.full(M, np.inf)
+    band = gap <= 4 * _bf16_ulp(srt[:, k - 1])
+    print(f"wide router M={M} C={C} E={E} k={k}: differ={int((~same).sum())} in_band={int(band.sum())} "
+          f"exact_ties={int((gap == 0).sum())}")
+    assert np.all(same | band)
+    yv = y.view(M, E, 32).cpu().numpy()
+    sel = np.zeros((M, E), bool)
+    np.put_along_axis(sel, idx.astype(np.int64), True, -1)
+    assert np.all(yv[~sel] == 0) and np.all(yv[sel] == 7.0)
+
+
+def test_router_wide_module_path():
+    """HadamardRouter at n_embd 4096 in bf16 takes the wide router (no
+    library GEMM); the module's dense outputs match a direct call."""
+    from src.model import kernels
+    m = make_moe(4096, max_experts=6, seed=3)
+    x = torch.randn(5, 4096, device="cuda").bfloat16()
+    r = m.router.route(x, dense=True)
+    w1 = m.router.gate[0].weight.detach().bfloat16().contiguous()
+    w2 = m.router.gate[2].weight.detach().bfloat16().contiguous()
+    r2 = kernels.moe_router_wide(x, w1, w2, 128, 6, dense=True)
+    assert torch.equal(r.topk_idx, r2.topk_idx) and torch.equal(r.probs, r2.probs)
 
 
 # ------------------------------------------------------------ router + module, float32

@@ -395,6 +395,26 @@ __device__ __forceinline__ void wide3_load_x(__amdgpu_buffer_rsrc_t xr, uint32_t
     for (int g = G0; g < G1; ++g) r[g] = __builtin_amdgcn_raw_buffer_load_b64(xr, voff, (uint32_t)g * gstride, 0);
 }
 
+// The lane's 4 columns of one row, scaled by alpha (fp16 in LDS, al[g * 128])
+// and transformed over the 32 groups, into the stage as bf16 (xdst[g * 128]
+// in uint2 units).  Two passes of 2 columns keep the transform at 64
+// registers.
+__device__ __forceinline__ void wide3_transform_x(const u32x2 (&xraw)[32], const _Float16 *al, uint2 *xdst) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        f32x2 v[32];
+#pragma unroll
+        for (int g = 0; g < 32; ++g) {
+            const uint32_t u = p ? xraw[g].y : xraw[g].x;
+            const _Float16 *ag = al + g * kW3MaxO + 2 * p;
+            v[g] = f32x2{__uint_as_float(u << 16) * (float)ag[0], __uint_as_float(u & 0xffff0000u) * (float)ag[1]};
+        }
+        fht32<f32x2>(v);
+#pragma unroll
+        for (int g = 0; g < 32; ++g) ((uint32_t *)&xdst[g * 128])[p] = pack_bf16x2(v[g][0], v[g][1]);
+    }
+}
+
 // GS: 128 for in_o = out_o = 128 with unpadded groups (the n_embd 4096
 // layers: strides fixed at compile time), 0 for any other shape.
 // DENSE: dense bf16 weights (the head mixer at head_dim 128) as 16x16x32
@@ -459,22 +479,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs
     for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
         const int next = tile + gridDim.x;
         lds_barrier();  // tables ready / previous tile done with the stage
-        if (xwave) {
-            // two passes of 2 columns keep the transform at 64 registers
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                f32x2 v[32];
-#pragma unroll
-                for (int g = 0; g < 32; ++g) {
-                    const uint32_t u = p ? xraw[g].y : xraw[g].x;
-                    const _Float16 *ag = al + g * kW3MaxO + 2 * p;
-                    v[g] = f32x2{__uint_as_float(u << 16) * (float)ag[0], __uint_as_float(u & 0xffff0000u) * (float)ag[1]};
-                }
-                fht32<f32x2>(v);
-#pragma unroll
-                for (int g = 0; g < 32; ++g) ((uint32_t *)&xdst[g * 128])[p] = pack_bf16x2(v[g][0], v[g][1]);
-            }
-        }
+        if (xwave) wide3_transform_x(xraw, al, xdst);
         if (DENSE) {
             // the first fragments load while the other waves finish their
             // transforms
@@ -590,6 +595,168 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_wide3_kernel(HadArgs
             }
         }
     }
+}
+
+// ---------------------------------------------------------------- decode-sized batches
+// With a few 16-token tiles the wide3 kernel runs one workgroup per tile, so
+// a whole layer's codes stream through a handful of CUs and the launch lasts
+// as long as one workgroup's chunk loop.  Here a workgroup takes one (token
+// tile, output tile, layer): its 8 waves stage the tile's transformed input
+// as the wide3 kernel does, wave w contracts groups 4w..4w+3 over every
+// chunk, the 32 group products meet in LDS and 4 waves run the output
+// transform, one column quad each.  Every rounding and every sum follows
+// the wide3 kernel's order, so both give bitwise the same rows; the input
+// transform is repeated per output tile, which a few rows make cheap.
+#ifndef WALSH_SPLIT_ROWS
+#define WALSH_SPLIT_ROWS 256
+#endif
+constexpr int kSplitRows = WALSH_SPLIT_ROWS;            // row counts up to this take the split kernel
+constexpr size_t kSplitBetaBytes = (size_t)32 * kNTile * 2;  // [32 h][16 o] fp16
+
+static size_t split3_lds_bytes(int Kc32) {
+    const size_t stage = (size_t)Kc32 * 32 * 64 * 16, part = (size_t)32 * 64 * 16;
+    return kW3LutBytes + kW3AlphaBytes + kSplitBetaBytes + (stage > part ? stage : part);
+}
+
+// Grid: x = token tile * Nt + output tile, y = layer of `an`.  GS and DENSE
+// as for the wide3 kernel.
+template <int GS, bool DENSE>
+__global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArgsN an) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const HadArgs &a = an.p[blockIdx.y];
+    uint2 *lut = (uint2 *)smem;                                           // [81 entries][16 copies]
+    _Float16 *alpha_l = (_Float16 *)(smem + kW3LutBytes);                 // [32 g][128 cols]
+    _Float16 *beta_l = (_Float16 *)(smem + kW3LutBytes + kW3AlphaBytes);  // [32 h][16 o] of this tile
+    uint4 *xs = (uint4 *)(smem + kW3LutBytes + kW3AlphaBytes + kSplitBetaBytes);  // [Kc32][32 g][64 lanes]
+    f32x4 *part = (f32x4 *)xs;  // after the products: [32 g][64 lanes]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane & 15, q = lane >> 4;
+    const int nt = (int)blockIdx.x % a.Nt, tile = (int)blockIdx.x / a.Nt;
+    const int Kc32 = (a.in_o + 31) >> 5;
+
+    // every load first, so one memory round trip covers them all: this
+    // wave's weights of groups 4w..4w+3 for every chunk, the tile's input,
+    // alpha and this output tile's beta
+    uint2 wv[4];
+    uint4 wd[4][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        if (c < Kc32) {
+            if constexpr (DENSE) {
+                const uint4 *src = (const uint4 *)a.kw + ((int64_t)(nt * Kc32 + c) * 32 + 4 * wave) * 64 + lane;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wd[c][j] = src[j * 64];
+            } else {
+                wv[c] = *(const uint2 *)(a.kw3 + ((int64_t)(nt * Kc32 + c) * 64 + lane) * 64 + 8 * wave);
+            }
+        }
+    }
+    const int i0 = 16 * wave + 4 * q;
+    const bool xwave = wave < 2 * Kc32;
+    u32x2 xraw[32];
+    if (xwave) {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a, 2));
+        const int row = tile * kTile + t;
+        const uint32_t voff = (row < a.M && i0 < a.in_o) ? x_row_off(a, row, 2) + (uint32_t)i0 * 2 : kOOB;
+        wide3_load_x(xr, voff, (uint32_t)(GS ? GS : a.gsx) * 2, xraw);
+    }
+    const float a32 = DENSE ? 0.03125f : 1.f;  // the dense weights' share of the transforms' 1/32
+    float av[32 * kW3MaxO / kWideThreads];
+#pragma unroll
+    for (int k = 0; k < 32 * kW3MaxO / kWideThreads; ++k) {
+        const int e = tid + k * kWideThreads, g = e / kW3MaxO, i = e % kW3MaxO;
+        av[k] = i < a.in_o ? (a.alpha ? a.alpha[g * a.in_o + i] : 1.f) * a32 : 0.f;
+    }
+    const int bo = kNTile * nt + (tid & 15);
+    const float bv = bo < a.out_o ? a.beta[(tid >> 4) * a.beta_h + bo] : 0.f;
+
+    for (int e = tid; e < (DENSE ? 0 : kW3Entries * kW3Copies); e += kWideThreads) {
+        int r = e / kW3Copies;
+        float val[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            val[j] = (float)(r % 3 - 1) * 0.03125f;
+            r /= 3;
+        }
+        lut[e] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
+    }
+#pragma unroll
+    for (int k = 0; k < 32 * kW3MaxO / kWideThreads; ++k) alpha_l[tid + k * kWideThreads] = (_Float16)av[k];
+    beta_l[tid] = (_Float16)bv;
+    lds_barrier();  // tables ready
+    if (xwave)
+        wide3_transform_x(xraw, alpha_l + i0,
+                          (uint2 *)(xs + (size_t)(i0 >> 5) * 32 * 64 + t + 16 * ((i0 >> 3) & 3)) + ((i0 >> 2) & 1));
+    lds_barrier();  // stage ready
+
+    f32x4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint4 *xsrc = xs + 4 * wave * 64 + lane;
+    const uint2 *lut_l = lut + (lane & 15);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        if (c < Kc32) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint4 wa;
+                if constexpr (DENSE) {
+                    wa = wd[c][j];
+                } else {
+                    const uint32_t word = (j < 2 ? wv[c].x : wv[c].y) >> (16 * (j & 1));
+                    const uint2 lo = lut_l[(word & 0xffu) * kW3Copies];
+                    const uint2 hi = lut_l[((word >> 8) & 0xffu) * kW3Copies];
+                    wa = uint4{lo.x, lo.y, hi.x, hi.y};
+                }
+                const uint4 xb = xsrc[(c * 32 + j) * 64];
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wa),
+                                                                 __builtin_bit_cast(bf16x8, xb), acc[j], 0, 0, 0);
+            }
+        }
+    }
+    lds_barrier();  // every wave is done with the stage: it now takes the products
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[(4 * wave + j) * 64 + lane] = acc[j];
+    lds_barrier();
+    if (wave >= 4) return;
+    // wave w: outputs 4w..4w+3 of the tile; lane = (token tt, output jj), so
+    // one read instruction covers 64 consecutive floats
+    const int tt = lane >> 2, jj = lane & 3, o16 = 4 * wave + jj;
+    const float *pp = (const float *)part + (tt + 16 * wave) * 4 + jj;
+    float v[32];
+#pragma unroll
+    for (int g = 0; g < 32; ++g) v[g] = pp[g * 256];
+    fht32<float>(v);
+    const int row = tile * kTile + tt, o = kNTile * nt + o16;
+    const bool ok = row < a.M && o < a.out_o;
+    const bool rope = a.rope != nullptr;
+    f32x2 cs = f32x2{1.f, 0.f};
+    if (rope && ok) {
+        const int rt = (row + a.rope_row0) % a.rope_T;
+        cs = *(const f32x2 *)(a.rope + ((int64_t)rt * (a.rope_D >> 1) + ((o % a.rope_D) >> 1)) * 2);
+    }
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
+    const uint32_t voff = ok ? (uint32_t)((int64_t)row * a.ldy * 2) + (uint32_t)o * 2 : kOOB;
+    const uint32_t hstride = (uint32_t)(GS ? GS : a.gsy) * 2;
+#pragma unroll
+    for (int h = 0; h < 32; ++h) {
+        float r = v[h] * (float)beta_l[h * kNTile + o16];
+        if (rope) {
+            const float p = __shfl_xor(r, 1);  // the other element of the pair
+            r = (jj & 1) ? rope_odd(p, r, cs[0], cs[1]) : rope_even(r, p, cs[0], cs[1]);
+        }
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(r), yr, voff, (uint32_t)h * hstride, 0);
+    }
+}
+
+// Launches the split kernel over `an` (n layers of M rows each, shapes the
+// wide3 kernel takes).
+static void split3_launch(const HadArgsN &an, bool gs128, bool dense, hipStream_t s) {
+    const HadArgs &a = an.p[0];
+    const size_t lds = split3_lds_bytes((a.in_o + 31) / 32);
+    const dim3 G((unsigned)(ceil_div(a.M, kTile) * a.Nt), (unsigned)an.n), B(kWideThreads);
+    if (dense) launch(hadamard_split3_kernel<0, true>, G, B, lds, s, an);
+    else if (gs128) launch(hadamard_split3_kernel<128, false>, G, B, lds, s, an);
+    else launch(hadamard_split3_kernel<0, false>, G, B, lds, s, an);
 }
 
 // ---------------------------------------------------------------- fused SwiGLU
@@ -981,6 +1148,11 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
                 else     { if (one) WALSH_SW_LAUNCH(float, false, false, true); else WALSH_SW_LAUNCH(float, false, false, false); }
             }
 #undef WALSH_SW_LAUNCH
+        } else if (wide3 && rows <= kSplitRows) {
+            HadArgsN an;
+            an.n = 1;
+            an.p[0] = a;
+            split3_launch(an, a.gsx == 128 && a.gsy == 128 && a.in_o == 128 && a.out_o == 128, false, s);
         } else if (wide3) {
             const int64_t items = ceil_div(rows, kTile);
             const int64_t wcap = (int64_t)device_info().cu_count;
@@ -1122,6 +1294,20 @@ WALSH_EXPORT int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int
     const bool kc1 = Kc == 1 && (bf16 || Nt == 1);
     const size_t lds = hadamard_lds_bytes(bf16, Kc, Nt);
     hipStream_t s = (hipStream_t)stream;
+    const int64_t ld = ldx > ldy ? ldx : ldy;
+    if (bf16 && vec && base[0].kw3 && Kc >= 2 && Nt >= 4 && M <= kSplitRows &&
+        M * ld * esz <= (int64_t)kMaxBufferBytes &&
+        split3_lds_bytes((int)ceil_div(in_o, 32)) <= (size_t)device_info().max_shared_per_block) {
+        // a few rows of a wide3 shape: every layer in one split launch
+        HadArgsN an;
+        an.n = (int)n;
+        for (int i = 0; i < n; ++i) {
+            an.p[i] = base[i];
+            an.p[i].M = (int)M;
+        }
+        split3_launch(an, in_o == 128 && out_o == 128, false, s);
+        return check_hip(hipGetLastError(), fn);
+    }
     if (!kc1 || !vec || lds > (size_t)device_info().max_shared_per_block) {
         // shapes served by the other kernels: one launch per layer
         for (int i = 0; i < n; ++i) {
@@ -1130,7 +1316,6 @@ WALSH_EXPORT int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int
         }
         return WALSH_OK;
     }
-    const int64_t ld = ldx > ldy ? ldx : ldy;
     int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * esz) / kTile * kTile;
     if (rows_max < kTile) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
     rows_max = balanced_rows(M, rows_max, kTile);
@@ -1243,6 +1428,13 @@ WALSH_EXPORT int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64
         const size_t lds = wide3_lds_bytes((int)ceil_div(D, 32));
         if (lds > (size_t)device_info().max_shared_per_block)
             return set_error(WALSH_ENOTSUP, "%s: needs %zu B of LDS", fn, lds);
+        if (M <= kSplitRows) {
+            HadArgsN an;
+            an.n = 1;
+            an.p[0] = a;
+            split3_launch(an, false, true, (hipStream_t)stream);
+            return check_hip(hipGetLastError(), fn);
+        }
         const int64_t items = ceil_div(M, kTile), cap = (int64_t)device_info().cu_count;
         launch(hadamard_wide3_kernel<0, true>, dim3((unsigned)(items < cap ? items : cap)), dim3(kWideThreads), lds,
                (hipStream_t)stream, a);

@@ -24,6 +24,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "gemm256.h"
 
 namespace walsh {
 
@@ -53,12 +54,6 @@ __device__ __forceinline__ f32x4 mma16(f32x4 a, f32x4 b, f32x4 acc) {
     }
 }
 
-__device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
-
-// Round to the nearest bfloat16 and back: where the reference runs under
-// bf16 autocast, every Linear/einsum output and elementwise result is a
-// bf16 tensor, so the bf16 path rounds at the same points.
-__device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 // ------------------------------------------------------------------ routing
 struct RouteOut {
@@ -414,6 +409,70 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Softmax, rank top-k and the routing outputs of token `tok`, whose logits
+// the wave holds as lg[0] (expert lane) and lg[1] (expert lane + 64), -inf
+// past E.  pl: the wave's kMaxE-float LDS row (16-byte aligned).
+__device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], float *pl, const RouteOut &o, int *cnt_l,
+                                           float *ps_l) {
+    const int lane = threadIdx.x & 63;
+    const int E = o.E, k = o.k;
+    float p[2];
+    int e[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) e[h] = lane + 64 * h;
+    const float mx = wave_max(fmaxf(lg[0], lg[1]));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) p[h] = (lg[h] == -INFINITY) ? 0.f : expf(lg[h] - mx);
+    const float sum = wave_sum(p[0] + p[1]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        p[h] = __fdiv_rn(p[h], sum);
+        pl[e[h]] = e[h] < E ? p[h] : -1.f;  // probabilities are >= 0: -1 never beats
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ranks: the token's probabilities read back 32 at a time (8 x 16-byte
+    // broadcast reads in flight together); entries past E hold -1
+    int rank[2] = {0, 0};
+    const int E32 = (E + 31) & ~31;
+    for (int j0 = 0; j0 < E32; j0 += 32) {
+        f32x4 pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) pv[u] = *(const f32x4 *)&pl[j0 + 4 * u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int j = j0 + 4 * u + c;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) rank[h] += beats(pv[u][c], p[h], j < e[h]);
+            }
+    }
+    bool sel[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) sel[h] = e[h] < E && rank[h] < k;
+    const float den = fmaxf(wave_sum((sel[0] ? p[0] : 0.f) + (sel[1] ? p[1] : 0.f)), 1e-8f);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (e[h] >= E) continue;
+        const int64_t pe = (int64_t)tok * E + e[h];
+        if (sel[h]) {
+            const int64_t at = (int64_t)tok * k + rank[h];
+            o.topk_idx[at] = e[h];
+            o.topk_w[at] = __fdiv_rn(p[h], den);
+            atomicAdd(cnt_l + e[h], 1);
+        }
+        atomicAdd(ps_l + e[h], p[h]);
+        if (o.probs) o.probs[pe] = p[h];
+        if (o.mask) o.mask[pe] = sel[h] ? 1.f : 0.f;
+        if (o.wdense) o.wdense[pe] = sel[h] ? __fdiv_rn(p[h], den) : 0.f;
+        if (o.y && !sel[h]) zero_block(o.y, o.y_bf16, tok * o.ldy + 32 * e[h]);
+    }
+    // the wave's next token overwrites pl only after every lane read it
+    __builtin_amdgcn_wave_barrier();
+}
+
 __global__ __launch_bounds__(kMoeThreads) void moe_topk_rank_kernel(const float *__restrict__ logits, RouteOut o) {
     __shared__ int cnt_l[kMaxE];
     __shared__ float ps_l[kMaxE];
@@ -421,66 +480,14 @@ __global__ __launch_bounds__(kMoeThreads) void moe_topk_rank_kernel(const float 
     part_init(cnt_l, ps_l);
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int E = o.E, k = o.k;
     for (int tok = blockIdx.x * kMoeWaves + wave; tok < o.M; tok += gridDim.x * kMoeWaves) {
-        float p[2], lg[2];
-        int e[2];
+        float lg[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            e[h] = lane + 64 * h;
-            lg[h] = e[h] < E ? logits[(int64_t)tok * E + e[h]] : -INFINITY;
+            const int e = lane + 64 * h;
+            lg[h] = e < o.E ? logits[(int64_t)tok * o.E + e] : -INFINITY;
         }
-        const float mx = wave_max(fmaxf(lg[0], lg[1]));
-#pragma unroll
-        for (int h = 0; h < 2; ++h) p[h] = (lg[h] == -INFINITY) ? 0.f : expf(lg[h] - mx);
-        const float sum = wave_sum(p[0] + p[1]);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            p[h] = __fdiv_rn(p[h], sum);
-            pl[wave][e[h]] = e[h] < E ? p[h] : -1.f;  // probabilities are >= 0: -1 never beats
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // ranks: the token's probabilities read back 32 at a time (8 x 16-byte
-        // broadcast reads in flight together); entries past E hold -1
-        int rank[2] = {0, 0};
-        const int E32 = (E + 31) & ~31;
-        for (int j0 = 0; j0 < E32; j0 += 32) {
-            f32x4 pv[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) pv[u] = *(const f32x4 *)&pl[wave][j0 + 4 * u];
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int j = j0 + 4 * u + c;
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) rank[h] += beats(pv[u][c], p[h], j < e[h]);
-                }
-        }
-        bool sel[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) sel[h] = e[h] < E && rank[h] < k;
-        const float den = fmaxf(wave_sum((sel[0] ? p[0] : 0.f) + (sel[1] ? p[1] : 0.f)), 1e-8f);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (e[h] >= E) continue;
-            const int64_t pe = (int64_t)tok * E + e[h];
-            if (sel[h]) {
-                const int64_t at = (int64_t)tok * k + rank[h];
-                o.topk_idx[at] = e[h];
-                o.topk_w[at] = __fdiv_rn(p[h], den);
-                atomicAdd(cnt_l + e[h], 1);
-            }
-            atomicAdd(ps_l + e[h], p[h]);
-            if (o.probs) o.probs[pe] = p[h];
-            if (o.mask) o.mask[pe] = sel[h] ? 1.f : 0.f;
-            if (o.wdense) o.wdense[pe] = sel[h] ? __fdiv_rn(p[h], den) : 0.f;
-            if (o.y && !sel[h]) zero_block(o.y, o.y_bf16, tok * o.ldy + 32 * e[h]);
-        }
-        // the next token of this wave overwrites pl only after every lane read it
-        __builtin_amdgcn_wave_barrier();
+        rank_token(tok, lg, pl[wave], o, cnt_l, ps_l);
     }
     part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
 }
@@ -499,15 +506,14 @@ __global__ void moe_zero_kernel(int *count, float *probsum, int n) {
 // offset = exclusive scan of the counts, tile_off = exclusive scan of
 // ceil(count / 16), cursor cleared.
 constexpr int kFinSlices = 8;
-__global__ __launch_bounds__(kMaxE * kFinSlices) void moe_finalize_kernel(const int *__restrict__ count_part,
-                                                                          const float *__restrict__ probsum_part,
-                                                                          int n_part, int E, int *__restrict__ count,
-                                                                          float *__restrict__ probsum,
-                                                                          int *__restrict__ cursor,
-                                                                          int *__restrict__ offset,
-                                                                          int *__restrict__ tile_off) {
-    __shared__ int c_s[kFinSlices][kMaxE];
-    __shared__ float p_s[kFinSlices][kMaxE];
+// Totals, scans and cleared cursors (every thread of a kMaxE * kFinSlices
+// workgroup); leaves the counts in c_s[0] and the offsets in off_s.
+__device__ __forceinline__ void finalize_body(const int *__restrict__ count_part,
+                                              const float *__restrict__ probsum_part, int n_part, int E,
+                                              int *__restrict__ count, float *__restrict__ probsum,
+                                              int *__restrict__ cursor, int *__restrict__ offset,
+                                              int *__restrict__ tile_off, int (&c_s)[kFinSlices][kMaxE],
+                                              float (&p_s)[kFinSlices][kMaxE], int *off_s) {
     const int e = threadIdx.x % kMaxE, sl = threadIdx.x / kMaxE;
     int c = 0;
     float ps = 0.f;
@@ -551,6 +557,7 @@ __global__ __launch_bounds__(kMaxE * kFinSlices) void moe_finalize_kernel(const 
     if (threadIdx.x == 0) {
         int acc = 0, tacc = 0;
         for (int i = 0; i < E; ++i) {
+            off_s[i] = acc;
             offset[i] = acc;
             tile_off[i] = tacc;
             acc += c_s[0][i];
@@ -559,6 +566,42 @@ __global__ __launch_bounds__(kMaxE * kFinSlices) void moe_finalize_kernel(const 
         offset[E] = acc;
         tile_off[E] = tacc;
     }
+}
+
+__global__ __launch_bounds__(kMaxE * kFinSlices) void moe_finalize_kernel(const int *__restrict__ count_part,
+                                                                          const float *__restrict__ probsum_part,
+                                                                          int n_part, int E, int *__restrict__ count,
+                                                                          float *__restrict__ probsum,
+                                                                          int *__restrict__ cursor,
+                                                                          int *__restrict__ offset,
+                                                                          int *__restrict__ tile_off) {
+    __shared__ int c_s[kFinSlices][kMaxE];
+    __shared__ float p_s[kFinSlices][kMaxE];
+    __shared__ int off_s[kMaxE];
+    finalize_body(count_part, probsum_part, n_part, E, count, probsum, cursor, offset, tile_off, c_s, p_s, off_s);
+}
+
+// Few pairs (decode): the totals and the lists in one workgroup, the list
+// ranks from LDS atomics; cursor ends at the counts, as after the
+// two-launch form.
+constexpr int kScatterSmallPairs = 4096;
+__global__ __launch_bounds__(kMaxE * kFinSlices) void moe_scatter_small_kernel(
+    const int *__restrict__ topk_idx, int n_pairs, const int *__restrict__ count_part,
+    const float *__restrict__ probsum_part, int n_part, int E, int *__restrict__ count, float *__restrict__ probsum,
+    int *__restrict__ cursor, int *__restrict__ offset, int *__restrict__ tile_off, int *__restrict__ list) {
+    __shared__ int c_s[kFinSlices][kMaxE];
+    __shared__ float p_s[kFinSlices][kMaxE];
+    __shared__ int off_s[kMaxE];
+    __shared__ int cur_s[kMaxE];
+    if (threadIdx.x < kMaxE) cur_s[threadIdx.x] = 0;
+    finalize_body(count_part, probsum_part, n_part, E, count, probsum, cursor, offset, tile_off, c_s, p_s, off_s);
+    __syncthreads();  // offsets ready
+    for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
+        const int e = topk_idx[p];
+        if ((unsigned)e < (unsigned)E) list[off_s[e] + atomicAdd(&cur_s[e], 1)] = p;
+    }
+    __syncthreads();
+    if (threadIdx.x < E) cursor[threadIdx.x] = cur_s[threadIdx.x];
 }
 
 // Each workgroup places a contiguous chunk of kScatterPerThread * 256 pairs:
@@ -968,6 +1011,167 @@ static int grid_cap(int64_t waves_needed, int64_t limit = 0) {
     return (int)(g < 1 ? 1 : g);
 }
 
+// ------------------------------------------------------------------ wide router
+// The router of wide models (n_embd above the fused router's limit, e.g.
+// 4096 -> 1024 -> 128 experts; moe.py:407-447) as two launches on bf16
+// matrix cores:
+//   1. h = silu(x W1^T) [M, H] into a caller workspace: the 256 x 256-tile
+//      GEMM at many rows; at few rows (decode) router_w1_small_kernel, one
+//      workgroup per 16 hidden units x 16 tokens whose 8 waves split K.
+//   2. router_w2_topk_kernel: logits = h W2^T for 64 tokens per workgroup
+//      (the tile of h staged in LDS, wave w taking experts 16w..16w+15),
+//      then softmax / rank top-k / routing outputs per token as in
+//      walsh_moe_topk_fwd.
+// Products are rounded to bf16 where the reference's autocast Linears round
+// their outputs, with SiLU on the rounded first product.
+constexpr int kR1Waves = 8;
+constexpr int kR1SmallRows = 256;  // row counts up to this take the split-K kernel
+__global__ __launch_bounds__(64 * kR1Waves) void router_w1_small_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                                        int M, int C, const uint16_t *__restrict__ w1,
+                                                                        uint16_t *__restrict__ h, int64_t ldh) {
+    __shared__ f32x4 part[kR1Waves][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, fr = lane & 15, fq = lane >> 4;
+    const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16, H = gridDim.x * 16;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)((int64_t)M * ldx * 2));
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w1, (uint32_t)((int64_t)H * C * 2));
+    // wave w: columns [w C/8, (w+1) C/8) in 32-column steps, 8 steps of
+    // operands in flight
+    const int kw = C / kR1Waves, k0 = wave * kw;
+    const uint32_t wo = (uint32_t)(((int64_t)(n0 + fr) * C + k0 + 8 * fq) * 2);
+    const bool row_ok = m0 + fr < M;
+    const uint32_t xo = row_ok ? (uint32_t)(((int64_t)(m0 + fr) * ldx + k0 + 8 * fq) * 2) : 0;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < kw; kk += 8 * 32) {
+        u32x4 a[8], b[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = kk + 32 * j;
+            a[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, k < kw ? wo + (uint32_t)k * 2 : kOOB, 0, 0);
+            b[j] = __builtin_amdgcn_raw_buffer_load_b128(xr, (k < kw && row_ok) ? xo + (uint32_t)k * 2 : kOOB, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[j]),
+                                                          __builtin_bit_cast(bf16x8, b[j]), acc, 0, 0, 0);
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave) return;
+    f32x4 v = part[0][lane];
+#pragma unroll
+    for (int w = 1; w < kR1Waves; ++w) v = v + part[w][lane];
+    // lane holds D[n = n0 + 4 fq + r][m = m0 + fr]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = silu_f(bf16r(v[r]));
+    const __amdgpu_buffer_rsrc_t hr = make_rsrc(h, (uint32_t)((int64_t)M * ldh * 2));
+    Buf4<uint16_t>::store(v, hr, row_ok ? (uint32_t)(((int64_t)(m0 + fr) * ldh + n0 + 4 * fq) * 2) : kOOB, 0);
+}
+
+constexpr int kR2Tok = 64;     // tokens per workgroup tile
+constexpr int kR2Waves = 8;    // wave w: experts 16w..16w+15
+constexpr int kR2MaxH = 1024;  // staged tile of h: 64 x 1024 bf16 = 128 KB of LDS
+constexpr int kR2LgStride = kMaxE + 4;
+
+static size_t router_w2_lds_bytes(int H) {
+    const size_t stage = (size_t)kR2Tok * H * 2, lg = (size_t)kR2Tok * kR2LgStride * 4;
+    return stage > lg ? stage : lg;
+}
+
+// smem: the h tile, 16-byte chunk c of row r at r * 2H + ((c ^ (r & 15)) << 4)
+// (the 16 rows of a fragment read fall on 16 different chunk columns); after
+// the products the rounded logits [64][kR2LgStride] float.
+__global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uint16_t *__restrict__ h, int64_t ldh,
+                                                                       int H, const uint16_t *__restrict__ w2,
+                                                                       RouteOut o) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int cnt_l[kMaxE];
+    __shared__ float ps_l[kMaxE];
+    __shared__ __align__(16) float pl[kR2Waves][kMaxE];
+    part_init(cnt_l, ps_l);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, fr = lane & 15, fq = lane >> 4;
+    const int M = o.M, E = o.E, nch = H / 8, nks = H / 32;
+    const __amdgpu_buffer_rsrc_t hr = make_rsrc(h, (uint32_t)((int64_t)M * ldh * 2));
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w2, (uint32_t)((int64_t)E * H * 2));
+    const int e_row = 16 * wave + fr;
+    const uint32_t wo = e_row < E ? (uint32_t)(((int64_t)e_row * H + 8 * fq) * 2) : kOOB;
+    float *lg_l = (float *)smem;
+    const int n_tiles = (int)ceil_div(M, kR2Tok);
+    for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const int m0 = tile * kR2Tok;
+        // the first half of this wave's W2 fragments and the whole h tile in
+        // flight together
+        u32x4 wa[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            wa[s] = __builtin_amdgcn_raw_buffer_load_b128(wr, (s < nks && wo != kOOB) ? wo + (uint32_t)s * 64 : kOOB,
+                                                          0, 0);
+        u32x4 st[kR2Tok * kR2MaxH / 8 / (64 * kR2Waves)];
+#pragma unroll
+        for (int j = 0; j < kR2Tok * kR2MaxH / 8 / (64 * kR2Waves); ++j) {
+            const int i = tid + j * 64 * kR2Waves, r = i / nch, c = i - r * nch;
+            const bool ok = i < kR2Tok * nch && m0 + r < M;
+            st[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                hr, ok ? (uint32_t)(((int64_t)(m0 + r) * ldh + 8 * c) * 2) : kOOB, 0, 0);
+        }
+        __syncthreads();  // the previous tile's logits are read
+#pragma unroll
+        for (int j = 0; j < kR2Tok * kR2MaxH / 8 / (64 * kR2Waves); ++j) {
+            const int i = tid + j * 64 * kR2Waves, r = i / nch, c = i - r * nch;
+            if (i < kR2Tok * nch) *(u32x4 *)(smem + r * 2 * H + ((c ^ (r & 15)) << 4)) = st[j];
+        }
+        __syncthreads();
+        f32x4 acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < nks; s0 += 16) {
+            u32x4 wn[16];
+            const bool more = s0 + 16 < nks;
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int sn = s0 + 16 + s;
+                wn[s] = __builtin_amdgcn_raw_buffer_load_b128(
+                    wr, (more && sn < nks && wo != kOOB) ? wo + (uint32_t)sn * 64 : kOOB, 0, 0);
+            }
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                if (s0 + s < nks) {
+                    const int c = 4 * (s0 + s) + fq;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int r = 16 * t + fr;
+                        const u32x4 b = *(const u32x4 *)(smem + r * 2 * H + ((c ^ (r & 15)) << 4));
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wa[s]),
+                                                                         __builtin_bit_cast(bf16x8, b), acc[t], 0, 0,
+                                                                         0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < 16; ++s) wa[s] = wn[s];
+        }
+        __syncthreads();  // every wave is done with the h tile
+        // acc[t][r] = logit of expert 16 w + 4 fq + r for token m0 + 16 t + fr
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            f32x4 v;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = bf16r(acc[t][r]);
+            *(f32x4 *)(lg_l + (16 * t + fr) * kR2LgStride + 16 * wave + 4 * fq) = v;
+        }
+        __syncthreads();
+        for (int tl = wave; tl < kR2Tok && m0 + tl < M; tl += kR2Waves) {
+            float lg[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int e = lane + 64 * hh;
+                lg[hh] = e < E ? lg_l[tl * kR2LgStride + e] : -INFINITY;
+            }
+            rank_token(m0 + tl, lg, pl[wave], o, cnt_l, ps_l);
+        }
+    }
+    part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
+}
+
 static int route_out_check(const char *fn, int64_t M, int64_t E, int64_t k, const int *topk_idx, const float *topk_w,
                            const int *count, const float *probsum, int64_t n_part) {
     if (!count || !probsum || (M > 0 && (!topk_idx || !topk_w)))
@@ -1021,6 +1225,61 @@ WALSH_EXPORT int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int6
     return check_hip(hipGetLastError(), fn);
 }
 
+WALSH_EXPORT int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_t H,
+                                           const void *w1, const void *w2, int64_t E, int64_t k, void *h, int64_t ldh,
+                                           float *probs, float *mask, float *weights_dense, int *topk_idx,
+                                           float *topk_w, int *count, float *probsum, int64_t n_part, void *y,
+                                           int64_t ldy, int ydtype, void *stream) {
+    const char *fn = "walsh_moe_router_wide_fwd";
+    int rc = route_out_check(fn, M, E, k, topk_idx, topk_w, count, probsum, n_part);
+    if (rc) return rc;
+    if ((M > 0 && (!x || !h)) || !w1 || !w2) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (C % (32 * kR1Waves) || H % 32 || H < 32 || H > kR2MaxH || ldx < C || ldh < H || (y && ldy < 32 * E))
+        return set_error(WALSH_ENOTSUP, "%s: needs C %% %d == 0 and H %% 32 == 0, H <= %d (C=%lld H=%lld)", fn,
+                         32 * kR1Waves, kR2MaxH, (long long)C, (long long)H);
+    if (ydtype != WALSH_F32 && ydtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: ydtype", fn);
+    const int64_t ysz = ydtype == WALSH_BF16 ? 2 : 4;
+    if (ldx % 8 || ldh % 8 || (uintptr_t)x % 16 || (uintptr_t)h % 16 || (uintptr_t)w1 % 16 || (uintptr_t)w2 % 16 ||
+        (y && ((uintptr_t)y % 16 || ldy % (16 / ysz))))
+        return set_error(WALSH_ENOTSUP, "%s: operands and rows must be 16-byte aligned", fn);
+    if (M * ldx * 2 > (int64_t)kMaxBufferBytes || M * ldh * 2 > (int64_t)kMaxBufferBytes ||
+        H * C * 2 > (int64_t)kMaxBufferBytes)
+        return set_error(WALSH_ENOTSUP, "%s: operands above 2^31 bytes", fn);
+    if (router_w2_lds_bytes((int)H) + 8 * kMaxE + kR2Waves * kMaxE * 4 > (size_t)device_info().max_shared_per_block)
+        return set_error(WALSH_ENOTSUP, "%s: H=%lld needs more LDS than a workgroup has", fn, (long long)H);
+    hipStream_t s = (hipStream_t)stream;
+    if (M == 0) {
+        launch(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
+        return check_hip(hipGetLastError(), fn);
+    }
+    if (M <= kR1SmallRows) {
+        launch(router_w1_small_kernel, dim3((unsigned)(H / 16), (unsigned)ceil_div(M, 16)), dim3(64 * kR1Waves), 0, s,
+               (const uint16_t *)x, ldx, (int)M, (int)C, (const uint16_t *)w1, (uint16_t *)h, ldh);
+    } else {
+        Gemm256Args g;
+        g.x = x;
+        g.ldx = ldx;
+        g.M = (int)M;
+        g.N = (int)H;
+        g.K = (int)C;
+        g.Kp = (int)C;
+        g.B = w1;
+        g.beta = nullptr;
+        g.out_o = (int)H;
+        g.y = h;
+        g.ldy = ldh;
+        gemm256_launch<kEpiSilu>(g, s);
+    }
+    rc = check_hip(hipGetLastError(), fn);
+    if (rc) return rc;
+    const RouteOut o{(int)M, (int)E, (int)k, probs, mask, weights_dense, topk_idx, topk_w, count, probsum,
+                     (int)n_part, y, ldy, ydtype == WALSH_BF16};
+    const int64_t tiles = ceil_div(M, kR2Tok);
+    launch(router_w2_topk_kernel, dim3((unsigned)(tiles < n_part ? tiles : n_part)), dim3(64 * kR2Waves),
+           (uint32_t)router_w2_lds_bytes((int)H), s, (const uint16_t *)h, ldh, (int)H, (const uint16_t *)w2, o);
+    return check_hip(hipGetLastError(), fn);
+}
+
 WALSH_EXPORT int walsh_moe_topk_fwd(const float *logits, int64_t M, int64_t E, int64_t k, float *probs, float *mask,
                                     float *weights_dense, int *topk_idx, float *topk_w, int *count, float *probsum,
                                     int64_t n_part, void *stream) {
@@ -1058,9 +1317,14 @@ WALSH_EXPORT int walsh_moe_scatter(const int *topk_idx, int64_t M, int64_t E, in
         return set_error(WALSH_EINVAL, "%s: bad shape (M=%lld E=%lld k=%lld n_part=%lld)", fn, (long long)M,
                          (long long)E, (long long)k, (long long)n_part);
     hipStream_t s = (hipStream_t)stream;
+    const int64_t n_pairs = M * k;
+    if (n_pairs <= kScatterSmallPairs) {
+        launch(moe_scatter_small_kernel, dim3(1), dim3(kMaxE * kFinSlices), 0, s, topk_idx, (int)n_pairs,
+               count_part, probsum_part, (int)n_part, (int)E, count, probsum, cursor, offset, tile_off, list);
+        return check_hip(hipGetLastError(), fn);
+    }
     launch(moe_finalize_kernel, dim3(1), dim3(kMaxE * kFinSlices), 0, s, count_part, probsum_part, (int)n_part,
                        (int)E, count, probsum, cursor, offset, tile_off);
-    const int64_t n_pairs = M * k;
     if (n_pairs > 0) {
         const int64_t grid = ceil_div(n_pairs, 256 * kScatterPerThread);
         launch(moe_scatter_kernel, dim3((unsigned)grid), dim3(256), 0, s, topk_idx, n_pairs, (int)E,

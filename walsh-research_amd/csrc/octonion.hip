@@ -14,6 +14,7 @@
 // four wavefronts each owning 64x64 (4x4 tiles of 16x16), K staged through
 // double-buffered LDS, and beta fused into the epilogue.
 #include "common.h"
+#include "gemm256.h"
 
 namespace walsh {
 
@@ -57,16 +58,7 @@ template <> struct GemmCfg<uint16_t> { static constexpr int BK = 32; };  // 64 B
 template <> struct GemmCfg<float> { static constexpr int BK = 16; };     // 64 B per row
 constexpr int kLdsStride = 80;  // 64 B + 16 B pad: 8 consecutive rows cover all banks once
 
-struct OctArgs {
-    const void *x;
-    int64_t ldx;
-    int M, N, K, Kp;     // K = 8*in_o (multiple of 8), Kp = B row length
-    const void *B;
-    const float *beta;
-    int out_o;
-    void *y;
-    int64_t ldy;
-};
+typedef Gemm256Args OctArgs;
 
 template <typename T>
 __global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs a) {
@@ -165,139 +157,6 @@ __global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs 
                 const uint32_t off = (m < a.M && n < a.N) ? (uint32_t)(((int64_t)m * a.ldy + n) * esz) : kOOB;
                 Buf4<T>::store1(acc[i][j][r] * b, yr, off, 0);
             }
-    }
-}
-
-// ------------------------------------------------------- bf16 GEMM, 256 x 256
-// The bf16 forward at every shape.  256 x 256 output tiles, 8 wavefronts of
-// 64 outputs x 128 tokens each.  The product runs transposed, D[n][m] =
-// sum_k B[n][k] x[m][k] on 16x16x32 bf16 MFMA, so a lane's accumulator holds
-// 4 consecutive outputs of one token: the epilogue writes 8-byte pieces of
-// rows with beta applied.
-//   * Per 64-wide K stage both operand tiles (x: 256 tokens, the dense +-1/0
-//     block matrix: 256 outputs; 32 KB each) go global -> registers -> LDS,
-//     double buffered with one barrier per stage; every global byte is
-//     fetched once per workgroup (two wavefronts share each weight row, four
-//     each x row).
-//   * LDS rows are 128 B with the 16-byte chunks XOR-swizzled by the row
-//     (chunk ^ (row & 7)), so fragment reads and tile stores are free of bank
-//     conflicts (measured with SQ_LDS_BANK_CONFLICT).
-//   * Tiles are numbered XCD-major: workgroup b runs on XCD b % 8, and takes
-//     tile (b % 8) * per_xcd + b / 8, so the output tiles of one row block run
-//     side by side on one XCD and x comes from HBM once into that XCD's L2.
-constexpr int kOBM = 256, kOBN = 256, kOBK = 64;
-constexpr int kOThreads = 512;
-constexpr int kOTile = kOBM * 128;  // bytes of one staged operand tile
-
-// byte offset of 16-byte chunk `part` (0..7) of staged row `row`
-__device__ __forceinline__ int oct_off(int row, int part) { return row * 128 + ((part ^ (row & 7)) << 4); }
-
-__global__ __launch_bounds__(kOThreads, 1) void octonion_gemm256_kernel(OctArgs a, int nM, int nN, int per_xcd) {
-    __shared__ __align__(16) unsigned char lds[2][2][kOTile];  // [buffer][x | weights]
-
-    const int tile = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-    if (tile >= nM * nN) return;
-    const int mb = tile / nN, nb = tile - mb * nN;
-    const int m0 = mb * kOBM, n0 = nb * kOBN;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wn = wave & 3, wm = wave >> 2;
-    const int fr = lane & 15, fq = lane >> 4;
-
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * 2));
-    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.B, (uint32_t)((int64_t)a.N * a.Kp * 2));
-
-    // staging: each operand tile is 256 rows x 8 chunks of 16 B; thread takes
-    // chunk tid + 512 i (i = 0..3) of both: row (tid >> 3) + 64 i, chunk
-    // tid & 7.  Out-of-range chunks read zeros.
-    const int srow = tid >> 3, spart = tid & 7;
-    auto load = [&](int k0, u32x4 (&xst)[4], u32x4 (&wst)[4]) {
-        const int k = k0 + spart * 8;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m0 + srow + 64 * i, n = n0 + srow + 64 * i;
-            xst[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                xr, (m < a.M && k < a.K) ? (uint32_t)(((int64_t)m * a.ldx + k) * 2) : kOOB, 0, 0);
-            wst[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                br, (n < a.N && k < a.Kp) ? (uint32_t)(((int64_t)n * a.Kp + k) * 2) : kOOB, 0, 0);
-        }
-    };
-    auto store = [&](int buf, const u32x4 (&xst)[4], const u32x4 (&wst)[4]) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int off = oct_off(srow + 64 * i, spart);
-            *(u32x4 *)(&lds[buf][0][off]) = xst[i];
-            *(u32x4 *)(&lds[buf][1][off]) = wst[i];
-        }
-    };
-
-    f32x4 acc[4][8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // Stage st + 2 is fetched during stage st into the register set stage
-    // st + 1 was stored from, so each global load has two stages of products
-    // to land in; sched_barrier(0) keeps the compiler from sinking the
-    // prefetch below the products.
-    auto stage = [&](int st, u32x4 (&xn)[4], u32x4 (&wn_)[4], u32x4 (&xf_)[4], u32x4 (&wf_)[4]) {
-        const int cur = st & 1;
-        load((st + 2) * kOBK, xf_, wf_);  // zeros past the end
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            u32x4 wf[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) wf[t] = *(const u32x4 *)(&lds[cur][1][oct_off(wn * 64 + t * 16 + fr, sub * 4 + fq)]);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {  // the wave's 8 token tiles in two halves (register pressure)
-                u32x4 xf[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    xf[t] = *(const u32x4 *)(&lds[cur][0][oct_off(wm * 128 + (h * 4 + t) * 16 + fr, sub * 4 + fq)]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[i][h * 4 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8, wf[i]), __builtin_bit_cast(bf16x8, xf[j]), acc[i][h * 4 + j], 0,
-                            0, 0);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        store(cur ^ 1, xn, wn_);            // stage st + 1
-        __syncthreads();
-    };
-
-    const int nst = (int)ceil_div(a.K, kOBK);
-    u32x4 xa[4], wa[4], xb[4], wb[4];
-    load(0, xa, wa);
-    load(kOBK, xb, wb);
-    store(0, xa, wa);
-    __syncthreads();
-    int st = 0;
-    for (; st + 1 < nst; st += 2) {
-        stage(st, xb, wb, xa, wa);
-        stage(st + 1, xa, wa, xb, wb);
-    }
-    if (st < nst) stage(st, xb, wb, xa, wa);
-
-    // epilogue: acc[i][j][r] = D[n = 16 i + 4 fq + r][m = 16 j + fr] of the wave's tile
-    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int n = n0 + wn * 64 + i * 16 + fq * 4;
-        f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (n < a.N) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) bv[r] = a.beta ? a.beta[(n + r) % a.out_o] : 1.f;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int m = m0 + wm * 128 + j * 16 + fr;
-            const uint32_t off = (m < a.M && n < a.N) ? (uint32_t)(((int64_t)m * a.ldy + n) * 2) : kOOB;
-            Buf4<uint16_t>::store(acc[i][j] * bv, yr, off, 0);
-        }
     }
 }
 
@@ -488,7 +347,7 @@ WALSH_EXPORT int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M
         if (dtype == WALSH_BF16) {
             const int nM = (int)ceil_div(rows, kOBM), nN = (int)ceil_div(N, kOBN);
             const int per_xcd = (int)ceil_div((int64_t)nM * nN, 8);
-            launch(octonion_gemm256_kernel, dim3((unsigned)(per_xcd * 8)), dim3(kOThreads), 0, (hipStream_t)stream, a,
+            launch(gemm256_beta_kernel, dim3((unsigned)(per_xcd * 8)), dim3(kOThreads), 0, (hipStream_t)stream, a,
                    nM, nN, per_xcd);
         } else {
             const dim3 G((unsigned)ceil_div(rows, kBM), (unsigned)ceil_div(N, kBN)), Bk(kGemmThreads);

@@ -22,7 +22,7 @@ from .hadamard import HadamardLinearFunction
 from .hadamard import HadamardHeadMixer, HadamardHeadMixerFused
 from .octonion import OctonionHeadMixerFused, OctonionTernaryLinear
 from . import kernels
-from ._common import act_dtype
+from ._common import WeightCache, act_dtype, cached_linear
 
 _HADAMARD_AVAILABLE = True
 _HADAMARD_HEAD_MIXER_AVAILABLE = True
@@ -344,6 +344,7 @@ class Walsh(nn.Module):
         self.tok_embeddings.weight = self.output.weight
         self.layers = nn.ModuleList([LlamaBlock(config) for _ in range(config.n_layer)])
         self.norm = RMSNorm(config.n_embd)
+        self._output_cast = WeightCache()
         self.register_buffer("freqs_cis", precompute_freqs_cis(config.n_embd // config.n_head, config.block_size * 2))
         self.apply(self._init_weights)
         for pn, p in self.named_parameters():
@@ -367,10 +368,10 @@ class Walsh(nn.Module):
                 h = layer(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
         h = self.norm(h)
         if targets is not None:
-            logits = self.output(h)
+            logits = cached_linear(self.output, h, self._output_cast)
             loss = F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1))
         else:
-            logits = self.output(h[:, [-1], :])
+            logits = cached_linear(self.output, h[:, [-1], :], self._output_cast)
             loss = None
         if return_hidden:
             return logits, loss, h

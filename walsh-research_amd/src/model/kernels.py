@@ -1115,6 +1115,47 @@ def moe_route(x: torch.Tensor, w1f: torch.Tensor, w2f: torch.Tensor, H1: int, E:
     return r
 
 
+def moe_router_wide_supported(x2d: torch.Tensor, H: int, E: int, k: int) -> bool:
+    """Whether walsh_moe_router_wide_fwd takes this bf16 router: C % 256 == 0,
+    H % 32 == 0, H <= 1024, E <= 128, k <= 8, 16-byte aligned rows, x under
+    2^31 bytes."""
+    if x2d.dtype != torch.bfloat16 or not x2d.is_cuda or x2d.dim() != 2:
+        return False
+    M, C = x2d.shape
+    shape_ok = C % 256 == 0 and H % 32 == 0 and 32 <= H <= 1024 and E <= 128 and k <= min(8, E)
+    if M == 0:
+        return shape_ok
+    return shape_ok and x2d.stride(-1) == 1 and x2d.stride(0) % 8 == 0 and x2d.data_ptr() % 16 == 0 and M * x2d.stride(0) * 2 < 2 ** 31
+
+
+def moe_router_wide(x2d: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, E: int, k: int, dense: bool = False,
+                    y: torch.Tensor = None, return_hidden: bool = False):
+    """HadamardRouter.forward (moe.py:418-447) of a wide bf16 model on matrix
+    cores: h = silu(x W1^T), logits = h W2^T, softmax / top-k / routing
+    outputs.  x2d [M, C] bf16 (moe_router_wide_supported), w1 [H, C] and w2
+    [E, H] bf16 contiguous.  If y [M, 32E] is given, the blocks of unselected
+    experts are zeroed.  ``return_hidden`` also returns silu(x W1^T) [M, H]."""
+    _hip.require_device(x2d, "input")
+    assert w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16 and w1.is_contiguous() and w2.is_contiguous()
+    M, C = x2d.shape
+    H = w1.shape[0]
+    r = MoERoute(M, E, k, x2d.device, dense, _parts(M, 64, x2d.device))
+    h = torch.empty(max(M, 1), H, device=x2d.device, dtype=torch.bfloat16)
+    ldy, ydt = 0, torch.bfloat16
+    if y is not None:
+        assert y.shape[-1] == 32 * E and y.stride(-1) == 1, "output layout"
+        ldy, ydt = (y.stride(0) if y.dim() == 2 else 32 * E), y.dtype
+    nbytes = M * C * 2 + (H * C + E * H) * 2 + 2 * M * H * 2 + M * k * 8
+    if y is not None:
+        nbytes += M * (E - k) * 32 * y.element_size()
+    _hip.call("walsh_moe_router_wide_fwd", x2d.data_ptr(), x2d.stride(0) if M else C, M, C, H, w1.data_ptr(), w2.data_ptr(), E, k,
+              h.data_ptr(), H, _hip.ptr(r.probs), _hip.ptr(r.mask), _hip.ptr(r.weights), r.topk_idx.data_ptr(),
+              r.topk_w.data_ptr(), r.count_part.data_ptr(), r.probsum_part.data_ptr(), r.parts, _hip.ptr(y), ldy,
+              _hip.dtype_code(ydt), _hip.stream(x2d.device), kernel="moe_router_wide<bf16>", nbytes=nbytes,
+              flops=2 * M * (C * H + H * E))
+    return (r, h[:M]) if return_hidden else r
+
+
 def moe_topk(logits: torch.Tensor, k: int, dense: bool = False) -> MoERoute:
     """Softmax / top-k / renormalisation (moe.py:432-445) on float32 logits [M, E]."""
     _hip.require_device(logits, "logits")

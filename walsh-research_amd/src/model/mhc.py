@@ -13,7 +13,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import kernels
-from ._common import WeightCache, act_dtype, invalidate_weight_caches
+from ._common import WeightCache, act_dtype, cached_linear, invalidate_weight_caches
 
 _MAX_STREAMS = 4
 
@@ -421,6 +421,7 @@ class mHCWalsh(nn.Module):
         self.layers = nn.ModuleList([mHCLlamaBlock(config, n_streams) for _ in range(config.n_layer)])
         self.stream_merge = nn.Linear(n_streams * config.n_embd, config.n_embd)
         self.norm = RMSNorm(config.n_embd)
+        self._casts = {"proj": WeightCache(), "merge": WeightCache(), "output": WeightCache()}
         self.register_buffer("freqs_cis", precompute_freqs_cis(config.n_embd // config.n_head,
                                                                config.block_size * 2))
         self.apply(self._init_weights)
@@ -445,7 +446,7 @@ class mHCWalsh(nn.Module):
     def forward(self, idx, targets=None, kv_cache=None, start_pos=0, return_hidden=False):
         B, T = idx.shape
         h = self.tok_embeddings(idx)
-        h = self.stream_proj(h)
+        h = cached_linear(self.stream_proj, h, self._casts["proj"])
         dt = act_dtype(h)
         h = h.to(dt).view(B, T, self.n_streams, self.config.n_embd)
         freqs_cis = self.freqs_cis[start_pos:start_pos + T]
@@ -461,12 +462,12 @@ class mHCWalsh(nn.Module):
                 h = layer.forward_deferred(h, freqs_cis, kv_cache=kv_cache, layer_idx=layer_idx)
         h = materialize(h)
         h_flat = h.reshape(B, T, self.n_streams * self.config.n_embd)
-        h_out = self.norm(self.stream_merge(h_flat))
+        h_out = self.norm(cached_linear(self.stream_merge, h_flat, self._casts["merge"]))
         if targets is not None:
-            logits = self.output(h_out)
+            logits = cached_linear(self.output, h_out, self._casts["output"])
             loss = F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1), ignore_index=-1)
         else:
-            logits = self.output(h_out[:, -1:, :])
+            logits = cached_linear(self.output, h_out[:, -1:, :], self._casts["output"])
             loss = None
         if return_hidden:
             return logits, loss, h_out

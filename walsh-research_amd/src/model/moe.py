@@ -207,10 +207,14 @@ class HadamardRouter(nn.Module):
             f1, f2 = self._frag.get((w1, w2), lambda: kernels.moe_router_fragments(w1, w2, x2d.dtype),
                                     extra=(x2d.dtype,))
             return kernels.moe_route(x2d, f1, f2, w1.shape[0], self.n_experts, self.top_k, dense=dense, y=y2d)
-        # wide router: the two Linears are plain GEMMs (weights cast to the
-        # activation dtype once per weight version); routing on the logits
-        w1c, w2c = self._frag.get((w1, w2), lambda: (w1.detach().to(x2d.dtype), w2.detach().to(x2d.dtype)),
+        # wide router: weights cast to the activation dtype once per weight
+        # version; in bf16 both products, SiLU and the routing run on the
+        # matrix-core router, in float32 the Linears are library GEMMs
+        w1c, w2c = self._frag.get((w1, w2), lambda: (w1.detach().to(x2d.dtype).contiguous(),
+                                                     w2.detach().to(x2d.dtype).contiguous()),
                                   extra=(x2d.dtype, "gemm"))
+        if kernels.moe_router_wide_supported(x2d, w1.shape[0], self.n_experts, self.top_k):
+            return kernels.moe_router_wide(x2d, w1c, w2c, self.n_experts, self.top_k, dense=dense, y=y2d)
         logits = F.linear(F.silu(F.linear(x2d, w1c)), w2c)
         r = kernels.moe_topk(logits, self.top_k, dense=dense)
         if y2d is not None:
