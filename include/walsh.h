@@ -175,6 +175,19 @@ int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int64_t M, int64
                                     const float *const *betas, void *const *ys, int64_t ldy, const float *rope,
                                     int64_t rope_T, int64_t head_dim, int rope_mask, int dtype, void *stream);
 
+/* walsh_hadamard_linear_multi_ex_fwd: walsh_hadamard_linear_multi_fwd with
+ *   each output's own row stride ldys[i] and group stride gsys[i]
+ *   (element (row, g, o) of output i at ys[i] + row*ldys[i] + g*gsys[i] + o;
+ *   gsys[i] >= out_o, ldys[i] >= 32*gsys[i]): lets the k and v projections
+ *   of a decode step write straight into a head-major KV cache slot
+ *   ([batch][head][position][head_dim], CausalSelfAttention.forward with
+ *   KVCache.update, chassis.py:441-455). */
+int walsh_hadamard_linear_multi_ex_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                                       int64_t n, const uint8_t *const *kweights, const float *const *alphas,
+                                       const float *const *betas, void *const *ys, const int64_t *ldys,
+                                       const int64_t *gsys, const float *rope, int64_t rope_T, int64_t head_dim,
+                                       int rope_mask, int dtype, void *stream);
+
 /* walsh_hadamard_swiglu_fwd: h = silu(gate(x)) * up(x) for two Hadamard
  *   linears of the same shape (in_o -> hid_o) on the same input, fused
  *   (SwiGLUMLP.forward, src/model/chassis.py:498-504, gate_proj/up_proj).
@@ -496,18 +509,20 @@ int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_
 
 /* walsh_moe_router_wide_fwd: HadamardRouter.forward (src/model/moe.py:
  *   418-447) for wide models (n_embd 4096: W1 4096 -> 1024, W2 -> 128
- *   experts), bf16 only, on matrix cores in two launches: h = silu(x W1^T)
- *   [M, H] into the caller's bf16 workspace h (row stride ldh), then
+ *   experts), bf16 only, on matrix cores: h = silu(x W1^T) [M, H], then
  *   logits = h W2^T with the softmax / top-k / routing outputs of
  *   walsh_moe_route_fwd.  W1 [H, C] and W2 [E, H] are plain row-major bf16
  *   matrices (the Linear weights cast to bf16).  The first product, SiLU's
  *   result and the logits are rounded to bfloat16 where torch.autocast
- *   rounds them.  Needs C % 256 == 0, H % 32 == 0, H <= 1024, 16-byte
+ *   rounds them.  work: walsh_moe_router_wide_workspace_bytes(M, H, E)
+ *   bytes, 256-byte aligned; its first M*H bf16 values hold h afterwards.
+ *   Needs C % 256 == 0, H % 128 == 0, H <= 1024, E % 4 == 0, 16-byte
  *   aligned operands and rows. */
+int64_t walsh_moe_router_wide_workspace_bytes(int64_t M, int64_t H, int64_t E);
 int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_t H, const void *w1,
-                              const void *w2, int64_t E, int64_t k, void *h, int64_t ldh, float *probs, float *mask,
-                              float *weights_dense, int *topk_idx, float *topk_w, int *count, float *probsum,
-                              int64_t n_part, void *y, int64_t ldy, int ydtype, void *stream);
+                              const void *w2, int64_t E, int64_t k, void *work, int64_t work_bytes, float *probs,
+                              float *mask, float *weights_dense, int *topk_idx, float *topk_w, int *count,
+                              float *probsum, int64_t n_part, void *y, int64_t ldy, int ydtype, void *stream);
 
 /* walsh_moe_topk_fwd: the softmax / top-k / renormalisation part of
  *   HadamardRouter.forward (src/model/moe.py:432-445) from given float32

@@ -161,8 +161,10 @@ __global__ __launch_bounds__(D) void decode_attn_combine_kernel(const float *__r
     const int b = bh / H, h = bh % H;
     const float *p = part + (int64_t)bh * S * (D + 2);
     float M = -INFINITY;
+#pragma unroll 16
     for (int s = 0; s < S; ++s) M = fmaxf(M, p[s * (D + 2) + D]);
     float num = 0.f, den = 0.f;
+#pragma unroll 16
     for (int s = 0; s < S; ++s) {
         const float w = expf(p[s * (D + 2) + D] - M);
         num += w * p[s * (D + 2) + d];
@@ -172,8 +174,10 @@ __global__ __launch_bounds__(D) void decode_attn_combine_kernel(const float *__r
 }
 
 static int dec_split(int64_t L, int64_t BH, int *chunk) {
-    // enough workgroups to cover the chip twice, chunks of 128 .. kDecMaxChunk keys
-    const int64_t want = (int64_t)device_info().cu_count * 2;
+    // about 8 workgroups per CU, chunks of 128 .. kDecMaxChunk keys (measured
+    // at L 4095, 32 heads: batch 1 takes 32 chunks of 128 keys, batch 16
+    // four of 1024, batch 64 two of 2048)
+    const int64_t want = (int64_t)device_info().cu_count * 8;
     int64_t S = ceil_div(want, BH);
     const int64_t maxS = ceil_div(L, 128);
     if (S > maxS) S = maxS;

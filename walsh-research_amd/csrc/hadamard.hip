@@ -1260,21 +1260,19 @@ WALSH_EXPORT int walsh_hadamard_linear_rope_fwd(const void *x, int64_t ldx, int6
     return hadamard_launch(fn, a, nullptr, M, dtype == WALSH_BF16, (hipStream_t)stream);
 }
 
-WALSH_EXPORT int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
-                                                 int64_t n, const uint8_t *const *kweights, const float *const *alphas,
-                                                 const float *const *betas, void *const *ys, int64_t ldy,
-                                                 const float *rope, int64_t rope_T, int64_t head_dim, int rope_mask,
-                                                 int dtype, void *stream) {
-    const char *fn = "walsh_hadamard_linear_multi_fwd";
-    if (n < 1 || n > kMaxMulti || !kweights || !alphas || !betas || !ys)
+static int hadamard_multi(const char *fn, const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                          int64_t n, const uint8_t *const *kweights, const float *const *alphas,
+                          const float *const *betas, void *const *ys, const int64_t *ldys, const int64_t *gsys,
+                          const float *rope, int64_t rope_T, int64_t head_dim, int rope_mask, int dtype, void *stream) {
+    if (n < 1 || n > kMaxMulti || !kweights || !alphas || !betas || !ys || !ldys || !gsys)
         return set_error(WALSH_EINVAL, "%s: n=%lld (1..%d) or null array", fn, (long long)n, kMaxMulti);
     if (rope_mask & ~((1 << n) - 1)) return set_error(WALSH_EINVAL, "%s: rope_mask 0x%x past n", fn, rope_mask);
     HadArgs base[kMaxMulti];
     for (int i = 0; i < n; ++i) {
-        int rc = hadamard_check(fn, x, ldx, in_o, M, in_o, out_o, ys[i], ldy, out_o, dtype);
+        int rc = hadamard_check(fn, x, ldx, in_o, M, in_o, out_o, ys[i], ldys[i], gsys[i], dtype);
         if (rc) return rc;
         if (!kweights[i] || !alphas[i] || !betas[i]) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
-        base[i] = had_args(x, ldx, in_o, in_o, out_o, kweights[i], alphas[i], betas[i], ys[i], ldy, out_o);
+        base[i] = had_args(x, ldx, in_o, in_o, out_o, kweights[i], alphas[i], betas[i], ys[i], ldys[i], gsys[i]);
         if (rope_mask & (1 << i)) {
             if (!rope || rope_T < 1 || head_dim < 4 || head_dim % 4 || out_o % head_dim || (uintptr_t)rope % 16)
                 return set_error(WALSH_ENOTSUP, "%s: RoPE needs head_dim %% 4 == 0 dividing out_o, 16-byte aligned "
@@ -1289,8 +1287,14 @@ WALSH_EXPORT int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int
     const int64_t esz = bf16 ? 2 : 4;
     const size_t valign = bf16 ? 8 : 16;
     const int Nt = base[0].Nt, Kc = base[0].Kc;
-    bool vec = in_o % 4 == 0 && out_o % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && (uintptr_t)x % valign == 0;
-    for (int i = 0; i < n; ++i) vec = vec && (uintptr_t)ys[i] % valign == 0;
+    bool vec = in_o % 4 == 0 && out_o % 4 == 0 && ldx % 4 == 0 && (uintptr_t)x % valign == 0;
+    int64_t ldy = 0;  // the longest output row stride
+    bool gs128 = in_o == 128 && out_o == 128;
+    for (int i = 0; i < n; ++i) {
+        vec = vec && (uintptr_t)ys[i] % valign == 0 && ldys[i] % 4 == 0 && gsys[i] % 4 == 0;
+        gs128 = gs128 && gsys[i] == 128;
+        if (ldys[i] > ldy) ldy = ldys[i];
+    }
     const bool kc1 = Kc == 1 && (bf16 || Nt == 1);
     const size_t lds = hadamard_lds_bytes(bf16, Kc, Nt);
     hipStream_t s = (hipStream_t)stream;
@@ -1305,10 +1309,12 @@ WALSH_EXPORT int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int
             an.p[i] = base[i];
             an.p[i].M = (int)M;
         }
-        split3_launch(an, in_o == 128 && out_o == 128, false, s);
+        split3_launch(an, gs128, false, s);
         return check_hip(hipGetLastError(), fn);
     }
-    if (!kc1 || !vec || lds > (size_t)device_info().max_shared_per_block) {
+    bool gs_plain = true;  // the one-launch kernel for small in_o writes packed groups
+    for (int i = 0; i < n; ++i) gs_plain = gs_plain && gsys[i] == out_o;
+    if (!kc1 || !vec || !gs_plain || lds > (size_t)device_info().max_shared_per_block) {
         // shapes served by the other kernels: one launch per layer
         for (int i = 0; i < n; ++i) {
             const int rc = hadamard_launch(fn, base[i], nullptr, M, bf16, s);
@@ -1327,7 +1333,7 @@ WALSH_EXPORT int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int
         for (int i = 0; i < n; ++i) {
             an.p[i] = base[i];
             an.p[i].x = (const char *)x + r0 * ldx * esz;
-            an.p[i].y = (char *)ys[i] + r0 * ldy * esz;
+            an.p[i].y = (char *)ys[i] + r0 * ldys[i] * esz;
             an.p[i].M = (int)rows;
             an.p[i].rope_row0 = (int)(r0 % base[i].rope_T);
         }
@@ -1340,6 +1346,30 @@ WALSH_EXPORT int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int
         if (rc) return rc;
     }
     return WALSH_OK;
+}
+
+WALSH_EXPORT int walsh_hadamard_linear_multi_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                                                 int64_t n, const uint8_t *const *kweights, const float *const *alphas,
+                                                 const float *const *betas, void *const *ys, int64_t ldy,
+                                                 const float *rope, int64_t rope_T, int64_t head_dim, int rope_mask,
+                                                 int dtype, void *stream) {
+    int64_t ldys[kMaxMulti], gsys[kMaxMulti];
+    for (int i = 0; i < kMaxMulti; ++i) {
+        ldys[i] = ldy;
+        gsys[i] = out_o;
+    }
+    return hadamard_multi("walsh_hadamard_linear_multi_fwd", x, ldx, M, in_o, out_o, n, kweights, alphas, betas, ys,
+                          ldys, gsys, rope, rope_T, head_dim, rope_mask, dtype, stream);
+}
+
+WALSH_EXPORT int walsh_hadamard_linear_multi_ex_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o,
+                                                    int64_t out_o, int64_t n, const uint8_t *const *kweights,
+                                                    const float *const *alphas, const float *const *betas,
+                                                    void *const *ys, const int64_t *ldys, const int64_t *gsys,
+                                                    const float *rope, int64_t rope_T, int64_t head_dim,
+                                                    int rope_mask, int dtype, void *stream) {
+    return hadamard_multi("walsh_hadamard_linear_multi_ex_fwd", x, ldx, M, in_o, out_o, n, kweights, alphas, betas,
+                          ys, ldys, gsys, rope, rope_T, head_dim, rope_mask, dtype, stream);
 }
 
 WALSH_EXPORT int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t gsx, int64_t M, int64_t in_o,

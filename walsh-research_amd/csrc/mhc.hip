@@ -1141,6 +1141,21 @@ __global__ __launch_bounds__(256) void mhc_apply_tok_kernel(ApplyArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tok = blockIdx.x;
     const int n = a.n, C = a.C, K = n * C;
+    // the token's streams are loaded first: their round trip overlaps the
+    // split sums and the constraints
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
+    const uint32_t xrow = (uint32_t)((int64_t)tok * a.ldx * esz);
+    const int nq = C / 4;
+    constexpr int kQ = 4;  // quads per thread: 256 x 4 x 4 = 4096 columns
+    f32x4 xv[kQ][kMaxStreams];
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) {
+        const int q = tid + 256 * j;
+#pragma unroll
+        for (int st = 0; st < kMaxStreams; ++st)
+            xv[j][st] = Buf4<T>::load(xr, (st < n && q < nq) ? xrow + (uint32_t)(st * C + 4 * q) * esz : kOOB, 0);
+    }
     {
         // splits <= 64 (K / 256 with K <= 16384): each thread's 8 loads are
         // issued together, then added in split order
@@ -1174,20 +1189,14 @@ __global__ __launch_bounds__(256) void mhc_apply_tok_kernel(ApplyArgs a) {
     float hp[kMaxStreams];
 #pragma unroll
     for (int st = 0; st < kMaxStreams; ++st) hp[st] = hpre_s[st];
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
-    const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
-    const uint32_t xrow = (uint32_t)((int64_t)tok * a.ldx * esz);
-    const int nq = C / 4;
-    constexpr int kQ = 4;  // quads per thread: 256 x 4 x 4 = 4096 columns
     f32x4 v[kQ];
     float sq = 0.f;
 #pragma unroll
     for (int j = 0; j < kQ; ++j) {
-        const int q = tid + 256 * j;
         f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int st = 0; st < kMaxStreams; ++st)
-            if (st < n) acc4 += hp[st] * Buf4<T>::load(xr, q < nq ? xrow + (uint32_t)(st * C + 4 * q) * esz : kOOB, 0);
+            if (st < n) acc4 += hp[st] * xv[j][st];
         v[j] = acc4;
         sq += acc4.x * acc4.x + acc4.y * acc4.y + acc4.z * acc4.z + acc4.w * acc4.w;
     }

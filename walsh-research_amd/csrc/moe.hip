@@ -1017,18 +1017,23 @@ static int grid_cap(int64_t waves_needed, int64_t limit = 0) {
 // matrix cores:
 //   1. h = silu(x W1^T) [M, H] into a caller workspace: the 256 x 256-tile
 //      GEMM at many rows; at few rows (decode) router_w1_small_kernel, one
-//      workgroup per 16 hidden units x 16 tokens whose 8 waves split K.
-//   2. router_w2_topk_kernel: logits = h W2^T for 64 tokens per workgroup
-//      (the tile of h staged in LDS, wave w taking experts 16w..16w+15),
-//      then softmax / rank top-k / routing outputs per token as in
-//      walsh_moe_topk_fwd.
+//      workgroup per 16 hidden units x 16 tokens whose 8 waves split K, and
+//      which also forms its 16 hidden units' share of every logit (a
+//      16x16x16 product per 16 experts) into partial sums [H/16][M][E];
+//   2. many rows: router_w2_topk_kernel, logits = h W2^T for 64 tokens per
+//      workgroup (the tile of h staged in LDS, wave w taking experts
+//      16w..16w+15); few rows: router_topk_part_kernel adds the H/16
+//      partial sums in order; then softmax / rank top-k / routing outputs
+//      per token as in walsh_moe_topk_fwd.
 // Products are rounded to bf16 where the reference's autocast Linears round
 // their outputs, with SiLU on the rounded first product.
 constexpr int kR1Waves = 8;
 constexpr int kR1SmallRows = 256;  // row counts up to this take the split-K kernel
 __global__ __launch_bounds__(64 * kR1Waves) void router_w1_small_kernel(const uint16_t *__restrict__ x, int64_t ldx,
                                                                         int M, int C, const uint16_t *__restrict__ w1,
-                                                                        uint16_t *__restrict__ h, int64_t ldh) {
+                                                                        uint16_t *__restrict__ h, int64_t ldh,
+                                                                        const uint16_t *__restrict__ w2, int E,
+                                                                        float *__restrict__ lpart) {
     __shared__ f32x4 part[kR1Waves][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, fr = lane & 15, fq = lane >> 4;
     const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16, H = gridDim.x * 16;
@@ -1038,6 +1043,15 @@ __global__ __launch_bounds__(64 * kR1Waves) void router_w1_small_kernel(const ui
     // operands in flight
     const int kw = C / kR1Waves, k0 = wave * kw;
     const uint32_t wo = (uint32_t)(((int64_t)(n0 + fr) * C + k0 + 8 * fq) * 2);
+    // wave 0's W2 fragments for the partial logits, in flight from the start
+    const __amdgpu_buffer_rsrc_t w2r = make_rsrc(w2, (uint32_t)((int64_t)E * H * 2));
+    u32x2 a2[kMaxE / 16];
+#pragma unroll
+    for (int et = 0; et < kMaxE / 16; ++et) {
+        const int e = 16 * et + fr;
+        a2[et] = __builtin_amdgcn_raw_buffer_load_b64(
+            w2r, (wave == 0 && e < E) ? (uint32_t)(((int64_t)e * H + n0 + 4 * fq) * 2) : kOOB, 0, 0);
+    }
     const bool row_ok = m0 + fr < M;
     const uint32_t xo = row_ok ? (uint32_t)(((int64_t)(m0 + fr) * ldx + k0 + 8 * fq) * 2) : 0;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1065,24 +1079,91 @@ __global__ __launch_bounds__(64 * kR1Waves) void router_w1_small_kernel(const ui
     for (int r = 0; r < 4; ++r) v[r] = silu_f(bf16r(v[r]));
     const __amdgpu_buffer_rsrc_t hr = make_rsrc(h, (uint32_t)((int64_t)M * ldh * 2));
     Buf4<uint16_t>::store(v, hr, row_ok ? (uint32_t)(((int64_t)(m0 + fr) * ldh + n0 + 4 * fq) * 2) : kOOB, 0);
+    // these 16 hidden units' share of the logits: lane (fr, fq) holds the
+    // B operand of a 16x16x16 product (hidden n0 + 4 fq .. +3 of token
+    // m0 + fr); A = W2[16 et + fr][n0 + 4 fq .. +3]
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(lpart + (int64_t)blockIdx.x * M * E, (uint32_t)((int64_t)M * E * 4));
+    const u32x2 b = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+#pragma unroll
+    for (int et = 0; et < kMaxE / 16; ++et) {
+        const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a2[et]),
+                                                                 __builtin_bit_cast(i16x4, b),
+                                                                 f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        // d[r] = partial logit of expert 16 et + 4 fq + r for token m0 + fr
+        // (E % 4 == 0: the 4 experts are valid together)
+        const int e0 = 16 * et + 4 * fq;
+        Buf4<float>::store(d, pr, (row_ok && e0 < E) ? (uint32_t)(((int64_t)(m0 + fr) * E + e0) * 4) : kOOB, 0);
+    }
 }
 
-constexpr int kR2Tok = 64;     // tokens per workgroup tile
+// Few rows: logits = the H/16 partial sums of router_w1_small_kernel added
+// in a fixed order (wave w sums partials 16w..16w+15, then the 4 wave sums
+// in wave order), rounded to bf16; then wave 0 routes the token.
+constexpr int kTopkPartMax = 64;  // H / 16 <= 64
+__global__ __launch_bounds__(kMoeThreads) void router_topk_part_kernel(const float *__restrict__ lpart, int nparts,
+                                                                       RouteOut o) {
+    __shared__ int cnt_l[kMaxE];
+    __shared__ float ps_l[kMaxE];
+    __shared__ __align__(16) float pl[kMaxE];
+    __shared__ __align__(16) float ws[kMoeWaves][kMaxE];
+    part_init(cnt_l, ps_l);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int E = o.E, M = o.M;
+    constexpr int kPer = kTopkPartMax / kMoeWaves;
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(lpart, (uint32_t)((int64_t)nparts * M * E * 4));
+    const int e = 2 * lane;  // lane: experts 2 lane, 2 lane + 1 (one 8-byte load per partial)
+    for (int tok = blockIdx.x; tok < M; tok += gridDim.x) {
+        u32x2 pv[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int jj = wave * kPer + j;
+            pv[j] = __builtin_amdgcn_raw_buffer_load_b64(
+                pr, (e < E && jj < nparts) ? (uint32_t)((((int64_t)jj * M + tok) * E + e) * 4) : kOOB, 0, 0);
+        }
+        float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            acc0 += __uint_as_float(pv[j].x);
+            acc1 += __uint_as_float(pv[j].y);
+        }
+        __syncthreads();  // the previous token's ws is read
+        *(f32x2 *)&ws[wave][e] = f32x2{acc0, acc1};
+        __syncthreads();
+        if (wave == 0) {
+            float lg[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int ee = lane + 64 * hh;
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < kMoeWaves; ++w) v += ws[w][ee];
+                lg[hh] = ee < E ? bf16r(v) : -INFINITY;
+            }
+            rank_token(tok, lg, pl, o, cnt_l, ps_l);
+        }
+    }
+    part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
+}
+
 constexpr int kR2Waves = 8;    // wave w: experts 16w..16w+15
-constexpr int kR2MaxH = 1024;  // staged tile of h: 64 x 1024 bf16 = 128 KB of LDS
+constexpr int kR2MaxH = 1024;  // staged tile of h: up to 64 x 1024 bf16 = 128 KB of LDS
 constexpr int kR2LgStride = kMaxE + 4;
 
-static size_t router_w2_lds_bytes(int H) {
-    const size_t stage = (size_t)kR2Tok * H * 2, lg = (size_t)kR2Tok * kR2LgStride * 4;
+// TT 16-token tiles per workgroup: 4 (64 tokens) for many rows, 1 for a
+// decode-sized batch (a quarter of the staging and the products)
+static size_t router_w2_lds_bytes(int H, int TT) {
+    const size_t stage = (size_t)16 * TT * H * 2, lg = (size_t)16 * TT * kR2LgStride * 4;
     return stage > lg ? stage : lg;
 }
 
 // smem: the h tile, 16-byte chunk c of row r at r * 2H + ((c ^ (r & 15)) << 4)
 // (the 16 rows of a fragment read fall on 16 different chunk columns); after
 // the products the rounded logits [64][kR2LgStride] float.
+template <int TT>
 __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uint16_t *__restrict__ h, int64_t ldh,
                                                                        int H, const uint16_t *__restrict__ w2,
                                                                        RouteOut o) {
+    constexpr int kR2Tok = 16 * TT;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int cnt_l[kMaxE];
     __shared__ float ps_l[kMaxE];
@@ -1105,7 +1186,7 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
         for (int s = 0; s < 16; ++s)
             wa[s] = __builtin_amdgcn_raw_buffer_load_b128(wr, (s < nks && wo != kOOB) ? wo + (uint32_t)s * 64 : kOOB,
                                                           0, 0);
-        u32x4 st[kR2Tok * kR2MaxH / 8 / (64 * kR2Waves)];
+        u32x4 st[kR2Tok * kR2MaxH / 8 / (64 * kR2Waves)];  // TT * 4 chunks per thread
 #pragma unroll
         for (int j = 0; j < kR2Tok * kR2MaxH / 8 / (64 * kR2Waves); ++j) {
             const int i = tid + j * 64 * kR2Waves, r = i / nch, c = i - r * nch;
@@ -1120,9 +1201,9 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
             if (i < kR2Tok * nch) *(u32x4 *)(smem + r * 2 * H + ((c ^ (r & 15)) << 4)) = st[j];
         }
         __syncthreads();
-        f32x4 acc[4];
+        f32x4 acc[TT];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         for (int s0 = 0; s0 < nks; s0 += 16) {
             u32x4 wn[16];
             const bool more = s0 + 16 < nks;
@@ -1137,7 +1218,7 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
                 if (s0 + s < nks) {
                     const int c = 4 * (s0 + s) + fq;
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
+                    for (int t = 0; t < TT; ++t) {
                         const int r = 16 * t + fr;
                         const u32x4 b = *(const u32x4 *)(smem + r * 2 * H + ((c ^ (r & 15)) << 4));
                         acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wa[s]),
@@ -1152,7 +1233,7 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
         __syncthreads();  // every wave is done with the h tile
         // acc[t][r] = logit of expert 16 w + 4 fq + r for token m0 + 16 t + fr
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < TT; ++t) {
             f32x4 v;
 #pragma unroll
             for (int r = 0; r < 4; ++r) v[r] = bf16r(acc[t][r]);
@@ -1225,58 +1306,77 @@ WALSH_EXPORT int walsh_moe_route_fwd(const void *x, int64_t ldx, int64_t M, int6
     return check_hip(hipGetLastError(), fn);
 }
 
+// workspace: h [M][H] bf16, then (M <= kR1SmallRows) the partial logits
+// [H/16][M][E] float
+static int64_t router_h_bytes(int64_t M, int64_t H) { return ceil_div(M * H * 2, 256) * 256; }
+
+WALSH_EXPORT int64_t walsh_moe_router_wide_workspace_bytes(int64_t M, int64_t H, int64_t E) {
+    if (M < 0 || H <= 0 || E <= 0) return 0;
+    return router_h_bytes(M, H) + (M <= kR1SmallRows ? (H / 16) * M * E * 4 : 0);
+}
+
 WALSH_EXPORT int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_t H,
-                                           const void *w1, const void *w2, int64_t E, int64_t k, void *h, int64_t ldh,
-                                           float *probs, float *mask, float *weights_dense, int *topk_idx,
-                                           float *topk_w, int *count, float *probsum, int64_t n_part, void *y,
-                                           int64_t ldy, int ydtype, void *stream) {
+                                           const void *w1, const void *w2, int64_t E, int64_t k, void *work,
+                                           int64_t work_bytes, float *probs, float *mask, float *weights_dense,
+                                           int *topk_idx, float *topk_w, int *count, float *probsum, int64_t n_part,
+                                           void *y, int64_t ldy, int ydtype, void *stream) {
     const char *fn = "walsh_moe_router_wide_fwd";
     int rc = route_out_check(fn, M, E, k, topk_idx, topk_w, count, probsum, n_part);
     if (rc) return rc;
-    if ((M > 0 && (!x || !h)) || !w1 || !w2) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
-    if (C % (32 * kR1Waves) || H % 32 || H < 32 || H > kR2MaxH || ldx < C || ldh < H || (y && ldy < 32 * E))
-        return set_error(WALSH_ENOTSUP, "%s: needs C %% %d == 0 and H %% 32 == 0, H <= %d (C=%lld H=%lld)", fn,
-                         32 * kR1Waves, kR2MaxH, (long long)C, (long long)H);
+    if ((M > 0 && (!x || !work)) || !w1 || !w2) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (C % (32 * kR1Waves) || H % 128 || H > kR2MaxH || E % 4 || ldx < C || (y && ldy < 32 * E))
+        return set_error(WALSH_ENOTSUP, "%s: needs C %% %d == 0, H %% 128 == 0, H <= %d, E %% 4 == 0 (C=%lld H=%lld "
+                         "E=%lld)", fn, 32 * kR1Waves, kR2MaxH, (long long)C, (long long)H, (long long)E);
+    if (work_bytes < walsh_moe_router_wide_workspace_bytes(M, H, E))
+        return set_error(WALSH_EINVAL, "%s: workspace of %lld bytes, needs %lld", fn, (long long)work_bytes,
+                         (long long)walsh_moe_router_wide_workspace_bytes(M, H, E));
     if (ydtype != WALSH_F32 && ydtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: ydtype", fn);
     const int64_t ysz = ydtype == WALSH_BF16 ? 2 : 4;
-    if (ldx % 8 || ldh % 8 || (uintptr_t)x % 16 || (uintptr_t)h % 16 || (uintptr_t)w1 % 16 || (uintptr_t)w2 % 16 ||
+    if (ldx % 8 || (uintptr_t)x % 16 || (uintptr_t)work % 256 || (uintptr_t)w1 % 16 || (uintptr_t)w2 % 16 ||
         (y && ((uintptr_t)y % 16 || ldy % (16 / ysz))))
-        return set_error(WALSH_ENOTSUP, "%s: operands and rows must be 16-byte aligned", fn);
-    if (M * ldx * 2 > (int64_t)kMaxBufferBytes || M * ldh * 2 > (int64_t)kMaxBufferBytes ||
+        return set_error(WALSH_ENOTSUP, "%s: operands and rows must be 16-byte aligned (workspace 256)", fn);
+    if (M * ldx * 2 > (int64_t)kMaxBufferBytes || M * H * 2 > (int64_t)kMaxBufferBytes ||
         H * C * 2 > (int64_t)kMaxBufferBytes)
         return set_error(WALSH_ENOTSUP, "%s: operands above 2^31 bytes", fn);
-    if (router_w2_lds_bytes((int)H) + 8 * kMaxE + kR2Waves * kMaxE * 4 > (size_t)device_info().max_shared_per_block)
+    if (router_w2_lds_bytes((int)H, 4) + 8 * kMaxE + kR2Waves * kMaxE * 4 > (size_t)device_info().max_shared_per_block)
         return set_error(WALSH_ENOTSUP, "%s: H=%lld needs more LDS than a workgroup has", fn, (long long)H);
     hipStream_t s = (hipStream_t)stream;
     if (M == 0) {
         launch(moe_zero_kernel, dim3(1), dim3(256), 0, s, count, probsum, (int)(n_part * E));
         return check_hip(hipGetLastError(), fn);
     }
-    if (M <= kR1SmallRows) {
-        launch(router_w1_small_kernel, dim3((unsigned)(H / 16), (unsigned)ceil_div(M, 16)), dim3(64 * kR1Waves), 0, s,
-               (const uint16_t *)x, ldx, (int)M, (int)C, (const uint16_t *)w1, (uint16_t *)h, ldh);
-    } else {
-        Gemm256Args g;
-        g.x = x;
-        g.ldx = ldx;
-        g.M = (int)M;
-        g.N = (int)H;
-        g.K = (int)C;
-        g.Kp = (int)C;
-        g.B = w1;
-        g.beta = nullptr;
-        g.out_o = (int)H;
-        g.y = h;
-        g.ldy = ldh;
-        gemm256_launch<kEpiSilu>(g, s);
-    }
-    rc = check_hip(hipGetLastError(), fn);
-    if (rc) return rc;
+    uint16_t *h = (uint16_t *)work;
     const RouteOut o{(int)M, (int)E, (int)k, probs, mask, weights_dense, topk_idx, topk_w, count, probsum,
                      (int)n_part, y, ldy, ydtype == WALSH_BF16};
-    const int64_t tiles = ceil_div(M, kR2Tok);
-    launch(router_w2_topk_kernel, dim3((unsigned)(tiles < n_part ? tiles : n_part)), dim3(64 * kR2Waves),
-           (uint32_t)router_w2_lds_bytes((int)H), s, (const uint16_t *)h, ldh, (int)H, (const uint16_t *)w2, o);
+    if (M <= kR1SmallRows) {
+        float *lpart = (float *)((char *)work + router_h_bytes(M, H));
+        launch(router_w1_small_kernel, dim3((unsigned)(H / 16), (unsigned)ceil_div(M, 16)), dim3(64 * kR1Waves), 0, s,
+               (const uint16_t *)x, ldx, (int)M, (int)C, (const uint16_t *)w1, h, H, (const uint16_t *)w2, (int)E,
+               lpart);
+        rc = check_hip(hipGetLastError(), fn);
+        if (rc) return rc;
+        launch(router_topk_part_kernel, dim3((unsigned)(M < n_part ? M : n_part)), dim3(kMoeThreads), 0, s,
+               (const float *)lpart, (int)(H / 16), o);
+        return check_hip(hipGetLastError(), fn);
+    }
+    Gemm256Args g;
+    g.x = x;
+    g.ldx = ldx;
+    g.M = (int)M;
+    g.N = (int)H;
+    g.K = (int)C;
+    g.Kp = (int)C;
+    g.B = w1;
+    g.beta = nullptr;
+    g.out_o = (int)H;
+    g.y = h;
+    g.ldy = H;
+    gemm256_launch<kEpiSilu>(g, s);
+    rc = check_hip(hipGetLastError(), fn);
+    if (rc) return rc;
+    const int64_t tiles = ceil_div(M, 64), grid = tiles < n_part ? tiles : n_part;
+    launch(router_w2_topk_kernel<4>, dim3((unsigned)grid), dim3(64 * kR2Waves), (uint32_t)router_w2_lds_bytes((int)H, 4),
+           s, (const uint16_t *)h, (int64_t)H, (int)H, (const uint16_t *)w2, o);
     return check_hip(hipGetLastError(), fn);
 }
 

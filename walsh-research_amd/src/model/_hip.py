@@ -44,6 +44,8 @@ SIGNATURES = {
     "walsh_hadamard_linear_rope_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I, _P]),
     "walsh_hadamard_linear_multi_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _I64, _I64,
                                              _I, _I, _P]),
+    "walsh_hadamard_linear_multi_ex_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                                _I64, _I, _I, _P]),
     "walsh_hadamard_dense_weight_bytes": (_I64, [_I64, _I64, _I]),
     "walsh_hadamard_dense_prepare": (_I, [_P, _I64, _I64, _I, _I, _P, _P]),
     "walsh_head_mixer_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I, _P]),
@@ -90,6 +92,7 @@ SIGNATURES = {
                                     _P, _I64, _I, _P]),
     "walsh_moe_route_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64,
                                  _P, _I64, _I, _I, _P]),
+    "walsh_moe_router_wide_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "walsh_moe_router_wide_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P,
                                        _P, _P, _I64, _P, _I64, _I, _P]),
     "walsh_moe_topk_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),

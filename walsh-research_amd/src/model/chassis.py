@@ -113,6 +113,20 @@ class KVCache:
         vc[:b, s:e] = v.to(vc.dtype)
         return kc[:b, :e], vc[:b, :e]
 
+    def slot(self, layer_idx: int, b: int, new_len: int = 1) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Views [b, new_len, n_head, head_dim] of the positions the next
+        ``update`` of this layer would write, for producers that store there
+        directly (then ``filled`` replaces ``update``)."""
+        s = self.cached_len
+        assert b <= self.batch and s + new_len <= self.max_seq_len, "KV cache overflow"
+        return (self.k_cache[layer_idx].transpose(1, 2)[:b, s:s + new_len],
+                self.v_cache[layer_idx].transpose(1, 2)[:b, s:s + new_len])
+
+    def filled(self, layer_idx: int, b: int, new_len: int = 1) -> Tuple[torch.Tensor, torch.Tensor]:
+        """What ``update`` returns, once the new positions hold their k and v."""
+        e = self.cached_len + new_len
+        return self.k_cache[layer_idx].transpose(1, 2)[:b, :e], self.v_cache[layer_idx].transpose(1, 2)[:b, :e]
+
     def increment(self, n: int = 1):
         self.cached_len += n
 
@@ -190,23 +204,32 @@ class CausalSelfAttention(nn.Module):
         self.dropout = config.dropout
         self.head_mixer = get_head_mixer(config, self.head_dim)
 
-    def _qkv_multi(self, x, freqs_cis, T):
+    def _qkv_multi(self, x, freqs_cis, T, outs=None):
         """q (roped), k (roped), v in one launch (walsh_hadamard_linear_multi_fwd),
-        or None when the layers, shapes or autograd do not allow it."""
+        or None when the layers, shapes or autograd do not allow it.  ``outs``:
+        optional tensors to write (kernels.hadamard_linear_multi)."""
         inner = _qkv_layers(self)
         if inner is None or x.dim() != 3 or freqs_cis.shape[0] < T:
             return None
         if any(i._needs_grad(x) for i in inner) or not kernels.rope_supported(x, inner[0].out_o, self.head_dim):
             return None
         layers = [(i.ternary_state()[2], i.alpha, i.beta, r) for i, r in zip(inner, (True, True, False))]
-        return kernels.hadamard_linear_multi(x, inner[0].in_o, inner[0].out_o, layers, freqs_cis, self.head_dim)
+        return kernels.hadamard_linear_multi(x, inner[0].in_o, inner[0].out_o, layers, freqs_cis, self.head_dim,
+                                             outs=outs)
 
     def forward(self, x, freqs_cis, kv_cache: Optional[KVCache] = None, layer_idx: int = 0):
         B, T, C = x.size()
         dt = act_dtype(x)
         x = x.to(dt)
         q = k = None
-        fused = self._qkv_multi(x, freqs_cis, T)
+        fused, in_cache = None, False
+        if (kv_cache is not None and T == 1 and B <= kv_cache.batch and self.n_head == 32
+                and kv_cache.cached_len < kv_cache.max_seq_len and kv_cache.k_cache[layer_idx].dtype == dt):
+            # decode: k and v go straight into the cache slot (no copy kernels)
+            fused = self._qkv_multi(x, freqs_cis, T, outs=(None,) + kv_cache.slot(layer_idx, B))
+            in_cache = fused is not None
+        if fused is None:
+            fused = self._qkv_multi(x, freqs_cis, T)
         if fused is not None:
             q, k, v = (t.view(B, T, self.n_head, self.head_dim) for t in fused)
         elif hasattr(self.wq, "forward_full_rope") and freqs_cis.shape[0] >= T:
@@ -225,7 +248,7 @@ class CausalSelfAttention(nn.Module):
             v = _full(self.wv, x).view(B, T, self.n_head, self.head_dim)
             q, k = apply_rotary_emb(q, k, freqs_cis)
         if kv_cache is not None:
-            k, v = kv_cache.update(layer_idx, k, v)
+            k, v = kv_cache.filled(layer_idx, B) if in_cache else kv_cache.update(layer_idx, k, v)
         q = q.transpose(1, 2)
         k = k.transpose(1, 2).to(q.dtype)
         v = v.transpose(1, 2).to(q.dtype)

@@ -200,12 +200,26 @@ def hadamard_linear_rope(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.
     return y
 
 
+def _group_rows_view(y: torch.Tensor, rows: int, out_o: int):
+    """(row stride, group stride) of an output given as [rows, 32, out_o]
+    (any leading shape with that many rows) with unit inner stride, or None."""
+    if y.dim() < 2 or y.stride(-1) != 1 or y.shape[-1] != out_o or y.shape[-2] != 32:
+        return None
+    lead = [(d, st) for d, st in zip(y.shape[:-2], y.stride()[:-2]) if d != 1]
+    if len(lead) > 1 or (lead and lead[0][0] != rows) or (not lead and rows != 1):
+        return None
+    return (lead[0][1] if lead else 32 * y.stride(-2)), y.stride(-2)
+
+
 def hadamard_linear_multi(x: torch.Tensor, in_o: int, out_o: int, layers, freqs_cis: torch.Tensor = None,
-                          head_dim: int = None):
+                          head_dim: int = None, outs=None):
     """Several Hadamard linears of one shape on the same rows x [B, T, C] in
     one launch: ``layers`` = [(kweight, alpha, beta, rope)], rope True applies
     the rotary embedding (freqs_cis rows, head_dim) on that layer's store.
-    Returns the outputs [B, T, 32*out_o] in x.dtype."""
+    Returns the outputs [B, T, 32*out_o] in x.dtype.  ``outs`` may give, per
+    layer, a tensor to write instead (None: allocate), viewed as
+    [rows, 32, out_o] with any row and group strides (e.g. a KV cache slot
+    [B, 1, n_head, head_dim]); it is returned in that layer's place."""
     import ctypes
     _hip.require_device(x, "input")
     n = len(layers)
@@ -215,9 +229,19 @@ def hadamard_linear_multi(x: torch.Tensor, in_o: int, out_o: int, layers, freqs_
     if xv.data_ptr() % (4 * x.element_size()) or ldx % 4:
         xv = xv.contiguous()
         ldx = xv.stride(0)
-    ys = [torch.empty(x.shape[:-1] + (32 * out_o,), device=x.device, dtype=dt) for _ in range(n)]
+    outs = list(outs) if outs is not None else [None] * n
+    ys = [o if o is not None else torch.empty(x.shape[:-1] + (32 * out_o,), device=x.device, dtype=dt)
+          for o in outs]
     if rows == 0:
         return ys
+    strides = []
+    for i, o in enumerate(outs):
+        if o is None:
+            strides.append((32 * out_o, out_o))
+        else:
+            st = _group_rows_view(o, rows, out_o)
+            assert st is not None and o.dtype == dt, "output view must be [rows, 32, out_o] in x.dtype"
+            strides.append(st)
     keep = []
     kws, als, bes, yps = [], [], [], []
     mask = 0
@@ -237,11 +261,19 @@ def hadamard_linear_multi(x: torch.Tensor, in_o: int, out_o: int, layers, freqs_
     arrs = [(ctypes.c_void_p * n)(*v) for v in (kws, als, bes, yps)]
     kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, True, in_o <= 16)
     nbytes = rows * 32 * (in_o + n * out_o) * x.element_size()
-    _hip.call("walsh_hadamard_linear_multi_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, n,
-              *[ctypes.addressof(a) for a in arrs], 32 * out_o, 0 if table is None else table.data_ptr(),
-              T, head_dim or 4, mask, _hip.dtype_code(dt), _hip.stream(x.device),
-              kernel="hadamard_fwdn_kernel<%s,x%d>" % ("bf16" if dt == torch.bfloat16 else "f32", n),
-              nbytes=nbytes, flops=flops * n)
+    kname = "hadamard_fwdn_kernel<%s,x%d>" % ("bf16" if dt == torch.bfloat16 else "f32", n)
+    rope_args = (0 if table is None else table.data_ptr(), T, head_dim or 4, mask, _hip.dtype_code(dt),
+                 _hip.stream(x.device))
+    if all(o is None for o in outs):
+        _hip.call("walsh_hadamard_linear_multi_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, n,
+                  *[ctypes.addressof(a) for a in arrs], 32 * out_o, *rope_args, kernel=kname, nbytes=nbytes,
+                  flops=flops * n)
+    else:
+        lds = (ctypes.c_int64 * n)(*[st[0] for st in strides])
+        gss = (ctypes.c_int64 * n)(*[st[1] for st in strides])
+        _hip.call("walsh_hadamard_linear_multi_ex_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, n,
+                  *[ctypes.addressof(a) for a in arrs], ctypes.addressof(lds), ctypes.addressof(gss), *rope_args,
+                  kernel=kname, nbytes=nbytes, flops=flops * n)
     return ys
 
 
@@ -1117,15 +1149,16 @@ def moe_route(x: torch.Tensor, w1f: torch.Tensor, w2f: torch.Tensor, H1: int, E:
 
 def moe_router_wide_supported(x2d: torch.Tensor, H: int, E: int, k: int) -> bool:
     """Whether walsh_moe_router_wide_fwd takes this bf16 router: C % 256 == 0,
-    H % 32 == 0, H <= 1024, E <= 128, k <= 8, 16-byte aligned rows, x under
+    H % 128 == 0, H <= 1024, E <= 128 with E % 4 == 0, k <= 8, 16-byte aligned rows, x under
     2^31 bytes."""
     if x2d.dtype != torch.bfloat16 or not x2d.is_cuda or x2d.dim() != 2:
         return False
     M, C = x2d.shape
-    shape_ok = C % 256 == 0 and H % 32 == 0 and 32 <= H <= 1024 and E <= 128 and k <= min(8, E)
+    shape_ok = C % 256 == 0 and H % 128 == 0 and 128 <= H <= 1024 and E <= 128 and E % 4 == 0 and k <= min(8, E)
     if M == 0:
         return shape_ok
-    return shape_ok and x2d.stride(-1) == 1 and x2d.stride(0) % 8 == 0 and x2d.data_ptr() % 16 == 0 and M * x2d.stride(0) * 2 < 2 ** 31
+    return (shape_ok and x2d.stride(-1) == 1 and x2d.stride(0) % 8 == 0 and x2d.data_ptr() % 16 == 0
+            and M * x2d.stride(0) * 2 < 2 ** 31)
 
 
 def moe_router_wide(x2d: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, E: int, k: int, dense: bool = False,
@@ -1139,8 +1172,9 @@ def moe_router_wide(x2d: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, E: in
     assert w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16 and w1.is_contiguous() and w2.is_contiguous()
     M, C = x2d.shape
     H = w1.shape[0]
-    r = MoERoute(M, E, k, x2d.device, dense, _parts(M, 64, x2d.device))
-    h = torch.empty(max(M, 1), H, device=x2d.device, dtype=torch.bfloat16)
+    r = MoERoute(M, E, k, x2d.device, dense, _parts(M, 64 if M > 256 else 1, x2d.device))
+    nws = _hip.lib().walsh_moe_router_wide_workspace_bytes(M, H, E)
+    work = torch.empty(max(nws, 256), device=x2d.device, dtype=torch.uint8)
     ldy, ydt = 0, torch.bfloat16
     if y is not None:
         assert y.shape[-1] == 32 * E and y.stride(-1) == 1, "output layout"
@@ -1148,12 +1182,14 @@ def moe_router_wide(x2d: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, E: in
     nbytes = M * C * 2 + (H * C + E * H) * 2 + 2 * M * H * 2 + M * k * 8
     if y is not None:
         nbytes += M * (E - k) * 32 * y.element_size()
-    _hip.call("walsh_moe_router_wide_fwd", x2d.data_ptr(), x2d.stride(0) if M else C, M, C, H, w1.data_ptr(), w2.data_ptr(), E, k,
-              h.data_ptr(), H, _hip.ptr(r.probs), _hip.ptr(r.mask), _hip.ptr(r.weights), r.topk_idx.data_ptr(),
-              r.topk_w.data_ptr(), r.count_part.data_ptr(), r.probsum_part.data_ptr(), r.parts, _hip.ptr(y), ldy,
-              _hip.dtype_code(ydt), _hip.stream(x2d.device), kernel="moe_router_wide<bf16>", nbytes=nbytes,
-              flops=2 * M * (C * H + H * E))
-    return (r, h[:M]) if return_hidden else r
+    _hip.call("walsh_moe_router_wide_fwd", x2d.data_ptr(), x2d.stride(0) if M else C, M, C, H, w1.data_ptr(),
+              w2.data_ptr(), E, k, work.data_ptr(), work.numel(), _hip.ptr(r.probs), _hip.ptr(r.mask),
+              _hip.ptr(r.weights), r.topk_idx.data_ptr(), r.topk_w.data_ptr(), r.count_part.data_ptr(),
+              r.probsum_part.data_ptr(), r.parts, _hip.ptr(y), ldy, _hip.dtype_code(ydt), _hip.stream(x2d.device),
+              kernel="moe_router_wide<bf16>", nbytes=nbytes, flops=2 * M * (C * H + H * E))
+    if return_hidden:
+        return r, work[:M * H * 2].view(torch.bfloat16).view(M, H)
+    return r
 
 
 def moe_topk(logits: torch.Tensor, k: int, dense: bool = False) -> MoERoute:
