@@ -17,6 +17,8 @@
 //
 // Both transforms are left unnormalised; the 1/sqrt(32)^2 = 1/32 is folded
 // into beta (exact: a power of two).
+#include <type_traits>
+
 #include "hadamard_core.h"
 
 namespace walsh {
@@ -53,8 +55,11 @@ __global__ void hadamard_prepare_kernel(const uint8_t *__restrict__ packed, int 
 // DENSE: float weights instead of ternary codes (the Hadamard head mixer),
 // as matrix-core A fragments [Nt][Kc][32 g][64 lanes] (bf16x4 or f32x4)
 // copied into LDS in place of the code table.
-template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE>
+// PIPE1: the bf16 single-chunk, single-output-tile shape (in_o, out_o <= 16,
+// VEC, not DENSE) in its own software-pipelined loop.
+template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE, bool PIPE1 = false>
 __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int nblk) {
+    static_assert(!PIPE1 || (BF16MMA && VEC && KC1 && !DENSE), "PIPE1 shape");
     extern __shared__ __align__(16) unsigned char smem[];
     void *lut = smem;
     const size_t wbytes = DENSE ? (size_t)a.Nt * a.Kc * 32 * 64 * dense_frag_bytes<BF16MMA>() : lut_bytes<BF16MMA>();
@@ -117,6 +122,94 @@ __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int
             contract<BF16MMA>(a, nt, c, lane, xm, lut, acc);
     };
 
+    if constexpr (PIPE1) {
+        // bf16, one input chunk and one output tile (in_o, out_o <= 16):
+        // software-pipelined over the wave's tiles.
+        // The next tile's x (raw bf16, 64 registers) is requested right after
+        // the last products of the current one, so its loads are in flight
+        // during the output transform and the stores; the input transform
+        // runs in two passes of 2 columns (64 registers of float pairs).
+        const int i0 = 4 * q;
+        const uint32_t gsb = (uint32_t)a.gsx * 2;
+        auto x_off = [&](int tl) -> uint32_t {
+            const int r = tl * kTile + t;
+            return (tl < n_tiles && r < a.M && i0 < a.in_o) ? x_row_off(a, r, 2) + (uint32_t)i0 * 2 : kOOB;
+        };
+        const f32x4 *al = alpha_l + q * 32;
+        u32x2 xraw[32];
+        int tile = blk * wt + wave;
+        {
+            const uint32_t o0 = x_off(tile);
+#pragma unroll
+            for (int g = 0; g < 32; ++g) xraw[g] = __builtin_amdgcn_raw_buffer_load_b64(xr, o0, (uint32_t)g * gsb, 0);
+        }
+        for (; tile < n_tiles; tile += stride) {
+            const int row = tile * kTile + t;
+            const bool row_ok = row < a.M;
+            const uint32_t yoff = (uint32_t)((int64_t)row * a.ldy * esz);
+            XM<true> xm;
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                f32x2 v[32];
+#pragma unroll
+                for (int g = 0; g < 32; ++g) {
+                    const uint32_t u = p ? xraw[g].y : xraw[g].x;
+                    const f32x2 ag = *((const f32x2 *)&al[g] + p);
+                    v[g] = f32x2{__uint_as_float(u << 16) * ag[0], __uint_as_float(u & 0xffff0000u) * ag[1]};
+                    if ((g & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+                }
+                fht32<f32x2>(v);
+#pragma unroll
+                for (int g = 0; g < 32; ++g) ((uint32_t *)&xm.b[g])[p] = pack_bf16x2(v[g][0], v[g][1]);
+            }
+            {
+                constexpr int nt = 0;
+                f32x4 acc[32];
+#pragma unroll
+                for (int g = 0; g < 32; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+                contract<true>(a, nt, 0, lane, xm, lut, acc);
+                // the next tile's x is requested before any store of this one:
+                // a wait for a load also waits for every memory operation
+                // issued before it, so loads queued behind stores would wait
+                // for the stores
+                __builtin_amdgcn_sched_barrier(0);
+                {
+                    const uint32_t on = x_off(tile + stride);
+#pragma unroll
+                    for (int g = 0; g < 32; ++g)
+                        xraw[g] = __builtin_amdgcn_raw_buffer_load_b64(xr, on, (uint32_t)g * gsb, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // output transform, then beta (and RoPE) and the stores
+                fht32x4(acc);
+                const int o0 = kNTile * nt + 4 * q;
+                const bool ok = row_ok && o0 < a.out_o;
+                const uint32_t voff = ok ? yoff + (uint32_t)o0 * 2 : kOOB;
+                const uint32_t hstride = (uint32_t)a.gsy * 2;
+                const f32x4 *bl = beta_l + (nt * 4 + q) * 32;
+                const bool rope = a.rope != nullptr;
+                const f32x4 cs = (rope && ok) ? rope_cs(a, row, o0) : f32x4{1.f, 0.f, 1.f, 0.f};
+                auto stores = [&](auto with_rope) {
+#pragma unroll
+                    for (int h0 = 0; h0 < 32; h0 += 4) {
+                        f32x4 b8[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) b8[j] = bl[h0 + j];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            f32x4 r = acc[h0 + j] * b8[j];
+                            if constexpr (decltype(with_rope)::value) r = rope_apply(r, cs);
+                            Buf4<uint16_t>::store(r, yr, voff, (uint32_t)(h0 + j) * hstride);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                };
+                if (rope) stores(std::true_type{});
+                else stores(std::false_type{});
+            }
+        }
+        return;
+    }
     for (int tile = blk * wt + wave; tile < n_tiles; tile += stride) {
         const int row = tile * kTile + t;
         const bool row_ok = row < a.M;
@@ -148,9 +241,9 @@ __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int
     }
 }
 
-template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE = false>
+template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE = false, bool PIPE1 = false>
 __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void hadamard_fwd_kernel(HadArgs a) {
-    hadamard_fwd_body<T, BF16MMA, VEC, KC1, DENSE>(a, blockIdx.x, gridDim.x);
+    hadamard_fwd_body<T, BF16MMA, VEC, KC1, DENSE, PIPE1>(a, blockIdx.x, gridDim.x);
 }
 
 // Several Hadamard linears of one shape on the same input rows in one launch
@@ -163,10 +256,10 @@ struct HadArgsN {
     int n;
 };
 
-template <typename T, bool BF16MMA, bool VEC, bool KC1>
+template <typename T, bool BF16MMA, bool VEC, bool KC1, bool PIPE1 = false>
 __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void hadamard_fwdn_kernel(HadArgsN an) {
     const int l = blockIdx.x % an.n;
-    hadamard_fwd_body<T, BF16MMA, VEC, KC1, false>(an.p[l], blockIdx.x / an.n, gridDim.x / an.n);
+    hadamard_fwd_body<T, BF16MMA, VEC, KC1, false, PIPE1>(an.p[l], blockIdx.x / an.n, gridDim.x / an.n);
 }
 
 // ---------------------------------------------------------------- wide layers
@@ -1175,7 +1268,8 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
         } else {
 #define WALSH_HAD_LAUNCH(T, MMA, V, K1) launch((hadamard_fwd_kernel<T, MMA, V, K1>), G, B, lds, s, a)
             if (bf16) {
-                if (vec) { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, true, true); else WALSH_HAD_LAUNCH(uint16_t, true, true, false); }
+                if (vec && kc1 && Nt == 1) launch((hadamard_fwd_kernel<uint16_t, true, true, true, false, true>), G, B, lds, s, a);
+                else if (vec) { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, true, true); else WALSH_HAD_LAUNCH(uint16_t, true, true, false); }
                 else     { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, false, true); else WALSH_HAD_LAUNCH(uint16_t, true, false, false); }
             } else {
                 if (vec) { if (kc1) WALSH_HAD_LAUNCH(float, false, true, true); else WALSH_HAD_LAUNCH(float, false, true, false); }
@@ -1340,7 +1434,8 @@ static int hadamard_multi(const char *fn, const void *x, int64_t ldx, int64_t M,
         int64_t grid = ceil_div(ceil_div(rows, kTile), kWaves);
         if (grid > cap) grid = cap;
         const dim3 G((unsigned)(grid * n)), B(kThreads);
-        if (bf16) launch((hadamard_fwdn_kernel<uint16_t, true, true, true>), G, B, lds, s, an);
+        if (bf16 && Nt == 1) launch((hadamard_fwdn_kernel<uint16_t, true, true, true, true>), G, B, lds, s, an);
+        else if (bf16) launch((hadamard_fwdn_kernel<uint16_t, true, true, true>), G, B, lds, s, an);
         else launch((hadamard_fwdn_kernel<float, false, true, true>), G, B, lds, s, an);
         const int rc = check_hip(hipGetLastError(), fn);
         if (rc) return rc;
