@@ -316,6 +316,19 @@ int walsh_octonion_bwd_fold(const float *C, int64_t ldc, int64_t n_parts, int64_
                             int64_t in_o, int64_t out_o, const float *beta, const float *latent, float *dweight,
                             float *dbeta, void *stream);
 
+/* walsh_octonion_bwd_params: the parameter gradients of
+ *   walsh_octonion_bwd_fold with C = gy^T x formed here, on the GPU:
+ *   gy [M, ldg] and x [M, ldx] (dtype) are transposed into token-contiguous
+ *   rows in the workspace, a split-K matrix-core GEMM writes float32 partial
+ *   sums of C (one per K split) and the fold adds them in split order
+ *   (the dW kernel of cayley_dickson_cuda.py:225-307 with the dbeta sum of
+ *   :540-563).  work: walsh_octonion_bwd_params_workspace_bytes(M, in_o,
+ *   out_o, dtype) bytes, 256-byte aligned.  M >= 1. */
+int64_t walsh_octonion_bwd_params_workspace_bytes(int64_t M, int64_t in_o, int64_t out_o, int dtype);
+int walsh_octonion_bwd_params(const void *gy, int64_t ldg, const void *x, int64_t ldx, int64_t M, int64_t in_o,
+                              int64_t out_o, const uint8_t *packed, const float *beta, const float *latent,
+                              float *dweight, float *dbeta, int dtype, void *work, int64_t work_bytes, void *stream);
+
 /* ------------------------------------------------------------------ decode attention
  * CausalSelfAttention.forward with a KV cache at T == 1
  * (src/model/chassis.py:441-478, cache :262-330): o = softmax(q K^T * scale) V

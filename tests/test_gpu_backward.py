@@ -157,8 +157,11 @@ def _oct_parts(rows, n_o):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("in_o,out_o,M", [(128, 128, 300), (16, 8, 100), (5, 3, 33), (64, 128, 1)])
+@pytest.mark.parametrize("in_o,out_o,M", [(128, 128, 300), (16, 8, 100), (5, 3, 33), (64, 128, 1), (128, 128, 4000)])
 def test_octonion_bwd_vs_oracle(K, in_o, out_o, M, dtype):
+    """gx on the forward GEMM (transposed block matrix), dweight / dbeta from
+    the split-K product C = gy^T x (16 splits, the last partial, at M 4000;
+    one at M <= 100) and the fold, against the float64 oracle."""
     from oracle import octonion as ooct
     print(f"case octonion in_o={in_o} out_o={out_o} M={M} dtype={dtype}", flush=True)
     gen = torch.Generator().manual_seed(in_o + 3 * out_o + M)

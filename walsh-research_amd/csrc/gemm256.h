@@ -14,9 +14,15 @@ struct Gemm256Args {
     int out_o;
     void *y;
     int64_t ldy;
+    // split-K (kspan > 0): split s sums columns [s kspan, (s+1) kspan) and
+    // writes its own output ysplit elements after split s-1's
+    int splits;
+    int64_t kspan, ysplit;
 };
 
-enum { kEpiBeta = 0, kEpiSilu = 1 };
+// epilogues: beta scaling to bf16 (octonion forward), SiLU of the bf16-rounded
+// product to bf16 (router), plain float32 (split-K partial sums)
+enum { kEpiBeta = 0, kEpiSilu = 1, kEpiF32 = 2 };
 
 // Round to the nearest bfloat16 and back: where the reference runs under
 // bf16 autocast, every Linear/einsum output and elementwise result is a
@@ -52,8 +58,13 @@ template <int EPI>
 __device__ __forceinline__ void gemm256_body(const Gemm256Args &a, int nM, int nN, int per_xcd) {
     __shared__ __align__(16) unsigned char lds[2][2][kOTile];  // [buffer][x | weights]
 
-    const int tile = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-    if (tile >= nM * nN) return;
+    int tile = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    const int splits = a.splits > 0 ? a.splits : 1;
+    if (tile >= nM * nN * splits) return;
+    const int split = tile / (nM * nN);
+    tile -= split * nM * nN;
+    const int k_lo = a.kspan > 0 ? (int)(split * a.kspan) : 0;
+    const int k_hi = a.kspan > 0 ? (int)(k_lo + a.kspan < a.K ? k_lo + a.kspan : a.K) : a.K;
     const int mb = tile / nN, nb = tile - mb * nN;
     const int m0 = mb * kOBM, n0 = nb * kOBN;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -68,14 +79,15 @@ __device__ __forceinline__ void gemm256_body(const Gemm256Args &a, int nM, int n
     // tid & 7.  Out-of-range chunks read zeros.
     const int srow = tid >> 3, spart = tid & 7;
     auto load = [&](int k0, u32x4 (&xst)[4], u32x4 (&wst)[4]) {
-        const int k = k0 + spart * 8;
+        const int k = k_lo + k0 + spart * 8;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = m0 + srow + 64 * i, n = n0 + srow + 64 * i;
             xst[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                xr, (m < a.M && k < a.K) ? (uint32_t)(((int64_t)m * a.ldx + k) * 2) : kOOB, 0, 0);
+                xr, (m < a.M && k < k_hi) ? (uint32_t)(((int64_t)m * a.ldx + k) * 2) : kOOB, 0, 0);
             wst[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                br, (n < a.N && k < a.Kp) ? (uint32_t)(((int64_t)n * a.Kp + k) * 2) : kOOB, 0, 0);
+                br, (n < a.N && k < (a.kspan > 0 ? k_hi : a.Kp)) ? (uint32_t)(((int64_t)n * a.Kp + k) * 2) : kOOB,
+                0, 0);
         }
     };
     auto store = [&](int buf, const u32x4 (&xst)[4], const u32x4 (&wst)[4]) {
@@ -126,7 +138,7 @@ __device__ __forceinline__ void gemm256_body(const Gemm256Args &a, int nM, int n
         __syncthreads();
     };
 
-    const int nst = (int)ceil_div(a.K, kOBK);
+    const int nst = (int)ceil_div(k_hi - k_lo, kOBK);
     u32x4 xa[4], wa[4], xb[4], wb[4];
     load(0, xa, wa);
     load(kOBK, xb, wb);
@@ -140,6 +152,22 @@ __device__ __forceinline__ void gemm256_body(const Gemm256Args &a, int nM, int n
     if (st < nst) stage(st, xb, wb, xa, wa);
 
     // epilogue: acc[i][j][r] = D[n = 16 i + 4 fq + r][m = 16 j + fr] of the wave's tile
+    if constexpr (EPI == kEpiF32) {
+        const int64_t span = a.kspan > 0 ? (int64_t)(splits - 1) * a.ysplit + (int64_t)a.M * a.ldy : (int64_t)a.M * a.ldy;
+        const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)(span * 4));
+        const int64_t ybase = (int64_t)split * a.ysplit;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = n0 + wn * 64 + i * 16 + fq * 4;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int m = m0 + wm * 128 + j * 16 + fr;
+                const uint32_t off = (m < a.M && n < a.N) ? (uint32_t)((ybase + (int64_t)m * a.ldy + n) * 4) : kOOB;
+                Buf4<float>::store(acc[i][j], yr, off, 0);
+            }
+        }
+        return;
+    }
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -172,16 +200,21 @@ static __global__ __launch_bounds__(kOThreads, 1) void gemm256_beta_kernel(Gemm2
 static __global__ __launch_bounds__(kOThreads, 1) void gemm256_silu_kernel(Gemm256Args a, int nM, int nN, int per_xcd) {
     gemm256_body<kEpiSilu>(a, nM, nN, per_xcd);
 }
+static __global__ __launch_bounds__(kOThreads, 1) void gemm256_f32_kernel(Gemm256Args a, int nM, int nN, int per_xcd) {
+    gemm256_body<kEpiF32>(a, nM, nN, per_xcd);
+}
 
-// grid: ceil(M / 256) x ceil(N / 256) tiles in XCD-major order
+// grid: ceil(M / 256) x ceil(N / 256) tiles (x splits) in XCD-major order
 template <int EPI>
 static inline void gemm256_launch(const Gemm256Args &a, hipStream_t s) {
     const int nM = (int)ceil_div(a.M, kOBM), nN = (int)ceil_div(a.N, kOBN);
-    const int per_xcd = (int)ceil_div((int64_t)nM * nN, 8);
+    const int per_xcd = (int)ceil_div((int64_t)nM * nN * (a.splits > 0 ? a.splits : 1), 8);
     if constexpr (EPI == kEpiBeta)
         launch(gemm256_beta_kernel, dim3((unsigned)(per_xcd * 8)), dim3(kOThreads), 0, s, a, nM, nN, per_xcd);
-    else
+    else if constexpr (EPI == kEpiSilu)
         launch(gemm256_silu_kernel, dim3((unsigned)(per_xcd * 8)), dim3(kOThreads), 0, s, a, nM, nN, per_xcd);
+    else
+        launch(gemm256_f32_kernel, dim3((unsigned)(per_xcd * 8)), dim3(kOThreads), 0, s, a, nM, nN, per_xcd);
 }
 
 }  // namespace walsh

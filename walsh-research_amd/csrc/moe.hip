@@ -1359,7 +1359,7 @@ WALSH_EXPORT int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M
                (const float *)lpart, (int)(H / 16), o);
         return check_hip(hipGetLastError(), fn);
     }
-    Gemm256Args g;
+    Gemm256Args g{};
     g.x = x;
     g.ldx = ldx;
     g.M = (int)M;

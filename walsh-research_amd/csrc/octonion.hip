@@ -70,6 +70,11 @@ __global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs 
     const int wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;
+    // split-K: split blockIdx.z sums columns [k_lo, k_hi)
+    const int split = blockIdx.z;
+    const int k_lo = a.kspan > 0 ? (int)(split * a.kspan) : 0;
+    const int k_hi = a.kspan > 0 ? (int)(k_lo + a.kspan < a.K ? k_lo + a.kspan : a.K) : a.K;
+    const int kb_hi = a.kspan > 0 ? k_hi : a.Kp;
 
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
     const __amdgpu_buffer_rsrc_t br = make_rsrc(a.B, (uint32_t)((int64_t)a.N * a.Kp * esz));
@@ -81,17 +86,17 @@ __global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs 
     constexpr int kElemsPerChunk = 16 / esz;
 
     auto load_tile = [&](int k0, u32x4 (&ra)[2], u32x4 (&rb)[2]) {
-        const int ka0 = k0 + pa0 * kElemsPerChunk, ka1 = k0 + pa1 * kElemsPerChunk;
+        const int ka0 = k_lo + k0 + pa0 * kElemsPerChunk, ka1 = k_lo + k0 + pa1 * kElemsPerChunk;
         const int am0 = m0 + ra0, am1 = m0 + ra1;
         ra[0] = __builtin_amdgcn_raw_buffer_load_b128(
-            xr, (am0 < a.M && ka0 < a.K) ? (uint32_t)(((int64_t)am0 * a.ldx + ka0) * esz) : kOOB, 0, 0);
+            xr, (am0 < a.M && ka0 < k_hi) ? (uint32_t)(((int64_t)am0 * a.ldx + ka0) * esz) : kOOB, 0, 0);
         ra[1] = __builtin_amdgcn_raw_buffer_load_b128(
-            xr, (am1 < a.M && ka1 < a.K) ? (uint32_t)(((int64_t)am1 * a.ldx + ka1) * esz) : kOOB, 0, 0);
+            xr, (am1 < a.M && ka1 < k_hi) ? (uint32_t)(((int64_t)am1 * a.ldx + ka1) * esz) : kOOB, 0, 0);
         const int bn0 = n0 + ra0, bn1 = n0 + ra1;
         rb[0] = __builtin_amdgcn_raw_buffer_load_b128(
-            br, (bn0 < a.N && ka0 < a.Kp) ? (uint32_t)(((int64_t)bn0 * a.Kp + ka0) * esz) : kOOB, 0, 0);
+            br, (bn0 < a.N && ka0 < kb_hi) ? (uint32_t)(((int64_t)bn0 * a.Kp + ka0) * esz) : kOOB, 0, 0);
         rb[1] = __builtin_amdgcn_raw_buffer_load_b128(
-            br, (bn1 < a.N && ka1 < a.Kp) ? (uint32_t)(((int64_t)bn1 * a.Kp + ka1) * esz) : kOOB, 0, 0);
+            br, (bn1 < a.N && ka1 < kb_hi) ? (uint32_t)(((int64_t)bn1 * a.Kp + ka1) * esz) : kOOB, 0, 0);
     };
     auto store_tile = [&](int buf, const u32x4 (&ra)[2], const u32x4 (&rb)[2]) {
         *(u32x4 *)(&lds[buf][0][ra0 * kLdsStride + pa0 * 16]) = ra[0];
@@ -106,7 +111,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs 
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nk = (int)ceil_div(a.K, BK);
+    const int nk = (int)ceil_div(k_hi - k_lo, BK);
     u32x4 ra[2], rb[2];
     load_tile(0, ra, rb);
     store_tile(0, ra, rb);
@@ -144,7 +149,10 @@ __global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs 
     }
 
     // epilogue: lane holds D[m = 4*fq + r][n = fr] of each 16x16 tile
-    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * esz));
+    const int64_t yspan = a.kspan > 0 ? (int64_t)(gridDim.z - 1) * a.ysplit + (int64_t)a.M * a.ldy
+                                      : (int64_t)a.M * a.ldy;
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)(yspan * esz));
+    const int64_t ybase = (int64_t)split * a.ysplit;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int n = n0 + wn * 64 + j * 16 + fr;
@@ -154,7 +162,8 @@ __global__ __launch_bounds__(kGemmThreads, 2) void octonion_gemm_kernel(OctArgs 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm * 64 + i * 16 + 4 * fq + r;
-                const uint32_t off = (m < a.M && n < a.N) ? (uint32_t)(((int64_t)m * a.ldy + n) * esz) : kOOB;
+                const uint32_t off =
+                    (m < a.M && n < a.N) ? (uint32_t)((ybase + (int64_t)m * a.ldy + n) * esz) : kOOB;
                 Buf4<T>::store1(acc[i][j][r] * b, yr, off, 0);
             }
     }
@@ -286,6 +295,183 @@ WALSH_EXPORT int walsh_octonion_bwd_fold(const float *C, int64_t ldc, int64_t n_
     return check_hip(hipGetLastError(), "walsh_octonion_bwd_fold launch");
 }
 
+// ------------------------------------------------------------------ weight-gradient product
+// C = gy^T x ([8*out_o][8*in_o], K = tokens) on the forward's GEMM kernels:
+// both operands are first transposed into token-contiguous rows (one pass
+// each through a 64 x 64 LDS tile; rows padded with zeros to a multiple of
+// 8 tokens), then a split-K GEMM writes float32
+// partial sums, one slab per K split, which the fold adds in split order.
+template <typename T>
+__global__ __launch_bounds__(256) void octonion_transpose_kernel(const T *__restrict__ in, int64_t ldi, int R, int C,
+                                                                 T *__restrict__ out, int64_t ldo) {
+    // 4-element pieces both ways; odd row stride in 4-byte words keeps the
+    // column reads on different banks
+    __shared__ T tile[64][64 + (sizeof(T) == 2 ? 2 : 1)];
+    const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+    const int tq = threadIdx.x & 15, tr = threadIdx.x >> 4;  // 16 pieces of 4 x 16 rows
+#pragma unroll
+    for (int r = tr; r < 64; r += 16) {
+        const int rr = r0 + r, cc = c0 + 4 * tq;
+        T v[4];
+        if (rr < R && cc + 3 < C && (ldi & 3) == 0 && ((uintptr_t)in & (4 * sizeof(T) - 1)) == 0) {
+            if constexpr (sizeof(T) == 2) {
+                const uint2 u = *(const uint2 *)(in + (int64_t)rr * ldi + cc);
+                v[0] = (T)(u.x & 0xffff); v[1] = (T)(u.x >> 16); v[2] = (T)(u.y & 0xffff); v[3] = (T)(u.y >> 16);
+            } else {
+                const f32x4 u = *(const f32x4 *)(in + (int64_t)rr * ldi + cc);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = u[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = (rr < R && cc + j < C) ? in[(int64_t)rr * ldi + cc + j] : T(0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tile[r][4 * tq + j] = v[j];
+    }
+    __syncthreads();
+    // output row c (= input column), 4 consecutive input rows per thread;
+    // columns R .. ldo-1 (the row padding) are written as zeros
+#pragma unroll
+    for (int c = tr; c < 64; c += 16) {
+        const int cc = c0 + c, rr = r0 + 4 * tq;
+        if (cc >= C || rr >= ldo) continue;
+        T v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = tile[4 * tq + j][c];
+        T *dst = out + (int64_t)cc * ldo + rr;
+        if (rr + 3 < ldo) {
+            if constexpr (sizeof(T) == 2)
+                *(uint2 *)dst = uint2{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
+            else
+                *(f32x4 *)dst = f32x4{v[0], v[1], v[2], v[3]};
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (rr + j < ldo) dst[j] = v[j];
+        }
+    }
+}
+
+// C = the split-K partial sums added in split order (float32).
+__global__ __launch_bounds__(256) void octonion_sum_parts_kernel(const float *__restrict__ parts, int S,
+                                                                 int64_t stride, int64_t n, float *__restrict__ C) {
+    for (int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; e < n;
+         e += (int64_t)gridDim.x * blockDim.x * 4) {
+        f32x4 acc = *(const f32x4 *)(parts + e);
+        for (int sp = 1; sp < S; ++sp) acc += *(const f32x4 *)(parts + sp * stride + e);
+        *(f32x4 *)(C + e) = acc;
+    }
+}
+
+// split-K plan: about two work items per CU, splits of whole K stages and at
+// least 4 stages each
+static void octonion_dw_plan(int64_t M, int64_t in_o, int64_t out_o, bool bf16, int64_t *S, int64_t *kspan,
+                             int64_t *Mp) {
+    const int64_t N8o = 8 * out_o, N8i = 8 * in_o;
+    const int64_t tiles = bf16 ? ceil_div(N8o, kOBM) * ceil_div(N8i, kOBN) : ceil_div(N8o, kBM) * ceil_div(N8i, kBN);
+    const int64_t stage = bf16 ? kOBK : GemmCfg<float>::BK;
+    int64_t s = ceil_div(2 * (int64_t)device_info().cu_count, tiles);
+    const int64_t smax = ceil_div(M, 4 * stage);
+    if (s > smax) s = smax;
+    if (s < 1) s = 1;
+    *kspan = ceil_div(ceil_div(M, s), stage) * stage;
+    *S = ceil_div(M, *kspan);
+    *Mp = ceil_div(M, 8) * 8;
+}
+
+static int64_t octonion_dw_ws(int64_t M, int64_t in_o, int64_t out_o, int dtype, int64_t *S, int64_t *kspan,
+                              int64_t *Mp, int64_t *off_x, int64_t *off_c) {
+    const int64_t esz = dtype == WALSH_BF16 ? 2 : 4;
+    octonion_dw_plan(M, in_o, out_o, dtype == WALSH_BF16, S, kspan, Mp);
+    *off_x = ceil_div(8 * out_o * *Mp * esz, 256) * 256;
+    *off_c = *off_x + ceil_div(8 * in_o * *Mp * esz, 256) * 256;
+    // partial sums [S][8 out_o][8 in_o], then (S > 1) their total
+    return *off_c + (*S + (*S > 1 ? 1 : 0)) * 64 * out_o * in_o * 4;
+}
+
+WALSH_EXPORT int64_t walsh_octonion_bwd_params_workspace_bytes(int64_t M, int64_t in_o, int64_t out_o, int dtype) {
+    if (M <= 0 || in_o <= 0 || out_o <= 0 || (dtype != WALSH_F32 && dtype != WALSH_BF16)) return 0;
+    int64_t S, kspan, Mp, ox, oc;
+    return octonion_dw_ws(M, in_o, out_o, dtype, &S, &kspan, &Mp, &ox, &oc);
+}
+
+WALSH_EXPORT int walsh_octonion_bwd_params(const void *gy, int64_t ldg, const void *x, int64_t ldx, int64_t M,
+                                           int64_t in_o, int64_t out_o, const uint8_t *packed, const float *beta,
+                                           const float *latent, float *dweight, float *dbeta, int dtype, void *work,
+                                           int64_t work_bytes, void *stream) {
+    const char *fn = "walsh_octonion_bwd_params";
+    if (!gy || !x || !packed || !beta || !work) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (M <= 0 || in_o <= 0 || out_o <= 0 || in_o > 65536 || out_o > 65536 || ldg < 8 * out_o || ldx < 8 * in_o)
+        return set_error(WALSH_EINVAL, "%s: bad shape M=%lld in_o=%lld out_o=%lld", fn, (long long)M,
+                         (long long)in_o, (long long)out_o);
+    if (dtype != WALSH_F32 && dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: dtype", fn);
+    if (!dweight && !dbeta) return WALSH_OK;
+    const bool bf16 = dtype == WALSH_BF16;
+    const int64_t esz = bf16 ? 2 : 4;
+    int64_t S, kspan, Mp, ox, oc;
+    const int64_t need = octonion_dw_ws(M, in_o, out_o, dtype, &S, &kspan, &Mp, &ox, &oc);
+    if (work_bytes < need || (uintptr_t)work % 256)
+        return set_error(WALSH_EINVAL, "%s: workspace of %lld bytes (256-aligned), needs %lld", fn,
+                         (long long)work_bytes, (long long)need);
+    if (8 * out_o * Mp * esz > (int64_t)kMaxBufferBytes || 8 * in_o * Mp * esz > (int64_t)kMaxBufferBytes ||
+        S * 64 * out_o * in_o * 4 > (int64_t)kMaxBufferBytes || M * ldg * esz > (int64_t)kMaxBufferBytes)
+        return set_error(WALSH_ENOTSUP, "%s: operands above 2^31 bytes", fn);
+    hipStream_t s = (hipStream_t)stream;
+    char *w = (char *)work;
+    void *gyT = w, *xT = w + ox;
+    float *Cp = (float *)(w + oc);
+    const dim3 tb(256);
+    const dim3 tg_g((unsigned)ceil_div(8 * out_o, 64), (unsigned)ceil_div(M, 64));
+    const dim3 tg_x((unsigned)ceil_div(8 * in_o, 64), (unsigned)ceil_div(M, 64));
+    if (bf16) {
+        launch(octonion_transpose_kernel<uint16_t>, tg_g, tb, 0, s, (const uint16_t *)gy, ldg, (int)M,
+               (int)(8 * out_o), (uint16_t *)gyT, Mp);
+        launch(octonion_transpose_kernel<uint16_t>, tg_x, tb, 0, s, (const uint16_t *)x, ldx, (int)M,
+               (int)(8 * in_o), (uint16_t *)xT, Mp);
+    } else {
+        launch(octonion_transpose_kernel<float>, tg_g, tb, 0, s, (const float *)gy, ldg, (int)M, (int)(8 * out_o),
+               (float *)gyT, Mp);
+        launch(octonion_transpose_kernel<float>, tg_x, tb, 0, s, (const float *)x, ldx, (int)M, (int)(8 * in_o),
+               (float *)xT, Mp);
+    }
+    OctArgs a{};
+    a.x = gyT;
+    a.ldx = Mp;
+    a.M = (int)(8 * out_o);
+    a.N = (int)(8 * in_o);
+    a.K = (int)M;
+    a.Kp = (int)Mp;
+    a.B = xT;
+    a.beta = nullptr;
+    a.out_o = (int)(8 * in_o);
+    a.y = Cp;
+    a.ldy = 8 * in_o;
+    a.splits = (int)S;
+    a.kspan = kspan;
+    a.ysplit = 64 * out_o * in_o;
+    if (bf16) {
+        gemm256_launch<kEpiF32>(a, s);
+    } else {
+        const dim3 G((unsigned)ceil_div(8 * out_o, kBM), (unsigned)ceil_div(8 * in_o, kBN), (unsigned)S);
+        launch(octonion_gemm_kernel<float>, G, dim3(kGemmThreads), 0, s, a);
+    }
+    int rc = check_hip(hipGetLastError(), fn);
+    if (rc) return rc;
+    const int64_t nC = 64 * out_o * in_o;
+    float *Ct = Cp;
+    if (S > 1) {
+        // one pass adds the partial sums, so the fold reads a single C
+        Ct = Cp + S * nC;
+        int64_t grid = ceil_div(nC / 4, 256);
+        if (grid > 4096) grid = 4096;
+        launch(octonion_sum_parts_kernel, dim3((unsigned)grid), dim3(256), 0, s, (const float *)Cp, (int)S, nC, nC, Ct);
+        rc = check_hip(hipGetLastError(), fn);
+        if (rc) return rc;
+    }
+    return walsh_octonion_bwd_fold(Ct, 8 * in_o, 1, 0, packed, in_o, out_o, beta, latent, dweight, dbeta, stream);
+}
+
 WALSH_EXPORT int64_t walsh_octonion_weight_elems(int64_t in_o, int64_t out_o) {
     if (in_o <= 0 || out_o <= 0) return 0;
     return 8 * out_o * ceil_div(8 * in_o, 32) * 32;
@@ -332,7 +518,7 @@ WALSH_EXPORT int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M
     rows_max = balanced_rows(M, rows_max, kOBM);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
-        OctArgs a;
+        OctArgs a{};
         a.x = (const char *)x + r0 * ldx * esz;
         a.ldx = ldx;
         a.M = (int)rows;

@@ -60,6 +60,8 @@ SIGNATURES = {
     "walsh_octonion_linear_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I, _P]),
     "walsh_octonion_prepare_t": (_I, [_P, _I64, _I64, _P, _P, _I, _P]),
     "walsh_octonion_bwd_fold": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+    "walsh_octonion_bwd_params_workspace_bytes": (_I64, [_I64, _I64, _I64, _I]),
+    "walsh_octonion_bwd_params": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I, _P, _I64, _P]),
     "walsh_decode_attention_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "walsh_decode_attention": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
                                     _P, _I64, _I64, _I, _P, _I64, _P]),

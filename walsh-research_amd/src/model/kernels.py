@@ -540,8 +540,9 @@ def octonion_linear_bwd(x: torch.Tensor, gy: torch.Tensor, in_o: int, out_o: int
 
     Returns (gx, dweight, dbeta); entries not requested in ``need`` are None.
     gx = (gy .* beta) B on the HIP GEMM (transposed block matrix); the
-    parameter gradients fold C = gy^T x ([8*out_o, 8*in_o], one library GEMM
-    with float32 output, K = tokens) in walsh_octonion_bwd_fold."""
+    parameter gradients come from C = gy^T x ([8*out_o, 8*in_o], K = tokens:
+    transposed operands, split-K GEMM with float32 partial sums, then the
+    fold) in walsh_octonion_bwd_params."""
     _hip.require_device(x, "input")
     dt = x.dtype
     assert gy.dtype == dt, f"gradient dtype {gy.dtype} != input dtype {dt}"
@@ -553,20 +554,26 @@ def octonion_linear_bwd(x: torch.Tensor, gy: torch.Tensor, in_o: int, out_o: int
         Bt = octonion_prepare_t(packed, in_o, out_o, beta, dt)
         gx = octonion_linear(gr, out_o, in_o, Bt, None).view(x.shape)
     if want_w or want_b:
-        if gr.shape[0] == 0:
-            C = torch.zeros(8 * out_o, 8 * in_o, device=x.device, dtype=torch.float32)
-        elif dt == torch.float32:
-            C = torch.mm(gr.t(), xr)
-        else:
-            C = torch.mm(gr.t(), xr, out_dtype=torch.float32)
-        C = C.contiguous()
         dw = torch.empty(8, out_o, in_o, device=x.device, dtype=torch.float32) if want_w else None
         db = torch.empty(out_o, device=x.device, dtype=torch.float32) if want_b else None
         lat = latent.detach().float().contiguous() if (latent is not None and want_w) else None
         beta = beta.detach().float().contiguous()
         ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
-        _hip.call("walsh_octonion_bwd_fold", C.data_ptr(), 8 * in_o, 1, 0, packed.contiguous().data_ptr(), in_o,
-                  out_o, beta.data_ptr(), ptr(lat), ptr(dw), ptr(db), _hip.stream(x.device))
+        M = gr.shape[0]
+        if M == 0:
+            C = torch.zeros(8 * out_o, 8 * in_o, device=x.device, dtype=torch.float32)
+            _hip.call("walsh_octonion_bwd_fold", C.data_ptr(), 8 * in_o, 1, 0, packed.contiguous().data_ptr(), in_o,
+                      out_o, beta.data_ptr(), ptr(lat), ptr(dw), ptr(db), _hip.stream(x.device))
+        else:
+            gr, xr = gr.contiguous(), xr.contiguous()
+            nws = _hip.lib().walsh_octonion_bwd_params_workspace_bytes(M, in_o, out_o, _hip.dtype_code(dt))
+            ws = torch.empty(nws, device=x.device, dtype=torch.uint8)
+            esz = x.element_size()
+            _hip.call("walsh_octonion_bwd_params", gr.data_ptr(), gr.stride(0), xr.data_ptr(), xr.stride(0), M, in_o,
+                      out_o, packed.contiguous().data_ptr(), beta.data_ptr(), ptr(lat), ptr(dw), ptr(db),
+                      _hip.dtype_code(dt), ws.data_ptr(), nws, _hip.stream(x.device),
+                      kernel="octonion_bwd_params<%s>" % ("bf16" if dt == torch.bfloat16 else "f32"),
+                      nbytes=2 * M * 8 * (in_o + out_o) * esz, flops=2 * M * 64 * in_o * out_o)
     return gx, dw, db
 
 
