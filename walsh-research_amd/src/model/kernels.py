@@ -997,6 +997,14 @@ def _dense(t: torch.Tensor, dtype=None) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
+def _check_extents(fn: str, M: int, operands) -> None:
+    """Host-side bounds check for the raw-pointer stream-mixing kernels: each
+    (tensor, elements per token) must hold exactly M tokens' worth."""
+    for i, (t, per) in enumerate(operands):
+        if t.numel() != M * per:
+            raise ValueError(f"{fn}: operand {i} has {t.numel()} elements, the kernel addresses {M} x {per}")
+
+
 def mhc_aggregate(x: torch.Tensor, h_pre: torch.Tensor) -> torch.Tensor:
     """layer_in = H_pre @ x (mhc.py:366) for x [..., n, C], h_pre [..., 1, n] or
     [..., n]; float32 sums, result in x.dtype [..., C]."""
@@ -1019,6 +1027,9 @@ def mhc_aggregate_bwd(x: torch.Tensor, h_pre: torch.Tensor, d_li: torch.Tensor):
     M = xv.numel() // (n * C)
     hp = _dense(h_pre.detach(), torch.float32)
     g = _dense(d_li, x.dtype)
+    # the kernel walks dense [M][n][C] / [M][C] / [M][n] rows with raw
+    # pointers: every operand must hold exactly that many elements
+    _check_extents("mhc_aggregate_bwd", M, ((xv, n * C), (hp, n), (g, C)))
     dx = torch.empty_like(xv)
     dh = torch.empty(hp.shape, device=x.device, dtype=torch.float32)
     _hip.call("walsh_mhc_aggregate_bwd", xv.data_ptr(), hp.data_ptr(), g.data_ptr(), dx.data_ptr(), dh.data_ptr(),
@@ -1037,6 +1048,7 @@ def mhc_post_bwd(x: torch.Tensor, out: torch.Tensor, h_res: torch.Tensor, h_post
     hr = _dense(h_res.detach(), torch.float32)
     hq = _dense(h_post.detach(), torch.float32)
     g = _dense(d_new, x.dtype)
+    _check_extents("mhc_post_bwd", M, ((xv, n * C), (o, C), (hr, n * n), (hq, n), (g, n * C)))
     dx = torch.empty_like(xv)
     dout = torch.empty_like(o)
     dhr = torch.empty(hr.shape, device=x.device, dtype=torch.float32)
