@@ -537,6 +537,24 @@ int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, 
                               float *mask, float *weights_dense, int *topk_idx, float *topk_w, int *count,
                               float *probsum, int64_t n_part, void *y, int64_t ldy, int ydtype, void *stream);
 
+/* walsh_moe_experts_bwd: backward of FastMoEExperts.forward (src/model/moe.py
+ *   :337-380, autograd of its einsums, SiLU and routing product, with the
+ *   MoE STE of :289-294) over the routed pairs of a walsh_moe_scatter
+ *   grouping (list, offset), float32: x, dout [M, >= 32E] (row strides ldx,
+ *   ldd), the packed codes (gate / up [E][H][8], down [E][32][H/4]), gammas
+ *   [3] and topk_w [M*k].  Writes dx[t, 32e:32e+32] of every routed pair
+ *   (other blocks untouched: zero them first), d_pair_w [M*k] (gradient of
+ *   each pair's routing weight) and clamp(dW, -2, 2) of the three weight
+ *   tensors (gate / up [E][H][32], down [E][32][H]; NULL skips).  Hidden H
+ *   <= 128, multiple of 16.  work: walsh_moe_experts_bwd_workspace_bytes(E,
+ *   H) bytes. */
+int64_t walsh_moe_experts_bwd_workspace_bytes(int64_t E, int64_t H);
+int walsh_moe_experts_bwd(const float *x, int64_t ldx, const float *dout, int64_t ldd, int64_t M, int64_t E,
+                          int64_t k, int64_t H, const uint8_t *gate_packed, const uint8_t *up_packed,
+                          const uint8_t *down_packed, const float *gammas, const int *list, const int *offset,
+                          const float *topk_w, float *dx, int64_t ldgx, float *d_pair_w, float *dgate, float *dup,
+                          float *ddown, void *work, int64_t work_bytes, void *stream);
+
 /* walsh_moe_topk_fwd: the softmax / top-k / renormalisation part of
  *   HadamardRouter.forward (src/model/moe.py:432-445) from given float32
  *   logits [M, E] (contiguous). */

@@ -305,11 +305,13 @@ def test_ternary_ste_bwd_modes(K):
     assert torch.equal(m0[:6], torch.tensor([0.0, -2.0, -0.5, 0.0, 0.0, 0.0])) and torch.isnan(m0[6])
 
 
-@pytest.mark.parametrize("C,k", [(256, 4), (512, 6)])
-def test_moe_backward_matches_oracle(C, k):
-    """HadamardMoE training backward (routing, balance loss, experts with the
-    MoE STE) against float64 autograd of the oracle's MoE (moe.py:418-447,
-    :337-380, :544-560) on the same parameters."""
+@pytest.mark.parametrize("C,k,T", [(256, 4, 24), (512, 6, 24), (512, 6, 512), (1024, 6, 24)])
+def test_moe_backward_matches_oracle(C, k, T):
+    """HadamardMoE training backward (routing, balance loss, the experts'
+    forward and backward on the HIP kernels over the routed pairs, MoE STE)
+    against float64 autograd of the oracle's MoE (moe.py:418-447, :337-380,
+    :544-560) on the same parameters; T 512 gives each expert workgroup many
+    pairs, C 1024 (32 experts) leaves some workgroups without pairs."""
     from oracle.model import Oracle
     from src.model import WalshConfig
     from src.model.moe import HadamardMoE
@@ -320,8 +322,8 @@ def test_moe_backward_matches_oracle(C, k):
         for lin in (m.router.gate[0], m.router.gate[2]):
             lin.weight.normal_(0, 0.2)
     g = torch.Generator().manual_seed(5)
-    x = torch.randn(2, 24, C, generator=g).cuda().requires_grad_(True)
-    gy = torch.randn(2, 24, C, generator=g).cuda()
+    x = torch.randn(2, T, C, generator=g).cuda().requires_grad_(True)
+    gy = torch.randn(2, T, C, generator=g).cuda()
     y = m(x)
     loss = (y * gy).sum() + 0.3 * m.get_aux_loss()
     loss.backward()

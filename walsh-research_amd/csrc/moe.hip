@@ -1253,6 +1253,192 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
     part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
 }
 
+// ------------------------------------------------------------------ experts backward
+// Backward of FastMoEExperts.forward (moe.py:337-380: autograd of its three
+// einsums, SiLU and the routing product, with the MoE STE of moe.py:289-294)
+// over the routed (token, expert) pairs only -- a pair with routing weight
+// zero adds nothing to dx or to the weight gradients -- in float32:
+//   do = dout w;  g = Wg x, u = Wu x, s = silu(g), h = s u, o = Wd h
+//   dw_pair = <dout, o>;  dh = Wd^T do;  dg = dh u silu'(g);  du = dh s
+//   dx = Wg^T dg + Wu^T du;  dWg += dg x^T, dWu += du x^T, dWd += do h^T
+// with W = code * gamma.  A workgroup takes a share of one expert's pairs
+// (S workgroups per expert), two pairs at a time with 128 threads each
+// (thread j owns hidden unit j), the expert's three matrices staged in LDS
+// as float32 and the next pairs' rows prefetched during the current ones;
+// each workgroup writes its weight-gradient sums, which
+// moe_experts_bwd_reduce_kernel adds in workgroup order before the STE clamp.
+constexpr int kEbSlots = 2;
+constexpr int kEbH = 128;  // hidden units per expert <= 128
+constexpr int kEbThreads = kEbSlots * kEbH;
+struct ExpBwdArgs {
+    const float *x;
+    int64_t ldx;
+    const float *dout;
+    int64_t ldd;
+    float *dx;
+    int64_t ldgx;
+    const int *list, *offset;  // pair ids t*k + j grouped by expert (walsh_moe_scatter)
+    const float *topk_w;       // [M*k] routing weight of each pair
+    int M, E, k, H, S;
+    const uint8_t *pg, *pu, *pd;  // packed codes: gate / up [E][H][8], down [E][32][H/4]
+    const float *gammas;          // [3]
+    float *dpair;                 // [M*k] gradient of each pair's routing weight
+    float *part;                  // [S][E][3][H*32] per-workgroup weight-gradient sums
+};
+
+__device__ __forceinline__ float packed_code(const uint8_t *row, int i) {
+    const uint32_t b = row[i >> 2];
+    return (float)((int)((b >> (6 - 2 * (i & 3))) & 3u) - 1);
+}
+
+__global__ __launch_bounds__(kEbThreads) void moe_experts_bwd_kernel(ExpBwdArgs a) {
+    __shared__ float wg_l[kEbH][33], wu_l[kEbH][33], wd_l[32][kEbH + 1];
+    __shared__ float xs[kEbSlots][32], os[kEbSlots][32], dos[kEbSlots][32];
+    __shared__ float gs[kEbSlots][kEbH], us[kEbSlots][kEbH], hs[kEbSlots][kEbH];
+    __shared__ float red[kEbSlots][2][32][2];
+    const int e = (int)blockIdx.x / a.S, sp = (int)blockIdx.x % a.S;
+    const int tid = threadIdx.x, slot = tid / kEbH, j = tid % kEbH;
+    const int H = a.H, k = a.k;
+    {
+        const float g0 = a.gammas[0], g1 = a.gammas[1], g2 = a.gammas[2];
+        for (int i = tid; i < H * 32; i += kEbThreads) {
+            const int h = i >> 5, d = i & 31;
+            wg_l[h][d] = packed_code(a.pg + ((int64_t)e * H + h) * 8, d) * g0;
+            wu_l[h][d] = packed_code(a.pu + ((int64_t)e * H + h) * 8, d) * g1;
+            wd_l[d][h] = packed_code(a.pd + ((int64_t)e * 32 + d) * (H / 4), h) * g2;
+        }
+    }
+    const int p0 = a.offset[e], p1 = a.offset[e + 1];
+    const int per = (p1 - p0 + a.S - 1) / a.S;
+    const int b0 = p0 + sp * per, b1 = min(p1, b0 + per);
+    const int iters = b1 > b0 ? (b1 - b0 + kEbSlots - 1) / kEbSlots : 0;
+    float agw[32], auw[32], adw[32];
+#pragma unroll
+    for (int d = 0; d < 32; ++d) agw[d] = auw[d] = adw[d] = 0.f;
+    // the slot's next pair: id, weight and (threads j < 32) element j of its
+    // x and dout rows, loaded one iteration ahead
+    int npid = -1;
+    float nw = 0.f, nx = 0.f, nd = 0.f;
+    auto fetch = [&](int it) {
+        const int p = b0 + it * kEbSlots + slot;
+        npid = (it < iters && p < b1) ? a.list[p] : -1;
+        if (npid >= 0) {
+            const int64_t t = npid / k;
+            nw = a.topk_w[npid];
+            if (j < 32) {
+                nx = a.x[t * a.ldx + 32 * e + j];
+                nd = a.dout[t * a.ldd + 32 * e + j];
+            }
+        }
+    };
+    fetch(0);
+    for (int it = 0; it < iters; ++it) {
+        const int pid = npid;
+        const float w = nw;
+        if (j < 32) {
+            xs[slot][j] = nx;
+            os[slot][j] = nd;
+            dos[slot][j] = nd * w;
+        }
+        fetch(it + 1);
+        __syncthreads();  // rows in LDS (and, on the first pass, the matrices)
+        if (pid >= 0 && j < H) {
+            float g = 0.f, u = 0.f, dh = 0.f;
+#pragma unroll
+            for (int d = 0; d < 32; ++d) {
+                const float xv = xs[slot][d];
+                g += wg_l[j][d] * xv;
+                u += wu_l[j][d] * xv;
+                dh += wd_l[d][j] * dos[slot][d];
+            }
+            const float sg = 1.0f / (1.0f + expf(-g));
+            const float sv = g * sg, dsil = sg * (1.0f + g * (1.0f - sg));
+            const float hv = sv * u, dg = dh * u * dsil, du = dh * sv;
+#pragma unroll
+            for (int d = 0; d < 32; ++d) {
+                const float xv = xs[slot][d];
+                agw[d] += dg * xv;
+                auw[d] += du * xv;
+                adw[d] += dos[slot][d] * hv;
+            }
+            gs[slot][j] = dg;
+            us[slot][j] = du;
+            hs[slot][j] = hv;
+        }
+        __syncthreads();
+        {
+            // thread (d = j % 32, q = j / 32) sums hidden units [32q, 32q + 32)
+            const int d = j & 31, q = j >> 5;
+            float vx = 0.f, vo = 0.f;
+            if (pid >= 0) {
+                const int h1 = min(H, 32 * q + 32);
+                for (int h = 32 * q; h < h1; ++h) {
+                    vx += gs[slot][h] * wg_l[h][d] + us[slot][h] * wu_l[h][d];
+                    vo += hs[slot][h] * wd_l[d][h];
+                }
+            }
+            vx += __shfl_xor(vx, 32, 64);  // q and q ^ 1 share a wave
+            vo += __shfl_xor(vo, 32, 64);
+            if ((j & 63) < 32) {
+                red[slot][j >> 6][d][0] = vx;
+                red[slot][j >> 6][d][1] = vo;
+            }
+        }
+        __syncthreads();
+        if (pid >= 0 && j < 32) {
+            const float vx = red[slot][0][j][0] + red[slot][1][j][0];
+            const float vo = red[slot][0][j][1] + red[slot][1][j][1];
+            a.dx[(int64_t)(pid / k) * a.ldgx + 32 * e + j] = vx;
+            float pw = os[slot][j] * vo;
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1) pw += __shfl_xor(pw, off, 64);
+            if (j == 0) a.dpair[pid] = pw;
+        }
+    }
+    // the two slots' sums meet in LDS (the matrices are no longer needed)
+    __syncthreads();
+    if (slot == 1 && j < H) {
+#pragma unroll
+        for (int d = 0; d < 32; ++d) {
+            wg_l[j][d] = agw[d];
+            wu_l[j][d] = auw[d];
+            wd_l[d][j] = adw[d];
+        }
+    }
+    __syncthreads();
+    if (slot == 0 && j < H) {
+        float *dst = a.part + ((int64_t)sp * a.E + e) * 3 * H * 32;
+#pragma unroll
+        for (int d = 0; d < 32; ++d) {
+            dst[j * 32 + d] = agw[d] + wg_l[j][d];
+            dst[H * 32 + j * 32 + d] = auw[d] + wu_l[j][d];
+            dst[2 * H * 32 + d * H + j] = adw[d] + wd_l[d][j];
+        }
+    }
+}
+
+// Weight gradients: the per-workgroup sums added in workgroup order, then
+// clamp(., -2, 2) (the MoE STE); gate / up [E][H][32], down [E][32][H].
+__global__ __launch_bounds__(256) void moe_experts_bwd_reduce_kernel(const float *__restrict__ part, int S, int E,
+                                                                     int H, float *__restrict__ dg,
+                                                                     float *__restrict__ du, float *__restrict__ dd) {
+    const int64_t per = 3LL * H * 32, n = (int64_t)E * per;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int e = (int)(i / per), r = (int)(i % per);
+        float v = 0.f;
+        for (int sp = 0; sp < S; ++sp) v += part[((int64_t)sp * E + e) * per + r];
+        v = fminf(fmaxf(v, -2.f), 2.f);
+        const int kind = r / (H * 32), rr = r % (H * 32);
+        float *dst = kind == 0 ? dg : (kind == 1 ? du : dd);
+        if (dst) dst[(int64_t)e * H * 32 + rr] = v;
+    }
+}
+
+static int experts_bwd_splits(int64_t E) {
+    int64_t S = ceil_div(2 * (int64_t)device_info().cu_count, E);
+    return (int)(S < 1 ? 1 : (S > 16 ? 16 : S));
+}
+
 static int route_out_check(const char *fn, int64_t M, int64_t E, int64_t k, const int *topk_idx, const float *topk_w,
                            const int *count, const float *probsum, int64_t n_part) {
     if (!count || !probsum || (M > 0 && (!topk_idx || !topk_w)))
@@ -1377,6 +1563,61 @@ WALSH_EXPORT int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M
     const int64_t tiles = ceil_div(M, 64), grid = tiles < n_part ? tiles : n_part;
     launch(router_w2_topk_kernel<4>, dim3((unsigned)grid), dim3(64 * kR2Waves), (uint32_t)router_w2_lds_bytes((int)H, 4),
            s, (const uint16_t *)h, (int64_t)H, (int)H, (const uint16_t *)w2, o);
+    return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int64_t walsh_moe_experts_bwd_workspace_bytes(int64_t E, int64_t H) {
+    if (E < 1 || E > kMaxE || H < 16 || H > kEbH) return 0;
+    return (int64_t)experts_bwd_splits(E) * E * 3 * H * 32 * 4;
+}
+
+WALSH_EXPORT int walsh_moe_experts_bwd(const float *x, int64_t ldx, const float *dout, int64_t ldd, int64_t M,
+                                       int64_t E, int64_t k, int64_t H, const uint8_t *gate_packed,
+                                       const uint8_t *up_packed, const uint8_t *down_packed, const float *gammas,
+                                       const int *list, const int *offset, const float *topk_w, float *dx,
+                                       int64_t ldgx, float *d_pair_w, float *dgate, float *dup, float *ddown,
+                                       void *work, int64_t work_bytes, void *stream) {
+    const char *fn = "walsh_moe_experts_bwd";
+    if (!gate_packed || !up_packed || !down_packed || !gammas || !offset || !work ||
+        (M > 0 && (!x || !dout || !list || !topk_w || !dx || !d_pair_w)))
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (M < 0 || E < 1 || E > kMaxE || k < 1 || k > E || H < 16 || H > kEbH || H % 16 || ldx < 32 * E ||
+        ldd < 32 * E || ldgx < 32 * E)
+        return set_error(WALSH_ENOTSUP, "%s: needs E <= %d, hidden H in [16, %d] (multiple of 16), rows >= 32 E", fn,
+                         kMaxE, kEbH);
+    if (work_bytes < walsh_moe_experts_bwd_workspace_bytes(E, H))
+        return set_error(WALSH_EINVAL, "%s: workspace of %lld bytes, needs %lld", fn, (long long)work_bytes,
+                         (long long)walsh_moe_experts_bwd_workspace_bytes(E, H));
+    hipStream_t s = (hipStream_t)stream;
+    const int S = experts_bwd_splits(E);
+    ExpBwdArgs a;
+    a.x = x;
+    a.ldx = ldx;
+    a.dout = dout;
+    a.ldd = ldd;
+    a.dx = dx;
+    a.ldgx = ldgx;
+    a.list = list;
+    a.offset = offset;
+    a.topk_w = topk_w;
+    a.M = (int)M;
+    a.E = (int)E;
+    a.k = (int)k;
+    a.H = (int)H;
+    a.S = S;
+    a.pg = gate_packed;
+    a.pu = up_packed;
+    a.pd = down_packed;
+    a.gammas = gammas;
+    a.dpair = d_pair_w;
+    a.part = (float *)work;
+    launch(moe_experts_bwd_kernel, dim3((unsigned)(E * S)), dim3(kEbThreads), 0, s, a);
+    int rc = check_hip(hipGetLastError(), fn);
+    if (rc) return rc;
+    int64_t grid = ceil_div(E * 3 * H * 32, 256);
+    if (grid > 4096) grid = 4096;
+    launch(moe_experts_bwd_reduce_kernel, dim3((unsigned)grid), dim3(256), 0, s, (const float *)work, S, (int)E,
+           (int)H, dgate, dup, ddown);
     return check_hip(hipGetLastError(), fn);
 }
 

@@ -97,6 +97,9 @@ SIGNATURES = {
     "walsh_moe_router_wide_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "walsh_moe_router_wide_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P,
                                        _P, _P, _I64, _P, _I64, _I, _P]),
+    "walsh_moe_experts_bwd_workspace_bytes": (_I64, [_I64, _I64]),
+    "walsh_moe_experts_bwd": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                   _P, _P, _P, _P, _P, _I64, _P]),
     "walsh_moe_topk_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "walsh_moe_scatter": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P]),
     "walsh_moe_experts_fwd": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,

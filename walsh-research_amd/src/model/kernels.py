@@ -1266,6 +1266,35 @@ def moe_experts(x: torch.Tensor, y: torch.Tensor, r: MoERoute, lists, frags, gam
               flops=2 * pairs * 3 * 32 * H)
 
 
+def moe_experts_bwd(x: torch.Tensor, dout: torch.Tensor, r: MoERoute, lists, packed, gammas: torch.Tensor,
+                    H: int, need_w: bool = True):
+    """Backward of the routed experts (moe.py:337-380 with the MoE STE) over
+    the pairs of ``r``: returns (dx [M, 32E] float32 with zeros outside the
+    routed blocks, d_pair_w [M, k], (dgate, dup, ddown) or None).  x, dout
+    [M, 32E] float32; packed = (gate, up, down) 2-bit codes; gammas [3]."""
+    _hip.require_device(x, "input")
+    E, k = r.E, r.k
+    xv, M, ldx = _rows_view(x, 32 * E)
+    dv, Md, ldd = _rows_view(dout, 32 * E)
+    assert M == r.M == Md and x.dtype == torch.float32 and dout.dtype == torch.float32, "expert operands"
+    lst, offset, _ = lists
+    pg, pu, pd = (t.contiguous() for t in packed)
+    dev = x.device
+    dx = torch.zeros(M, 32 * E, device=dev, dtype=torch.float32)
+    dpair = torch.empty(max(M * k, 1), device=dev, dtype=torch.float32)
+    grads = tuple(torch.empty(sh, device=dev, dtype=torch.float32) for sh in ((E, H, 32), (E, H, 32), (E, 32, H))) \
+        if need_w else (None, None, None)
+    nws = _hip.lib().walsh_moe_experts_bwd_workspace_bytes(E, H)
+    ws = torch.empty(max(nws, 4), device=dev, dtype=torch.uint8)
+    g = gammas.detach().float().contiguous()
+    _hip.call("walsh_moe_experts_bwd", xv.data_ptr(), ldx, dv.data_ptr(), ldd, M, E, k, H, pg.data_ptr(),
+              pu.data_ptr(), pd.data_ptr(), g.data_ptr(), lst.data_ptr(), offset.data_ptr(), r.topk_w.data_ptr(),
+              dx.data_ptr(), 32 * E, dpair.data_ptr(), *[_hip.ptr(t) for t in grads], ws.data_ptr(), ws.numel(),
+              _hip.stream(dev), kernel="moe_experts_bwd_kernel", nbytes=M * k * 32 * 16 + 3 * E * H * 32 * 4,
+              flops=2 * M * k * 32 * H * 9)
+    return dx, dpair[:M * k].view(M, k), (grads if need_w else None)
+
+
 def moe_ffn_supported(x2d: torch.Tensor, E: int, H: int, k: int) -> bool:
     """Whether walsh_moe_ffn_fwd (single-launch MoE) handles this call."""
     return (x2d.dtype == torch.bfloat16 and x2d.shape[-1] == 512 and E == 16 and H in (64, 128) and 1 <= k <= 8)

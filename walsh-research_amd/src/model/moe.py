@@ -128,13 +128,22 @@ class FastMoEExperts(nn.Module):
         lists = kernels.moe_scatter(route)
         kernels.moe_experts(x2d, y2d, route, lists, frags, gammas, self.hidden)
 
-    def forward_autograd(self, x: torch.Tensor, expert_weights: torch.Tensor) -> torch.Tensor:
-        """The experts as differentiable products for training (moe.py:337-380):
-        quantize_ternary (HIP quantiser, straight-through gradient clipped to
-        [-2, 2] on the GPU), then per-expert matrix products in float32 (see
-        tracked_dtype), times the routing weights; float32 result."""
+    def forward_autograd(self, x: torch.Tensor, expert_weights: torch.Tensor, mask: torch.Tensor = None,
+                         k: int = None) -> torch.Tensor:
+        """The experts as differentiable products for training (moe.py:337-380),
+        float32 result.  Given the routing selection (``mask`` [B, T, E] with
+        ``k`` ones per token) on the GPU with hidden size <= 128: forward and
+        backward on the HIP kernels over the routed pairs only (the others have
+        weight zero and add nothing; their routing-weight gradient is returned
+        as zero, which the routing's mask multiplies away).  Otherwise
+        quantize_ternary (straight-through gradient clipped to [-2, 2]) and
+        per-expert matrix products in float32 (see tracked_dtype), times the
+        routing weights."""
         self._check()
         B, T, E, D = x.shape
+        if mask is not None and k is not None and x.is_cuda and self.hidden <= 128:
+            return _RoutedExperts.apply(x, expert_weights, mask, k, self.gate_weights, self.up_weights,
+                                        self.down_weights, self)
         gw, uw, dw = (quantize_ternary(w) for w in (self.gate_weights, self.up_weights, self.down_weights))
         dt = tracked_dtype(act_dtype(x))
         dev = x.device.type
@@ -168,6 +177,53 @@ class FastMoEExperts(nn.Module):
             r.probsum_part.zero_()
             self.routed(x2d, r, y)
         return y.view(B, T, E, D)
+
+
+class _RoutedExperts(torch.autograd.Function):
+    """FastMoEExperts on the routed pairs, forward and backward on HIP
+    (walsh_moe_experts_fwd / walsh_moe_experts_bwd), float32 arithmetic.
+    Inputs: x [B, T, E, 32], expert_weights [B, T, E], mask [B, T, E] (k
+    ones per token), k, the three latent weight tensors and the module."""
+
+    @staticmethod
+    def forward(ctx, x, expert_weights, mask, k, gate_w, up_w, down_w, mod):
+        B, T, E, D = x.shape
+        M = B * T
+        dev = x.device
+        idx = mask.reshape(M, E).topk(k, dim=-1).indices
+        w = expert_weights.detach().reshape(M, E).float().gather(-1, idx).contiguous()
+        r = kernels.MoERoute(M, E, k, dev, dense=False, parts=1)
+        r.topk_idx.copy_(idx)
+        r.topk_w.copy_(w)
+        r.count_part.copy_(mask.reshape(M, E).sum(0).to(torch.int32).view(1, E))
+        r.probsum_part.zero_()
+        lists = kernels.moe_scatter(r)
+        gammas, packed = mod.quantized()
+        frags = kernels.moe_expert_fragments(*packed)
+        x2d = x.detach().reshape(M, E * D).float().contiguous()
+        y = torch.zeros(M, E * D, device=dev, dtype=torch.float32)
+        if M:
+            kernels.moe_experts(x2d, y, r, lists, frags, gammas, mod.hidden)
+        ctx.save_for_backward(x2d, idx, gammas, *packed)
+        ctx.route, ctx.lists, ctx.shape, ctx.H, ctx.x_dtype = r, lists, (B, T, E, D), mod.hidden, x.dtype
+        return y.view(B, T, E, D)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x2d, idx, gammas, pg, pu, pd = ctx.saved_tensors
+        B, T, E, D = ctx.shape
+        M = B * T
+        need_x, need_w_route = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        need_w = any(ctx.needs_input_grad[4:7])
+        gy2d = gy.reshape(M, E * D).float().contiguous()
+        dx, dpair, grads = kernels.moe_experts_bwd(x2d, gy2d, ctx.route, ctx.lists, (pg, pu, pd), gammas, ctx.H,
+                                                   need_w=need_w)
+        d_ew = None
+        if need_w_route:
+            d_ew = torch.zeros(M, E, device=gy.device, dtype=torch.float32).scatter_(1, idx, dpair).view(B, T, E)
+        gx = dx.view(B, T, E, D).to(ctx.x_dtype) if need_x else None
+        gg, gu, gd = grads if grads is not None else (None, None, None)
+        return gx, d_ew, None, None, gg, gu, gd, None
 
 
 class HadamardRouter(nn.Module):
@@ -357,7 +413,8 @@ class HadamardMoE(nn.Module):
             with torch.no_grad():
                 self._expert_counts += mask.reshape(-1, E).sum(0)
                 self._total_tokens += B * T
-        out = self.experts.forward_autograd(xr.reshape(B, T, E, self.block_dim), weights).reshape(B, T, C)
+        out = self.experts.forward_autograd(xr.reshape(B, T, E, self.block_dim), weights, mask=mask.detach(),
+                                            k=self.router.top_k).reshape(B, T, C)
         ydt = _output_dtype(x) if out_dtype is None else out_dtype
         return out.to(torch.float32 if dt == torch.float32 else ydt)
 
