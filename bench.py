@@ -25,6 +25,8 @@ Other workloads (``--workload``), each printing one JSON line of its own:
             with targets, backward, AdamW), batch x seq tokens;
   walsh_load  a .walsh v4 file of config-5 ternary weights decoded on the
             GPU straight into 2-bit packed buffers;
+  router    HadamardRouter alone at the n_embd-4096 width (hidden 1024,
+            128 experts, k = 6), bf16, x [64, 1024, 4096];
   chanmod   the block's channel modulation x + cm(RMSNorm(x)) on the
             headline model's streams ([8, 1024, 4, 512] bf16, viewed as 32
             groups of 1024 rows), and a sweep with rotated buffers.
@@ -65,7 +67,7 @@ def parse():
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
     ap.add_argument("--workload", default="mhcwalsh",
                     choices=["mhcwalsh", "moe", "octonion", "hadamard", "prefill5", "decode5", "hadamard_bwd",
-                             "train2", "walsh_load", "chanmod"])
+                             "train2", "walsh_load", "chanmod", "router"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (reference for HBM byte counters)")
     return ap.parse_args()
@@ -196,7 +198,7 @@ def main():
         line = {"moe": bench_moe, "octonion": bench_octonion, "hadamard": bench_hadamard, "prefill5": bench_prefill5,
                 "decode5": bench_decode5, "hadamard_bwd": bench_hadamard_bwd,
                 "train2": bench_train2, "walsh_load": bench_walsh_load,
-                "chanmod": bench_chanmod}[args.workload](torch, args)
+                "chanmod": bench_chanmod, "router": bench_router}[args.workload](torch, args)
         print(json.dumps(line), flush=True)
         return
     _hip.lib()
@@ -389,6 +391,47 @@ def bench_moe(torch, args):
                  "synthetic: x N(0,1), router N(0,0.02), experts U(-1,1) latents",
                  {"workload": "HadamardMoE n_embd 512, 16 experts, k 6, expansion 4", "global_batch": B,
                   "seq_len": T, "parallelism": "single GPU", "rotated_buffers": nbuf}, roof, cpu)
+
+
+def bench_router(torch, args):
+    """HadamardRouter.forward's routing (moe.py:407-447) at the n_embd-4096
+    width: Linear(4096, 1024) -> SiLU -> Linear(1024, 128), softmax, top-6;
+    weights N(0, 0.01) as the module's init, x [64, 1024, 4096] bf16."""
+    from src.model import _hip
+    from src.model.moe import HadamardRouter
+    torch.manual_seed(0)
+    m = HadamardRouter(4096, n_experts=128, max_experts=6).cuda().eval()
+    B, T, C = 64, 1024, 4096
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(B * T, C, generator=gen).bfloat16().cuda()
+
+    def step(i):
+        with torch.no_grad():
+            return m.route(x)
+    dt = _time_steps(torch, step, args.steps, args.warmup)
+    with _hip.LaunchTimer() as lt:
+        for i in range(args.steps):
+            step(i)
+    roof = _roofline_of(lt.summary(), args.steps, bound="mfma")
+    cpu = None
+    if not args.no_cpu:
+        host = cpu_setup(torch)
+        from oracle.moe import route_from_probs, router_logits, softmax
+        w1 = m.gate[0].weight.detach().float().cpu().numpy()
+        w2 = m.gate[2].weight.detach().float().cpu().numpy()
+        xc = x[:1024].float().cpu().numpy()
+        t0, reps = time.perf_counter(), 0
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0) or reps == 0:
+            route_from_probs(softmax(router_logits(xc, w1, w2)), 6)
+            reps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=round(reps * 1024 / el, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                   host=host,
+                   sample=f"{reps} x 1024 tokens through oracle/moe.py's router (numpy), {el:.1f} s")
+    return _line("tokens/sec through the MoE router at 1 GPU; % of MFMA roofline", B * T / dt, "tokens/s",
+                 args.steps, args.warmup, dt * 1e3, "bf16", "synthetic: x N(0,1), router weights N(0,0.01)",
+                 {"workload": "HadamardRouter n_embd 4096, hidden 1024, 128 experts, k 6", "global_batch": B,
+                  "seq_len": T, "parallelism": "single GPU"}, roof, cpu)
 
 
 def bench_octonion(torch, args):

@@ -1,6 +1,8 @@
 // bf16 GEMM y[m][n] = epi(sum_k x[m][k] B[n][k]) on 256 x 256 output tiles
-// (the octonion forward and the wide MoE router's first layer).
+// (the octonion forward and weight gradient, the wide MoE router's first layer).
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace walsh {
@@ -31,190 +33,289 @@ __device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16
 __device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 // ------------------------------------------------------- bf16 GEMM, 256 x 256
-// The bf16 forward at every shape.  256 x 256 output tiles, 8 wavefronts of
-// 64 outputs x 128 tokens each.  The product runs transposed, D[n][m] =
-// sum_k B[n][k] x[m][k] on 16x16x32 bf16 MFMA, so a lane's accumulator holds
-// 4 consecutive outputs of one token: the epilogue writes 8-byte pieces of
-// rows with beta applied.
-//   * Per 64-wide K stage both operand tiles (x: 256 tokens, the dense +-1/0
-//     block matrix: 256 outputs; 32 KB each) go global -> registers -> LDS,
-//     double buffered with one barrier per stage; every global byte is
-//     fetched once per workgroup (two wavefronts share each weight row, four
-//     each x row).
-//   * LDS rows are 128 B with the 16-byte chunks XOR-swizzled by the row
-//     (chunk ^ (row & 7)), so fragment reads and tile stores are free of bank
-//     conflicts (measured with SQ_LDS_BANK_CONFLICT).
-//   * Tiles are numbered XCD-major: workgroup b runs on XCD b % 8, and takes
-//     tile (b % 8) * per_xcd + b / 8, so the output tiles of one row block run
-//     side by side on one XCD and x comes from HBM once into that XCD's L2.
-constexpr int kOBM = 256, kOBN = 256, kOBK = 64;
-constexpr int kOThreads = 512;
-constexpr int kOTile = kOBM * 128;  // bytes of one staged operand tile
+// Persistent workgroups of 4 wavefronts (one per SIMD), each wavefront 128
+// outputs x 128 tokens, so a K step of 32 costs 16 fragment reads from LDS
+// per 64 MFMA (16x16x32 bf16).  The product runs transposed, D[n][m] =
+// sum_k B[n][k] x[m][k], so a lane's accumulator holds 4 consecutive outputs
+// of one token and the epilogue writes 8- or 16-byte pieces of rows.  The
+// 64 accumulator tiles (256 registers a lane) live in the AGPR half of the
+// register file.
+//   * Operands move global -> LDS with buffer_load_dwordx4 ... lds (no VGPR
+//     round trip).  A super-stage is 64 columns of both 256-row tiles, 128
+//     bytes a row (whole cache lines: half-line requests halved the L2
+//     throughput), 64 KB; two of them fit the LDS.  Each load instruction
+//     fills 1 KB = 8 rows; lane l lands at byte 16 l of it, so lane l
+//     fetches row l >> 3, chunk (l & 7) ^ (row & 7): 16-byte chunk c of row
+//     r sits at position c ^ (r & 7), and fragment reads (8 lanes per LDS
+//     cycle, rows r..r+7 of one chunk) are free of bank conflicts.
+//   * K runs in sub-stages of 32 columns (half a super-stage): the
+//     fragments of sub-stage t + 1 are read (interleaved with the products,
+//     two reads per eight MFMA) while the products of t run from registers.
+//     At every odd sub-stage 2S + 1 the workgroup waits for super-stage S + 1
+//     and synchronises once; super-stage S's buffer is then free (its last
+//     fragments are in registers) and super-stage S + 2 is issued into it,
+//     interleaved with that sub-stage's products, two sub-stages ahead of use.
+//   * The load stream runs across work items, so the next item's first
+//     super-stages are in flight while an item's epilogue stores.
+//   * Work items (tile, split) are numbered XCD-major: item w runs on XCD
+//     w / per_xcd (workgroup b lives on XCD b % 8), so the output tiles of one
+//     row block run side by side on one XCD and x comes from HBM about once
+//     into that XCD's L2.
+constexpr int kOBM = 256, kOBN = 256, kOBK = 64;  // tile rows of x, rows of B, columns per super-stage
+constexpr int kOThreads = 256;
+constexpr int kORow = 128;         // bytes of one staged row
+constexpr int kOOp = 256 * kORow;  // one operand of a super-stage
+constexpr int kOStage = 2 * kOOp;  // both operands: 64 KB
 
-// byte offset of 16-byte chunk `part` (0..7) of staged row `row`
-__device__ __forceinline__ int oct_off(int row, int part) { return row * 128 + ((part ^ (row & 7)) << 4); }
+struct Gemm256Plan {
+    int nM, nN, items, per_xcd, wg_per_xcd, nss;  // nss: super-stages per item
+};
+
+// position of 16-byte chunk c of staged row r
+__device__ __forceinline__ int g256_pos(int r, int c) { return c ^ (r & 7); }
 
 template <int EPI>
-__device__ __forceinline__ void gemm256_body(const Gemm256Args &a, int nM, int nN, int per_xcd) {
-    __shared__ __align__(16) unsigned char lds[2][2][kOTile];  // [buffer][x | weights]
+__device__ __forceinline__ void gemm256_body(const Gemm256Args &a, const Gemm256Plan &p) {
+    __shared__ __align__(1024) unsigned char lds[2 * kOStage];
 
-    int tile = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-    const int splits = a.splits > 0 ? a.splits : 1;
-    if (tile >= nM * nN * splits) return;
-    const int split = tile / (nM * nN);
-    tile -= split * nM * nN;
-    const int k_lo = a.kspan > 0 ? (int)(split * a.kspan) : 0;
-    const int k_hi = a.kspan > 0 ? (int)(k_lo + a.kspan < a.K ? k_lo + a.kspan : a.K) : a.K;
-    const int mb = tile / nN, nb = tile - mb * nN;
-    const int m0 = mb * kOBM, n0 = nb * kOBN;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wn = wave & 3, wm = wave >> 2;
-    const int fr = lane & 15, fq = lane >> 4;
+    const int xcd = (int)(blockIdx.x % 8), wgi = (int)(blockIdx.x / 8);
+    const int first = xcd * p.per_xcd + wgi;
+    const int end = min((xcd + 1) * p.per_xcd, p.items);
+    if (first >= end) return;
+    const int n_items = (end - first + p.wg_per_xcd - 1) / p.wg_per_xcd;  // items first, first + wg_per_xcd, ..
+    const int tiles = p.nM * p.nN;
 
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * 2));
-    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.B, (uint32_t)((int64_t)a.N * a.Kp * 2));
+    const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15, fq = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 1, wm = wave >> 1;
 
-    // staging: each operand tile is 256 rows x 8 chunks of 16 B; thread takes
-    // chunk tid + 512 i (i = 0..3) of both: row (tid >> 3) + 64 i, chunk
-    // tid & 7.  Out-of-range chunks read zeros.
-    const int srow = tid >> 3, spart = tid & 7;
-    auto load = [&](int k0, u32x4 (&xst)[4], u32x4 (&wst)[4]) {
-        const int k = k_lo + k0 + spart * 8;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m0 + srow + 64 * i, n = n0 + srow + 64 * i;
-            xst[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                xr, (m < a.M && k < k_hi) ? (uint32_t)(((int64_t)m * a.ldx + k) * 2) : kOOB, 0, 0);
-            wst[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                br, (n < a.N && k < (a.kspan > 0 ? k_hi : a.Kp)) ? (uint32_t)(((int64_t)n * a.Kp + k) * 2) : kOOB,
-                0, 0);
-        }
+    // work item r of this workgroup: output tile and K range
+    struct Item {
+        int m0, n0, k_lo, k_hi, split;
     };
-    auto store = [&](int buf, const u32x4 (&xst)[4], const u32x4 (&wst)[4]) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int off = oct_off(srow + 64 * i, spart);
-            *(u32x4 *)(&lds[buf][0][off]) = xst[i];
-            *(u32x4 *)(&lds[buf][1][off]) = wst[i];
+    auto item = [&](int r) {
+        Item it;
+        const int w = first + r * p.wg_per_xcd;
+        it.split = w / tiles;
+        const int tile = w - it.split * tiles;
+        const int mb = tile / p.nN;
+        it.m0 = mb * kOBM;
+        it.n0 = (tile - mb * p.nN) * kOBN;
+        if (a.kspan > 0) {
+            it.k_lo = (int)(it.split * a.kspan);
+            it.k_hi = (int)min((int64_t)a.K, (int64_t)it.k_lo + a.kspan);
+        } else {
+            it.k_lo = 0;
+            it.k_hi = a.K;
         }
+        return it;
     };
 
-    f32x4 acc[4][8];
+    // loads: waves 0, 1 stage x rows 128 (wave & 1) .. +127 of the tile, waves
+    // 2, 3 the B rows; instruction i (0..15) covers rows 8 i .. 8 i + 7 of them
+    const bool xrole = wave < 2;
+    const __amdgpu_buffer_rsrc_t rs = xrole ? make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * 2))
+                                            : make_rsrc(a.B, (uint32_t)((int64_t)a.N * a.Kp * 2));
+    const uint32_t ld2 = (uint32_t)((xrole ? a.ldx : (int64_t)a.Kp) * 2);
+    const int lim = xrole ? a.M : a.N;
+    const int dch = (lane & 7) ^ (lane >> 3);
+    const int lrow = (wave & 1) * 128 + (lane >> 3);
+    const int opoff = (xrole ? 0 : kOOp) + (wave & 1) * 16 * 1024;
+    // super-stage G of the workgroup's stream (item G / nss): per-lane byte
+    // offset of instruction 0 (kOOB when nothing is to load) and whether
+    // instruction i's row exists (row + 8 i < lim)
+    struct Src {
+        uint32_t off;
+        int rows_left;
+    };
+    auto src = [&](int G) {
+        Src s;
+        const int r = G / p.nss, S = G - r * p.nss;
+        s.off = kOOB;
+        s.rows_left = 0;
+        if (r < n_items) {
+            const Item it = item(r);
+            const int row = (xrole ? it.m0 : it.n0) + lrow;
+            const int k = it.k_lo + S * kOBK + dch * 8;
+            if (k < it.k_hi && row < lim) {
+                s.off = (uint32_t)row * ld2 + (uint32_t)k * 2;
+                s.rows_left = lim - row;
+            }
+        }
+        return s;
+    };
+    auto dma = [&](int G, const Src &s, int i) {
+        unsigned char *dst = lds + (G & 1) * kOStage + opoff + i * 1024;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16,
+                                                 8 * i < s.rows_left ? s.off + (uint32_t)(8 * i) * ld2 : kOOB, 0, 0,
+                                                 0);
+    };
+    // fragments of sub-stage t: super-stage t / 2, chunks 4 (t & 1) + fq
+    auto rd = [&](int t, int g, u32x4 &bf, u32x4 &xf) {
+        const unsigned char *base = lds + ((t >> 1) & 1) * kOStage;
+        const int c = 4 * (t & 1) + fq;
+        const int rb = wn * 128 + g * 16 + fr, rx = wm * 128 + g * 16 + fr;
+        bf = *(const u32x4 *)(base + kOOp + rb * kORow + (g256_pos(rb, c) << 4));
+        xf = *(const u32x4 *)(base + rx * kORow + (g256_pos(rx, c) << 4));
+    };
+
+    f32x4 acc[8][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Stage st + 2 is fetched during stage st into the register set stage
-    // st + 1 was stored from, so each global load has two stages of products
-    // to land in; sched_barrier(0) keeps the compiler from sinking the
-    // prefetch below the products.
-    auto stage = [&](int st, u32x4 (&xn)[4], u32x4 (&wn_)[4], u32x4 (&xf_)[4], u32x4 (&wf_)[4]) {
-        const int cur = st & 1;
-        load((st + 2) * kOBK, xf_, wf_);  // zeros past the end
-        __builtin_amdgcn_sched_barrier(0);
+    // epilogue of item r: acc[i][j][q] = D[n = n0 + 128 wn + 16 i + 4 fq + q][m = m0 + 128 wm + 16 j + fr]
+    auto epilogue = [&](int r) {
+        const Item it = item(r);
+        if constexpr (EPI == kEpiF32) {
+            const int64_t span = a.kspan > 0 ? (int64_t)(p.items / tiles - 1) * a.ysplit + (int64_t)a.M * a.ldy
+                                             : (int64_t)a.M * a.ldy;
+            const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)(span * 4));
+            const int64_t ybase = a.kspan > 0 ? (int64_t)it.split * a.ysplit : 0;
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            u32x4 wf[4];
+            for (int i = 0; i < 8; ++i) {
+                const int n = it.n0 + wn * 128 + i * 16 + fq * 4;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) wf[t] = *(const u32x4 *)(&lds[cur][1][oct_off(wn * 64 + t * 16 + fr, sub * 4 + fq)]);
+                for (int j = 0; j < 8; ++j) {
+                    const int m = it.m0 + wm * 128 + j * 16 + fr;
+                    const uint32_t off =
+                        (m < a.M && n < a.N) ? (uint32_t)((ybase + (int64_t)m * a.ldy + n) * 4) : kOOB;
+                    Buf4<float>::store(acc[i][j], yr, off, 0);
+                }
+            }
+        } else {
+            const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {  // the wave's 8 token tiles in two halves (register pressure)
-                u32x4 xf[4];
+            for (int i = 0; i < 8; ++i) {
+                const int n = it.n0 + wn * 128 + i * 16 + fq * 4;
+                f32x4 bv = f32x4{1.f, 1.f, 1.f, 1.f};
+                if (EPI == kEpiBeta && a.beta && n < a.N) {
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    xf[t] = *(const u32x4 *)(&lds[cur][0][oct_off(wm * 128 + (h * 4 + t) * 16 + fr, sub * 4 + fq)]);
+                    for (int q = 0; q < 4; ++q) bv[q] = a.beta[(n + q) % a.out_o];
+                }
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 8; ++j) {
+                    const int m = it.m0 + wm * 128 + j * 16 + fr;
+                    const uint32_t off = (m < a.M && n < a.N) ? (uint32_t)(((int64_t)m * a.ldy + n) * 2) : kOOB;
+                    if constexpr (EPI == kEpiBeta) {
+                        Buf4<uint16_t>::store(acc[i][j] * bv, yr, off, 0);
+                    } else {
+                        // the product rounded to bf16, SiLU on that value, rounded again
+                        f32x4 v;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[i][h * 4 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8, wf[i]), __builtin_bit_cast(bf16x8, xf[j]), acc[i][h * 4 + j], 0,
-                            0, 0);
+                        for (int q = 0; q < 4; ++q) v[q] = silu_f(bf16r(acc[i][j][q]));
+                        Buf4<uint16_t>::store(v, yr, off, 0);
+                    }
+                }
             }
         }
-        __builtin_amdgcn_sched_barrier(0);
-        store(cur ^ 1, xn, wn_);            // stage st + 1
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
 
-    const int nst = (int)ceil_div(k_hi - k_lo, kOBK);
-    u32x4 xa[4], wa[4], xb[4], wb[4];
-    load(0, xa, wa);
-    load(kOBK, xb, wb);
-    store(0, xa, wa);
-    __syncthreads();
-    int st = 0;
-    for (; st + 1 < nst; st += 2) {
-        stage(st, xb, wb, xa, wa);
-        stage(st + 1, xa, wa, xb, wb);
+    // prologue: super-stages 0 and 1 in flight, wait for 0
+    {
+        const Src s0 = src(0), s1 = src(1);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dma(0, s0, i);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dma(1, s1, i);
     }
-    if (st < nst) stage(st, xb, wb, xa, wa);
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    u32x4 b0[8], x0[8], b1[8], x1[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) rd(0, g, b0[g], x0[g]);
 
-    // epilogue: acc[i][j][r] = D[n = 16 i + 4 fq + r][m = 16 j + fr] of the wave's tile
-    if constexpr (EPI == kEpiF32) {
-        const int64_t span = a.kspan > 0 ? (int64_t)(splits - 1) * a.ysplit + (int64_t)a.M * a.ldy : (int64_t)a.M * a.ldy;
-        const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)(span * 4));
-        const int64_t ybase = (int64_t)split * a.ysplit;
+    // sub-stage t (of the workgroup's stream; 2 nss per item): products of t
+    // from registers while the fragments of t + 1 are read.  The previous
+    // sub-stage's reads are complete (lgkmcnt(0); they were issued a whole
+    // sub-stage ago).  Odd t: super-stage (t + 1) / 2 has landed (nothing was
+    // issued after it but stores), and once every wave is past the barrier
+    // none reads the buffer of super-stage (t - 1) / 2, which takes
+    // super-stage (t - 1) / 2 + 2.
+    auto step = [&](int t, const u32x4 (&bc)[8], const u32x4 (&xc)[8], u32x4 (&bn)[8], u32x4 (&xn)[8], auto odd) {
+        constexpr bool ODD = decltype(odd)::value;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        Src s{kOOB, 0};
+        const int G = (t - 1) / 2 + 2;
+        if constexpr (ODD) {
+            s = src(G);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            asm volatile("s_barrier" ::: "memory");
+        }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int n = n0 + wn * 64 + i * 16 + fq * 4;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int m = m0 + wm * 128 + j * 16 + fr;
-                const uint32_t off = (m < a.M && n < a.N) ? (uint32_t)((ybase + (int64_t)m * a.ldy + n) * 4) : kOOB;
-                Buf4<float>::store(acc[i][j], yr, off, 0);
+        for (int g = 0; g < 8; ++g) {
+            if constexpr (ODD) {
+                dma(G, s, 2 * g);
+                dma(G, s, 2 * g + 1);
             }
+            rd(t + 1, g, bn[g], xn[g]);  // past the stream's end: unused values
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bc[g]),
+                                                                    __builtin_bit_cast(bf16x8, xc[j]), acc[g][j], 0,
+                                                                    0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        return;
+    };
+    const int per_item = 2 * p.nss;
+    for (int r = 0; r < n_items; ++r) {
+        const int t0 = r * per_item;
+        for (int t = t0; t < t0 + per_item; t += 2) {
+            step(t, b0, x0, b1, x1, std::false_type{});
+            step(t + 1, b1, x1, b0, x0, std::true_type{});
+        }
+        epilogue(r);
+        // the next item's first fragments again (its super-stage landed before
+        // the last barrier): the values read by the last step are not kept
+        // across the epilogue
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+#pragma unroll
+        for (int g = 0; g < 8; ++g) rd(t0 + per_item, g, b0[g], x0[g]);
     }
-    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int n = n0 + wn * 64 + i * 16 + fq * 4;
-        f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (EPI == kEpiBeta && n < a.N) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) bv[r] = a.beta ? a.beta[(n + r) % a.out_o] : 1.f;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int m = m0 + wm * 128 + j * 16 + fr;
-            const uint32_t off = (m < a.M && n < a.N) ? (uint32_t)(((int64_t)m * a.ldy + n) * 2) : kOOB;
-            if constexpr (EPI == kEpiBeta) {
-                Buf4<uint16_t>::store(acc[i][j] * bv, yr, off, 0);
-            } else {
-                // the product rounded to bf16, SiLU on that value, rounded again
-                f32x4 v;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = silu_f(bf16r(acc[i][j][r]));
-                Buf4<uint16_t>::store(v, yr, off, 0);
-            }
-        }
-    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write may outlive the workgroup
 }
 
-static __global__ __launch_bounds__(kOThreads, 1) void gemm256_beta_kernel(Gemm256Args a, int nM, int nN, int per_xcd) {
-    gemm256_body<kEpiBeta>(a, nM, nN, per_xcd);
+static __global__ __launch_bounds__(kOThreads, 1) void gemm256_beta_kernel(Gemm256Args a, Gemm256Plan p) {
+    gemm256_body<kEpiBeta>(a, p);
 }
-static __global__ __launch_bounds__(kOThreads, 1) void gemm256_silu_kernel(Gemm256Args a, int nM, int nN, int per_xcd) {
-    gemm256_body<kEpiSilu>(a, nM, nN, per_xcd);
+static __global__ __launch_bounds__(kOThreads, 1) void gemm256_silu_kernel(Gemm256Args a, Gemm256Plan p) {
+    gemm256_body<kEpiSilu>(a, p);
 }
-static __global__ __launch_bounds__(kOThreads, 1) void gemm256_f32_kernel(Gemm256Args a, int nM, int nN, int per_xcd) {
-    gemm256_body<kEpiF32>(a, nM, nN, per_xcd);
+static __global__ __launch_bounds__(kOThreads, 1) void gemm256_f32_kernel(Gemm256Args a, Gemm256Plan p) {
+    gemm256_body<kEpiF32>(a, p);
 }
 
-// grid: ceil(M / 256) x ceil(N / 256) tiles (x splits) in XCD-major order
+// Requirements (checked by the callers): K % 8 == 0, N % 4 == 0, ldx and Kp
+// multiples of 8, x / B / y within 2^31 bytes, 16-byte aligned operands.
+static inline Gemm256Plan gemm256_plan(const Gemm256Args &a) {
+    Gemm256Plan p;
+    p.nM = (int)ceil_div(a.M, kOBM);
+    p.nN = (int)ceil_div(a.N, kOBN);
+    p.items = p.nM * p.nN * (a.splits > 0 ? a.splits : 1);
+    p.nss = (int)ceil_div(a.kspan > 0 ? a.kspan : (int64_t)a.K, kOBK);
+    p.per_xcd = (int)ceil_div(p.items, 8);
+    const int per_xcd_cus = device_info().cu_count / 8 > 0 ? device_info().cu_count / 8 : 1;
+    p.wg_per_xcd = p.per_xcd < per_xcd_cus ? p.per_xcd : per_xcd_cus;
+    return p;
+}
+
+// one workgroup per CU at most (128 KB of LDS each), items XCD-major
 template <int EPI>
 static inline void gemm256_launch(const Gemm256Args &a, hipStream_t s) {
-    const int nM = (int)ceil_div(a.M, kOBM), nN = (int)ceil_div(a.N, kOBN);
-    const int per_xcd = (int)ceil_div((int64_t)nM * nN * (a.splits > 0 ? a.splits : 1), 8);
+    const Gemm256Plan p = gemm256_plan(a);
+    if (p.items == 0 || p.nss == 0) return;
+    const dim3 grid((unsigned)(8 * p.wg_per_xcd)), block(kOThreads);
     if constexpr (EPI == kEpiBeta)
-        launch(gemm256_beta_kernel, dim3((unsigned)(per_xcd * 8)), dim3(kOThreads), 0, s, a, nM, nN, per_xcd);
+        launch(gemm256_beta_kernel, grid, block, 0, s, a, p);
     else if constexpr (EPI == kEpiSilu)
-        launch(gemm256_silu_kernel, dim3((unsigned)(per_xcd * 8)), dim3(kOThreads), 0, s, a, nM, nN, per_xcd);
+        launch(gemm256_silu_kernel, grid, block, 0, s, a, p);
     else
-        launch(gemm256_f32_kernel, dim3((unsigned)(per_xcd * 8)), dim3(kOThreads), 0, s, a, nM, nN, per_xcd);
+        launch(gemm256_f32_kernel, grid, block, 0, s, a, p);
 }
 
 }  // namespace walsh

@@ -394,25 +394,50 @@ __global__ __launch_bounds__(kMoeThreads) void moe_topk_kernel(const float *__re
 
 // Top-k routing for 16 < E <= 128 experts: one wavefront per token, lane l
 // holding experts l and l + 64.  Softmax by wave reductions (max, then a
-// fixed-order sum); the probabilities go to LDS and each lane ranks its own
-// experts by counting the entries that beat them (larger probability, ties to
-// the lower index), so the k selected experts and their order need no
-// sequential rounds.  Same outputs as moe_topk_kernel.
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int sh = 32; sh > 0; sh >>= 1) v = fmaxf(v, __shfl_xor(v, sh));
-    return v;
+// fixed-order sum); the k selected experts come from k rounds of a wave
+// argmax (largest probability, ties to the lower expert index), each round a
+// register max over the wave and a ballot of the lanes holding it, so no LDS
+// round trip and O(k) instead of O(E) steps per lane.  Same outputs as
+// moe_topk_kernel.
+//
+// Wave reductions on the VALU: DPP moves within each row of 16 lanes and the
+// gfx950 permlane16/32 swaps across rows (with both operands equal a swap
+// returns a lane's value and its partner's, lanes i ^ 16 or i ^ 32).
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]: lanes ^ 1
+    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]: lanes ^ 2
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror: the other quad of 8
+    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror: the other 8 of the row
+    const u32x2v a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a.x), __uint_as_float(a.y));
+    const u32x2v b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b.x), __uint_as_float(b.y));
+}
+// Sum over the wave as the butterfly v += v[lane ^ s] for s = 32, 16, 8, 4,
+// 2, 1 (every lane ends with the same, order-fixed value).  Within a row the
+// partner comes from a rotation by s: after the steps of 2s, 4s, .. the row's
+// values depend only on lane mod 2s, where lane + s and lane ^ s agree.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int sh = 32; sh > 0; sh >>= 1) v += __shfl_xor(v, sh);
+    const u32x2v b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(b.x) + __uint_as_float(b.y);
+    const u32x2v a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a.x) + __uint_as_float(a.y);
+    v += dpp_f<0x128>(v);  // row_ror 8
+    v += dpp_f<0x124>(v);  // row_ror 4
+    v += dpp_f<0x122>(v);  // row_ror 2
+    v += dpp_f<0x121>(v);  // row_ror 1
     return v;
 }
 
-// Softmax, rank top-k and the routing outputs of token `tok`, whose logits
-// the wave holds as lg[0] (expert lane) and lg[1] (expert lane + 64), -inf
-// past E.  pl: the wave's kMaxE-float LDS row (16-byte aligned).
-__device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], float *pl, const RouteOut &o, int *cnt_l,
+// Softmax, top-k and the routing outputs of token `tok`, whose logits the
+// wave holds as lg[0] (expert lane) and lg[1] (expert lane + 64), -inf past
+// E.  Every lane of the wave takes part.
+__device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], const RouteOut &o, int *cnt_l,
                                            float *ps_l) {
     const int lane = threadIdx.x & 63;
     const int E = o.E, k = o.k;
@@ -424,29 +449,26 @@ __device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], float 
 #pragma unroll
     for (int h = 0; h < 2; ++h) p[h] = (lg[h] == -INFINITY) ? 0.f : expf(lg[h] - mx);
     const float sum = wave_sum(p[0] + p[1]);
+    // q: the candidates of the argmax rounds; probabilities are >= 0, entries
+    // past E hold -1 and a selected entry -inf, so neither wins again
+    float q[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         p[h] = __fdiv_rn(p[h], sum);
-        pl[e[h]] = e[h] < E ? p[h] : -1.f;  // probabilities are >= 0: -1 never beats
+        q[h] = e[h] < E ? p[h] : -1.f;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ranks: the token's probabilities read back 32 at a time (8 x 16-byte
-    // broadcast reads in flight together); entries past E hold -1
-    int rank[2] = {0, 0};
-    const int E32 = (E + 31) & ~31;
-    for (int j0 = 0; j0 < E32; j0 += 32) {
-        f32x4 pv[8];
+    int rank[2] = {kMaxE, kMaxE};
+    for (int r = 0; r < k; ++r) {
+        const float m = wave_max(fmaxf(q[0], q[1]));
+        const uint64_t b0 = __ballot(q[0] == m), b1 = __ballot(q[1] == m);
+        // the lowest expert index holding the maximum (experts 0..63 first);
+        // none when the probabilities are not numbers
+        const int win = b0 ? (int)__builtin_ctzll(b0) : (b1 ? 64 + (int)__builtin_ctzll(b1) : -1);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) pv[u] = *(const f32x4 *)&pl[j0 + 4 * u];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int j = j0 + 4 * u + c;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) rank[h] += beats(pv[u][c], p[h], j < e[h]);
+        for (int h = 0; h < 2; ++h)
+            if (win == e[h]) {
+                rank[h] = r;
+                q[h] = -INFINITY;
             }
     }
     bool sel[2];
@@ -469,14 +491,11 @@ __device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], float 
         if (o.wdense) o.wdense[pe] = sel[h] ? __fdiv_rn(p[h], den) : 0.f;
         if (o.y && !sel[h]) zero_block(o.y, o.y_bf16, tok * o.ldy + 32 * e[h]);
     }
-    // the wave's next token overwrites pl only after every lane read it
-    __builtin_amdgcn_wave_barrier();
 }
 
 __global__ __launch_bounds__(kMoeThreads) void moe_topk_rank_kernel(const float *__restrict__ logits, RouteOut o) {
     __shared__ int cnt_l[kMaxE];
     __shared__ float ps_l[kMaxE];
-    __shared__ __align__(16) float pl[kMoeWaves][kMaxE];
     part_init(cnt_l, ps_l);
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -487,7 +506,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_topk_rank_kernel(const float 
             const int e = lane + 64 * h;
             lg[h] = e < o.E ? logits[(int64_t)tok * o.E + e] : -INFINITY;
         }
-        rank_token(tok, lg, pl[wave], o, cnt_l, ps_l);
+        rank_token(tok, lg, o, cnt_l, ps_l);
     }
     part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
 }
@@ -1104,7 +1123,6 @@ __global__ __launch_bounds__(kMoeThreads) void router_topk_part_kernel(const flo
                                                                        RouteOut o) {
     __shared__ int cnt_l[kMaxE];
     __shared__ float ps_l[kMaxE];
-    __shared__ __align__(16) float pl[kMaxE];
     __shared__ __align__(16) float ws[kMoeWaves][kMaxE];
     part_init(cnt_l, ps_l);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1139,7 +1157,7 @@ __global__ __launch_bounds__(kMoeThreads) void router_topk_part_kernel(const flo
                 for (int w = 0; w < kMoeWaves; ++w) v += ws[w][ee];
                 lg[hh] = ee < E ? bf16r(v) : -INFINITY;
             }
-            rank_token(tok, lg, pl, o, cnt_l, ps_l);
+            rank_token(tok, lg, o, cnt_l, ps_l);
         }
     }
     part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
@@ -1167,7 +1185,6 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int cnt_l[kMaxE];
     __shared__ float ps_l[kMaxE];
-    __shared__ __align__(16) float pl[kR2Waves][kMaxE];
     part_init(cnt_l, ps_l);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, fr = lane & 15, fq = lane >> 4;
     const int M = o.M, E = o.E, nch = H / 8, nks = H / 32;
@@ -1247,7 +1264,7 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
                 const int e = lane + 64 * hh;
                 lg[hh] = e < E ? lg_l[tl * kR2LgStride + e] : -INFINITY;
             }
-            rank_token(m0 + tl, lg, pl[wave], o, cnt_l, ps_l);
+            rank_token(m0 + tl, lg, o, cnt_l, ps_l);
         }
     }
     part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
@@ -1524,7 +1541,7 @@ WALSH_EXPORT int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M
     if (M * ldx * 2 > (int64_t)kMaxBufferBytes || M * H * 2 > (int64_t)kMaxBufferBytes ||
         H * C * 2 > (int64_t)kMaxBufferBytes)
         return set_error(WALSH_ENOTSUP, "%s: operands above 2^31 bytes", fn);
-    if (router_w2_lds_bytes((int)H, 4) + 8 * kMaxE + kR2Waves * kMaxE * 4 > (size_t)device_info().max_shared_per_block)
+    if (router_w2_lds_bytes((int)H, 4) + 8 * kMaxE > (size_t)device_info().max_shared_per_block)
         return set_error(WALSH_ENOTSUP, "%s: H=%lld needs more LDS than a workgroup has", fn, (long long)H);
     hipStream_t s = (hipStream_t)stream;
     if (M == 0) {

@@ -531,10 +531,7 @@ WALSH_EXPORT int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M
         a.y = (char *)y + r0 * ldy * esz;
         a.ldy = ldy;
         if (dtype == WALSH_BF16) {
-            const int nM = (int)ceil_div(rows, kOBM), nN = (int)ceil_div(N, kOBN);
-            const int per_xcd = (int)ceil_div((int64_t)nM * nN, 8);
-            launch(gemm256_beta_kernel, dim3((unsigned)(per_xcd * 8)), dim3(kOThreads), 0, (hipStream_t)stream, a,
-                   nM, nN, per_xcd);
+            gemm256_launch<kEpiBeta>(a, (hipStream_t)stream);
         } else {
             const dim3 G((unsigned)ceil_div(rows, kBM), (unsigned)ceil_div(N, kBN)), Bk(kGemmThreads);
             launch(octonion_gemm_kernel<float>, G, Bk, 0, (hipStream_t)stream, a);
