@@ -76,14 +76,19 @@ __device__ __forceinline__ f32x4 rope_cs(const HadArgs &a, int row, int o0) {
     return *(const f32x4 *)(a.rope + ((int64_t)t * (a.rope_D >> 1) + i0) * 2);
 }
 
-// One pair (e, o) turned by (c, s), with the fused multiply-adds written out
-// so that every kernel rounds a rotation the same way.
+// One pair (e, o) turned by (c, s) with the fused multiply-adds written out:
+// e c - o s as fma(e, c, -(o s)) and e s + o c as fma(e, s, o c).  The
+// kernels that rotate whole fragments (rope_apply) leave the contraction to
+// the compiler, which forms exactly these two (checked in the gfx950 code and
+// by the tests that compare the decode-sized kernel, which uses these, with
+// the wide kernel bitwise); writing them out there instead made the wide
+// kernel spill.
 __device__ __forceinline__ float rope_even(float e, float o, float c, float s) { return __builtin_fmaf(e, c, -(o * s)); }
 __device__ __forceinline__ float rope_odd(float e, float o, float c, float s) { return __builtin_fmaf(e, s, o * c); }
 
 __device__ __forceinline__ f32x4 rope_apply(f32x4 r, f32x4 cs) {
-    return f32x4{rope_even(r[0], r[1], cs[0], cs[1]), rope_odd(r[0], r[1], cs[0], cs[1]),
-                 rope_even(r[2], r[3], cs[2], cs[3]), rope_odd(r[2], r[3], cs[2], cs[3])};
+    return f32x4{r[0] * cs[0] - r[1] * cs[1], r[0] * cs[1] + r[1] * cs[0], r[2] * cs[2] - r[3] * cs[3],
+                 r[2] * cs[3] + r[3] * cs[2]};
 }
 
 __device__ __forceinline__ uint32_t x_row_off(const HadArgs &a, int row, uint32_t esz) {
