@@ -537,6 +537,28 @@ int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, 
                               float *mask, float *weights_dense, int *topk_idx, float *topk_w, int *count,
                               float *probsum, int64_t n_part, void *y, int64_t ldy, int ydtype, void *stream);
 
+/* walsh_moe_decode_fwd: the whole HadamardMoE.forward (src/model/moe.py:
+ *   512-542: HadamardRouter.forward :418-447, then FastMoEExperts.forward
+ *   :337-380 on the routed pairs) for 1..4 tokens (decode) of a wide bf16
+ *   model, in one launch: the router as walsh_moe_router_wide_fwd (C ==
+ *   32 E, C % 256 == 0, hidden H % 128 == 0 and <= 1024, E % 4 == 0), the
+ *   experts as walsh_moe_experts_fwd (expert hidden He in {64, 128, 256},
+ *   fragments from the same layout) with y [M, >= 32E] (ydtype) written
+ *   whole: expert output * routing weight in the routed blocks, zeros in
+ *   the others.  Outputs equal the router / scatter / experts calls bitwise;
+ *   partial row t of count / probsum holds token t's counts and
+ *   probabilities (rows M.. of n_part zero), as the per-token rows of
+ *   walsh_moe_router_wide_fwd.  work: walsh_moe_decode_workspace_bytes(M, H, E) bytes,
+ *   256-byte aligned.  sync: one unsigned counter, zero before the first
+ *   call; each call leaves it at zero.  Calls that share a counter must not
+ *   overlap. */
+int64_t walsh_moe_decode_workspace_bytes(int64_t M, int64_t H, int64_t E);
+int walsh_moe_decode_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_t H, const void *w1, const void *w2,
+                         int64_t E, int64_t k, int64_t He, const uint8_t *gate_frag, const uint8_t *up_frag,
+                         const uint8_t *down_frag, const float *gammas, void *work, int64_t work_bytes, unsigned *sync,
+                         float *probs, float *mask, float *weights_dense, int *topk_idx, float *topk_w, int *count,
+                         float *probsum, int64_t n_part, void *y, int64_t ldy, int ydtype, void *stream);
+
 /* walsh_moe_experts_bwd: backward of FastMoEExperts.forward (src/model/moe.py
  *   :337-380, autograd of its einsums, SiLU and routing product, with the
  *   MoE STE of :289-294) over the routed pairs of a walsh_moe_scatter

@@ -215,6 +215,66 @@ def test_router_wide_module_path():
     assert torch.equal(r.topk_idx, r2.topk_idx) and torch.equal(r.probs, r2.probs)
 
 
+@pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
+def test_moe_decode_one_launch_equals_separate_launches(ydt):
+    """walsh_moe_decode_fwd (router, routing and experts of 1..4 tokens in one
+    launch, the last workgroup routing) against the wide router + scatter +
+    experts launches: outputs, selections, weights and the per-expert totals
+    bitwise, on consecutive calls (each must leave the completion counter at
+    zero for the next)."""
+    from src.model import kernels
+    m = make_moe(4096, max_experts=6, seed=11)
+    with torch.no_grad():
+        for lin in (m.router.gate[0], m.router.gate[2]):
+            lin.weight.normal_(0.0, 0.03)
+    for M in (1, 4, 2, 3, 1):
+        x = torch.randn(M, 4096, device="cuda").bfloat16()
+        y1 = torch.empty(M, 4096, device="cuda", dtype=ydt)
+        y2 = torch.empty_like(y1)
+        with torch.no_grad():
+            m.use_fused = True
+            r1 = m._decode(x, y1)
+            assert r1 is not None, "decode path not taken"
+            m.use_fused = False
+            r2 = m.router.route(x, y2d=y2)
+            m.experts.routed(x, r2, y2)
+        torch.cuda.synchronize()
+        assert int(m._decode_sync.item()) == 0, "counter not reset"
+        assert torch.equal(r1.topk_idx, r2.topk_idx), M
+        assert torch.equal(r1.topk_w, r2.topk_w), M
+        assert torch.equal(r1.count_part, r2.count_part) and torch.equal(r1.probsum_part, r2.probsum_part), M
+        assert torch.equal(r1.count, r2.count), M
+        assert torch.equal(y1, y2), (M, float((y1.float() - y2.float()).abs().max()))
+    m.use_fused = True
+
+
+def test_moe_decode_direct_dense_outputs():
+    """The entry point at another width (E 40, C 1280, k 4, expert hidden 64)
+    with the dense routing outputs, against the separate launches."""
+    from src.model import kernels
+    from src.model.moe import FastMoEExperts
+    torch.manual_seed(5)
+    E, C, H, k, He = 40, 1280, 384, 4, 64
+    w1 = (torch.randn(H, C, device="cuda") * 0.03).bfloat16().contiguous()
+    w2 = (torch.randn(E, H, device="cuda") * 0.03).bfloat16().contiguous()
+    ex = FastMoEExperts(E, 32, expansion=He // 32).cuda()
+    gammas, frags = ex.ternary_state(torch.bfloat16)
+    sync = torch.zeros(1, device="cuda", dtype=torch.int32)
+    for M in (3, 1):
+        x = torch.randn(M, C, device="cuda").bfloat16()
+        y1 = torch.full((M, C), 7.0, device="cuda", dtype=torch.bfloat16)
+        y2 = torch.full((M, C), 7.0, device="cuda", dtype=torch.bfloat16)
+        r1 = kernels.moe_decode(x, y1, w1, w2, E, k, frags, gammas, He, sync, dense=True)
+        r2 = kernels.moe_router_wide(x, w1, w2, E, k, dense=True, y=y2)
+        lists = kernels.moe_scatter(r2)
+        kernels.moe_experts(x, y2, r2, lists, frags, gammas, He)
+        torch.cuda.synchronize()
+        for a, b in ((r1.probs, r2.probs), (r1.mask, r2.mask), (r1.weights, r2.weights), (r1.topk_idx, r2.topk_idx),
+                     (r1.topk_w, r2.topk_w), (y1, y2)):
+            assert torch.equal(a, b), M
+        assert int(sync.item()) == 0
+
+
 # ------------------------------------------------------------ router + module, float32
 
 @pytest.mark.parametrize("B,T,C,kmax", [(2, 256, 512, 6), (1, 77, 512, 4), (3, 40, 256, 8), (1, 64, 2048, 6)])

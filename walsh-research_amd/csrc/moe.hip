@@ -438,7 +438,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // wave holds as lg[0] (expert lane) and lg[1] (expert lane + 64), -inf past
 // E.  Every lane of the wave takes part.
 __device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], const RouteOut &o, int *cnt_l,
-                                           float *ps_l) {
+                                           float *ps_l, int *sel_l = nullptr) {
     const int lane = threadIdx.x & 63;
     const int E = o.E, k = o.k;
     float p[2];
@@ -483,6 +483,7 @@ __device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], const 
             const int64_t at = (int64_t)tok * k + rank[h];
             o.topk_idx[at] = e[h];
             o.topk_w[at] = __fdiv_rn(p[h], den);
+            if (sel_l) sel_l[at] = e[h];  // (LDS copy for a caller that goes on to the experts)
             atomicAdd(cnt_l + e[h], 1);
         }
         atomicAdd(ps_l + e[h], p[h]);
@@ -666,25 +667,83 @@ struct ExpArgs {
     const float *topk_w;           // [M*k]
 };
 
-template <typename T, typename TY, bool BF16MMA, int NHT>
-__global__ __launch_bounds__(kMoeThreads, 2) void moe_experts_kernel(ExpArgs a) {
-    __shared__ __align__(16) f32x4 lut[256];
-    __shared__ int toff[129];
-    {
-        const uint32_t byte = threadIdx.x;
+// Code byte -> its 4 ternary values as floats (the MFMA A-operand table).
+__device__ __forceinline__ void expert_lut_init(f32x4 *lut) {
+    for (uint32_t byte = threadIdx.x; byte < 256; byte += blockDim.x) {
         f32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = (float)((int)((byte >> (6 - 2 * j)) & 3u) - 1);
         lut[byte] = v;
     }
+}
+
+// One wavefront's item: expert e for up to 16 routed pairs, lane column t
+// holding pair `pair` (ok: the column is in use).  gate/up as D[hidden][pair],
+// silu(g) * u, then down; y[tok, 32e:32e+32] = expert output * routing
+// weight.  Every column is computed on its own, so a pair's result does not
+// depend on which item or column it lands in.
+template <typename T, typename TY, bool BF16MMA, int NHT>
+__device__ __forceinline__ void expert_item(const ExpArgs &a, const f32x4 *lut, __amdgpu_buffer_rsrc_t xr,
+                                            __amdgpu_buffer_rsrc_t yr, int e, int pair, bool ok) {
+    constexpr uint32_t esz = sizeof(T);
+    constexpr int nht = NHT;  // hidden tiles of 16 (H = 16 * NHT)
+    const int lane = threadIdx.x & 63, q = lane >> 4;
+    const float gg = a.gammas[0], gu = a.gammas[1], gd = a.gammas[2];
+    const int tok = pair / a.k;
+    const float wr = ok ? a.topk_w[pair] : 0.f;
+    const uint32_t xo = ok ? (uint32_t)(((int64_t)tok * a.ldx + 32 * e) * esz) : kOOB;
+    f32x4 xb[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) xb[c] = Buf4<T>::load(xr, xo == kOOB ? kOOB : xo + (uint32_t)(16 * c + 4 * q) * esz, 0);
+    // gate/up: D[hidden][pair]; lane (t, q) ends with hidden 16nt + 4q + j of pair t
+    f32x4 hb[NHT];
+    const uint8_t *gf = a.gate_f + (int64_t)e * nht * 128;
+    const uint8_t *uf = a.up_f + (int64_t)e * nht * 128;
+#pragma unroll
+    for (int nt = 0; nt < nht; ++nt) {
+        f32x4 g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            g = mma16<BF16MMA>(lut[gf[(nt * 2 + c) * 64 + lane]], xb[c], g);
+            u = mma16<BF16MMA>(lut[uf[(nt * 2 + c) * 64 + lane]], xb[c], u);
+        }
+        f32x4 h;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (BF16MMA) {
+                h[j] = bf16r(silu_f(bf16r(gg * g[j]))) * bf16r(gu * u[j]);
+            } else {
+                h[j] = silu_f(gg * g[j]) * (gu * u[j]);
+            }
+        }
+        hb[nt] = h;
+    }
+    // down: D[d][pair], 2 tiles of 16 output dims, K = H in steps of 16
+    const uint8_t *df = a.down_f + (int64_t)e * nht * 128;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < nht; ++ks) d = mma16<BF16MMA>(lut[df[(mt * nht + ks) * 64 + lane]], hb[ks], d);
+        f32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = (BF16MMA ? bf16r(gd * d[j]) : gd * d[j]) * wr;
+        Buf4<TY>::store(o, yr,
+                        xo == kOOB ? kOOB : (uint32_t)(((int64_t)tok * a.ldy + 32 * e + 16 * mt + 4 * q) * sizeof(TY)),
+                        0);
+    }
+}
+
+template <typename T, typename TY, bool BF16MMA, int NHT>
+__global__ __launch_bounds__(kMoeThreads, 2) void moe_experts_kernel(ExpArgs a) {
+    __shared__ __align__(16) f32x4 lut[256];
+    __shared__ int toff[129];
+    expert_lut_init(lut);
     for (int e = threadIdx.x; e <= a.E; e += kMoeThreads) toff[e] = a.tile_off[e];
     __syncthreads();
-    constexpr uint32_t esz = sizeof(T);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = lane & 15, q = lane >> 4;
-    constexpr int nht = NHT;                  // hidden tiles of 16 (H = 16 * NHT)
-    const float gg = a.gammas[0], gu = a.gammas[1], gd = a.gammas[2];
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const int t = lane & 15;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * sizeof(T)));
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * sizeof(TY)));
     const int total = toff[a.E];
     for (int item = blockIdx.x * kMoeWaves + wave; item < total; item += gridDim.x * kMoeWaves) {
@@ -698,50 +757,7 @@ __global__ __launch_bounds__(kMoeThreads, 2) void moe_experts_kernel(ExpArgs a) 
         const int cnt = min(16, a.count[e] - 16 * local);
         const bool ok = t < cnt;
         const int pair = ok ? a.list[a.offset[e] + 16 * local + t] : 0;
-        const int tok = pair / a.k;
-        const float wr = ok ? a.topk_w[pair] : 0.f;
-        const uint32_t xo = ok ? (uint32_t)(((int64_t)tok * a.ldx + 32 * e) * esz) : kOOB;
-        f32x4 xb[2];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) xb[c] = Buf4<T>::load(xr, xo == kOOB ? kOOB : xo + (uint32_t)(16 * c + 4 * q) * esz, 0);
-        // gate/up: D[hidden][pair]; lane (t, q) ends with hidden 16nt + 4q + j of pair t
-        f32x4 hb[NHT];
-        const uint8_t *gf = a.gate_f + (int64_t)e * nht * 128;
-        const uint8_t *uf = a.up_f + (int64_t)e * nht * 128;
-#pragma unroll
-        for (int nt = 0; nt < nht; ++nt) {
-            f32x4 g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                g = mma16<BF16MMA>(lut[gf[(nt * 2 + c) * 64 + lane]], xb[c], g);
-                u = mma16<BF16MMA>(lut[uf[(nt * 2 + c) * 64 + lane]], xb[c], u);
-            }
-            f32x4 h;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if constexpr (BF16MMA) {
-                    h[j] = bf16r(silu_f(bf16r(gg * g[j]))) * bf16r(gu * u[j]);
-                } else {
-                    h[j] = silu_f(gg * g[j]) * (gu * u[j]);
-                }
-            }
-            hb[nt] = h;
-        }
-        // down: D[d][pair], 2 tiles of 16 output dims, K = H in steps of 16
-        const uint8_t *df = a.down_f + (int64_t)e * nht * 128;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            f32x4 d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < nht; ++ks) d = mma16<BF16MMA>(lut[df[(mt * nht + ks) * 64 + lane]], hb[ks], d);
-            f32x4 o;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) o[j] = (BF16MMA ? bf16r(gd * d[j]) : gd * d[j]) * wr;
-            Buf4<TY>::store(o, yr,
-                            xo == kOOB ? kOOB
-                                       : (uint32_t)(((int64_t)tok * a.ldy + 32 * e + 16 * mt + 4 * q) * sizeof(TY)),
-                            0);
-        }
+        expert_item<T, TY, BF16MMA, NHT>(a, lut, xr, yr, e, pair, ok);
     }
 }
 
@@ -1048,12 +1064,10 @@ static int grid_cap(int64_t waves_needed, int64_t limit = 0) {
 // their outputs, with SiLU on the rounded first product.
 constexpr int kR1Waves = 8;
 constexpr int kR1SmallRows = 256;  // row counts up to this take the split-K kernel
-__global__ __launch_bounds__(64 * kR1Waves) void router_w1_small_kernel(const uint16_t *__restrict__ x, int64_t ldx,
-                                                                        int M, int C, const uint16_t *__restrict__ w1,
-                                                                        uint16_t *__restrict__ h, int64_t ldh,
-                                                                        const uint16_t *__restrict__ w2, int E,
-                                                                        float *__restrict__ lpart) {
-    __shared__ f32x4 part[kR1Waves][64];
+__device__ __forceinline__ void router_w1_small_body(const uint16_t *__restrict__ x, int64_t ldx, int M, int C,
+                                                     const uint16_t *__restrict__ w1, uint16_t *__restrict__ h,
+                                                     int64_t ldh, const uint16_t *__restrict__ w2, int E,
+                                                     float *__restrict__ lpart, f32x4 (*part)[64]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, fr = lane & 15, fq = lane >> 4;
     const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16, H = gridDim.x * 16;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)((int64_t)M * ldx * 2));
@@ -1089,7 +1103,7 @@ __global__ __launch_bounds__(64 * kR1Waves) void router_w1_small_kernel(const ui
     }
     part[wave][lane] = acc;
     __syncthreads();
-    if (wave) return;
+    if (wave) return;  // waves 1.. leave the body here; wave 0 finishes it
     f32x4 v = part[0][lane];
 #pragma unroll
     for (int w = 1; w < kR1Waves; ++w) v = v + part[w][lane];
@@ -1113,6 +1127,15 @@ __global__ __launch_bounds__(64 * kR1Waves) void router_w1_small_kernel(const ui
         const int e0 = 16 * et + 4 * fq;
         Buf4<float>::store(d, pr, (row_ok && e0 < E) ? (uint32_t)(((int64_t)(m0 + fr) * E + e0) * 4) : kOOB, 0);
     }
+}
+
+__global__ __launch_bounds__(64 * kR1Waves) void router_w1_small_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                                        int M, int C, const uint16_t *__restrict__ w1,
+                                                                        uint16_t *__restrict__ h, int64_t ldh,
+                                                                        const uint16_t *__restrict__ w2, int E,
+                                                                        float *__restrict__ lpart) {
+    __shared__ f32x4 part[kR1Waves][64];
+    router_w1_small_body(x, ldx, M, C, w1, h, ldh, w2, E, lpart, part);
 }
 
 // Few rows: logits = the H/16 partial sums of router_w1_small_kernel added
@@ -1268,6 +1291,118 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
         }
     }
     part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
+}
+
+// ------------------------------------------------------------------ decode-sized MoE
+// The whole HadamardMoE.forward (moe.py:512-542) of a wide model for a few
+// tokens (decode) in one launch.  The H/16 workgroups of
+// router_w1_small_kernel compute the router's hidden units and their shares
+// of the logits; each then counts itself done on a counter, and the last one
+// (release / acquire fences at device scope around the count) adds the
+// partial logits in router_topk_part_kernel's order, routes every token
+// (rank_token), lists the routed pairs by expert and runs the experts
+// (expert_item, one wavefront per expert), so every output is bitwise the
+// four-launch path's.  The counter is the caller's and starts at zero; the
+// last workgroup sets it back to zero.
+constexpr int kDecTok = 4;                       // tokens a launch takes
+constexpr int kDecPairs = kDecTok * kMaxK;       // routed pairs at most
+
+template <typename TY, int NHT>
+__global__ __launch_bounds__(64 * kR1Waves) void moe_decode_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                                   int C, const uint16_t *__restrict__ w1,
+                                                                   uint16_t *__restrict__ h,
+                                                                   const uint16_t *__restrict__ w2,
+                                                                   float *__restrict__ lpart, RouteOut o, ExpArgs ex,
+                                                                   unsigned *__restrict__ sync) {
+    __shared__ f32x4 part[kR1Waves][64];
+    __shared__ int cnt_l[kDecTok][kMaxE];
+    __shared__ float ps_l[kDecTok][kMaxE];
+    __shared__ __align__(16) f32x4 lut[256];
+    __shared__ int item_e[kDecPairs], item_n[kDecPairs], item_p[kDecPairs][kDecTok];
+    __shared__ int sel_l[kDecPairs];
+    __shared__ int n_items;
+    __shared__ int last;
+    const int M = o.M, E = o.E, H = (int)gridDim.x * 16;
+    router_w1_small_body(x, ldx, M, C, w1, h, H, w2, E, lpart, part);
+    __syncthreads();  // this workgroup's partial logits are stored
+    if (threadIdx.x == 0) {
+        __threadfence();  // release: the partials before the count
+        last = atomicAdd(sync, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();  // acquire: every workgroup's partials are visible
+    for (int i = threadIdx.x; i < kDecTok * kMaxE; i += blockDim.x) {
+        cnt_l[i / kMaxE][i % kMaxE] = 0;
+        ps_l[i / kMaxE][i % kMaxE] = 0.f;
+    }
+    for (int i = threadIdx.x; i < kDecPairs; i += blockDim.x) sel_l[i] = -1;  // slots no token fills stay -1
+    expert_lut_init(lut);
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nparts = (int)gridDim.x;  // H / 16 <= kTopkPartMax
+    if (wave < M) {
+        // the partial logits added as router_topk_part_kernel adds them:
+        // groups of 16 partials (zeros past nparts) in order, then the 4
+        // group sums in order; all 64 loads of an expert in flight together
+        const int tok = wave;
+        const __amdgpu_buffer_rsrc_t pr = make_rsrc(lpart, (uint32_t)((int64_t)nparts * M * E * 4));
+        float lg[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int e = lane + 64 * hh;
+            float pv[kTopkPartMax];
+#pragma unroll
+            for (int j = 0; j < kTopkPartMax; ++j)
+                pv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    pr, (e < E && j < nparts) ? (uint32_t)((((int64_t)j * M + tok) * E + e) * 4) : kOOB, 0, 0));
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < kTopkPartMax / 16; ++w) {
+                float acc = 0.f;
+#pragma unroll
+                for (int u = 0; u < 16; ++u) acc += pv[16 * w + u];
+                v += acc;
+            }
+            lg[hh] = e < E ? bf16r(v) : -INFINITY;
+        }
+        rank_token(tok, lg, o, cnt_l[tok], ps_l[tok], sel_l);
+    }
+    __syncthreads();  // routing outputs and the LDS rows are complete
+    // partial-count rows: row t holds token t's counts and probabilities (as
+    // router_topk_part_kernel's workgroup per token writes them), rows past
+    // M zero
+    for (int i = threadIdx.x; i < o.n_part * E; i += blockDim.x) {
+        const int r = i / E, e = i % E;
+        o.count[i] = r < M ? cnt_l[r][e] : 0;
+        o.probsum[i] = r < M ? ps_l[r][e] : 0.f;
+    }
+    if (threadIdx.x == 0) {
+        // the routed pairs grouped by expert, in pair order (at most kDecPairs)
+        int n = 0;
+        for (int p = 0; p < M * o.k; ++p) {
+            const int e = sel_l[p];
+            if (e < 0 || e >= E) continue;  // (probabilities that are not numbers select fewer than k)
+            int i = 0;
+            while (i < n && item_e[i] != e) ++i;
+            if (i == n) {
+                item_e[n] = e;
+                item_n[n] = 0;
+                ++n;
+            }
+            item_p[i][item_n[i]++] = p;
+        }
+        n_items = n;
+    }
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(ex.x, (uint32_t)((int64_t)ex.M * ex.ldx * 2));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(ex.y, (uint32_t)((int64_t)ex.M * ex.ldy * sizeof(TY)));
+    const int t = lane & 15;
+    for (int i = wave; i < n_items; i += kR1Waves) {
+        const bool ok = t < item_n[i];
+        expert_item<uint16_t, TY, true, NHT>(ex, lut, xr, yr, item_e[i], ok ? item_p[i][t] : 0, ok);
+    }
+    if (threadIdx.x == 0) *sync = 0u;  // no other workgroup of this launch reads it any more
 }
 
 // ------------------------------------------------------------------ experts backward
@@ -1580,6 +1715,74 @@ WALSH_EXPORT int walsh_moe_router_wide_fwd(const void *x, int64_t ldx, int64_t M
     const int64_t tiles = ceil_div(M, 64), grid = tiles < n_part ? tiles : n_part;
     launch(router_w2_topk_kernel<4>, dim3((unsigned)grid), dim3(64 * kR2Waves), (uint32_t)router_w2_lds_bytes((int)H, 4),
            s, (const uint16_t *)h, (int64_t)H, (int)H, (const uint16_t *)w2, o);
+    return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int64_t walsh_moe_decode_workspace_bytes(int64_t M, int64_t H, int64_t E) {
+    if (M < 1 || M > kDecTok || H <= 0 || E <= 0) return 0;
+    return router_h_bytes(M, H) + (H / 16) * M * E * 4;
+}
+
+WALSH_EXPORT int walsh_moe_decode_fwd(const void *x, int64_t ldx, int64_t M, int64_t C, int64_t H, const void *w1,
+                                      const void *w2, int64_t E, int64_t k, int64_t He, const uint8_t *gate_frag,
+                                      const uint8_t *up_frag, const uint8_t *down_frag, const float *gammas,
+                                      void *work, int64_t work_bytes, unsigned *sync, float *probs, float *mask,
+                                      float *weights_dense, int *topk_idx, float *topk_w, int *count,
+                                      float *probsum, int64_t n_part, void *y, int64_t ldy, int ydtype,
+                                      void *stream) {
+    const char *fn = "walsh_moe_decode_fwd";
+    int rc = route_out_check(fn, M, E, k, topk_idx, topk_w, count, probsum, n_part);
+    if (rc) return rc;
+    if (!x || !w1 || !w2 || !gate_frag || !up_frag || !down_frag || !gammas || !work || !sync || !y)
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (M < 1 || M > kDecTok)
+        return set_error(WALSH_ENOTSUP, "%s: takes 1..%d tokens (M=%lld)", fn, kDecTok, (long long)M);
+    if (C % (32 * kR1Waves) || H % 128 || H > kR2MaxH || E % 4 || C != 32 * E || ldx < C || ldy < 32 * E)
+        return set_error(WALSH_ENOTSUP, "%s: needs C %% %d == 0, H %% 128 == 0, H <= %d, E %% 4 == 0, C == 32 E "
+                         "(C=%lld H=%lld E=%lld)", fn, 32 * kR1Waves, kR2MaxH, (long long)C, (long long)H,
+                         (long long)E);
+    if (He != 64 && He != 128 && He != 256)
+        return set_error(WALSH_ENOTSUP, "%s: expert hidden must be 64, 128 or 256", fn);
+    if (work_bytes < walsh_moe_decode_workspace_bytes(M, H, E))
+        return set_error(WALSH_EINVAL, "%s: workspace of %lld bytes, needs %lld", fn, (long long)work_bytes,
+                         (long long)walsh_moe_decode_workspace_bytes(M, H, E));
+    if (ydtype != WALSH_F32 && ydtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: ydtype", fn);
+    const int64_t ysz = ydtype == WALSH_BF16 ? 2 : 4;
+    if (ldx % 8 || (uintptr_t)x % 16 || (uintptr_t)work % 256 || (uintptr_t)w1 % 16 || (uintptr_t)w2 % 16 ||
+        (uintptr_t)y % 16 || ldy % (16 / ysz) || (uintptr_t)sync % 4)
+        return set_error(WALSH_ENOTSUP, "%s: operands and rows must be 16-byte aligned (workspace 256)", fn);
+    if (H * C * 2 > (int64_t)kMaxBufferBytes) return set_error(WALSH_ENOTSUP, "%s: W1 above 2^31 bytes", fn);
+    uint16_t *h = (uint16_t *)work;
+    float *lpart = (float *)((char *)work + router_h_bytes(M, H));
+    const RouteOut o{(int)M, (int)E, (int)k, probs, mask, weights_dense, topk_idx, topk_w, count, probsum,
+                     (int)n_part, y, ldy, ydtype == WALSH_BF16};
+    ExpArgs a{};
+    a.x = x;
+    a.ldx = ldx;
+    a.y = y;
+    a.ldy = ldy;
+    a.M = (int)M;
+    a.E = (int)E;
+    a.k = (int)k;
+    a.H = (int)He;
+    a.gate_f = gate_frag;
+    a.up_f = up_frag;
+    a.down_f = down_frag;
+    a.gammas = gammas;
+    a.topk_w = topk_w;
+    const dim3 G((unsigned)(H / 16)), B(64 * kR1Waves);
+    hipStream_t s = (hipStream_t)stream;
+#define WALSH_DEC_LAUNCH(NH)                                                                                      \
+    if (ydtype == WALSH_BF16)                                                                                     \
+        launch((moe_decode_kernel<uint16_t, NH>), G, B, 0, s, (const uint16_t *)x, ldx, (int)C,                 \
+               (const uint16_t *)w1, h, (const uint16_t *)w2, lpart, o, a, sync);                                 \
+    else                                                                                                          \
+        launch((moe_decode_kernel<float, NH>), G, B, 0, s, (const uint16_t *)x, ldx, (int)C, (const uint16_t *)w1, \
+               h, (const uint16_t *)w2, lpart, o, a, sync);
+    if (He == 64) { WALSH_DEC_LAUNCH(4) }
+    else if (He == 128) { WALSH_DEC_LAUNCH(8) }
+    else { WALSH_DEC_LAUNCH(16) }
+#undef WALSH_DEC_LAUNCH
     return check_hip(hipGetLastError(), fn);
 }
 

@@ -97,6 +97,11 @@ SIGNATURES = {
     "walsh_moe_router_wide_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "walsh_moe_router_wide_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P,
                                        _P, _P, _I64, _P, _I64, _I, _P]),
+    "walsh_moe_decode_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    # x ldx M C H w1 w2 E k He gate up down gammas work work_bytes sync probs mask weights idx w count probsum
+    # n_part y ldy ydtype stream
+    "walsh_moe_decode_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P,
+                                  _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I, _P]),
     "walsh_moe_experts_bwd_workspace_bytes": (_I64, [_I64, _I64]),
     "walsh_moe_experts_bwd": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                                    _P, _P, _P, _P, _P, _I64, _P]),

@@ -1211,6 +1211,48 @@ def moe_router_wide(x2d: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, E: in
     return r
 
 
+MOE_DECODE_MAX_TOKENS = 4
+
+
+def moe_decode_supported(x2d: torch.Tensor, H: int, E: int, k: int, He: int, y: torch.Tensor) -> bool:
+    """Whether walsh_moe_decode_fwd takes this MoE call: 1..4 tokens of a bf16
+    wide model (the wide router's shapes with C == 32 E), expert hidden 64 /
+    128 / 256, y with 16-byte-aligned rows."""
+    M = x2d.shape[0] if x2d.dim() == 2 else 0
+    return (1 <= M <= MOE_DECODE_MAX_TOKENS and x2d.shape[1] == 32 * E and He in (64, 128, 256)
+            and moe_router_wide_supported(x2d, H, E, k) and y.is_cuda and y.dim() == 2 and y.stride(-1) == 1
+            and y.dtype in (torch.bfloat16, torch.float32) and y.data_ptr() % 16 == 0
+            and y.stride(0) % (16 // y.element_size()) == 0)
+
+
+def moe_decode(x2d: torch.Tensor, y: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, E: int, k: int, frags,
+               gammas: torch.Tensor, He: int, sync: torch.Tensor, dense: bool = False) -> MoERoute:
+    """HadamardMoE.forward (moe.py:512-542) for a few tokens in one launch:
+    routing (as moe_router_wide) and the routed experts (as moe_scatter +
+    moe_experts) into y [M, 32E], bitwise their result.  sync: a one-element
+    int32 device tensor that starts at zero (the kernel leaves it at zero);
+    calls sharing it must not overlap."""
+    _hip.require_device(x2d, "input")
+    assert moe_decode_supported(x2d, w1.shape[0], E, k, He, y), "moe_decode shape"
+    assert w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16 and w1.is_contiguous() and w2.is_contiguous()
+    assert sync.dtype == torch.int32 and sync.numel() >= 1 and sync.device == x2d.device
+    M, C = x2d.shape
+    H = w1.shape[0]
+    r = MoERoute(M, E, k, x2d.device, dense, M)  # one partial row per token
+    nws = _hip.lib().walsh_moe_decode_workspace_bytes(M, H, E)
+    work = torch.empty(max(nws, 256), device=x2d.device, dtype=torch.uint8)
+    gf, uf, df = frags
+    g = gammas.detach().float().contiguous()
+    nbytes = M * C * 2 + (H * C + E * H) * 2 + M * C * y.element_size() + M * k * 8 + 3 * E * He * 8
+    _hip.call("walsh_moe_decode_fwd", x2d.data_ptr(), x2d.stride(0), M, C, H, w1.data_ptr(), w2.data_ptr(), E, k, He,
+              gf.data_ptr(), uf.data_ptr(), df.data_ptr(), g.data_ptr(), work.data_ptr(), work.numel(),
+              sync.data_ptr(), _hip.ptr(r.probs), _hip.ptr(r.mask), _hip.ptr(r.weights), r.topk_idx.data_ptr(),
+              r.topk_w.data_ptr(), r.count_part.data_ptr(), r.probsum_part.data_ptr(), r.parts, y.data_ptr(),
+              y.stride(0), _hip.dtype_code(y.dtype), _hip.stream(x2d.device), kernel="moe_decode<bf16>",
+              nbytes=nbytes, flops=2 * M * (C * H + H * E) + 2 * M * k * 3 * 32 * He)
+    return r
+
+
 def moe_topk(logits: torch.Tensor, k: int, dense: bool = False) -> MoERoute:
     """Softmax / top-k / renormalisation (moe.py:432-445) on float32 logits [M, E]."""
     _hip.require_device(logits, "logits")

@@ -384,9 +384,11 @@ class HadamardMoE(nn.Module):
             g, frags = self._ffn_state()
             r = kernels.moe_ffn(x2d, y, frags, g, self.n_experts, self.router.top_k, ex.hidden)
         else:
-            r = self.router.route(x2d, y2d=y)
-            if M:
-                ex.routed(x2d, r, y)
+            r = self._decode(x2d, y) if self.use_fused else None
+            if r is None:
+                r = self.router.route(x2d, y2d=y)
+                if M:
+                    ex.routed(x2d, r, y)
         self._route, self._route_shape = r, (B, T)
         self._aux_value = self._mask_value = None
         if self.training:
@@ -395,7 +397,27 @@ class HadamardMoE(nn.Module):
                 self._total_tokens += M
         return y.view(B, T, C)
 
-    use_fused = True   # single-launch kernel where supported (tests switch it off to compare paths)
+    use_fused = True   # single-launch kernels where supported (tests switch it off to compare paths)
+
+    def _decode(self, x2d: torch.Tensor, y: torch.Tensor) -> Optional["kernels.MoERoute"]:
+        """A few tokens of a wide bf16 model (decode): router, routing and the
+        routed experts in one launch (walsh_moe_decode_fwd); None where that
+        kernel does not apply."""
+        rt, ex = self.router, self.experts
+        w1, w2 = rt.gate[0].weight, rt.gate[2].weight
+        if not kernels.moe_decode_supported(x2d, w1.shape[0], self.n_experts, rt.top_k, ex.hidden, y):
+            return None
+        w1c, w2c = rt._frag.get((w1, w2), lambda: (w1.detach().to(x2d.dtype).contiguous(),
+                                                   w2.detach().to(x2d.dtype).contiguous()),
+                                extra=(x2d.dtype, "gemm"))
+        gammas, frags = ex.ternary_state(x2d.dtype)
+        sync = self._decode_sync
+        if sync is None or sync.device != x2d.device:
+            # the kernel's completion counter: zero once, left at zero by every call
+            sync = self._decode_sync = torch.zeros(1, device=x2d.device, dtype=torch.int32)
+        return kernels.moe_decode(x2d, y, w1c, w2c, self.n_experts, rt.top_k, frags, gammas, ex.hidden, sync)
+
+    _decode_sync = None
 
     def _forward_autograd(self, x: torch.Tensor, out_dtype: Optional[torch.dtype]) -> torch.Tensor:
         """Training form (moe.py:512-542): differentiable routing, the
