@@ -66,42 +66,77 @@ __device__ __forceinline__ float quad_sum(float v) {
 // output o of this token.  Column sums of the Sinkhorn iteration are quad
 // shuffles; each lane divides its own row, so a whole wavefront projects 16
 // tokens at once.  Results go to hpre_lds[t*4 + r] and (if tok valid) global.
+// In two parts: the gates (H_pre, H_post and exp of the residual logits),
+// then the Sinkhorn iterations and the stores, so that a caller can publish
+// H_pre before running the iterations.
+struct QuadGates {
+    float pre, post;
+    float m[kMaxStreams];
+};
+
+template <typename DynF>
+__device__ __forceinline__ QuadGates token_gates_quad(int r, int n, const float *coef, const float *bias, DynF dynf) {
+    const bool act = r < n;
+    QuadGates q;
+    q.pre = 0.f;
+    q.post = 0.f;
+    if (act) {
+        q.pre = __builtin_amdgcn_rcpf(1.0f + __expf(-(coef[0] * dynf(r) + bias[r])));
+        q.post = 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(-(coef[1] * dynf(n + r) + bias[n + r])));
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxStreams; ++j)
+        q.m[j] = (act && j < n) ? __expf(coef[2] * dynf(2 * n + r * n + j) + bias[2 * n + r * n + j]) : 0.f;
+    return q;
+}
+
+// One Sinkhorn iteration on a quad: column sums by quad shuffles, then the
+// lane's own row.
+__device__ __forceinline__ void sinkhorn_quad_step(float (&m)[kMaxStreams], int n, float sk_eps) {
+#pragma unroll
+    for (int j = 0; j < kMaxStreams; ++j) {
+        const float cs = quad_sum(m[j]);
+        if (j < n) m[j] *= __builtin_amdgcn_rcpf(cs + sk_eps);
+    }
+    float rs = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxStreams; ++j) rs += (j < n) ? m[j] : 0.f;
+    const float rd = __builtin_amdgcn_rcpf(rs + sk_eps);
+#pragma unroll
+    for (int j = 0; j < kMaxStreams; ++j)
+        if (j < n) m[j] *= rd;
+}
+
+__device__ __forceinline__ void token_store_quad(const QuadGates &q, int r, int tok, int M, int n, float *h_pre,
+                                                 float *h_post, float *h_res) {
+    if (r < n && tok < M) {
+        h_pre[(int64_t)tok * n + r] = q.pre;
+        h_post[(int64_t)tok * n + r] = q.post;
+#pragma unroll
+        for (int j = 0; j < kMaxStreams; ++j)
+            if (j < n) h_res[((int64_t)tok * n + r) * n + j] = q.m[j];
+    }
+}
+
+__device__ __forceinline__ void token_sinkhorn_quad(QuadGates &q, int r, int tok, int M, int n, int n_iter,
+                                                    float sk_eps, float *h_pre, float *h_post, float *h_res) {
+    for (int it = 0; it < n_iter; ++it) sinkhorn_quad_step(q.m, n, sk_eps);
+    token_store_quad(q, r, tok, M, n, h_pre, h_post, h_res);
+}
+
+// v of quad lane S, broadcast to the quad (DPP quad_perm [S, S, S, S]).
+template <int S>
+__device__ __forceinline__ float quad_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), S * 0x55, 0xF, 0xF, true));
+}
+
 template <typename DynF>
 __device__ __forceinline__ void token_constraints_quad(int t, int r, int tok, int M, int n, const float *coef,
                                                        const float *bias, int n_iter, float sk_eps, DynF dynf,
                                                        float *hpre_lds, float *h_pre, float *h_post, float *h_res) {
-    const bool act = r < n;
-    float pre = 0.f, post = 0.f;
-    if (act) {
-        pre = __builtin_amdgcn_rcpf(1.0f + __expf(-(coef[0] * dynf(r) + bias[r])));
-        post = 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(-(coef[1] * dynf(n + r) + bias[n + r])));
-    }
-    float m[kMaxStreams];
-#pragma unroll
-    for (int j = 0; j < kMaxStreams; ++j)
-        m[j] = (act && j < n) ? __expf(coef[2] * dynf(2 * n + r * n + j) + bias[2 * n + r * n + j]) : 0.f;
-    for (int it = 0; it < n_iter; ++it) {
-#pragma unroll
-        for (int j = 0; j < kMaxStreams; ++j) {
-            const float cs = quad_sum(m[j]);
-            if (j < n) m[j] *= __builtin_amdgcn_rcpf(cs + sk_eps);
-        }
-        float rs = 0.f;
-#pragma unroll
-        for (int j = 0; j < kMaxStreams; ++j) rs += (j < n) ? m[j] : 0.f;
-        const float rd = __builtin_amdgcn_rcpf(rs + sk_eps);
-#pragma unroll
-        for (int j = 0; j < kMaxStreams; ++j)
-            if (j < n) m[j] *= rd;
-    }
-    hpre_lds[t * 4 + r] = pre;
-    if (act && tok < M) {
-        h_pre[(int64_t)tok * n + r] = pre;
-        h_post[(int64_t)tok * n + r] = post;
-#pragma unroll
-        for (int j = 0; j < kMaxStreams; ++j)
-            if (j < n) h_res[((int64_t)tok * n + r) * n + j] = m[j];
-    }
+    QuadGates q = token_gates_quad(r, n, coef, bias, dynf);
+    hpre_lds[t * 4 + r] = q.pre;
+    token_sinkhorn_quad(q, r, tok, M, n, n_iter, sk_eps, h_pre, h_post, h_res);
 }
 
 // ---------------------------------------------------------------- sinkhorn
@@ -601,12 +636,13 @@ struct Pre2Args {
 constexpr int kTileBytes = 128 * 1024;
 constexpr int kPostItems = 4;             // POST: (token, 16-byte column chunk) items per thread per round
 
-template <typename T, bool BF16MMA, int MT, bool POST = false>
+// FAST: n = 4 streams of C = 512 (n_embd 512), as compile-time constants.
+template <typename T, bool BF16MMA, int MT, bool POST = false, bool FAST = false>
 __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     constexpr int TT = 16 * MT;
     constexpr uint32_t esz = sizeof(T);
     extern __shared__ __align__(16) unsigned char smem[];
-    const int n = a.n, C = a.C, K = n * C;
+    const int n = FAST ? 4 : a.n, C = FAST ? 512 : a.C, K = n * C;
     const int rowb = K * (int)esz;
     const int stride = rowb + 8;              // 8-byte pad: 16 rows of a fragment read hit distinct banks
     unsigned char *xs = smem;                 // [TT][stride]
@@ -642,16 +678,26 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
                     dst[u][nt] = Buf4<T>::load(pr, off, 0);
             }
     };
-    constexpr int kTpt = kPreThreads / TT;    // threads per token in phase 3
-    constexpr int kMaxQ = 1024 / 4 / kTpt;    // C <= 1024
-    // the norm weights (or ones) go to LDS with the tile
-    for (int c4 = tid; c4 < C / 4; c4 += kPreThreads)
-        nw_l[c4] = a.norm_w ? *(const f32x4 *)(a.norm_w + 4 * c4) : f32x4{1.f, 1.f, 1.f, 1.f};
+    // the norm weights (or ones), coef and bias go to LDS with the tile; they
+    // are requested before the tile (C / 4 <= kPreThreads) and written once
+    // it is in flight, so waiting for them does not wait for the tile
+    static_assert(1024 / 4 <= kPreThreads, "one norm-weight quad per thread");
+    const f32x4 nwv = (tid < C / 4 && a.norm_w) ? *(const f32x4 *)(a.norm_w + 4 * tid) : f32x4{1.f, 1.f, 1.f, 1.f};
+    float *cb_l = (float *)(nw_l + C / 4);    // [3 coef][2n + n*n bias]
+    const int ncb = 3 + 2 * n + n * n;
+    const float cbv = tid < ncb ? (tid < 3 ? a.coef[tid] : a.bias[tid - 3]) : 0.f;
+    auto put_small = [&]() {
+        if (tid < C / 4) nw_l[tid] = nwv;
+        if (tid < ncb) cb_l[tid] = cbv;
+    };
 
     // phase 0 (POST): the stream update of the previous layer, formed per
     // (token, 16-byte column chunk) from the n old stream chunks and the
     // layer output chunk, in mhc_post_kernel's operation order (so x_new is
     // bitwise what that kernel writes); rounded to T, kept in LDS, stored.
+    // The stores drain behind this phase's arithmetic (5 multiply-adds per
+    // value) and the projection's first phi batch, which was requested
+    // before them.
     if constexpr (POST) {
         const int cpc = C * (int)esz / 16;    // chunks per stream row
         const int nit = TT * cpc;
@@ -676,15 +722,26 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
                     orr, ok ? (uint32_t)((int64_t)(tok0 + r) * a.ld_out * esz + cc * 16) : kOOB, 0, 0);
             }
         };
-        load_round(0);
-        for (int e = tid; e < TT * nh; e += kPreThreads) {
+        // the previous H_res / H_post rows of the tile are requested first, so
+        // the barrier waits for them alone and each item below waits only for
+        // its own loads
+        constexpr int kMaxH = (TT * (kMaxStreams * kMaxStreams + kMaxStreams) + kPreThreads - 1) / kPreThreads;
+        float hv[kMaxH];
+#pragma unroll
+        for (int i = 0; i < kMaxH; ++i) {
+            const int e = tid + i * kPreThreads;
             const int r = e / nh, k = e - r * nh;
-            const bool ok = tok0 + r < a.M;
-            hprev[e] = !ok ? 0.f : k < n * n ? a.hr_prev[(int64_t)(tok0 + r) * n * n + k]
-                                             : a.hp_prev[(int64_t)(tok0 + r) * n + (k - n * n)];
+            const bool ok = e < TT * nh && tok0 + r < a.M;
+            hv[i] = !ok ? 0.f : k < n * n ? a.hr_prev[(int64_t)(tok0 + r) * n * n + k]
+                                          : a.hp_prev[(int64_t)(tok0 + r) * n + (k - n * n)];
         }
+        load_round(0);
         load_phi(ks0, pa);
-        __syncthreads();
+        put_small();
+#pragma unroll
+        for (int i = 0; i < kMaxH; ++i)
+            if (tid + i * kPreThreads < TT * nh) hprev[tid + i * kPreThreads] = hv[i];
+        lds_barrier();
         constexpr int VE = 16 / (int)esz;     // values per chunk: 8 bf16 or 4 f32
         for (int it0 = 0; it0 < nit; it0 += kPostItems * kPreThreads) {
             if (it0) load_round(it0);
@@ -762,6 +819,7 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
                 xr, ok ? (uint32_t)(((int64_t)(tok0 + r) * a.ldx) * esz + cc * 16) : kOOB, 0, 0);
         }
         load_phi(ks0, pa);
+        put_small();
 #pragma unroll
         for (int j = 0; j < kMaxPer; ++j) {
             const int ch = tid + j * kPreThreads;
@@ -773,7 +831,8 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
             }
         }
     }
-    __syncthreads();
+    // LDS only: the x_new stores (POST) and the first phi batch stay in flight
+    lds_barrier();
 
     // phase 1: projection on matrix cores, K split over the 4 wavefronts
     f32x4 acc[MT][2], accss[MT];
@@ -849,77 +908,92 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
             for (int j = 0; j < 4; ++j)
                 part[(wave * TT + 16 * mt + 4 * kq + j) * (kPhiRows + 1) + 16 * nt + m] = acc[mt][nt][j];
     }
-    __syncthreads();
+    lds_barrier();
 
-    // phase 2: per-token constraints, 4 lanes per token
-    if (tid < 4 * TT) {
-        const int t = tid >> 2, r = tid & 3;
+    // phases 2 and 3, one group of 4 tokens per wavefront: lane l serves
+    // token t = 4 wave + l / 16.
+    //   constraints: each quad of the token's 16 lanes runs them (lane row
+    //     r = l % 4); the four quads compute the same values, the first stores.
+    //   layer_in = sum_s H_pre[s] x[s, :]: 16 lanes per token, 4 values per
+    //     item (H_pre from the lane's quad), optionally RMS-normalised over
+    //     the row with weight norm_w.
+    // The Sinkhorn iterations, a dependent chain of quad shuffles and
+    // reciprocals, are interleaved with the layer_in items, one item per
+    // iteration, so that the items' arithmetic fills the chain's latency.
+    static_assert(MT == 1, "one 16-token tile: 4 wavefronts x 4 tokens");
+    {
+        const int gt = 4 * wave + (lane >> 4), gr = lane & 3, sub = lane & 15;
         float ssum = 0.f;
 #pragma unroll
-        for (int w = 0; w < kPreWaves; ++w) ssum += ssp[w * TT + t];
+        for (int w = 0; w < kPreWaves; ++w) ssum += ssp[w * TT + gt];
         const float rs = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(ssum, (float)K) + a.rms_eps));
         auto dynf = [&](int o) {
             float s = 0.f;
 #pragma unroll
-            for (int w = 0; w < kPreWaves; ++w) s += part[(w * TT + t) * (kPhiRows + 1) + o];
+            for (int w = 0; w < kPreWaves; ++w) s += part[(w * TT + gt) * (kPhiRows + 1) + o];
             return s * rs;
         };
-        token_constraints_quad(t, r, tok0 + t, a.M, n, a.coef, a.bias, a.n_iter, a.sk_eps, dynf, hpre, a.h_pre,
-                               a.h_post, a.h_res);
-    }
-    __syncthreads();
-
-    // phase 3: layer_in = sum_s H_pre[s] x[s, :] (kTpt threads per token, 4
-    // values per item), optional RMS normalisation over the row with weight norm_w
-    {
-        const int tt = tid / kTpt, sub = tid % kTpt;
-        const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
-        const int tok = tok0 + tt;
+        QuadGates gq = token_gates_quad(gr, n, cb_l, cb_l + 3, dynf);
+        const float hp[kMaxStreams] = {quad_bcast<0>(gq.pre), quad_bcast<1>(gq.pre), quad_bcast<2>(gq.pre),
+                                       quad_bcast<3>(gq.pre)};
+        constexpr int KQ = FAST ? 8 : 1024 / 4 / 16;   // items per lane (C <= 1024)
         const int nq = C / 4;
-        f32x4 v[kMaxQ];
+        f32x4 v[KQ];
         float sq = 0.f;
-        float hp[kMaxStreams];
 #pragma unroll
-        for (int s = 0; s < kMaxStreams; ++s) hp[s] = hpre[tt * 4 + s];
+        for (int j = 0; j < KQ; ++j) {
+            {
+                float mn[kMaxStreams];
 #pragma unroll
-        for (int j = 0; j < kMaxQ; ++j) {
-            const int q = sub + kTpt * j;
-            f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
-            if (q < nq) {
+                for (int i = 0; i < kMaxStreams; ++i) mn[i] = gq.m[i];
+                sinkhorn_quad_step(mn, n, a.sk_eps);
+                const bool live = j < a.n_iter;
 #pragma unroll
-                for (int s = 0; s < kMaxStreams; ++s) {
-                    if (s >= n) continue;
-                    const unsigned char *src = xs + tt * stride + (s * C + 4 * q) * esz;
-                    f32x4 xv;
-                    if constexpr (sizeof(T) == 2) {
-                        const u32x2 u2 = *(const u32x2 *)src;
-                        xv.x = __uint_as_float(u2.x << 16);
-                        xv.y = __uint_as_float(u2.x & 0xffff0000u);
-                        xv.z = __uint_as_float(u2.y << 16);
-                        xv.w = __uint_as_float(u2.y & 0xffff0000u);
-                    } else {
-                        const u32x2 lo = *(const u32x2 *)src, hi = *(const u32x2 *)(src + 8);
-                        xv = __builtin_bit_cast(f32x4, u32x4{lo.x, lo.y, hi.x, hi.y});
-                    }
-                    acc4 += hp[s] * xv;
-                }
+                for (int i = 0; i < kMaxStreams; ++i) gq.m[i] = live ? mn[i] : gq.m[i];
             }
+            const int q = sub + 16 * j;
+            const bool qok = q < nq;
+            const int qc = qok ? q : 0;
+            f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < kMaxStreams; ++s) {
+                if (s >= n) continue;
+                const unsigned char *src = xs + gt * stride + (s * C + 4 * qc) * esz;
+                f32x4 xv;
+                if constexpr (sizeof(T) == 2) {
+                    const u32x2 u2 = *(const u32x2 *)src;
+                    xv.x = __uint_as_float(u2.x << 16);
+                    xv.y = __uint_as_float(u2.x & 0xffff0000u);
+                    xv.z = __uint_as_float(u2.y << 16);
+                    xv.w = __uint_as_float(u2.y & 0xffff0000u);
+                } else {
+                    const u32x2 lo = *(const u32x2 *)src, hi = *(const u32x2 *)(src + 8);
+                    xv = __builtin_bit_cast(f32x4, u32x4{lo.x, lo.y, hi.x, hi.y});
+                }
+                acc4 += hp[s] * xv;
+            }
+            if (!qok) acc4 = f32x4{0.f, 0.f, 0.f, 0.f};
             v[j] = acc4;
             sq += acc4.x * acc4.x + acc4.y * acc4.y + acc4.z * acc4.z + acc4.w * acc4.w;
         }
+        for (int it = KQ; it < a.n_iter; ++it) sinkhorn_quad_step(gq.m, n, a.sk_eps);
+        if (((lane >> 2) & 3) == 0)
+            token_store_quad(gq, gr, tok0 + gt, a.M, n, a.h_pre, a.h_post, a.h_res);
+
         float scale = 1.f;
         if (a.norm_w) {
 #pragma unroll
-            for (int sh = 1; sh < kTpt; sh <<= 1) sq += __shfl_xor(sq, sh);
+            for (int sh = 1; sh < 16; sh <<= 1) sq += __shfl_xor(sq, sh);
             scale = 1.0f / sqrtf(__fdiv_rn(sq, (float)C) + a.norm_eps);
         }
+        const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
+        const int tok = tok0 + gt;
         const bool ok = tok < a.M;
 #pragma unroll
-        for (int j = 0; j < kMaxQ; ++j) {
-            const int q = sub + kTpt * j;
-            if (q >= nq) continue;
-            const f32x4 o = v[j] * scale * nw_l[q];
-            Buf4<T>::store(o, lr, ok ? (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz) : kOOB, 0);
+        for (int j = 0; j < KQ; ++j) {
+            const int q = sub + 16 * j;
+            const f32x4 o = v[j] * scale * nw_l[q < nq ? q : 0];
+            Buf4<T>::store(o, lr, ok && q < nq ? (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz) : kOOB, 0);
         }
     }
 }
@@ -1449,7 +1523,7 @@ static int mhc_pre_norm_impl(const char *fn, const void *x, int64_t ldx, int64_t
     const int MT = 1;
     const int TT = 16 * MT;
     const size_t lds = (size_t)TT * (rowb + 8) + (size_t)kPreWaves * TT * (kPhiRows + 1) * 4 + kPreWaves * TT * 4 +
-                       TT * 16 + (size_t)C * 4;
+                       TT * 16 + (size_t)C * 4 + 32 * 4;   // ... norm weights, coef and bias
     if (lds > (size_t)device_info().max_shared_per_block)
         return set_error(WALSH_ENOTSUP, "%s: needs %zu B of LDS", fn, lds);
     int64_t ld = ld_in;
@@ -1495,11 +1569,16 @@ static int mhc_pre_norm_impl(const char *fn, const void *x, int64_t ldx, int64_t
         }
         const dim3 G((unsigned)ceil_div(rows, TT)), B(kPreThreads);
         hipStream_t s = (hipStream_t)stream;
+        const bool fast = n == 4 && C == 512;
         if (dtype == WALSH_BF16) {
-            if (post) launch((mhc_pre2_kernel<uint16_t, true, 1, true>), G, B, lds, s, a);
+            if (post && fast) launch((mhc_pre2_kernel<uint16_t, true, 1, true, true>), G, B, lds, s, a);
+            else if (post) launch((mhc_pre2_kernel<uint16_t, true, 1, true>), G, B, lds, s, a);
+            else if (fast) launch((mhc_pre2_kernel<uint16_t, true, 1, false, true>), G, B, lds, s, a);
             else launch((mhc_pre2_kernel<uint16_t, true, 1>), G, B, lds, s, a);
         } else {
-            if (post) launch((mhc_pre2_kernel<float, false, 1, true>), G, B, lds, s, a);
+            if (post && fast) launch((mhc_pre2_kernel<float, false, 1, true, true>), G, B, lds, s, a);
+            else if (post) launch((mhc_pre2_kernel<float, false, 1, true>), G, B, lds, s, a);
+            else if (fast) launch((mhc_pre2_kernel<float, false, 1, false, true>), G, B, lds, s, a);
             else launch((mhc_pre2_kernel<float, false, 1>), G, B, lds, s, a);
         }
         const int rc = check_hip(hipGetLastError(), fn);
