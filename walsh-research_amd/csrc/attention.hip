@@ -218,22 +218,28 @@ struct PfArgs {
     float sl2;                       // scale * log2(e)
 };
 
-// One 64-key step of the online softmax for a wave's 16 queries.  K rows
-// kl[key * ks + d], V transposed vt[d * vs + key] (LDS); key index kbase +
-// r for LDS row r.  FULL: every key of the step is at or before the wave's
-// first query (no mask); otherwise keys past each query are masked and
-// 16-key blocks wholly after the wave's last query are skipped.
+// max(a, b) as med3(a, b, +inf): the same value, without the operand
+// canonicalisation the compiler puts in front of fmaxf on matrix-core
+// results (no NaNs arise here: scores are finite or -inf).  +inf comes from
+// a register the compiler cannot see into, or it folds med3 back into fmaxf.
+__device__ __forceinline__ float opaque_inf() {
+    float v;
+    asm volatile("v_mov_b32 %0, 0x7f800000" : "=v"(v));
+    return v;
+}
+__device__ __forceinline__ float max2(float a, float b, float pinf) { return __builtin_amdgcn_fmed3f(a, b, pinf); }
+
 // max over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (a query's lanes) with
 // the gfx950 row / half swaps (VALU; no LDS traffic as ds_bpermute has):
 // permlane16_swap exchanges odd rows of one operand with even rows of the
 // other, permlane32_swap the upper half of one with the lower half of the
 // other, so with both operands equal each pair of results covers the pair.
-__device__ __forceinline__ float max_over_rows(float v) {
+__device__ __forceinline__ float max_over_rows(float v, float pinf) {
     typedef unsigned int u2 __attribute__((ext_vector_type(2)));
     const u2 a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(a.x), __uint_as_float(a.y));
+    v = max2(__uint_as_float(a.x), __uint_as_float(a.y), pinf);
     const u2 b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(b.x), __uint_as_float(b.y));
+    return max2(__uint_as_float(b.x), __uint_as_float(b.y), pinf);
 }
 
 struct AttnState {
@@ -242,10 +248,33 @@ struct AttnState {
     float m_run;
 };
 
+// The matrix-core fragments of one 64-key step: K rows (A of S^T = K Q^T)
+// and V^T rows (A of O^T = V^T P^T), per 16-key block j and 16-wide d block c.
+template <int D> struct StepFrags {
+    u32x2 k[4][D / 16], v[4][D / 16];
+};
+
+// K rows kl[key * ks + d], V transposed vt[d * vs + key] (LDS); LDS row r0
+// is the step's first key.
+template <int D>
+__device__ __forceinline__ void load_frags(StepFrags<D> &f, const uint16_t *kl, int ks, const uint16_t *vt, int vs,
+                                           int r0, int n, int kq) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+            f.k[j][c] = *(const u32x2 *)(kl + (r0 + 16 * j + n) * ks + 16 * c + 4 * kq);
+            f.v[j][c] = *(const u32x2 *)(vt + (16 * c + n) * vs + r0 + 16 * j + 4 * kq);
+        }
+}
+
+// One 64-key step of the online softmax for a wave's 16 queries, keys
+// k0 .. k0 + 63.  FULL: every key of the step is at or before the wave's
+// first query (no mask); otherwise keys past each query are masked and
+// 16-key blocks wholly after the wave's last query are skipped.
 template <int D, bool FULL>
-__device__ __forceinline__ void attn_step(AttnState &st, const u32x2 (&qf)[D / 16], const uint16_t *kl, int ks,
-                                          const uint16_t *vt, int vs, int r0, int k0, int qw, int qi, int n, int kq,
-                                          float sl2) {
+__device__ __forceinline__ void attn_step_frags(AttnState &st, const u32x2 (&qf)[D / 16], const StepFrags<D> &f,
+                                                int k0, int qw, int qi, int kq, float sl2) {
     constexpr int ND = D / 16;
     const u32x2 ones = {0x3f803f80u, 0x3f803f80u};   // four bf16 1.0
     f32x4 s[4];
@@ -258,11 +287,9 @@ __device__ __forceinline__ void attn_step(AttnState &st, const u32x2 (&qf)[D / 1
         }
         f32x4 t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < ND; ++c) {
-            const u32x2 kf = *(const u32x2 *)(kl + (r0 + 16 * j + n) * ks + 16 * c + 4 * kq);
-            t = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, kf),
+        for (int c = 0; c < ND; ++c)
+            t = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, f.k[j][c]),
                                                          __builtin_bit_cast(i16x4, qf[c]), t, 0, 0, 0);
-        }
         // t[i]: S[query qi][key kb + 4kq + i], unscaled (the scale is folded
         // into the exponent; scale > 0 keeps the max)
         if (!FULL && kb + 15 > qw) {           // the diagonal block: mask keys past the query
@@ -272,12 +299,13 @@ __device__ __forceinline__ void attn_step(AttnState &st, const u32x2 (&qf)[D / 1
         }
         s[j] = t;
     }
-    float mx = fmaxf(fmaxf(fmaxf(s[0].x, s[0].y), fmaxf(s[0].z, s[0].w)),
-                     fmaxf(fmaxf(s[1].x, s[1].y), fmaxf(s[1].z, s[1].w)));
-    mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[2].x, s[2].y), fmaxf(s[2].z, s[2].w)),
-                         fmaxf(fmaxf(s[3].x, s[3].y), fmaxf(s[3].z, s[3].w))));
-    mx = max_over_rows(mx);
-    const float m_new = fmaxf(st.m_run, mx);
+    const float pinf = opaque_inf();
+    float mj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mj[j] = max2(max2(s[j].x, s[j].y, pinf), max2(s[j].z, s[j].w, pinf), pinf);
+    float mx = max2(max2(mj[0], mj[1], pinf), max2(mj[2], mj[3], pinf), pinf);
+    mx = max_over_rows(mx, pinf);
+    const float m_new = max2(st.m_run, mx, pinf);
     // v_exp_f32 directly: arguments are <= 0 (or -inf -> 0); results below
     // the float32 normal range flush to zero
     const float alpha = __builtin_amdgcn_exp2f((st.m_run - m_new) * sl2);
@@ -302,12 +330,20 @@ __device__ __forceinline__ void attn_step(AttnState &st, const u32x2 (&qf)[D / 1
         st.lacc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, ones),
                                                            __builtin_bit_cast(i16x4, pf[j]), st.lacc, 0, 0, 0);
 #pragma unroll
-        for (int c = 0; c < ND; ++c) {
-            const u32x2 vf = *(const u32x2 *)(vt + (16 * c + n) * vs + r0 + 16 * j + 4 * kq);
-            st.acc[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, vf),
+        for (int c = 0; c < ND; ++c)
+            st.acc[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, f.v[j][c]),
                                                                  __builtin_bit_cast(i16x4, pf[j]), st.acc[c], 0, 0, 0);
-        }
     }
+}
+
+// The step with its fragments read from LDS rows r0 .. r0 + 63.
+template <int D, bool FULL>
+__device__ __forceinline__ void attn_step(AttnState &st, const u32x2 (&qf)[D / 16], const uint16_t *kl, int ks,
+                                          const uint16_t *vt, int vs, int r0, int k0, int qw, int qi, int n, int kq,
+                                          float sl2) {
+    StepFrags<D> f;
+    load_frags<D>(f, kl, ks, vt, vs, r0, n, kq);
+    attn_step_frags<D, FULL>(st, qf, f, k0, qw, qi, kq, sl2);
 }
 
 template <int D>
@@ -420,9 +456,10 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PfArgs a) {
 }
 
 // Whole-head variant, for heads whose K and V fit in LDS together (T_pad *
-// D * 4 bytes plus padding; head_dim 16 up to about 2,300 positions): one
-// workgroup of 16 waves per (sequence, head) stages K (row-major) and V
-// (transposed) once, then each wave takes 16-query sub-tiles in a snake
+// (D + 4) * 2 + D * (T_pad + 4) * 2 bytes; head_dim 16 up to about 2,200
+// positions): one workgroup of 16 waves per (sequence, head) stages K
+// (row-major) and V (transposed) once, then each wave takes 16-query
+// sub-tiles in a snake
 // order (w, 31 - w, 32 + w, 63 - w, ...) so every wave gets about the same
 // number of key steps.  No barriers after the staging.  (gridDim.z
 // workgroups may share a head, each taking its share of the sub-tiles; one
@@ -433,10 +470,13 @@ template <int D>
 __global__ __launch_bounds__(64 * kPhWaves) void prefill_attn_head_kernel(PfArgs a, int tpad) {
     constexpr int ND = D / 16;
     extern __shared__ __align__(16) uint16_t ph_smem[];
-    const int ks = D;                    // K row: D / 2 dwords (16 B-aligned rows, bank-spread at D = 16)
-    const int vs = tpad + 16;            // V^T row: (tpad + 16) / 2 dwords = 8 mod 64 banks
-    uint16_t *k_l = ph_smem;                         // [tpad][D]
-    uint16_t *vt_l = ph_smem + tpad * D;             // [D][vs]
+    // padded rows: the 16 lanes of a fragment read (one key or one d per
+    // lane, 8 bytes each) start 2 dwords mod 32 apart, so they hit distinct
+    // banks (K rows of D + 4 elements; V^T rows of tpad + 4, tpad % 64 == 0)
+    const int ks = D + 4;
+    const int vs = tpad + 4;
+    uint16_t *k_l = ph_smem;                         // [tpad][ks]
+    uint16_t *vt_l = ph_smem + tpad * ks;            // [D][vs]
     const int h = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
     // gridDim.z workgroups share a head: global wave index over them
@@ -452,7 +492,9 @@ __global__ __launch_bounds__(64 * kPhWaves) void prefill_attn_head_kernel(PfArgs
             kv = *(const uint4 *)(kbase + (int64_t)key * a.kv_st + part * 8);
             vv = *(const uint4 *)(vbase + (int64_t)key * a.kv_st + part * 8);
         }
-        *(uint4 *)(k_l + key * ks + part * 8) = kv;
+        u32x2 *kd = (u32x2 *)(k_l + key * ks + part * 8);   // 8-byte aligned rows
+        kd[0] = u32x2{kv.x, kv.y};
+        kd[1] = u32x2{kv.z, kv.w};
         const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -477,10 +519,22 @@ __global__ __launch_bounds__(64 * kPhWaves) void prefill_attn_head_kernel(PfArgs
         for (int c = 0; c < ND; ++c) st.acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
         st.lacc = f32x4{0.f, 0.f, 0.f, 0.f};
         st.m_run = -INFINITY;
+        // each step's fragments are read from LDS one step ahead, into two
+        // sets used in turn (two steps per trip)
+        const int last = qw + 15;
+        StepFrags<D> f0, f1;
+        load_frags<D>(f0, k_l, ks, vt_l, vs, 0, n, kq);
+        auto step = [&](const StepFrags<D> &f, int k0) {
+            if (k0 + 63 <= qw) attn_step_frags<D, true>(st, qf, f, k0, qw, qi, kq, a.sl2);
+            else attn_step_frags<D, false>(st, qf, f, k0, qw, qi, kq, a.sl2);
+        };
 #pragma unroll 1
-        for (int k0 = 0; k0 <= qw + 15; k0 += 64) {
-            if (k0 + 63 <= qw) attn_step<D, true>(st, qf, k_l, ks, vt_l, vs, k0, k0, qw, qi, n, kq, a.sl2);
-            else attn_step<D, false>(st, qf, k_l, ks, vt_l, vs, k0, k0, qw, qi, n, kq, a.sl2);
+        for (int k0 = 0; k0 <= last; k0 += 128) {
+            if (k0 + 64 <= last) load_frags<D>(f1, k_l, ks, vt_l, vs, k0 + 64, n, kq);
+            step(f0, k0);
+            if (k0 + 64 > last) break;
+            if (k0 + 128 <= last) load_frags<D>(f0, k_l, ks, vt_l, vs, k0 + 128, n, kq);
+            step(f1, k0 + 64);
         }
         if (qi < a.T) attn_store<D>(st, a.o + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st, kq);
     }
@@ -627,7 +681,7 @@ WALSH_EXPORT int walsh_prefill_attention(const void *q, int64_t q_sb, int64_t q_
     hipStream_t s = (hipStream_t)stream;
     // whole heads in LDS when they fit (tpad rows of K and of V^T, padded)
     const int64_t tpad = ceil_div(T, 64) * 64;
-    const int64_t head_lds = (tpad * D + D * (tpad + 16)) * 2;
+    const int64_t head_lds = (tpad * (D + 4) + D * (tpad + 4)) * 2;
     if (D == 16 && head_lds <= device_info().max_shared_per_block) {
         launch(prefill_attn_head_kernel<16>, dim3((unsigned)H, (unsigned)B, 1u), dim3(64 * kPhWaves),
                (uint32_t)head_lds, s, a, (int)tpad);
