@@ -1183,9 +1183,13 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
     const int Nt = base.Nt, Kc = base.Kc;
     const bool swiglu = ubase != nullptr;
     size_t lds = hadamard_lds_bytes(bf16, Kc, Nt);
-    if (swiglu) lds += (size_t)16 * 128 * (Kc + Nt) + (size_t)kWaves * 32 * 64 * (bf16 ? 8 : 16);
-    if (lds > (size_t)device_info().max_shared_per_block)
-        return set_error(WALSH_ENOTSUP, "%s: in_o=%d out_o=%d need %zu B of LDS", fn, base.in_o, base.out_o, lds);
+    // SwiGLU: the up projection's alpha / beta tables and, per working wave,
+    // the gate output (32 groups x 64 lanes x 4 values)
+    const size_t stash_wave = (size_t)32 * 64 * (bf16 ? 8 : 16);
+    if (swiglu) lds += (size_t)16 * 128 * (Kc + Nt);
+    if (lds + (swiglu ? kWaves * stash_wave : 0) > (size_t)device_info().max_shared_per_block)
+        return set_error(WALSH_ENOTSUP, "%s: in_o=%d out_o=%d need %zu B of LDS", fn, base.in_o, base.out_o,
+                         lds + (swiglu ? kWaves * stash_wave : 0));
     const size_t valign = bf16 ? 8 : 16;
     const bool vec = (base.gsx % 4 == 0) && (base.ldx % 4 == 0) && ((uintptr_t)base.x % valign == 0) &&
                      (base.gsy % 4 == 0) && (base.ldy % 4 == 0) && ((uintptr_t)base.y % valign == 0);
@@ -1224,6 +1228,14 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
             a.wave_tiles = (int)wt;
             grid = ceil_div(work, wt);
         }
+        // the single-chunk SwiGLU kernel holds two workgroups per CU by its
+        // registers; with a stash for each of 4 waves its LDS would allow
+        // one, so 3 of its waves take items and the stash is sized for them
+        if (swiglu && Kc == 1 && (a.wave_tiles <= 0 || a.wave_tiles > 3)) {
+            a.wave_tiles = 3;
+            grid = ceil_div(work, 3);
+            if (grid > resident) grid = resident;   // one round; waves loop over the rest
+        }
         if (grid > cap) grid = cap;
         const dim3 G((unsigned)grid), B(kThreads);
         if (swiglu) {
@@ -1231,7 +1243,9 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
             ua.x = a.x;
             ua.y = a.y;
             ua.M = a.M;
-#define WALSH_SW_LAUNCH(T, MMA, V, K1) launch((hadamard_swiglu_kernel<T, MMA, V, K1>), G, B, lds, s, a, ua)
+            ua.wave_tiles = a.wave_tiles;
+            const size_t sw_lds = lds + (size_t)(a.wave_tiles > 0 ? a.wave_tiles : kWaves) * stash_wave;
+#define WALSH_SW_LAUNCH(T, MMA, V, K1) launch((hadamard_swiglu_kernel<T, MMA, V, K1>), G, B, sw_lds, s, a, ua)
             const bool one = Kc == 1;
             if (bf16) {
                 if (vec) { if (one) WALSH_SW_LAUNCH(uint16_t, true, true, true); else WALSH_SW_LAUNCH(uint16_t, true, true, false); }
