@@ -262,6 +262,208 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
     hadamard_fwd_body<T, BF16MMA, VEC, KC1, false, PIPE1>(an.p[l], blockIdx.x / an.n, gridDim.x / an.n);
 }
 
+// ---------------------------------------------------------------- wavefront pairs
+// bf16, in_o <= 16 and out_o <= 16 (one input chunk, one output tile), VEC
+// layouts: the PIPE1 shape with each 16-token tile split over a PAIR of
+// wavefronts by group, so a wavefront holds 16 groups (half the registers
+// and half the dependent chain of the one-wavefront kernel; twice the
+// wavefronts in flight).  Every butterfly of both transforms is computed as
+// in fht32 (stages h = 1, 2, 4, 8, 16 in that order, (a, b) -> (a + b, a - b)
+// with a the lower group), so results equal hadamard_fwd_kernel's bitwise.
+//
+// Wavefront HF of the pair loads groups 16 HF .. 16 HF + 15 (slot s = group
+// - 16 HF) and runs input stages 1..8 locally.  Stage 16 pairs group g with
+// g + 16 across the pair: HF 0 computes the pairs g = 0..7, HF 1 the pairs
+// g = 8..15, each sending the other the 8 slots it needs (8 KB through LDS)
+// and keeping both results of its pairs, so afterwards slot s holds group
+//   g_in(s) = 8 HF + (s & 7) + 16 (s >> 3).
+// The contraction runs on those 16 groups.  Output stages 1, 2, 4 pair slots
+// within (s & 7); stage 8 pairs g_in(s) with g_in(s) + 8 across the pair (HF 0
+// computes the pairs with s & 4 == 0, HF 1 those with s & 4 != 0; low result
+// to the slot with bit 2 clear, high to the one with bit 2 set), after which
+// slot u holds group
+//   g_out(u) = (u & 3) + 4 HF + 8 ((u >> 2) & 1) + 16 (u >> 3),
+// and stage 16 pairs slots u and u + 8 locally.
+// Several layers on the same input rows (q, k, v): workgroup b runs layer
+// b % n over tiles b / n, b / n + G / n, ... as hadamard_fwdn_kernel does.
+constexpr int kPairThreads = 128;
+// Above this many 16-row tiles per layer the one-wavefront kernel (its next
+// tile's loads in flight during the current one's output) is faster: at
+// 8,192 / 65,536 / 262,144 rows one layer takes 9.8 / 36.6 / 157 us here
+// against 14.2 / 39.9 / 146 us there, and q, k, v 19.1 / 93.5 / 463 us
+// against 23.8 / 104 / 402 us.
+constexpr int64_t kPairMaxTiles = 6144;
+constexpr size_t kPairLds = 256 * 8 + 2 * 128 * 16 + 2 * 8 * 64 * 16;   // lut, alpha/beta, exchange
+
+template <int HF>
+__device__ __forceinline__ void pair_tile(const HadArgs &a, int tile, int lane, const uint2 *__restrict__ lut,
+                                          const f32x4 *__restrict__ alpha_l, const f32x4 *__restrict__ beta_l,
+                                          f32x4 *__restrict__ xch, __amdgpu_buffer_rsrc_t xr,
+                                          __amdgpu_buffer_rsrc_t yr) {
+    const int t = lane & 15, q = lane >> 4;
+    const int row = tile * kTile + t;
+    const bool row_ok = row < a.M;
+    f32x4 *mine = xch + HF * 8 * 64, *theirs = xch + (1 - HF) * 8 * 64;
+    // the lane's 32 code bytes (issued first: their wait is after the input
+    // transform)
+    uint4 w0, w1;
+    load_w(a, 0, 0, lane, w0, w1);
+    // input: groups 16 HF + s, columns 4q .. 4q + 3
+    f32x4 v[16];
+    {
+        const uint32_t gsb = (uint32_t)a.gsx * 2;
+        const uint32_t xo = (row_ok && 4 * q < a.in_o) ? x_row_off(a, row, 2) + (uint32_t)(8 * q) : kOOB;
+        u32x2 xraw[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            xraw[s] = __builtin_amdgcn_raw_buffer_load_b64(xr, xo, (uint32_t)(16 * HF + s) * gsb, 0);
+        const f32x4 *al = alpha_l + q * 32 + 16 * HF;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const f32x4 x4 = {__uint_as_float(xraw[s].x << 16), __uint_as_float(xraw[s].x & 0xffff0000u),
+                              __uint_as_float(xraw[s].y << 16), __uint_as_float(xraw[s].y & 0xffff0000u)};
+            v[s] = x4 * al[s];
+        }
+    }
+#pragma unroll
+    for (int h = 1; h < 16; h <<= 1) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            if (s & h) continue;
+            const f32x4 x0 = v[s], x1 = v[s + h];
+            v[s] = x0 + x1;
+            v[s + h] = x0 - x1;
+        }
+    }
+    // input stage 16 across the pair
+    lds_barrier();   // the partner is done reading the previous tile's output exchange
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mine[j * 64 + lane] = v[HF ? j : j + 8];
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const f32x4 other = theirs[j * 64 + lane];
+        if (HF == 0) {
+            const f32x4 x0 = v[j], x1 = other;           // groups j, 16 + j
+            v[j] = x0 + x1;
+            v[j + 8] = x0 - x1;
+        } else {
+            const f32x4 x0 = other, x1 = v[j + 8];       // groups 8 + j, 24 + j
+            v[j] = x0 + x1;
+            v[j + 8] = x0 - x1;
+        }
+    }
+    // contraction of the 16 groups g_in(s)
+    u32x2 xm[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) xm[s] = u32x2{pack_bf16x2(v[s].x, v[s].y), pack_bf16x2(v[s].z, v[s].w)};
+    const uint32_t wb[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    f32x4 acc[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        const int g = 8 * HF + (s & 7) + 16 * (s >> 3);
+        const uint32_t byte = (wb[g >> 2] >> (8 * (g & 3))) & 0xffu;
+        acc[s] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, lut[byte]),
+                                                            __builtin_bit_cast(i16x4, xm[s]),
+                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    }
+    // output stages 1, 2, 4 within (s & 7)
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            if (s & h) continue;
+            const f32x4 x0 = acc[s], x1 = acc[s + h];
+            acc[s] = x0 + x1;
+            acc[s + h] = x0 - x1;
+        }
+    }
+    // output stage 8 across the pair: HF keeps slots with (s & 4) == 4 HF
+    lds_barrier();   // the partner is done reading the input exchange
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int snd = (p & 3) + 4 * (1 - HF) + 8 * (p >> 2);
+        mine[p * 64 + lane] = acc[snd];
+    }
+    lds_barrier();
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int kept = (p & 3) + 4 * HF + 8 * (p >> 2);
+        const int lo = kept & ~4, hi = kept | 4;
+        const f32x4 other = theirs[p * 64 + lane];
+        const f32x4 x0 = HF == 0 ? acc[kept] : other;   // group with bit 3 clear
+        const f32x4 x1 = HF == 0 ? other : acc[kept];   // its partner + 8
+        acc[lo] = x0 + x1;
+        acc[hi] = x0 - x1;
+    }
+    // output stage 16: slots u, u + 8
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const f32x4 x0 = acc[u], x1 = acc[u + 8];
+        acc[u] = x0 + x1;
+        acc[u + 8] = x0 - x1;
+    }
+    // beta (and RoPE), stores of groups g_out(u)
+    const int o0 = 4 * q;
+    const bool ok = row_ok && o0 < a.out_o;
+    const uint32_t voff = ok ? (uint32_t)((int64_t)row * a.ldy * 2) + (uint32_t)o0 * 2 : kOOB;
+    const uint32_t hstride = (uint32_t)a.gsy * 2;
+    const f32x4 *bl = beta_l + q * 32;
+    if (a.rope) {
+        const f32x4 cs = ok ? rope_cs(a, row, o0) : f32x4{1.f, 0.f, 1.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int h = (u & 3) + 4 * HF + 8 * ((u >> 2) & 1) + 16 * (u >> 3);
+            Buf4<uint16_t>::store(rope_apply(acc[u] * bl[h], cs), yr, voff, (uint32_t)h * hstride);
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int h = (u & 3) + 4 * HF + 8 * ((u >> 2) & 1) + 16 * (u >> 3);
+            Buf4<uint16_t>::store(acc[u] * bl[h], yr, voff, (uint32_t)h * hstride);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kPairThreads, 4) void hadamard_pair_kernel(HadArgsN an) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint2 *lut = (uint2 *)smem;
+    f32x4 *alpha_l = (f32x4 *)(smem + 256 * 8);   // [4 q][32 g]
+    f32x4 *beta_l = alpha_l + 128;                 // [4 q][32 h]
+    f32x4 *xch = beta_l + 128;                     // [2 HF][8][64 lanes]
+    const int l = blockIdx.x % an.n;
+    const HadArgs &a = an.p[l];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < 256; e += kPairThreads) {
+        float val[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) val[j] = (float)((int)(((uint32_t)e >> (6 - 2 * j)) & 3u) - 1);
+        lut[e] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
+    }
+    {
+        const int e = tid;   // (q, g) = (e >> 5, e & 31); kPairThreads == 128 entries
+        const int g = e & 31, i0 = 4 * (e >> 5);
+        f32x4 va, vb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            va[j] = (i0 + j < a.in_o) ? (a.alpha ? a.alpha[g * a.in_o + i0 + j] : 1.f) : 0.f;
+            vb[j] = (i0 + j < a.out_o) ? a.beta[g * a.beta_h + i0 + j] * 0.03125f : 0.f;
+        }
+        alpha_l[e] = va;
+        beta_l[e] = vb;
+    }
+    __syncthreads();
+    const int hf = tid >> 6, lane = tid & 63;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a, 2));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
+    const int n_tiles = (int)ceil_div(a.M, kTile);
+    const int nb = (int)gridDim.x / an.n;
+    for (int tile = (int)blockIdx.x / an.n; tile < n_tiles; tile += nb) {
+        if (hf == 0) pair_tile<0>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
+        else pair_tile<1>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
+    }
+}
+
 // ---------------------------------------------------------------- wide layers
 // in_o > 16 with several output tiles (n_embd 4096: in_o = out_o = 128).  One
 // workgroup of 8 waves takes a (16-token tile, group of 8 output tiles): the
@@ -1178,6 +1380,19 @@ static int hadamard_check(const char *fn, const void *x, int64_t ldx, int64_t gs
 
 // Launch one Hadamard-linear (two for the fused SwiGLU: u != NULL) over M
 // rows in chunks whose byte offsets fit a 31-bit buffer range.
+// hadamard_pair_kernel over rows rows of an.n layers: one workgroup (a
+// wavefront pair) per 16-row tile and layer, up to the workgroups the CUs
+// hold at once (LDS: kPairLds each; registers: 4 wavefronts per SIMD), the
+// rest looped over.
+static void pair_launch(const HadArgsN &an, int64_t rows, hipStream_t s) {
+    const int64_t per_cu = (int64_t)(65536 + 98304) / (int64_t)kPairLds;   // 160 KB of LDS per CU
+    const int64_t resident = (int64_t)device_info().cu_count * (per_cu < 8 ? per_cu : 8);
+    int64_t per_layer = ceil_div(rows, kTile);
+    const int64_t cap = resident / an.n > 0 ? resident / an.n : 1;
+    if (per_layer > cap) per_layer = cap;
+    launch(hadamard_pair_kernel, dim3((unsigned)(per_layer * an.n)), dim3(kPairThreads), (uint32_t)kPairLds, s, an);
+}
+
 static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, int64_t M, bool bf16, hipStream_t s) {
     const int64_t esz = bf16 ? 2 : 4;
     const int Nt = base.Nt, Kc = base.Kc;
@@ -1279,6 +1494,13 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
                 if (a4) launch((hadamard_wide_kernel<float, false, true>), GW, BW, wide_lds, s, a);
                 else launch((hadamard_wide_kernel<float, false, false>), GW, BW, wide_lds, s, a);
             }
+        } else if (bf16 && vec && kc1 && Nt == 1 && ceil_div(rows, kTile) <= kPairMaxTiles) {
+            // one input chunk, one output tile, up to kPairMaxTiles tiles: a
+            // wavefront pair per tile
+            HadArgsN an;
+            an.n = 1;
+            an.p[0] = a;
+            pair_launch(an, rows, s);
         } else {
 #define WALSH_HAD_LAUNCH(T, MMA, V, K1) launch((hadamard_fwd_kernel<T, MMA, V, K1>), G, B, lds, s, a)
             if (bf16) {
@@ -1448,7 +1670,8 @@ static int hadamard_multi(const char *fn, const void *x, int64_t ldx, int64_t M,
         int64_t grid = ceil_div(ceil_div(rows, kTile), kWaves);
         if (grid > cap) grid = cap;
         const dim3 G((unsigned)(grid * n)), B(kThreads);
-        if (bf16 && Nt == 1) launch((hadamard_fwdn_kernel<uint16_t, true, true, true, true>), G, B, lds, s, an);
+        if (bf16 && Nt == 1 && ceil_div(rows, kTile) <= kPairMaxTiles) pair_launch(an, rows, s);
+        else if (bf16 && Nt == 1) launch((hadamard_fwdn_kernel<uint16_t, true, true, true, true>), G, B, lds, s, an);
         else if (bf16) launch((hadamard_fwdn_kernel<uint16_t, true, true, true>), G, B, lds, s, an);
         else launch((hadamard_fwdn_kernel<float, false, true, true>), G, B, lds, s, an);
         const int rc = check_hip(hipGetLastError(), fn);
