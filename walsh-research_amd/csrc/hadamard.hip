@@ -295,7 +295,7 @@ constexpr int kPairThreads = 128;
 constexpr int64_t kPairMaxTiles = 6144;
 constexpr size_t kPairLds = 256 * 8 + 2 * 128 * 16 + 2 * 8 * 64 * 16;   // lut, alpha/beta, exchange
 
-template <int HF>
+template <int HF, bool DENSE>
 __device__ __forceinline__ void pair_tile(const HadArgs &a, int tile, int lane, const uint2 *__restrict__ lut,
                                           const f32x4 *__restrict__ alpha_l, const f32x4 *__restrict__ beta_l,
                                           f32x4 *__restrict__ xch, __amdgpu_buffer_rsrc_t xr,
@@ -305,9 +305,9 @@ __device__ __forceinline__ void pair_tile(const HadArgs &a, int tile, int lane, 
     const bool row_ok = row < a.M;
     f32x4 *mine = xch + HF * 8 * 64, *theirs = xch + (1 - HF) * 8 * 64;
     // the lane's 32 code bytes (issued first: their wait is after the input
-    // transform)
+    // transform); DENSE reads its weight fragments just before the products
     uint4 w0, w1;
-    load_w(a, 0, 0, lane, w0, w1);
+    if constexpr (!DENSE) load_w(a, 0, 0, lane, w0, w1);
     // input: groups 16 HF + s, columns 4q .. 4q + 3
     f32x4 v[16];
     {
@@ -357,13 +357,24 @@ __device__ __forceinline__ void pair_tile(const HadArgs &a, int tile, int lane, 
     u32x2 xm[16];
 #pragma unroll
     for (int s = 0; s < 16; ++s) xm[s] = u32x2{pack_bf16x2(v[s].x, v[s].y), pack_bf16x2(v[s].z, v[s].w)};
-    const uint32_t wb[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    uint2 wd[16];
+    if constexpr (DENSE) {
+        const uint2 *wf = (const uint2 *)a.kw;   // [32 g][64 lanes] bf16x4
+#pragma unroll
+        for (int s = 0; s < 16; ++s) wd[s] = wf[(8 * HF + (s & 7) + 16 * (s >> 3)) * 64 + lane];
+    }
     f32x4 acc[16];
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
-        const int g = 8 * HF + (s & 7) + 16 * (s >> 3);
-        const uint32_t byte = (wb[g >> 2] >> (8 * (g & 3))) & 0xffu;
-        acc[s] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, lut[byte]),
+        uint2 wa;
+        if constexpr (DENSE) {
+            wa = wd[s];
+        } else {
+            const uint32_t wb[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            const int g = 8 * HF + (s & 7) + 16 * (s >> 3);
+            wa = lut[(wb[g >> 2] >> (8 * (g & 3))) & 0xffu];
+        }
+        acc[s] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, wa),
                                                             __builtin_bit_cast(i16x4, xm[s]),
                                                             f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
     }
@@ -425,7 +436,10 @@ __device__ __forceinline__ void pair_tile(const HadArgs &a, int tile, int lane, 
     }
 }
 
-__global__ __launch_bounds__(kPairThreads, 4) void hadamard_pair_kernel(HadArgsN an) {
+// DENSE: float weights as matrix-core A fragments [32 g][64 lanes] (the
+// Hadamard head mixer, one layer), read per tile from memory.
+template <bool DENSE>
+__global__ __launch_bounds__(kPairThreads, DENSE ? 3 : 4) void hadamard_pair_kernel(HadArgsN an) {
     extern __shared__ __align__(16) unsigned char smem[];
     uint2 *lut = (uint2 *)smem;
     f32x4 *alpha_l = (f32x4 *)(smem + 256 * 8);   // [4 q][32 g]
@@ -459,8 +473,8 @@ __global__ __launch_bounds__(kPairThreads, 4) void hadamard_pair_kernel(HadArgsN
     const int n_tiles = (int)ceil_div(a.M, kTile);
     const int nb = (int)gridDim.x / an.n;
     for (int tile = (int)blockIdx.x / an.n; tile < n_tiles; tile += nb) {
-        if (hf == 0) pair_tile<0>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
-        else pair_tile<1>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
+        if (hf == 0) pair_tile<0, DENSE>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
+        else pair_tile<1, DENSE>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
     }
 }
 
@@ -1384,13 +1398,16 @@ static int hadamard_check(const char *fn, const void *x, int64_t ldx, int64_t gs
 // wavefront pair) per 16-row tile and layer, up to the workgroups the CUs
 // hold at once (LDS: kPairLds each; registers: 4 wavefronts per SIMD), the
 // rest looped over.
-static void pair_launch(const HadArgsN &an, int64_t rows, hipStream_t s) {
+static void pair_launch(const HadArgsN &an, int64_t rows, hipStream_t s, bool dense = false) {
     const int64_t per_cu = (int64_t)(65536 + 98304) / (int64_t)kPairLds;   // 160 KB of LDS per CU
-    const int64_t resident = (int64_t)device_info().cu_count * (per_cu < 8 ? per_cu : 8);
+    const int64_t by_regs = dense ? 6 : 8;   // 3 or 4 wavefronts per SIMD
+    const int64_t resident = (int64_t)device_info().cu_count * (per_cu < by_regs ? per_cu : by_regs);
     int64_t per_layer = ceil_div(rows, kTile);
     const int64_t cap = resident / an.n > 0 ? resident / an.n : 1;
     if (per_layer > cap) per_layer = cap;
-    launch(hadamard_pair_kernel, dim3((unsigned)(per_layer * an.n)), dim3(kPairThreads), (uint32_t)kPairLds, s, an);
+    const dim3 G((unsigned)(per_layer * an.n)), B(kPairThreads);
+    if (dense) launch(hadamard_pair_kernel<true>, G, B, (uint32_t)kPairLds, s, an);
+    else launch(hadamard_pair_kernel<false>, G, B, (uint32_t)kPairLds, s, an);
 }
 
 static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, int64_t M, bool bf16, hipStream_t s) {
@@ -1810,6 +1827,14 @@ WALSH_EXPORT int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64
     const bool vec = D % 4 == 0 && x_hstride % 4 == 0 && x_tstride % 4 == 0 && x_bstride % 4 == 0 &&
                      (uintptr_t)x % valign == 0 && ldy % 4 == 0 && (uintptr_t)y % valign == 0;
     const bool kc1 = Kc == 1 && (bf16 || Nt == 1);
+    if (bf16 && vec && kc1 && Nt == 1 && ceil_div(M, kTile) <= kPairMaxTiles) {
+        // head_dim <= 16: a wavefront pair per tile
+        HadArgsN an;
+        an.n = 1;
+        an.p[0] = a;
+        pair_launch(an, M, (hipStream_t)stream, true);
+        return check_hip(hipGetLastError(), fn);
+    }
     int64_t grid = ceil_div(ceil_div(M, kTile), kWaves);
     const int64_t cap = (int64_t)device_info().cu_count * 2;
     if (grid > cap) grid = cap;
