@@ -39,6 +39,7 @@ Prints ONE JSON line.  Besides the timed region it
     on a bounded sample of the same workload -> "cpu_baseline".
 """
 import argparse
+import re
 import json
 import os
 import sys
@@ -86,10 +87,9 @@ def measured_traffic(kernel: str, workload: str = "mhcwalsh"):
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
-                if line.startswith("kernel=") and "traffic_bytes=" in line:
-                    fields = dict(kv.split("=", 1) for kv in line.split())
-                    if fields["kernel"] == kernel:
-                        return int(float(fields["traffic_bytes"]))
+                m = re.match(r"kernel=(\S+) .*\btraffic_bytes=([0-9.]+)", line)
+                if m and m.group(1) == kernel:
+                    return int(float(m.group(2)))
     except OSError:
         pass
     return None

@@ -288,11 +288,12 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void had
 // b % n over tiles b / n, b / n + G / n, ... as hadamard_fwdn_kernel does.
 constexpr int kPairThreads = 128;
 // Above this many 16-row tiles per layer the one-wavefront kernel (its next
-// tile's loads in flight during the current one's output) is faster: at
-// 8,192 / 65,536 / 262,144 rows one layer takes 9.8 / 36.6 / 157 us here
-// against 14.2 / 39.9 / 146 us there, and q, k, v 19.1 / 93.5 / 463 us
-// against 23.8 / 104 / 402 us.
-constexpr int64_t kPairMaxTiles = 6144;
+// tile's loads in flight during the current one's output) is faster once the
+// rows come from HBM rather than the Infinity Cache: 65,536 bf16 rows from
+// buffers rotated past the cache take 48.7 us here against 44.1 us there,
+// while at 8,192 rows one layer takes 9.8 us against 14.2 us and q, k, v
+// 19.1 us against 23.8 us.
+constexpr int64_t kPairMaxTiles = 2048;
 constexpr size_t kPairLds = 256 * 8 + 2 * 128 * 16 + 2 * 8 * 64 * 16;   // lut, alpha/beta, exchange
 
 template <int HF, bool DENSE>

@@ -150,7 +150,23 @@ def hadamard_prepare(packed: torch.Tensor, in_o: int, out_o: int) -> torch.Tenso
     return kw
 
 
-def _had_meta(rows, in_o, out_o, dt, vec, kc1, swiglu=False):
+# 16-row tiles per layer up to which the library runs the bf16 single-output-tile
+# shapes on wavefront pairs (hadamard_pair_kernel / hadamard_pair_kloop_kernel)
+PAIR_MAX_TILES = 2048
+
+
+def _pair_shape(rows, in_o, out_o, dt, vec, rope=False):
+    """The pair kernel the library dispatches for this shape, or None."""
+    if dt != torch.bfloat16 or not vec or out_o > 16 or (rows + 15) // 16 > PAIR_MAX_TILES:
+        return None
+    if in_o <= 16:
+        return "hadamard_pair_kernel"
+    if in_o <= 64 and not rope:
+        return "hadamard_pair_kloop_kernel"
+    return None
+
+
+def _had_meta(rows, in_o, out_o, dt, vec, kc1, swiglu=False, rope=False):
     esz = 2 if dt == torch.bfloat16 else 4
     tag = "bf16" if dt == torch.bfloat16 else "f32"
     if swiglu:
@@ -158,7 +174,9 @@ def _had_meta(rows, in_o, out_o, dt, vec, kc1, swiglu=False):
         nbytes = rows * 32 * (in_o + out_o) * esz + 2 * 32 * out_o * ((in_o + 3) // 4) + 8 * 32 * (in_o + out_o)
         flops = rows * 2 * (2 * 32 * in_o * out_o + 10 * 32 * (in_o + out_o)) + rows * 32 * out_o * 4
     else:
-        kname = "hadamard_fwd_kernel<%s,%s,%s>" % (tag, "vec" if vec else "scalar", "kc1" if kc1 else "kloop")
+        pair = _pair_shape(rows, in_o, out_o, dt, vec, rope)
+        kname = ("%s<%s>" % (pair, tag)) if pair else \
+            "hadamard_fwd_kernel<%s,%s,%s>" % (tag, "vec" if vec else "scalar", "kc1" if kc1 else "kloop")
         nbytes = rows * 32 * (in_o + out_o) * esz + 32 * out_o * ((in_o + 3) // 4) + 4 * 32 * (in_o + out_o)
         flops = rows * (2 * 32 * in_o * out_o + 10 * 32 * (in_o + out_o) + 32 * (in_o + out_o))
     return kname, nbytes, flops
@@ -190,7 +208,7 @@ def hadamard_linear_rope(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.
     beta = beta.detach().float().contiguous()
     vec = True
     kc1 = in_o <= 16
-    kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, vec, kc1)
+    kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, vec, kc1, rope=True)
     if in_o > 16 and out_o > 48:
         kname = "hadamard_wide3_kernel<bf16>" if dt == torch.bfloat16 and in_o <= 128 and out_o <= 128 else \
             "hadamard_wide_kernel<%s>" % ("bf16" if dt == torch.bfloat16 else "f32")
@@ -261,7 +279,8 @@ def hadamard_linear_multi(x: torch.Tensor, in_o: int, out_o: int, layers, freqs_
     arrs = [(ctypes.c_void_p * n)(*v) for v in (kws, als, bes, yps)]
     kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, True, in_o <= 16)
     nbytes = rows * 32 * (in_o + n * out_o) * x.element_size()
-    kname = "hadamard_fwdn_kernel<%s,x%d>" % ("bf16" if dt == torch.bfloat16 else "f32", n)
+    kname = ("hadamard_pair_kernel<bf16,x%d>" % n) if _pair_shape(rows, in_o, out_o, dt, True) == "hadamard_pair_kernel" \
+        else "hadamard_fwdn_kernel<%s,x%d>" % ("bf16" if dt == torch.bfloat16 else "f32", n)
     rope_args = (0 if table is None else table.data_ptr(), T, head_dim or 4, mask, _hip.dtype_code(dt),
                  _hip.stream(x.device))
     if all(o is None for o in outs):
