@@ -425,6 +425,39 @@ def test_hadamard_linear_multi_equals_single_launches(K, dtype, in_o, out_o, T):
         assert torch.equal(o, s)
 
 
+@pytest.mark.parametrize("rope", [False, True])
+def test_bf16_kernels_bitwise_across_tile_counts(K, rope):
+    """bf16 16x16 layers take wavefront pairs up to 2048 16-row tiles and the
+    pipelined one-wavefront kernel above; that kernel moves whole 512-value
+    rows through per-wave LDS areas when the rows are contiguous, and 32-byte
+    row segments per lane quad otherwise.  All compute the same butterflies
+    in the same order, so their outputs are equal bitwise."""
+    torch.manual_seed(11 + rope)
+    B, T, D = 5, 8001, 16   # 40005 rows: 2501 tiles, the last one ragged
+    codes = np.random.default_rng(11 + rope).integers(-1, 2, size=(32, 16, 16)).astype(np.int8)
+    kw = _prepare(K, codes)
+    a = (1 + 0.3 * torch.randn(32, 16)).cuda()
+    b = (0.2 * torch.randn(32, 16)).cuda()
+    x = torch.randn(B, T, 512, device="cuda").to(torch.bfloat16)
+    wide = torch.zeros(B, T, 1024, device="cuda", dtype=torch.bfloat16)
+    wide[:, :, 256:768] = x
+    xs = wide[:, :, 256:768]   # same values at row stride 1024
+    f = _freqs_cis(T, D).cuda()
+
+    def run(v):
+        return K.hadamard_linear_rope(v, 16, 16, kw, a, b, f, D) if rope else K.hadamard_linear(v, 16, 16, kw, a, b)
+    y = run(x)           # whole rows through LDS
+    y_seg = run(xs)      # row segments
+    y_pair = run(x[:4])  # 32004 rows: wavefront pairs
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_seg)
+    assert torch.equal(y[:4], y_pair)
+    if not rope:
+        tail = x[-1, -7:].float().cpu().numpy()
+        ref = ohad.hadamard_linear_f64(tail, codes, a.cpu().numpy(), b.cpu().numpy())
+        assert_close(y[-1, -7:].float().cpu().numpy(), ref, torch.bfloat16, "last rows")
+
+
 # --------------------------------------------------------------- decode-sized batches
 
 @pytest.mark.parametrize("in_o,out_o", [(128, 128), (100, 128), (128, 68), (36, 64)])

@@ -55,11 +55,26 @@ __global__ void hadamard_prepare_kernel(const uint8_t *__restrict__ packed, int 
 // DENSE: float weights instead of ternary codes (the Hadamard head mixer),
 // as matrix-core A fragments [Nt][Kc][32 g][64 lanes] (bf16x4 or f32x4)
 // copied into LDS in place of the code table.
+// Per-wave LDS area of the STAGED variant: the tile's 16 rows of 1 KB at a
+// pitch of 1 KB + 16 bytes, so the 64 lanes' 8-byte reads of one group
+// (row t, bytes 32 g + 8 q) fall on distinct banks.
+constexpr int kStagePitch = 1024 + 16;
+constexpr size_t kStageBytes = (size_t)kTile * kStagePitch;
+
 // PIPE1: the bf16 single-chunk, single-output-tile shape (in_o, out_o <= 16,
 // VEC, not DENSE) in its own software-pipelined loop.
-template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE, bool PIPE1 = false>
+// STAGED (with PIPE1): rows of exactly 512 contiguous bf16 on both sides
+// (in_o = out_o = gsx = gsy = 16, ldx = ldy = 512, plain rows).  Each wave
+// moves its tile as 16 whole 1 KB rows, 16 bytes per lane, through its own
+// LDS area (kStageRows rows at kStagePitch bytes) instead of loading and
+// storing 32-byte row segments per lane quad: the segment pattern alone
+// (16 rows x 32 bytes per instruction) holds a copy kernel to about half of
+// what whole-row accesses reach.  The arithmetic is PIPE1's, so the results
+// are equal bitwise.
+template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE, bool PIPE1 = false, bool STAGED = false>
 __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int nblk) {
     static_assert(!PIPE1 || (BF16MMA && VEC && KC1 && !DENSE), "PIPE1 shape");
+    static_assert(!STAGED || PIPE1, "STAGED is a PIPE1 variant");
     extern __shared__ __align__(16) unsigned char smem[];
     void *lut = smem;
     const size_t wbytes = DENSE ? (size_t)a.Nt * a.Kc * 32 * 64 * dense_frag_bytes<BF16MMA>() : lut_bytes<BF16MMA>();
@@ -138,12 +153,37 @@ __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int
         const f32x4 *al = alpha_l + q * 32;
         u32x2 xraw[32];
         int tile = blk * wt + wave;
-        {
+        // STAGED: the tile's rows (row i of the tile in xrow[i]) and the
+        // wave's LDS area
+        [[maybe_unused]] u32x4 xrow[STAGED ? kTile : 1];
+        [[maybe_unused]] unsigned char *area = (unsigned char *)(beta_l + a.Nt * 128) + (size_t)wave * kStageBytes;
+        [[maybe_unused]] auto load_rows = [&](int tl) {
+#pragma unroll
+            for (int i = 0; i < kTile; ++i) {
+                const int r = tl * kTile + i;
+                xrow[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)lane * 16,
+                                                                (tl < n_tiles && r < a.M) ? (uint32_t)r * 1024u : kOOB, 0);
+            }
+        };
+        if constexpr (STAGED) {
+            load_rows(tile);
+        } else {
             const uint32_t o0 = x_off(tile);
 #pragma unroll
             for (int g = 0; g < 32; ++g) xraw[g] = __builtin_amdgcn_raw_buffer_load_b64(xr, o0, (uint32_t)g * gsb, 0);
         }
         for (; tile < n_tiles; tile += stride) {
+            if constexpr (STAGED) {
+                // rows into the area, then each lane's 8 bytes of the 32
+                // groups of row t (the wave's LDS operations run in order;
+                // the fences keep the compiler from moving them)
+#pragma unroll
+                for (int i = 0; i < kTile; ++i) *(u32x4 *)(area + i * kStagePitch + lane * 16) = xrow[i];
+                wave_lds_fence();
+#pragma unroll
+                for (int g = 0; g < 32; ++g) xraw[g] = *(const u32x2 *)(area + t * kStagePitch + g * 32 + q * 8);
+                wave_lds_fence();
+            }
             const int row = tile * kTile + t;
             const bool row_ok = row < a.M;
             const uint32_t yoff = (uint32_t)((int64_t)row * a.ldy * esz);
@@ -173,7 +213,9 @@ __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int
                 // issued before it, so loads queued behind stores would wait
                 // for the stores
                 __builtin_amdgcn_sched_barrier(0);
-                {
+                if constexpr (STAGED) {
+                    load_rows(tile + stride);
+                } else {
                     const uint32_t on = x_off(tile + stride);
 #pragma unroll
                     for (int g = 0; g < 32; ++g)
@@ -199,13 +241,32 @@ __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int
                         for (int j = 0; j < 4; ++j) {
                             f32x4 r = acc[h0 + j] * b8[j];
                             if constexpr (decltype(with_rope)::value) r = rope_apply(r, cs);
-                            Buf4<uint16_t>::store(r, yr, voff, (uint32_t)(h0 + j) * hstride);
+                            if constexpr (STAGED) {
+                                u32x2 u;
+                                u.x = pack_bf16x2(r.x, r.y);
+                                u.y = pack_bf16x2(r.z, r.w);
+                                *(u32x2 *)(area + t * kStagePitch + (h0 + j) * 32 + q * 8) = u;
+                            } else {
+                                Buf4<uint16_t>::store(r, yr, voff, (uint32_t)(h0 + j) * hstride);
+                            }
                         }
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 };
                 if (rope) stores(std::true_type{});
                 else stores(std::false_type{});
+                if constexpr (STAGED) {
+                    // whole output rows out of the area (rows past M fall
+                    // outside the buffer and are dropped)
+                    wave_lds_fence();
+#pragma unroll
+                    for (int i = 0; i < kTile; ++i) {
+                        const u32x4 v = *(const u32x4 *)(area + i * kStagePitch + lane * 16);
+                        __builtin_amdgcn_raw_buffer_store_b128(v, yr, (uint32_t)lane * 16,
+                                                               (uint32_t)(tile * kTile + i) * 1024u, 0);
+                    }
+                    wave_lds_fence();
+                }
             }
         }
         return;
@@ -241,9 +302,9 @@ __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int
     }
 }
 
-template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE = false, bool PIPE1 = false>
+template <typename T, bool BF16MMA, bool VEC, bool KC1, bool DENSE = false, bool PIPE1 = false, bool STAGED = false>
 __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void hadamard_fwd_kernel(HadArgs a) {
-    hadamard_fwd_body<T, BF16MMA, VEC, KC1, DENSE, PIPE1>(a, blockIdx.x, gridDim.x);
+    hadamard_fwd_body<T, BF16MMA, VEC, KC1, DENSE, PIPE1, STAGED>(a, blockIdx.x, gridDim.x);
 }
 
 // Several Hadamard linears of one shape on the same input rows in one launch
@@ -1711,7 +1772,14 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
         } else {
 #define WALSH_HAD_LAUNCH(T, MMA, V, K1) launch((hadamard_fwd_kernel<T, MMA, V, K1>), G, B, lds, s, a)
             if (bf16) {
-                if (vec && kc1 && Nt == 1) launch((hadamard_fwd_kernel<uint16_t, true, true, true, false, true>), G, B, lds, s, a);
+                // whole 1 KB rows on both sides: through the per-wave LDS areas
+                const size_t st_lds = lds + (size_t)(a.wave_tiles > 0 ? a.wave_tiles : kWaves) * kStageBytes;
+                const bool staged = vec && kc1 && Nt == 1 && base.in_o == 16 && base.out_o == 16 && base.gsx == 16 &&
+                                    base.gsy == 16 && base.ldx == 512 && base.ldy == 512 && base.tpb == 0 &&
+                                    (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.y % 16 == 0 &&
+                                    st_lds <= (size_t)device_info().max_shared_per_block;
+                if (staged) launch((hadamard_fwd_kernel<uint16_t, true, true, true, false, true, true>), G, B, st_lds, s, a);
+                else if (vec && kc1 && Nt == 1) launch((hadamard_fwd_kernel<uint16_t, true, true, true, false, true>), G, B, lds, s, a);
                 else if (vec) { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, true, true); else WALSH_HAD_LAUNCH(uint16_t, true, true, false); }
                 else     { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, false, true); else WALSH_HAD_LAUNCH(uint16_t, true, false, false); }
             } else {
