@@ -532,7 +532,9 @@ def bench_hadamard(torch, args):
     # the same layer in bf16 (the dtype of the model configs) at prefill row counts
     sweep16 = []
     for rows in (65536, 262144, 1048576):
-        nbuf = max(1, min(16, (768 << 20) // (rows * 512 * 2 * 2)))
+        # at least two inputs, so the inputs alone exceed the 256 MB Infinity
+        # Cache (non-temporal output stores leave a lone input cached)
+        nbuf = max(2, min(16, (768 << 20) // (rows * 512 * 2 * 2)))
         gen = torch.Generator(device="cuda").manual_seed(0)
         xs = [torch.randn(rows, 512, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(nbuf)]
 

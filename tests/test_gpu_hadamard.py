@@ -427,11 +427,12 @@ def test_hadamard_linear_multi_equals_single_launches(K, dtype, in_o, out_o, T):
 
 @pytest.mark.parametrize("rope", [False, True])
 def test_bf16_kernels_bitwise_across_tile_counts(K, rope):
-    """bf16 16x16 layers take wavefront pairs up to 2048 16-row tiles and the
-    pipelined one-wavefront kernel above; that kernel moves whole 512-value
-    rows through per-wave LDS areas when the rows are contiguous, and 32-byte
-    row segments per lane quad otherwise.  All compute the same butterflies
-    in the same order, so their outputs are equal bitwise."""
+    """bf16 16x16 layers take wavefront pairs up to 1024 16-row tiles on
+    contiguous rows (2048 on strided ones) and the pipelined one-wavefront
+    kernel above; that kernel moves whole 512-value rows through per-wave LDS
+    areas when the rows are contiguous, and 32-byte row segments per lane quad
+    otherwise, for one layer or several in one launch.  All compute the same
+    butterflies in the same order, so their outputs are equal bitwise."""
     torch.manual_seed(11 + rope)
     B, T, D = 5, 8001, 16   # 40005 rows: 2501 tiles, the last one ragged
     codes = np.random.default_rng(11 + rope).integers(-1, 2, size=(32, 16, 16)).astype(np.int8)
@@ -448,10 +449,13 @@ def test_bf16_kernels_bitwise_across_tile_counts(K, rope):
         return K.hadamard_linear_rope(v, 16, 16, kw, a, b, f, D) if rope else K.hadamard_linear(v, 16, 16, kw, a, b)
     y = run(x)           # whole rows through LDS
     y_seg = run(xs)      # row segments
-    y_pair = run(x[:4])  # 32004 rows: wavefront pairs
+    y_pair = run(x[:2])  # 16002 rows: wavefront pairs
+    plain = K.hadamard_linear(x, 16, 16, kw, a, b)
+    multi = K.hadamard_linear_multi(x, 16, 16, [(kw, a, b, rope), (kw, a, b, False)], f, D)
     torch.cuda.synchronize()
     assert torch.equal(y, y_seg)
-    assert torch.equal(y[:4], y_pair)
+    assert torch.equal(y[:2], y_pair)
+    assert torch.equal(multi[0], y) and torch.equal(multi[1], plain)
     if not rope:
         tail = x[-1, -7:].float().cpu().numpy()
         ref = ohad.hadamard_linear_f64(tail, codes, a.cpu().numpy(), b.cpu().numpy())

@@ -60,6 +60,10 @@ __global__ void hadamard_prepare_kernel(const uint8_t *__restrict__ packed, int 
 // (row t, bytes 32 g + 8 q) fall on distinct banks.
 constexpr int kStagePitch = 1024 + 16;
 constexpr size_t kStageBytes = (size_t)kTile * kStagePitch;
+// Output size of one launch from which the STAGED variant stores
+// non-temporally: half the 256 MB Infinity Cache.  At 262,144 rows (256 MB
+// out) that takes one layer from 117 us to 102 us.
+constexpr int64_t kStreamOutBytes = (int64_t)128 << 20;
 
 // PIPE1: the bf16 single-chunk, single-output-tile shape (in_o, out_o <= 16,
 // VEC, not DENSE) in its own software-pipelined loop.
@@ -259,12 +263,18 @@ __device__ __forceinline__ void hadamard_fwd_body(const HadArgs &a, int blk, int
                     // whole output rows out of the area (rows past M fall
                     // outside the buffer and are dropped)
                     wave_lds_fence();
+                    auto store_rows = [&](auto aux) {
 #pragma unroll
-                    for (int i = 0; i < kTile; ++i) {
-                        const u32x4 v = *(const u32x4 *)(area + i * kStagePitch + lane * 16);
-                        __builtin_amdgcn_raw_buffer_store_b128(v, yr, (uint32_t)lane * 16,
-                                                               (uint32_t)(tile * kTile + i) * 1024u, 0);
-                    }
+                        for (int i = 0; i < kTile; ++i) {
+                            const u32x4 v = *(const u32x4 *)(area + i * kStagePitch + lane * 16);
+                            __builtin_amdgcn_raw_buffer_store_b128(v, yr, (uint32_t)lane * 16,
+                                                                   (uint32_t)(tile * kTile + i) * 1024u,
+                                                                   decltype(aux)::value);
+                        }
+                    };
+                    // cache policy 2: non-temporal
+                    if (a.nt_store) store_rows(std::integral_constant<int, 2>{});
+                    else store_rows(std::integral_constant<int, 0>{});
                     wave_lds_fence();
                 }
             }
@@ -317,10 +327,10 @@ struct HadArgsN {
     int n;
 };
 
-template <typename T, bool BF16MMA, bool VEC, bool KC1, bool PIPE1 = false>
+template <typename T, bool BF16MMA, bool VEC, bool KC1, bool PIPE1 = false, bool STAGED = false>
 __global__ __launch_bounds__(kThreads, (BF16MMA && KC1 && VEC) ? 2 : 1) void hadamard_fwdn_kernel(HadArgsN an) {
     const int l = blockIdx.x % an.n;
-    hadamard_fwd_body<T, BF16MMA, VEC, KC1, false, PIPE1>(an.p[l], blockIdx.x / an.n, gridDim.x / an.n);
+    hadamard_fwd_body<T, BF16MMA, VEC, KC1, false, PIPE1, STAGED>(an.p[l], blockIdx.x / an.n, gridDim.x / an.n);
 }
 
 // ---------------------------------------------------------------- wavefront pairs
@@ -355,6 +365,11 @@ constexpr int kPairThreads = 128;
 // while at 8,192 rows one layer takes 9.8 us against 14.2 us and q, k, v
 // 19.1 us against 23.8 us.
 constexpr int64_t kPairMaxTiles = 2048;
+// Where the one-wavefront kernel moves whole 1 KB rows through LDS (the
+// STAGED variant: 16x16 layers on contiguous rows) it is faster from fewer
+// tiles on: at 32,768 rows one layer takes 21.3 us against the pairs'
+// 22.7 us (20.9 against 22.8 from HBM), at 16,384 rows 16.1 against 15.0.
+constexpr int64_t kPairMaxTilesRows = 1024;
 constexpr size_t kPairLds = 256 * 8 + 2 * 128 * 16 + 2 * 8 * 64 * 16;   // lut, alpha/beta, exchange
 
 template <int HF, bool DENSE>
@@ -1687,6 +1702,14 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
     if (rows_max < kTile) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
     rows_max = balanced_rows(M, rows_max, kTile);
     const int64_t cap = (int64_t)device_info().cu_count * (swiglu ? 8 : 2);
+    // rows of exactly 512 contiguous bf16 on both sides (every chunk keeps
+    // the 16-byte alignment): the one-wavefront kernel's STAGED variant
+    const size_t st_lds_max = lds + (size_t)kWaves * kStageBytes;
+    const bool whole_rows = !swiglu && bf16 && vec && kc1 && Nt == 1 && base.in_o == 16 && base.out_o == 16 &&
+                            base.gsx == 16 && base.gsy == 16 && base.ldx == 512 && base.ldy == 512 && base.tpb == 0 &&
+                            (uintptr_t)base.x % 16 == 0 && (uintptr_t)base.y % 16 == 0 &&
+                            st_lds_max <= (size_t)device_info().max_shared_per_block;
+    const int64_t pair_max = whole_rows ? kPairMaxTilesRows : kPairMaxTiles;
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
         HadArgs a = base;
@@ -1762,8 +1785,8 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
                    ceil_div(rows, kTile) <= kPairMaxTiles) {
             // several input chunks, one output tile: a wavefront pair per tile
             pair_kloop_launch(a, rows, s);
-        } else if (bf16 && vec && kc1 && Nt == 1 && ceil_div(rows, kTile) <= kPairMaxTiles) {
-            // one input chunk, one output tile, up to kPairMaxTiles tiles: a
+        } else if (bf16 && vec && kc1 && Nt == 1 && ceil_div(rows, kTile) <= pair_max) {
+            // one input chunk, one output tile, up to pair_max tiles: a
             // wavefront pair per tile
             HadArgsN an;
             an.n = 1;
@@ -1774,11 +1797,8 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
             if (bf16) {
                 // whole 1 KB rows on both sides: through the per-wave LDS areas
                 const size_t st_lds = lds + (size_t)(a.wave_tiles > 0 ? a.wave_tiles : kWaves) * kStageBytes;
-                const bool staged = vec && kc1 && Nt == 1 && base.in_o == 16 && base.out_o == 16 && base.gsx == 16 &&
-                                    base.gsy == 16 && base.ldx == 512 && base.ldy == 512 && base.tpb == 0 &&
-                                    (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.y % 16 == 0 &&
-                                    st_lds <= (size_t)device_info().max_shared_per_block;
-                if (staged) launch((hadamard_fwd_kernel<uint16_t, true, true, true, false, true, true>), G, B, st_lds, s, a);
+                a.nt_store = rows * 1024 >= kStreamOutBytes;
+                if (whole_rows) launch((hadamard_fwd_kernel<uint16_t, true, true, true, false, true, true>), G, B, st_lds, s, a);
                 else if (vec && kc1 && Nt == 1) launch((hadamard_fwd_kernel<uint16_t, true, true, true, false, true>), G, B, lds, s, a);
                 else if (vec) { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, true, true); else WALSH_HAD_LAUNCH(uint16_t, true, true, false); }
                 else     { if (kc1) WALSH_HAD_LAUNCH(uint16_t, true, false, true); else WALSH_HAD_LAUNCH(uint16_t, true, false, false); }
@@ -1945,7 +1965,17 @@ static int hadamard_multi(const char *fn, const void *x, int64_t ldx, int64_t M,
         int64_t grid = ceil_div(ceil_div(rows, kTile), kWaves);
         if (grid > cap) grid = cap;
         const dim3 G((unsigned)(grid * n)), B(kThreads);
-        if (bf16 && Nt == 1 && ceil_div(rows, kTile) <= kPairMaxTiles) pair_launch(an, rows, s);
+        // whole 1 KB rows on both sides of every layer: through per-wave LDS areas
+        const size_t st_lds = lds + (size_t)kWaves * kStageBytes;
+        bool staged = bf16 && Nt == 1 && in_o == 16 && out_o == 16 && ldx == 512 && (uintptr_t)an.p[0].x % 16 == 0 &&
+                      st_lds <= (size_t)device_info().max_shared_per_block;
+        for (int i = 0; i < n; ++i) {
+            staged = staged && base[i].tpb == 0 && ldys[i] == 512 && (uintptr_t)an.p[i].y % 16 == 0;
+            an.p[i].nt_store = rows * 1024 >= kStreamOutBytes;
+        }
+        if (bf16 && Nt == 1 && ceil_div(rows, kTile) <= (staged ? kPairMaxTilesRows : kPairMaxTiles))
+            pair_launch(an, rows, s);
+        else if (staged) launch((hadamard_fwdn_kernel<uint16_t, true, true, true, true, true>), G, B, st_lds, s, an);
         else if (bf16 && Nt == 1) launch((hadamard_fwdn_kernel<uint16_t, true, true, true, true>), G, B, lds, s, an);
         else if (bf16) launch((hadamard_fwdn_kernel<uint16_t, true, true, true>), G, B, lds, s, an);
         else launch((hadamard_fwdn_kernel<float, false, true, true>), G, B, lds, s, an);

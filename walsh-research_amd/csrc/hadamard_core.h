@@ -67,6 +67,9 @@ struct HadArgs {
     // fewer tiles than wavefronts on the chip, one working wave per
     // workgroup spreads the tiles over every CU instead of a quarter of them.
     int wave_tiles;
+    // non-temporal output stores (whole-row variant): outputs far larger
+    // than the caches, which a later kernel would read from HBM anyway
+    int nt_store;
 };
 
 // The (cos, sin) of the lane's two output pairs o0..o0+3 (o0 % 4 == 0,

@@ -151,13 +151,24 @@ def hadamard_prepare(packed: torch.Tensor, in_o: int, out_o: int) -> torch.Tenso
 
 
 # 16-row tiles per layer up to which the library runs the bf16 single-output-tile
-# shapes on wavefront pairs (hadamard_pair_kernel / hadamard_pair_kloop_kernel)
+# shapes on wavefront pairs (hadamard_pair_kernel / hadamard_pair_kloop_kernel);
+# 16x16 layers on contiguous 512-value rows switch to the one-wavefront kernel
+# (whole rows through LDS) above PAIR_MAX_TILES_ROWS
 PAIR_MAX_TILES = 2048
+PAIR_MAX_TILES_ROWS = 1024
 
 
-def _pair_shape(rows, in_o, out_o, dt, vec, rope=False):
+def _whole_rows(in_o, out_o, ldx, dt, ptr):
+    """16x16 bf16 layer on 16-byte aligned rows of 512 contiguous values
+    (outputs allocated contiguous): the library's whole-row variant of the
+    one-wavefront kernel."""
+    return dt == torch.bfloat16 and in_o == 16 and out_o == 16 and ldx == 512 and ptr % 16 == 0
+
+
+def _pair_shape(rows, in_o, out_o, dt, vec, rope=False, whole_rows=False):
     """The pair kernel the library dispatches for this shape, or None."""
-    if dt != torch.bfloat16 or not vec or out_o > 16 or (rows + 15) // 16 > PAIR_MAX_TILES:
+    limit = PAIR_MAX_TILES_ROWS if whole_rows else PAIR_MAX_TILES
+    if dt != torch.bfloat16 or not vec or out_o > 16 or (rows + 15) // 16 > limit:
         return None
     if in_o <= 16:
         return "hadamard_pair_kernel"
@@ -166,7 +177,7 @@ def _pair_shape(rows, in_o, out_o, dt, vec, rope=False):
     return None
 
 
-def _had_meta(rows, in_o, out_o, dt, vec, kc1, swiglu=False, rope=False):
+def _had_meta(rows, in_o, out_o, dt, vec, kc1, swiglu=False, rope=False, whole_rows=False):
     esz = 2 if dt == torch.bfloat16 else 4
     tag = "bf16" if dt == torch.bfloat16 else "f32"
     if swiglu:
@@ -174,9 +185,11 @@ def _had_meta(rows, in_o, out_o, dt, vec, kc1, swiglu=False, rope=False):
         nbytes = rows * 32 * (in_o + out_o) * esz + 2 * 32 * out_o * ((in_o + 3) // 4) + 8 * 32 * (in_o + out_o)
         flops = rows * 2 * (2 * 32 * in_o * out_o + 10 * 32 * (in_o + out_o)) + rows * 32 * out_o * 4
     else:
-        pair = _pair_shape(rows, in_o, out_o, dt, vec, rope)
+        pair = _pair_shape(rows, in_o, out_o, dt, vec, rope, whole_rows)
         kname = ("%s<%s>" % (pair, tag)) if pair else \
             "hadamard_fwd_kernel<%s,%s,%s>" % (tag, "vec" if vec else "scalar", "kc1" if kc1 else "kloop")
+        if whole_rows and not pair:
+            kname = "hadamard_fwd_kernel<bf16,rows>"
         nbytes = rows * 32 * (in_o + out_o) * esz + 32 * out_o * ((in_o + 3) // 4) + 4 * 32 * (in_o + out_o)
         flops = rows * (2 * 32 * in_o * out_o + 10 * 32 * (in_o + out_o) + 32 * (in_o + out_o))
     return kname, nbytes, flops
@@ -208,7 +221,8 @@ def hadamard_linear_rope(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.
     beta = beta.detach().float().contiguous()
     vec = True
     kc1 = in_o <= 16
-    kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, vec, kc1, rope=True)
+    kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, vec, kc1, rope=True,
+                                     whole_rows=_whole_rows(in_o, out_o, ldx, dt, xv.data_ptr()))
     if in_o > 16 and out_o > 48:
         kname = "hadamard_wide3_kernel<bf16>" if dt == torch.bfloat16 and in_o <= 128 and out_o <= 128 else \
             "hadamard_wide_kernel<%s>" % ("bf16" if dt == torch.bfloat16 else "f32")
@@ -279,8 +293,10 @@ def hadamard_linear_multi(x: torch.Tensor, in_o: int, out_o: int, layers, freqs_
     arrs = [(ctypes.c_void_p * n)(*v) for v in (kws, als, bes, yps)]
     kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, True, in_o <= 16)
     nbytes = rows * 32 * (in_o + n * out_o) * x.element_size()
-    kname = ("hadamard_pair_kernel<bf16,x%d>" % n) if _pair_shape(rows, in_o, out_o, dt, True) == "hadamard_pair_kernel" \
-        else "hadamard_fwdn_kernel<%s,x%d>" % ("bf16" if dt == torch.bfloat16 else "f32", n)
+    whole = _whole_rows(in_o, out_o, ldx, dt, xv.data_ptr()) and all(o is None for o in outs)
+    kname = ("hadamard_pair_kernel<bf16,x%d>" % n) \
+        if _pair_shape(rows, in_o, out_o, dt, True, whole_rows=whole) == "hadamard_pair_kernel" \
+        else "hadamard_fwdn_kernel<%s,x%d%s>" % ("bf16" if dt == torch.bfloat16 else "f32", n, ",rows" if whole else "")
     rope_args = (0 if table is None else table.data_ptr(), T, head_dim or 4, mask, _hip.dtype_code(dt),
                  _hip.stream(x.device))
     if all(o is None for o in outs):
@@ -323,7 +339,8 @@ def hadamard_linear(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tenso
     esz = x.element_size()
     vec = gsx % 4 == 0 and gsy % 4 == 0 and ldx % 4 == 0 and xv.data_ptr() % (4 * esz) == 0
     kc1 = in_o <= 16 and (dt == torch.bfloat16 or out_o <= 16)
-    kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, vec, kc1)
+    whole = gsx == 16 and gsy == 16 and _whole_rows(in_o, out_o, ldx, dt, xv.data_ptr())
+    kname, nbytes, flops = _had_meta(rows, in_o, out_o, dt, vec, kc1, whole_rows=whole)
     if vec and in_o > 16 and out_o > 48:
         if dt == torch.bfloat16 and in_o <= 128 and out_o <= 128:
             kname = "hadamard_wide3_kernel<bf16>"
