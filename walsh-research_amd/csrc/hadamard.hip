@@ -1392,7 +1392,11 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1) ? 2 : 1) void hadamard_s
     __syncthreads();
 
     constexpr uint32_t esz = sizeof(T);
-    const int wave = tid >> 6, lane = tid & 63;
+    // with fewer working waves than wavefronts, the idle one rotates with
+    // the workgroup index, so the working waves of the workgroups on a CU
+    // spread over all four SIMDs instead of the same three
+    const int lane = tid & 63;
+    const int wave = ((tid >> 6) - (int)blockIdx.x) & (kWaves - 1);
     const int t = lane & 15, q = lane >> 4;
     SType *st = stash + wave * 32 * 64;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)g.M * g.ldx * esz));
