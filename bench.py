@@ -240,7 +240,13 @@ def main():
             for _ in range(args.steps):
                 step()
         kernels = lt.summary()
-        dom = max(kernels, key=lambda k: kernels[k]["ms"])
+        # the HBM roofline is quoted for the dominant HBM-bound kernel: the
+        # causal attention at head_dim 16 (between the q/k/v and output
+        # projections) is bound by its exponentials and VALU work, not by
+        # memory, so it is left out of the choice (its time stays in the
+        # breakdown and in whole_forward)
+        hbm_bound = [k for k in kernels if not k.startswith("prefill_attn")] or list(kernels)
+        dom = max(hbm_bound, key=lambda k: kernels[k]["ms"])
         d = kernels[dom]
         avg_ms = d["ms"] / d["launches"]
         bytes_per_launch = d["bytes"] / d["launches"]
