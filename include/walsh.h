@@ -223,6 +223,22 @@ int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64_t D, int64_t
                          int64_t x_tstride, const uint8_t *kweight, const float *beta, void *y, int64_t ldy, int dtype,
                          void *stream);
 
+/* walsh_head_mixer_proj_fwd: the attention block's head mixer followed by
+ *   its output projection (chassis.py:465-478: HadamardHeadMixerFused.forward,
+ *   fht_cuda.py:650-662, then self.wo, HadamardLinear.forward,
+ *   fht_cuda.py:489-519) in one launch, for head_dim 16, one group of 32
+ *   heads and a 16x16 projection, bf16.  x as in walsh_head_mixer_fwd; the
+ *   mixer's output rows are rounded to bf16 as walsh_head_mixer_fwd stores
+ *   them and go straight into the projection (mix_kweight from
+ *   walsh_hadamard_dense_prepare with w_io = 1, proj_kweight from
+ *   walsh_hadamard_prepare; proj_alpha may be NULL for all ones); y row
+ *   b*T + t at (b*T + t)*ldy, 512 values.  The result equals
+ *   walsh_head_mixer_fwd then walsh_hadamard_linear_fwd bitwise. */
+int walsh_head_mixer_proj_fwd(const void *x, int64_t B, int64_t T, int64_t x_bstride, int64_t x_hstride,
+                              int64_t x_tstride, const uint8_t *mix_kweight, const float *mix_beta,
+                              const uint8_t *proj_kweight, const float *proj_alpha, const float *proj_beta, void *y,
+                              int64_t ldy, int dtype, void *stream);
+
 /* ------------------------------------------------------------------ backward
  * Autograd of HadamardLinear.forward (src/model/fht_cuda.py:489-519) through
  * FHTFunction.backward (fht_cuda.py:328-332, H self-adjoint) and the

@@ -462,6 +462,33 @@ def test_bf16_kernels_bitwise_across_tile_counts(K, rope):
         assert_close(y[-1, -7:].float().cpu().numpy(), ref, torch.bfloat16, "last rows")
 
 
+@pytest.mark.parametrize("B,T,layout", [(8, 1024, "heads"), (3, 37, "heads"), (2, 50, "tokens")])
+def test_head_mixer_proj_bitwise_two_launches(K, B, T, layout):
+    """walsh_head_mixer_proj_fwd (the head mixer and the 16x16 output
+    projection in one launch) equals walsh_head_mixer_fwd followed by
+    walsh_hadamard_linear_fwd bitwise, on head-major x and on the attention
+    output's token-major layout viewed head-major."""
+    torch.manual_seed(B * T)
+    D = 16
+    if layout == "heads":
+        x = torch.randn(B, 32, T, D, device="cuda").to(torch.bfloat16)
+    else:
+        x = torch.randn(B, T, 32, D, device="cuda").to(torch.bfloat16).transpose(1, 2)
+    W = torch.randn(32, D, D, device="cuda") * 0.2
+    mkw = K.head_mixer_prepare(W, torch.bfloat16)
+    mbeta = (1 + 0.1 * torch.randn(D)).cuda()
+    codes = np.random.default_rng(B + T).integers(-1, 2, size=(32, 16, 16)).astype(np.int8)
+    pkw = _prepare(K, codes)
+    pa = (1 + 0.3 * torch.randn(32, 16)).cuda()
+    pb = (0.2 * torch.randn(32, 16)).cuda()
+    assert K.head_mixer_proj_supported(x, B * T)
+    y = K.head_mixer_proj(x, mkw, mbeta, pkw, pa, pb)
+    mid = K.head_mixer(x, mkw, mbeta)
+    ref = K.hadamard_linear(mid.view(B * T, 512), 16, 16, pkw, pa, pb).view(B, T, 512)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+
+
 # --------------------------------------------------------------- decode-sized batches
 
 @pytest.mark.parametrize("in_o,out_o", [(128, 128), (100, 128), (128, 68), (36, 64)])

@@ -516,6 +516,217 @@ __device__ __forceinline__ void pair_tile(const HadArgs &a, int tile, int lane, 
     }
 }
 
+// ---------------------------------------------------------------- head mixer + output projection
+// The attention block's head mixer (dense per-head weights, head_dim 16) and
+// the output projection (a 16x16 ternary Hadamard linear) on the same rows in
+// one launch, on wavefront pairs: the mixer's tile is computed as
+// hadamard_pair_kernel<true> computes it, rounded to bf16 as its store would
+// round it, handed to the projection's input layout through LDS and run
+// through the projection as hadamard_pair_kernel<false> runs it, so the
+// output equals the two launches' bitwise without the intermediate rows
+// going through memory.
+
+// Input transform (stages 1..8 local, 16 across the pair), the contraction of
+// groups g_in(s) and the output transform of pair_tile: v holds the scaled
+// inputs of groups 16 HF + s; on return acc[u] holds group g_out(u) before
+// beta.
+template <int HF, bool DENSE>
+__device__ __forceinline__ void pair_core(const HadArgs &a, int lane, const uint2 *__restrict__ lut, f32x4 *xch,
+                                          uint4 w0, uint4 w1, f32x4 (&v)[16], f32x4 (&acc)[16]) {
+    f32x4 *mine = xch + HF * 8 * 64, *theirs = xch + (1 - HF) * 8 * 64;
+#pragma unroll
+    for (int h = 1; h < 16; h <<= 1) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            if (s & h) continue;
+            const f32x4 x0 = v[s], x1 = v[s + h];
+            v[s] = x0 + x1;
+            v[s + h] = x0 - x1;
+        }
+    }
+    lds_barrier();   // the partner is done reading the previous exchange
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mine[j * 64 + lane] = v[HF ? j : j + 8];
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const f32x4 other = theirs[j * 64 + lane];
+        if (HF == 0) {
+            const f32x4 x0 = v[j], x1 = other;
+            v[j] = x0 + x1;
+            v[j + 8] = x0 - x1;
+        } else {
+            const f32x4 x0 = other, x1 = v[j + 8];
+            v[j] = x0 + x1;
+            v[j + 8] = x0 - x1;
+        }
+    }
+    u32x2 xm[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) xm[s] = u32x2{pack_bf16x2(v[s].x, v[s].y), pack_bf16x2(v[s].z, v[s].w)};
+    uint2 wd[16];
+    if constexpr (DENSE) {
+        const uint2 *wf = (const uint2 *)a.kw;   // [32 g][64 lanes] bf16x4
+#pragma unroll
+        for (int s = 0; s < 16; ++s) wd[s] = wf[(8 * HF + (s & 7) + 16 * (s >> 3)) * 64 + lane];
+    }
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        uint2 wa;
+        if constexpr (DENSE) {
+            wa = wd[s];
+        } else {
+            const uint32_t wb[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            const int g = 8 * HF + (s & 7) + 16 * (s >> 3);
+            wa = lut[(wb[g >> 2] >> (8 * (g & 3))) & 0xffu];
+        }
+        acc[s] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, wa),
+                                                            __builtin_bit_cast(i16x4, xm[s]),
+                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    }
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            if (s & h) continue;
+            const f32x4 x0 = acc[s], x1 = acc[s + h];
+            acc[s] = x0 + x1;
+            acc[s + h] = x0 - x1;
+        }
+    }
+    lds_barrier();   // the partner is done reading the input exchange
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int snd = (p & 3) + 4 * (1 - HF) + 8 * (p >> 2);
+        mine[p * 64 + lane] = acc[snd];
+    }
+    lds_barrier();
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int kept = (p & 3) + 4 * HF + 8 * (p >> 2);
+        const int lo = kept & ~4, hi = kept | 4;
+        const f32x4 other = theirs[p * 64 + lane];
+        const f32x4 x0 = HF == 0 ? acc[kept] : other;
+        const f32x4 x1 = HF == 0 ? other : acc[kept];
+        acc[lo] = x0 + x1;
+        acc[hi] = x0 - x1;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const f32x4 x0 = acc[u], x1 = acc[u + 8];
+        acc[u] = x0 + x1;
+        acc[u + 8] = x0 - x1;
+    }
+}
+
+template <int HF>
+__device__ __forceinline__ void mixproj_tile(const HadArgs &m, const HadArgs &p, int tile, int lane,
+                                             const uint2 *__restrict__ lut, const f32x4 *__restrict__ mbeta_l,
+                                             const f32x4 *__restrict__ palpha_l, const f32x4 *__restrict__ pbeta_l,
+                                             f32x4 *xch, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t yr) {
+    const int t = lane & 15, q = lane >> 4;
+    const int row = tile * kTile + t;
+    const bool row_ok = row < m.M;
+    f32x4 *mine = xch + HF * 8 * 64, *theirs = xch + (1 - HF) * 8 * 64;
+    uint4 w0, w1;
+    f32x4 v[16], acc[16];
+    {
+        // the mixer's input: heads 16 HF + s of the row (its alpha is 1)
+        const uint32_t gsb = (uint32_t)m.gsx * 2;
+        const uint32_t xo = row_ok ? x_row_off(m, row, 2) + (uint32_t)(8 * q) : kOOB;
+        u32x2 xraw[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            xraw[s] = __builtin_amdgcn_raw_buffer_load_b64(xr, xo, (uint32_t)(16 * HF + s) * gsb, 0);
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            v[s] = f32x4{__uint_as_float(xraw[s].x << 16), __uint_as_float(xraw[s].x & 0xffff0000u),
+                         __uint_as_float(xraw[s].y << 16), __uint_as_float(xraw[s].y & 0xffff0000u)};
+    }
+    pair_core<HF, true>(m, lane, lut, xch, w0, w1, v, acc);
+    // the projection's code bytes (requested here: live through the mixer
+    // they would push the kernel past its register budget)
+    load_w(p, 0, 0, lane, w0, w1);
+    // the mixer's beta and bf16 rounding: slot u holds group g_out(u)
+    const f32x4 *mb = mbeta_l + q * 32;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int h = (u & 3) + 4 * HF + 8 * ((u >> 2) & 1) + 16 * (u >> 3);
+        const f32x4 r = acc[u] * mb[h];
+        const uint32_t lo = pack_bf16x2(r.x, r.y), hi = pack_bf16x2(r.z, r.w);
+        acc[u] = f32x4{__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u), __uint_as_float(hi << 16),
+                       __uint_as_float(hi & 0xffff0000u)};
+    }
+    // to the projection's layout (groups 16 HF + s): slots u >> 3 == HF hold
+    // groups of this half, the others go to the partner
+    lds_barrier();   // the partner is done reading the output exchange
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mine[j * 64 + lane] = acc[8 * (1 - HF) + j];
+    lds_barrier();
+    const f32x4 *pa = palpha_l + q * 32 + 16 * HF;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int own = (j & 3) + 4 * HF + 8 * ((j >> 2) & 1);
+        const int other = (j & 3) + 4 * (1 - HF) + 8 * ((j >> 2) & 1);
+        v[own] = acc[8 * HF + j] * pa[own];
+        v[other] = theirs[j * 64 + lane] * pa[other];
+    }
+    pair_core<HF, false>(p, lane, lut, xch, w0, w1, v, acc);
+    // the projection's beta and the stores of groups g_out(u)
+    const int o0 = 4 * q;
+    const uint32_t voff = row_ok ? (uint32_t)((int64_t)row * p.ldy * 2) + (uint32_t)o0 * 2 : kOOB;
+    const uint32_t hstride = (uint32_t)p.gsy * 2;
+    const f32x4 *pb = pbeta_l + q * 32;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int h = (u & 3) + 4 * HF + 8 * ((u >> 2) & 1) + 16 * (u >> 3);
+        Buf4<uint16_t>::store(acc[u] * pb[h], yr, voff, (uint32_t)h * hstride);
+    }
+}
+
+constexpr size_t kMixProjLds = 256 * 8 + 3 * 128 * 16 + 2 * 8 * 64 * 16;   // lut, 3 tables, exchange
+
+// m: the mixer (HadArgs of walsh_head_mixer_fwd), p: the projection (in_o =
+// out_o = 16, its x unused: the mixer's output rows).
+__global__ __launch_bounds__(kPairThreads, 2) void hadamard_pair_mixproj_kernel(HadArgs m, HadArgs p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint2 *lut = (uint2 *)smem;
+    f32x4 *mbeta_l = (f32x4 *)(smem + 256 * 8);   // [4 q][32 h]
+    f32x4 *palpha_l = mbeta_l + 128;               // [4 q][32 g]
+    f32x4 *pbeta_l = palpha_l + 128;               // [4 q][32 h]
+    f32x4 *xch = pbeta_l + 128;                    // [2 HF][8][64 lanes]
+    const int tid = threadIdx.x;
+    for (int e = tid; e < 256; e += kPairThreads) {
+        float val[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) val[j] = (float)((int)(((uint32_t)e >> (6 - 2 * j)) & 3u) - 1);
+        lut[e] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
+    }
+    {
+        const int e = tid;   // (q, g) = (e >> 5, e & 31); kPairThreads == 128 entries
+        const int g = e & 31, i0 = 4 * (e >> 5);
+        f32x4 mb, pa, pb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            mb[j] = m.beta[g * m.beta_h + i0 + j] * 0.03125f;
+            pa[j] = p.alpha ? p.alpha[g * p.in_o + i0 + j] : 1.f;
+            pb[j] = p.beta[g * p.beta_h + i0 + j] * 0.03125f;
+        }
+        mbeta_l[e] = mb;
+        palpha_l[e] = pa;
+        pbeta_l[e] = pb;
+    }
+    __syncthreads();
+    const int hf = tid >> 6, lane = tid & 63;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(m.x, x_bytes(m, 2));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(p.y, (uint32_t)((int64_t)m.M * p.ldy * 2));
+    const int n_tiles = (int)ceil_div(m.M, kTile);
+    for (int tile = (int)blockIdx.x; tile < n_tiles; tile += (int)gridDim.x) {
+        if (hf == 0) mixproj_tile<0>(m, p, tile, lane, lut, mbeta_l, palpha_l, pbeta_l, xch, xr, yr);
+        else mixproj_tile<1>(m, p, tile, lane, lut, mbeta_l, palpha_l, pbeta_l, xch, xr, yr);
+    }
+}
+
 template <int HF>
 __device__ __forceinline__ void pair_tile_kloop(const HadArgs &a, int tile, int lane, const uint2 *__restrict__ lut,
                                           const f32x4 *__restrict__ alpha_l, const f32x4 *__restrict__ beta_l,
@@ -2144,6 +2355,46 @@ WALSH_EXPORT int walsh_head_mixer_fwd(const void *x, int64_t B, int64_t T, int64
         else     { if (kc1) WALSH_MIX_LAUNCH(float, false, false, true); else WALSH_MIX_LAUNCH(float, false, false, false); }
     }
 #undef WALSH_MIX_LAUNCH
+    return check_hip(hipGetLastError(), fn);
+}
+
+WALSH_EXPORT int walsh_head_mixer_proj_fwd(const void *x, int64_t B, int64_t T, int64_t x_bstride, int64_t x_hstride,
+                                           int64_t x_tstride, const uint8_t *mix_kweight, const float *mix_beta,
+                                           const uint8_t *proj_kweight, const float *proj_alpha,
+                                           const float *proj_beta, void *y, int64_t ldy, int dtype, void *stream) {
+    const char *fn = "walsh_head_mixer_proj_fwd";
+    if (!x || !y || !mix_kweight || !mix_beta || !proj_kweight || !proj_beta)
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (B < 0 || T < 0 || ldy < 512 || x_tstride < 16 || x_hstride < 16 || x_bstride < 0)
+        return set_error(WALSH_EINVAL, "%s: bad shape B=%lld T=%lld ldy=%lld", fn, (long long)B, (long long)T,
+                         (long long)ldy);
+    if (dtype != WALSH_BF16) return set_error(WALSH_ENOTSUP, "%s: bf16 only (dtype %d)", fn, dtype);
+    if (x_hstride % 4 || x_tstride % 4 || x_bstride % 4 || ldy % 4 || (uintptr_t)x % 8 || (uintptr_t)y % 8)
+        return set_error(WALSH_ENOTSUP, "%s: strides and pointers must be 4-element aligned", fn);
+    const int64_t M = B * T;
+    if (M == 0) return WALSH_OK;
+    const int64_t xspan = (B - 1) * x_bstride + 31 * x_hstride + (T - 1) * x_tstride + 16;
+    if (xspan * 2 > (int64_t)kMaxBufferBytes || M * ldy * 2 > (int64_t)kMaxBufferBytes || M > INT32_MAX)
+        return set_error(WALSH_ENOTSUP, "%s: tensors above 2^31 bytes", fn);
+    HadArgs m = had_args(x, x_tstride, x_hstride, 16, 16, mix_kweight, nullptr, mix_beta, y, ldy, 16);
+    m.kw3 = nullptr;
+    m.beta_h = 0;  // one beta row for all heads
+    m.M = (int)M;
+    m.tpb = (int)T;
+    m.bstride = x_bstride;
+    m.xspan = xspan;
+    HadArgs p = had_args(y, ldy, 16, 16, 16, proj_kweight, proj_alpha, proj_beta, y, ldy, 16);
+    p.M = (int)M;
+    // one wavefront pair per 16-row tile, up to the pairs the CUs hold at
+    // once (LDS: kMixProjLds each; registers: 2 wavefronts per SIMD, where
+    // 3 would spill)
+    int64_t per_cu = (int64_t)(65536 + 98304) / (int64_t)kMixProjLds;
+    if (per_cu > 4) per_cu = 4;
+    const int64_t resident = (int64_t)device_info().cu_count * per_cu;
+    int64_t grid = ceil_div(M, kTile);
+    if (grid > resident) grid = resident;
+    launch(hadamard_pair_mixproj_kernel, dim3((unsigned)grid), dim3(kPairThreads), (uint32_t)kMixProjLds,
+           (hipStream_t)stream, m, p);
     return check_hip(hipGetLastError(), fn);
 }
 

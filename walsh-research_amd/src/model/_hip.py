@@ -49,6 +49,7 @@ SIGNATURES = {
     "walsh_hadamard_dense_weight_bytes": (_I64, [_I64, _I64, _I]),
     "walsh_hadamard_dense_prepare": (_I, [_P, _I64, _I64, _I, _I, _P, _P]),
     "walsh_head_mixer_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I, _P]),
+    "walsh_head_mixer_proj_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _I, _P]),
     "walsh_hadamard_pack_transpose": (_I, [_P, _I64, _I64, _P, _P]),
     "walsh_hadamard_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I]),
     "walsh_hadamard_linear_bwd": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P, _P,

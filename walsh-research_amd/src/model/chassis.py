@@ -217,6 +217,22 @@ class CausalSelfAttention(nn.Module):
         return kernels.hadamard_linear_multi(x, inner[0].in_o, inner[0].out_o, layers, freqs_cis, self.head_dim,
                                              outs=outs)
 
+    def _mixer_proj(self, yg, B, T):
+        """The head mixer and the output projection in one launch
+        (kernels.head_mixer_proj, bitwise the two launches): inference in
+        bf16 with head_dim 16, one group of 32 heads and a 16x16 Hadamard
+        output projection; None where that does not hold."""
+        wo = getattr(self.wo, "inner", self.wo)
+        if (yg.shape[1] != 1 or self.head_dim != 16 or getattr(wo, "in_o", 0) != 16 or getattr(wo, "out_o", 0) != 16
+                or not hasattr(wo, "ternary_state") or not hasattr(self.head_mixer, "_kweight")):
+            return None
+        x = yg[:, 0]
+        if act_dtype(x) != torch.bfloat16 or not kernels.head_mixer_proj_supported(x, B * T) or wo._needs_grad(x):
+            return None
+        _, _, kw = wo.ternary_state()
+        return kernels.head_mixer_proj(x, self.head_mixer._kweight(torch.bfloat16), self.head_mixer.beta, kw,
+                                       wo.alpha, wo.beta)
+
     def forward(self, x, freqs_cis, kv_cache: Optional[KVCache] = None, layer_idx: int = 0):
         B, T, C = x.size()
         dt = act_dtype(x)
@@ -278,6 +294,9 @@ class CausalSelfAttention(nn.Module):
             n_groups = self.n_head // self.mixer_dim
             yg = y.view(B, n_groups, self.mixer_dim, T, self.head_dim)
             if hasattr(self.head_mixer, "forward_rows") and self.head_mixer.uses_kernel(y):
+                fused = self._mixer_proj(yg, B, T)
+                if fused is not None:
+                    return fused
                 # the mixer kernel writes each group's heads straight into
                 # the token-major rows: no cat and no transpose copy
                 gw = self.mixer_dim * self.head_dim

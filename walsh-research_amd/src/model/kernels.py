@@ -515,6 +515,41 @@ def head_mixer(x: torch.Tensor, kweight: torch.Tensor, beta: torch.Tensor, out: 
     return y
 
 
+def head_mixer_proj_supported(x: torch.Tensor, rows: int) -> bool:
+    """Can head_mixer_proj take x [B, 32, T, 16] (bf16, 4-element aligned
+    strides and pointer) at this many rows?  Above PAIR_MAX_TILES_ROWS tiles
+    the output projection's whole-row kernel is the faster second launch."""
+    return (x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 4 and tuple(x.shape[1:2]) == (32,)
+            and x.shape[3] == 16 and x.stride(3) == 1 and all(st % 4 == 0 for st in x.stride()[:3])
+            and x.data_ptr() % 8 == 0 and 0 < rows <= 16 * PAIR_MAX_TILES_ROWS)
+
+
+def head_mixer_proj(x: torch.Tensor, mix_kweight: torch.Tensor, mix_beta: torch.Tensor, proj_kweight: torch.Tensor,
+                    proj_alpha: torch.Tensor, proj_beta: torch.Tensor) -> torch.Tensor:
+    """The head mixer (HadamardHeadMixerFused.forward, fht_cuda.py:650-662) and
+    the attention output projection (a 16x16 HadamardLinear, fht_cuda.py:489-519)
+    on x [B, 32, T, 16] bf16 in one launch: the token-major rows [B, T, 512],
+    bitwise head_mixer followed by hadamard_linear."""
+    _hip.require_device(x, "input")
+    B, Hh, T, D = x.shape
+    assert Hh == 32 and D == 16 and x.dtype == torch.bfloat16, f"head_mixer_proj: x {tuple(x.shape)} {x.dtype}"
+    y = torch.empty(B, T, 512, device=x.device, dtype=x.dtype)
+    if B * T == 0:
+        return y
+    mb = mix_beta.detach().float().contiguous()
+    pa = proj_alpha.detach().float().contiguous()
+    pb = proj_beta.detach().float().contiguous()
+    assert mb.numel() == 16 and pa.numel() == 512 and pb.numel() == 512, "head_mixer_proj: parameter shapes"
+    rows = B * T
+    nbytes = 2 * rows * 512 * 2 + mix_kweight.numel() + proj_kweight.numel() + 4 * (16 + 1024)
+    flops = rows * 2 * (2 * 32 * 16 * 16 + 10 * 32 * 16 + 32 * 16)
+    _hip.call("walsh_head_mixer_proj_fwd", x.data_ptr(), B, T, x.stride(0), x.stride(1), x.stride(2),
+              mix_kweight.data_ptr(), mb.data_ptr(), proj_kweight.data_ptr(), pa.data_ptr(), pb.data_ptr(),
+              y.data_ptr(), 512, _hip.dtype_code(x.dtype), _hip.stream(x.device),
+              kernel="head_mixer_proj<bf16>", nbytes=nbytes, flops=flops)
+    return y
+
+
 # ------------------------------------------------------------------ octonion
 
 def octonion_prepare(packed: torch.Tensor, in_o: int, out_o: int, dtype: torch.dtype) -> torch.Tensor:
