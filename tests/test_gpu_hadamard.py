@@ -462,6 +462,28 @@ def test_bf16_kernels_bitwise_across_tile_counts(K, rope):
         assert_close(y[-1, -7:].float().cpu().numpy(), ref, torch.bfloat16, "last rows")
 
 
+@pytest.mark.parametrize("in_o", [24, 43, 64])
+def test_bf16_chunk_kernels_bitwise_across_tile_counts(K, in_o):
+    """bf16 layers with 2-4 input chunks and one output tile run on one
+    wavefront pair per chunk and tile up to 2048 tiles, and on the
+    one-wavefront chunk loop above; both accumulate the chunks in order
+    through one matrix-core chain, so their outputs are equal bitwise."""
+    rng = np.random.default_rng(in_o)
+    torch.manual_seed(in_o)
+    M = 2048 * 16 + 35   # 2051 tiles
+    codes = rng.integers(-1, 2, size=(32, 16, in_o)).astype(np.int8)
+    kw = _prepare(K, codes)
+    a = (1 + 0.3 * torch.randn(32, in_o)).cuda()
+    b = (0.2 * torch.randn(32, 16)).cuda()
+    x = torch.randn(M, 32 * in_o, device="cuda").to(torch.bfloat16)
+    y = K.hadamard_linear(x, in_o, 16, kw, a, b)
+    y_pair = K.hadamard_linear(x[:5003], in_o, 16, kw, a, b)   # 313 tiles, the last one ragged
+    torch.cuda.synchronize()
+    assert torch.equal(y[:5003], y_pair)
+    ref = ohad.hadamard_linear_f64(x[4996:5003].float().cpu().numpy(), codes, a.cpu().numpy(), b.cpu().numpy())
+    assert_close(y_pair[-7:].float().cpu().numpy(), ref, torch.bfloat16, f"in_o={in_o} last rows")
+
+
 @pytest.mark.parametrize("B,T,layout", [(8, 1024, "heads"), (3, 37, "heads"), (2, 50, "tokens")])
 def test_head_mixer_proj_bitwise_two_launches(K, B, T, layout):
     """walsh_head_mixer_proj_fwd (the head mixer and the 16x16 output

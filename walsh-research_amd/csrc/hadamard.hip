@@ -727,48 +727,45 @@ __global__ __launch_bounds__(kPairThreads, 2) void hadamard_pair_mixproj_kernel(
     }
 }
 
+// The pair kernel for several input chunks: bf16, 16 < in_o <= 64, out_o <= 16 (2 to 4 input chunks, one output tile),
+// no RoPE: the FFN down projection at n_embd 512.  A workgroup of Kc
+// wavefront pairs per 16-row tile.  Pair c loads input chunk c and runs its
+// input transform and stage-16 exchange (the bulk of the dependent chain,
+// now Kc-way parallel); pairs 1 .. Kc - 1 hand their packed inputs (the
+// products' B operands) to pair 0 through their exchange areas; pair 0 runs the
+// contraction in chunk order (one accumulator chain, as the chunk loop does),
+// the output transform and the stores: results equal hadamard_fwd_kernel's
+// chunk loop bitwise.  Every wavefront passes the same barriers (six per tile).
+constexpr int kPairMaxKc = 4;
+constexpr int kKparMaxKc = kPairMaxKc;
+constexpr size_t kpar_lds(int Kc) { return 256 * 8 + (size_t)(Kc + 1) * 128 * 16 + (size_t)Kc * 2 * 8 * 64 * 16; }
+
 template <int HF>
-__device__ __forceinline__ void pair_tile_kloop(const HadArgs &a, int tile, int lane, const uint2 *__restrict__ lut,
+__device__ __forceinline__ void kpar_tile(const HadArgs &a, int tile, int pair, int lane, const uint2 *__restrict__ lut,
                                           const f32x4 *__restrict__ alpha_l, const f32x4 *__restrict__ beta_l,
-                                          f32x4 *__restrict__ xch, __amdgpu_buffer_rsrc_t xr,
-                                          __amdgpu_buffer_rsrc_t yr) {
+                                          f32x4 *xch_all, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t yr) {
     const int t = lane & 15, q = lane >> 4;
     const int row = tile * kTile + t;
     const bool row_ok = row < a.M;
+    f32x4 *xch = xch_all + pair * 2 * 8 * 64;
     f32x4 *mine = xch + HF * 8 * 64, *theirs = xch + (1 - HF) * 8 * 64;
-    // input chunks c = 0 .. Kc - 1 (columns 16c + 4q .. + 3), each through the
-    // input transform and the exchange, accumulated into the 16 products in
-    // chunk order (as hadamard_fwd_kernel's chunk loop does)
-    f32x4 acc[16];
-#pragma unroll
-    for (int s = 0; s < 16; ++s) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint32_t gsb = (uint32_t)a.gsx * 2;
-    const uint32_t xrow = row_ok ? x_row_off(a, row, 2) : 0u;
-    // chunk c + 1's x is requested while chunk c is transformed
-    auto load_chunk = [&](int c, u32x2 (&dst)[16]) {
+    const int c = pair;   // this pair's input chunk: columns 16c + 4q .. + 3
+    u32x2 xm[16];
+    {
+        const uint32_t gsb = (uint32_t)a.gsx * 2;
         const int i0 = kKChunk * c + 4 * q;
-        const uint32_t xo = (c < a.Kc && row_ok && i0 < a.in_o) ? xrow + (uint32_t)(2 * i0) : kOOB;
+        const uint32_t xo = (row_ok && i0 < a.in_o) ? x_row_off(a, row, 2) + (uint32_t)(2 * i0) : kOOB;
+        u32x2 xraw[16];
 #pragma unroll
-        for (int s = 0; s < 16; ++s) dst[s] = __builtin_amdgcn_raw_buffer_load_b64(xr, xo, (uint32_t)(16 * HF + s) * gsb, 0);
-    };
-    u32x2 xnext[16];
-    load_chunk(0, xnext);
-    for (int c = 0; c < a.Kc; ++c) {
-        uint4 w0, w1;
-        load_w(a, 0, c, lane, w0, w1);
+        for (int s = 0; s < 16; ++s)
+            xraw[s] = __builtin_amdgcn_raw_buffer_load_b64(xr, xo, (uint32_t)(16 * HF + s) * gsb, 0);
+        const f32x4 *al = alpha_l + (c * 4 + q) * 32 + 16 * HF;
         f32x4 v[16];
-        {
-            u32x2 xraw[16];
 #pragma unroll
-            for (int s = 0; s < 16; ++s) xraw[s] = xnext[s];
-            if (c + 1 < a.Kc) load_chunk(c + 1, xnext);
-            const f32x4 *al = alpha_l + (c * 4 + q) * 32 + 16 * HF;
-#pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const f32x4 x4 = {__uint_as_float(xraw[s].x << 16), __uint_as_float(xraw[s].x & 0xffff0000u),
-                                  __uint_as_float(xraw[s].y << 16), __uint_as_float(xraw[s].y & 0xffff0000u)};
-                v[s] = x4 * al[s];
-            }
+        for (int s = 0; s < 16; ++s) {
+            const f32x4 x4 = {__uint_as_float(xraw[s].x << 16), __uint_as_float(xraw[s].x & 0xffff0000u),
+                              __uint_as_float(xraw[s].y << 16), __uint_as_float(xraw[s].y & 0xffff0000u)};
+            v[s] = x4 * al[s];
         }
 #pragma unroll
         for (int h = 1; h < 16; h <<= 1) {
@@ -780,10 +777,10 @@ __device__ __forceinline__ void pair_tile_kloop(const HadArgs &a, int tile, int 
                 v[s + h] = x0 - x1;
             }
         }
-        lds_barrier();   // the partner is done reading the previous exchange
+        lds_barrier();   // B1: every wave is done with the previous tile's areas
 #pragma unroll
         for (int j = 0; j < 8; ++j) mine[j * 64 + lane] = v[HF ? j : j + 8];
-        lds_barrier();
+        lds_barrier();   // B2
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const f32x4 other = theirs[j * 64 + lane];
@@ -791,114 +788,127 @@ __device__ __forceinline__ void pair_tile_kloop(const HadArgs &a, int tile, int 
             v[j] = x0 + x1;
             v[j + 8] = x0 - x1;
         }
-        const uint32_t wb[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const int g = 8 * HF + (s & 7) + 16 * (s >> 3);
-            const u32x2 xm = {pack_bf16x2(v[s].x, v[s].y), pack_bf16x2(v[s].z, v[s].w)};
-            acc[s] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-                __builtin_bit_cast(i16x4, lut[(wb[g >> 2] >> (8 * (g & 3))) & 0xffu]), __builtin_bit_cast(i16x4, xm),
-                acc[s], 0, 0, 0);
+        for (int s = 0; s < 16; ++s) xm[s] = u32x2{pack_bf16x2(v[s].x, v[s].y), pack_bf16x2(v[s].z, v[s].w)};
+    }
+    lds_barrier();   // B3: the partner has read this wave's exchange slots
+    if (pair > 0) {
+        u32x2 *out = (u32x2 *)mine;   // 16 slots x 64 lanes x 8 bytes: the wave's half of the area
+#pragma unroll
+        for (int s = 0; s < 16; ++s) out[s * 64 + lane] = xm[s];
+    }
+    lds_barrier();   // B4
+    f32x4 acc[16];
+    if (pair == 0) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int cc = 0; cc < a.Kc; ++cc) {
+            uint4 w0, w1;
+            load_w(a, 0, cc, lane, w0, w1);
+            u32x2 xc[16];
+            if (cc == 0) {
+#pragma unroll
+                for (int s = 0; s < 16; ++s) xc[s] = xm[s];
+            } else {
+                const u32x2 *in = (const u32x2 *)(xch_all + cc * 2 * 8 * 64 + HF * 8 * 64);
+#pragma unroll
+                for (int s = 0; s < 16; ++s) xc[s] = in[s * 64 + lane];
+            }
+            const uint32_t wb[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int g = 8 * HF + (s & 7) + 16 * (s >> 3);
+                acc[s] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                    __builtin_bit_cast(i16x4, lut[(wb[g >> 2] >> (8 * (g & 3))) & 0xffu]),
+                    __builtin_bit_cast(i16x4, xc[s]), acc[s], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                if (s & h) continue;
+                const f32x4 x0 = acc[s], x1 = acc[s + h];
+                acc[s] = x0 + x1;
+                acc[s + h] = x0 - x1;
+            }
         }
     }
-    // output stages 1, 2, 4 within (s & 7)
+    lds_barrier();   // B5: pair 0's area was last read before B3
+    if (pair == 0) {
 #pragma unroll
-    for (int h = 1; h < 8; h <<= 1) {
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            if (s & h) continue;
-            const f32x4 x0 = acc[s], x1 = acc[s + h];
-            acc[s] = x0 + x1;
-            acc[s + h] = x0 - x1;
+        for (int p = 0; p < 8; ++p) {
+            const int snd = (p & 3) + 4 * (1 - HF) + 8 * (p >> 2);
+            mine[p * 64 + lane] = acc[snd];
         }
     }
-    // output stage 8 across the pair: HF keeps slots with (s & 4) == 4 HF
-    lds_barrier();   // the partner is done reading the input exchange
-#pragma unroll
-    for (int p = 0; p < 8; ++p) {
-        const int snd = (p & 3) + 4 * (1 - HF) + 8 * (p >> 2);
-        mine[p * 64 + lane] = acc[snd];
-    }
-    lds_barrier();
+    lds_barrier();   // B6
+    if (pair != 0) return;
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
         const int kept = (p & 3) + 4 * HF + 8 * (p >> 2);
         const int lo = kept & ~4, hi = kept | 4;
         const f32x4 other = theirs[p * 64 + lane];
-        const f32x4 x0 = HF == 0 ? acc[kept] : other;   // group with bit 3 clear
-        const f32x4 x1 = HF == 0 ? other : acc[kept];   // its partner + 8
+        const f32x4 x0 = HF == 0 ? acc[kept] : other;
+        const f32x4 x1 = HF == 0 ? other : acc[kept];
         acc[lo] = x0 + x1;
         acc[hi] = x0 - x1;
     }
-    // output stage 16: slots u, u + 8
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const f32x4 x0 = acc[u], x1 = acc[u + 8];
         acc[u] = x0 + x1;
         acc[u + 8] = x0 - x1;
     }
-    // beta (and RoPE), stores of groups g_out(u)
     const int o0 = 4 * q;
     const bool ok = row_ok && o0 < a.out_o;
     const uint32_t voff = ok ? (uint32_t)((int64_t)row * a.ldy * 2) + (uint32_t)o0 * 2 : kOOB;
     const uint32_t hstride = (uint32_t)a.gsy * 2;
     const f32x4 *bl = beta_l + q * 32;
-    if (a.rope) {
-        const f32x4 cs = ok ? rope_cs(a, row, o0) : f32x4{1.f, 0.f, 1.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int h = (u & 3) + 4 * HF + 8 * ((u >> 2) & 1) + 16 * (u >> 3);
-            Buf4<uint16_t>::store(rope_apply(acc[u] * bl[h], cs), yr, voff, (uint32_t)h * hstride);
-        }
-    } else {
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int h = (u & 3) + 4 * HF + 8 * ((u >> 2) & 1) + 16 * (u >> 3);
-            Buf4<uint16_t>::store(acc[u] * bl[h], yr, voff, (uint32_t)h * hstride);
-        }
+    for (int u = 0; u < 16; ++u) {
+        const int h = (u & 3) + 4 * HF + 8 * ((u >> 2) & 1) + 16 * (u >> 3);
+        Buf4<uint16_t>::store(acc[u] * bl[h], yr, voff, (uint32_t)h * hstride);
     }
 }
 
-// The pair kernel for several input chunks (in_o <= 64, one output tile;
-// the FFN down projection at n_embd 512): the same tile with a chunk loop.
-constexpr int kPairMaxKc = 4;
-constexpr size_t pair_kloop_lds(int Kc) { return 256 * 8 + (size_t)(Kc + 1) * 128 * 16 + 2 * 8 * 64 * 16; }
-
-__global__ __launch_bounds__(kPairThreads, 2) void hadamard_pair_kloop_kernel(HadArgs a) {
+// blockDim.x = 128 * Kc (2 <= Kc <= kKparMaxKc), no RoPE.
+__global__ __launch_bounds__(kPairThreads * kKparMaxKc, 3) void hadamard_pair_kpar_kernel(HadArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     uint2 *lut = (uint2 *)smem;
     f32x4 *alpha_l = (f32x4 *)(smem + 256 * 8);   // [Kc][4 q][32 g]
     f32x4 *beta_l = alpha_l + a.Kc * 128;          // [4 q][32 h]
-    f32x4 *xch = beta_l + 128;                     // [2 HF][8][64 lanes]
-    const int tid = threadIdx.x;
-    for (int e = tid; e < 256; e += kPairThreads) {
+    f32x4 *xch = beta_l + 128;                     // [Kc pairs][2 HF][8][64 lanes]
+    const int tid = threadIdx.x, nthr = (int)blockDim.x;
+    for (int e = tid; e < 256; e += nthr) {
         float val[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) val[j] = (float)((int)(((uint32_t)e >> (6 - 2 * j)) & 3u) - 1);
         lut[e] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
     }
-    for (int e = tid; e < a.Kc * 128; e += kPairThreads) {   // e = (c*4 + q)*32 + g
+    for (int e = tid; e < a.Kc * 128; e += nthr) {   // e = (c*4 + q)*32 + g
         const int g = e & 31, i0 = 4 * (e >> 5);
         f32x4 va;
 #pragma unroll
         for (int j = 0; j < 4; ++j) va[j] = (i0 + j < a.in_o) ? (a.alpha ? a.alpha[g * a.in_o + i0 + j] : 1.f) : 0.f;
         alpha_l[e] = va;
     }
-    {
-        const int e = tid, h = e & 31, o0 = 4 * (e >> 5);
+    for (int e = tid; e < 128; e += nthr) {
+        const int h = e & 31, o0 = 4 * (e >> 5);
         f32x4 vb;
 #pragma unroll
         for (int j = 0; j < 4; ++j) vb[j] = (o0 + j < a.out_o) ? a.beta[h * a.beta_h + o0 + j] * 0.03125f : 0.f;
         beta_l[e] = vb;
     }
     __syncthreads();
-    const int hf = tid >> 6, lane = tid & 63;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int pair = wave >> 1, hf = wave & 1;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a, 2));
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
     const int n_tiles = (int)ceil_div(a.M, kTile);
     for (int tile = (int)blockIdx.x; tile < n_tiles; tile += (int)gridDim.x) {
-        if (hf == 0) pair_tile_kloop<0>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
-        else pair_tile_kloop<1>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
+        if (hf == 0) kpar_tile<0>(a, tile, pair, lane, lut, alpha_l, beta_l, xch, xr, yr);
+        else kpar_tile<1>(a, tile, pair, lane, lut, alpha_l, beta_l, xch, xr, yr);
     }
 }
 
@@ -1880,14 +1890,18 @@ static void pair_launch(const HadArgsN &an, int64_t rows, hipStream_t s, bool de
     else launch(hadamard_pair_kernel<false>, G, B, (uint32_t)kPairLds, s, an);
 }
 
-static void pair_kloop_launch(const HadArgs &a, int64_t rows, hipStream_t s) {
-    const size_t lds = pair_kloop_lds(a.Kc);
+static void pair_kpar_launch(const HadArgs &a, int64_t rows, hipStream_t s) {
+    // chunk-parallel: Kc wavefront pairs per tile, as many workgroups as the
+    // CUs hold at once (LDS: kpar_lds each; registers: 3 wavefronts per SIMD)
+    const size_t lds = kpar_lds(a.Kc);
     int64_t per_cu = (int64_t)(65536 + 98304) / (int64_t)lds;
-    if (per_cu > 4) per_cu = 4;   // 2 wavefronts per SIMD by registers
+    const int64_t by_regs = 12 / (2 * (int64_t)a.Kc);
+    if (per_cu > by_regs) per_cu = by_regs;
+    if (per_cu < 1) per_cu = 1;
     int64_t grid = ceil_div(rows, kTile);
     const int64_t resident = (int64_t)device_info().cu_count * per_cu;
     if (grid > resident) grid = resident;
-    launch(hadamard_pair_kloop_kernel, dim3((unsigned)grid), dim3(kPairThreads), (uint32_t)lds, s, a);
+    launch(hadamard_pair_kpar_kernel, dim3((unsigned)grid), dim3(kPairThreads * a.Kc), (uint32_t)lds, s, a);
 }
 
 static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, int64_t M, bool bf16, hipStream_t s) {
@@ -2002,7 +2016,7 @@ static int hadamard_launch(const char *fn, HadArgs base, const HadArgs *ubase, i
         } else if (bf16 && vec && Nt == 1 && Kc > 1 && Kc <= kPairMaxKc && !base.rope &&
                    ceil_div(rows, kTile) <= kPairMaxTiles) {
             // several input chunks, one output tile: a wavefront pair per tile
-            pair_kloop_launch(a, rows, s);
+            pair_kpar_launch(a, rows, s);
         } else if (bf16 && vec && kc1 && Nt == 1 && ceil_div(rows, kTile) <= pair_max) {
             // one input chunk, one output tile, up to pair_max tiles: a
             // wavefront pair per tile

@@ -151,7 +151,7 @@ def hadamard_prepare(packed: torch.Tensor, in_o: int, out_o: int) -> torch.Tenso
 
 
 # 16-row tiles per layer up to which the library runs the bf16 single-output-tile
-# shapes on wavefront pairs (hadamard_pair_kernel / hadamard_pair_kloop_kernel);
+# shapes on wavefront pairs (hadamard_pair_kernel / hadamard_pair_kpar_kernel);
 # 16x16 layers on contiguous 512-value rows switch to the one-wavefront kernel
 # (whole rows through LDS) above PAIR_MAX_TILES_ROWS
 PAIR_MAX_TILES = 2048
@@ -173,7 +173,7 @@ def _pair_shape(rows, in_o, out_o, dt, vec, rope=False, whole_rows=False):
     if in_o <= 16:
         return "hadamard_pair_kernel"
     if in_o <= 64 and not rope:
-        return "hadamard_pair_kloop_kernel"
+        return "hadamard_pair_kpar_kernel"
     return None
 
 
