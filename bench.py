@@ -251,10 +251,18 @@ def main():
         avg_ms = d["ms"] / d["launches"]
         bytes_per_launch = d["bytes"] / d["launches"]
         achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+        excluded = sorted(set(kernels) - set(hbm_bound))
+        by_time = max(kernels, key=lambda k: kernels[k]["ms"])
         roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                         frac=round(achieved / HBM_PEAK_GBS, 4), traffic=measured_traffic(dom), kernel=dom,
                         avg_launch_us=round(avg_ms * 1000, 2), launches_per_step=d["launches"] // args.steps,
-                        algorithmic_bytes_per_launch=int(bytes_per_launch))
+                        algorithmic_bytes_per_launch=int(bytes_per_launch),
+                        selection="largest time per step among the HBM-bound hot-path kernels",
+                        excluded_kernels={k: dict(reason="bound by its exponentials and VALU work, not memory",
+                                                  ms_per_step=round(kernels[k]["ms"] / args.steps, 3))
+                                          for k in excluded},
+                        dominant_by_time=dict(kernel=by_time,
+                                              ms_per_step=round(kernels[by_time]["ms"] / args.steps, 3)))
         # the whole forward: every hot-path kernel's algorithmic bytes per
         # step over the measured time per step (torch's embedding, stream
         # projection / merge and LM head are not counted)
@@ -452,11 +460,17 @@ def bench_octonion(torch, args):
     gen = torch.Generator().manual_seed(0)
     x = torch.randn(32 * 2048, 1024, generator=gen).bfloat16().cuda()
 
+    from src.model import kernels
+    mats = [l.block_matrix(torch.bfloat16) for l in layers]
+
     def step(i):
+        # each layer's bf16 output (beta folded, one rounding) is within one
+        # bf16 ulp of bf16(the module's float32 output), the value the
+        # reference's next layer reads (cayley_dickson_cuda.py:402)
         with torch.no_grad():
             h = x
-            for l in layers:
-                h = l.forward_full(h)
+            for l, B in zip(layers, mats):
+                h = kernels.octonion_linear(h, l.in_o, l.out_o, B, l.beta)
             return h
     dt = _time_steps(torch, step, args.steps, args.warmup)
     with _hip.LaunchTimer() as lt:

@@ -305,8 +305,11 @@ int walsh_fht_fwd(const void *x, int64_t rows, int64_t n, int normalize, void *y
  * walsh_octonion_linear_fwd: y[M, ldy] = (x[M, ldx] B^T) * beta[n % out_o];
  *   beta float [out_o]; x rows 16-byte aligned.  WALSH_BF16 multiplies bf16
  *   operands (the reference's kernel casts x to bf16 too, :402) with float32
- *   accumulation; WALSH_F32 uses float32 matrix cores.  beta may be null
- *   (all ones).
+ *   accumulation and stores bf16(x B^T * beta), one rounding: within one
+ *   bf16 ulp of bf16(walsh_octonion_fused_fwd's float32 output), the value
+ *   the reference's next layer reads after its bf16 cast, so a stack of
+ *   layers chains this output; WALSH_F32 uses float32 matrix cores.  beta
+ *   may be null (all ones).
  *
  * Backward (CayleyDicksonFunction.backward, src/model/cayley_dickson_cuda.py:
  * 500-567, with physics.quantize_ternary's STE, physics.py:43-50):
@@ -328,6 +331,19 @@ int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_
                               const float *beta, void *y, int64_t ldy, int dtype, void *stream);
 int walsh_octonion_prepare_t(const uint8_t *packed, int64_t in_o, int64_t out_o, const float *beta, void *Bt,
                              int dtype, void *stream);
+
+/* walsh_octonion_fused_fwd: the reference module's forward and output dtype,
+ *   OctonionFusedLinear.forward / OctonionPackedLinear.forward
+ *   (src/model/cayley_dickson_cuda.py:650-668, :761-765): the fused kernel
+ *   multiplies bf16 x by the bf16 weights with float32 accumulation and
+ *   returns bf16 (:402, :411, :421); the module then multiplies by the float32
+ *   beta, which promotes to float32.  Here:
+ *     y[M, ldy] (float32) = float(bf16(x B^T)) * beta[n % out_o],
+ *   x bf16 [M, ldx] (a float32 input is rounded to bf16 by the caller, as the
+ *   reference kernel does at :402), B from walsh_octonion_prepare in bf16,
+ *   beta float [out_o] or null (ones).  Rows of x, B and y 16-byte aligned. */
+int walsh_octonion_fused_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o, const void *B,
+                             const float *beta, float *y, int64_t ldy, void *stream);
 int walsh_octonion_bwd_fold(const float *C, int64_t ldc, int64_t n_parts, int64_t part_stride, const uint8_t *packed,
                             int64_t in_o, int64_t out_o, const float *beta, const float *latent, float *dweight,
                             float *dbeta, void *stream);

@@ -12,6 +12,10 @@ reference's order (generate.py:134 runs the CPU path without autocast):
   RMSNorm                      chassis.py:96-106
   HadamardLinear.forward       src/model/fht_cuda.py:489-519 (quantiser physics.py:13-51)
   HadamardHeadMixerFused       fht_cuda.py:652-670
+  OctonionTernaryLinearRef     src/model/physics.py:66-82 (algebra "octonion": the CPU
+                               module chassis.get_linear_layer picks without a GPU,
+                               chassis.py:54-65, physics.py:84-91)
+  OctonionHeadMixer            chassis.py:347-399
   HadamardMoE.forward          src/model/moe.py:512-542 (router :418-447, experts :337-380)
   HadamardChannelModulation    src/model/moe.py:676-762 (its use in the block: mhc.py:528-532)
 
@@ -21,6 +25,20 @@ import math
 
 import torch
 import torch.nn.functional as F
+
+
+# src/model/constants.py:13-31, rows = output part i, columns = input part j
+# (the Cayley-Dickson signs; oracle/octonion.py re-derives them)
+OCT_SIGN = (
+    (+1, -1, -1, -1, -1, -1, -1, -1),
+    (+1, +1, +1, -1, +1, -1, -1, +1),
+    (+1, -1, +1, +1, +1, +1, -1, -1),
+    (+1, +1, -1, +1, +1, -1, +1, -1),
+    (+1, -1, -1, -1, +1, +1, +1, +1),
+    (+1, +1, -1, +1, -1, +1, -1, +1),
+    (+1, +1, +1, -1, -1, +1, +1, -1),
+    (+1, -1, +1, +1, -1, -1, +1, +1),
+)
 
 
 def ternary_codes(w: torch.Tensor) -> torch.Tensor:
@@ -59,7 +77,8 @@ class Oracle:
     ``loss`` gives the cross-entropy whose backward fills ``leaf.grad``."""
 
     def __init__(self, sd, n_embd, n_head, n_layer, n_streams=4, head_mixing=True, block_size=256,
-                 use_moe=False, moe_max_experts=4, grad=False, grad_dtype=torch.float64, use_channel_mod=False):
+                 use_moe=False, moe_max_experts=4, grad=False, grad_dtype=torch.float64, use_channel_mod=False,
+                 algebra="hadamard", octonion_gpu=False):
         self.grad = grad
         self.dt = grad_dtype if grad else torch.float32
         if grad:
@@ -83,6 +102,11 @@ class Oracle:
         self.use_moe = use_moe
         self.use_channel_mod = use_channel_mod
         self.moe_k = moe_max_experts
+        self.algebra = algebra
+        # octonion_gpu: the octonion layers as the reference's GPU module
+        # computes them (OctonionFusedLinear, cayley_dickson_cuda.py:650-668):
+        # input rounded to bf16, the float32 sum rounded to bf16, then * beta
+        self.octonion_gpu = octonion_gpu
         self.H = sylvester(32).to(self.dt)
         self._codes = {}
 
@@ -106,6 +130,33 @@ class Oracle:
         yp = torch.einsum('...gi,goi->...go', xm, w)
         ym = torch.einsum('...go,gh->...ho', yp, self.H)
         return (ym * self.sd[p + '.beta']).reshape(*lead, G * out_o)
+
+    def octonion_linear(self, x, p):
+        """physics.py:66-82: parts x_j = x[..., j in_o:(j+1) in_o],
+        y_i = (sum_j S[i][j] x_j @ Wq[i^j]^T) * beta, the sum in the
+        reference's term order (S[i][0] = +1, the terms added left to right)."""
+        w = self.codes(p + '.weight')
+        out_o, in_o = w.shape[1], w.shape[2]
+        xs = x.to(self.dt)
+        if self.octonion_gpu:
+            xs = xs.to(torch.bfloat16).to(self.dt)
+        parts = xs.split(in_o, dim=-1)
+        ys = []
+        for i in range(8):
+            acc = None
+            for j in range(8):
+                t = parts[j] @ w[i ^ j].t()
+                acc = t if acc is None else (acc + t if OCT_SIGN[i][j] > 0 else acc - t)
+            if self.octonion_gpu:
+                acc = acc.to(torch.bfloat16).to(self.dt)
+            ys.append(acc * self.sd[p + '.beta'])
+        return torch.cat(ys, dim=-1)
+
+    def linear(self, x, p):
+        """The algebra's ternary linear of module ``p`` (chassis.py:54-65)."""
+        if self.algebra == "hadamard":
+            return self.hadamard_linear(x, p + '.inner')
+        return self.octonion_linear(x, p)
 
     def mapping(self, x_flat, p, kind):
         """mhc.py:283-318."""
@@ -191,6 +242,17 @@ class Oracle:
         return torch.view_as_real(xq_ * f).flatten(3), torch.view_as_real(xk_ * f).flatten(3)
 
     def head_mixer(self, y, p):
+        if self.algebra != "hadamard":
+            # OctonionHeadMixer (chassis.py:375-399): y_i = beta *
+            # sum_j S[i][j] heads_j @ W[i^j] (W not transposed)
+            W = self.sd[p + '.W']
+            out = []
+            for i in range(8):
+                acc = torch.zeros_like(y[:, 0])
+                for j in range(8):
+                    acc = acc + OCT_SIGN[i][j] * (y[:, j] @ W[i ^ j])
+                out.append(acc * self.sd[p + '.beta'])
+            return torch.stack(out, dim=1)
         xf = torch.einsum('bhti,hg->bgti', y, self.H)
         z = torch.einsum('bhti,hio->bhto', xf, self.sd[p + '.W'])
         zf = torch.einsum('bhti,hg->bgti', z, self.H)
@@ -199,22 +261,23 @@ class Oracle:
     def attention(self, x, p, freqs):
         B, T, C = x.shape
         hd = C // self.n_head
-        q = self.hadamard_linear(x, p + '.wq.inner').view(B, T, self.n_head, hd)
-        k = self.hadamard_linear(x, p + '.wk.inner').view(B, T, self.n_head, hd)
-        v = self.hadamard_linear(x, p + '.wv.inner').view(B, T, self.n_head, hd)
+        q = self.linear(x, p + '.wq').view(B, T, self.n_head, hd)
+        k = self.linear(x, p + '.wk').view(B, T, self.n_head, hd)
+        v = self.linear(x, p + '.wv').view(B, T, self.n_head, hd)
         q, k = self.rope(q, k, freqs)
         y = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True)
         if self.head_mixing:
-            ng = self.n_head // 32
-            yg = y.view(B, ng, 32, T, hd)
+            gsz = 32 if self.algebra == "hadamard" else 8
+            ng = self.n_head // gsz
+            yg = y.view(B, ng, gsz, T, hd)
             y = torch.cat([self.head_mixer(yg[:, g], p + '.head_mixer') for g in range(ng)], dim=1)
         y = y.transpose(1, 2).contiguous().view(B, T, C)
-        return self.hadamard_linear(y, p + '.wo.inner')
+        return self.linear(y, p + '.wo')
 
     def swiglu(self, x, p):
-        g = self.hadamard_linear(x, p + '.gate_proj.inner')
-        u = self.hadamard_linear(x, p + '.up_proj.inner')
-        return self.hadamard_linear(F.silu(g) * u, p + '.down_proj.inner')
+        g = self.linear(x, p + '.gate_proj')
+        u = self.linear(x, p + '.up_proj')
+        return self.linear(F.silu(g) * u, p + '.down_proj')
 
     def loss(self, idx, targets):
         """mHCWalsh.forward's loss with targets (mhc.py:668-672): logits of

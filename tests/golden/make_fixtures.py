@@ -26,10 +26,23 @@ Fixtures (each well under 1 MB):
 * ``sinkhorn.npz``         SinkhornKnopp on [64, 4, 4] (mhc.py:198-229)
 * ``hadamard_linear.npz``  HadamardLinear 512 -> 512 on x [2, 8, 512] (fht_cuda.py:436-519)
 * ``octonion_ref.npz``     OctonionTernaryLinearRef 64 -> 64 on x [2, 8, 64] (physics.py:53-82)
+* ``tiny_hadamard.walsh``  compress.py's compress_model (the reference's .walsh v4
+  ``tiny_octonion.walsh``  writer, compress.py:121-358) run on tiny Walsh
+  ``walsh_files.npz``      checkpoints (chassis.py:533-668; n_embd 64, one
+                           layer, Hadamard with head mixing / octonion), and the
+                           checkpoints' tensors the files were written from
+* ``model_oct_c64.npz``    mHCWalsh, octonion algebra, head mixing, 2 layers,
+                           n_embd 64, n_head 8, SwiGLU FFN, with the CPU
+                           module the reference selects when its GPU kernels
+                           are absent (chassis.OctonionTernaryLinear =
+                           physics.OctonionTernaryLinearRef, physics.py:84-91)
+                           and the pure-torch OctonionHeadMixer
+                           (chassis.py:347-399, chosen without CUDA at :14-19)
 """
 import math
 import os
 import sys
+import tempfile
 
 import numpy as np
 import torch
@@ -70,7 +83,8 @@ def _perturb(module, gen):
     dynamic part of each mapping is not negligible."""
     for name, p in module.named_parameters():
         leaf = name.rsplit(".", 1)[-1]
-        if leaf in ("weight",) and any(s in name for s in (".wq.", ".wk.", ".wv.", ".wo.", "_proj.inner")):
+        if leaf in ("weight",) and any(s in name for s in (".wq.", ".wk.", ".wv.", ".wo.", "_proj.inner",
+                                                           ".gate_proj.", ".up_proj.", ".down_proj.")):
             continue  # ternary latents
         if name.endswith("_weights"):
             continue  # MoE ternary latents
@@ -85,10 +99,11 @@ def _perturb(module, gen):
 
 
 def model_fixture(chassis, mhc, path, *, n_embd, n_head, n_layer, use_moe=False, max_experts=4,
-                  use_channel_mod=False, head_mixing=True, vocab=128, block_size=32, B=2, T=16, seed=0):
+                  use_channel_mod=False, head_mixing=True, vocab=128, block_size=32, B=2, T=16, seed=0,
+                  algebra="hadamard"):
     torch.manual_seed(seed)
     cfg = chassis.WalshConfig(block_size=block_size, vocab_size=vocab, n_layer=n_layer, n_head=n_head,
-                              n_embd=n_embd, algebra="hadamard", head_mixing=head_mixing, use_moe=use_moe,
+                              n_embd=n_embd, algebra=algebra, head_mixing=head_mixing, use_moe=use_moe,
                               moe_max_experts=max_experts, use_channel_mod=use_channel_mod)
     model = mhc.mHCWalsh(cfg, n_streams=4)
     gen = torch.Generator().manual_seed(seed + 1)
@@ -105,6 +120,7 @@ def model_fixture(chassis, mhc, path, *, n_embd, n_head, n_layer, use_moe=False,
         "cfg/use_moe": np.int64(use_moe), "cfg/max_experts": np.int64(max_experts),
         "cfg/use_channel_mod": np.int64(use_channel_mod), "cfg/head_mixing": np.int64(head_mixing),
         "cfg/vocab": np.int64(vocab), "cfg/block_size": np.int64(block_size),
+        "cfg/algebra": np.array(algebra),
         "in/idx": idx.numpy(), "in/targets": targets.numpy(),
         "out/logits_last": _np(logits_last), "out/h_out": _np(h_out),
         "out/logits_all": _np(logits_all), "out/loss": _np(loss),
@@ -114,6 +130,45 @@ def model_fixture(chassis, mhc, path, *, n_embd, n_head, n_layer, use_moe=False,
             out[f"out/moe_mask_{l}"] = _np(layer.feed_forward._last_expert_mask)
             out[f"out/moe_aux_{l}"] = _np(layer.feed_forward._aux_loss)
     np.savez_compressed(path, **out)
+
+
+def octonion_model_fixture(chassis, mhc, physics, path):
+    """The octonion-algebra model on the reference's CPU path.  Without a GPU
+    the reference would still bind chassis.OctonionTernaryLinear to the
+    Triton module when triton imports (physics.py:84-88), and that module
+    cannot run on a CPU; the CPU module is what physics.py:89-91 falls back
+    to, so it is bound here for the duration of the construction."""
+    assert not torch.cuda.is_available()
+    bound = chassis.OctonionTernaryLinear
+    chassis.OctonionTernaryLinear = physics.OctonionTernaryLinearRef
+    try:
+        model_fixture(chassis, mhc, path, n_embd=64, n_head=8, n_layer=2, algebra="octonion", seed=9)
+    finally:
+        chassis.OctonionTernaryLinear = bound
+
+
+def walsh_file_fixtures(chassis, root, seed=0):
+    """Tiny Walsh checkpoints of plain tensors, compressed to .walsh v4 by the
+    reference's own writer.  The .npz keeps every tensor of each checkpoint
+    (prefix ``hadamard/`` or ``octonion/``) so a reader's output can be
+    checked against what was written: ternary latents (the writer quantises
+    them itself), float16 and int8 entries (the writer rounds them)."""
+    if root not in sys.path:
+        sys.path.insert(0, root)
+    import compress  # the reference's compress.py
+    out = {}
+    for algebra, mixing in (("hadamard", True), ("octonion", False)):
+        torch.manual_seed(seed)
+        args = dict(block_size=16, vocab_size=64, n_layer=1, n_head=32 if algebra == "hadamard" else 8, n_embd=64,
+                    algebra=algebra, head_mixing=mixing)
+        model = chassis.Walsh(chassis.WalshConfig(**args))
+        _perturb(model, torch.Generator().manual_seed(seed + 1))
+        with tempfile.TemporaryDirectory() as d:
+            ckpt = os.path.join(d, "ckpt.pt")
+            torch.save({"model_args": args, "model": model.state_dict()}, ckpt)
+            compress.compress_model(ckpt, os.path.join(HERE, f"tiny_{algebra}.walsh"))
+        out.update({f"{algebra}/{k}": _np(v) for k, v in model.state_dict().items()})
+    np.savez_compressed(os.path.join(HERE, "walsh_files.npz"), **out)
 
 
 def moe_fixture(chassis, moe, path, seed=0):
@@ -212,8 +267,10 @@ def main():
     sinkhorn_fixture(mhc, os.path.join(HERE, "sinkhorn.npz"))
     hadamard_fixture(fht_cuda, os.path.join(HERE, "hadamard_linear.npz"))
     octonion_fixture(physics, os.path.join(HERE, "octonion_ref.npz"))
+    octonion_model_fixture(chassis, mhc, physics, os.path.join(HERE, "model_oct_c64.npz"))
+    walsh_file_fixtures(chassis, root)
     for f in sorted(os.listdir(HERE)):
-        if f.endswith(".npz"):
+        if f.endswith((".npz", ".walsh")):
             print(f"{f}: {os.path.getsize(os.path.join(HERE, f))} bytes")
 
 

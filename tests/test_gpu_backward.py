@@ -183,13 +183,22 @@ def test_octonion_bwd_vs_oracle(K, in_o, out_o, M, dtype):
     assert_close(db.cpu().numpy(), ref[2], dtype, f"oct dbeta {in_o}x{out_o} M={M}")
 
 
+@pytest.mark.parametrize("cls", ["OctonionTernaryLinearRef", "OctonionFusedLinear"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_octonion_module_autograd(dtype):
+def test_octonion_module_autograd(dtype, cls):
+    """Gradients of both octonion modules vs float64 autograd of the layer.
+    OctonionTernaryLinearRef computes in the input dtype (float32 bars for
+    float32); OctonionFusedLinear multiplies bf16 operands whatever the input
+    dtype (the reference GPU module, cayley_dickson_cuda.py:402), so its
+    bars are bf16's."""
     from oracle import octonion as ooct
-    from src.model import kernels
-    from src.model.cayley_dickson_cuda import OctonionFusedLinear
+    from src.model import kernels, octonion
     torch.manual_seed(11)
-    layer = OctonionFusedLinear(256, 512).cuda()
+    layer = getattr(octonion, cls)(256, 512).cuda()
+    if cls == "OctonionFusedLinear":
+        dtype_bar = torch.bfloat16
+    else:
+        dtype_bar = dtype
     xr = torch.randn(2, 40, 256, device="cuda", dtype=dtype)
     parts = tuple(p.detach().requires_grad_(True) for p in xr.split(32, dim=-1))
     ys = layer(parts)
@@ -202,9 +211,10 @@ def test_octonion_module_autograd(dtype):
                                        np.stack([g.double().cpu().numpy().reshape(-1, 64) for g in gys]),
                                        latent=layer.weight.detach().double().cpu().numpy())
     gx = np.stack([p.grad.float().cpu().numpy().reshape(-1, 32) for p in parts])
-    assert_close(gx, ref[0], dtype, "oct module x.grad")
-    assert_close(layer.weight.grad.cpu().numpy(), ref[1], dtype, "oct module weight.grad")
-    assert_close(layer.beta.grad.cpu().numpy(), ref[2], dtype, "oct module beta.grad")
+    assert parts[0].grad.dtype == dtype
+    assert_close(gx, ref[0], dtype_bar, f"oct {cls} x.grad")
+    assert_close(layer.weight.grad.cpu().numpy(), ref[1], dtype_bar, f"oct {cls} weight.grad")
+    assert_close(layer.beta.grad.cpu().numpy(), ref[2], dtype_bar, f"oct {cls} beta.grad")
 
 
 # ---------------------------------------------------------------- Sinkhorn
@@ -346,6 +356,51 @@ def test_moe_backward_matches_oracle(C, k, T):
         err, nb = float(np.linalg.norm(a - b)), float(np.linalg.norm(b))
         print(f"moe C={C} k={k} {n}: rel_norm {err / max(nb, 1e-300):.2e} (|ref| {nb:.3e})", flush=True)
         assert err <= 1e-5 * nb + 1e-6 * G, (n, err, nb)
+
+
+def test_moe_checkpointed_backward_equals_plain():
+    """Activation checkpointing (non-reentrant, as mHCWalsh's
+    gradient_checkpointing uses) recomputes the MoE forward during the
+    backward; the gradients, including the routing weights' path through
+    the expert outputs into the router, equal the plain backward's bitwise:
+    the recomputed pair order and pair lists are the ones the backward
+    reads.  The experts' own weight gradients agree to float32 summation
+    order (1e-4 of the largest entry)."""
+    from src.model import WalshConfig
+    from src.model.moe import HadamardMoE
+    torch.manual_seed(6)
+    C, k, T = 512, 6, 96
+    cfg = WalshConfig(n_embd=C, n_head=32, n_layer=1, vocab_size=64, block_size=128)
+    m = HadamardMoE(cfg, max_experts=k).cuda().train()
+    with torch.no_grad():
+        for lin in (m.router.gate[0], m.router.gate[2]):
+            lin.weight.normal_(0, 0.2)
+    g = torch.Generator().manual_seed(7)
+    x0 = torch.randn(2, T, C, generator=g).cuda()
+    gy = torch.randn(2, T, C, generator=g).cuda()
+
+    def run(ckpt):
+        m.zero_grad(set_to_none=True)
+        x = x0.clone().requires_grad_(True)
+        y = torch.utils.checkpoint.checkpoint(m, x, use_reentrant=False) if ckpt else m(x)
+        (y * gy).sum().backward()
+        torch.cuda.synchronize()
+        return {"x": x.grad.clone(), **{n: p.grad.clone() for n, p in m.named_parameters()}}
+    plain, ck = run(False), run(True)
+    assert plain["router.gate.2.weight"].abs().max() > 0
+    for n in plain:
+        d = float((plain[n] - ck[n]).abs().max())
+        scale = float(plain[n].abs().max())
+        print(f"checkpointed MoE grad {n}: max |diff| {d:.3e} (max |grad| {scale:.3e})", flush=True)
+        if n.startswith("experts."):
+            # the experts' weight gradients sum their pairs per workgroup; the
+            # order of an expert's pair list comes from the scatter's atomics,
+            # so those float32 sums may group pairs differently run to run
+            assert d <= 1e-4 * scale, n
+        else:
+            # the routing-weight path (d expert_weights into the router) and
+            # the input gradient: bitwise
+            assert d == 0.0, n
 
 
 def test_mhcwalsh_backward_bf16_autocast():

@@ -85,7 +85,7 @@ def test_reference_fixture_model_on_gpu(name):
     within the bf16 bars of the reference's own bf16 drift."""
     from src.model import WalshConfig, mHCWalsh
     fx = load(name)
-    c = {k[4:]: int(v) for k, v in fx.items() if k.startswith("cfg/")}
+    c = {k[4:]: (str(v) if v.dtype.kind == "U" else int(v)) for k, v in fx.items() if k.startswith("cfg/")}
     cfg = WalshConfig(block_size=c["block_size"], vocab_size=c["vocab"], n_layer=c["n_layer"], n_head=c["n_head"],
                       n_embd=c["n_embd"], algebra="hadamard", head_mixing=bool(c["head_mixing"]),
                       use_moe=bool(c["use_moe"]), moe_max_experts=c["max_experts"],

@@ -156,37 +156,68 @@ def test_octonion_linear_matches_oracle(K, dtype, M, in_o, out_o):
 
 
 @torch.no_grad()
-def test_octonion_module_tuple_interface():
+def test_octonion_module_tuple_interface(K):
+    """OctonionFusedLinear keeps the reference GPU module's contract
+    (cayley_dickson_cuda.py:650-668): x rounded to bf16, the float32 sum
+    rounded to bf16, times the float32 beta, a float32 result with or
+    without autocast.  OctonionTernaryLinearRef (physics.py:53-82) computes
+    in float32 for float32 inputs.  The bf16-output kernel that chains the
+    layers in a stack stores bf16(x W^T beta), within one bf16 ulp of
+    bf16(the module's output)."""
     from src.model.cayley_dickson_cuda import OctonionFusedLinear, cayley_dickson_fused
     from src.model.physics import OctonionTernaryLinearRef
     torch.manual_seed(1)
     layer = OctonionFusedLinear(512, 256).cuda()
+    with torch.no_grad():
+        layer.beta.mul_(1 + 0.2 * torch.randn_like(layer.beta))
     x = torch.randn(2, 10, 512, device="cuda")
     parts = x.split(64, dim=-1)
     ys = layer(parts)
-    assert len(ys) == 8 and ys[0].shape == (2, 10, 32)
+    assert len(ys) == 8 and ys[0].shape == (2, 10, 32) and ys[0].dtype == torch.float32
     w = layer.weight.detach().cpu().numpy()
     codes = otern.ternary_codes(w, otern.absmean_gamma(w))
+    beta = layer.beta.detach().cpu().numpy()
     xp = x.double().cpu().numpy().reshape(20, 8, 64).transpose(1, 0, 2)
-    ref = ooct.octonion_linear_f64(xp, codes, layer.beta.detach().cpu().numpy())
+    ref = ooct.octonion_linear_gpu_semantics(xp, codes, beta)
     got = torch.stack(ys).double().cpu().numpy().reshape(8, 20, 32)
-    assert_close(got, ref, torch.float32, "module fp32")
+    assert_close(got, ref, torch.bfloat16, "module fp32 in (bf16 operands)")
+    # away from a bf16 rounding boundary of the float32 sum the result is the
+    # oracle's to float32 rounding of the beta product
+    acc = ooct.octonion_linear_f64(ooct.bf16_round(xp).astype(np.float64), codes, np.ones(32))
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(acc), 1e-30))) - 7)
+    safe = np.abs(acc / ulp - np.floor(acc / ulp) - 0.5) > 0.05  # not within 5% of an ulp of a midpoint
+    d = np.abs(got - ref)[safe] / np.maximum(np.abs(ref[safe]), 1e-30)
+    print(f"octonion module: {int(safe.sum())} of {safe.size} away from a bf16 boundary, max rel {d.max():.2e}")
+    assert d.max() <= 2 ** -23
     # non-adjacent parts (a copy is made) give the same result
     ys2 = layer(tuple(p.clone() for p in parts))
     assert all(torch.equal(a, b) for a, b in zip(ys, ys2))
-    # bf16 autocast path and the GPU-kernel semantics of the reference
+    # bf16 autocast: the same float32 result (the input is rounded to bf16 either way)
     with torch.autocast("cuda", dtype=torch.bfloat16):
         yb = layer(parts)
-    assert yb[0].dtype == torch.bfloat16
-    assert_close(torch.stack(yb).float().cpu().numpy().reshape(8, 20, 32),
-                 ooct.octonion_linear_gpu_semantics(xp, codes, layer.beta.detach().cpu().numpy()),
-                 torch.bfloat16, "module bf16")
-    # Ref class returns the input dtype; the functional form returns bf16
+    assert yb[0].dtype == torch.float32
+    assert all(torch.equal(a, b) for a, b in zip(ys, yb))
+    # the stack's bf16 kernel output (beta folded, one rounding) is within
+    # one bf16 ulp of bf16(module output)
+    yk = K.octonion_linear(x.bfloat16().reshape(20, 512), 64, 32, layer.block_matrix(torch.bfloat16), layer.beta)
+    ym = torch.cat(ys, -1).reshape(20, 256)
+    d = (yk.float() - ym.bfloat16().float()).abs()
+    assert torch.all(d <= torch.exp2(torch.floor(torch.log2(ym.abs().clamp_min(1e-30))) - 7) * 1.01)
+    # Ref class: float32 math for float32 input
     ref_layer = OctonionTernaryLinearRef(512, 256).cuda()
-    assert ref_layer(parts)[0].dtype == torch.float32
+    yr = ref_layer(parts)
+    assert yr[0].dtype == torch.float32
+    w = ref_layer.weight.detach().cpu().numpy()
+    codes_r = otern.ternary_codes(w, otern.absmean_gamma(w))
+    assert_close(torch.stack(yr).double().cpu().numpy().reshape(8, 20, 32),
+                 ooct.octonion_linear_f64(xp, codes_r, ref_layer.beta.detach().cpu().numpy()), torch.float32,
+                 "Ref module fp32")
+    # the functional form returns the kernel's bf16 (no beta)
     wq = torch.from_numpy(codes.astype(np.float32)).cuda()
     yf = cayley_dickson_fused(parts, wq)
     assert yf[0].dtype == torch.bfloat16
+    assert_close(torch.stack(yf).double().cpu().numpy().reshape(8, 20, 32), ooct.bf16_round(acc.astype(np.float32)),
+                 torch.bfloat16, "functional form (bf16, no beta)")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -98,3 +98,40 @@ def test_hadamard_packed_linear_and_optimize_for_inference():
         assert not any(isinstance(m, HadamardLinear) for m in model.modules())
         got, _ = model(idx)
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("algebra", ["hadamard", "octonion"])
+def test_load_reference_written_walsh_file(algebra):
+    """load_walsh on a file the reference's compress_model wrote
+    (tests/golden/tiny_<algebra>.walsh, compress.py:121-358): the ternary
+    weights decode on the GPU to the absmean codes of the latents the file
+    was written from (float codes and 2-bit packed buffers), float16 entries
+    are the latents rounded to float16, the embedding is its int8 codes times
+    the stored scale, RoPE as stored."""
+    import os
+    from src.walsh_format import load_walsh
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    path = os.path.join(golden, f"tiny_{algebra}.walsh")
+    with np.load(os.path.join(golden, "walsh_files.npz"), allow_pickle=False) as z:
+        ref = {k.split("/", 1)[1]: z[k] for k in z.files if k.startswith(algebra + "/")}
+    sd, config = load_walsh(path, device="cuda")
+    sdp, _ = load_walsh(path, device="cuda", packed_ternary=True)
+    torch.cuda.synchronize()
+    assert config["algebra"] == algebra
+    n_ternary = 0
+    for name, t in sd.items():
+        w = ref[name]
+        if name.endswith(".weight") and any(k in name for k in ("wq", "wk", "wv", "wo", "_proj")):
+            codes = otern.ternary_codes(w, otern.absmean_gamma(w))
+            assert np.array_equal(t.cpu().numpy(), codes.astype(np.float32)), name
+            assert np.array_equal(sdp[name].cpu().numpy(), otern.pack_codes(codes)), name
+            n_ternary += 1
+        elif name == "tok_embeddings.weight":
+            scale = np.float32(np.abs(w).max() / 127.0)
+            q = np.clip(np.round(w / scale), -127, 127).astype(np.float32)
+            assert np.array_equal(t.cpu().numpy(), q * scale)
+        elif name == "freqs_cis":
+            assert torch.equal(t.cpu(), torch.from_numpy(w))
+        else:
+            assert np.array_equal(t.cpu().numpy(), w.astype(np.float16).astype(np.float32)), name
+    assert n_ternary == 7 and "output.weight" not in sd

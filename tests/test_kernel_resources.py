@@ -52,6 +52,7 @@ ALLOWED = {
     "hadamard_wide3_kernelILi0ELb1E": 3,       # head mixer at head_dim 128
     "gemm256_silu_kernel": 4,                   # epilogue (SiLU), outside the K loop
     "gemm256_beta_kernel": 3,                   # epilogue (beta), outside the K loop
+    "gemm256_beta_f32_kernel": 5,               # epilogue (bf16 rounding, beta, float32 stores)
 }
 
 

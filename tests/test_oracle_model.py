@@ -60,16 +60,17 @@ def assert_close(a, b, tol=TOL, what=""):
     assert r_norm <= tol and r_max <= 10 * tol, f"{what}: rel {r_norm:.3e}, max-rel {r_max:.3e} (bar {tol})"
 
 
-def model_oracle(fx):
-    c = {k[4:]: int(v) for k, v in fx.items() if k.startswith("cfg/")}
+def model_oracle(fx, **kw):
+    c = {k[4:]: (str(v) if v.dtype.kind == "U" else int(v)) for k, v in fx.items() if k.startswith("cfg/")}
     sd = section(fx, "sd")
     return Oracle(sd, n_embd=c["n_embd"], n_head=c["n_head"], n_layer=c["n_layer"], n_streams=4,
                   head_mixing=bool(c["head_mixing"]), block_size=c["block_size"], use_moe=bool(c["use_moe"]),
-                  moe_max_experts=c["max_experts"], use_channel_mod=bool(c["use_channel_mod"])), c
+                  moe_max_experts=c["max_experts"], use_channel_mod=bool(c["use_channel_mod"]),
+                  algebra=c.get("algebra", "hadamard"), **kw), c
 
 
 # --------------------------------------------------------------- whole model
-@pytest.mark.parametrize("name", ["model_c64.npz", "model_c96_moe.npz"])
+@pytest.mark.parametrize("name", ["model_c64.npz", "model_c96_moe.npz", "model_oct_c64.npz"])
 def test_model_oracle_matches_reference(name):
     """oracle/model.py reproduces mHCWalsh.forward of the reference: the
     last-position logits, the final hidden states of every position and the
@@ -99,6 +100,68 @@ def test_model_oracle_matches_reference(name):
         # the loss pass ran the layers again: the first n_layer masks belong to forward()
         for l in range(cfg["n_layer"]):
             assert np.array_equal(seen[l].numpy(), fx[f"out/moe_mask_{l}"]), f"layer {l} expert mask"
+
+
+def test_octonion_model_fixture_discriminates():
+    """The octonion model fixture (algebra "octonion", the CPU module
+    OctonionTernaryLinearRef and the pure-torch OctonionHeadMixer) catches
+    an octonion layer with W[i^j] transposed per block, the head mixer
+    applied with its weights transposed (chassis.py:395 multiplies by W, not
+    W^T), and the conjugate sign table (x_j and w swapped in the product)."""
+    from oracle import model as omodel
+    fx = load("model_oct_c64.npz")
+    idx = torch.from_numpy(fx["in/idx"])
+    ref = fx["out/logits_last"]
+
+    def run(orc):
+        with torch.no_grad():
+            return orc.forward(idx).numpy()
+    orc, _ = model_oracle(fx)
+    assert rel(run(orc), ref)[0] <= TOL
+    # per-block transposed weights: only square blocks (in_o == out_o) take it
+    orc, _ = model_oracle(fx)
+    base = orc.octonion_linear
+
+    def lin_t(x, p):
+        w = orc.codes(p + '.weight')
+        if w.shape[1] != w.shape[2]:
+            return base(x, p)
+        orc._codes[p + '.weight'] = w.transpose(1, 2).contiguous()
+        try:
+            return base(x, p)
+        finally:
+            orc._codes[p + '.weight'] = w
+    orc.octonion_linear = lin_t
+    assert rel(run(orc), ref)[0] > 100 * TOL
+    # head mixer with W^T
+    orc, _ = model_oracle(fx)
+    for k in list(orc.sd):
+        if k.endswith("head_mixer.W"):
+            orc.sd[k] = orc.sd[k].transpose(1, 2).contiguous()
+    assert rel(run(orc), ref)[0] > 100 * TOL
+    # conjugate signs: S[i][j] of x . w replaced by that of w . x (S[j][i]
+    # with the non-scalar cross terms negated)
+    saved = omodel.OCT_SIGN
+    try:
+        omodel.OCT_SIGN = tuple(tuple(saved[i][j] if (i == 0 or j == 0 or i == j) else -saved[i][j]
+                                      for j in range(8)) for i in range(8))
+        orc, _ = model_oracle(fx)
+        assert rel(run(orc), ref)[0] > 100 * TOL
+    finally:
+        omodel.OCT_SIGN = saved
+
+
+def test_octonion_gpu_semantics_mode_is_bf16_close():
+    """The oracle's octonion_gpu mode (the reference GPU module's bf16
+    roundings) stays within bf16 reach of the CPU reference's float32 model
+    and is not identical to it."""
+    fx = load("model_oct_c64.npz")
+    idx = torch.from_numpy(fx["in/idx"])
+    orc, _ = model_oracle(fx, octonion_gpu=True)
+    with torch.no_grad():
+        out = orc.forward(idx).numpy()
+    r = rel(out, fx["out/logits_last"])[0]
+    assert 1e-5 < r < 3e-2, r
 
 
 def test_model_fixture_discriminates():

@@ -36,12 +36,14 @@ const DeviceInfo &device_info() {
         valid.resize(dev + 1, 0);
     }
     if (!valid[dev]) {
-        DeviceInfo d{256, 65536};
+        DeviceInfo d{256, 65536, 163840};
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
             d.cu_count = v;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
             d.max_shared_per_block = v;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) == hipSuccess && v > 0)
+            d.lds_per_cu = v;
         cache[dev] = d;
         valid[dev] = 1;
     }

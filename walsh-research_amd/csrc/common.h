@@ -28,6 +28,7 @@ int check_hip(hipError_t e, const char *what);
 struct DeviceInfo {
     int cu_count;
     int max_shared_per_block;
+    int lds_per_cu;  // LDS bytes of one CU (160 KB on gfx950), shared by its resident workgroups
 };
 const DeviceInfo &device_info();
 

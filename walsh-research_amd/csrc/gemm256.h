@@ -23,8 +23,10 @@ struct Gemm256Args {
 };
 
 // epilogues: beta scaling to bf16 (octonion forward), SiLU of the bf16-rounded
-// product to bf16 (router), plain float32 (split-K partial sums)
-enum { kEpiBeta = 0, kEpiSilu = 1, kEpiF32 = 2 };
+// product to bf16 (router), plain float32 (split-K partial sums), the product
+// rounded to bf16 and then scaled by beta in float32, stored as float32 (the
+// octonion module's output: a bf16 kernel result times a float32 parameter)
+enum { kEpiBeta = 0, kEpiSilu = 1, kEpiF32 = 2, kEpiBetaF32 = 3 };
 
 // Round to the nearest bfloat16 and back: where the reference runs under
 // bf16 autocast, every Linear/einsum output and elementwise result is a
@@ -168,7 +170,27 @@ __device__ __forceinline__ void gemm256_body(const Gemm256Args &a, const Gemm256
     // epilogue of item r: acc[i][j][q] = D[n = n0 + 128 wn + 16 i + 4 fq + q][m = m0 + 128 wm + 16 j + fr]
     auto epilogue = [&](int r) {
         const Item it = item(r);
-        if constexpr (EPI == kEpiF32) {
+        if constexpr (EPI == kEpiBetaF32) {
+            const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 4));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int n = it.n0 + wn * 128 + i * 16 + fq * 4;
+                f32x4 bv = f32x4{1.f, 1.f, 1.f, 1.f};
+                if (a.beta && n < a.N) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) bv[q] = a.beta[(n + q) % a.out_o];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int m = it.m0 + wm * 128 + j * 16 + fr;
+                    const uint32_t off = (m < a.M && n < a.N) ? (uint32_t)(((int64_t)m * a.ldy + n) * 4) : kOOB;
+                    f32x4 v;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) v[q] = bf16r(acc[i][j][q]) * bv[q];
+                    Buf4<float>::store(v, yr, off, 0);
+                }
+            }
+        } else if constexpr (EPI == kEpiF32) {
             const int64_t span = a.kspan > 0 ? (int64_t)(p.items / tiles - 1) * a.ysplit + (int64_t)a.M * a.ldy
                                              : (int64_t)a.M * a.ldy;
             const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)(span * 4));
@@ -289,6 +311,9 @@ static __global__ __launch_bounds__(kOThreads, 1) void gemm256_silu_kernel(Gemm2
 static __global__ __launch_bounds__(kOThreads, 1) void gemm256_f32_kernel(Gemm256Args a, Gemm256Plan p) {
     gemm256_body<kEpiF32>(a, p);
 }
+static __global__ __launch_bounds__(kOThreads, 1) void gemm256_beta_f32_kernel(Gemm256Args a, Gemm256Plan p) {
+    gemm256_body<kEpiBetaF32>(a, p);
+}
 
 // Requirements (checked by the callers): K % 8 == 0, N % 4 == 0, ldx and Kp
 // multiples of 8, x / B / y within 2^31 bytes, 16-byte aligned operands.
@@ -314,6 +339,8 @@ static inline void gemm256_launch(const Gemm256Args &a, hipStream_t s) {
         launch(gemm256_beta_kernel, grid, block, 0, s, a, p);
     else if constexpr (EPI == kEpiSilu)
         launch(gemm256_silu_kernel, grid, block, 0, s, a, p);
+    else if constexpr (EPI == kEpiBetaF32)
+        launch(gemm256_beta_f32_kernel, grid, block, 0, s, a, p);
     else
         launch(gemm256_f32_kernel, grid, block, 0, s, a, p);
 }

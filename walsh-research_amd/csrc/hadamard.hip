@@ -1879,7 +1879,7 @@ static int hadamard_check(const char *fn, const void *x, int64_t ldx, int64_t gs
 // hold at once (LDS: kPairLds each; registers: 4 wavefronts per SIMD), the
 // rest looped over.
 static void pair_launch(const HadArgsN &an, int64_t rows, hipStream_t s, bool dense = false) {
-    const int64_t per_cu = (int64_t)(65536 + 98304) / (int64_t)kPairLds;   // 160 KB of LDS per CU
+    const int64_t per_cu = (int64_t)device_info().lds_per_cu / (int64_t)kPairLds;
     const int64_t by_regs = dense ? 6 : 8;   // 3 or 4 wavefronts per SIMD
     const int64_t resident = (int64_t)device_info().cu_count * (per_cu < by_regs ? per_cu : by_regs);
     int64_t per_layer = ceil_div(rows, kTile);
@@ -1894,7 +1894,7 @@ static void pair_kpar_launch(const HadArgs &a, int64_t rows, hipStream_t s) {
     // chunk-parallel: Kc wavefront pairs per tile, as many workgroups as the
     // CUs hold at once (LDS: kpar_lds each; registers: 3 wavefronts per SIMD)
     const size_t lds = kpar_lds(a.Kc);
-    int64_t per_cu = (int64_t)(65536 + 98304) / (int64_t)lds;
+    int64_t per_cu = (int64_t)device_info().lds_per_cu / (int64_t)lds;
     const int64_t by_regs = 12 / (2 * (int64_t)a.Kc);
     if (per_cu > by_regs) per_cu = by_regs;
     if (per_cu < 1) per_cu = 1;
@@ -2402,7 +2402,7 @@ WALSH_EXPORT int walsh_head_mixer_proj_fwd(const void *x, int64_t B, int64_t T, 
     // one wavefront pair per 16-row tile, up to the pairs the CUs hold at
     // once (LDS: kMixProjLds each; registers: 2 wavefronts per SIMD, where
     // 3 would spill)
-    int64_t per_cu = (int64_t)(65536 + 98304) / (int64_t)kMixProjLds;
+    int64_t per_cu = (int64_t)device_info().lds_per_cu / (int64_t)kMixProjLds;
     if (per_cu > 4) per_cu = 4;
     const int64_t resident = (int64_t)device_info().cu_count * per_cu;
     int64_t grid = ceil_div(M, kTile);

@@ -1737,6 +1737,10 @@ WALSH_EXPORT int walsh_moe_decode_fwd(const void *x, int64_t ldx, int64_t M, int
         return set_error(WALSH_EINVAL, "%s: null pointer", fn);
     if (M < 1 || M > kDecTok)
         return set_error(WALSH_ENOTSUP, "%s: takes 1..%d tokens (M=%lld)", fn, kDecTok, (long long)M);
+    // the routing workgroup writes partial row t of count / probsum for token t
+    if (n_part < M)
+        return set_error(WALSH_EINVAL, "%s: n_part=%lld partial rows for M=%lld tokens (one row per token)", fn,
+                         (long long)n_part, (long long)M);
     if (C % (32 * kR1Waves) || H % 128 || H > kR2MaxH || E % 4 || C != 32 * E || ldx < C || ldy < 32 * E)
         return set_error(WALSH_ENOTSUP, "%s: needs C %% %d == 0, H %% 128 == 0, H <= %d, E %% 4 == 0, C == 32 E "
                          "(C=%lld H=%lld E=%lld)", fn, 32 * kR1Waves, kR2MaxH, (long long)C, (long long)H,

@@ -541,3 +541,46 @@ WALSH_EXPORT int walsh_octonion_linear_fwd(const void *x, int64_t ldx, int64_t M
     }
     return WALSH_OK;
 }
+
+// The reference module's forward (OctonionFusedLinear.forward and
+// OctonionPackedLinear.forward, cayley_dickson_cuda.py:650-668, :761-765): the
+// fused kernel multiplies bf16 operands with float32 accumulation and returns
+// bf16 (:402, :411, :421), and the module multiplies that by the float32 beta,
+// which promotes to float32.  Here the rounding to bf16 and the beta product
+// are the GEMM's epilogue, so y [M, ldy] float32 = float(bf16(x B^T)) * beta.
+WALSH_EXPORT int walsh_octonion_fused_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t out_o,
+                                          const void *B, const float *beta, float *y, int64_t ldy, void *stream) {
+    const char *fn = "walsh_octonion_fused_fwd";
+    if (!x || !B || !y) return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (M < 0 || in_o <= 0 || out_o <= 0 || ldx < 8 * in_o || ldy < 8 * out_o)
+        return set_error(WALSH_EINVAL, "%s: bad shape M=%lld in_o=%lld out_o=%lld", fn, (long long)M,
+                         (long long)in_o, (long long)out_o);
+    if (M == 0) return WALSH_OK;
+    if (ldx % 8 || (8 * in_o) % 8 || (uintptr_t)x % 16 || (uintptr_t)B % 16 || ldy % 4 || (uintptr_t)y % 16)
+        return set_error(WALSH_ENOTSUP, "%s: x/B/y must be 16-byte aligned rows", fn);
+    const int64_t N = 8 * out_o, K = 8 * in_o, Kp = ceil_div(K, 32) * 32;
+    if (N * Kp * 2 > (int64_t)kMaxBufferBytes) return set_error(WALSH_ENOTSUP, "%s: too large", fn);
+    const int64_t row_bytes = ldx * 2 > ldy * 4 ? ldx * 2 : ldy * 4;
+    int64_t rows_max = (int64_t)kMaxBufferBytes / row_bytes / kOBM * kOBM;
+    if (rows_max < kOBM) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
+    rows_max = balanced_rows(M, rows_max, kOBM);
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        OctArgs a{};
+        a.x = (const char *)x + r0 * ldx * 2;
+        a.ldx = ldx;
+        a.M = (int)rows;
+        a.N = (int)N;
+        a.K = (int)K;
+        a.Kp = (int)Kp;
+        a.B = B;
+        a.beta = beta;
+        a.out_o = (int)out_o;
+        a.y = y + r0 * ldy;
+        a.ldy = ldy;
+        gemm256_launch<kEpiBetaF32>(a, (hipStream_t)stream);
+        const int rc = check_hip(hipGetLastError(), fn);
+        if (rc) return rc;
+    }
+    return WALSH_OK;
+}

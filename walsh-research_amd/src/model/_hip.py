@@ -59,6 +59,7 @@ SIGNATURES = {
     "walsh_octonion_weight_elems": (_I64, [_I64, _I64]),
     "walsh_octonion_prepare": (_I, [_P, _I64, _I64, _P, _I, _P]),
     "walsh_octonion_linear_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I, _P]),
+    "walsh_octonion_fused_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "walsh_octonion_prepare_t": (_I, [_P, _I64, _I64, _P, _P, _I, _P]),
     "walsh_octonion_bwd_fold": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P]),
     "walsh_octonion_bwd_params_workspace_bytes": (_I64, [_I64, _I64, _I64, _I]),

@@ -201,6 +201,46 @@ def rope_supported(x: torch.Tensor, out_o: int, head_dim: int) -> bool:
             and x.shape[-1] % 4 == 0 and x.stride(-1) == 1)
 
 
+# The bf16 Hadamard kernels for in_o > 16 and out_o > 48 (n_embd 4096: the
+# base-3 wide kernel and its decode-sized split) keep alpha and beta in LDS as
+# float16 for the whole launch.  float16 overflows above 65504 and rounds
+# non-zeros below 2^-24 (its smallest subnormal) to zero or to a value 100%
+# off; in between, its absolute error stays below 2^-25 (relative 2^-11 from
+# 2^-14 up, and no worse than the bf16 activations' 2^-8 down to 2^-16).  A
+# value that float16 would destroy (a trained scale that blew up or collapsed,
+# or a non-finite one) raises instead of being damaged silently.  The check
+# reads the values once per parameter version (one host round trip after
+# each optimizer step, none under graph capture).
+F16_MAX = 65504.0
+F16_MIN_SUBNORMAL = 2.0 ** -24
+_f16_checked = {}
+
+
+def half_scales_used(dtype: torch.dtype, in_o: int, out_o: int) -> bool:
+    return dtype == torch.bfloat16 and 16 < in_o <= 128 and 48 < out_o <= 128
+
+
+def check_half_range(name: str, t: torch.Tensor, scale: float = 1.0) -> None:
+    """Raise ValueError if a value of ``t * scale`` is not finite, exceeds
+    float16's largest value, or is a non-zero below its smallest subnormal.
+    Cached on the tensor's storage and version."""
+    if t is None or t.numel() == 0 or (t.is_cuda and torch.cuda.is_current_stream_capturing()):
+        return
+    key = (t.data_ptr(), t._version, t.numel(), scale)
+    if key in _f16_checked:
+        return
+    a = t.detach().float().abs() * scale
+    hi = float(a.max())
+    nz = a[a > 0]
+    lo = float(nz.min()) if nz.numel() else 1.0
+    if not (hi <= F16_MAX) or lo < F16_MIN_SUBNORMAL:
+        raise ValueError(f"{name}: |values| span [{lo:.3e}, {hi:.3e}], outside [{F16_MIN_SUBNORMAL:.3e}, {F16_MAX}]: "
+                         f"the n_embd-4096 bf16 Hadamard kernels hold them as float16")
+    if len(_f16_checked) > 4096:
+        _f16_checked.clear()
+    _f16_checked[key] = True
+
+
 def hadamard_linear_rope(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tensor, alpha: torch.Tensor,
                          beta: torch.Tensor, freqs_cis: torch.Tensor, head_dim: int) -> torch.Tensor:
     """HadamardLinear forward followed by apply_rotary_emb (chassis.py:339-345)
@@ -217,6 +257,9 @@ def hadamard_linear_rope(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.
         return y
     table = torch.view_as_real(freqs_cis[:T].contiguous())
     assert table.shape == (T, head_dim // 2, 2) and table.dtype == torch.float32, "freqs_cis shape"
+    if half_scales_used(dt, in_o, out_o):
+        check_half_range("alpha", alpha)
+        check_half_range("beta", beta)
     alpha = alpha.detach().float().contiguous()
     beta = beta.detach().float().contiguous()
     vec = True
@@ -278,6 +321,9 @@ def hadamard_linear_multi(x: torch.Tensor, in_o: int, out_o: int, layers, freqs_
     kws, als, bes, yps = [], [], [], []
     mask = 0
     for i, (kw, a, b, rope) in enumerate(layers):
+        if half_scales_used(dt, in_o, out_o):
+            check_half_range("alpha", a)
+            check_half_range("beta", b)
         a = a.detach().float().contiguous()
         b = b.detach().float().contiguous()
         keep += [a, b]
@@ -333,6 +379,9 @@ def hadamard_linear(x: torch.Tensor, in_o: int, out_o: int, kweight: torch.Tenso
     y = torch.empty(lead + (32 * gsy,), device=x.device, dtype=dt)
     if rows == 0:
         return y
+    if half_scales_used(dt, in_o, out_o):
+        check_half_range("alpha", alpha)
+        check_half_range("beta", beta)
     alpha = alpha.detach().float().contiguous()
     beta = beta.detach().float().contiguous()
     assert alpha.numel() == 32 * in_o and beta.numel() == 32 * out_o, "alpha/beta shapes"
@@ -505,6 +554,8 @@ def head_mixer(x: torch.Tensor, kweight: torch.Tensor, beta: torch.Tensor, out: 
         assert B == 1 or y.stride(0) == T * y.stride(1), "head mixer output rows must be evenly spaced"
     if B * T == 0:
         return y
+    if half_scales_used(dt, D, D):
+        check_half_range("head mixer beta", beta)
     b = beta.detach().float().contiguous()
     esz = x.element_size()
     nbytes = 2 * B * T * 32 * D * esz + kweight.numel() + 4 * D
@@ -587,6 +638,34 @@ def octonion_linear(x: torch.Tensor, in_o: int, out_o: int, B: torch.Tensor, bet
               y.data_ptr(), 8 * out_o, _hip.dtype_code(x.dtype), _hip.stream(x.device),
               kernel="octonion_gemm_kernel<%s>" % ("bf16" if x.dtype == torch.bfloat16 else "f32"),
               nbytes=nbytes, flops=flops)
+    return y
+
+
+def octonion_fused_linear(x: torch.Tensor, in_o: int, out_o: int, B: torch.Tensor,
+                          beta: torch.Tensor) -> torch.Tensor:
+    """The reference GPU module's forward (OctonionFusedLinear.forward,
+    cayley_dickson_cuda.py:650-668): x rounded to bf16, the bf16 product with
+    float32 accumulation rounded to bf16, times the float32 beta -> float32
+    [..., 8*out_o].  B from octonion_prepare in bf16; beta None = ones."""
+    _hip.require_device(x, "input")
+    assert B.dtype == torch.bfloat16, "the fused layer multiplies bf16 operands"
+    K = 8 * in_o
+    lead = x.shape[:-1]
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    xv, rows, ldx = _rows_view(x, K)
+    y = torch.empty(lead + (8 * out_o,), device=x.device, dtype=torch.float32)
+    if rows == 0:
+        return y
+    if ldx % 8 or xv.data_ptr() % 16:
+        xv = xv.reshape(rows, -1)[:, :K].contiguous()
+        ldx = K
+    beta_p = 0 if beta is None else beta.detach().float().contiguous().data_ptr()
+    nbytes = rows * 8 * (2 * in_o + 4 * out_o) + 8 * out_o * ((in_o + 3) // 4) + 4 * out_o
+    flops = 2 * rows * (8 * in_o) * (8 * out_o)
+    _hip.call("walsh_octonion_fused_fwd", xv.data_ptr(), ldx, rows, in_o, out_o, B.data_ptr(), beta_p,
+              y.data_ptr(), 8 * out_o, _hip.stream(x.device),
+              kernel="octonion_fused<bf16,f32>", nbytes=nbytes, flops=flops)
     return y
 
 

@@ -22,6 +22,7 @@ for every token (moe.py:434-436); ``threshold`` and ``min_experts`` are
 stored and unused, as there.  Equal probabilities select the lower expert
 index first.
 """
+import types
 from typing import Optional, Tuple
 
 import numpy as np
@@ -183,19 +184,28 @@ class _RoutedExperts(torch.autograd.Function):
     """FastMoEExperts on the routed pairs, forward and backward on HIP
     (walsh_moe_experts_fwd / walsh_moe_experts_bwd), float32 arithmetic.
     Inputs: x [B, T, E, 32], expert_weights [B, T, E], mask [B, T, E] (k
-    ones per token), k, the three latent weight tensors and the module."""
+    ones per token), k, the three latent weight tensors and the module.
+
+    A token's k experts are taken in ascending expert order (a stable sort
+    of its mask row), so a recomputed forward (activation checkpointing)
+    lists the pairs exactly as the first one did.  Everything the backward
+    reads (inputs, pair order and weights, the per-expert pair lists) goes
+    through save_for_backward: under non-reentrant checkpointing those are
+    the recomputation's tensors, consistent with each other, and nothing
+    outlives the forward outside the saved set."""
 
     @staticmethod
     def forward(ctx, x, expert_weights, mask, k, gate_w, up_w, down_w, mod):
         B, T, E, D = x.shape
         M = B * T
         dev = x.device
-        idx = mask.reshape(M, E).topk(k, dim=-1).indices
+        m2 = mask.detach().reshape(M, E)
+        idx = torch.sort(m2, dim=-1, descending=True, stable=True).indices[:, :k]
         w = expert_weights.detach().reshape(M, E).float().gather(-1, idx).contiguous()
         r = kernels.MoERoute(M, E, k, dev, dense=False, parts=1)
         r.topk_idx.copy_(idx)
         r.topk_w.copy_(w)
-        r.count_part.copy_(mask.reshape(M, E).sum(0).to(torch.int32).view(1, E))
+        r.count_part.copy_(m2.sum(0).to(torch.int32).view(1, E))
         r.probsum_part.zero_()
         lists = kernels.moe_scatter(r)
         gammas, packed = mod.quantized()
@@ -204,22 +214,24 @@ class _RoutedExperts(torch.autograd.Function):
         y = torch.zeros(M, E * D, device=dev, dtype=torch.float32)
         if M:
             kernels.moe_experts(x2d, y, r, lists, frags, gammas, mod.hidden)
-        ctx.save_for_backward(x2d, idx, gammas, *packed)
-        ctx.route, ctx.lists, ctx.shape, ctx.H, ctx.x_dtype = r, lists, (B, T, E, D), mod.hidden, x.dtype
+        ctx.save_for_backward(x2d, idx, r.topk_w, *lists, gammas, *packed)
+        ctx.shape, ctx.k, ctx.H, ctx.x_dtype = (B, T, E, D), k, mod.hidden, x.dtype
         return y.view(B, T, E, D)
 
     @staticmethod
     def backward(ctx, gy):
-        x2d, idx, gammas, pg, pu, pd = ctx.saved_tensors
+        x2d, idx, topk_w, lst, offset, toff, gammas, pg, pu, pd = ctx.saved_tensors
         B, T, E, D = ctx.shape
         M = B * T
         need_x, need_w_route = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         need_w = any(ctx.needs_input_grad[4:7])
+        route = types.SimpleNamespace(M=M, E=E, k=ctx.k, topk_w=topk_w)
         gy2d = gy.reshape(M, E * D).float().contiguous()
-        dx, dpair, grads = kernels.moe_experts_bwd(x2d, gy2d, ctx.route, ctx.lists, (pg, pu, pd), gammas, ctx.H,
-                                                   need_w=need_w)
+        dx, dpair, grads = kernels.moe_experts_bwd(x2d, gy2d, route, (lst, offset, toff), (pg, pu, pd), gammas,
+                                                   ctx.H, need_w=need_w)
         d_ew = None
         if need_w_route:
+            # dpair[t, j] belongs to expert idx[t, j]: the same saved order the pair lists were built from
             d_ew = torch.zeros(M, E, device=gy.device, dtype=torch.float32).scatter_(1, idx, dpair).view(B, T, E)
         gx = dx.view(B, T, E, D).to(ctx.x_dtype) if need_x else None
         gg, gu, gd = grads if grads is not None else (None, None, None)

@@ -52,11 +52,17 @@ class OctonionLinearFunction(torch.autograd.Function):
     CayleyDicksonFunction, cayley_dickson_cuda.py:428-567): the exact
     transpose of the forward's signed-permutation block matrix for dx, and
     dW / dbeta folded from gy^T x; the weight gradient passes the STE clamp
-    of physics.quantize_ternary (physics.py:48-50)."""
+    of physics.quantize_ternary (physics.py:48-50).  ``fused``: the forward
+    is the reference GPU module's (bf16 operands, the product rounded to
+    bf16, times beta in float32: a float32 result); the roundings pass the
+    gradient straight through."""
 
     @staticmethod
-    def forward(ctx, x, weight, beta, layer):
-        y = kernels.octonion_linear(x, layer.in_o, layer.out_o, layer.block_matrix(x.dtype), beta)
+    def forward(ctx, x, weight, beta, layer, fused):
+        if fused:
+            y = kernels.octonion_fused_linear(x, layer.in_o, layer.out_o, layer.block_matrix(torch.bfloat16), beta)
+        else:
+            y = kernels.octonion_linear(x, layer.in_o, layer.out_o, layer.block_matrix(x.dtype), beta)
         ctx.layer = layer
         ctx.save_for_backward(x, weight, beta)
         return y
@@ -65,20 +71,17 @@ class OctonionLinearFunction(torch.autograd.Function):
     def backward(ctx, gy):
         x, weight, beta = ctx.saved_tensors
         layer = ctx.layer
-        nx, nw, nb, _ = ctx.needs_input_grad
+        nx, nw, nb, _, _ = ctx.needs_input_grad
         packed = layer.ternary_state()[1]
         gx, dw, db = kernels.octonion_linear_bwd(x, gy.to(x.dtype).contiguous(), layer.in_o, layer.out_o, packed,
                                                  beta, latent=weight, need=(nx, nw, nb))
-        return gx, dw, db, None
+        return gx, dw, db, None, None
 
 
-class OctonionFusedLinear(nn.Module):
-    """Octonion ternary linear (cayley_dickson_cuda.py:622-668): 8 parts
-    [..., in_o] in, 8 parts [..., out_o] out, y_i scaled by beta [out_o].
-
-    Computes in the activation dtype (float32 matrix cores for float32
-    inputs, bf16 operands with float32 accumulation under bf16 autocast or
-    for bf16 inputs) and returns that dtype."""
+class _OctonionTernaryBase(nn.Module):
+    """Parameters of the octonion ternary layers (physics.py:55-64,
+    cayley_dickson_cuda.py:628-641): latent ``weight`` [8, out_o, in_o] drawn
+    from U(-1, 1) and ``beta`` [out_o] = sqrt(3 / (2 in_o))."""
 
     def __init__(self, in_features, out_features, bias=False):
         super().__init__()
@@ -103,25 +106,47 @@ class OctonionFusedLinear(nn.Module):
     def block_matrix(self, dtype: torch.dtype) -> torch.Tensor:
         return _prepared(self._wcache, self.weight, lambda: self.ternary_state()[1], self.in_o, self.out_o, dtype)
 
-    def forward_full(self, x: torch.Tensor) -> torch.Tensor:
-        """Rows x [..., 8*in_o] (parts side by side) -> [..., 8*out_o] in the activation dtype."""
-        dt = act_dtype(x)
-        x = x if x.dtype == dt else x.to(dt)
-        if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad or self.beta.requires_grad):
-            return OctonionLinearFunction.apply(x, self.weight, self.beta, self)
-        return kernels.octonion_linear(x, self.in_o, self.out_o, self.block_matrix(dt), self.beta)
+    def _tracked(self, x):
+        return torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad or self.beta.requires_grad)
 
     def forward(self, x_parts):
         y = self.forward_full(_parts_to_rows(x_parts, self.in_o))
         return tuple(y.split(self.out_o, dim=-1))
 
 
-class OctonionTernaryLinearRef(OctonionFusedLinear):
-    """physics.py:53-82: same parameters and math; returns the input dtype."""
+class OctonionFusedLinear(_OctonionTernaryBase):
+    """Octonion ternary linear, the reference's GPU module
+    (cayley_dickson_cuda.py:622-668): 8 parts [..., in_o] in, 8 parts
+    [..., out_o] out.  As there, the input is rounded to bf16, the product
+    accumulates in float32 and is rounded to bf16 (the fused kernel's output,
+    :402, :411, :421), and the module multiplies it by the float32 beta
+    (:668), so the result is float32 whatever the input dtype or autocast."""
 
-    def forward(self, x_parts):
-        dt = x_parts[0].dtype
-        return tuple(y.to(dt) for y in super().forward(x_parts))
+    def forward_full(self, x: torch.Tensor) -> torch.Tensor:
+        """Rows x [..., 8*in_o] (parts side by side) -> float32 [..., 8*out_o]."""
+        xb = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
+        if self._tracked(x):
+            return OctonionLinearFunction.apply(xb, self.weight, self.beta, self, True)
+        return kernels.octonion_fused_linear(xb, self.in_o, self.out_o, self.block_matrix(torch.bfloat16),
+                                             self.beta)
+
+
+class OctonionTernaryLinearRef(_OctonionTernaryBase):
+    """physics.py:53-82, the reference's CPU module: the same parameters and
+    math, computed in the activation dtype (float32 matrix cores for float32
+    inputs, bf16 operands with float32 accumulation under bf16 autocast or
+    for bf16 inputs).  The result has the dtype of y * beta in the
+    reference: the input dtype promoted with beta's (float32)."""
+
+    def forward_full(self, x: torch.Tensor) -> torch.Tensor:
+        out_dt = torch.promote_types(x.dtype, self.beta.dtype)
+        dt = act_dtype(x)
+        x = x if x.dtype == dt else x.to(dt)
+        if self._tracked(x):
+            y = OctonionLinearFunction.apply(x, self.weight, self.beta, self, False)
+        else:
+            y = kernels.octonion_linear(x, self.in_o, self.out_o, self.block_matrix(dt), self.beta)
+        return y if y.dtype == out_dt else y.to(out_dt)
 
 
 OctonionTernaryLinear = OctonionFusedLinear
@@ -129,7 +154,9 @@ OctonionTernaryLinear = OctonionFusedLinear
 
 class OctonionPackedLinear(nn.Module):
     """Inference layer holding 2-bit packed codes (cayley_dickson_cuda.py:702-772):
-    buffer ``weight_packed`` [8, out_o, in_o//4] uint8 and parameter ``beta``."""
+    buffer ``weight_packed`` [8, out_o, in_o//4] uint8 and parameter ``beta``.
+    Its forward is OctonionFusedLinear's (float32 = bf16 product times beta,
+    :761-765)."""
 
     def __init__(self, in_features, out_features, bias=False):
         super().__init__()
@@ -149,10 +176,9 @@ class OctonionPackedLinear(nn.Module):
         return packed
 
     def forward_full(self, x):
-        dt = act_dtype(x)
-        x = x if x.dtype == dt else x.to(dt)
-        B = _prepared(self._wcache, self.weight_packed, lambda: self.weight_packed, self.in_o, self.out_o, dt)
-        return kernels.octonion_linear(x, self.in_o, self.out_o, B, self.beta)
+        B = _prepared(self._wcache, self.weight_packed, lambda: self.weight_packed, self.in_o, self.out_o,
+                      torch.bfloat16)
+        return kernels.octonion_fused_linear(x, self.in_o, self.out_o, B, self.beta)
 
     def forward(self, x_parts):
         y = self.forward_full(_parts_to_rows(x_parts, self.in_o))
