@@ -279,6 +279,27 @@ class Oracle:
         u = self.linear(x, p + '.up_proj')
         return self.linear(F.silu(g) * u, p + '.down_proj')
 
+    def block(self, h, l, freqs):
+        """mHCLlamaBlock.forward (mhc.py:507-534) of layer l on the streams
+        h [B, T, n, C] with the RoPE rows freqs [T, head_dim/2]."""
+        sd = self.sd
+        B, T = h.shape[0], h.shape[1]
+        p = f'layers.{l}'
+        h = self.stream(h, p + '.attn_stream',
+                        lambda v: self.attention(self.rmsnorm(v, sd[p + '.attention_norm.weight']),
+                                                 p + '.attention', freqs))
+        if self.use_moe:
+            ffn = lambda v: self.moe(self.rmsnorm(v, sd[p + '.ffn_norm.weight']), p + '.feed_forward')[0]  # noqa: E731
+        else:
+            ffn = lambda v: self.swiglu(self.rmsnorm(v, sd[p + '.ffn_norm.weight']), p + '.feed_forward')  # noqa: E731
+        h = self.stream(h, p + '.ffn_stream', ffn)
+        if self.use_channel_mod:
+            # the [B*n, T, C] view of the streams (mhc.py:528-532)
+            hf = h.reshape(B * self.n, T, self.C)
+            hn = self.rmsnorm(hf, sd[p + '.channel_mod_norm.weight'])
+            h = (hf + self.channel_mod(hn, p + '.channel_mod')).view(B, T, self.n, self.C)
+        return h
+
     def loss(self, idx, targets):
         """mHCWalsh.forward's loss with targets (mhc.py:668-672): logits of
         every position, cross-entropy with ignore_index -1."""
@@ -295,20 +316,7 @@ class Oracle:
         h = h.view(B, T, self.n, self.C)
         freqs = sd['freqs_cis'][:T]
         for l in range(self.n_layer):
-            p = f'layers.{l}'
-            h = self.stream(h, p + '.attn_stream',
-                            lambda v: self.attention(self.rmsnorm(v, sd[p + '.attention_norm.weight']),
-                                                     p + '.attention', freqs))
-            if self.use_moe:
-                ffn = lambda v: self.moe(self.rmsnorm(v, sd[p + '.ffn_norm.weight']), p + '.feed_forward')[0]  # noqa: E731
-            else:
-                ffn = lambda v: self.swiglu(self.rmsnorm(v, sd[p + '.ffn_norm.weight']), p + '.feed_forward')  # noqa: E731
-            h = self.stream(h, p + '.ffn_stream', ffn)
-            if self.use_channel_mod:
-                # the [B*n, T, C] view of the streams (mhc.py:528-532)
-                hf = h.reshape(B * self.n, T, self.C)
-                hn = self.rmsnorm(hf, sd[p + '.channel_mod_norm.weight'])
-                h = (hf + self.channel_mod(hn, p + '.channel_mod')).view(B, T, self.n, self.C)
+            h = self.block(h, l, freqs)
         hm = h.reshape(B, T, self.n * self.C) @ sd['stream_merge.weight'].t() + sd['stream_merge.bias']
         ho = self.rmsnorm(hm, sd['norm.weight'])
         logits = ho[:, [-1], :] @ sd['output.weight'].t()
