@@ -300,12 +300,18 @@ __device__ __forceinline__ void attn_step_frags(AttnState &st, const u32x2 (&qf)
         s[j] = t;
     }
     const float pinf = opaque_inf();
-    float mj[4];
+    // the running max is the same in a query's four lanes, so it can start
+    // the chain: 16 scores and m_run in 8 three-input maxima (v_max3_f32;
+    // m_run is already canonical, so the compiler puts no canonicalising
+    // max in front), then the two lane swaps
+    float mx = fmaxf(fmaxf(st.m_run, s[0].x), s[0].y);
+    mx = fmaxf(fmaxf(mx, s[0].z), s[0].w);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) mj[j] = max2(max2(s[j].x, s[j].y, pinf), max2(s[j].z, s[j].w, pinf), pinf);
-    float mx = max2(max2(mj[0], mj[1], pinf), max2(mj[2], mj[3], pinf), pinf);
-    mx = max_over_rows(mx, pinf);
-    const float m_new = max2(st.m_run, mx, pinf);
+    for (int j = 1; j < 4; ++j) {
+        mx = fmaxf(fmaxf(mx, s[j].x), s[j].y);
+        mx = fmaxf(fmaxf(mx, s[j].z), s[j].w);
+    }
+    const float m_new = max_over_rows(mx, pinf);
     // v_exp_f32 directly: arguments are <= 0 (or -inf -> 0); results below
     // the float32 normal range flush to zero
     const float alpha = __builtin_amdgcn_exp2f((st.m_run - m_new) * sl2);
@@ -458,12 +464,16 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PfArgs a) {
 // Whole-head variant, for heads whose K and V fit in LDS together (T_pad *
 // (D + 4) * 2 + D * (T_pad + 4) * 2 bytes; head_dim 16 up to about 2,200
 // positions): one workgroup of 16 waves per (sequence, head) stages K
-// (row-major) and V (transposed) once, then each wave takes 16-query
-// sub-tiles in a snake
-// order (w, 31 - w, 32 + w, 63 - w, ...) so every wave gets about the same
-// number of key steps.  No barriers after the staging.  (gridDim.z
-// workgroups may share a head, each taking its share of the sub-tiles; one
-// measured fastest at head_dim 16, T = 1024: 51 us against 60 us for two.)
+// (row-major) and V (transposed) once, then the waves take 16-query
+// sub-tiles from a counter in LDS, longest first (sub-tile s needs
+// floor((16 s + 15) / 64) + 1 key steps).  A static split of equal step
+// counts does not balance: the SIMD issues from its oldest wave first, so
+// the oldest waves finish early and the rest run with fewer waves per SIMD
+// (half the VALU rate at one).  Taking work as a wave frees up keeps every
+// wave busy until the last few short sub-tiles.  No barriers after the
+// staging.  (gridDim.z workgroups may share a head, each with its own
+// counter over every gridDim.z-th sub-tile; one measured fastest at
+// head_dim 16, T = 1024.)
 constexpr int kPhWaves = 16;
 
 template <int D>
@@ -477,11 +487,11 @@ __global__ __launch_bounds__(64 * kPhWaves) void prefill_attn_head_kernel(PfArgs
     const int vs = tpad + 4;
     uint16_t *k_l = ph_smem;                         // [tpad][ks]
     uint16_t *vt_l = ph_smem + tpad * ks;            // [D][vs]
+    __shared__ int next_tile;
     const int h = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
-    // gridDim.z workgroups share a head: global wave index over them
-    const int nw = kPhWaves * (int)gridDim.z, wave = (int)blockIdx.z * kPhWaves + (tid >> 6);
     const int n = lane & 15, kq = lane >> 4;
+    if (tid == 0) next_tile = 0;
     const uint16_t *kbase = a.k + b * a.kv_sb + h * a.kv_sh;
     const uint16_t *vbase = a.v + b * a.kv_sb + h * a.kv_sh;
     // stage K and V^T; rows T .. tpad - 1 are zeros (finite, masked)
@@ -503,11 +513,15 @@ __global__ __launch_bounds__(64 * kPhWaves) void prefill_attn_head_kernel(PfArgs
         }
     }
     __syncthreads();
-    const int nst = tpad / 16;
-    for (int i = 0;; ++i) {
-        const int stile = nw * i + ((i & 1) ? nw - 1 - wave : wave);
-        if (nw * i >= nst) break;
-        if (stile >= nst) continue;
+    // this workgroup's sub-tiles: nst - 1 - (z + Z j), j = 0, 1, ... (z =
+    // blockIdx.z, Z = gridDim.z), in that order (decreasing length)
+    const int nst = tpad / 16, Z = (int)gridDim.z, z = (int)blockIdx.z;
+    for (;;) {
+        int j = 0;
+        if (lane == 0) j = atomicAdd(&next_tile, 1);
+        j = __builtin_amdgcn_readfirstlane(__shfl(j, 0));
+        const int stile = nst - 1 - (z + Z * j);
+        if (stile < 0) break;  // wave-uniform: every wave leaves once the counter passes the last sub-tile
         const int qw = 16 * stile, qi = qw + n;
         const int qc = qi < a.T ? qi : a.T - 1;
         u32x2 qf[ND];
@@ -679,10 +693,11 @@ WALSH_EXPORT int walsh_prefill_attention(const void *q, int64_t q_sb, int64_t q_
     PfArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o, q_sb, q_sh, q_st,
              kv_sb, kv_sh, kv_st, o_sb, o_sh, o_st, (int)T, (int)ceil_div(T, kPfQ), scale * 1.4426950408889634f};
     hipStream_t s = (hipStream_t)stream;
-    // whole heads in LDS when they fit (tpad rows of K and of V^T, padded)
+    // whole heads in LDS when they fit (tpad rows of K and of V^T, padded;
+    // 256 bytes kept for the kernel's static LDS, its sub-tile counter)
     const int64_t tpad = ceil_div(T, 64) * 64;
     const int64_t head_lds = (tpad * (D + 4) + D * (tpad + 4)) * 2;
-    if (D == 16 && head_lds <= device_info().max_shared_per_block) {
+    if (D == 16 && head_lds + 256 <= device_info().max_shared_per_block) {
         launch(prefill_attn_head_kernel<16>, dim3((unsigned)H, (unsigned)B, 1u), dim3(64 * kPhWaves),
                (uint32_t)head_lds, s, a, (int)tpad);
         return check_hip(hipGetLastError(), fn);
