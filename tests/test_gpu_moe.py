@@ -529,3 +529,58 @@ def test_moe_ffn_single_launch(M, kmax, expansion, ydt):
     sel = np.zeros((M, 16), bool)
     np.put_along_axis(sel, idx.astype(np.int64), True, -1)
     assert np.all(yv[~sel] == 0)
+
+
+def test_moe_probsum_reproducible():
+    """The per-expert probability sums behind the aux loss (moe.py:544-560)
+    are bitwise the same on every run: every routing kernel adds them in a
+    fixed order (one LDS row per wave, rows added in wave order; the
+    single-launch kernel reduces its routing waves' tokens with DPP row
+    shifts and row swaps).  Three runs each of the single-launch MoE
+    (config 3: 16,384 tokens), the three-launch router, the top-k kernel and
+    the n_embd-4096 router's logits + top-k kernel at prefill rows; the
+    totals against the float64 sum of the dense probabilities."""
+    from src.model import kernels
+    B, T, C, k = 16, 1024, 512, 6
+    m = make_moe(C, max_experts=k, seed=5)
+    gen = torch.Generator().manual_seed(5)
+    xb = torch.randn(B, T, C, generator=gen).bfloat16().cuda()
+
+    def runs(fn):
+        out = []
+        for _ in range(3):
+            r = fn()
+            torch.cuda.synchronize()
+            out.append((r.probsum_part.cpu().numpy().copy(), r.count_part.cpu().numpy().copy(), r))
+        for ps, cnt, _ in out[1:]:
+            assert np.array_equal(ps.view(np.uint32), out[0][0].view(np.uint32))
+            assert np.array_equal(cnt, out[0][1])
+        return out[0][2]
+
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        def fused():
+            m(xb)
+            return m._route
+        rf = runs(fused)
+
+        def three():
+            m.use_fused = False
+            try:
+                m(xb)
+            finally:
+                m.use_fused = True
+            return m._route
+        r3 = runs(three)
+    check(rf.probsum.cpu().numpy(), r3.probsum.cpu().numpy(), 1e-3, "single vs three launches")
+    rng = np.random.default_rng(6)
+    lg = torch.from_numpy(rng.standard_normal((5000, 128)).astype(np.float32)).cuda()
+    rt = runs(lambda: kernels.moe_topk(lg, 6, dense=True))
+    ref = rt.probs.double().sum(0).cpu().numpy()
+    check(rt.probsum.double().cpu().numpy(), ref, 1e-6, "top-k kernel probsum vs float64 sum of its probabilities")
+    C5, H5, E5 = 4096, 1024, 128
+    x5 = torch.from_numpy(rng.standard_normal((2048, C5)).astype(np.float32)).cuda().bfloat16()
+    w1 = torch.from_numpy((rng.standard_normal((H5, C5)) * 0.02).astype(np.float32)).cuda().bfloat16()
+    w2 = torch.from_numpy((rng.standard_normal((E5, H5)) * 0.02).astype(np.float32)).cuda().bfloat16()
+    rw = runs(lambda: kernels.moe_router_wide(x5, w1, w2, E5, 6, dense=True))
+    check(rw.probsum.double().cpu().numpy(), rw.probs.double().sum(0).cpu().numpy(), 1e-6,
+          "wide router probsum vs float64 sum of its probabilities")

@@ -73,7 +73,9 @@ struct RouteOut {
 
 // Softmax and top-k of one 16-token tile.  Lane (t, q) holds lg[et][j] =
 // logit of expert 16*et + 4q + j of its token; the token's 4 lanes (q = 0..3)
-// cooperate through cross-lane exchanges.  Results: p = probabilities,
+// cooperate through cross-lane exchanges: the lanes of quads q ^ 1 and q ^ 2
+// are lane ^ X1 and lane ^ X2 (16 and 32 for t = lane % 16, q = lane / 16;
+// 1 and 2 for q = lane % 4, whose exchanges stay inside a DPP quad).  Results: p = probabilities,
 // rank = position of each of the lane's experts in the token's order
 // (largest probability first, lower expert index on ties; >= k when not
 // selected), sel = bit j of sel[et] set when rank[et][j] < k, and den =
@@ -85,11 +87,27 @@ template <int NET> struct TopK {
     float den;
 };
 
+// The value of lane (l ^ X): X = 16 or 32 through ds_bpermute; X = 1 or 2
+// (lanes of one quad) as a DPP quad permutation, a modifier on a VALU move
+// with no LDS round trip.
+template <int X> __device__ __forceinline__ int xchg_i(int v) {
+    if constexpr (X == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+    else if constexpr (X == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    else return __shfl_xor(v, X);
+}
+template <int X> __device__ __forceinline__ float xchg(float v) { return __int_as_float(xchg_i<X>(__float_as_int(v))); }
+
+// The value of lane l - N of the same 16-lane row (DPP row_shr; 0 where
+// l - N falls before the row).
+template <int N> __device__ __forceinline__ float row_shr(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + N, 0xf, 0xf, true));
+}
+
 // x > y in the routing order (ties: the lower expert index wins; lower_x
 // says whether x's expert index is the lower one).
 __device__ __forceinline__ int beats(float x, float y, bool lower_x) { return (x > y) || (x == y && lower_x); }
 
-template <int NET>
+template <int NET, int X1 = 16, int X2 = 32>
 __device__ __forceinline__ void topk_core(float (&lg)[NET][4], int net, int E, int k, int q, TopK<NET> &r) {
     // softmax (fp32): max, exp, sum over the token's 4 lanes
     float mx = -INFINITY;
@@ -101,8 +119,8 @@ __device__ __forceinline__ void topk_core(float (&lg)[NET][4], int net, int E, i
             if (et >= net || e >= E) lg[et][j] = -INFINITY;
             mx = fmaxf(mx, lg[et][j]);
         }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = fmaxf(mx, xchg<X1>(mx));
+    mx = fmaxf(mx, xchg<X2>(mx));
     float sum = 0.f;
 #pragma unroll
     for (int et = 0; et < NET; ++et)
@@ -111,8 +129,8 @@ __device__ __forceinline__ void topk_core(float (&lg)[NET][4], int net, int E, i
             r.p[et][j] = (lg[et][j] == -INFINITY) ? 0.f : expf(lg[et][j] - mx);
             sum += r.p[et][j];
         }
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
+    sum += xchg<X1>(sum);
+    sum += xchg<X2>(sum);
 #pragma unroll
     for (int et = 0; et < NET; ++et)
 #pragma unroll
@@ -126,11 +144,11 @@ __device__ __forceinline__ void topk_core(float (&lg)[NET][4], int net, int E, i
         for (int j = 0; j < 4; ++j) o[j] = (4 * q + j < E) ? r.p[0][j] : -1.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            a1[j] = __shfl_xor(o[j], 16);
-            a2[j] = __shfl_xor(o[j], 32);
+            a1[j] = xchg<X1>(o[j]);
+            a2[j] = xchg<X2>(o[j]);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a3[j] = __shfl_xor(a1[j], 32);
+        for (int j = 0; j < 4; ++j) a3[j] = xchg<X2>(a1[j]);
         const bool l1 = (q ^ 1) < q, l2 = (q ^ 2) < q, l3 = (q ^ 3) < q;
         float ssum = 0.f;
         r.sel[0] = 0;
@@ -149,8 +167,8 @@ __device__ __forceinline__ void topk_core(float (&lg)[NET][4], int net, int E, i
             r.sel[0] |= s ? 1u << j : 0u;
             ssum += s ? r.p[0][j] : 0.f;
         }
-        ssum += __shfl_xor(ssum, 16);
-        ssum += __shfl_xor(ssum, 32);
+        ssum += xchg<X1>(ssum);
+        ssum += xchg<X2>(ssum);
         r.den = fmaxf(ssum, 1e-8f);
     } else {
         // k rounds of (largest probability, lowest expert index on ties)
@@ -175,10 +193,16 @@ __device__ __forceinline__ void topk_core(float (&lg)[NET][4], int net, int E, i
                     bv = better ? r.p[et][j] : bv;
                     be = better ? e : be;
                 }
-#pragma unroll
-            for (int sh = 16; sh <= 32; sh <<= 1) {
-                const float ov = __shfl_xor(bv, sh);
-                const int oe = __shfl_xor(be, sh);
+            {
+                const float ov = xchg<X1>(bv);
+                const int oe = xchg_i<X1>(be);
+                const bool better = beats(ov, bv, oe < be);
+                bv = better ? ov : bv;
+                be = better ? oe : be;
+            }
+            {
+                const float ov = xchg<X2>(bv);
+                const int oe = xchg_i<X2>(be);
                 const bool better = beats(ov, bv, oe < be);
                 bv = better ? ov : bv;
                 be = better ? oe : be;
@@ -212,11 +236,11 @@ __device__ __forceinline__ void zero_block(void *y, int bf16, int64_t at) {
     }
 }
 
-// Outputs of a routed tile (see RouteOut); counts and probability sums go
-// to the workgroup's LDS accumulators cnt_l / ps_l.
+// Outputs of a routed tile (see RouteOut); counts go to the workgroup's LDS
+// counters cnt_l, probability sums to this wave's row ps_w (PartSums).
 template <int NET>
 __device__ __forceinline__ void route_tile(float (&lg)[NET][4], int net, int tok, bool tok_ok, int q,
-                                           const RouteOut &o, int *cnt_l, float *ps_l) {
+                                           const RouteOut &o, int *cnt_l, float *ps_w) {
     const int E = o.E;
     TopK<NET> r;
     topk_core<NET>(lg, net, E, o.k, q, r);
@@ -265,28 +289,41 @@ __device__ __forceinline__ void route_tile(float (&lg)[NET][4], int net, int tok
             const int e = 16 * et + 4 * q + j;
             if ((threadIdx.x & 15) == 0 && e < E) {
                 if (c > 0.f) atomicAdd(cnt_l + e, (int)c);
-                atomicAdd(ps_l + e, ps);
+                ps_w[e] += ps;
             }
         }
     }
 }
 
-__device__ __forceinline__ void part_init(int *cnt_l, float *ps_l) {
-    for (int e = threadIdx.x; e < kMaxE; e += blockDim.x) {
-        cnt_l[e] = 0;
-        ps_l[e] = 0.f;
+// Per-workgroup partial sums in LDS.  Counts: integer atomics (exact in any
+// order).  Probability sums: one row per wave, each row written only by its
+// own wave (the lanes of one instruction add to distinct experts) and the
+// rows added in wave order by part_store, so the float sums are the same on
+// every run.
+constexpr int kPartRows = 8;
+struct PartSums {
+    int cnt[kMaxE];
+    float ps[kPartRows][kMaxE];
+};
+
+__device__ __forceinline__ void part_init(PartSums &s) {
+    for (int i = threadIdx.x; i < kPartRows * kMaxE; i += blockDim.x) {
+        s.ps[i / kMaxE][i % kMaxE] = 0.f;
+        if (i < kMaxE) s.cnt[i] = 0;
     }
 }
 
 // Store this workgroup's partial sums in row blockIdx.x (and zero the rows
 // no workgroup of this launch owns).  Same-address global atomics from
 // every workgroup would serialise across the chip.
-__device__ __forceinline__ void part_store(const int *cnt_l, const float *ps_l, int *count, float *probsum, int E,
-                                           int n_part) {
+__device__ __forceinline__ void part_store(const PartSums &s, int *count, float *probsum, int E, int n_part) {
     __syncthreads();
+    const int rows = (int)(blockDim.x >> 6) < kPartRows ? (int)(blockDim.x >> 6) : kPartRows;
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        count[(int64_t)blockIdx.x * E + e] = cnt_l[e];
-        probsum[(int64_t)blockIdx.x * E + e] = ps_l[e];
+        float ps = s.ps[0][e];
+        for (int w = 1; w < rows; ++w) ps += s.ps[w][e];
+        count[(int64_t)blockIdx.x * E + e] = s.cnt[e];
+        probsum[(int64_t)blockIdx.x * E + e] = ps;
         for (int r = blockIdx.x + gridDim.x; r < n_part; r += gridDim.x) {
             count[(int64_t)r * E + e] = 0;
             probsum[(int64_t)r * E + e] = 0.f;
@@ -306,9 +343,8 @@ struct RouterArgs {
 
 template <typename T, bool BF16MMA, int NET>
 __global__ __launch_bounds__(kMoeThreads, 2) void moe_route_kernel(RouterArgs a) {
-    __shared__ int cnt_l[kMaxE];
-    __shared__ float ps_l[kMaxE];
-    part_init(cnt_l, ps_l);
+    __shared__ PartSums part;
+    part_init(part);
     __syncthreads();
     constexpr uint32_t esz = sizeof(T);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -361,17 +397,16 @@ __global__ __launch_bounds__(kMoeThreads, 2) void moe_route_kernel(RouterArgs a)
         for (int et = 0; et < NET; ++et)
 #pragma unroll
             for (int j = 0; j < 4; ++j) l2[et][j] = BF16MMA ? bf16r(lg[et][j]) : lg[et][j];
-        route_tile(l2, a.net, tok, tok_ok, q, a.o, cnt_l, ps_l);
+        route_tile(l2, a.net, tok, tok_ok, q, a.o, part.cnt, part.ps[wave]);
     }
-    part_store(cnt_l, ps_l, a.o.count, a.o.probsum, a.o.E, a.o.n_part);
+    part_store(part, a.o.count, a.o.probsum, a.o.E, a.o.n_part);
 }
 
 template <int NET>
 __global__ __launch_bounds__(kMoeThreads) void moe_topk_kernel(const float *__restrict__ logits, int net,
                                                                RouteOut o) {
-    __shared__ int cnt_l[kMaxE];
-    __shared__ float ps_l[kMaxE];
-    part_init(cnt_l, ps_l);
+    __shared__ PartSums part;
+    part_init(part);
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = lane & 15, q = lane >> 4;
@@ -387,9 +422,9 @@ __global__ __launch_bounds__(kMoeThreads) void moe_topk_kernel(const float *__re
                 const int e = 16 * et + 4 * q + j;
                 lg[et][j] = (tok_ok && et < net && e < o.E) ? logits[(int64_t)tok * o.E + e] : -INFINITY;
             }
-        route_tile(lg, net, tok, tok_ok, q, o, cnt_l, ps_l);
+        route_tile(lg, net, tok, tok_ok, q, o, part.cnt, part.ps[wave]);
     }
-    part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
+    part_store(part, o.count, o.probsum, o.E, o.n_part);
 }
 
 // Top-k routing for 16 < E <= 128 experts: one wavefront per token, lane l
@@ -438,7 +473,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // wave holds as lg[0] (expert lane) and lg[1] (expert lane + 64), -inf past
 // E.  Every lane of the wave takes part.
 __device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], const RouteOut &o, int *cnt_l,
-                                           float *ps_l, int *sel_l = nullptr) {
+                                           float *ps_w, int *sel_l = nullptr) {
     const int lane = threadIdx.x & 63;
     const int E = o.E, k = o.k;
     float p[2];
@@ -486,7 +521,7 @@ __device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], const 
             if (sel_l) sel_l[at] = e[h];  // (LDS copy for a caller that goes on to the experts)
             atomicAdd(cnt_l + e[h], 1);
         }
-        atomicAdd(ps_l + e[h], p[h]);
+        ps_w[e[h]] += p[h];
         if (o.probs) o.probs[pe] = p[h];
         if (o.mask) o.mask[pe] = sel[h] ? 1.f : 0.f;
         if (o.wdense) o.wdense[pe] = sel[h] ? __fdiv_rn(p[h], den) : 0.f;
@@ -495,9 +530,8 @@ __device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], const 
 }
 
 __global__ __launch_bounds__(kMoeThreads) void moe_topk_rank_kernel(const float *__restrict__ logits, RouteOut o) {
-    __shared__ int cnt_l[kMaxE];
-    __shared__ float ps_l[kMaxE];
-    part_init(cnt_l, ps_l);
+    __shared__ PartSums part;
+    part_init(part);
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int tok = blockIdx.x * kMoeWaves + wave; tok < o.M; tok += gridDim.x * kMoeWaves) {
@@ -507,9 +541,9 @@ __global__ __launch_bounds__(kMoeThreads) void moe_topk_rank_kernel(const float 
             const int e = lane + 64 * h;
             lg[h] = e < o.E ? logits[(int64_t)tok * o.E + e] : -INFINITY;
         }
-        rank_token(tok, lg, o, cnt_l, ps_l);
+        rank_token(tok, lg, o, part.cnt, part.ps[wave]);
     }
-    part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
+    part_store(part, o.count, o.probsum, o.E, o.n_part);
 }
 
 __global__ void moe_zero_kernel(int *count, float *probsum, int n) {
@@ -767,10 +801,11 @@ __global__ __launch_bounds__(kMoeThreads, 2) void moe_experts_kernel(ExpArgs a) 
 // matrix cores.  A workgroup (8 waves, two per SIMD so that one wave's
 // matrix-core and memory waits overlap the other's VALU work) takes 64
 // tokens at a time:
-//   0. the 64 x 512 input tile is copied to LDS (the only HBM read of x);
-//   1. wave w computes router hidden units 16w..16w+15 for all 64 tokens
-//      (its W1 rows come from L2 in the same batch of loads as the tile),
-//      applies silu and forms its partial logits over those 16 units;
+//   0. the 64 x 512 input tile is copied to LDS (the only HBM read of x),
+//      its rows requested in 16-token sub-tiles behind the wave's W1 rows;
+//   1. as each sub-tile lands (the later ones still in flight), wave w
+//      computes router hidden units 16w..16w+15 for its 16 tokens, applies
+//      silu and forms its partial logits over those 16 units;
 //   2. waves 0-3 each sum the 8 partial logits of 16 tokens (fixed order)
 //      and route them (softmax, top-k, weights): routing outputs, and a
 //      per-token selection mask and weights in LDS;
@@ -779,9 +814,11 @@ __global__ __launch_bounds__(kMoeThreads, 2) void moe_experts_kernel(ExpArgs a) 
 //      tokens' masks and a prefix count compact the tokens that did, which
 //      are processed 16 at a time (gate/up, silu, down) with x read back
 //      from LDS; outputs go straight to y (blocks are disjoint).
-// Per-expert counts and probability sums accumulate in LDS; each workgroup
-// stores its partial sums in its own row (same-address global atomics from
-// every workgroup would serialise across the chip).
+// Per-expert counts accumulate in LDS (integer atomics), probability sums
+// in a fixed order (DPP row shifts and row swaps within a routing wave, the
+// four waves' rows in order), so they are the same on every run; each
+// workgroup stores its partial sums in its own row (same-address global
+// atomics from every workgroup would serialise across the chip).
 constexpr int kFfnC = 512, kFfnE = 16, kFfnTok = 64, kFfnWaves = 8, kFfnThreads = 64 * kFfnWaves;
 constexpr int kXsStride = kFfnC * 2 + 16;  // bytes per token row of the LDS tile (padded)
 
@@ -846,7 +883,8 @@ __global__ __launch_bounds__(kFfnThreads, 1) void moe_ffn_kernel(FfnArgs a) {
     __shared__ int list_s[kFfnWaves][kFfnTok];
     __shared__ uint2 lut[256];
     __shared__ int cnt_s[kFfnE];
-    __shared__ float ps_s[kFfnE];
+    __shared__ float ps_s[kFfnE];                              // written by thread e only
+    __shared__ __align__(16) float ps_w[4][kFfnE];             // per routing wave, per tile
     static_assert(NH <= 8, "hidden <= 128");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int t = lane & 15, q = lane >> 4;
@@ -875,11 +913,23 @@ __global__ __launch_bounds__(kFfnThreads, 1) void moe_ffn_kernel(FfnArgs a) {
 
     for (int base = blockIdx.x * kFfnTok; base < M; base += gridDim.x * kFfnTok) {
         lds_barrier();  // the previous tile is no longer read
-        // 0. input tile -> LDS (rows past M read as zeros), with this wave's
-        //    router rows requested in the same batch of loads
+        // 0. this wave's router rows first (L2-resident: the x rows queue
+        //    behind them), then the input tile's rows (past M: zeros), wave
+        //    w taking rows 8i + w, so the rows of 16-token sub-tile s (i = 2s,
+        //    2s + 1) land in sub-tile order; then this wave's expert codes
+        //    (w, w + 8), decoded in phase 3.  (All reloaded per tile: kept
+        //    across the expert phase they would take its registers.)
         uint4 w1r[kFfnC / 32];
-        uint2 w2;
-        // this wave's experts (w, w + 8): packed codes, decoded in phase 3
+#pragma unroll
+        for (int ks = 0; ks < kFfnC / 32; ++ks) w1r[ks] = a.w1f[(wave * 16 + ks) * 64 + lane];
+        const uint2 w2 = a.w2f[wave * 64 + lane];
+        uint4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 8 * i + wave, c = lane;
+            const uint32_t off = base + r < M ? (uint32_t)(((int64_t)(base + r) * a.ldx + 8 * c) * 2) : kOOB;
+            v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        }
         uint32_t cg[2][NH / 2], cu[2][NH / 2], cd[2][NH / 2];
 #pragma unroll
         for (int x2 = 0; x2 < 2; ++x2) {
@@ -888,77 +938,82 @@ __global__ __launch_bounds__(kFfnThreads, 1) void moe_ffn_kernel(FfnArgs a) {
             load_codes<NH>(a.up_f + off, cu[x2]);
             load_codes<NH>(a.down_f + off, cd[x2]);
         }
-        {
-            uint4 v[8];
+        // 1. per sub-tile, as its rows land (the later sub-tiles still in
+        //    flight): router hidden units 16w..16w+15 of its 16 tokens, then
+        //    this wave's partial logits
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int r = 8 * i + wave, c = lane;
-                const uint32_t off = base + r < M ? (uint32_t)(((int64_t)(base + r) * a.ldx + 8 * c) * 2) : kOOB;
-                v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
-            }
+        for (int sub = 0; sub < 4; ++sub) {
 #pragma unroll
-            for (int ks = 0; ks < kFfnC / 32; ++ks) w1r[ks] = a.w1f[(wave * 16 + ks) * 64 + lane];
-            w2 = a.w2f[wave * 64 + lane];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) *(uint4 *)(xs + (8 * i + wave) * kXsStride + 16 * lane) = v[i];
-        }
-        lds_barrier();
-        // 1. router hidden units 16w..16w+15 for the 64 tokens, then partial logits
-        {
-            f32x4 acc[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int i = 2 * sub; i < 2 * sub + 2; ++i)
+                *(uint4 *)(xs + (8 * i + wave) * kXsStride + 16 * lane) = v[i];
+            lds_barrier();
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < kFfnC / 32; ++ks) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint4 b = *(const uint4 *)(xs + (16 * i + t) * kXsStride + (32 * ks + 8 * q) * 2);
-                    acc[i] = mma32(w1r[ks], b, acc[i]);
-                }
+                const uint4 b = *(const uint4 *)(xs + (16 * sub + t) * kXsStride + (32 * ks + 8 * q) * 2);
+                acc = mma32(w1r[ks], b, acc);
             }
+            float h[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float h[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) h[j] = silu_f(bf16r(acc[i][j]));
-                const uint2 hb{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
-                lp[wave][16 * i + t][q] = mma16bf(w2, hb, f32x4{0.f, 0.f, 0.f, 0.f});
-            }
+            for (int j = 0; j < 4; ++j) h[j] = silu_f(bf16r(acc[j]));
+            const uint2 hb{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+            lp[wave][16 * sub + t][q] = mma16bf(w2, hb, f32x4{0.f, 0.f, 0.f, 0.f});
         }
         lds_barrier();
-        // 2. routing of tokens 16w..16w+15 (waves 0-3)
+        // 2. routing of tokens 16w..16w+15 (waves 0-3).  Lane l takes token
+        //    16w + l / 4 and experts 4 (l % 4) .. +3: a token's four lanes
+        //    form a DPP quad, so the top-k exchanges stay in the VALU
         if (wave < 4) {
-            const int tl = 16 * wave + t, tok = base + tl;
+            const int rq = lane & 3, tl = 16 * wave + (lane >> 2), tok = base + tl;
             const bool tok_ok = tok < M;
-            f32x4 sl = lp[0][tl][q];
+            f32x4 sl = lp[0][tl][rq];
 #pragma unroll
-            for (int w = 1; w < kFfnWaves; ++w) sl += lp[w][tl][q];
+            for (int w = 1; w < kFfnWaves; ++w) sl += lp[w][tl][rq];
             float lg[1][4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) lg[0][j] = bf16r(sl[j]);
             TopK<1> r;
-            topk_core<1>(lg, 1, kFfnE, a.k, q, r);
-            f32x4 wv;
+            topk_core<1, 1, 2>(lg, 1, kFfnE, a.k, rq, r);
+            f32x4 wv, pv;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const bool sj = tok_ok && ((r.sel[0] >> j) & 1u);
                 wv[j] = sj ? __fdiv_rn(r.p[0][j], r.den) : 0.f;
                 if (sj) {
                     const int64_t at = (int64_t)tok * a.k + r.rank[0][j];
-                    a.topk_idx[at] = 4 * q + j;
+                    a.topk_idx[at] = 4 * rq + j;
                     a.topk_w[at] = wv[j];
                 }
-                if (sj) atomicAdd(&cnt_s[4 * q + j], 1);
-                if (tok_ok) atomicAdd(&ps_s[4 * q + j], r.p[0][j]);
+                if (sj) atomicAdd(&cnt_s[4 * rq + j], 1);
+                pv[j] = tok_ok ? r.p[0][j] : 0.f;
             }
-            *(f32x4 *)&ws[tl][4 * q] = wv;
-            uint32_t m = tok_ok ? (r.sel[0] & 15u) << (4 * q) : 0u;
-            m |= __shfl_xor(m, 16);
-            m |= __shfl_xor(m, 32);
-            if (q == 0) sel_s[tl] = m;
+            *(f32x4 *)&ws[tl][4 * rq] = wv;
+            // the wave's probability sums per expert in a fixed order: the 4
+            // tokens of each 16-lane row (DPP row shifts by 4 and 8, ending
+            // in lanes 12..15), then the 4 rows (row and half swaps)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v = pv[j];
+                v += row_shr<4>(v);
+                v += row_shr<8>(v);
+                const u32x2 h1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+                v = __uint_as_float(h1.x) + __uint_as_float(h1.y);
+                const u32x2 h2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+                pv[j] = __uint_as_float(h2.x) + __uint_as_float(h2.y);
+            }
+            if (lane >= 12 && lane < 16) *(f32x4 *)&ps_w[wave][4 * rq] = pv;
+            uint32_t m = tok_ok ? (r.sel[0] & 15u) << (4 * rq) : 0u;
+            m |= (uint32_t)xchg_i<1>((int)m);
+            m |= (uint32_t)xchg_i<2>((int)m);
+            if (rq == 0) sel_s[tl] = m;
         }
         lds_barrier();
-        // 3. experts w and w + 8 on the tokens that chose them
+        // this tile's probability sums: the four routing waves' rows in order
+        if (tid < kFfnE) ps_s[tid] += ((ps_w[0][tid] + ps_w[1][tid]) + ps_w[2][tid]) + ps_w[3][tid];
+        // 3. experts w and w + 8 on the tokens that chose them.  (Taking
+        //    (expert, group) items from a counter, with every expert's codes
+        //    in LDS, balanced the waves but ran slower: the expert phase is
+        //    bound by the SIMDs' VALU work, which that does not reduce.)
 #pragma unroll
         for (int x2 = 0; x2 < 2; ++x2) {
             const int e = wave + kFfnWaves * x2;
@@ -1144,10 +1199,9 @@ __global__ __launch_bounds__(64 * kR1Waves) void router_w1_small_kernel(const ui
 constexpr int kTopkPartMax = 64;  // H / 16 <= 64
 __global__ __launch_bounds__(kMoeThreads) void router_topk_part_kernel(const float *__restrict__ lpart, int nparts,
                                                                        RouteOut o) {
-    __shared__ int cnt_l[kMaxE];
-    __shared__ float ps_l[kMaxE];
+    __shared__ PartSums part;
     __shared__ __align__(16) float ws[kMoeWaves][kMaxE];
-    part_init(cnt_l, ps_l);
+    part_init(part);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int E = o.E, M = o.M;
     constexpr int kPer = kTopkPartMax / kMoeWaves;
@@ -1180,10 +1234,10 @@ __global__ __launch_bounds__(kMoeThreads) void router_topk_part_kernel(const flo
                 for (int w = 0; w < kMoeWaves; ++w) v += ws[w][ee];
                 lg[hh] = ee < E ? bf16r(v) : -INFINITY;
             }
-            rank_token(tok, lg, o, cnt_l, ps_l);
+            rank_token(tok, lg, o, part.cnt, part.ps[wave]);
         }
     }
-    part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
+    part_store(part, o.count, o.probsum, o.E, o.n_part);
 }
 
 constexpr int kR2Waves = 8;    // wave w: experts 16w..16w+15
@@ -1206,9 +1260,8 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
                                                                        RouteOut o) {
     constexpr int kR2Tok = 16 * TT;
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ int cnt_l[kMaxE];
-    __shared__ float ps_l[kMaxE];
-    part_init(cnt_l, ps_l);
+    __shared__ PartSums part;
+    part_init(part);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, fr = lane & 15, fq = lane >> 4;
     const int M = o.M, E = o.E, nch = H / 8, nks = H / 32;
     const __amdgpu_buffer_rsrc_t hr = make_rsrc(h, (uint32_t)((int64_t)M * ldh * 2));
@@ -1287,10 +1340,10 @@ __global__ __launch_bounds__(64 * kR2Waves) void router_w2_topk_kernel(const uin
                 const int e = lane + 64 * hh;
                 lg[hh] = e < E ? lg_l[tl * kR2LgStride + e] : -INFINITY;
             }
-            rank_token(m0 + tl, lg, o, cnt_l, ps_l);
+            rank_token(m0 + tl, lg, o, part.cnt, part.ps[wave]);
         }
     }
-    part_store(cnt_l, ps_l, o.count, o.probsum, o.E, o.n_part);
+    part_store(part, o.count, o.probsum, o.E, o.n_part);
 }
 
 // ------------------------------------------------------------------ decode-sized MoE
