@@ -330,20 +330,25 @@ def _queue_ahead(torch, steps, us_per_step=200.0):
     torch.cuda._sleep(int(min(steps * us_per_step, 50000.0) * 2500))
 
 
-def _graphs_per_input(torch, step, n):
-    """One captured HIP graph of step(i) per rotated input i < n (after the
-    caller's warmup has built the weight caches); returns a replay function
-    of the step index, or None when capture fails (the step then runs
-    eagerly)."""
+def _time_graph_of_steps(torch, step, steps, n):
+    """Seconds per step of ``steps`` steps captured in one HIP graph (after
+    the caller's warmup has built the weight caches) and replayed once after
+    one untimed replay; the last n outputs stay alive, so the outputs rotate
+    over n buffers as the inputs do.  None when capture fails."""
     try:
-        graphs = []
-        for i in range(n):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                step(i)
-            graphs.append(g)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs = [None] * n
+            for i in range(steps):
+                outs[i % n] = step(i)
+        g.replay()
         torch.cuda.synchronize()
-        return lambda i: graphs[i % n].replay()
+        t0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        del g, outs
+        return dt
     except Exception as e:  # noqa: BLE001
         print(f"graph capture failed ({type(e).__name__}: {e}); timing eager launches", file=sys.stderr)
         return None
@@ -409,9 +414,11 @@ def bench_moe(torch, args):
     for i in range(max(args.warmup, 1)):
         step(i)
     # the step is one kernel launch, shorter than the host's cost of a
-    # module call: timed as captured graphs (one per rotated input)
-    replay = None if args.eager else _graphs_per_input(torch, step, nbuf)
-    dt = _time_steps(torch, replay or step, args.steps, args.warmup)
+    # module call: the K timed steps run as one captured graph
+    dt = None if args.eager else _time_graph_of_steps(torch, step, args.steps, nbuf)
+    graphed = dt is not None
+    if dt is None:
+        dt = _time_steps(torch, step, args.steps, args.warmup)
     _queue_ahead(torch, args.steps)
     with _hip.LaunchTimer() as lt:
         for i in range(args.steps):
@@ -438,7 +445,7 @@ def bench_moe(torch, args):
                  "synthetic: x N(0,1), router N(0,0.02), experts U(-1,1) latents",
                  {"workload": "HadamardMoE n_embd 512, 16 experts, k 6, expansion 4", "global_batch": B,
                   "seq_len": T, "parallelism": "single GPU", "rotated_buffers": nbuf,
-                  "execution": "one HIP graph per rotated input" if replay else "eager launches"}, roof, cpu)
+                  "execution": "the timed steps as one HIP graph" if graphed else "eager launches"}, roof, cpu)
 
 
 def bench_router(torch, args):
