@@ -488,7 +488,13 @@ __global__ __launch_bounds__(64 * kPhWaves) void prefill_attn_head_kernel(PfArgs
     uint16_t *k_l = ph_smem;                         // [tpad][ks]
     uint16_t *vt_l = ph_smem + tpad * ks;            // [D][vs]
     __shared__ int next_tile;
-    const int h = blockIdx.x, b = blockIdx.y;
+    // heads to XCDs: the dispatcher deals consecutive workgroups to the 8
+    // XCDs in turn, so with H % 8 == 0 workgroup w runs on XCD w % 8.  Head
+    // (w % 8) (H / 8) + w / 8 puts H / 8 consecutive heads on one XCD: the
+    // 64 / D heads whose q / k / v share a 128-byte line of [B, T, H, D] rows
+    // (four at head_dim 16) fetch it into one L2 instead of four.
+    const int H = (int)gridDim.x, wg = (int)blockIdx.x;
+    const int h = H % 8 == 0 ? (wg % 8) * (H / 8) + wg / 8 : wg, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
     const int n = lane & 15, kq = lane >> 4;
     if (tid == 0) next_tile = 0;
