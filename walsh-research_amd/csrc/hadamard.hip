@@ -1652,18 +1652,28 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1) ? 2 : 1) void hadamard_s
         }
         fht32x4(acc);
         {
+            // beta from LDS four groups at a time, so the reads of a batch
+            // overlap (one at a time, each waited for, they serialise)
             const f32x4 *bl = bg_l + (nt * 4 + q) * 32;
 #pragma unroll
-            for (int h = 0; h < 32; ++h) {
-                const f32x4 v = acc[h] * bl[h];
-                if constexpr (BF16MMA) {
-                    uint2 e;
-                    e.x = pack_bf16x2(v.x, v.y);
-                    e.y = pack_bf16x2(v.z, v.w);
-                    st[h * 64 + lane] = e;
-                } else {
-                    st[h * 64 + lane] = v;
+            for (int h0 = 0; h0 < 32; h0 += 4) {
+                f32x4 b4[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b4[j] = bl[h0 + j];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int h = h0 + j;
+                    const f32x4 v = acc[h] * b4[j];
+                    if constexpr (BF16MMA) {
+                        uint2 e;
+                        e.x = pack_bf16x2(v.x, v.y);
+                        e.y = pack_bf16x2(v.z, v.w);
+                        st[h * 64 + lane] = e;
+                    } else {
+                        st[h * 64 + lane] = v;
+                    }
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         // up
@@ -1693,29 +1703,42 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1) ? 2 : 1) void hadamard_s
 #pragma unroll
             for (int j = 0; j < 4; ++j) voff[j] = (row_ok && o0 + j < g.out_o) ? yoff + (uint32_t)(o0 + j) * esz : kOOB;
         }
+        // beta and the stashed gate four groups at a time (reads of a batch
+        // in flight together)
 #pragma unroll
-        for (int h = 0; h < 32; ++h) {
-            const f32x4 uv = acc[h] * bl[h];
-            f32x4 gv;
-            if constexpr (BF16MMA) {
-                const uint2 e = st[h * 64 + lane];
-                gv.x = __uint_as_float(e.x << 16);
-                gv.y = __uint_as_float(e.x & 0xffff0000u);
-                gv.z = __uint_as_float(e.y << 16);
-                gv.w = __uint_as_float(e.y & 0xffff0000u);
-            } else {
-                gv = st[h * 64 + lane];
+        for (int h0 = 0; h0 < 32; h0 += 4) {
+            f32x4 b4[4];
+            SType e4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                b4[j] = bl[h0 + j];
+                e4[j] = st[(h0 + j) * 64 + lane];
             }
-            f32x4 hv;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) hv[j] = silu_fast(gv[j]) * uv[j];
-            if (VEC) {
-                Buf4<T>::store(hv, yr, voff[0], (uint32_t)h * hstride);
-            } else {
+            for (int j4 = 0; j4 < 4; ++j4) {
+                const int h = h0 + j4;
+                const f32x4 uv = acc[h] * b4[j4];
+                f32x4 gv;
+                if constexpr (BF16MMA) {
+                    const uint2 e = e4[j4];
+                    gv.x = __uint_as_float(e.x << 16);
+                    gv.y = __uint_as_float(e.x & 0xffff0000u);
+                    gv.z = __uint_as_float(e.y << 16);
+                    gv.w = __uint_as_float(e.y & 0xffff0000u);
+                } else {
+                    gv = e4[j4];
+                }
+                f32x4 hv;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) Buf4<T>::store1(hv[j], yr, voff[j], (uint32_t)h * hstride);
+                for (int j = 0; j < 4; ++j) hv[j] = silu_fast(gv[j]) * uv[j];
+                if (VEC) {
+                    Buf4<T>::store(hv, yr, voff[0], (uint32_t)h * hstride);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) Buf4<T>::store1(hv[j], yr, voff[j], (uint32_t)h * hstride);
+                }
             }
-            if ((h & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
