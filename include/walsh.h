@@ -199,7 +199,22 @@ int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t gsx, int64_t M
                               const uint8_t *kw_up, const float *alpha_up, const float *beta_up, void *h,
                               int64_t ldh, int64_t gsh, int dtype, void *stream);
 
-/* walsh_hadamard_dense_weight_bytes / walsh_hadamard_dense_prepare: float32
+/* walsh_hadamard_mlp_fwd: the whole SwiGLUMLP.forward, down(silu(gate(x)) *
+ *   up(x)) (src/model/chassis.py:498-504), in one launch for bf16 rows with
+ *   gate/up in_o -> hid_o and down hid_o -> out_o, in_o and out_o <= 16
+ *   (multiples of 4, e.g. n_embd 512) and 16 < hid_o <= 48 (two or three
+ *   16-wide hidden tiles).  x rows of 32*in_o values at x + m*ldx, y rows of
+ *   32*out_o at y + m*ldy; weights from walsh_hadamard_prepare for each
+ *   shape.  The hidden activation stays on chip; the result equals
+ *   walsh_hadamard_swiglu_fwd (gsh = roundup(hid_o, 4)) followed by
+ *   walsh_hadamard_linear_ex_fwd of the down projection bitwise. */
+int walsh_hadamard_mlp_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t hid_o, int64_t out_o,
+                           const uint8_t *kw_gate, const float *alpha_gate, const float *beta_gate,
+                           const uint8_t *kw_up, const float *alpha_up, const float *beta_up,
+                           const uint8_t *kw_down, const float *alpha_down, const float *beta_down, void *y,
+                           int64_t ldy, int dtype, void *stream);
+
+/* walsh_hadamard_dense_weight_bytes / walsh_hadamard_dense_prepare: float32/* walsh_hadamard_dense_weight_bytes / walsh_hadamard_dense_prepare: float32
  *   weights of a Hadamard-structured layer with dense per-group matrices
  *   (HadamardHeadMixerFused.W [32, head_dim, head_dim], fht_cuda.py:627-648)
  *   in the kernel's matrix-core layout, bf16 or float32 (dtype).  w is

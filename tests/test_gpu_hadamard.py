@@ -255,6 +255,47 @@ def test_hadamard_swiglu_and_padded_down(K, dtype, in_o, hid_o):
     assert_close(y.float().cpu().numpy(), ohad.hadamard_linear_f64(hq, cd, ad, bd), dtype, f"down {dtype}")
 
 
+@pytest.mark.parametrize("M,in_o,hid_o", [(8192, 16, 43), (20000, 16, 43), (100, 16, 48), (1, 16, 43),
+                                          (700, 16, 32), (333, 12, 20)])
+def test_hadamard_mlp_equals_swiglu_then_down(K, M, in_o, hid_o):
+    """walsh_hadamard_mlp_fwd (the whole SwiGLU MLP in one launch, the hidden
+    activation on chip) against walsh_hadamard_swiglu_fwd followed by the
+    down projection reading the padded hidden layout: bitwise.  20,000 rows
+    give a workgroup several 16-token tiles (the chunk areas reused across
+    tiles); hid_o 20 / 32 take two hidden tiles, 43 / 48 three; 1 and 333
+    rows leave partial tiles.  The output also against the float64 oracle of
+    the three layers."""
+    out_o = in_o
+    print(f"mlp case M={M} in_o={in_o} hid_o={hid_o}", flush=True)
+    rng = np.random.default_rng(M + hid_o)
+    cg = rng.integers(-1, 2, size=(32, hid_o, in_o)).astype(np.int8)
+    cu = rng.integers(-1, 2, size=(32, hid_o, in_o)).astype(np.int8)
+    cd = rng.integers(-1, 2, size=(32, out_o, hid_o)).astype(np.int8)
+    ag, au = (rng.uniform(0.5, 1.5, (32, in_o)).astype(np.float32) for _ in range(2))
+    bg, bu = (rng.uniform(0.1, 0.4, (32, hid_o)).astype(np.float32) for _ in range(2))
+    ad = rng.uniform(0.5, 1.5, (32, hid_o)).astype(np.float32)
+    bd = rng.uniform(0.1, 0.4, (32, out_o)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).cuda()  # noqa: E731
+    gen = torch.Generator(device="cuda").manual_seed(M)
+    x = torch.randn(M, 32 * in_o, device="cuda", generator=gen).bfloat16()
+    gate, up, down = (_prepare(K, cg), t(ag), t(bg)), (_prepare(K, cu), t(au), t(bu)), (_prepare(K, cd), t(ad), t(bd))
+    assert K.hadamard_mlp_supported(x, in_o, hid_o, out_o)
+    y = K.hadamard_mlp(x, in_o, hid_o, out_o, gate, up, down)
+    h = K.hadamard_swiglu(x, in_o, hid_o, gate, up)
+    gsh = ((hid_o + 3) // 4) * 4
+    y2 = K.hadamard_linear(h, hid_o, out_o, *down, gsx=gsh)
+    torch.cuda.synchronize()
+    nd = int((y.view(torch.int16) != y2.view(torch.int16)).sum())
+    print(f"mlp M={M} hid_o={hid_o}: {nd} of {y.numel()} outputs differ bitwise from the two launches", flush=True)
+    assert nd == 0
+    rows = np.unique(np.r_[0, M - 1, rng.integers(0, M, 64)])
+    xq = x[torch.from_numpy(rows).cuda()].float().cpu().numpy().astype(np.float64)
+    g = ohad.hadamard_linear_f64(xq, cg, ag, bg)
+    u = ohad.hadamard_linear_f64(xq, cu, au, bu)
+    ref = ohad.hadamard_linear_f64(g / (1 + np.exp(-g)) * u, cd, ad, bd)
+    assert_close(y[torch.from_numpy(rows).cuda()].float().cpu().numpy(), ref, torch.bfloat16, f"mlp M={M}")
+
+
 def test_launch_timer_records_kernel_time(K):
     """walsh_timing_*: every entry-point call inside LaunchTimer gets its
     kernel's own duration (hipExtLaunchKernelGGL events)."""

@@ -1743,6 +1743,193 @@ __global__ __launch_bounds__(kThreads, (BF16MMA && KC1) ? 2 : 1) void hadamard_s
     }
 }
 
+// ---------------------------------------------------------------- fused MLP
+// down(silu(gate(x)) * up(x)) (SwiGLUMLP.forward, chassis.py:498-504) in one
+// launch, for bf16 rows with in_o <= 16 (n_embd 512), a hidden width of two
+// or three 16-wide tiles (16 < hid_o <= 48) and a down projection with
+// out_o <= 16.  A workgroup takes one 16-token tile at a time:
+//   - wave nt < Nt runs the SwiGLU item of hidden tile nt as
+//     hadamard_swiglu_kernel does (gate into its LDS area, up, silu(g) u),
+//     rounds the hidden values to bf16 as that kernel's store does, and runs
+//     the down projection's input transform of chunk nt on them in
+//     registers: hidden tile nt's columns 16 nt + 4q .. +3 are exactly
+//     chunk nt's in the lane layout load_transform reads, so nothing is
+//     rearranged.  The transformed chunk (bf16, 16 KB) replaces the gate
+//     stash in the wave's area;
+//   - after a barrier wave 3 contracts the chunks in order into one
+//     accumulator chain (the one-wavefront chunk loop's order) and, after a
+//     second barrier that frees the areas for the next tile, runs the output
+//     transform, beta and the stores, overlapping the next tile's items.
+// The hidden activation never leaves the CU, and the output equals
+// walsh_hadamard_swiglu_fwd followed by the down projection bitwise.
+constexpr int kMlpDownWave = 3;
+
+__global__ __launch_bounds__(kThreads, 2) void hadamard_mlp_kernel(HadArgs g, HadArgs u, HadArgs d) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    void *lut = smem;
+    const int Nt = g.Nt;                                  // hidden tiles = down chunks (2 or 3)
+    f32x4 *ag_l = (f32x4 *)(smem + lut_bytes<true>());   // [1][4][32]
+    f32x4 *au_l = ag_l + 128;
+    f32x4 *bg_l = au_l + 128;                             // [Nt][4][32]
+    f32x4 *bu_l = bg_l + Nt * 128;
+    f32x4 *ad_l = bu_l + Nt * 128;                        // [Nt][4][32] down alpha per chunk
+    f32x4 *bd_l = ad_l + Nt * 128;                        // [1][4][32]
+    uint2 *areas = (uint2 *)(bd_l + 128);                 // [3][32][64]
+
+    const int tid = threadIdx.x;
+    {
+        const uint32_t byte = (uint32_t)tid;
+        float val[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) val[j] = (float)((int)((byte >> (6 - 2 * j)) & 3u) - 1);
+        ((uint2 *)lut)[byte] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
+    }
+    for (int e = tid; e < 128; e += kThreads) {
+        const int gg = e & 31, i0 = 4 * (e >> 5);
+        f32x4 va, vb, vd;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = i0 + j < g.in_o;
+            va[j] = ok ? g.alpha[gg * g.in_o + i0 + j] : 0.f;
+            vb[j] = ok ? u.alpha[gg * g.in_o + i0 + j] : 0.f;
+            vd[j] = i0 + j < d.out_o ? d.beta[gg * d.beta_h + i0 + j] * 0.03125f : 0.f;
+        }
+        ag_l[e] = va;
+        au_l[e] = vb;
+        bd_l[e] = vd;
+    }
+    for (int e = tid; e < Nt * 128; e += kThreads) {
+        const int h = e & 31, o0 = 4 * (e >> 5);
+        f32x4 va, vb, vd;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = o0 + j < g.out_o;
+            va[j] = ok ? g.beta[h * g.out_o + o0 + j] * 0.03125f : 0.f;
+            vb[j] = ok ? u.beta[h * g.out_o + o0 + j] * 0.03125f : 0.f;
+            vd[j] = o0 + j < d.in_o ? d.alpha[h * d.in_o + o0 + j] : 0.f;  // chunk e / 128, element (h, o0 + j)
+        }
+        bg_l[e] = va;
+        bu_l[e] = vb;
+        ad_l[e] = vd;
+    }
+    __syncthreads();
+
+    const int lane = tid & 63;
+    // logical wave: the down wave rotates over the SIMDs with the workgroup
+    const int wave = ((tid >> 6) - (int)blockIdx.x) & (kWaves - 1);
+    const int t = lane & 15, q = lane >> 4;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)g.M * g.ldx * 2));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(d.y, (uint32_t)((int64_t)d.M * d.ldy * 2));
+    const int n_tiles = (int)ceil_div(g.M, kTile);
+    for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const int row = tile * kTile + t;
+        const bool row_ok = row < g.M;
+        if (wave < Nt) {
+            const int nt = wave;
+            uint2 *st = areas + wave * 32 * 64;
+            const uint32_t xoff = (uint32_t)((int64_t)row * g.ldx * 2);
+            f32x4 acc[32];
+            {   // gate, into the area
+                XM<true> xm;
+                load_transform<uint16_t, true, true>(g, xr, xoff, row_ok, 0, q, ag_l, xm);
+#pragma unroll
+                for (int k = 0; k < 32; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+                contract<true>(g, nt, 0, lane, xm, lut, acc);
+            }
+            fht32x4(acc);
+            {
+                const f32x4 *bl = bg_l + (nt * 4 + q) * 32;
+#pragma unroll
+                for (int h0 = 0; h0 < 32; h0 += 4) {
+                    f32x4 b4[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) b4[j] = bl[h0 + j];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const f32x4 v = acc[h0 + j] * b4[j];
+                        st[(h0 + j) * 64 + lane] = uint2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            {   // up
+                XM<true> xm;
+                load_transform<uint16_t, true, true>(g, xr, xoff, row_ok, 0, q, au_l, xm);
+#pragma unroll
+                for (int k = 0; k < 32; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+                contract<true>(u, nt, 0, lane, xm, lut, acc);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            fht32x4(acc);
+            __builtin_amdgcn_sched_barrier(0);
+            // h = bf16(silu(g) u) (the SwiGLU kernel's stored value), then
+            // the down projection's alpha for chunk nt (zero past hid_o, so
+            // those columns contribute zeros, as the down projection's
+            // out-of-range loads do)
+            {
+                const f32x4 *bl = bu_l + (nt * 4 + q) * 32;
+                const f32x4 *al = ad_l + (nt * 4 + q) * 32;
+#pragma unroll
+                for (int h0 = 0; h0 < 32; h0 += 4) {
+                    f32x4 b4[4], a4[4];
+                    uint2 e4[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        b4[j] = bl[h0 + j];
+                        a4[j] = al[h0 + j];
+                        e4[j] = st[(h0 + j) * 64 + lane];
+                    }
+#pragma unroll
+                    for (int j4 = 0; j4 < 4; ++j4) {
+                        const int h = h0 + j4;
+                        const f32x4 uv = acc[h] * b4[j4];
+                        const uint2 e = e4[j4];
+                        const f32x4 gv{__uint_as_float(e.x << 16), __uint_as_float(e.x & 0xffff0000u),
+                                       __uint_as_float(e.y << 16), __uint_as_float(e.y & 0xffff0000u)};
+                        f32x4 hv;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) hv[j] = silu_fast(gv[j]) * uv[j];
+                        const uint32_t p0 = pack_bf16x2(hv.x, hv.y), p1 = pack_bf16x2(hv.z, hv.w);
+                        const f32x4 hb{__uint_as_float(p0 << 16), __uint_as_float(p0 & 0xffff0000u),
+                                       __uint_as_float(p1 << 16), __uint_as_float(p1 & 0xffff0000u)};
+                        acc[h] = hb * a4[j4];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            fht32x4(acc);
+            __builtin_amdgcn_sched_barrier(0);
+            // the transformed chunk replaces the gate stash (this wave's own
+            // area: its reads above are done, LDS operations run in order)
+            wave_lds_fence();
+#pragma unroll
+            for (int h = 0; h < 32; ++h)
+                st[h * 64 + lane] = uint2{pack_bf16x2(acc[h].x, acc[h].y), pack_bf16x2(acc[h].z, acc[h].w)};
+            lds_barrier();  // A: the chunks are in the areas
+            lds_barrier();  // B: the down wave has read them
+        } else if (wave == kMlpDownWave) {
+            lds_barrier();  // A
+            f32x4 acc[32];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int c = 0; c < Nt; ++c) {
+                XM<true> xm;
+                const uint2 *st = areas + c * 32 * 64;
+#pragma unroll
+                for (int h = 0; h < 32; ++h) xm.b[h] = st[h * 64 + lane];
+                contract<true>(d, 0, c, lane, xm, lut, acc);
+            }
+            lds_barrier();  // B
+            transform_store<uint16_t, true>(d, acc, yr, (uint32_t)((int64_t)row * d.ldy * 2), row_ok, 0, q, bd_l,
+                                            row);
+        } else {
+            lds_barrier();  // A
+            lds_barrier();  // B
+        }
+    }
+}
+
 // ---------------------------------------------------------------- standalone FHT
 // Normalised (or not) fast Walsh-Hadamard transform of rows of length
 // N = 2^logN (fht_cuda.py:281-309): rows staged in LDS, log2(N) butterfly
@@ -2278,6 +2465,50 @@ WALSH_EXPORT int walsh_hadamard_swiglu_fwd(const void *x, int64_t ldx, int64_t g
     const HadArgs ga = had_args(x, ldx, gsx, in_o, hid_o, kw_gate, alpha_gate, beta_gate, h, ldh, gsh);
     const HadArgs ua = had_args(x, ldx, gsx, in_o, hid_o, kw_up, alpha_up, beta_up, h, ldh, gsh);
     return hadamard_launch(fn, ga, &ua, M, dtype == WALSH_BF16, (hipStream_t)stream);
+}
+
+WALSH_EXPORT int walsh_hadamard_mlp_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, int64_t hid_o,
+                                       int64_t out_o, const uint8_t *kw_gate, const float *alpha_gate,
+                                       const float *beta_gate, const uint8_t *kw_up, const float *alpha_up,
+                                       const float *beta_up, const uint8_t *kw_down, const float *alpha_down,
+                                       const float *beta_down, void *y, int64_t ldy, int dtype, void *stream) {
+    const char *fn = "walsh_hadamard_mlp_fwd";
+    if (!x || !y || !kw_gate || !alpha_gate || !beta_gate || !kw_up || !alpha_up || !beta_up || !kw_down ||
+        !alpha_down || !beta_down)
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (dtype != WALSH_BF16 || in_o < 1 || in_o > kKChunk || in_o % 4 || hid_o <= kNTile || hid_o > 3 * kNTile ||
+        out_o < 1 || out_o > kNTile || out_o % 4)
+        return set_error(WALSH_ENOTSUP, "%s: needs bf16, in_o <= 16 and out_o <= 16 (multiples of 4), 16 < hid_o <= 48 "
+                         "(got in_o=%lld hid_o=%lld out_o=%lld)", fn, (long long)in_o, (long long)hid_o,
+                         (long long)out_o);
+    if (M < 0 || ldx < 32 * in_o || ldy < 32 * out_o || ldx % 4 || ldy % 4 || (uintptr_t)x % 8 || (uintptr_t)y % 8)
+        return set_error(WALSH_EINVAL, "%s: bad rows (M=%lld ldx=%lld ldy=%lld; rows 8-byte aligned, strides "
+                         "multiples of 4)", fn, (long long)M, (long long)ldx, (long long)ldy);
+    if (M == 0) return WALSH_OK;
+    HadArgs ga = had_args(x, ldx, in_o, in_o, hid_o, kw_gate, alpha_gate, beta_gate, nullptr, 0, hid_o);
+    HadArgs ua = had_args(x, ldx, in_o, in_o, hid_o, kw_up, alpha_up, beta_up, nullptr, 0, hid_o);
+    HadArgs da = had_args(nullptr, 0, hid_o, hid_o, out_o, kw_down, alpha_down, beta_down, y, ldy, out_o);
+    const int Nt = ga.Nt;
+    const size_t lds = lut_bytes<true>() + (size_t)16 * 128 * (2 + 3 * Nt + 1) + (size_t)3 * 32 * 64 * 8;
+    if (lds > (size_t)device_info().max_shared_per_block)
+        return set_error(WALSH_ENOTSUP, "%s: needs %zu B of LDS", fn, lds);
+    const int64_t ld = ldx > ldy ? ldx : ldy;
+    const int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * 2) / kTile * kTile;
+    const int64_t resident = (int64_t)device_info().cu_count * 2;
+    hipStream_t s = (hipStream_t)stream;
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        HadArgs g = ga, u = ua, d = da;
+        g.x = u.x = (const char *)x + r0 * ldx * 2;
+        d.y = (char *)y + r0 * ldy * 2;
+        g.M = u.M = d.M = (int)rows;
+        int64_t grid = ceil_div(rows, kTile);
+        if (grid > resident) grid = resident;
+        launch(hadamard_mlp_kernel, dim3((unsigned)grid), dim3(kThreads), (uint32_t)lds, s, g, u, d);
+        const int rc = check_hip(hipGetLastError(), fn);
+        if (rc) return rc;
+    }
+    return WALSH_OK;
 }
 
 // ---------------------------------------------------------------- head mixer

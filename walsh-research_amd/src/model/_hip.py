@@ -40,6 +40,8 @@ SIGNATURES = {
     "walsh_hadamard_linear_ex_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _I, _P]),
     "walsh_hadamard_swiglu_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                        _I, _P]),
+    "walsh_hadamard_mlp_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                    _I, _P]),
     "walsh_fht_fwd": (_I, [_P, _I64, _I64, _I, _P, _I, _P]),
     "walsh_hadamard_linear_rope_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I, _P]),
     "walsh_hadamard_linear_multi_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _I64, _I64,

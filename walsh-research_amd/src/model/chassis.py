@@ -331,6 +331,11 @@ class SwiGLUMLP(nn.Module):
             # a group-padded layout (stride roundup(hid_o, 4)) read in place by down_proj
             g, u, d = self.gate_proj.inner, self.up_proj.inner, self.down_proj.inner
             hid_o = g.out_o
+            if d.in_o == hid_o and kernels.hadamard_mlp_supported(x, g.in_o, hid_o, d.out_o):
+                # the whole MLP in one launch, the hidden activation on chip
+                return kernels.hadamard_mlp(x, g.in_o, hid_o, d.out_o, (g.ternary_state()[2], g.alpha, g.beta),
+                                            (u.ternary_state()[2], u.alpha, u.beta),
+                                            (d.ternary_state()[2], d.alpha, d.beta))
             h = kernels.hadamard_swiglu(x, g.in_o, hid_o, (g.ternary_state()[2], g.alpha, g.beta),
                                         (u.ternary_state()[2], u.alpha, u.beta))
             return kernels.hadamard_linear(h, d.in_o, d.out_o, d.ternary_state()[2], d.alpha, d.beta,

@@ -426,6 +426,41 @@ def hadamard_swiglu(x: torch.Tensor, in_o: int, hid_o: int, gate, up, gsh: int =
     return h
 
 
+def hadamard_mlp_supported(x: torch.Tensor, in_o: int, hid_o: int, out_o: int) -> bool:
+    """Shapes of walsh_hadamard_mlp_fwd: bf16 rows, in_o and out_o <= 16
+    (multiples of 4), 16 < hid_o <= 48."""
+    return (x.is_cuda and x.dtype == torch.bfloat16 and 0 < in_o <= 16 and in_o % 4 == 0 and 16 < hid_o <= 48
+            and 0 < out_o <= 16 and out_o % 4 == 0 and x.shape[-1] == 32 * in_o)
+
+
+def hadamard_mlp(x: torch.Tensor, in_o: int, hid_o: int, out_o: int, gate, up, down) -> torch.Tensor:
+    """down(silu(gate(x)) * up(x)) for three Hadamard linears (chassis.py:498-504)
+    in one launch; gate/up/down = (kweight, alpha, beta).  Returns
+    [..., 32*out_o] in x.dtype, bitwise equal to hadamard_swiglu followed by
+    the down projection."""
+    _hip.require_device(x, "input")
+    assert hadamard_mlp_supported(x, in_o, hid_o, out_o), "hadamard_mlp shape"
+    lead = x.shape[:-1]
+    xv, rows, ldx = _rows_view(x, 32 * in_o)
+    if xv.data_ptr() % 8 or ldx % 4:
+        xv = xv.contiguous()
+        ldx = xv.stride(0)
+    y = torch.empty(lead + (32 * out_o,), device=x.device, dtype=x.dtype)
+    if rows == 0:
+        return y
+    ws = []
+    for kw, a, b in (gate, up, down):
+        ws += [kw, a.detach().float().contiguous(), b.detach().float().contiguous()]
+    gsh = (hid_o + 3) // 4 * 4
+    nbytes = rows * 32 * (in_o + out_o) * 2 + 32 * (2 * hid_o * ((in_o + 3) // 4) + out_o * ((hid_o + 3) // 4))
+    flops = rows * (2 * (2 * 32 * in_o * hid_o + 10 * 32 * (in_o + hid_o)) + 32 * hid_o * 4
+                    + 2 * 32 * gsh * out_o + 10 * 32 * (gsh + out_o))
+    _hip.call("walsh_hadamard_mlp_fwd", xv.data_ptr(), ldx, rows, in_o, hid_o, out_o,
+              *[w.data_ptr() for w in ws], y.data_ptr(), 32 * out_o, _hip.dtype_code(x.dtype),
+              _hip.stream(x.device), kernel="hadamard_mlp_kernel<bf16>", nbytes=nbytes, flops=flops)
+    return y
+
+
 def hadamard_pack_transpose(packed: torch.Tensor, in_o: int, out_o: int) -> torch.Tensor:
     """Packed codes of the transposed layer: [32, in_o, ceil(out_o/4)] from
     [32, out_o, ceil(in_o/4)] (fht_cuda.py:65-93 packing of W^T)."""
