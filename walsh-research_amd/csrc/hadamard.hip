@@ -921,7 +921,14 @@ __global__ __launch_bounds__(kPairThreads, DENSE ? 3 : 4) void hadamard_pair_ker
     f32x4 *alpha_l = (f32x4 *)(smem + 256 * 8);   // [4 q][32 g]
     f32x4 *beta_l = alpha_l + 128;                 // [4 q][32 h]
     f32x4 *xch = beta_l + 128;                     // [2 HF][8][64 lanes]
-    const int l = blockIdx.x % an.n;
+    // (layer, first tile) of this workgroup.  Consecutive workgroups go to
+    // the 8 XCDs in turn; workgroups 8 (n k + l) + x (l < n) take layer l of
+    // tile slot 8 k + x, so the n layers of a tile run on one XCD and read
+    // its rows from one L2.  A last partial group of 8 n workgroups keeps
+    // slot b / n, layer b % n.
+    const int b = (int)blockIdx.x, n = an.n, full = (int)gridDim.x / (8 * n) * (8 * n);
+    const int l = b < full ? (b / 8) % n : b % n;
+    const int slot = b < full ? (b / (8 * n)) * 8 + b % 8 : b / n;
     const HadArgs &a = an.p[l];
     const int tid = threadIdx.x;
     for (int e = tid; e < 256; e += kPairThreads) {
@@ -948,7 +955,7 @@ __global__ __launch_bounds__(kPairThreads, DENSE ? 3 : 4) void hadamard_pair_ker
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
     const int n_tiles = (int)ceil_div(a.M, kTile);
     const int nb = (int)gridDim.x / an.n;
-    for (int tile = (int)blockIdx.x / an.n; tile < n_tiles; tile += nb) {
+    for (int tile = slot; tile < n_tiles; tile += nb) {
         if (hf == 0) pair_tile<0, DENSE>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
         else pair_tile<1, DENSE>(a, tile, lane, lut, alpha_l, beta_l, xch, xr, yr);
     }
