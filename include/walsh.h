@@ -214,7 +214,7 @@ int walsh_hadamard_mlp_fwd(const void *x, int64_t ldx, int64_t M, int64_t in_o, 
                            const uint8_t *kw_down, const float *alpha_down, const float *beta_down, void *y,
                            int64_t ldy, int dtype, void *stream);
 
-/* walsh_hadamard_dense_weight_bytes / walsh_hadamard_dense_prepare: float32/* walsh_hadamard_dense_weight_bytes / walsh_hadamard_dense_prepare: float32
+/* walsh_hadamard_dense_weight_bytes / walsh_hadamard_dense_prepare: float32
  *   weights of a Hadamard-structured layer with dense per-group matrices
  *   (HadamardHeadMixerFused.W [32, head_dim, head_dim], fht_cuda.py:627-648)
  *   in the kernel's matrix-core layout, bf16 or float32 (dtype).  w is
@@ -506,6 +506,28 @@ int walsh_mhc_pre_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int
                            float *h_pre, float *h_post, float *h_res, void *layer_in, int64_t ld_in,
                            const float *norm_w, float norm_eps, void *workspace, int64_t workspace_bytes, int dtype,
                            void *stream);
+
+/* walsh_mhc_post_pre_wide_fwd: the stream update of one mHCResidualStream
+ *   (src/model/mhc.py:366-381) fused with the wide mappings of the next one
+ *   (walsh_mhc_pre_wide_fwd, src/model/mhc.py:283-364), bf16 only: the
+ *   projection launch forms x_new[t, r, :] = sum_s h_res_prev[t, r, s]
+ *   x_old[t, s, :] + h_post_prev[t, r] out[t, :] from x_old and out as it
+ *   loads them, writes it (row stride ld_new) and feeds it to the matrix
+ *   cores, so the separate update pass (read x_old, write x_new) and the
+ *   projection's read of x_new become one pass; the per-token launch then
+ *   reads x_new as walsh_mhc_pre_wide_fwd reads x.  x_new is bitwise what
+ *   walsh_mhc_post_fwd writes; h_pre / h_post / h_res / layer_in equal
+ *   walsh_mhc_pre_wide_fwd's on x_new up to the float32 summation order of
+ *   the projection.  C a multiple of 32 up to 4096, row strides multiples of
+ *   8, 16-byte aligned buffers; workspace as walsh_mhc_pre_wide_workspace;
+ *   x_new may not alias x_old, nor the new h_post / h_res the previous
+ *   ones. */
+int walsh_mhc_post_pre_wide_fwd(const void *x_old, int64_t ld_old, const void *out, int64_t ld_out,
+                                const float *h_res_prev, const float *h_post_prev, void *x_new, int64_t ld_new,
+                                int64_t M, int64_t n, int64_t C, const void *phi_frag32, const float *coef,
+                                const float *bias, float rms_eps, int64_t n_iter, float sk_eps, float *h_pre,
+                                float *h_post, float *h_res, void *layer_in, int64_t ld_in, const float *norm_w,
+                                float norm_eps, void *workspace, int64_t workspace_bytes, int dtype, void *stream);
 
 /* walsh_mhc_post_fwd: x_new = H_res @ x + H_post^T (x) out
  *   (src/model/mhc.py:366-381).  out [M, C] row stride ld_out; x_new may not

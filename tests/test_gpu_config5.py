@@ -216,6 +216,57 @@ def test_mhc_pre_wide_vs_oracle_across_chunks(dtype):
         assert rel(got["layer_in"][j], ref["layer_in"][j])[0] <= tol
 
 
+@pytest.mark.parametrize("M,n,C", [(1, 4, 4096), (100, 4, 4096), (2051, 4, 4096), (40, 3, 96), (7, 2, 64),
+                                   (65568, 4, 4096)])
+def test_mhc_post_pre_wide_equals_separate_kernels(M, n, C):
+    """The stream update fused into the wide mapping's projection launch
+    (walsh_mhc_post_pre_wide_fwd, bf16): x_new bitwise walsh_mhc_post_fwd's
+    result; the mappings and layer input those of walsh_mhc_pre_wide_fwd on
+    that x_new (pinned against the oracle above) up to the projection's
+    float32 summation order (it runs column-major over the streams).
+    M=1 and 100 take many column splits, 2051 a ragged last tile, 65568 two
+    row chunks (x_new rows of 32 KiB)."""
+    from src.model import kernels
+    from src.model.chassis import RMSNorm
+    from src.model.mhc import mHCResidualStream, _rms_eps
+    dtype = torch.bfloat16
+    print(f"post+pre wide M={M} n={n} C={C}", flush=True)
+    torch.manual_seed(M + n + C)
+    stream = mHCResidualStream(C, n).cuda()
+    norm = RMSNorm(C).cuda()
+    g = torch.Generator().manual_seed(M * 3 + C)
+    with torch.no_grad():
+        for m in (stream.H_pre, stream.H_post, stream.H_res):
+            m.alpha.fill_(0.5)
+            m.bias.add_(0.5 * torch.randn(m.bias.shape, generator=g).cuda())
+            m.phi.weight.copy_(0.02 * torch.randn(m.phi.weight.shape, generator=g))
+        norm.weight.mul_(1 + 0.2 * torch.randn(C, generator=g).cuda())
+    gdev = torch.Generator(device="cuda").manual_seed(M + 7)
+    x_old = torch.randn(M, n, C, device="cuda", generator=gdev).to(dtype)
+    out = torch.randn(M, C, device="cuda", generator=gdev).to(dtype)
+    h_res_prev = torch.rand(M, n, n, device="cuda", generator=gdev) * 0.5
+    h_post_prev = torch.rand(M, n, device="cuda", generator=gdev) * 2
+    _, coef, bias, frag = stream.fused_params(dtype, x_old.device)
+    assert frag.numel() == 32 * n * C and kernels.mhc_pre_wide_supported(n, C)
+    eps = _rms_eps(dtype)
+    with torch.no_grad():
+        x_new, li, hp, hq, hr = kernels.mhc_post_pre_wide(x_old, out, h_res_prev, h_post_prev, frag, coef, bias, eps,
+                                                          norm_w=norm.weight, norm_eps=1e-6)
+        x_ref = kernels.mhc_post(x_old, out, h_res_prev, h_post_prev)
+        li_r, hp_r, hq_r, hr_r = kernels.mhc_pre_wide(x_ref, frag, coef, bias, eps, norm_w=norm.weight,
+                                                       norm_eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(x_new, x_ref)
+    for name, a, b in (("h_pre", hp, hp_r), ("h_post", hq, hq_r), ("h_res", hr, hr_r)):
+        d = (a - b).abs().max().item()
+        assert d <= 2e-5, f"{name}: max |diff| {d:.3e}"
+    # layer_in: bf16 values, a last-place difference where the float32 sums
+    # straddle a rounding boundary (2^-7 relative covers one bf16 ulp)
+    lf, lr = li.float(), li_r.float()
+    d = ((lf - lr).abs() / lr.abs().clamp_min(1e-3)).max().item()
+    assert d <= 2 ** -7, f"layer_in: max rel diff {d:.3e}"
+
+
 # --------------------------------------------------------------- config-5 layers
 def _make5(n_layer, block=64, seed=5, vocab=1000):
     from src.model import WalshConfig, mHCWalsh

@@ -1102,6 +1102,197 @@ __global__ __launch_bounds__(256) void mhc_proj_kernel(ProjArgs a) {
     if (j >= 0 && j < 4 && tile * 16 + m < a.M) dst[(int64_t)(tile * 16 + m) * kProjOut + kProjOut - 1] = accss[j];
 }
 
+// The previous stream's update fused into the projection (bf16): the same
+// work items, but a K split is a range of columns c of every stream, and the
+// lane's 8 columns of stream r are formed as mhc_post_kernel forms them
+// (x_new[t, r, c] = H_post[t, r] out[t, c] + sum_s H_res[t, r, s] x[t, s, c],
+// in that operation order, rounded to bf16), stored once, and fed to the
+// products from registers.  The rows are read once, not three times (update
+// read, update write, projection read); the products run c-major over the
+// streams, so the partial sums are those of mhc_proj_kernel on x_new up to
+// the order of the float32 accumulation.
+struct PostProjArgs {
+    const uint16_t *xo;       // previous streams [M, ld_xo]
+    int64_t ld_xo;
+    const uint16_t *out;      // the layer's output [M, ld_out]
+    int64_t ld_out;
+    const float *hr_prev, *hp_prev;  // [M, n, n], [M, n]
+    uint16_t *x_new;          // [M, ld_new]
+    int64_t ld_new;
+    int M, n, C, splits, cper;  // cper: columns per split (multiple of 32)
+    const uint16_t *phi32;    // [K/32][2][64][8]
+    float *part;              // [splits][M][25]
+};
+
+// One 32-column block of a work item's loads: the lane's 8 columns of each
+// previous stream and of the layer output, and the phi fragments of those
+// columns for each new stream.
+template <int N>
+struct PostProjBlock {
+    u32x4 x[N], o, p[N][2];
+};
+
+// No bounds selects: rows past M lie past the end of the x / out buffers
+// (which end at row M) and load zeros; a block at or past the split's end
+// (a prefetch beyond the last block) loads whatever lies there, within or
+// past the buffers, and is never formed.
+template <int N>
+__device__ __forceinline__ void post_proj_load(PostProjBlock<N> &b, const PostProjArgs &a,
+                                               __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t orr,
+                                               __amdgpu_buffer_rsrc_t pr, uint32_t xrow, uint32_t orow, int c, int kq,
+                                               int lane) {
+    const uint32_t co = (uint32_t)(c + 8 * kq) * 2;
+#pragma unroll
+    for (int s2 = 0; s2 < N; ++s2)
+        b.x[s2] = __builtin_amdgcn_raw_buffer_load_b128(xr, xrow + (uint32_t)(s2 * a.C) * 2 + co, 0, 0);
+    b.o = __builtin_amdgcn_raw_buffer_load_b128(orr, orow + co, 0, 0);
+#pragma unroll
+    for (int r = 0; r < N; ++r)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+            b.p[r][nt] = __builtin_amdgcn_raw_buffer_load_b128(
+                pr, (uint32_t)(((((r * a.C + c) >> 5) * 2 + nt) * 64 + lane) * 16), 0, 0);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Forms block d (0 or 1) of a pair of 32-column blocks: x_new goes to the
+// wave's LDS stage (row m at m * kStagePitch, block d at byte 64 d) and to
+// the matrix cores.
+constexpr int kStagePitch = 2 * 64 + 16;   // two blocks of a row + 16 bytes (conflict-free writes)
+
+template <int N>
+__device__ __forceinline__ void post_proj_block(const PostProjBlock<N> &b, const float (&hr)[N][N],
+                                                const float (&hp)[N], uint8_t *stage, int d, int m, int kq,
+                                                f32x4 (&acc)[2], f32x4 &accss) {
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        uint32_t w[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            // columns 2d, 2d + 1 of the lane's 8, in mhc_post_kernel's operation order
+            const uint32_t ow = d == 0 ? b.o.x : d == 1 ? b.o.y : d == 2 ? b.o.z : b.o.w;
+            float lo = hp[r] * bf16_lo(ow), hi = hp[r] * bf16_hi(ow);
+#pragma unroll
+            for (int s2 = 0; s2 < N; ++s2) {
+                const uint32_t xw = d == 0 ? b.x[s2].x : d == 1 ? b.x[s2].y : d == 2 ? b.x[s2].z : b.x[s2].w;
+                lo += hr[r][s2] * bf16_lo(xw);
+                hi += hr[r][s2] * bf16_hi(xw);
+            }
+            w[d] = pack_bf16x2(lo, hi);
+        }
+        const u32x4 nb = {w[0], w[1], w[2], w[3]};
+        *(u32x4 *)(stage + (r * 16 + m) * kStagePitch + 64 * d + 16 * kq) = nb;
+        // rows past M hold zeros (the loads gave zeros)
+        const bf16x8 x8 = __builtin_bit_cast(bf16x8, nb);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, __builtin_bit_cast(bf16x8, b.p[r][nt]), acc[nt], 0,
+                                                              0, 0);
+        accss = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8, x8, accss, 0, 0, 0);
+    }
+}
+
+// Stores a pair of blocks from the wave's LDS stage: each store instruction
+// covers 8 rows x 128 contiguous bytes (whole cache lines; stores of 64-byte
+// halves a block apart write HBM at a fraction of its rate).
+template <int N>
+__device__ __forceinline__ void post_proj_flush(const uint8_t *stage, const PostProjArgs &a,
+                                                __amdgpu_buffer_rsrc_t nr, int tile, int cb, int c1, int lane) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int chunk = lane & 7;             // 16-byte chunk of the row's 128 bytes
+    const bool cok = cb + 32 * (chunk >> 2) < c1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int row = 8 * i + (lane >> 3), t = tile * 16 + row;
+        const uint32_t nrow = t < a.M ? (uint32_t)((int64_t)t * a.ld_new * 2) : kOOB;
+#pragma unroll
+        for (int r = 0; r < N; ++r) {
+            const u32x4 v = *(const u32x4 *)(stage + (r * 16 + row) * kStagePitch + 16 * chunk);
+            __builtin_amdgcn_raw_buffer_store_b128(
+                v, nr, (nrow == kOOB || !cok) ? kOOB : nrow + (uint32_t)(r * a.C + cb + 8 * chunk) * 2, 0, 0);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int N>
+__global__ __launch_bounds__(256) void mhc_post_proj_kernel(PostProjArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t stage_all[4][N * 16 * kStagePitch];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, m = lane & 15,
+              kq = lane >> 4;
+    const int n_tiles = (int)ceil_div(a.M, 16);
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= n_tiles * a.splits) return;
+    const int tile = item / a.splits, split = item % a.splits;
+    const int C = a.C, K = N * C;
+    const int c0 = split * a.cper, c1 = min(C, c0 + a.cper);
+    const int tok = tile * 16 + m;
+    const bool ok = tok < a.M;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xo, (uint32_t)((int64_t)a.M * a.ld_xo * 2));
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.out, (uint32_t)((int64_t)a.M * a.ld_out * 2));
+    const __amdgpu_buffer_rsrc_t nr = make_rsrc(a.x_new, (uint32_t)((int64_t)a.M * a.ld_new * 2));
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.phi32, (uint32_t)((int64_t)K * 32 * 2));
+    // (tok < M + 16 and both buffers below 2^31 bytes: these offsets do not wrap)
+    const uint32_t xrow = (uint32_t)((int64_t)tok * a.ld_xo * 2);
+    const uint32_t orow = (uint32_t)((int64_t)tok * a.ld_out * 2);
+    uint8_t *stage = stage_all[wave];
+    // this lane's token's update coefficients, then the first two blocks'
+    // loads (issued after the coefficients', so that the wait at the head
+    // of the loop counts only block loads)
+    float hr[N][N], hp[N];
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        hp[r] = ok ? a.hp_prev[(int64_t)tok * N + r] : 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < N; ++s2) hr[r][s2] = ok ? a.hr_prev[(int64_t)tok * N * N + r * N + s2] : 0.f;
+    }
+    PostProjBlock<N> b0, b1;
+    __builtin_amdgcn_sched_barrier(0);
+    post_proj_load<N>(b0, a, xr, orr, pr, xrow, orow, c0, kq, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    post_proj_load<N>(b1, a, xr, orr, pr, xrow, orow, c0 + 32, kq, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, accss = {0.f, 0.f, 0.f, 0.f};
+    // two blocks in flight: a block's loads are issued while the block
+    // before it is formed, stored and multiplied.  No branches around them
+    // (a block past c1 loads zeros, stores nothing and adds zeros), so the
+    // compiler's wait before each block counts only that block's loads.
+    // (scheduling barriers keep the compiler from merging the two blocks'
+    // work and issuing both blocks' loads after it)
+    for (int cb = c0; cb < c1; cb += 64) {
+        post_proj_block<N>(b0, hr, hp, stage, 0, m, kq, acc, accss);
+        __builtin_amdgcn_sched_barrier(0);
+        post_proj_load<N>(b0, a, xr, orr, pr, xrow, orow, cb + 64, kq, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        if (cb + 32 < c1) post_proj_block<N>(b1, hr, hp, stage, 1, m, kq, acc, accss);
+        __builtin_amdgcn_sched_barrier(0);
+        post_proj_load<N>(b1, a, xr, orr, pr, xrow, orow, cb + 96, kq, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        post_proj_flush<N>(stage, a, nr, tile, cb, c1, lane);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // lane (n = m, q = kq) holds rows 4kq..4kq+3 (tokens) of column m (output)
+    float *dst = a.part + (int64_t)split * a.M * kProjOut;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const int o = 16 * nt + m;
+        if (o >= kProjOut - 1) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = tile * 16 + 4 * kq + j;
+            if (t < a.M) dst[(int64_t)t * kProjOut + o] = acc[nt][j];
+        }
+    }
+    const int j = m - 4 * kq;
+    if (j >= 0 && j < 4 && tile * 16 + m < a.M) dst[(int64_t)(tile * 16 + m) * kProjOut + kProjOut - 1] = accss[j];
+}
+
 struct ApplyArgs {
     const void *x;
     int64_t ldx;
@@ -1123,34 +1314,55 @@ __global__ __launch_bounds__(256) void mhc_apply_kernel(ApplyArgs a) {
     constexpr int kMaxQ = 16;                 // C <= 4096: 16 quads per lane
     __shared__ float dyn_s[4][kProjOut + 7];
     __shared__ float hpre_s[4][4];
+    __shared__ float par_s[4][32];            // coef[3], then bias[2n + n*n]
     __shared__ float red_s[4][64][kProjOut];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int tok = blockIdx.x * 4 + wave;
     const bool live = tok < a.M;
     const int n = a.n, C = a.C, K = n * C;
-    // sum the K splits: lane l loads splits l, l+64, ... (all loads in flight
-    // together), then lane o < 25 adds the 64 lane sums from LDS in lane order
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
+    const int nq = C / 4;
+    // the K split partials (splits <= 64: lane l holds split l) and the
+    // mapping parameters are requested before the row: loads complete in
+    // order, so waiting for them then does not wait for the row
+    float pv[kProjOut];
     {
-        float v[kProjOut];
+        const bool has = live && lane < a.splits;
+        const float *src = a.part + ((int64_t)(has ? lane : 0) * a.M + (live ? tok : 0)) * kProjOut;
 #pragma unroll
-        for (int o = 0; o < kProjOut; ++o) v[o] = 0.f;
-        if (live)
-            for (int sp = lane; sp < a.splits; sp += 64) {
-                const float *src = a.part + ((int64_t)sp * a.M + tok) * kProjOut;
-#pragma unroll
-                for (int o = 0; o < kProjOut; ++o) v[o] += src[o];
-            }
-#pragma unroll
-        for (int o = 0; o < kProjOut; ++o) red_s[wave][lane][o] = v[o];
+        for (int o = 0; o < kProjOut; ++o) pv[o] = has ? src[o] : 0.f;
     }
+    const int n_par = 3 + 2 * n + n * n;
+    const float par = lane < 3 ? a.coef[lane] : lane < n_par ? a.bias[lane - 3] : 0.f;
+    // bf16: the token's whole row (n x C <= 16384 values, 128 registers per
+    // lane) is requested next, 16 bytes (8 columns) per lane and load, so its
+    // round trip overlaps the split sums and the constraints below
+    constexpr int kRawO = sizeof(T) == 2 ? kMaxQ / 2 : 1;
+    u32x4 raw[kRawO][kMaxStreams];
+    if constexpr (sizeof(T) == 2) {
+        const uint32_t xrow0 = live ? (uint32_t)((int64_t)tok * a.ldx * esz) : kOOB;
+#pragma unroll
+        for (int j = 0; j < kRawO; ++j) {
+            const int c8 = 8 * (lane + 64 * j);
+#pragma unroll
+            for (int s = 0; s < kMaxStreams; ++s)
+                raw[j][s] = __builtin_amdgcn_raw_buffer_load_b128(
+                    xr, (xrow0 == kOOB || s >= n || c8 >= C) ? kOOB : xrow0 + (uint32_t)(s * C + c8) * esz, 0, 0);
+        }
+    }
+    // sum the splits: lane o < 25 adds the 64 lane values from LDS in lane
+    // (split) order
+#pragma unroll
+    for (int o = 0; o < kProjOut; ++o) red_s[wave][lane][o] = pv[o];
+    if (lane < n_par) par_s[wave][lane] = par;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane < kProjOut) {
         const int nl = a.splits < 64 ? a.splits : 64;
-        float v = 0.f;
-        for (int l = 0; l < nl; ++l) v += red_s[wave][l][lane];
-        dyn_s[wave][lane] = v;
+        float sum = 0.f;
+        for (int l = 0; l < nl; ++l) sum += red_s[wave][l][lane];
+        dyn_s[wave][lane] = sum;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1158,8 +1370,8 @@ __global__ __launch_bounds__(256) void mhc_apply_kernel(ApplyArgs a) {
     if (lane < 4) {
         const float rs = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(dyn_s[wave][kProjOut - 1], (float)K) + a.rms_eps));
         auto dynf = [&](int o) { return dyn_s[wave][o] * rs; };
-        token_constraints_quad(wave, lane, live ? tok : a.M, a.M, n, a.coef, a.bias, a.n_iter, a.sk_eps, dynf,
-                               &hpre_s[0][0], a.h_pre, a.h_post, a.h_res);
+        token_constraints_quad(wave, lane, live ? tok : a.M, a.M, n, &par_s[wave][0], &par_s[wave][3], a.n_iter,
+                               a.sk_eps, dynf, &hpre_s[0][0], a.h_pre, a.h_post, a.h_res);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1168,19 +1380,34 @@ __global__ __launch_bounds__(256) void mhc_apply_kernel(ApplyArgs a) {
     float hp[kMaxStreams];
 #pragma unroll
     for (int s = 0; s < kMaxStreams; ++s) hp[s] = hpre_s[wave][s];
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
     const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
     const uint32_t xrow = (uint32_t)((int64_t)tok * a.ldx * esz);
-    const int nq = C / 4;
+    // quad j of the lane: columns 4 q .. 4 q + 3 (bf16: the halves of the
+    // lane's 8-column groups, q = 2 (lane + 64 (j / 2)) + j % 2)
+    auto quad = [&](int j) { return sizeof(T) == 2 ? 2 * (lane + 64 * (j >> 1)) + (j & 1) : lane + 64 * j; };
     f32x4 v[kMaxQ];
     float sq = 0.f;
 #pragma unroll
     for (int j = 0; j < kMaxQ; ++j) {
-        const int q = lane + 64 * j;
+        const int q = quad(j);
         f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < kMaxStreams; ++s)
-            if (s < n) acc4 += hp[s] * Buf4<T>::load(xr, q < nq ? xrow + (uint32_t)(s * C + 4 * q) * esz : kOOB, 0);
+        for (int s = 0; s < kMaxStreams; ++s) {
+            if (s >= n) continue;
+            f32x4 xv;
+            if constexpr (sizeof(T) == 2) {
+                const u32x4 u = raw[j >> 1][s];
+                const uint32_t u0 = (j & 1) ? u.z : u.x, u1 = (j & 1) ? u.w : u.y;
+                xv = f32x4{__uint_as_float(u0 << 16), __uint_as_float(u0 & 0xffff0000u),
+                           __uint_as_float(u1 << 16), __uint_as_float(u1 & 0xffff0000u)};
+            } else {
+                xv = Buf4<T>::load(xr, q < nq ? xrow + (uint32_t)(s * C + 4 * q) * esz : kOOB, 0);
+            }
+            acc4 += hp[s] * xv;
+        }
+        // (bf16, C % 8 == 4: the upper half of the last group read the next
+        // stream's columns)
+        if (q >= nq) acc4 = f32x4{0.f, 0.f, 0.f, 0.f};
         v[j] = acc4;
         sq += acc4.x * acc4.x + acc4.y * acc4.y + acc4.z * acc4.z + acc4.w * acc4.w;
     }
@@ -1190,13 +1417,36 @@ __global__ __launch_bounds__(256) void mhc_apply_kernel(ApplyArgs a) {
         for (int sh = 1; sh < 64; sh <<= 1) sq += __shfl_xor(sq, sh);
         scale = 1.0f / sqrtf(__fdiv_rn(sq, (float)C) + a.norm_eps);
     }
+    if constexpr (sizeof(T) == 2) {
+        // 8 columns per store where both halves are in the row
 #pragma unroll
-    for (int j = 0; j < kMaxQ; ++j) {
-        const int q = lane + 64 * j;
-        if (q >= nq) continue;
-        f32x4 o = v[j] * scale;
-        if (a.norm_w) o *= *(const f32x4 *)(a.norm_w + 4 * q);
-        Buf4<T>::store(o, lr, (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz), 0);
+        for (int j = 0; j < kMaxQ; j += 2) {
+            const int q = quad(j);
+            if (q >= nq) continue;
+            f32x4 o0 = v[j] * scale, o1 = v[j + 1] * scale;
+            const uint32_t off = (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz);
+            if (q + 1 < nq) {
+                if (a.norm_w) {
+                    o0 *= *(const f32x4 *)(a.norm_w + 4 * q);
+                    o1 *= *(const f32x4 *)(a.norm_w + 4 * q + 4);
+                }
+                const u32x4 u = {pack_bf16x2(o0.x, o0.y), pack_bf16x2(o0.z, o0.w), pack_bf16x2(o1.x, o1.y),
+                                 pack_bf16x2(o1.z, o1.w)};
+                __builtin_amdgcn_raw_buffer_store_b128(u, lr, off, 0, 0);
+            } else {
+                if (a.norm_w) o0 *= *(const f32x4 *)(a.norm_w + 4 * q);
+                Buf4<T>::store(o0, lr, off, 0);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kMaxQ; ++j) {
+            const int q = quad(j);
+            if (q >= nq) continue;
+            f32x4 o = v[j] * scale;
+            if (a.norm_w) o *= *(const f32x4 *)(a.norm_w + 4 * q);
+            Buf4<T>::store(o, lr, (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz), 0);
+        }
     }
 }
 
@@ -1628,6 +1878,46 @@ WALSH_EXPORT int64_t walsh_mhc_pre_wide_workspace(int64_t M, int64_t n, int64_t 
     return (int64_t)mhc_wide_splits(M, n * C) * M * kProjOut * 4;
 }
 
+// The per-token apply launch of the wide mapping on rows [r0, r0 + rows)
+// (x already offset to row r0), after a projection wrote its partial sums.
+static void wide_apply_launch(const void *xc, int64_t ldx, int64_t rows, int64_t r0, int64_t n, int64_t C,
+                              int splits, const float *part, const float *coef, const float *bias, float rms_eps,
+                              int64_t n_iter, float sk_eps, float *h_pre, float *h_post, float *h_res, void *layer_in,
+                              int64_t ld_in, const float *norm_w, float norm_eps, int dtype, hipStream_t s) {
+    const int64_t esz = dtype == WALSH_BF16 ? 2 : 4;
+    ApplyArgs aa;
+    aa.x = xc;
+    aa.ldx = ldx;
+    aa.M = (int)rows;
+    aa.n = (int)n;
+    aa.C = (int)C;
+    aa.splits = splits;
+    aa.part = part;
+    aa.coef = coef;
+    aa.bias = bias;
+    aa.rms_eps = rms_eps;
+    aa.sk_eps = sk_eps;
+    aa.n_iter = (int)n_iter;
+    aa.h_pre = h_pre + r0 * n;
+    aa.h_post = h_post + r0 * n;
+    aa.h_res = h_res + r0 * n * n;
+    aa.layer_in = (char *)layer_in + r0 * ld_in * esz;
+    aa.ld_in = ld_in;
+    aa.norm_w = norm_w;
+    aa.norm_eps = norm_eps;
+    const dim3 B(256);
+    if (rows <= kApplyTokRows && splits <= 64) {
+        // few tokens: a workgroup per token
+        const dim3 G2((unsigned)rows);
+        if (dtype == WALSH_BF16) launch(mhc_apply_tok_kernel<uint16_t>, G2, B, 0, s, aa);
+        else launch(mhc_apply_tok_kernel<float>, G2, B, 0, s, aa);
+    } else {
+        const dim3 G2((unsigned)ceil_div(rows, 4));
+        if (dtype == WALSH_BF16) launch(mhc_apply_kernel<uint16_t>, G2, B, 0, s, aa);
+        else launch(mhc_apply_kernel<float>, G2, B, 0, s, aa);
+    }
+}
+
 WALSH_EXPORT int walsh_mhc_pre_wide_fwd(const void *x, int64_t ldx, int64_t M, int64_t n, int64_t C,
                                         const void *phi_frag32, const float *coef, const float *bias, float rms_eps,
                                         int64_t n_iter, float sk_eps, float *h_pre, float *h_post, float *h_res,
@@ -1648,6 +1938,8 @@ WALSH_EXPORT int walsh_mhc_pre_wide_fwd(const void *x, int64_t ldx, int64_t M, i
         return set_error(WALSH_ENOTSUP, "%s: pointers must be 16-byte aligned", fn);
     if (M == 0) return WALSH_OK;
     const int splits = mhc_wide_splits(M, K);
+    // the per-token launches hold one split per lane
+    if (splits > 64) return set_error(WALSH_ENOTSUP, "%s: %d K splits (at most 64)", fn, splits);
     const int64_t need = (int64_t)splits * M * kProjOut * 4;
     if (!workspace || workspace_bytes < need)
         return set_error(WALSH_EINVAL, "%s: workspace of %lld bytes needed", fn, (long long)need);
@@ -1673,36 +1965,77 @@ WALSH_EXPORT int walsh_mhc_pre_wide_fwd(const void *x, int64_t ldx, int64_t M, i
         const dim3 G1((unsigned)ceil_div(items, 4)), B(256);
         if (dtype == WALSH_BF16) launch(mhc_proj_kernel<uint16_t>, G1, B, 0, s, pa);
         else launch(mhc_proj_kernel<float>, G1, B, 0, s, pa);
-        ApplyArgs aa;
-        aa.x = xc;
-        aa.ldx = ldx;
-        aa.M = (int)rows;
-        aa.n = (int)n;
-        aa.C = (int)C;
-        aa.splits = splits;
-        aa.part = (const float *)workspace;
-        aa.coef = coef;
-        aa.bias = bias;
-        aa.rms_eps = rms_eps;
-        aa.sk_eps = sk_eps;
-        aa.n_iter = (int)n_iter;
-        aa.h_pre = h_pre + r0 * n;
-        aa.h_post = h_post + r0 * n;
-        aa.h_res = h_res + r0 * n * n;
-        aa.layer_in = (char *)layer_in + r0 * ld_in * esz;
-        aa.ld_in = ld_in;
-        aa.norm_w = norm_w;
-        aa.norm_eps = norm_eps;
-        if (rows <= kApplyTokRows && splits <= 64) {
-            // few tokens: a workgroup per token
-            const dim3 G2((unsigned)rows);
-            if (dtype == WALSH_BF16) launch(mhc_apply_tok_kernel<uint16_t>, G2, B, 0, s, aa);
-            else launch(mhc_apply_tok_kernel<float>, G2, B, 0, s, aa);
-        } else {
-            const dim3 G2((unsigned)ceil_div(rows, 4));
-            if (dtype == WALSH_BF16) launch(mhc_apply_kernel<uint16_t>, G2, B, 0, s, aa);
-            else launch(mhc_apply_kernel<float>, G2, B, 0, s, aa);
+        wide_apply_launch(xc, ldx, rows, r0, n, C, splits, (const float *)workspace, coef, bias, rms_eps, n_iter,
+                          sk_eps, h_pre, h_post, h_res, layer_in, ld_in, norm_w, norm_eps, dtype, s);
+        const int rc = check_hip(hipGetLastError(), fn);
+        if (rc) return rc;
+    }
+    return WALSH_OK;
+}
+
+WALSH_EXPORT int walsh_mhc_post_pre_wide_fwd(const void *xo, int64_t ld_xo, const void *out, int64_t ld_out,
+                                             const float *hr_prev, const float *hp_prev, void *x_new, int64_t ld_new,
+                                             int64_t M, int64_t n, int64_t C, const void *phi_frag32,
+                                             const float *coef, const float *bias, float rms_eps, int64_t n_iter,
+                                             float sk_eps, float *h_pre, float *h_post, float *h_res, void *layer_in,
+                                             int64_t ld_in, const float *norm_w, float norm_eps, void *workspace,
+                                             int64_t workspace_bytes, int dtype, void *stream) {
+    const char *fn = "walsh_mhc_post_pre_wide_fwd";
+    if (!xo || !out || !hr_prev || !hp_prev || !x_new || !phi_frag32 || !coef || !bias || !h_pre || !h_post ||
+        !h_res || !layer_in)
+        return set_error(WALSH_EINVAL, "%s: null pointer", fn);
+    if (M < 0 || n < 1 || C < 32 || ld_xo < n * C || ld_new < n * C || ld_out < C || ld_in < C || n_iter < 0)
+        return set_error(WALSH_EINVAL, "%s: bad shape M=%lld n=%lld C=%lld", fn, (long long)M, (long long)n,
+                         (long long)C);
+    if (dtype != WALSH_BF16 || n > kMaxStreams || C % 32 || C > 4096 || ld_xo % 8 || ld_new % 8 || ld_out % 8 ||
+        ld_in % 4)
+        return set_error(WALSH_ENOTSUP, "%s: needs bf16, n <= %d, C a multiple of 32 up to 4096, row strides "
+                         "multiples of 8", fn, kMaxStreams);
+    if ((uintptr_t)xo % 16 || (uintptr_t)out % 16 || (uintptr_t)x_new % 16 || (uintptr_t)layer_in % 16 ||
+        (uintptr_t)phi_frag32 % 16 || (norm_w && (uintptr_t)norm_w % 16))
+        return set_error(WALSH_ENOTSUP, "%s: pointers must be 16-byte aligned", fn);
+    if (M == 0) return WALSH_OK;
+    const int64_t K = n * C;
+    const int splits = mhc_wide_splits(M, K);
+    // the per-token launches hold one split per lane
+    if (splits > 64) return set_error(WALSH_ENOTSUP, "%s: %d K splits (at most 64)", fn, splits);
+    const int64_t need = (int64_t)splits * M * kProjOut * 4;
+    if (!workspace || workspace_bytes < need)
+        return set_error(WALSH_EINVAL, "%s: workspace of %lld bytes needed", fn, (long long)need);
+    int64_t ld = ld_xo > ld_new ? ld_xo : ld_new;
+    if (ld_in > ld) ld = ld_in;
+    int64_t rows_max = (int64_t)kMaxBufferBytes / (ld * 2) / 16 * 16;
+    if (rows_max < 16) return set_error(WALSH_ENOTSUP, "%s: row stride too large", fn);
+    rows_max = balanced_rows(M, rows_max, 16);
+    hipStream_t s = (hipStream_t)stream;
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        const int64_t rows = (M - r0) < rows_max ? (M - r0) : rows_max;
+        PostProjArgs pa;
+        pa.xo = (const uint16_t *)xo + r0 * ld_xo;
+        pa.ld_xo = ld_xo;
+        pa.out = (const uint16_t *)out + r0 * ld_out;
+        pa.ld_out = ld_out;
+        pa.hr_prev = hr_prev + r0 * n * n;
+        pa.hp_prev = hp_prev + r0 * n;
+        pa.x_new = (uint16_t *)x_new + r0 * ld_new;
+        pa.ld_new = ld_new;
+        pa.M = (int)rows;
+        pa.n = (int)n;
+        pa.C = (int)C;
+        pa.splits = splits;
+        pa.cper = (int)(ceil_div(ceil_div(C, splits), 32) * 32);
+        pa.phi32 = (const uint16_t *)phi_frag32;
+        pa.part = (float *)workspace;
+        const int64_t items = ceil_div(rows, 16) * splits;
+        const dim3 G((unsigned)ceil_div(items, 4)), B(256);
+        switch (n) {
+        case 1: launch(mhc_post_proj_kernel<1>, G, B, 0, s, pa); break;
+        case 2: launch(mhc_post_proj_kernel<2>, G, B, 0, s, pa); break;
+        case 3: launch(mhc_post_proj_kernel<3>, G, B, 0, s, pa); break;
+        default: launch(mhc_post_proj_kernel<4>, G, B, 0, s, pa); break;
         }
+        wide_apply_launch(pa.x_new, ld_new, rows, r0, n, C, splits, (const float *)workspace, coef, bias, rms_eps,
+                          n_iter, sk_eps, h_pre, h_post, h_res, layer_in, ld_in, norm_w, norm_eps, dtype, s);
         const int rc = check_hip(hipGetLastError(), fn);
         if (rc) return rc;
     }

@@ -96,6 +96,8 @@ SIGNATURES = {
     "walsh_mhc_pre_wide_workspace": (_I64, [_I64, _I64, _I64]),
     "walsh_mhc_pre_wide_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _I64, _F, _P, _P, _P, _P, _I64, _P, _F,
                                     _P, _I64, _I, _P]),
+    "walsh_mhc_post_pre_wide_fwd": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _F,
+                                         _I64, _F, _P, _P, _P, _P, _I64, _P, _F, _P, _I64, _I, _P]),
     "walsh_moe_route_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64,
                                  _P, _I64, _I, _I, _P]),
     "walsh_moe_router_wide_workspace_bytes": (_I64, [_I64, _I64, _I64]),

@@ -1153,6 +1153,60 @@ def mhc_pre_wide(x: torch.Tensor, phi_frag32: torch.Tensor, coef: torch.Tensor, 
     return layer_in, h_pre, h_post, h_res
 
 
+def mhc_post_pre_wide_supported(n: int, C: int, dtype: torch.dtype) -> bool:
+    """Whether walsh_mhc_post_pre_wide_fwd handles this shape (bf16, C a
+    multiple of 32 up to 4096)."""
+    return dtype == torch.bfloat16 and n <= 4 and C % 32 == 0 and C <= 4096
+
+
+def mhc_post_pre_wide(x_old: torch.Tensor, out: torch.Tensor, h_res_prev: torch.Tensor, h_post_prev: torch.Tensor,
+                      phi_frag32: torch.Tensor, coef: torch.Tensor, bias_cat: torch.Tensor, rms_eps: float,
+                      norm_w: torch.Tensor = None, norm_eps: float = 1e-6, n_iter: int = 20, sk_eps: float = 1e-8):
+    """mhc_post of the previous stream fused with mhc_pre_wide of the next
+    (mhc.py:366-381 then :283-364): the projection launch forms x_new while
+    it loads x_old and out, stores it and feeds it to the matrix cores; the
+    per-token launch reads x_new.  Returns (x_new, layer_in, h_pre, h_post,
+    h_res); x_new is bitwise mhc_post's result."""
+    _hip.require_device(x_old, "stream input")
+    n, C = x_old.shape[-2], x_old.shape[-1]
+    lead = x_old.shape[:-2]
+    xo = x_old if x_old.is_contiguous() else x_old.contiguous()
+    M = xo.numel() // (n * C)
+    dev = x_old.device
+    o = out.to(x_old.dtype)
+    o = o if o.is_contiguous() else o.contiguous()
+    assert o.numel() == M * C, "layer output shape"
+    hr = h_res_prev.detach().float().contiguous()
+    hp = h_post_prev.detach().float().contiguous()
+    x_new = torch.empty_like(xo)
+    layer_in = torch.empty(lead + (C,), device=dev, dtype=x_old.dtype)
+    h_pre = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_post = torch.empty(lead + (n,), device=dev, dtype=torch.float32)
+    h_res = torch.empty(lead + (n, n), device=dev, dtype=torch.float32)
+    if M == 0:
+        return x_new, layer_in, h_pre, h_post, h_res
+    assert phi_frag32.dtype == x_old.dtype and phi_frag32.numel() == 32 * n * C, "phi_frag32 layout"
+    nw = None
+    if norm_w is not None:
+        nw = norm_w.detach().float().contiguous()
+        assert nw.numel() == C
+    wsb = _hip.lib().walsh_mhc_pre_wide_workspace(M, n, C)
+    ws = torch.empty(max(wsb, 4), device=dev, dtype=torch.uint8)
+    esz = x_old.element_size()
+    # algorithmic bytes: x_old and out read once, x_new written once, the
+    # layer input and the mappings written once, phi once (the per-token
+    # launch's read of x_new is measured traffic, not algorithmic)
+    nbytes = M * (2 * n * C + 2 * C) * esz + M * (3 * n + 2 * n * n) * 4 + 32 * n * C * esz
+    flops = M * (2 * n * C * 32 + 2 * n * C + 2 * n * C + n * C * (2 * n + 2))
+    _hip.call("walsh_mhc_post_pre_wide_fwd", xo.data_ptr(), n * C, o.data_ptr(), C, hr.data_ptr(), hp.data_ptr(),
+              x_new.data_ptr(), n * C, M, n, C, phi_frag32.data_ptr(), coef.data_ptr(), bias_cat.data_ptr(),
+              float(rms_eps), int(n_iter), float(sk_eps), h_pre.data_ptr(), h_post.data_ptr(), h_res.data_ptr(),
+              layer_in.data_ptr(), C, _hip.ptr(nw), float(norm_eps), ws.data_ptr(), ws.numel(),
+              _hip.dtype_code(x_old.dtype), _hip.stream(dev), kernel="mhc_post_proj+apply<bf16>", nbytes=nbytes,
+              flops=flops)
+    return x_new, layer_in, h_pre, h_post, h_res
+
+
 def mhc_post(x: torch.Tensor, out: torch.Tensor, h_res: torch.Tensor, h_post: torch.Tensor) -> torch.Tensor:
     """x_new = H_res @ x + H_post^T (x) out (mhc.py:366-381); x [..., n, C], out [..., C]."""
     _hip.require_device(x, "stream input")

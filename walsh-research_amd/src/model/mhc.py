@@ -175,8 +175,9 @@ class ResidualStreamMapping(nn.Module):
 class PendingUpdate:
     """A stream update x_new = H_res @ x + H_post^T (x) out (mhc.py:366-381)
     that has not been applied yet.  The next stream's mapping kernel forms it
-    while loading its tile (walsh_mhc_post_pre_norm_fwd), which saves one
-    pass over the streams; ``materialize`` applies it on its own."""
+    while loading its tile (walsh_mhc_post_pre_norm_fwd; for rows too long for
+    an LDS tile, its projection launch, walsh_mhc_post_pre_wide_fwd), which
+    saves one pass over the streams; ``materialize`` applies it on its own."""
     __slots__ = ('x', 'out', 'h_res', 'h_post')
 
     def __init__(self, x, out, h_res, h_post):
@@ -282,14 +283,21 @@ class mHCResidualStream(nn.Module):
         """The pending update of the previous stream fused with this stream's
         mappings, or None when the fused kernel does not take the shape."""
         n, C = self.n_streams, self.n_embd
-        if p.x.dtype != dt or n > _MAX_STREAMS or not kernels.mhc_post_pre_supported(n, C, dt):
+        if p.x.dtype != dt or n > _MAX_STREAMS:
             return None
-        _, coef, bias, frag = self.fused_params(dt, p.x.device)
-        if frag is None:
-            return None
-        return kernels.mhc_post_pre_norm(p.x, p.out, p.h_res, p.h_post, frag, coef, bias, _rms_eps(dt),
-                                         norm_w=None if norm is None else norm.weight,
-                                         norm_eps=1e-6 if norm is None else norm.eps)
+        nw = None if norm is None else norm.weight
+        neps = 1e-6 if norm is None else norm.eps
+        if kernels.mhc_post_pre_supported(n, C, dt):
+            _, coef, bias, frag = self.fused_params(dt, p.x.device)
+            if frag is not None:
+                return kernels.mhc_post_pre_norm(p.x, p.out, p.h_res, p.h_post, frag, coef, bias, _rms_eps(dt),
+                                                 norm_w=nw, norm_eps=neps)
+        elif kernels.mhc_pre_wide_supported(n, C) and kernels.mhc_post_pre_wide_supported(n, C, dt):
+            _, coef, bias, frag = self.fused_params(dt, p.x.device)
+            if frag is not None:
+                return kernels.mhc_post_pre_wide(p.x, p.out, p.h_res, p.h_post, frag, coef, bias, _rms_eps(dt),
+                                                 norm_w=nw, norm_eps=neps)
+        return None
 
     def forward_normed(self, x, norm, layer_fn, defer: bool = False):
         """forward(x, lambda v: layer_fn(norm(v))) with the RMSNorm ``norm``
