@@ -236,8 +236,15 @@ def main():
     roofline = None
     kernels = None
     if not args.no_roofline:
+        # per-kernel durations from an instrumented eager pass of up to 8
+        # forwards, queued behind a GPU spin so that the launches run back
+        # to back as in the graph (the host issues a forward's ~200 launches
+        # and their timing events more slowly than the GPU runs them, several
+        # times more slowly under a kernel tracer)
+        n_roof = min(args.steps, 8)
+        _queue_ahead(torch, n_roof, us_per_step=25000.0)
         with _hip.LaunchTimer() as lt:
-            for _ in range(args.steps):
+            for _ in range(n_roof):
                 step()
         kernels = lt.summary()
         # the HBM roofline is quoted for the dominant HBM-bound kernel: the
@@ -255,23 +262,23 @@ def main():
         by_time = max(kernels, key=lambda k: kernels[k]["ms"])
         roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                         frac=round(achieved / HBM_PEAK_GBS, 4), traffic=measured_traffic(dom), kernel=dom,
-                        avg_launch_us=round(avg_ms * 1000, 2), launches_per_step=d["launches"] // args.steps,
+                        avg_launch_us=round(avg_ms * 1000, 2), launches_per_step=d["launches"] // n_roof,
                         algorithmic_bytes_per_launch=int(bytes_per_launch),
                         selection="largest time per step among the HBM-bound hot-path kernels",
                         excluded_kernels={k: dict(reason="bound by its exponentials and VALU work, not memory",
-                                                  ms_per_step=round(kernels[k]["ms"] / args.steps, 3))
+                                                  ms_per_step=round(kernels[k]["ms"] / n_roof, 3))
                                           for k in excluded},
                         dominant_by_time=dict(kernel=by_time,
-                                              ms_per_step=round(kernels[by_time]["ms"] / args.steps, 3)))
+                                              ms_per_step=round(kernels[by_time]["ms"] / n_roof, 3)))
         # the whole forward: every hot-path kernel's algorithmic bytes per
         # step over the measured time per step (torch's embedding, stream
         # projection / merge and LM head are not counted)
-        fwd_bytes = sum(v["bytes"] for v in kernels.values()) / args.steps
+        fwd_bytes = sum(v["bytes"] for v in kernels.values()) / n_roof
         whole = fwd_bytes / (ms * 1e-3) / 1e9
         roofline["whole_forward"] = dict(algorithmic_bytes_per_step=int(fwd_bytes), achieved=round(whole, 1),
                                          frac=round(whole / HBM_PEAK_GBS, 4),
                                          kernel_ms_per_step=round(sum(v["ms"] for v in kernels.values())
-                                                                  / args.steps, 3))
+                                                                  / n_roof, 3))
 
     cpu = None if args.no_cpu else cpu_baseline(torch, model, cfg, args.seq, args.cpu_seconds)
 
@@ -297,10 +304,10 @@ def main():
         "sustained": sustained,
     }
     if kernels is not None:
-        line["kernels"] = {k: dict(launches_per_step=v["launches"] // args.steps,
+        line["kernels"] = {k: dict(launches_per_step=v["launches"] // n_roof,
                                    us_per_launch=round(v["ms"] * 1000 / v["launches"], 2),
                                    gbs=round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1),
-                                   ms_per_step=round(v["ms"] / args.steps, 3)) for k, v in kernels.items()}
+                                   ms_per_step=round(v["ms"] / n_roof, 3)) for k, v in kernels.items()}
     print(json.dumps(line), flush=True)
 
 
@@ -327,7 +334,7 @@ def _queue_ahead(torch, steps, us_per_step=200.0):
     host to queue ``steps`` steps behind it, so timed launches run back to
     back instead of each starting on an idle, down-clocked GPU."""
     torch.cuda.synchronize()
-    torch.cuda._sleep(int(min(steps * us_per_step, 50000.0) * 2500))
+    torch.cuda._sleep(int(min(steps * us_per_step, 250000.0) * 2500))
 
 
 def _time_graph_of_steps(torch, step, steps, n):
