@@ -445,10 +445,12 @@ def test_head_mixer_wide_bf16(K, B, T, D):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("in_o,out_o,T", [(16, 16, 1024), (16, 16, 37), (64, 64, 20)])
+@pytest.mark.parametrize("in_o,out_o,T", [(16, 16, 1024), (16, 16, 37), (64, 64, 20), (128, 128, 1100),
+                                           (100, 128, 700)])
 def test_hadamard_linear_multi_equals_single_launches(K, dtype, in_o, out_o, T):
     """walsh_hadamard_linear_multi_fwd (q, k with RoPE, v in one launch) is
-    bitwise the three single-layer calls."""
+    bitwise the three single-layer calls, also for the bf16 n_embd-4096
+    shapes above 256 rows (one wide launch per layer)."""
     torch.manual_seed(in_o + T)
     B, D = 2, 16
     x = torch.randn(B, T, 32 * in_o, device="cuda").to(dtype)
