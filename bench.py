@@ -97,7 +97,9 @@ def measured_traffic(kernel: str, workload: str = "mhcwalsh"):
 
 def calibrate_copy(torch):
     """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE readings
-    give the scale factor from counter units to bytes."""
+    give the scale factor from counter units to bytes.  Also times torch's
+    copy of 1 GiB each way (read + write), the practical HBM rate of a
+    kernel that reads and writes each byte once."""
     n = 256 << 20
     src = torch.ones(n // 4, device="cuda")
     dst = torch.empty_like(src)
@@ -107,6 +109,21 @@ def calibrate_copy(torch):
     torch.cuda.synchronize()
     print(json.dumps({"calibration": "device copy", "bytes_read_per_launch": n, "bytes_written_per_launch": n,
                       "launches": 5}), flush=True)
+    big = 1 << 30
+    a = torch.ones(big // 4, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 100.0
+    print(json.dumps({"copy": "torch copy_ of 1 GiB (read + write)", "us_per_copy": round(us, 1),
+                      "read_plus_write_gbs": round(2 * big / (us * 1e-6) / 1e9, 1),
+                      "frac_of_8tbs": round(2 * big / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
 
 
 def build_model(torch, batch, seq):
