@@ -508,10 +508,12 @@ def bench_router(torch, args):
         cpu = dict(value=round(reps * 1024 / el, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
                    host=host,
                    sample=f"{reps} x 1024 tokens through oracle/moe.py's router (numpy), {el:.1f} s")
-    return _line("tokens/sec through the MoE router at 1 GPU; % of MFMA roofline", B * T / dt, "tokens/s",
+    line = _line("tokens/sec through the MoE router at 1 GPU; % of MFMA roofline", B * T / dt, "tokens/s",
                  args.steps, args.warmup, dt * 1e3, "bf16", "synthetic: x N(0,1), router weights N(0,0.01)",
                  {"workload": "HadamardRouter n_embd 4096, hidden 1024, 128 experts, k 6", "global_batch": B,
                   "seq_len": T, "parallelism": "single GPU"}, roof, cpu)
+    line["library_gemm_reference"] = _library_gemm(torch, x, 1024)
+    return line
 
 
 def bench_octonion(torch, args):
@@ -561,11 +563,33 @@ def bench_octonion(torch, args):
                    host=host,
                    sample=f"{reps} x one layer on 2048 tokens (oracle/octonion.py, 64 block matmuls as the reference "
                           f"CPU path), {el:.1f} s; tokens/s of the 8-layer stack = layer rate / 8")
-    return _line("tokens/sec through the octonion ternary linear stack at 1 GPU; % of MFMA roofline",
+    line = _line("tokens/sec through the octonion ternary linear stack at 1 GPU; % of MFMA roofline",
                  32 * 2048 / dt, "tokens/s", args.steps, args.warmup, dt * 1e3, "bf16",
                  "synthetic: x N(0,1), weights N(0,0.02) latents",
                  {"workload": "8 x OctonionFusedLinear(1024, 1024)", "global_batch": 32, "seq_len": 2048,
                   "parallelism": "single GPU"}, roof, cpu)
+    line["library_gemm_reference"] = _library_gemm(torch, x, 1024)
+    return line
+
+
+def _library_gemm(torch, x, n):
+    """The GEMM x [M, K] @ W^T [K, n] as a plain library call (torch.matmul:
+    hipBLASLt) on an independent bf16 matrix, for scale: what the platform's
+    tuned GEMM reaches at the shape a hand-written kernel runs."""
+    M, K = x.shape
+    wt = torch.randn(n, K, device=x.device).bfloat16()
+    for _ in range(3):
+        x @ wt.t()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(20):
+        x @ wt.t()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / 20
+    return dict(what=f"torch.matmul (hipBLASLt), bf16, M {M} x N {n} x K {K}", us_per_call=round(us, 2),
+                tflops=round(2.0 * M * n * K / (us * 1e-6) / 1e12, 1))
 
 
 def bench_hadamard(torch, args):
