@@ -525,7 +525,20 @@ __device__ __forceinline__ void rank_token(int tok, const float (&lg)[2], const 
         if (o.probs) o.probs[pe] = p[h];
         if (o.mask) o.mask[pe] = sel[h] ? 1.f : 0.f;
         if (o.wdense) o.wdense[pe] = sel[h] ? __fdiv_rn(p[h], den) : 0.f;
-        if (o.y && !sel[h]) zero_block(o.y, o.y_bf16, tok * o.ldy + 32 * e[h]);
+    }
+    if (o.y) {
+        // the unselected experts' output blocks of the row, zeroed with the
+        // lanes on consecutive 16-byte chunks (1 KB per store instruction,
+        // whole cache lines; one lane per expert block wrote 16 bytes of 64
+        // different lines per instruction, at a fraction of the HBM rate)
+        const uint64_t s0 = __ballot(sel[0]), s1 = __ballot(sel[1]);
+        const int cpb = o.y_bf16 ? 4 : 8;  // 16-byte chunks per 32-value block
+        uint4 *row = (uint4 *)((char *)o.y + (int64_t)tok * o.ldy * (o.y_bf16 ? 2 : 4));
+        for (int c = lane; c < E * cpb; c += 64) {
+            const int ex = c / cpb;
+            const bool chosen = ex < 64 ? (s0 >> ex) & 1u : (s1 >> (ex - 64)) & 1u;
+            if (!chosen) row[c] = uint4{0, 0, 0, 0};
+        }
     }
 }
 
