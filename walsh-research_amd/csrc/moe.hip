@@ -1032,10 +1032,24 @@ __global__ __launch_bounds__(kFfnThreads, 1) void moe_ffn_kernel(FfnArgs a) {
             const int e = wave + kFfnWaves * x2;
             const uint32_t tsel = sel_s[lane];
             const bool mine = (tsel >> e) & 1u;
-            // zero blocks of the tile's tokens that did not choose e (their
-            // stores overlap this wave's expert arithmetic)
-            if (!mine && base + lane < M) zero_block(a.y, ybf, (int64_t)(base + lane) * a.ldy + 32 * e);
             const uint64_t bal = __ballot(mine);
+            // zero the blocks of the tile's tokens that did not choose e (their
+            // stores overlap this wave's expert arithmetic): 8 (fp32) or 4
+            // (bf16) lanes per token block, so each store instruction writes
+            // whole blocks (128 / 64 contiguous bytes) of 8 or 16 tokens
+            {
+                const int per = ybf ? 4 : 8, rows = 64 / per;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if (ybf && i >= 4) break;
+                    const int tl = rows * i + lane / per, tok = base + tl;
+                    if (tok < M && !((bal >> tl) & 1ull)) {
+                        const int64_t at = (int64_t)tok * a.ldy + 32 * e;
+                        uint4 *d = ybf ? (uint4 *)((uint16_t *)a.y + at) : (uint4 *)((float *)a.y + at);
+                        d[lane % per] = uint4{0, 0, 0, 0};
+                    }
+                }
+            }
             const int n = __popcll(bal);
             if (mine) {
                 const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
