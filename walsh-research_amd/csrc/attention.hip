@@ -461,6 +461,163 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PfArgs a) {
     if (qi < a.T) attn_store<D>(st, a.o + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st, kq);
 }
 
+// head_dim 128: 128 queries per workgroup (8 waves of 16), 64-key chunks of
+// K (row-major) and V (transposed) double-buffered in LDS, the next chunk's
+// global loads in flight while the current one is used; one barrier per
+// chunk.  Products on 16x16x32 bf16 MFMA: S^T = K Q^T takes 4 per 16-key
+// block (a lane's A operand is 8 dims of one key, read from a K row, its B
+// operand 8 dims of its query, held in registers); O^T = V^T P^T takes one
+// per 16 dims and 32 keys, with the 32 keys of a product in the order the
+// score accumulators hold them (slots 0-3: keys 4kq..4kq+3 of the first
+// 16-key block, slots 4-7: of the second), so the probabilities are the B
+// operand as computed and the V^T operand is read in the same order (two
+// 8-byte reads from a V^T row).  The row sums of P ride along as a product
+// with a ones matrix.  Softmax, masking and roundings as prefill_attn_kernel.
+constexpr int kFaQ = 128, kFaKC = 64, kFaKS = 128 + 8, kFaVS = kFaKC + 8;
+constexpr int kFaBuf = (kFaKC * kFaKS + 128 * kFaVS) * 2;     // one K + V^T chunk: 35,840 bytes
+
+__device__ __forceinline__ f32x4 fa_mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+}
+
+// One 64-key step for a wave's 16 queries (keys k0 .. k0 + 63 at LDS rows
+// 0..63 of the chunk).  FULL: every key at or before the wave's first query.
+template <bool FULL>
+__device__ __forceinline__ void fa_step(AttnState &st, const u32x4 (&qf)[4], const uint16_t *kl, const uint16_t *vt,
+                                        int k0, int qw, int qi, int n, int kq, float sl2) {
+    f32x4 s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int kb = k0 + 16 * j;
+        if (!FULL && kb > qw + 15) {           // wave-uniform
+            s[j] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            continue;
+        }
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+        const uint16_t *kr = kl + (16 * j + n) * kFaKS + 8 * kq;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) t = fa_mma(*(const u32x4 *)(kr + 32 * c), qf[c], t);
+        // t[i]: S[query qi][key kb + 4kq + i], unscaled
+        if (!FULL && kb + 15 > qw) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (kb + 4 * kq + i > qi) t[i] = -INFINITY;
+        }
+        s[j] = t;
+    }
+    const float pinf = opaque_inf();
+    float mx = fmaxf(fmaxf(st.m_run, s[0].x), s[0].y);
+    mx = fmaxf(fmaxf(mx, s[0].z), s[0].w);
+#pragma unroll
+    for (int j = 1; j < 4; ++j) {
+        mx = fmaxf(fmaxf(mx, s[j].x), s[j].y);
+        mx = fmaxf(fmaxf(mx, s[j].z), s[j].w);
+    }
+    const float m_new = max_over_rows(mx, pinf);
+    const float alpha = __builtin_amdgcn_exp2f((st.m_run - m_new) * sl2);
+    st.m_run = m_new;
+    const float moff = -m_new * sl2;
+    u32x2 pf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(fmaf(s[j][i], sl2, moff));
+        pf[j] = u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+    }
+    st.lacc *= alpha;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) st.acc[c] *= alpha;
+    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};   // eight bf16 1.0
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (!FULL && k0 + 32 * h > qw + 15) continue;   // both 16-key blocks past the wave's queries
+        const u32x4 pb = {pf[2 * h].x, pf[2 * h].y, pf[2 * h + 1].x, pf[2 * h + 1].y};
+        st.lacc = fa_mma(ones, pb, st.lacc);
+        const uint16_t *vr = vt + n * kFaVS + 32 * h + 4 * kq;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const u32x2 lo = *(const u32x2 *)(vr + 16 * c * kFaVS), hi = *(const u32x2 *)(vr + 16 * c * kFaVS + 16);
+            st.acc[c] = fa_mma(u32x4{lo.x, lo.y, hi.x, hi.y}, pb, st.acc[c]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(512, 2) void prefill_fa128_kernel(PfArgs a) {
+    extern __shared__ __align__(16) unsigned char fa_smem[];
+    const int qt = a.nqt - 1 - (int)blockIdx.x;      // longest query tiles first
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, kq = lane >> 4;
+    const int qw = qt * kFaQ + wave * 16;            // this wave's first query
+    const int qi = qw + n;                           // this lane's query
+    const int qc = qi < a.T ? qi : a.T - 1;
+    const int kend = min((qt + 1) * kFaQ, ((a.T + kFaKC - 1) / kFaKC) * kFaKC);  // keys the workgroup can need
+    u32x4 qf[4];
+    {
+        const uint16_t *qp = a.q + b * a.q_sb + h * a.q_sh + (int64_t)qc * a.q_st;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qf[c] = *(const u32x4 *)(qp + 32 * c + 8 * kq);
+    }
+    AttnState st;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) st.acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.lacc = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m_run = -INFINITY;
+    const uint16_t *kbase = a.k + b * a.kv_sb + h * a.kv_sh;
+    const uint16_t *vbase = a.v + b * a.kv_sb + h * a.kv_sh;
+    // staging: thread tid takes K pieces (key tid / 16 + 32 i, dims 8 (tid % 16)
+    // ..), i = 0, 1, and the V pieces of keys 2 (tid % 32) and 2 (tid % 32) + 1,
+    // dims 8 (tid / 32) .., which it writes to V^T as 32-bit pairs of keys (a
+    // wave's 64 lanes then cover 64 distinct banks); keys past T load row
+    // T - 1 (finite values the causal mask zeroes)
+    u32x4 kst[2], vst[2];
+    auto gload = [&](int ch) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            int kk = ch * kFaKC + tid / 16 + 32 * i;
+            kk = kk < a.T ? kk : a.T - 1;
+            kst[i] = *(const u32x4 *)(kbase + (int64_t)kk * a.kv_st + 8 * (tid % 16));
+            int kv = ch * kFaKC + 2 * (tid % 32) + i;
+            kv = kv < a.T ? kv : a.T - 1;
+            vst[i] = *(const u32x4 *)(vbase + (int64_t)kv * a.kv_st + 8 * (tid / 32));
+        }
+    };
+    auto lstore = [&](int buf) {
+        uint16_t *kl = (uint16_t *)(fa_smem + buf * kFaBuf);
+        uint16_t *vt = kl + kFaKC * kFaKS;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) *(u32x4 *)(kl + (tid / 16 + 32 * i) * kFaKS + 8 * (tid % 16)) = kst[i];
+        const int key = 2 * (tid % 32), d0 = 8 * (tid / 32);
+        const uint32_t wa[4] = {vst[0].x, vst[0].y, vst[0].z, vst[0].w};
+        const uint32_t wb[4] = {vst[1].x, vst[1].y, vst[1].z, vst[1].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // dims 2e, 2e + 1: (key, key + 1) packed low / high
+            *(uint32_t *)(vt + (d0 + 2 * e) * kFaVS + key) = __builtin_amdgcn_perm(wb[e], wa[e], 0x05040100u);
+            *(uint32_t *)(vt + (d0 + 2 * e + 1) * kFaVS + key) = __builtin_amdgcn_perm(wb[e], wa[e], 0x07060302u);
+        }
+    };
+    const int nch = kend / kFaKC;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int ch = 0; ch < nch; ++ch) {
+        if (ch + 1 < nch) gload(ch + 1);   // in flight during this chunk
+        const uint16_t *kl = (const uint16_t *)(fa_smem + (ch & 1) * kFaBuf);
+        const uint16_t *vt = kl + kFaKC * kFaKS;
+        const int k0 = ch * kFaKC;
+        if (k0 <= qw + 15) {               // wave-uniform: keys at or before some query of the wave
+            if (k0 + kFaKC - 1 <= qw) fa_step<true>(st, qf, kl, vt, k0, qw, qi, n, kq, a.sl2);
+            else fa_step<false>(st, qf, kl, vt, k0, qw, qi, n, kq, a.sl2);
+        }
+        if (ch + 1 < nch) lstore((ch + 1) & 1);   // the other buffer: read last in chunk ch - 1
+        __syncthreads();
+    }
+    if (qi < a.T) attn_store<128>(st, a.o + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st, kq);
+}
+
 // Whole-head variant, for heads whose K and V fit in LDS together (T_pad *
 // (D + 4) * 2 + D * (T_pad + 4) * 2 bytes; head_dim 16 up to about 2,200
 // positions): one workgroup of 16 waves per (sequence, head) stages K
@@ -706,6 +863,13 @@ WALSH_EXPORT int walsh_prefill_attention(const void *q, int64_t q_sb, int64_t q_
     if (D == 16 && head_lds + 256 <= device_info().max_shared_per_block) {
         launch(prefill_attn_head_kernel<16>, dim3((unsigned)H, (unsigned)B, 1u), dim3(64 * kPhWaves),
                (uint32_t)head_lds, s, a, (int)tpad);
+        return check_hip(hipGetLastError(), fn);
+    }
+    if (D == 128 && (size_t)(2 * kFaBuf) <= (size_t)device_info().max_shared_per_block) {
+        PfArgs a2 = a;
+        a2.nqt = (int)ceil_div(T, kFaQ);
+        launch(prefill_fa128_kernel, dim3((unsigned)a2.nqt, (unsigned)H, (unsigned)B), dim3(512),
+               (uint32_t)(2 * kFaBuf), s, a2);
         return check_hip(hipGetLastError(), fn);
     }
     const dim3 G((unsigned)a.nqt, (unsigned)H, (unsigned)B);
