@@ -839,9 +839,10 @@ def prefill_attention_preferred(q: torch.Tensor) -> bool:
     """Whether the model should route causal prefill attention here rather
     than to SDPA: head_dim 16, where the whole-head kernel is VALU-bound
     and measured 2.4x faster than SDPA at T = 1024 (51 vs 125 us per layer,
-    config 2).  At head_dim 128 SDPA's matrix-core kernel is faster (2.35 ms
-    against 4.6 ms per layer at config 5), so those shapes stay there."""
-    return q.shape[-1] == 16
+    config 2), and head_dim 128 (the 128-query matrix-core kernel: 1.86 ms
+    against SDPA's 2.32 ms per layer at config 5).  Head dims 32 and 64 stay
+    on SDPA."""
+    return q.shape[-1] in (16, 128)
 
 
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = None) -> torch.Tensor:
