@@ -476,6 +476,11 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PfArgs a) {
 constexpr int kFaQ = 128, kFaKC = 64, kFaKS = 128 + 8, kFaVS = kFaKC + 8;
 constexpr int kFaBuf = (kFaKC * kFaKS + 128 * kFaVS) * 2;     // one K + V^T chunk: 35,840 bytes
 
+// Column of key offset o (0..31) within its 32-key half of a V^T row: the
+// keys of product slots 8kq .. 8kq + 7 (4kq .. 4kq + 3, then 16 + 4kq ..
+// 16 + 4kq + 3) lie at 8kq .. 8kq + 7.  Keys 2m and 2m + 1 stay adjacent.
+__device__ __forceinline__ int fa_vt_pos(int o) { return 8 * ((o & 15) >> 2) + 4 * (o >> 4) + (o & 3); }
+
 __device__ __forceinline__ f32x4 fa_mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                    0, 0);
@@ -535,12 +540,11 @@ __device__ __forceinline__ void fa_step(AttnState &st, const u32x4 (&qf)[4], con
         if (!FULL && k0 + 32 * h > qw + 15) continue;   // both 16-key blocks past the wave's queries
         const u32x4 pb = {pf[2 * h].x, pf[2 * h].y, pf[2 * h + 1].x, pf[2 * h + 1].y};
         st.lacc = fa_mma(ones, pb, st.lacc);
-        const uint16_t *vr = vt + n * kFaVS + 32 * h + 4 * kq;
+        // V^T rows hold each 32-key half in product order (fa_vt_pos), so a
+        // lane's 8 keys are one 16-byte read
+        const uint16_t *vr = vt + n * kFaVS + 32 * h + 8 * kq;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const u32x2 lo = *(const u32x2 *)(vr + 16 * c * kFaVS), hi = *(const u32x2 *)(vr + 16 * c * kFaVS + 16);
-            st.acc[c] = fa_mma(u32x4{lo.x, lo.y, hi.x, hi.y}, pb, st.acc[c]);
-        }
+        for (int c = 0; c < 8; ++c) st.acc[c] = fa_mma(*(const u32x4 *)(vr + 16 * c * kFaVS), pb, st.acc[c]);
     }
 }
 
@@ -590,13 +594,14 @@ __global__ __launch_bounds__(512, 2) void prefill_fa128_kernel(PfArgs a) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) *(u32x4 *)(kl + (tid / 16 + 32 * i) * kFaKS + 8 * (tid % 16)) = kst[i];
         const int key = 2 * (tid % 32), d0 = 8 * (tid / 32);
+        const int col = (key & 32) + fa_vt_pos(key & 31);
         const uint32_t wa[4] = {vst[0].x, vst[0].y, vst[0].z, vst[0].w};
         const uint32_t wb[4] = {vst[1].x, vst[1].y, vst[1].z, vst[1].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             // dims 2e, 2e + 1: (key, key + 1) packed low / high
-            *(uint32_t *)(vt + (d0 + 2 * e) * kFaVS + key) = __builtin_amdgcn_perm(wb[e], wa[e], 0x05040100u);
-            *(uint32_t *)(vt + (d0 + 2 * e + 1) * kFaVS + key) = __builtin_amdgcn_perm(wb[e], wa[e], 0x07060302u);
+            *(uint32_t *)(vt + (d0 + 2 * e) * kFaVS + col) = __builtin_amdgcn_perm(wb[e], wa[e], 0x05040100u);
+            *(uint32_t *)(vt + (d0 + 2 * e + 1) * kFaVS + col) = __builtin_amdgcn_perm(wb[e], wa[e], 0x07060302u);
         }
     };
     const int nch = kend / kFaKC;
