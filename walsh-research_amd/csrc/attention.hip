@@ -462,19 +462,25 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PfArgs a) {
 }
 
 // head_dim 128: 128 queries per workgroup (8 waves of 16), 64-key chunks of
-// K (row-major) and V (transposed) double-buffered in LDS, the next chunk's
-// global loads in flight while the current one is used; one barrier per
-// chunk.  Products on 16x16x32 bf16 MFMA: S^T = K Q^T takes 4 per 16-key
+// K (row-major, three buffers, loaded straight into LDS two chunks ahead) and
+// V (transposed through registers into two buffers, one chunk ahead) in LDS;
+// one barrier per chunk.  Products on 16x16x32 bf16 MFMA: S^T = K Q^T takes 4 per 16-key
 // block (a lane's A operand is 8 dims of one key, read from a K row, its B
 // operand 8 dims of its query, held in registers); O^T = V^T P^T takes one
 // per 16 dims and 32 keys, with the 32 keys of a product in the order the
 // score accumulators hold them (slots 0-3: keys 4kq..4kq+3 of the first
 // 16-key block, slots 4-7: of the second), so the probabilities are the B
-// operand as computed and the V^T operand is read in the same order (two
-// 8-byte reads from a V^T row).  The row sums of P ride along as a product
+// operand as computed and the V^T operand is read in the same order (one
+// 16-byte read from a V^T row).  The row sums of P ride along as a product
 // with a ones matrix.  Softmax, masking and roundings as prefill_attn_kernel.
-constexpr int kFaQ = 128, kFaKC = 64, kFaKS = 128 + 8, kFaVS = kFaKC + 8;
-constexpr int kFaBuf = (kFaKC * kFaKS + 128 * kFaVS) * 2;     // one K + V^T chunk: 35,840 bytes
+constexpr int kFaQ = 128, kFaKC = 64;
+// LDS: three K buffers (64 keys x 256 bytes; 16-byte chunk c of key row r at
+// position c ^ (r & 15)) and two V^T buffers (128 dims x 128 bytes; chunk u
+// of dim row d at position u ^ ((d >> 1) & 7)): 80 KB, two workgroups per CU.
+// The swizzles keep the fragment reads (16 rows of one chunk column) and the
+// V^T stores on distinct banks without padding.
+constexpr int kFaKBuf = kFaKC * 256, kFaVBuf = 128 * kFaKC * 2;
+constexpr int kFaLds = 3 * kFaKBuf + 2 * kFaVBuf;
 
 // Column of key offset o (0..31) within its 32-key half of a V^T row: the
 // keys of product slots 8kq .. 8kq + 7 (4kq .. 4kq + 3, then 16 + 4kq ..
@@ -500,9 +506,9 @@ __device__ __forceinline__ void fa_step(AttnState &st, const u32x4 (&qf)[4], con
             continue;
         }
         f32x4 t = {0.f, 0.f, 0.f, 0.f};
-        const uint16_t *kr = kl + (16 * j + n) * kFaKS + 8 * kq;
+        const unsigned char *kr = (const unsigned char *)kl + (16 * j + n) * 256;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) t = fa_mma(*(const u32x4 *)(kr + 32 * c), qf[c], t);
+        for (int c = 0; c < 4; ++c) t = fa_mma(*(const u32x4 *)(kr + (((4 * c + kq) ^ n) << 4)), qf[c], t);
         // t[i]: S[query qi][key kb + 4kq + i], unscaled
         if (!FULL && kb + 15 > qw) {
 #pragma unroll
@@ -541,15 +547,15 @@ __device__ __forceinline__ void fa_step(AttnState &st, const u32x4 (&qf)[4], con
         const u32x4 pb = {pf[2 * h].x, pf[2 * h].y, pf[2 * h + 1].x, pf[2 * h + 1].y};
         st.lacc = fa_mma(ones, pb, st.lacc);
         // V^T rows hold each 32-key half in product order (fa_vt_pos), so a
-        // lane's 8 keys are one 16-byte read
-        const uint16_t *vr = vt + n * kFaVS + 32 * h + 8 * kq;
+        // lane's 8 keys are one 16-byte read (chunk 4h + kq of dim row 16c + n)
+        const unsigned char *vr = (const unsigned char *)vt + n * 128 + (((4 * h + kq) ^ (n >> 1)) << 4);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) st.acc[c] = fa_mma(*(const u32x4 *)(vr + 16 * c * kFaVS), pb, st.acc[c]);
+        for (int c = 0; c < 8; ++c) st.acc[c] = fa_mma(*(const u32x4 *)(vr + 16 * c * 128), pb, st.acc[c]);
     }
 }
 
 __global__ __launch_bounds__(512, 2) void prefill_fa128_kernel(PfArgs a) {
-    extern __shared__ __align__(16) unsigned char fa_smem[];
+    extern __shared__ __align__(1024) unsigned char fa_smem[];
     const int qt = a.nqt - 1 - (int)blockIdx.x;      // longest query tiles first
     const int h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -571,55 +577,102 @@ __global__ __launch_bounds__(512, 2) void prefill_fa128_kernel(PfArgs a) {
     st.m_run = -INFINITY;
     const uint16_t *kbase = a.k + b * a.kv_sb + h * a.kv_sh;
     const uint16_t *vbase = a.v + b * a.kv_sb + h * a.kv_sh;
-    // staging: thread tid takes K pieces (key tid / 16 + 32 i, dims 8 (tid % 16)
-    // ..), i = 0, 1, and the V pieces of keys 2 (tid % 32) and 2 (tid % 32) + 1,
-    // dims 8 (tid / 32) .., which it writes to V^T as 32-bit pairs of keys (a
-    // wave's 64 lanes then cover 64 distinct banks); keys past T load row
-    // T - 1 (finite values the causal mask zeroes)
-    u32x4 kst[2], vst[2];
-    auto gload = [&](int ch) {
+    // K: straight to LDS (buffer loads into LDS, no registers): wave w fills
+    // key rows 8w .. 8w + 7 of a chunk, 4 rows (1 KB) per instruction, lane l
+    // landing at position l % 16 of row 8w + 4i + l / 16, which holds chunk
+    // (l % 16) ^ (row & 15).  Keys past T load row T - 1 (finite values the
+    // causal mask zeroes).
+    // byte span of one head's K (or V) rows; below 4 GiB (the host checks)
+    const uint32_t kspan = (uint32_t)(((int64_t)(a.T - 1) * a.kv_st + 128) * 2);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase, kspan);
+    auto kload = [&](int ch) {
+        // the LDS destination of a buffer-to-LDS load is wave-uniform (M0)
+        unsigned char *dst = fa_smem + (ch % 3) * kFaKBuf + __builtin_amdgcn_readfirstlane(wave) * 2048;
+        int t = tid;
+        asm volatile("" : "+v"(t));
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            int kk = ch * kFaKC + tid / 16 + 32 * i;
+            const int row = 8 * (t >> 6) + 4 * i + (t & 63) / 16;
+            int kk = ch * kFaKC + row;
             kk = kk < a.T ? kk : a.T - 1;
-            kst[i] = *(const u32x4 *)(kbase + (int64_t)kk * a.kv_st + 8 * (tid % 16));
-            int kv = ch * kFaKC + 2 * (tid % 32) + i;
-            kv = kv < a.T ? kv : a.T - 1;
-            vst[i] = *(const u32x4 *)(vbase + (int64_t)kv * a.kv_st + 8 * (tid / 32));
+            const uint32_t off = (uint32_t)kk * (uint32_t)(2 * a.kv_st) + 16 * ((t % 16) ^ (row & 15));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (__attribute__((address_space(3))) void *)(dst + i * 1024),
+                                                     16, off, 0, 0, 0);
         }
     };
-    auto lstore = [&](int buf) {
-        uint16_t *kl = (uint16_t *)(fa_smem + buf * kFaBuf);
-        uint16_t *vt = kl + kFaKC * kFaKS;
+    // V: through registers (two chunks ahead in two sets), then to V^T as
+    // 32-bit pairs of keys: thread tid takes keys 2 (tid % 32), + 1 at dims
+    // 8 (tid / 32) ..; lanes 32..63 of a wave write the row pair's other
+    // member first, so each store instruction covers both bank halves
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, kspan);
+    auto vload = [&](int ch, u32x4 (&vr)[2]) {
+        int t = tid;
+        asm volatile("" : "+v"(t));
 #pragma unroll
-        for (int i = 0; i < 2; ++i) *(u32x4 *)(kl + (tid / 16 + 32 * i) * kFaKS + 8 * (tid % 16)) = kst[i];
-        const int key = 2 * (tid % 32), d0 = 8 * (tid / 32);
-        const int col = (key & 32) + fa_vt_pos(key & 31);
-        const uint32_t wa[4] = {vst[0].x, vst[0].y, vst[0].z, vst[0].w};
-        const uint32_t wb[4] = {vst[1].x, vst[1].y, vst[1].z, vst[1].w};
+        for (int u = 0; u < 2; ++u) {
+            int kv = ch * kFaKC + 2 * (t % 32) + u;
+            kv = kv < a.T ? kv : a.T - 1;
+            vr[u] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (uint32_t)kv * (uint32_t)(2 * a.kv_st) + 16 * (t / 32),
+                                                          0, 0);
+        }
+    };
+    auto vstore = [&](int ch, const u32x4 (&vr)[2]) {
+        unsigned char *vt = fa_smem + 3 * kFaKBuf + (ch & 1) * kFaVBuf;
+        // the lane's store addresses are recomputed for every chunk (a few
+        // VALU ops) rather than held in registers across the loop
+        int t = tid;
+        asm volatile("" : "+v"(t));
+        const int key = 2 * (t % 32), d0 = 8 * (t / 32);
+        const int col = (key & 32) + fa_vt_pos(key & 31), sw = (t >> 5) & 1;
+        const uint32_t wa[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
+        const uint32_t wb[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             // dims 2e, 2e + 1: (key, key + 1) packed low / high
-            *(uint32_t *)(vt + (d0 + 2 * e) * kFaVS + col) = __builtin_amdgcn_perm(wb[e], wa[e], 0x05040100u);
-            *(uint32_t *)(vt + (d0 + 2 * e + 1) * kFaVS + col) = __builtin_amdgcn_perm(wb[e], wa[e], 0x07060302u);
+            const uint32_t p0 = __builtin_amdgcn_perm(wb[e], wa[e], 0x05040100u);
+            const uint32_t p1 = __builtin_amdgcn_perm(wb[e], wa[e], 0x07060302u);
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) {
+                const int d = d0 + 2 * e + (t2 ^ sw);
+                const int pos = (((col >> 3) ^ ((d >> 1) & 7)) << 3) + (col & 7);
+                *(uint32_t *)(vt + d * 128 + pos * 2) = (t2 ^ sw) ? p1 : p0;
+            }
         }
     };
+    // Loads are issued unconditionally (past the last chunk they fetch clamped
+    // rows into buffers no wave reads again), so every wave has the same
+    // number of loads in flight and the waits below count exactly.  The
+    // barriers are bare s_barrier: a __syncthreads would also wait for the
+    // K loads of the chunk after next.
     const int nch = kend / kFaKC;
-    gload(0);
-    lstore(0);
-    __syncthreads();
+    u32x4 va[2];
+    kload(0);
+    vload(0, va);
+    kload(1);
+    vstore(0, va);
+    asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)" ::: "memory");   // K(0) in LDS, V^T(0) stored
+    asm volatile("s_barrier" ::: "memory");
+    // chunk ch: V(ch + 1) to registers and K(ch + 2) to LDS requested, the
+    // products of ch, V^T(ch + 1) stored, K(ch + 1) waited for, one barrier
     for (int ch = 0; ch < nch; ++ch) {
-        if (ch + 1 < nch) gload(ch + 1);   // in flight during this chunk
-        const uint16_t *kl = (const uint16_t *)(fa_smem + (ch & 1) * kFaBuf);
-        const uint16_t *vt = kl + kFaKC * kFaKS;
+        vload(ch + 1, va);
+        kload(ch + 2);
+        const uint16_t *kl = (const uint16_t *)(fa_smem + (ch % 3) * kFaKBuf);
+        const uint16_t *vt = (const uint16_t *)(fa_smem + 3 * kFaKBuf + (ch & 1) * kFaVBuf);
         const int k0 = ch * kFaKC;
-        if (k0 <= qw + 15) {               // wave-uniform: keys at or before some query of the wave
-            if (k0 + kFaKC - 1 <= qw) fa_step<true>(st, qf, kl, vt, k0, qw, qi, n, kq, a.sl2);
-            else fa_step<false>(st, qf, kl, vt, k0, qw, qi, n, kq, a.sl2);
+        // lane-derived offsets are recomputed for every chunk rather than
+        // held in registers across the loop
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        if (k0 <= qw + 15) {               // keys at or before some query of the wave
+            if (k0 + kFaKC - 1 <= qw) fa_step<true>(st, qf, kl, vt, k0, qw, qi, ln & 15, ln >> 4, a.sl2);
+            else fa_step<false>(st, qf, kl, vt, k0, qw, qi, ln & 15, ln >> 4, a.sl2);
         }
-        if (ch + 1 < nch) lstore((ch + 1) & 1);   // the other buffer: read last in chunk ch - 1
-        __syncthreads();
+        vstore(ch + 1, va);                // the V^T buffer of chunk ch - 1
+        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)" ::: "memory");   // all but K(ch + 2)
+        asm volatile("s_barrier" ::: "memory");
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no load into LDS outlives the workgroup
     if (qi < a.T) attn_store<128>(st, a.o + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st, kq);
 }
 
@@ -870,11 +923,13 @@ WALSH_EXPORT int walsh_prefill_attention(const void *q, int64_t q_sb, int64_t q_
                (uint32_t)head_lds, s, a, (int)tpad);
         return check_hip(hipGetLastError(), fn);
     }
-    if (D == 128 && (size_t)(2 * kFaBuf) <= (size_t)device_info().max_shared_per_block) {
+    // prefill_fa128_kernel addresses a head's K and V rows with 32-bit byte offsets
+    const bool fa_span_ok = ((T - 1) * kv_st + 128) * 2 <= (int64_t)UINT32_MAX;
+    if (D == 128 && fa_span_ok && (size_t)kFaLds <= (size_t)device_info().max_shared_per_block) {
         PfArgs a2 = a;
         a2.nqt = (int)ceil_div(T, kFaQ);
         launch(prefill_fa128_kernel, dim3((unsigned)a2.nqt, (unsigned)H, (unsigned)B), dim3(512),
-               (uint32_t)(2 * kFaBuf), s, a2);
+               (uint32_t)kFaLds, s, a2);
         return check_hip(hipGetLastError(), fn);
     }
     const dim3 G((unsigned)a.nqt, (unsigned)H, (unsigned)B);
