@@ -1415,7 +1415,7 @@ static size_t split3_lds_bytes(int Kc32) {
 template <int GS, bool DENSE>
 __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArgsN an) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const HadArgs &a = an.p[blockIdx.y];
+    const HadArgs a = load_args(an.p[blockIdx.y]);
     uint2 *lut = (uint2 *)smem;                                           // [81 entries][16 copies]
     _Float16 *alpha_l = (_Float16 *)(smem + kW3LutBytes);                 // [32 g][128 cols]
     _Float16 *beta_l = (_Float16 *)(smem + kW3LutBytes + kW3AlphaBytes);  // [32 h][16 o] of this tile
@@ -1425,41 +1425,88 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
     const int nt = (int)blockIdx.x % a.Nt, tile = (int)blockIdx.x / a.Nt;
     const int Kc32 = (a.in_o + 31) >> 5;
 
-    // every load first, so one memory round trip covers them all: this
-    // wave's weights of groups 4w..4w+3 for every chunk, the tile's input,
-    // alpha and this output tile's beta
+    // every load first, so one memory round trip covers them all, in the
+    // order of use (vector loads complete in order): the tile's input, alpha
+    // and this output tile's beta, this wave's weights of groups 4w..4w+3
+    // for every chunk, the output waves' rotary coefficients
+    const int i0 = 16 * wave + 4 * q;
+    const bool xwave = wave < 2 * Kc32;
+    // Few valid rows in the tile (decode): a thread transforms one column
+    // pair of one valid row (unit tid: row tid / (in_o / 2), pair tid % (in_o
+    // / 2)) instead of 4 columns of each of the 16 row slots, most of them
+    // rows past M.  The stage slots of rows past M are then left unwritten:
+    // a product column is one row, and those rows are not stored.
+    const int mt = min(kTile, a.M - tile * kTile), hp = a.in_o >> 1;
+    const bool narrow = (a.in_o & 31) == 0 && mt * hp <= kWideThreads;   // workgroup-uniform
+    const int n_tok = tid / hp, n_col = 2 * (tid - n_tok * hp);
+    const bool n_ok = narrow && n_tok < mt;
+    u32x2 xraw[32];
+    uint32_t xn[32];
+    {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a, 2));
+        const uint32_t gstride = (uint32_t)(GS ? GS : a.gsx) * 2;
+        if (narrow) {
+            const uint32_t voff = n_ok ? x_row_off(a, tile * kTile + n_tok, 2) + (uint32_t)n_col * 2 : kOOB;
+#pragma unroll
+            for (int g = 0; g < 32; ++g) xn[g] = __builtin_amdgcn_raw_buffer_load_b32(xr, voff, (uint32_t)g * gstride, 0);
+        } else if (xwave) {
+            const int row = tile * kTile + t;
+            const uint32_t voff = (row < a.M && i0 < a.in_o) ? x_row_off(a, row, 2) + (uint32_t)i0 * 2 : kOOB;
+            wide3_load_x(xr, voff, gstride, xraw);
+        }
+    }
+    // (buffer loads, zero past their ranges, and no arithmetic on the loaded
+    // values until they are used: a conversion right after a load would wait
+    // for every load before it)
+    const float a32 = DENSE ? 0.03125f : 1.f;  // the dense weights' share of the transforms' 1/32
+    constexpr int kAv = 32 * kW3MaxO / kWideThreads;
+    uint32_t avr[kAv];
+    if (a.alpha) {
+        const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.alpha, (uint32_t)(32 * a.in_o * 4));
+#pragma unroll
+        for (int k = 0; k < kAv; ++k) {
+            const int e = tid + k * kWideThreads, g = e / kW3MaxO, i = e % kW3MaxO;
+            avr[k] = __builtin_amdgcn_raw_buffer_load_b32(ar, i < a.in_o ? (uint32_t)(g * a.in_o + i) * 4 : kOOB, 0, 0);
+        }
+    }
+    const int bo = kNTile * nt + (tid & 15);
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.beta, (uint32_t)((31 * a.beta_h + a.out_o) * 4));
+    const uint32_t bvr = __builtin_amdgcn_raw_buffer_load_b32(
+        br, bo < a.out_o ? (uint32_t)((tid >> 4) * a.beta_h + bo) * 4 : kOOB, 0, 0);
     uint2 wv[4];
     uint4 wd[4][4];
+    {
+        const __amdgpu_buffer_rsrc_t kr =
+            DENSE ? make_rsrc(a.kw, (uint32_t)(a.Nt * Kc32 * 32768)) : make_rsrc(a.kw3, (uint32_t)(a.Nt * Kc32 * 4096));
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        if (c < Kc32) {
-            if constexpr (DENSE) {
-                const uint4 *src = (const uint4 *)a.kw + ((int64_t)(nt * Kc32 + c) * 32 + 4 * wave) * 64 + lane;
+        for (int c = 0; c < 4; ++c) {
+            if (c < Kc32) {
+                if constexpr (DENSE) {
+                    const uint32_t off = (uint32_t)((((nt * Kc32 + c) * 32 + 4 * wave) * 64 + lane) * 16);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) wd[c][j] = src[j * 64];
-            } else {
-                wv[c] = *(const uint2 *)(a.kw3 + ((int64_t)(nt * Kc32 + c) * 64 + lane) * 64 + 8 * wave);
+                    for (int j = 0; j < 4; ++j)
+                        wd[c][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, off, j * 1024, 0));
+                } else {
+                    wv[c] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                          kr, (uint32_t)(((nt * Kc32 + c) * 64 + lane) * 64 + 8 * wave), 0, 0));
+                }
             }
         }
     }
-    const int i0 = 16 * wave + 4 * q;
-    const bool xwave = wave < 2 * Kc32;
-    u32x2 xraw[32];
-    if (xwave) {
-        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a, 2));
-        const int row = tile * kTile + t;
-        const uint32_t voff = (row < a.M && i0 < a.in_o) ? x_row_off(a, row, 2) + (uint32_t)i0 * 2 : kOOB;
-        wide3_load_x(xr, voff, (uint32_t)(GS ? GS : a.gsx) * 2, xraw);
+    // the output waves' rotary (cos, sin): wave w < 4 takes outputs
+    // 4w..4w+3 of the tile, lane = (token tt, output jj)
+    const int tt = lane >> 2, jj = lane & 3, o16 = 4 * wave + jj;
+    const int orow = tile * kTile + tt, o = kNTile * nt + o16;
+    const bool ok = orow < a.M && o < a.out_o;
+    const bool rope = a.rope != nullptr;
+    const bool cs_ok = rope && ok && wave < 4;
+    u32x2 csr = {0u, 0u};
+    if (rope) {
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.rope, (uint32_t)(a.rope_T * a.rope_D * 4));
+        const uint32_t off = cs_ok ? (uint32_t)((((orow + a.rope_row0) % a.rope_T) * (a.rope_D >> 1) + ((o % a.rope_D) >> 1)) * 8)
+                                   : kOOB;
+        csr = __builtin_amdgcn_raw_buffer_load_b64(rr, off, 0, 0);
     }
-    const float a32 = DENSE ? 0.03125f : 1.f;  // the dense weights' share of the transforms' 1/32
-    float av[32 * kW3MaxO / kWideThreads];
-#pragma unroll
-    for (int k = 0; k < 32 * kW3MaxO / kWideThreads; ++k) {
-        const int e = tid + k * kWideThreads, g = e / kW3MaxO, i = e % kW3MaxO;
-        av[k] = i < a.in_o ? (a.alpha ? a.alpha[g * a.in_o + i] : 1.f) * a32 : 0.f;
-    }
-    const int bo = kNTile * nt + (tid & 15);
-    const float bv = bo < a.out_o ? a.beta[(tid >> 4) * a.beta_h + bo] : 0.f;
 
     for (int e = tid; e < (DENSE ? 0 : kW3Entries * kW3Copies); e += kWideThreads) {
         int r = e / kW3Copies;
@@ -1472,12 +1519,35 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
         lut[e] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
     }
 #pragma unroll
-    for (int k = 0; k < 32 * kW3MaxO / kWideThreads; ++k) alpha_l[tid + k * kWideThreads] = (_Float16)av[k];
-    beta_l[tid] = (_Float16)bv;
+    for (int k = 0; k < kAv; ++k) {
+        const int i = (tid + k * kWideThreads) % kW3MaxO;
+        alpha_l[tid + k * kWideThreads] = (_Float16)(i < a.in_o ? (a.alpha ? __uint_as_float(avr[k]) : 1.f) * a32 : 0.f);
+    }
+    beta_l[tid] = (_Float16)(bo < a.out_o ? __uint_as_float(bvr) : 0.f);
     lds_barrier();  // tables ready
-    if (xwave)
+    if (narrow) {
+        // the column pair as one pass of wide3_transform_x: the same
+        // products, transform and roundings
+        if (n_ok) {
+            f32x2 v[32];
+#pragma unroll
+            for (int g = 0; g < 32; ++g) {
+                const uint32_t u = xn[g];
+                const _Float16 *ag = alpha_l + g * kW3MaxO + n_col;
+                v[g] = f32x2{__uint_as_float(u << 16) * (float)ag[0], __uint_as_float(u & 0xffff0000u) * (float)ag[1]};
+            }
+            fht32<f32x2>(v);
+            // stage position of (row n_tok, column n_col): chunk n_col / 32,
+            // lane n_tok + 16 ((n_col / 8) % 4), bf16 element n_col % 8
+            uint32_t *dst = (uint32_t *)(xs + (size_t)(n_col >> 5) * 32 * 64 + n_tok + 16 * ((n_col >> 3) & 3)) +
+                            ((n_col & 7) >> 1);
+#pragma unroll
+            for (int g = 0; g < 32; ++g) dst[g * 64 * 4] = pack_bf16x2(v[g][0], v[g][1]);
+        }
+    } else if (xwave) {
         wide3_transform_x(xraw, alpha_l + i0,
                           (uint2 *)(xs + (size_t)(i0 >> 5) * 32 * 64 + t + 16 * ((i0 >> 3) & 3)) + ((i0 >> 2) & 1));
+    }
     lds_barrier();  // stage ready
 
     f32x4 acc[4];
@@ -1512,28 +1582,21 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
     if (wave >= 4) return;
     // wave w: outputs 4w..4w+3 of the tile; lane = (token tt, output jj), so
     // one read instruction covers 64 consecutive floats
-    const int tt = lane >> 2, jj = lane & 3, o16 = 4 * wave + jj;
     const float *pp = (const float *)part + (tt + 16 * wave) * 4 + jj;
     float v[32];
 #pragma unroll
     for (int g = 0; g < 32; ++g) v[g] = pp[g * 256];
     fht32<float>(v);
-    const int row = tile * kTile + tt, o = kNTile * nt + o16;
-    const bool ok = row < a.M && o < a.out_o;
-    const bool rope = a.rope != nullptr;
-    f32x2 cs = f32x2{1.f, 0.f};
-    if (rope && ok) {
-        const int rt = (row + a.rope_row0) % a.rope_T;
-        cs = *(const f32x2 *)(a.rope + ((int64_t)rt * (a.rope_D >> 1) + ((o % a.rope_D) >> 1)) * 2);
-    }
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)a.M * a.ldy * 2));
-    const uint32_t voff = ok ? (uint32_t)((int64_t)row * a.ldy * 2) + (uint32_t)o * 2 : kOOB;
+    const uint32_t voff = ok ? (uint32_t)((int64_t)orow * a.ldy * 2) + (uint32_t)o * 2 : kOOB;
     const uint32_t hstride = (uint32_t)(GS ? GS : a.gsy) * 2;
+    const f32x2 cs = cs_ok ? f32x2{__uint_as_float(csr.x), __uint_as_float(csr.y)} : f32x2{1.f, 0.f};
 #pragma unroll
     for (int h = 0; h < 32; ++h) {
         float r = v[h] * (float)beta_l[h * kNTile + o16];
         if (rope) {
-            const float p = __shfl_xor(r, 1);  // the other element of the pair
+            // the other element of the pair (lane ^ 1, a DPP quad permutation)
+            const float p = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(r), 0xB1, 0xF, 0xF, true));
             r = (jj & 1) ? rope_odd(p, r, cs[0], cs[1]) : rope_even(r, p, cs[0], cs[1]);
         }
         __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(r), yr, voff, (uint32_t)h * hstride, 0);

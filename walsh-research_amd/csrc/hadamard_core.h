@@ -72,6 +72,21 @@ struct HadArgs {
     int nt_store;
 };
 
+// A kernel reads its arguments with scalar loads placed where each field is
+// first used, and in a latency-bound launch (decode sizes) every such load
+// that misses the caches waits a memory round trip of its own, in sequence
+// with the branches between them.  Reading every field at entry and passing
+// the values through an empty asm statement (which the compiler cannot
+// re-read from argument memory) leaves a single round trip for all of them.
+__device__ __forceinline__ HadArgs load_args(const HadArgs &src) {
+    HadArgs a = src;
+    asm volatile("" : "+s"(a.x), "+s"(a.ldx), "+s"(a.M), "+s"(a.in_o), "+s"(a.out_o), "+s"(a.Nt), "+s"(a.Kc),
+                 "+s"(a.gsx), "+s"(a.gsy), "+s"(a.kw), "+s"(a.kw3), "+s"(a.alpha), "+s"(a.beta), "+s"(a.beta_h));
+    asm volatile("" : "+s"(a.y), "+s"(a.ldy), "+s"(a.tpb), "+s"(a.bstride), "+s"(a.xspan), "+s"(a.rope),
+                 "+s"(a.rope_T), "+s"(a.rope_D), "+s"(a.rope_row0), "+s"(a.wave_tiles), "+s"(a.nt_store));
+    return a;
+}
+
 // The (cos, sin) of the lane's two output pairs o0..o0+3 (o0 % 4 == 0,
 // rope_D % 4 == 0, out_o % rope_D == 0: the same pairs in every group).
 __device__ __forceinline__ f32x4 rope_cs(const HadArgs &a, int row, int o0) {

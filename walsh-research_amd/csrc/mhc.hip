@@ -1462,11 +1462,30 @@ __global__ __launch_bounds__(256) void mhc_apply_tok_kernel(ApplyArgs a) {
     __shared__ float dyn_s[kProjOut + 7];
     __shared__ float hpre_s[4];
     __shared__ float sq_s[4];
+    __shared__ float par_s[32];  // coef[3], then bias[2n + n*n]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tok = blockIdx.x;
     const int n = a.n, C = a.C, K = n * C;
-    // the token's streams are loaded first: their round trip overlaps the
-    // split sums and the constraints
+    // loads in the order they are needed (vector loads complete in order):
+    // the split partials (buffer loads, zero past the splits; splits <= 64,
+    // K / 256 with K <= 16384: 8 per thread), then the token's streams and the
+    // norm weights, whose round trip overlaps the split sums and the
+    // constraints
+    const int po = tid & 31, pg = tid >> 5;
+    float pv[8];
+    {
+        const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.part, (uint32_t)((int64_t)a.splits * a.M * kProjOut * 4));
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int sp = pg + 8 * r;
+            pv[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                pr, (po < kProjOut && sp < a.splits) ? (uint32_t)((((int64_t)sp * a.M + tok) * kProjOut + po) * 4)
+                                                     : kOOB,
+                0, 0));
+        }
+    }
+    const int n_par = 3 + 2 * n + n * n;
+    const float par = tid < 3 ? a.coef[tid] : tid < n_par ? a.bias[tid - 3] : 0.f;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * esz));
     const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.layer_in, (uint32_t)((int64_t)a.M * a.ld_in * esz));
     const uint32_t xrow = (uint32_t)((int64_t)tok * a.ldx * esz);
@@ -1480,21 +1499,23 @@ __global__ __launch_bounds__(256) void mhc_apply_tok_kernel(ApplyArgs a) {
         for (int st = 0; st < kMaxStreams; ++st)
             xv[j][st] = Buf4<T>::load(xr, (st < n && q < nq) ? xrow + (uint32_t)(st * C + 4 * q) * esz : kOOB, 0);
     }
-    {
-        // splits <= 64 (K / 256 with K <= 16384): each thread's 8 loads are
-        // issued together, then added in split order
-        const int o = tid & 31, g = tid >> 5;
-        float pv[8];
+    f32x4 nw[kQ];
+    if (a.norm_w) {
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.norm_w, (uint32_t)(C * 4));
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int sp = g + 8 * r;
-            pv[r] = (o < kProjOut && sp < a.splits) ? a.part[((int64_t)sp * a.M + tok) * kProjOut + o] : 0.f;
+        for (int j = 0; j < kQ; ++j) {
+            const int q = tid + 256 * j;
+            nw[j] = Buf4<float>::load(wr, q < nq ? (uint32_t)(16 * q) : kOOB, 0);
         }
+    }
+    {
+        // the partials added in split order
         float v = 0.f;
 #pragma unroll
         for (int r = 0; r < 8; ++r) v += pv[r];
-        grp_s[g][o] = v;
+        grp_s[pg][po] = v;
     }
+    if (tid < n_par) par_s[tid] = par;
     __syncthreads();
     if (tid < kProjOut) {
         float v = 0.f;
@@ -1506,7 +1527,7 @@ __global__ __launch_bounds__(256) void mhc_apply_tok_kernel(ApplyArgs a) {
     if (tid < 4) {
         const float rs = __fdiv_rn(1.0f, sqrtf(__fdiv_rn(dyn_s[kProjOut - 1], (float)K) + a.rms_eps));
         auto dynf = [&](int o) { return dyn_s[o] * rs; };
-        token_constraints_quad(0, tid, tok, a.M, n, a.coef, a.bias, a.n_iter, a.sk_eps, dynf, hpre_s, a.h_pre,
+        token_constraints_quad(0, tid, tok, a.M, n, &par_s[0], &par_s[3], a.n_iter, a.sk_eps, dynf, hpre_s, a.h_pre,
                                a.h_post, a.h_res);
     }
     __syncthreads();
@@ -1538,7 +1559,7 @@ __global__ __launch_bounds__(256) void mhc_apply_tok_kernel(ApplyArgs a) {
         const int q = tid + 256 * j;
         if (q >= nq) continue;
         f32x4 o = v[j] * scale;
-        if (a.norm_w) o *= *(const f32x4 *)(a.norm_w + 4 * q);
+        if (a.norm_w) o *= nw[j];
         Buf4<T>::store(o, lr, (uint32_t)(((int64_t)tok * a.ld_in + 4 * q) * esz), 0);
     }
 }
