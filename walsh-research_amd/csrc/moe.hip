@@ -729,7 +729,10 @@ __device__ __forceinline__ void expert_lut_init(f32x4 *lut) {
 // silu(g) * u, then down; y[tok, 32e:32e+32] = expert output * routing
 // weight.  Every column is computed on its own, so a pair's result does not
 // depend on which item or column it lands in.
-template <typename T, typename TY, bool BF16MMA, int NHT>
+// PRELOAD: every code byte of the item is requested before the first
+// product (one memory round trip; for a launch whose item is its critical
+// path), instead of as the products go.
+template <typename T, typename TY, bool BF16MMA, int NHT, bool PRELOAD = false>
 __device__ __forceinline__ void expert_item(const ExpArgs &a, const f32x4 *lut, __amdgpu_buffer_rsrc_t xr,
                                             __amdgpu_buffer_rsrc_t yr, int e, int pair, bool ok) {
     constexpr uint32_t esz = sizeof(T);
@@ -746,13 +749,25 @@ __device__ __forceinline__ void expert_item(const ExpArgs &a, const f32x4 *lut, 
     f32x4 hb[NHT];
     const uint8_t *gf = a.gate_f + (int64_t)e * nht * 128;
     const uint8_t *uf = a.up_f + (int64_t)e * nht * 128;
+    const uint8_t *df = a.down_f + (int64_t)e * nht * 128;
+    uint32_t gb[PRELOAD ? 2 * NHT : 1], ub[PRELOAD ? 2 * NHT : 1], db[PRELOAD ? 2 * NHT : 1];
+    if constexpr (PRELOAD) {
+#pragma unroll
+        for (int i = 0; i < 2 * nht; ++i) {
+            gb[i] = gf[i * 64 + lane];
+            ub[i] = uf[i * 64 + lane];
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * nht; ++i) db[i] = df[i * 64 + lane];
+        __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int nt = 0; nt < nht; ++nt) {
         f32x4 g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            g = mma16<BF16MMA>(lut[gf[(nt * 2 + c) * 64 + lane]], xb[c], g);
-            u = mma16<BF16MMA>(lut[uf[(nt * 2 + c) * 64 + lane]], xb[c], u);
+            g = mma16<BF16MMA>(lut[PRELOAD ? gb[nt * 2 + c] : gf[(nt * 2 + c) * 64 + lane]], xb[c], g);
+            u = mma16<BF16MMA>(lut[PRELOAD ? ub[nt * 2 + c] : uf[(nt * 2 + c) * 64 + lane]], xb[c], u);
         }
         f32x4 h;
 #pragma unroll
@@ -766,12 +781,12 @@ __device__ __forceinline__ void expert_item(const ExpArgs &a, const f32x4 *lut, 
         hb[nt] = h;
     }
     // down: D[d][pair], 2 tiles of 16 output dims, K = H in steps of 16
-    const uint8_t *df = a.down_f + (int64_t)e * nht * 128;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
         f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < nht; ++ks) d = mma16<BF16MMA>(lut[df[(mt * nht + ks) * 64 + lane]], hb[ks], d);
+        for (int ks = 0; ks < nht; ++ks)
+            d = mma16<BF16MMA>(lut[PRELOAD ? db[mt * nht + ks] : df[(mt * nht + ks) * 64 + lane]], hb[ks], d);
         f32x4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = (BF16MMA ? bf16r(gd * d[j]) : gd * d[j]) * wr;
@@ -1402,6 +1417,7 @@ __global__ __launch_bounds__(64 * kR1Waves) void moe_decode_kernel(const uint16_
     __shared__ int sel_l[kDecPairs];
     __shared__ int n_items;
     __shared__ int last;
+    __shared__ float gsum_l[kDecTok][4][kMaxE];  // group sums of the partial logits
     const int M = o.M, E = o.E, H = (int)gridDim.x * 16;
     router_w1_small_body(x, ldx, M, C, w1, h, H, w2, E, lpart, part);
     __syncthreads();  // this workgroup's partial logits are stored
@@ -1412,38 +1428,51 @@ __global__ __launch_bounds__(64 * kR1Waves) void moe_decode_kernel(const uint16_
     __syncthreads();
     if (!last) return;
     __threadfence();  // acquire: every workgroup's partials are visible
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nparts = (int)gridDim.x;  // H / 16 <= kTopkPartMax
+    // the partial logits added as router_topk_part_kernel adds them: groups
+    // of 16 partials (zeros past nparts) in order, then the 4 group sums in
+    // order.  Wave w forms group w % 4 of the experts lane + 64 (w / 4) for
+    // every token, its loads requested before the LDS set-up below; wave
+    // t < M then adds token t's group sums.
+    const int grp = wave & 3, ge = lane + 64 * (wave >> 2);
+    float pv[kDecTok][16];
+    {
+        const __amdgpu_buffer_rsrc_t pr = make_rsrc(lpart, (uint32_t)((int64_t)nparts * M * E * 4));
+#pragma unroll
+        for (int t = 0; t < kDecTok; ++t) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int j = 16 * grp + u;
+                pv[t][u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    pr, (t < M && ge < E && j < nparts) ? (uint32_t)((((int64_t)j * M + t) * E + ge) * 4) : kOOB, 0,
+                    0));
+            }
+        }
+    }
     for (int i = threadIdx.x; i < kDecTok * kMaxE; i += blockDim.x) {
         cnt_l[i / kMaxE][i % kMaxE] = 0;
         ps_l[i / kMaxE][i % kMaxE] = 0.f;
     }
     for (int i = threadIdx.x; i < kDecPairs; i += blockDim.x) sel_l[i] = -1;  // slots no token fills stay -1
     expert_lut_init(lut);
+#pragma unroll
+    for (int t = 0; t < kDecTok; ++t) {
+        float acc = 0.f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc += pv[t][u];
+        gsum_l[t][grp][ge] = acc;
+    }
     __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nparts = (int)gridDim.x;  // H / 16 <= kTopkPartMax
     if (wave < M) {
-        // the partial logits added as router_topk_part_kernel adds them:
-        // groups of 16 partials (zeros past nparts) in order, then the 4
-        // group sums in order; all 64 loads of an expert in flight together
         const int tok = wave;
-        const __amdgpu_buffer_rsrc_t pr = make_rsrc(lpart, (uint32_t)((int64_t)nparts * M * E * 4));
         float lg[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int e = lane + 64 * hh;
-            float pv[kTopkPartMax];
-#pragma unroll
-            for (int j = 0; j < kTopkPartMax; ++j)
-                pv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    pr, (e < E && j < nparts) ? (uint32_t)((((int64_t)j * M + tok) * E + e) * 4) : kOOB, 0, 0));
             float v = 0.f;
 #pragma unroll
-            for (int w = 0; w < kTopkPartMax / 16; ++w) {
-                float acc = 0.f;
-#pragma unroll
-                for (int u = 0; u < 16; ++u) acc += pv[16 * w + u];
-                v += acc;
-            }
+            for (int w = 0; w < kTopkPartMax / 16; ++w) v += gsum_l[tok][w][e];
             lg[hh] = e < E ? bf16r(v) : -INFINITY;
         }
         rank_token(tok, lg, o, cnt_l[tok], ps_l[tok], sel_l);
@@ -1457,22 +1486,29 @@ __global__ __launch_bounds__(64 * kR1Waves) void moe_decode_kernel(const uint16_
         o.count[i] = r < M ? cnt_l[r][e] : 0;
         o.probsum[i] = r < M ? ps_l[r][e] : 0.f;
     }
-    if (threadIdx.x == 0) {
-        // the routed pairs grouped by expert, in pair order (at most kDecPairs)
+    if (wave == 0) {
+        // the routed pairs grouped by expert, in pair order (at most
+        // kDecPairs <= 64, lane p holding pair p): each round takes the
+        // expert of the lowest pair not yet listed (experts in order of first
+        // appearance) and lists every pair of that expert
+        const int ep = lane < M * o.k ? sel_l[lane] : -1;
+        // (probabilities that are not numbers select fewer than k)
+        const bool valid = ep >= 0 && ep < E;
+        uint64_t pending = __ballot(valid);
         int n = 0;
-        for (int p = 0; p < M * o.k; ++p) {
-            const int e = sel_l[p];
-            if (e < 0 || e >= E) continue;  // (probabilities that are not numbers select fewer than k)
-            int i = 0;
-            while (i < n && item_e[i] != e) ++i;
-            if (i == n) {
-                item_e[n] = e;
-                item_n[n] = 0;
-                ++n;
+        while (pending) {
+            const int lead = (int)__builtin_ctzll(pending);
+            const int el = __builtin_amdgcn_readlane(ep, lead);
+            const uint64_t same = __ballot(valid && ep == el);
+            if ((same >> lane) & 1u) item_p[n][__builtin_popcountll(same & ((1ull << lane) - 1))] = lane;
+            if (lane == 0) {
+                item_e[n] = el;
+                item_n[n] = __builtin_popcountll(same);
             }
-            item_p[i][item_n[i]++] = p;
+            pending &= ~same;
+            ++n;
         }
-        n_items = n;
+        if (lane == 0) n_items = n;
     }
     __syncthreads();
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(ex.x, (uint32_t)((int64_t)ex.M * ex.ldx * 2));
@@ -1480,7 +1516,7 @@ __global__ __launch_bounds__(64 * kR1Waves) void moe_decode_kernel(const uint16_
     const int t = lane & 15;
     for (int i = wave; i < n_items; i += kR1Waves) {
         const bool ok = t < item_n[i];
-        expert_item<uint16_t, TY, true, NHT>(ex, lut, xr, yr, item_e[i], ok ? item_p[i][t] : 0, ok);
+        expert_item<uint16_t, TY, true, NHT, true>(ex, lut, xr, yr, item_e[i], ok ? item_p[i][t] : 0, ok);
     }
     if (threadIdx.x == 0) *sync = 0u;  // no other workgroup of this launch reads it any more
 }
