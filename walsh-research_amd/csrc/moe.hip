@@ -1161,6 +1161,9 @@ static int grid_cap(int64_t waves_needed, int64_t limit = 0) {
 // their outputs, with SiLU on the rounded first product.
 constexpr int kR1Waves = 8;
 constexpr int kR1SmallRows = 256;  // row counts up to this take the split-K kernel
+// CPOL: cache policy of the partial-logit stores (16: device scope, sc1, for
+// a reader in another workgroup of the same launch).
+template <int CPOL = 0>
 __device__ __forceinline__ void router_w1_small_body(const uint16_t *__restrict__ x, int64_t ldx, int M, int C,
                                                      const uint16_t *__restrict__ w1, uint16_t *__restrict__ h,
                                                      int64_t ldh, const uint16_t *__restrict__ w2, int E,
@@ -1222,7 +1225,9 @@ __device__ __forceinline__ void router_w1_small_body(const uint16_t *__restrict_
         // d[r] = partial logit of expert 16 et + 4 fq + r for token m0 + fr
         // (E % 4 == 0: the 4 experts are valid together)
         const int e0 = 16 * et + 4 * fq;
-        Buf4<float>::store(d, pr, (row_ok && e0 < E) ? (uint32_t)(((int64_t)(m0 + fr) * E + e0) * 4) : kOOB, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d), pr,
+                                               (row_ok && e0 < E) ? (uint32_t)(((int64_t)(m0 + fr) * E + e0) * 4) : kOOB,
+                                               0, CPOL);
     }
 }
 
@@ -1419,15 +1424,18 @@ __global__ __launch_bounds__(64 * kR1Waves) void moe_decode_kernel(const uint16_
     __shared__ int last;
     __shared__ float gsum_l[kDecTok][4][kMaxE];  // group sums of the partial logits
     const int M = o.M, E = o.E, H = (int)gridDim.x * 16;
-    router_w1_small_body(x, ldx, M, C, w1, h, H, w2, E, lpart, part);
-    __syncthreads();  // this workgroup's partial logits are stored
+    // The hand-off without device-scope fences (whose L2 write-back and
+    // invalidation cost microseconds here): wave 0 stores the partial logits
+    // at device scope (sc1: performed at the point every XCD's accesses meet),
+    // waits until they are acknowledged, then counts; the last workgroup
+    // reads them with device-scope loads issued after its count returned.
+    router_w1_small_body<16>(x, ldx, M, C, w1, h, H, w2, E, lpart, part);
     if (threadIdx.x == 0) {
-        __threadfence();  // release: the partials before the count
-        last = atomicAdd(sync, 1u) == gridDim.x - 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial-logit stores are performed
+        last = __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();  // acquire: every workgroup's partials are visible
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nparts = (int)gridDim.x;  // H / 16 <= kTopkPartMax
     // the partial logits added as router_topk_part_kernel adds them: groups
@@ -1446,7 +1454,7 @@ __global__ __launch_bounds__(64 * kR1Waves) void moe_decode_kernel(const uint16_
                 const int j = 16 * grp + u;
                 pv[t][u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
                     pr, (t < M && ge < E && j < nparts) ? (uint32_t)((((int64_t)j * M + t) * E + ge) * 4) : kOOB, 0,
-                    0));
+                    16));  // device scope (sc1)
             }
         }
     }
