@@ -31,29 +31,6 @@ struct DecArgs {
     float *part;                    // [B][H][S][D + 2]: acc[0..D), max, sum
 };
 
-template <typename T> struct Ld8;
-template <> struct Ld8<uint16_t> {
-    static __device__ __forceinline__ void load(const uint16_t *p, float (&f)[8]) {
-        const uint4 u = *(const uint4 *)p;
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[2 * i] = __uint_as_float(w[i] << 16);
-            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-        }
-    }
-};
-template <> struct Ld8<float> {
-    static __device__ __forceinline__ void load(const float *p, float (&f)[8]) {
-        const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[i] = a[i];
-            f[4 + i] = b[i];
-        }
-    }
-};
-
 // Sum over the LPK lanes that share a key row (aligned groups of LPK lanes).
 template <int LPK>
 __device__ __forceinline__ float group_sum(float v) {
@@ -62,11 +39,49 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// A lane's 8 elements of one cache row, loaded raw (converted at use).
+template <typename T> struct Raw8;
+template <> struct Raw8<uint16_t> {
+    uint4 u;
+    __device__ __forceinline__ void load(const uint16_t *p) { u = *(const uint4 *)p; }
+    __device__ __forceinline__ void get(float (&f)[8]) const {
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+};
+template <> struct Raw8<float> {
+    f32x4 a, b;
+    __device__ __forceinline__ void load(const float *p) {
+        a = *(const f32x4 *)p;
+        b = *(const f32x4 *)(p + 4);
+    }
+    __device__ __forceinline__ void get(float (&f)[8]) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[i] = a[i];
+            f[4 + i] = b[i];
+        }
+    }
+};
+
+// One (sequence, head, chunk of keys): the chunk's scores into LDS, their
+// maximum, then p = exp(score - max) and sum_j p_j v_j over the lane's rows.
+// A workgroup step covers KPB keys (LPK lanes per key row); the rows are
+// requested kDecGroup steps at a time, the next group while the current one
+// is used, and the first group of V with the first group of K, so that V's
+// first round trip overlaps the scores.  Keys past the chunk load its first
+// row (finite values, never used).
+constexpr int kDecGroup = 4;
 template <typename T, int D>
 __global__ __launch_bounds__(kDecThreads) void decode_attn_partial_kernel(DecArgs a) {
     constexpr int LPK = D / 8;             // lanes per key row
     constexpr int KPW = 64 / LPK;          // keys per wavefront step
     constexpr int KPB = KPW * kDecWaves;   // keys per workgroup step
+    constexpr int G = kDecGroup;
     __shared__ float sc[kDecMaxChunk];
     __shared__ float red[kDecWaves];
     __shared__ float accl[kDecWaves][D];
@@ -77,28 +92,51 @@ __global__ __launch_bounds__(kDecThreads) void decode_attn_partial_kernel(DecArg
     const int j0 = s * a.chunk;
     const int j1 = j0 + a.chunk < a.L ? j0 + a.chunk : a.L;
     const int n = j1 - j0;  // >= 1 by construction of S
+    const int nst = (n + KPB - 1) / KPB;   // workgroup steps
+    const int koff = wave * KPW + kw;      // the lane's key within a step
 
-    float qv[8];
-    Ld8<T>::load((const T *)a.q + b * a.q_bs + h * a.q_hs + 8 * sub, qv);
     const T *kb = (const T *)a.k + b * a.kv_bs + h * a.kv_hs + 8 * sub;
     const T *vb = (const T *)a.v + b * a.kv_bs + h * a.kv_hs + 8 * sub;
-
-    // scores of the chunk (rows past j1 are not read)
-    float mx = -INFINITY;
-    for (int base = 0; base < n; base += KPB) {
-        const int jj = base + wave * KPW + kw;
-        float d = 0.f;
-        if (jj < n) {
-            float kv[8];
-            Ld8<T>::load(kb + (int64_t)(j0 + jj) * a.kv_rs, kv);
+    auto row = [&](const T *base, int step) {
+        const int jj = step * KPB + koff;
+        return base + (int64_t)(j0 + (jj < n ? jj : 0)) * a.kv_rs;
+    };
+    Raw8<T> kc[G], kn[G], vc[G], vn[G];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) d += qv[i] * kv[i];
+    for (int i = 0; i < G; ++i) kc[i].load(row(kb, i));
+#pragma unroll
+    for (int i = 0; i < G; ++i) vc[i].load(row(vb, i));
+    float qv[8];
+    {
+        Raw8<T> qr;
+        qr.load((const T *)a.q + b * a.q_bs + h * a.q_hs + 8 * sub);
+        qr.get(qv);
+    }
+
+    // scores of the chunk
+    float mx = -INFINITY;
+    for (int g0 = 0; g0 < nst; g0 += G) {
+        if (g0 + G < nst) {
+#pragma unroll
+            for (int i = 0; i < G; ++i) kn[i].load(row(kb, g0 + G + i));
         }
-        d = group_sum<LPK>(d) * a.scale;
-        if (jj < n) {
-            if (sub == 0) sc[jj] = d;
-            mx = fmaxf(mx, d);
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            if (g0 + i >= nst) break;   // workgroup-uniform
+            const int jj = (g0 + i) * KPB + koff;
+            float kv[8];
+            kc[i].get(kv);
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d += qv[e] * kv[e];
+            d = group_sum<LPK>(d) * a.scale;
+            if (jj < n) {
+                if (sub == 0) sc[jj] = d;
+                mx = fmaxf(mx, d);
+            }
         }
+#pragma unroll
+        for (int i = 0; i < G; ++i) kc[i] = kn[i];
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
@@ -112,16 +150,26 @@ __global__ __launch_bounds__(kDecThreads) void decode_attn_partial_kernel(DecArg
     // p_j = exp(score_j - max); acc = sum_j p_j v_j over this lane's rows
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float sum = 0.f;
-    for (int base = 0; base < n; base += KPB) {
-        const int jj = base + wave * KPW + kw;
-        if (jj < n) {
-            const float p = expf(sc[jj] - mx);
-            float vv[8];
-            Ld8<T>::load(vb + (int64_t)(j0 + jj) * a.kv_rs, vv);
+    for (int g0 = 0; g0 < nst; g0 += G) {
+        if (g0 + G < nst) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] += p * vv[i];
-            if (sub == 0) sum += p;
+            for (int i = 0; i < G; ++i) vn[i].load(row(vb, g0 + G + i));
         }
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            if (g0 + i >= nst) break;
+            const int jj = (g0 + i) * KPB + koff;
+            if (jj < n) {
+                const float p = expf(sc[jj] - mx);
+                float vv[8];
+                vc[i].get(vv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[e] += p * vv[e];
+                if (sub == 0) sum += p;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < G; ++i) vc[i] = vn[i];
     }
     // reduce over the KPW row groups of the wavefront (lane bits above LPK)
 #pragma unroll
