@@ -1124,6 +1124,17 @@ struct PostProjArgs {
     float *part;              // [splits][M][25]
 };
 
+// Every argument read at entry in one batch of scalar loads, the values kept
+// through an empty asm statement: left to itself the compiler reads each
+// field where it is first used, one memory round trip after another.
+__device__ __forceinline__ PostProjArgs load_args(const PostProjArgs &src) {
+    PostProjArgs a = src;
+    asm volatile("" : "+s"(a.xo), "+s"(a.ld_xo), "+s"(a.out), "+s"(a.ld_out), "+s"(a.hr_prev), "+s"(a.hp_prev),
+                 "+s"(a.x_new), "+s"(a.ld_new), "+s"(a.M), "+s"(a.n), "+s"(a.C), "+s"(a.splits), "+s"(a.cper),
+                 "+s"(a.phi32), "+s"(a.part));
+    return a;
+}
+
 // One 32-column block of a work item's loads: the lane's 8 columns of each
 // previous stream and of the layer output, and the phi fragments of those
 // columns for each new stream.
@@ -1222,7 +1233,8 @@ __device__ __forceinline__ void post_proj_flush(const uint8_t *stage, const Post
 }
 
 template <int N>
-__global__ __launch_bounds__(256) void mhc_post_proj_kernel(PostProjArgs a) {
+__global__ __launch_bounds__(256) void mhc_post_proj_kernel(PostProjArgs args) {
+    const PostProjArgs a = load_args(args);
     __shared__ __attribute__((aligned(16))) uint8_t stage_all[4][N * 16 * kStagePitch];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, m = lane & 15,
               kq = lane >> 4;
@@ -1245,12 +1257,19 @@ __global__ __launch_bounds__(256) void mhc_post_proj_kernel(PostProjArgs a) {
     // this lane's token's update coefficients, then the first two blocks'
     // loads (issued after the coefficients', so that the wait at the head
     // of the loop counts only block loads)
+    // (buffer loads, zero past M: no branch around them, so none waits)
     float hr[N][N], hp[N];
+    {
+        const __amdgpu_buffer_rsrc_t hrr = make_rsrc(a.hr_prev, (uint32_t)((int64_t)a.M * N * N * 4));
+        const __amdgpu_buffer_rsrc_t hpr = make_rsrc(a.hp_prev, (uint32_t)((int64_t)a.M * N * 4));
+        const uint32_t ho = ok ? (uint32_t)tok * (N * N * 4) : kOOB, po = ok ? (uint32_t)tok * (N * 4) : kOOB;
 #pragma unroll
-    for (int r = 0; r < N; ++r) {
-        hp[r] = ok ? a.hp_prev[(int64_t)tok * N + r] : 0.f;
+        for (int r = 0; r < N; ++r) {
+            hp[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(hpr, po, r * 4, 0));
 #pragma unroll
-        for (int s2 = 0; s2 < N; ++s2) hr[r][s2] = ok ? a.hr_prev[(int64_t)tok * N * N + r * N + s2] : 0.f;
+            for (int s2 = 0; s2 < N; ++s2)
+                hr[r][s2] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(hrr, ho, (r * N + s2) * 4, 0));
+        }
     }
     PostProjBlock<N> b0, b1;
     __builtin_amdgcn_sched_barrier(0);
