@@ -1440,6 +1440,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
     const bool narrow = (a.in_o & 31) == 0 && mt * hp <= kWideThreads;   // workgroup-uniform
     const int n_tok = tid / hp, n_col = 2 * (tid - n_tok * hp);
     const bool n_ok = narrow && n_tok < mt;
+    // Full tiles of contiguous 4096-element rows: the tile (16 rows x 8 KB)
+    // comes straight into the stage region with buffer-to-LDS loads, a whole
+    // 1 KB row segment per instruction (the per-thread loads below touch 16
+    // rows per instruction, 32 bytes of each, and queue up behind each
+    // other); 16-byte chunk p of row t sits at position p ^ t of its 256-byte
+    // window, so that one column's 16 rows fall on distinct banks when each
+    // thread reads its 32 groups back.
+    const bool lds_x = !narrow && a.in_o == 128 && a.gsx == 128;   // workgroup-uniform
     u32x2 xraw[32];
     uint32_t xn[32];
     {
@@ -1449,6 +1457,18 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
             const uint32_t voff = n_ok ? x_row_off(a, tile * kTile + n_tok, 2) + (uint32_t)n_col * 2 : kOOB;
 #pragma unroll
             for (int g = 0; g < 32; ++g) xn[g] = __builtin_amdgcn_raw_buffer_load_b32(xr, voff, (uint32_t)g * gstride, 0);
+        } else if (lds_x) {
+            const int w = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int seg = w * 16 + i, tr = seg >> 3, sg = seg & 7;   // row of the tile, 1 KB segment
+                const int row = tile * kTile + tr;
+                const uint32_t off =
+                    row < a.M ? x_row_off(a, row, 2) + (uint32_t)(sg * 1024 + ((lane ^ tr) << 4)) : kOOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    xr, (__attribute__((address_space(3))) void *)((unsigned char *)xs + tr * 8192 + sg * 1024), 16,
+                    off, 0, 0, 0);
+            }
         } else if (xwave) {
             const int row = tile * kTile + t;
             const uint32_t voff = (row < a.M && i0 < a.in_o) ? x_row_off(a, row, 2) + (uint32_t)i0 * 2 : kOOB;
@@ -1524,7 +1544,19 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
         alpha_l[tid + k * kWideThreads] = (_Float16)(i < a.in_o ? (a.alpha ? __uint_as_float(avr[k]) : 1.f) * a32 : 0.f);
     }
     beta_l[tid] = (_Float16)(bo < a.out_o ? __uint_as_float(bvr) : 0.f);
+    if (lds_x) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's share of the tile is in LDS
     lds_barrier();  // tables ready
+    if (lds_x) {
+        // the thread's 4 columns i0..i0+3 of row t in every group: byte
+        // g * 256 + 2 i0 of the row, chunk p = 16 g + i0 / 8 at p ^ t
+        const unsigned char *xrow = (const unsigned char *)xs + t * 8192;
+#pragma unroll
+        for (int g = 0; g < 32; ++g) {
+            const int p = 16 * g + (i0 >> 3);
+            xraw[g] = *(const u32x2 *)(xrow + (p >> 6) * 1024 + (((p & 63) ^ t) << 4) + (i0 & 7) * 2);
+        }
+        lds_barrier();  // every thread holds its columns: the stage region is free
+    }
     if (narrow) {
         // the column pair as one pass of wide3_transform_x: the same
         // products, transform and roundings
@@ -1544,7 +1576,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
 #pragma unroll
             for (int g = 0; g < 32; ++g) dst[g * 64 * 4] = pack_bf16x2(v[g][0], v[g][1]);
         }
-    } else if (xwave) {
+    } else if (xwave || lds_x) {
         wide3_transform_x(xraw, alpha_l + i0,
                           (uint2 *)(xs + (size_t)(i0 >> 5) * 32 * 64 + t + 16 * ((i0 >> 3) & 3)) + ((i0 >> 2) & 1));
     }
