@@ -931,20 +931,36 @@ __global__ __launch_bounds__(kPairThreads, DENSE ? 3 : 4) void hadamard_pair_ker
     const int slot = b < full ? (b / (8 * n)) * 8 + b % 8 : b / n;
     const HadArgs &a = an.p[l];
     const int tid = threadIdx.x;
-    for (int e = tid; e < 256; e += kPairThreads) {
-        float val[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) val[j] = (float)((int)(((uint32_t)e >> (6 - 2 * j)) & 3u) - 1);
-        lut[e] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
-    }
     {
         const int e = tid;   // (q, g) = (e >> 5, e & 31); kPairThreads == 128 entries
         const int g = e & 31, i0 = 4 * (e >> 5);
+        // buffer loads (zero past in_o / out_o) with no branch around them,
+        // converted after the LUT is built: a conversion or branch right
+        // after a load waits for it
+        uint32_t ra[4] = {0u, 0u, 0u, 0u}, rb[4];
+        const __amdgpu_buffer_rsrc_t br = make_rsrc(a.beta, (uint32_t)((31 * a.beta_h + a.out_o) * 4));
+        if (a.alpha) {
+            const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.alpha, (uint32_t)(32 * a.in_o * 4));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                ra[j] = __builtin_amdgcn_raw_buffer_load_b32(ar, i0 + j < a.in_o ? (uint32_t)(g * a.in_o + i0 + j) * 4 : kOOB,
+                                                             0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            rb[j] = __builtin_amdgcn_raw_buffer_load_b32(br, i0 + j < a.out_o ? (uint32_t)(g * a.beta_h + i0 + j) * 4 : kOOB,
+                                                         0, 0);
+        for (int c = tid; c < 256; c += kPairThreads) {
+            float val[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) val[j] = (float)((int)(((uint32_t)c >> (6 - 2 * j)) & 3u) - 1);
+            lut[c] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
+        }
         f32x4 va, vb;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            va[j] = (i0 + j < a.in_o) ? (a.alpha ? a.alpha[g * a.in_o + i0 + j] : 1.f) : 0.f;
-            vb[j] = (i0 + j < a.out_o) ? a.beta[g * a.beta_h + i0 + j] * 0.03125f : 0.f;
+            va[j] = (i0 + j < a.in_o) ? (a.alpha ? __uint_as_float(ra[j]) : 1.f) : 0.f;
+            vb[j] = (i0 + j < a.out_o) ? __uint_as_float(rb[j]) * 0.03125f : 0.f;
         }
         alpha_l[e] = va;
         beta_l[e] = vb;
