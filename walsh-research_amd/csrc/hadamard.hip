@@ -1902,33 +1902,73 @@ __global__ __launch_bounds__(kThreads, 2) void hadamard_mlp_kernel(HadArgs g, Ha
         for (int j = 0; j < 4; ++j) val[j] = (float)((int)((byte >> (6 - 2 * j)) & 3u) - 1);
         ((uint2 *)lut)[byte] = uint2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
     }
-    for (int e = tid; e < 128; e += kThreads) {
-        const int gg = e & 31, i0 = 4 * (e >> 5);
-        f32x4 va, vb, vd;
+    // alpha / beta of the three layers: every load issued before any
+    // conversion (buffer loads, zero past the shapes, no branch around them;
+    // a conversion or branch right after a load waits for it)
+    {
+        const __amdgpu_buffer_rsrc_t gar = make_rsrc(g.alpha, (uint32_t)(32 * g.in_o * 4));
+        const __amdgpu_buffer_rsrc_t uar = make_rsrc(u.alpha, (uint32_t)(32 * g.in_o * 4));
+        const __amdgpu_buffer_rsrc_t dbr = make_rsrc(d.beta, (uint32_t)((31 * d.beta_h + d.out_o) * 4));
+        const __amdgpu_buffer_rsrc_t gbr = make_rsrc(g.beta, (uint32_t)(32 * g.out_o * 4));
+        const __amdgpu_buffer_rsrc_t ubr = make_rsrc(u.beta, (uint32_t)(32 * g.out_o * 4));
+        const __amdgpu_buffer_rsrc_t dar = make_rsrc(d.alpha, (uint32_t)(32 * d.in_o * 4));
+        constexpr int kIt = (3 * 128 + kThreads - 1) / kThreads;   // Nt <= 3
+        uint32_t r1[3][4], r2[kIt][3][4];
+        {
+            const int e = tid, gg = e & 31, i0 = 4 * (e >> 5);
+            const bool live = e < 128;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const bool ok = i0 + j < g.in_o;
-            va[j] = ok ? g.alpha[gg * g.in_o + i0 + j] : 0.f;
-            vb[j] = ok ? u.alpha[gg * g.in_o + i0 + j] : 0.f;
-            vd[j] = i0 + j < d.out_o ? d.beta[gg * d.beta_h + i0 + j] * 0.03125f : 0.f;
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = live && i0 + j < g.in_o, okd = live && i0 + j < d.out_o;
+                r1[0][j] = __builtin_amdgcn_raw_buffer_load_b32(gar, ok ? (uint32_t)(gg * g.in_o + i0 + j) * 4 : kOOB, 0, 0);
+                r1[1][j] = __builtin_amdgcn_raw_buffer_load_b32(uar, ok ? (uint32_t)(gg * g.in_o + i0 + j) * 4 : kOOB, 0, 0);
+                r1[2][j] = __builtin_amdgcn_raw_buffer_load_b32(
+                    dbr, okd ? (uint32_t)(gg * d.beta_h + i0 + j) * 4 : kOOB, 0, 0);
+            }
         }
-        ag_l[e] = va;
-        au_l[e] = vb;
-        bd_l[e] = vd;
-    }
-    for (int e = tid; e < Nt * 128; e += kThreads) {
-        const int h = e & 31, o0 = 4 * (e >> 5);
-        f32x4 va, vb, vd;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const bool ok = o0 + j < g.out_o;
-            va[j] = ok ? g.beta[h * g.out_o + o0 + j] * 0.03125f : 0.f;
-            vb[j] = ok ? u.beta[h * g.out_o + o0 + j] * 0.03125f : 0.f;
-            vd[j] = o0 + j < d.in_o ? d.alpha[h * d.in_o + o0 + j] : 0.f;  // chunk e / 128, element (h, o0 + j)
+        for (int it = 0; it < kIt; ++it) {
+            const int e = tid + it * kThreads, h = e & 31, o0 = 4 * (e >> 5);
+            const bool live = e < Nt * 128;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = live && o0 + j < g.out_o, okd = live && o0 + j < d.in_o;
+                r2[it][0][j] = __builtin_amdgcn_raw_buffer_load_b32(gbr, ok ? (uint32_t)(h * g.out_o + o0 + j) * 4 : kOOB, 0, 0);
+                r2[it][1][j] = __builtin_amdgcn_raw_buffer_load_b32(ubr, ok ? (uint32_t)(h * g.out_o + o0 + j) * 4 : kOOB, 0, 0);
+                r2[it][2][j] = __builtin_amdgcn_raw_buffer_load_b32(
+                    dar, okd ? (uint32_t)(h * d.in_o + o0 + j) * 4 : kOOB, 0, 0);
+            }
         }
-        bg_l[e] = va;
-        bu_l[e] = vb;
-        ad_l[e] = vd;
+        if (tid < 128) {
+            const int e = tid, i0 = 4 * (e >> 5);
+            f32x4 va, vb, vd;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = i0 + j < g.in_o;
+                va[j] = ok ? __uint_as_float(r1[0][j]) : 0.f;
+                vb[j] = ok ? __uint_as_float(r1[1][j]) : 0.f;
+                vd[j] = i0 + j < d.out_o ? __uint_as_float(r1[2][j]) * 0.03125f : 0.f;
+            }
+            ag_l[e] = va;
+            au_l[e] = vb;
+            bd_l[e] = vd;
+        }
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int e = tid + it * kThreads, o0 = 4 * (e >> 5);
+            if (e >= Nt * 128) continue;
+            f32x4 va, vb, vd;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = o0 + j < g.out_o;
+                va[j] = ok ? __uint_as_float(r2[it][0][j]) * 0.03125f : 0.f;
+                vb[j] = ok ? __uint_as_float(r2[it][1][j]) * 0.03125f : 0.f;
+                vd[j] = o0 + j < d.in_o ? __uint_as_float(r2[it][2][j]) : 0.f;  // chunk e / 128, element (h, o0 + j)
+            }
+            bg_l[e] = va;
+            bu_l[e] = vb;
+            ad_l[e] = vd;
+        }
     }
     __syncthreads();
 
