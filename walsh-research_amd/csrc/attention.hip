@@ -763,22 +763,37 @@ __global__ __launch_bounds__(64 * kPhWaves) void prefill_attn_head_kernel(PfArgs
     if (tid == 0) next_tile = 0;
     const uint16_t *kbase = a.k + b * a.kv_sb + h * a.kv_sh;
     const uint16_t *vbase = a.v + b * a.kv_sb + h * a.kv_sh;
-    // stage K and V^T; rows T .. tpad - 1 are zeros (finite, masked)
-    for (int p = tid; p < tpad * (D / 8); p += 64 * kPhWaves) {
-        const int key = p / (D / 8), part = p - key * (D / 8);
-        uint4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-        if (key < a.T) {
-            kv = *(const uint4 *)(kbase + (int64_t)key * a.kv_st + part * 8);
-            vv = *(const uint4 *)(vbase + (int64_t)key * a.kv_st + part * 8);
-        }
-        u32x2 *kd = (u32x2 *)(k_l + key * ks + part * 8);   // 8-byte aligned rows
-        kd[0] = u32x2{kv.x, kv.y};
-        kd[1] = u32x2{kv.z, kv.w};
-        const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+    // stage K and V^T; rows T .. tpad - 1 are zeros (finite, masked).  The
+    // rows come in batches of kPhBatch per thread, every load of a batch
+    // requested before its stores (buffer loads, zero past T: no branch
+    // around them, so one round trip per batch rather than per row)
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase, (uint32_t)(((int64_t)(a.T - 1) * a.kv_st + D) * 2));
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(vbase, (uint32_t)(((int64_t)(a.T - 1) * a.kv_st + D) * 2));
+    constexpr int kPhBatch = 4;
+    const int nstage = tpad * (D / 8);
+    for (int p0 = tid; p0 < nstage; p0 += kPhBatch * 64 * kPhWaves) {
+        uint4 kv[kPhBatch], vv[kPhBatch];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            vt_l[(part * 8 + 2 * e) * vs + key] = (uint16_t)(w[e] & 0xffffu);
-            vt_l[(part * 8 + 2 * e + 1) * vs + key] = (uint16_t)(w[e] >> 16);
+        for (int i = 0; i < kPhBatch; ++i) {
+            const int p = p0 + i * 64 * kPhWaves, key = p / (D / 8), part = p - key * (D / 8);
+            const uint32_t off =
+                (p < nstage && key < a.T) ? (uint32_t)(((int64_t)key * a.kv_st + part * 8) * 2) : kOOB;
+            kv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
+            vv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < kPhBatch; ++i) {
+            const int p = p0 + i * 64 * kPhWaves, key = p / (D / 8), part = p - key * (D / 8);
+            if (p >= nstage) break;
+            u32x2 *kd = (u32x2 *)(k_l + key * ks + part * 8);   // 8-byte aligned rows
+            kd[0] = u32x2{kv[i].x, kv[i].y};
+            kd[1] = u32x2{kv[i].z, kv[i].w};
+            const uint32_t w[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vt_l[(part * 8 + 2 * e) * vs + key] = (uint16_t)(w[e] & 0xffffu);
+                vt_l[(part * 8 + 2 * e + 1) * vs + key] = (uint16_t)(w[e] >> 16);
+            }
         }
     }
     __syncthreads();
