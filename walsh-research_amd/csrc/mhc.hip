@@ -681,14 +681,23 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
     // the norm weights (or ones), coef and bias go to LDS with the tile; they
     // are requested before the tile (C / 4 <= kPreThreads) and written once
     // it is in flight, so waiting for them does not wait for the tile
+    // (buffer loads, zero past their ranges, with no branch around them and
+    // no conversion until put_small: a branch or conversion right after a
+    // load waits for every load issued before it)
     static_assert(1024 / 4 <= kPreThreads, "one norm-weight quad per thread");
-    const f32x4 nwv = (tid < C / 4 && a.norm_w) ? *(const f32x4 *)(a.norm_w + 4 * tid) : f32x4{1.f, 1.f, 1.f, 1.f};
+    u32x4 nwr = {0u, 0u, 0u, 0u};
+    if (a.norm_w)
+        nwr = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(a.norm_w, (uint32_t)(C * 4)),
+                                                    tid < C / 4 ? (uint32_t)(16 * tid) : kOOB, 0, 0);
     float *cb_l = (float *)(nw_l + C / 4);    // [3 coef][2n + n*n bias]
     const int ncb = 3 + 2 * n + n * n;
-    const float cbv = tid < ncb ? (tid < 3 ? a.coef[tid] : a.bias[tid - 3]) : 0.f;
+    const uint32_t cr = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.coef, 12u), tid < 3 ? (uint32_t)(4 * tid) : kOOB,
+                                                             0, 0);
+    const uint32_t br = __builtin_amdgcn_raw_buffer_load_b32(
+        make_rsrc(a.bias, (uint32_t)((ncb - 3) * 4)), tid >= 3 && tid < ncb ? (uint32_t)(4 * (tid - 3)) : kOOB, 0, 0);
     auto put_small = [&]() {
-        if (tid < C / 4) nw_l[tid] = nwv;
-        if (tid < ncb) cb_l[tid] = cbv;
+        if (tid < C / 4) nw_l[tid] = a.norm_w ? __builtin_bit_cast(f32x4, nwr) : f32x4{1.f, 1.f, 1.f, 1.f};
+        if (tid < ncb) cb_l[tid] = __uint_as_float(tid < 3 ? cr : br);
     };
 
     // phase 0 (POST): the stream update of the previous layer, formed per
@@ -726,21 +735,30 @@ __global__ __launch_bounds__(kPreThreads, 2) void mhc_pre2_kernel(Pre2Args a) {
         // the barrier waits for them alone and each item below waits only for
         // its own loads
         constexpr int kMaxH = (TT * (kMaxStreams * kMaxStreams + kMaxStreams) + kPreThreads - 1) / kPreThreads;
-        float hv[kMaxH];
+        uint32_t hvr[kMaxH], hvp[kMaxH];
+        {
+            const __amdgpu_buffer_rsrc_t hrr = make_rsrc(a.hr_prev, (uint32_t)((int64_t)a.M * n * n * 4));
+            const __amdgpu_buffer_rsrc_t hpr = make_rsrc(a.hp_prev, (uint32_t)((int64_t)a.M * n * 4));
 #pragma unroll
-        for (int i = 0; i < kMaxH; ++i) {
-            const int e = tid + i * kPreThreads;
-            const int r = e / nh, k = e - r * nh;
-            const bool ok = e < TT * nh && tok0 + r < a.M;
-            hv[i] = !ok ? 0.f : k < n * n ? a.hr_prev[(int64_t)(tok0 + r) * n * n + k]
-                                          : a.hp_prev[(int64_t)(tok0 + r) * n + (k - n * n)];
+            for (int i = 0; i < kMaxH; ++i) {
+                const int e = tid + i * kPreThreads;
+                const int r = e / nh, k = e - r * nh;
+                const bool ok = e < TT * nh && tok0 + r < a.M;
+                hvr[i] = __builtin_amdgcn_raw_buffer_load_b32(
+                    hrr, ok && k < n * n ? (uint32_t)(((int64_t)(tok0 + r) * n * n + k) * 4) : kOOB, 0, 0);
+                hvp[i] = __builtin_amdgcn_raw_buffer_load_b32(
+                    hpr, ok && k >= n * n ? (uint32_t)(((int64_t)(tok0 + r) * n + (k - n * n)) * 4) : kOOB, 0, 0);
+            }
         }
         load_round(0);
         load_phi(ks0, pa);
         put_small();
 #pragma unroll
-        for (int i = 0; i < kMaxH; ++i)
-            if (tid + i * kPreThreads < TT * nh) hprev[tid + i * kPreThreads] = hv[i];
+        for (int i = 0; i < kMaxH; ++i) {
+            const int e = tid + i * kPreThreads;
+            const int k = e - (e / nh) * nh;
+            if (e < TT * nh) hprev[e] = __uint_as_float(k < n * n ? hvr[i] : hvp[i]);
+        }
         lds_barrier();
         constexpr int VE = 16 / (int)esz;     // values per chunk: 8 bf16 or 4 f32
         for (int it0 = 0; it0 < nit; it0 += kPostItems * kPreThreads) {
