@@ -1531,11 +1531,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
     }
     // the output waves' rotary (cos, sin): wave w < 4 takes outputs
     // 4w..4w+3 of the tile, lane = (token tt, output jj)
-    const int tt = lane >> 2, jj = lane & 3, o16 = 4 * wave + jj;
+    // (waves w and w + 4 both take outputs 4 (w % 4) .. + 3, groups h of
+    // their half: [16 (w / 4), 16 (w / 4) + 16))
+    const int ow = wave & 3, h0 = 16 * (wave >> 2);
+    const int tt = lane >> 2, jj = lane & 3, o16 = 4 * ow + jj;
     const int orow = tile * kTile + tt, o = kNTile * nt + o16;
     const bool ok = orow < a.M && o < a.out_o;
     const bool rope = a.rope != nullptr;
-    const bool cs_ok = rope && ok && wave < 4;
+    const bool cs_ok = rope && ok;
     u32x2 csr = {0u, 0u};
     if (rope) {
         const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.rope, (uint32_t)(a.rope_T * a.rope_D * 4));
@@ -1627,10 +1630,11 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
 #pragma unroll
     for (int j = 0; j < 4; ++j) part[(4 * wave + j) * 64 + lane] = acc[j];
     lds_barrier();
-    if (wave >= 4) return;
-    // wave w: outputs 4w..4w+3 of the tile; lane = (token tt, output jj), so
-    // one read instruction covers 64 consecutive floats
-    const float *pp = (const float *)part + (tt + 16 * wave) * 4 + jj;
+    // waves w and w + 4: outputs 4 (w % 4)..+3 of the tile, lane = (token tt,
+    // output jj), so one read instruction covers 64 consecutive floats; both
+    // run the output transform, each stores half of the 32 groups (two
+    // shorter store chains per SIMD instead of one)
+    const float *pp = (const float *)part + (tt + 16 * ow) * 4 + jj;
     float v[32];
 #pragma unroll
     for (int g = 0; g < 32; ++g) v[g] = pp[g * 256];
@@ -1640,8 +1644,9 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
     const uint32_t hstride = (uint32_t)(GS ? GS : a.gsy) * 2;
     const f32x2 cs = cs_ok ? f32x2{__uint_as_float(csr.x), __uint_as_float(csr.y)} : f32x2{1.f, 0.f};
 #pragma unroll
-    for (int h = 0; h < 32; ++h) {
-        float r = v[h] * (float)beta_l[h * kNTile + o16];
+    for (int hi = 0; hi < 16; ++hi) {
+        const int h = h0 + hi;
+        float r = (h0 ? v[16 + hi] : v[hi]) * (float)beta_l[h * kNTile + o16];
         if (rope) {
             // the other element of the pair (lane ^ 1, a DPP quad permutation)
             const float p = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(r), 0xB1, 0xF, 0xF, true));
