@@ -604,8 +604,27 @@ __device__ __forceinline__ void fa_step(AttnState &st, const u32x4 (&qf)[4], con
 
 __global__ __launch_bounds__(512, 2) void prefill_fa128_kernel(PfArgs a) {
     extern __shared__ __align__(1024) unsigned char fa_smem[];
-    const int qt = a.nqt - 1 - (int)blockIdx.x;      // longest query tiles first
-    const int h = blockIdx.y, b = blockIdx.z;
+    // Work items to XCDs: workgroups go to the 8 XCDs in turn (linear id w
+    // on XCD w % 8), so with the query tiles on x every head's tiles would
+    // land on 8 different XCDs and each L2 would fetch the head's K and V
+    // again.  Instead slot s = w / 8 of XCD w % 8 takes query tile s % nqt
+    // (longest first) of head group s / nqt: all tiles of one (sequence,
+    // head) run on one XCD and share its L2.
+    int qt, h, b;
+    {
+        const int H = (int)gridDim.y, BH = H * (int)gridDim.z;
+        const int w = (int)blockIdx.x + a.nqt * ((int)blockIdx.y + H * (int)blockIdx.z);
+        if (BH % 8 == 0) {
+            const int slot = w >> 3, bh = (slot / a.nqt) * 8 + (w & 7);
+            qt = a.nqt - 1 - slot % a.nqt;
+            h = bh % H;
+            b = bh / H;
+        } else {
+            qt = a.nqt - 1 - (int)blockIdx.x;
+            h = blockIdx.y;
+            b = blockIdx.z;
+        }
+    }
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int n = lane & 15, kq = lane >> 4;
     const int qw = qt * kFaQ + wave * 16;            // this wave's first query
