@@ -839,8 +839,8 @@ def prefill_attention_preferred(q: torch.Tensor) -> bool:
     """Whether the model should route causal prefill attention here rather
     than to SDPA: head_dim 16, where the whole-head kernel is VALU-bound
     and measured 2.4x faster than SDPA at T = 1024 (51 vs 125 us per layer,
-    config 2), and head_dim 128 (the 128-query matrix-core kernel: 1.55 ms
-    against SDPA's 2.32 ms per layer at config 5).  Head dims 32 and 64 stay
+    config 2), and head_dim 128 (the 128-query matrix-core kernel: 1.18 ms
+    against SDPA's 2.33 ms per layer at config 5).  Head dims 32 and 64 stay
     on SDPA."""
     return q.shape[-1] in (16, 128)
 
