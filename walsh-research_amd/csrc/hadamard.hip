@@ -937,15 +937,14 @@ __global__ __launch_bounds__(kPairThreads, DENSE ? 3 : 4) void hadamard_pair_ker
         // buffer loads (zero past in_o / out_o) with no branch around them,
         // converted after the LUT is built: a conversion or branch right
         // after a load waits for it
-        uint32_t ra[4] = {0u, 0u, 0u, 0u}, rb[4];
+        // (no alpha: a resource of no records, every load out of range)
+        uint32_t ra[4], rb[4];
         const __amdgpu_buffer_rsrc_t br = make_rsrc(a.beta, (uint32_t)((31 * a.beta_h + a.out_o) * 4));
-        if (a.alpha) {
-            const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.alpha, (uint32_t)(32 * a.in_o * 4));
+        const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.alpha, a.alpha ? (uint32_t)(32 * a.in_o * 4) : 0u);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                ra[j] = __builtin_amdgcn_raw_buffer_load_b32(ar, i0 + j < a.in_o ? (uint32_t)(g * a.in_o + i0 + j) * 4 : kOOB,
-                                                             0, 0);
-        }
+        for (int j = 0; j < 4; ++j)
+            ra[j] = __builtin_amdgcn_raw_buffer_load_b32(ar, i0 + j < a.in_o ? (uint32_t)(g * a.in_o + i0 + j) * 4 : kOOB,
+                                                         0, 0);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             rb[j] = __builtin_amdgcn_raw_buffer_load_b32(br, i0 + j < a.out_o ? (uint32_t)(g * a.beta_h + i0 + j) * 4 : kOOB,
