@@ -705,12 +705,24 @@ __global__ __launch_bounds__(kPairThreads, 2) void hadamard_pair_mixproj_kernel(
     {
         const int e = tid;   // (q, g) = (e >> 5, e & 31); kPairThreads == 128 entries
         const int g = e & 31, i0 = 4 * (e >> 5);
+        // buffer loads issued together, with no branch around them (no
+        // alpha: a resource of no records), converted after
+        const __amdgpu_buffer_rsrc_t mbr = make_rsrc(m.beta, (uint32_t)((31 * m.beta_h + 16) * 4));
+        const __amdgpu_buffer_rsrc_t par = make_rsrc(p.alpha, p.alpha ? (uint32_t)((31 * p.in_o + 16) * 4) : 0u);
+        const __amdgpu_buffer_rsrc_t pbr = make_rsrc(p.beta, (uint32_t)((31 * p.beta_h + 16) * 4));
+        uint32_t rm[4], ra[4], rp[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            rm[j] = __builtin_amdgcn_raw_buffer_load_b32(mbr, (uint32_t)(g * m.beta_h + i0 + j) * 4, 0, 0);
+            ra[j] = __builtin_amdgcn_raw_buffer_load_b32(par, (uint32_t)(g * p.in_o + i0 + j) * 4, 0, 0);
+            rp[j] = __builtin_amdgcn_raw_buffer_load_b32(pbr, (uint32_t)(g * p.beta_h + i0 + j) * 4, 0, 0);
+        }
         f32x4 mb, pa, pb;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            mb[j] = m.beta[g * m.beta_h + i0 + j] * 0.03125f;
-            pa[j] = p.alpha ? p.alpha[g * p.in_o + i0 + j] : 1.f;
-            pb[j] = p.beta[g * p.beta_h + i0 + j] * 0.03125f;
+            mb[j] = __uint_as_float(rm[j]) * 0.03125f;
+            pa[j] = p.alpha ? __uint_as_float(ra[j]) : 1.f;
+            pb[j] = __uint_as_float(rp[j]) * 0.03125f;
         }
         mbeta_l[e] = mb;
         palpha_l[e] = pa;
