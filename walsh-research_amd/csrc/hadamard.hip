@@ -1508,8 +1508,9 @@ __global__ __launch_bounds__(kWideThreads, 1) void hadamard_split3_kernel(HadArg
     const float a32 = DENSE ? 0.03125f : 1.f;  // the dense weights' share of the transforms' 1/32
     constexpr int kAv = 32 * kW3MaxO / kWideThreads;
     uint32_t avr[kAv];
-    if (a.alpha) {
-        const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.alpha, (uint32_t)(32 * a.in_o * 4));
+    {
+        // (no alpha: a resource of no records, every load out of range)
+        const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.alpha, a.alpha ? (uint32_t)(32 * a.in_o * 4) : 0u);
 #pragma unroll
         for (int k = 0; k < kAv; ++k) {
             const int e = tid + k * kWideThreads, g = e / kW3MaxO, i = e % kW3MaxO;
